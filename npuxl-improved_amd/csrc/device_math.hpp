@@ -1,0 +1,81 @@
+// device_math.hpp - elementwise math shared by every gfx950 kernel.
+//
+// The activation math is the reference's own published method, not a libm
+// call: exp(x) = 2^floor(z) * P5(z - floor(z)) with z = x*log2(e) and P5 the
+// degree-5 Taylor polynomial of 2^f (reference src/internal.h:87-110 and its
+// AVX2 twin src/kernels/llm.cpp:31-56, which evaluates P5 with FMA Horner as
+// done here).  Using a different exp would move SiLU/GELU/softmax by ~1e-4
+// relative and break parity with the reference.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace vnpu {
+namespace dev {
+
+__device__ __forceinline__ float fast_expf(float x)
+{
+    if (x < -80.0f) return 0.0f;
+    if (x > 80.0f) return __builtin_inff();
+    const float z = x * 1.4426950408889634f;
+    const float zi = floorf(z);
+    const float f = z - zi;
+    float p = fmaf(0.0013333558146428443f, f, 0.009618129107628477f);
+    p = fmaf(p, f, 0.05550410866482158f);
+    p = fmaf(p, f, 0.2402265069591007f);
+    p = fmaf(p, f, 0.6931471805599453f);
+    p = fmaf(p, f, 1.0f);
+    return ldexpf(p, static_cast<int>(zi));
+}
+
+// reference src/internal.h:112
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + fast_expf(-x)); }
+
+// reference src/internal.h:114-121
+__device__ __forceinline__ float gelu_tanh(float x)
+{
+    const float k0 = 0.7978845608028654f;
+    const float k1 = 0.035677408136300125f;
+    const float x3 = x * x * x;
+    const float inner = k0 * (x + k1 * x3);
+    const float t = 2.0f / (1.0f + fast_expf(-2.0f * inner)) - 1.0f;
+    return 0.5f * x * (1.0f + t);
+}
+
+// reference src/internal.h:123-136 (GELU_ERF evaluated as tanh-GELU)
+__device__ __forceinline__ float epilogue(float v, uint32_t epi)
+{
+    switch (epi) {
+    case 1: return v > 0.0f ? v : 0.0f;
+    case 2: return silu(v);
+    case 3:
+    case 4: return gelu_tanh(v);
+    default: return v;
+    }
+}
+
+// Wave-wide reductions (wave64).
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace dev
+}  // namespace vnpu

@@ -1,0 +1,738 @@
+// dispatch.cpp - the vnpu command processor on a HIP stream.
+//
+// Replaces the reference's schedule_command and execute_* functions
+// (src/core/scheduler.cpp:320-753).  For each vnpu_command_t it
+//   1. validates arguments and applies the reference's defaults (same rules,
+//      same rejections) - a rejected command throws ArgError, which the
+//      stream turns into the reference's sticky-error behaviour;
+//   2. stages host pointers through HBM (device pointers pass through);
+//   3. picks the kernel from the shape (the "grid scheduler": decode GEMV for
+//      M <= 8, MFMA GEMM otherwise) and enqueues it on the stream;
+//   4. accounts algorithmic bytes / flops exactly as the reference does.
+#include "vnpu_internal.hpp"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <memory>
+#include <tuple>
+
+namespace vnpu {
+
+bool is_device_pointer(const void *p)
+{
+    if (!p) return false;
+    hipPointerAttribute_t attr;
+    std::memset(&attr, 0, sizeof(attr));
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged ||
+           attr.type == hipMemoryTypeUnified ||
+           (attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr);
+}
+
+namespace {
+
+// Host-pointer staging for one command.  Device-accessible pointers are used
+// as is; a pageable host pointer gets an HBM copy (in), a result copy-back
+// (out) or both.  Any staging makes the command synchronous: pageable
+// host copies are synchronous in HIP anyway.
+class Stager {
+public:
+    explicit Stager(hipStream_t s) : s_(s) {}
+    ~Stager() { release(); }
+
+    template <typename T>
+    const T *in(const T *p, size_t bytes)
+    {
+        if (!p || !bytes || is_device_pointer(p)) return p;
+        void *d = alloc(bytes);
+        VNPU_HIP(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, s_));
+        return static_cast<const T *>(d);
+    }
+    template <typename T>
+    T *out(T *p, size_t bytes)
+    {
+        if (!p || !bytes || is_device_pointer(p)) return p;
+        void *d = alloc(bytes);
+        outs_.emplace_back(static_cast<void *>(p), d, bytes);
+        return static_cast<T *>(d);
+    }
+    template <typename T>
+    T *inout(T *p, size_t bytes)
+    {
+        if (!p || !bytes || is_device_pointer(p)) return p;
+        void *d = alloc(bytes);
+        VNPU_HIP(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, s_));
+        outs_.emplace_back(static_cast<void *>(p), d, bytes);
+        return static_cast<T *>(d);
+    }
+    bool staged() const { return !temps_.empty(); }
+    void finish()
+    {
+        for (auto &o : outs_)
+            VNPU_HIP(hipMemcpyAsync(std::get<0>(o), std::get<1>(o), std::get<2>(o),
+                                    hipMemcpyDeviceToHost, s_));
+        outs_.clear();
+        release();
+    }
+
+private:
+    void *alloc(size_t bytes)
+    {
+        void *d = nullptr;
+        VNPU_HIP(hipMalloc(&d, bytes));
+        temps_.push_back(d);
+        return d;
+    }
+    void release()
+    {
+        if (temps_.empty()) return;
+        (void)hipStreamSynchronize(s_);
+        for (void *d : temps_) (void)hipFree(d);
+        temps_.clear();
+    }
+    hipStream_t s_;
+    std::vector<void *> temps_;
+    std::vector<std::tuple<void *, void *, size_t>> outs_;
+};
+
+inline void require(bool ok, const char *what)
+{
+    if (!ok) throw ArgError(what);
+}
+
+inline bool mul_overflow(uint64_t a, uint64_t b, uint64_t c)
+{
+    if (!a || !b || !c) return false;
+    const uint64_t ab = a * b;
+    if (ab / b != a) return true;
+    return ab > std::numeric_limits<uint64_t>::max() / c;
+}
+
+// Bytes spanned by `rows` rows of `cols` elements at leading dimension ld.
+inline size_t span(uint64_t rows, uint64_t cols, uint64_t ld, size_t elem)
+{
+    if (!rows || !cols) return 0;
+    return static_cast<size_t>(((rows - 1) * ld + cols) * elem);
+}
+
+inline uint32_t cdiv(uint32_t a, uint32_t b) { return b ? (a + b - 1) / b : 0; }
+
+// choose_unit (reference scheduler.cpp:43-59).  UNIT_GPU is this backend's
+// native unit and behaves like AUTO.
+uint32_t choose_unit(uint32_t unit, bool has_mask, uint32_t flags)
+{
+    if (flags & VNPU_CMD_FLAG_CELL_DMA) return VNPU_UNIT_CELL;
+    if (flags & VNPU_CMD_FLAG_VOODOO_FIFO) return VNPU_UNIT_VOODOO;
+    if (unit != VNPU_UNIT_AUTO && unit != VNPU_UNIT_GPU) return unit;
+    if (has_mask || (flags & VNPU_CMD_FLAG_WILDCAT_CULL)) return VNPU_UNIT_WILDCAT;
+    return VNPU_UNIT_VOODOO;
+}
+
+bool pack_b_enabled()
+{
+    const char *e = std::getenv("VNPU_PACK");
+    if (e && e[0] == '0' && e[1] == '\0') return false;
+    const char *mode = std::getenv("VNPU_MODE");
+    if (mode && std::strcmp(mode, "reference") == 0) return false;
+    return true;
+}
+
+// The reference's f32 tile geometry (scheduler.cpp:96-206, the !int8
+// branches), used only to sample a Wildcat cull mask so that the culled
+// output region is the one the reference culls for the same device tiles and
+// unit count.
+void cull_geometry(const vnpu_device_t *dev, uint32_t unit, uint32_t M, uint32_t N, uint32_t &tm,
+                   uint32_t &tn)
+{
+    tm = std::max<uint32_t>(1, dev->tile_m.load());
+    tn = std::max<uint32_t>(1, dev->tile_n.load());
+    const uint32_t units = std::max<uint32_t>(1, dev->info.num_threads);
+    if (M <= 8 && (unit == VNPU_UNIT_VOODOO || unit == VNPU_UNIT_AUTO)) {
+        tm = M;
+        tn = std::min<uint32_t>(std::max<uint32_t>(32, tn), 64);
+        if (tn > N) tn = N;
+        return;
+    }
+    if (pack_b_enabled() && (unit == VNPU_UNIT_VOODOO || unit == VNPU_UNIT_AUTO)) {
+        if (M >= 3 && cdiv(N, 64) >= 2 * units) {
+            tm = M;
+            tn = 64;
+            return;
+        }
+    }
+    if (unit == VNPU_UNIT_WILDCAT) {
+        tm = std::min<uint32_t>(tm, 32);
+        tn = std::min<uint32_t>(tn, 64);
+    } else if (unit == VNPU_UNIT_CELL) {
+        tm = std::min<uint32_t>(tm, 16);
+        tn = std::min<uint32_t>(tn, 64);
+    }
+    uint64_t tiles = static_cast<uint64_t>(cdiv(M, tm)) * cdiv(N, tn);
+    const uint64_t target = static_cast<uint64_t>(dev->info.num_threads) * 64;
+    while (tiles > target && (tm < M || tn < N)) {
+        if (tm < M) tm = std::min<uint32_t>(M, tm * 2);
+        if (tn < N) tn = std::min<uint32_t>(N, tn * 2);
+        tiles = static_cast<uint64_t>(cdiv(M, tm)) * cdiv(N, tn);
+    }
+}
+
+// RoPE inverse-frequency table, computed on the host with the reference's
+// expression 1 / powf(theta, 2j / dim) (llm.cpp:195-210) and cached per
+// (theta, dim) in HBM for the device's lifetime.
+struct InvFreqCache {
+    std::mutex mutex;
+    std::map<std::tuple<vnpu_device_t *, uint32_t, uint32_t>, float *> tables;
+    ~InvFreqCache()
+    {
+        // Tables are released with their device (release_device_tables).
+    }
+};
+InvFreqCache &inv_cache()
+{
+    static InvFreqCache *c = new InvFreqCache();
+    return *c;
+}
+
+const float *rope_table(vnpu_device_t *dev, float theta, uint32_t dim)
+{
+    uint32_t bits;
+    std::memcpy(&bits, &theta, 4);
+    auto key = std::make_tuple(dev, bits, dim);
+    auto &c = inv_cache();
+    std::lock_guard<std::mutex> lock(c.mutex);
+    auto it = c.tables.find(key);
+    if (it != c.tables.end()) return it->second;
+    const uint32_t half = dim / 2;
+    std::vector<float> inv(half);
+    for (uint32_t j = 0; j < half; ++j)
+        inv[j] = 1.0f / std::pow(theta, 2.0f * static_cast<float>(j) / static_cast<float>(dim));
+    float *d = nullptr;
+    VNPU_HIP(hipMalloc(&d, half * sizeof(float)));
+    VNPU_HIP(hipMemcpy(d, inv.data(), half * sizeof(float), hipMemcpyHostToDevice));
+    c.tables.emplace(key, d);
+    return d;
+}
+
+// ---------------------------------------------------------------------------
+
+void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32_args_t &in,
+                     uint32_t flags, ExecStats &st)
+{
+    // prepare_matmul_f32 (scheduler.cpp:274-318)
+    require(in.A && in.B && in.C && in.M && in.K && in.N, "invalid matmul_f32 arguments");
+    require(!mul_overflow(in.M, in.K, in.N), "matmul_f32 shape overflow");
+    require(in.trans_a <= 1 && in.trans_b <= 1 && in.epilogue <= VNPU_EPILOGUE_GELU_ERF,
+            "invalid matmul_f32 mode");
+    const bool has_mask = in.tile_mask && in.mask_tile_m && in.mask_tile_n;
+    const uint32_t unit = choose_unit(in.unit, in.tile_mask != nullptr, flags);
+    st.unit = unit;
+    k::F32Gemm p;
+    p.M = in.M; p.K = in.K; p.N = in.N;
+    p.lda = in.lda ? in.lda : (in.trans_a ? in.M : in.K);
+    p.ldb = in.ldb ? in.ldb : (in.trans_b ? in.K : in.N);
+    p.ldc = in.ldc ? in.ldc : in.N;
+    require(p.lda >= (in.trans_a ? in.M : in.K) && p.ldb >= (in.trans_b ? in.K : in.N) &&
+                p.ldc >= in.N,
+            "invalid matmul_f32 leading dimensions");
+    p.trans_a = in.trans_a;
+    p.trans_b = in.trans_b;
+    p.alpha = in.alpha == 0.0f ? 1.0f : in.alpha;
+    p.beta = in.beta;
+    p.epilogue = in.epilogue;
+
+    Stager sg(s->hip);
+    p.A = sg.in(in.A, in.trans_a ? span(in.K, in.M, p.lda, 4) : span(in.M, in.K, p.lda, 4));
+    p.B = sg.in(in.B, in.trans_b ? span(in.N, in.K, p.ldb, 4) : span(in.K, in.N, p.ldb, 4));
+    p.bias = sg.in(in.bias, in.bias ? static_cast<size_t>(in.N) * 4 : 0);
+
+    // Wildcat cull: sample the mask on the reference's tile grid, then
+    // classify each 128 x 128 kernel tile as compute / culled / mixed.
+    std::vector<uint8_t> cull, state;
+    uint64_t culled_tiles = 0, total_tiles = 1;
+    if (has_mask) {
+        uint32_t tm, tn;
+        cull_geometry(dev, unit, in.M, in.N, tm, tn);
+        const uint32_t mt = cdiv(in.M, tm), nt = cdiv(in.N, tn);
+        const uint8_t *mask = in.tile_mask;
+        std::vector<uint8_t> host_mask;
+        if (is_device_pointer(mask)) {
+            host_mask.resize(static_cast<size_t>(in.mask_tile_m) * in.mask_tile_n);
+            VNPU_HIP(hipMemcpy(host_mask.data(), mask, host_mask.size(), hipMemcpyDeviceToHost));
+            mask = host_mask.data();
+        }
+        cull.assign(static_cast<size_t>(mt) * nt, 0);
+        for (uint32_t mi = 0; mi < mt; ++mi)
+            for (uint32_t ni = 0; ni < nt; ++ni) {
+                const uint32_t mm = std::min<uint32_t>(in.mask_tile_m - 1,
+                    static_cast<uint32_t>((static_cast<uint64_t>(mi) * in.mask_tile_m) / mt));
+                const uint32_t nn = std::min<uint32_t>(in.mask_tile_n - 1,
+                    static_cast<uint32_t>((static_cast<uint64_t>(ni) * in.mask_tile_n) / nt));
+                if (mask[static_cast<size_t>(mm) * in.mask_tile_n + nn] == 0) {
+                    cull[static_cast<size_t>(mi) * nt + ni] = 1;
+                    ++culled_tiles;
+                }
+            }
+        total_tiles = static_cast<uint64_t>(mt) * nt;
+        uint32_t bm, bn;
+        k::gemm_f32_tile_dims(bm, bn);
+        const uint32_t gm = cdiv(in.M, bm), gn = cdiv(in.N, bn);
+        state.assign(static_cast<size_t>(gm) * gn, 0);
+        for (uint32_t gi = 0; gi < gm; ++gi)
+            for (uint32_t gj = 0; gj < gn; ++gj) {
+                const uint32_t r0 = gi * bm / tm, r1 = (std::min(in.M, (gi + 1) * bm) - 1) / tm;
+                const uint32_t c0 = gj * bn / tn, c1 = (std::min(in.N, (gj + 1) * bn) - 1) / tn;
+                bool any_c = false, any_k = false;
+                for (uint32_t r = r0; r <= r1; ++r)
+                    for (uint32_t c = c0; c <= c1; ++c)
+                        (cull[static_cast<size_t>(r) * nt + c] ? any_c : any_k) = true;
+                state[static_cast<size_t>(gi) * gn + gj] = any_c ? (any_k ? 2 : 1) : 0;
+            }
+        p.cull = sg.in(cull.data(), cull.size());
+        p.ktile_state = sg.in(state.data(), state.size());
+        p.cull_tm = tm;
+        p.cull_tn = tn;
+        p.cull_nt = nt;
+        // A host vector always stages; keep them alive until finish().
+    }
+    const bool c_in = in.beta != 0.0f || p.ldc != in.N;
+    const size_t c_bytes = span(in.M, in.N, p.ldc, 4);
+    p.C = c_in ? sg.inout(in.C, c_bytes) : sg.out(in.C, c_bytes);
+
+    if (!has_mask && in.M <= 8 && !in.trans_a && !in.trans_b) {
+        const size_t ws = k::gemv_f32_ws_bytes(in.M, in.N, in.K);
+        float *w = static_cast<float *>(s->ensure_workspace(ws));
+        k::gemv_f32(s->hip, p, w);
+    } else {
+        k::gemm_f32(s->hip, p);
+    }
+    VNPU_HIP(hipGetLastError());
+    sg.finish();
+
+    st.tiles_dispatched += total_tiles - culled_tiles;
+    st.tiles_culled += culled_tiles;
+    const uint64_t a_b = static_cast<uint64_t>(in.M) * in.K * 4;
+    const uint64_t b_b = static_cast<uint64_t>(in.K) * in.N * 4;
+    const uint64_t c_b = static_cast<uint64_t>(in.M) * in.N * 4;
+    const uint64_t bias_b = in.bias ? static_cast<uint64_t>(in.N) * 4 : 0;
+    st.bytes_read += a_b + b_b + bias_b + (in.beta != 0.0f ? c_b : 0);
+    st.bytes_written += c_b;
+    st.flops += 2ull * in.M * in.K * in.N;
+}
+
+void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_args_t &in,
+                    uint32_t flags, ExecStats &st)
+{
+    // execute_matmul_i8 (scheduler.cpp:370-428)
+    vnpu_packed_weights_t *w = in.B;
+    require(in.A && w && in.C && in.M && in.K && in.N, "invalid matmul_i8 arguments");
+    require(w->K == in.K && w->N == in.N, "packed weight shape mismatch");
+    require(w->device == nullptr || w->device->hip_device == dev->hip_device,
+            "packed weights live on another device");
+    st.unit = choose_unit(in.unit, false, flags);
+    k::I8Gemm p;
+    p.M = in.M; p.N = in.N; p.K = in.K;
+    p.lda = in.lda ? in.lda : in.K;
+    p.ldc = in.ldc ? in.ldc : in.N;
+    require(p.lda >= in.K && p.ldc >= in.N, "invalid int8 leading dimensions");
+    p.frag = w->frag;
+    p.zero_blocks = w->zero_block_count ? w->zero_blocks : nullptr;
+    p.Kp = w->Kp;
+    p.Np = w->Np;
+    p.scale_b = w->scales_dev;
+    p.epilogue = in.epilogue;
+    require(in.epilogue <= VNPU_EPILOGUE_GELU_ERF, "invalid matmul_i8 epilogue");
+
+    Stager sg(s->hip);
+    p.A = sg.in(in.A, span(in.M, in.K, p.lda, 1));
+    p.scale_a = sg.in(in.scale_a, in.scale_a ? static_cast<size_t>(in.M) * 4 : 0);
+    p.bias = sg.in(in.bias, in.bias ? static_cast<size_t>(in.N) * 4 : 0);
+    const size_t c_bytes = span(in.M, in.N, p.ldc, 4);
+    p.C = p.ldc != in.N ? sg.inout(in.C, c_bytes) : sg.out(in.C, c_bytes);
+
+    if (in.M <= 8)
+        k::gemv_i8(s->hip, p);
+    else
+        k::gemm_i8(s->hip, p);
+    VNPU_HIP(hipGetLastError());
+    sg.finish();
+
+    st.tiles_dispatched += 1;
+    const uint64_t a_b = static_cast<uint64_t>(in.M) * in.K;
+    const uint64_t b_b = static_cast<uint64_t>(in.K) * in.N;
+    const uint64_t c_b = static_cast<uint64_t>(in.M) * in.N * 4;
+    const uint64_t sc_b = static_cast<uint64_t>(in.N + (in.scale_a ? in.M : 0)) * 4;
+    st.bytes_read += a_b + b_b + sc_b;
+    st.bytes_written += c_b;
+    st.flops += 2ull * in.M * in.K * in.N;
+}
+
+void exec_quantize(vnpu_device_t *, vnpu_stream_t *s, const vnpu_quantize_i8_args_t &a,
+                   ExecStats &st)
+{
+    // execute_quantize_i8 (scheduler.cpp:430-473)
+    require(a.X && a.Y && a.scales && a.rows && a.cols && a.axis <= VNPU_QUANT_PER_TENSOR,
+            "invalid quantize_i8 arguments");
+    require(!mul_overflow(a.rows, a.cols, 1), "quantize shape overflow");
+    const uint64_t total = a.rows * a.cols;
+    const size_t n_scales = a.axis == VNPU_QUANT_PER_ROW ? a.rows
+                            : a.axis == VNPU_QUANT_PER_COLUMN ? a.cols : 1;
+    Stager sg(s->hip);
+    const float *X = sg.in(a.X, total * 4);
+    int8_t *Y = sg.out(a.Y, total);
+    float *sc = sg.out(a.scales, n_scales * 4);
+    if (a.axis == VNPU_QUANT_PER_ROW) {
+        k::quantize_rows(s->hip, X, Y, sc, a.rows, a.cols);
+    } else if (a.axis == VNPU_QUANT_PER_COLUMN) {
+        require(a.cols <= 0xffffffffull * 64ull, "quantize column count too large");
+        k::quantize_cols(s->hip, X, Y, sc, a.rows, a.cols);
+    } else {
+        float *ws = static_cast<float *>(s->ensure_workspace(k::quantize_tensor_ws_bytes()));
+        k::quantize_tensor(s->hip, X, Y, sc, total, ws);
+    }
+    VNPU_HIP(hipGetLastError());
+    sg.finish();
+    st.bytes_read += total * 4;
+    st.bytes_written += total;
+    st.flops += total * 3;
+}
+
+void exec_rmsnorm(vnpu_stream_t *s, const vnpu_rmsnorm_f32_args_t &a, ExecStats &st)
+{
+    // execute_rmsnorm (scheduler.cpp:475-492), eps default llm.cpp:67
+    require(a.X && a.Y && a.rows && a.cols, "invalid rmsnorm arguments");
+    const float eps = a.eps > 0.0f ? a.eps : 1e-5f;
+    const uint64_t n = static_cast<uint64_t>(a.rows) * a.cols;
+    Stager sg(s->hip);
+    const float *X = sg.in(a.X, n * 4);
+    const float *W = sg.in(a.W, a.W ? static_cast<size_t>(a.cols) * 4 : 0);
+    float *Y = (a.Y == a.X) ? sg.inout(a.Y, n * 4) : sg.out(a.Y, n * 4);
+    if (a.Y == a.X && !is_device_pointer(a.X)) X = Y;
+    k::rmsnorm(s->hip, X, W, Y, a.rows, a.cols, eps);
+    VNPU_HIP(hipGetLastError());
+    sg.finish();
+    st.bytes_read += n * 4 + (a.W ? static_cast<uint64_t>(a.cols) * 4 : 0);
+    st.bytes_written += n * 4;
+    st.flops += n * 5;
+}
+
+void exec_softmax(vnpu_stream_t *s, const vnpu_softmax_f32_args_t &a, ExecStats &st)
+{
+    // execute_softmax (scheduler.cpp:494-510), temperature default llm.cpp:119
+    require(a.X && a.Y && a.rows && a.cols, "invalid softmax arguments");
+    const float inv_t = a.temperature > 0.0f ? 1.0f / a.temperature : 1.0f;
+    const uint64_t n = static_cast<uint64_t>(a.rows) * a.cols;
+    Stager sg(s->hip);
+    const float *X = sg.in(a.X, n * 4);
+    float *Y = (a.Y == a.X) ? sg.inout(a.Y, n * 4) : sg.out(a.Y, n * 4);
+    if (a.Y == a.X && !is_device_pointer(a.X)) X = Y;
+    k::softmax(s->hip, X, Y, a.rows, a.cols, inv_t);
+    VNPU_HIP(hipGetLastError());
+    sg.finish();
+    st.bytes_read += n * 4;
+    st.bytes_written += n * 4;
+    st.flops += n * 6;
+}
+
+void exec_rope(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_rope_f32_args_t &a, ExecStats &st)
+{
+    // execute_rope (scheduler.cpp:512-534), defaults llm.cpp:583-584
+    require((a.Q || a.K) && a.batch && a.heads && a.head_dim && (a.q_seq || a.k_seq) &&
+                !(a.head_dim & 1u),
+            "invalid rope arguments");
+    const float theta = a.theta_base > 0.0f ? a.theta_base : 10000.0f;
+    const float scaling = a.scaling > 0.0f ? a.scaling : 1.0f;
+    const uint64_t bh = static_cast<uint64_t>(a.batch) * a.heads;
+    const uint64_t qn = bh * a.q_seq * a.head_dim, kn = bh * a.k_seq * a.head_dim;
+    const uint32_t seq = std::max(a.q_seq, a.k_seq);
+    const float *inv = rope_table(dev, theta, a.head_dim);
+    Stager sg(s->hip);
+    float *Q = a.Q && a.q_seq ? sg.inout(a.Q, qn * 4) : nullptr;
+    float *K = a.K && a.k_seq ? sg.inout(a.K, kn * 4) : nullptr;
+    const int32_t *pos = sg.in(a.positions, a.positions ? static_cast<size_t>(seq) * 4 : 0);
+    k::rope(s->hip, Q, K, pos, a.batch, a.heads, Q ? a.q_seq : 0, K ? a.k_seq : 0, a.head_dim,
+            a.position_offset, a.interleaved, scaling, inv);
+    VNPU_HIP(hipGetLastError());
+    sg.finish();
+    st.bytes_read += (qn + kn) * 4;
+    st.bytes_written += (qn + kn) * 4;
+    st.flops += (qn + kn) * 8;
+}
+
+void exec_elementwise(vnpu_stream_t *s, const vnpu_command_t &cmd, ExecStats &st)
+{
+    Stager sg(s->hip);
+    if (cmd.opcode == VNPU_OP_SWIGLU_F32) {
+        const auto &a = cmd.args.swiglu;  // scheduler.cpp:536-548
+        require(a.gate && a.up && a.Y && a.count, "invalid swiglu arguments");
+        const float alpha = a.alpha == 0.0f ? 1.0f : a.alpha;
+        const float *g = sg.in(a.gate, a.count * 4);
+        const float *u = sg.in(a.up, a.count * 4);
+        float *Y = sg.out(a.Y, a.count * 4);
+        k::swiglu(s->hip, g, u, Y, a.count, alpha);
+        st.bytes_read += a.count * 8;
+        st.bytes_written += a.count * 4;
+        st.flops += a.count * 8;
+    } else if (cmd.opcode == VNPU_OP_GELU_F32) {
+        const auto &a = cmd.args.unary;  // scheduler.cpp:550-562
+        require(a.X && a.Y && a.count, "invalid gelu arguments");
+        const float *X = sg.in(a.X, a.count * 4);
+        float *Y = sg.out(a.Y, a.count * 4);
+        k::gelu(s->hip, X, Y, a.count);
+        st.bytes_read += a.count * 4;
+        st.bytes_written += a.count * 4;
+        st.flops += a.count * 12;
+    } else {
+        const auto &a = cmd.args.binary;  // scheduler.cpp:564-581
+        require(a.A && a.B && a.Y && a.count, "invalid binary arguments");
+        const float *A = sg.in(a.A, a.count * 4);
+        const float *B = sg.in(a.B, a.count * 4);
+        float *Y = sg.out(a.Y, a.count * 4);
+        if (cmd.opcode == VNPU_OP_ADD_F32) {
+            const bool both0 = a.alpha == 0.0f && a.beta == 0.0f;  // llm.cpp:226-227
+            k::add(s->hip, A, B, Y, a.count, both0 ? 1.0f : a.alpha, both0 ? 1.0f : a.beta);
+        } else {
+            k::mul(s->hip, A, B, Y, a.count, a.alpha == 0.0f ? 1.0f : a.alpha, a.beta);
+        }
+        st.bytes_read += a.count * 8;
+        st.bytes_written += a.count * 4;
+        st.flops += a.count * 3;
+    }
+    VNPU_HIP(hipGetLastError());
+    sg.finish();
+}
+
+void exec_attention(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecStats &st)
+{
+    // execute_attention (scheduler.cpp:583-608), scale default llm.cpp:452-453
+    require(a.Q && a.K && a.V && a.O && a.batch && a.heads && a.seq_q && a.seq_k && a.head_dim,
+            "invalid attention arguments");
+    require(a.head_dim <= 256, "attention head_dim above 256 is not supported on this backend");
+    require(static_cast<uint64_t>(a.batch) * a.heads <= 65535u,
+            "attention batch*heads above 65535 is not supported on this backend");
+    k::Attn p;
+    p.batch = a.batch; p.heads = a.heads; p.seq_q = a.seq_q; p.seq_k = a.seq_k;
+    p.head_dim = a.head_dim; p.causal = a.causal;
+    p.scale = a.scale > 0.0f ? a.scale : 1.0f / std::sqrt(static_cast<float>(a.head_dim));
+    const uint64_t bh = static_cast<uint64_t>(a.batch) * a.heads;
+    const uint64_t qn = bh * a.seq_q * a.head_dim, kn = bh * a.seq_k * a.head_dim;
+    const uint64_t mn = a.mask ? bh * a.seq_q * a.seq_k : 0;
+    Stager sg(s->hip);
+    p.Q = sg.in(a.Q, qn * 4);
+    p.K = sg.in(a.K, kn * 4);
+    p.V = sg.in(a.V, kn * 4);
+    p.mask = sg.in(a.mask, mn * 4);
+    p.O = sg.out(a.O, qn * 4);
+    float *ws = static_cast<float *>(s->ensure_workspace(k::attention_ws_bytes(p)));
+    k::attention(s->hip, p, ws);
+    VNPU_HIP(hipGetLastError());
+    sg.finish();
+    st.bytes_read += (qn + 2 * kn + mn) * 4;
+    st.bytes_written += qn * 4;
+    st.flops += 4ull * a.batch * a.heads * a.seq_q * a.seq_k * a.head_dim;
+}
+
+void exec_copy(vnpu_stream_t *s, const vnpu_copy_args_t &a, ExecStats &st)
+{
+    // execute_copy (scheduler.cpp:643-651): memmove semantics for host copies
+    require(a.dst && a.src && a.bytes, "invalid copy arguments");
+    const bool dd = is_device_pointer(a.dst), sd = is_device_pointer(a.src);
+    if (!dd && !sd) {
+        VNPU_HIP(hipStreamSynchronize(s->hip));
+        std::memmove(a.dst, a.src, static_cast<size_t>(a.bytes));
+    } else {
+        VNPU_HIP(hipMemcpyAsync(a.dst, a.src, static_cast<size_t>(a.bytes), hipMemcpyDefault, s->hip));
+        if (!dd || !sd) VNPU_HIP(hipStreamSynchronize(s->hip));
+    }
+    st.bytes_read += a.bytes;
+    st.bytes_written += a.bytes;
+    st.dma_bytes += a.bytes;
+}
+
+void exec_memset(vnpu_stream_t *s, const vnpu_memset_args_t &a, ExecStats &st)
+{
+    // execute_memset (scheduler.cpp:653-662)
+    require(a.dst && a.bytes, "invalid memset arguments");
+    if (is_device_pointer(a.dst)) {
+        k::fill_u8(s->hip, a.dst, static_cast<uint8_t>(a.value & 0xffu), a.bytes);
+    } else {
+        VNPU_HIP(hipStreamSynchronize(s->hip));
+        std::memset(a.dst, static_cast<int>(a.value & 0xffu), static_cast<size_t>(a.bytes));
+    }
+    VNPU_HIP(hipGetLastError());
+    st.bytes_written += a.bytes;
+    st.dma_bytes += a.bytes;
+}
+
+}  // namespace
+
+void execute_command(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &cmd,
+                     uint32_t flags, ExecStats &st)
+{
+    switch (cmd.opcode) {
+    case VNPU_OP_NOP:
+    case VNPU_OP_BARRIER:
+        return;
+    case VNPU_OP_MATMUL_F32:
+        exec_matmul_f32(dev, s, cmd.args.matmul_f32, flags, st);
+        return;
+    case VNPU_OP_MATMUL_I8:
+        exec_matmul_i8(dev, s, cmd.args.matmul_i8, flags, st);
+        return;
+    case VNPU_OP_RMSNORM_F32:
+        exec_rmsnorm(s, cmd.args.rmsnorm, st);
+        return;
+    case VNPU_OP_SOFTMAX_F32:
+        exec_softmax(s, cmd.args.softmax, st);
+        return;
+    case VNPU_OP_ROPE_F32:
+        exec_rope(dev, s, cmd.args.rope, st);
+        return;
+    case VNPU_OP_SWIGLU_F32:
+    case VNPU_OP_GELU_F32:
+    case VNPU_OP_ADD_F32:
+    case VNPU_OP_MUL_F32:
+        exec_elementwise(s, cmd, st);
+        return;
+    case VNPU_OP_ATTENTION_F32:
+        exec_attention(s, cmd.args.attention, st);
+        return;
+    case VNPU_OP_QUANTIZE_I8:
+        exec_quantize(dev, s, cmd.args.quantize_i8, st);
+        return;
+    case VNPU_OP_PACK_WEIGHTS_I8: {
+        // execute_pack_weights (scheduler.cpp:664-677)
+        const auto &a = cmd.args.pack_weights_i8;
+        require(a.B && a.out && a.K && a.N, "invalid pack_weights arguments");
+        VNPU_HIP(hipStreamSynchronize(s->hip));  // B may be produced earlier on this stream
+        vnpu_packed_weights_t *w = pack_weights(dev, a.B, a.scales, a.K, a.N, a.ldb, a.trans_b);
+        *a.out = w;
+        st.bytes_read += static_cast<uint64_t>(a.K) * a.N * 2;
+        st.bytes_written += w->frag_bytes;
+        st.dma_bytes += static_cast<uint64_t>(a.K) * a.N * 2;
+        return;
+    }
+    case VNPU_OP_MTP_HEAD_F32: {
+        // execute_mtp_head (scheduler.cpp:610-641): a MATMUL_F32 with
+        // M = gamma, K = hidden_dim, N = vocab, trans_b = trans_w.
+        const auto &a = cmd.args.mtp_head;
+        require(a.hidden && a.W && a.logits && a.gamma && a.hidden_dim && a.vocab,
+                "invalid mtp_head arguments");
+        vnpu_matmul_f32_args_t g{};
+        g.A = a.hidden;
+        g.B = a.W;
+        g.bias = a.bias;
+        g.C = a.logits;
+        g.M = a.gamma;
+        g.K = a.hidden_dim;
+        g.N = a.vocab;
+        g.trans_b = a.trans_w;
+        g.alpha = 1.0f;
+        g.unit = a.unit;
+        exec_matmul_f32(dev, s, g, flags, st);
+        return;
+    }
+    case VNPU_OP_COPY:
+        exec_copy(s, cmd.args.copy, st);
+        return;
+    case VNPU_OP_MEMSET:
+        exec_memset(s, cmd.args.memset, st);
+        return;
+    default:
+        throw ArgError("invalid opcode");
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Packed weights (reference scheduler.cpp:763-858)
+// ---------------------------------------------------------------------------
+
+vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const float *scales,
+                                    uint32_t K, uint32_t N, uint32_t ldb, uint32_t trans_b)
+{
+    const uint32_t ld = ldb ? ldb : (trans_b ? K : N);
+    require(ld >= (trans_b ? K : N), "invalid pack ldb");
+    VNPU_HIP(hipSetDevice(dev->hip_device));
+    std::unique_ptr<vnpu_packed_weights_t, void (*)(vnpu_packed_weights_t *)> w(
+        new vnpu_packed_weights_t(), destroy_packed);
+    w->device = dev;
+    w->K = K;
+    w->N = N;
+    w->Kp = (K + 63) / 64 * 64;
+    w->Np = (N + 15) / 16 * 16;
+    const uint64_t blocks = static_cast<uint64_t>(w->Kp / 64) * (w->Np / 16);
+    w->frag_bytes = blocks * 1024;
+    VNPU_HIP(hipMalloc(&w->frag, w->frag_bytes));
+    VNPU_HIP(hipMalloc(&w->scales_dev, static_cast<size_t>(w->Np) * 4));
+    VNPU_HIP(hipMalloc(&w->zero_blocks, blocks));
+    int32_t *sums_dev = nullptr;
+    VNPU_HIP(hipMalloc(&sums_dev, static_cast<size_t>(N) * 4));
+    std::unique_ptr<int32_t, hipError_t (*)(void *)> sums_guard(sums_dev, hipFree);
+
+    hipStream_t st = nullptr;
+    VNPU_HIP(hipStreamCreate(&st));
+    std::unique_ptr<std::remove_pointer<hipStream_t>::type, hipError_t (*)(hipStream_t)> st_guard(
+        st, hipStreamDestroy);
+    const size_t b_bytes = trans_b ? span(N, K, ld, 1) : span(K, N, ld, 1);
+    Stager sg(st);
+    const int8_t *Bd = sg.in(B, b_bytes);
+    k::pack_fragments(st, Bd, K, N, ld, trans_b, w->frag, w->Kp, w->Np, sums_dev, w->zero_blocks);
+    VNPU_HIP(hipGetLastError());
+
+    // Scales: NULL keeps 1.0 (the reference does not derive them, F5 of its
+    // scheduler.cpp:806-808).
+    w->scales.assign(w->Np, 1.0f);
+    if (scales) {
+        if (is_device_pointer(scales))
+            VNPU_HIP(hipMemcpyAsync(w->scales.data(), scales, static_cast<size_t>(N) * 4,
+                                    hipMemcpyDeviceToHost, st));
+        else
+            std::memcpy(w->scales.data(), scales, static_cast<size_t>(N) * 4);
+    }
+    VNPU_HIP(hipStreamSynchronize(st));
+    VNPU_HIP(hipMemcpy(w->scales_dev, w->scales.data(), static_cast<size_t>(w->Np) * 4,
+                       hipMemcpyHostToDevice));
+    w->column_sums.assign(w->Np, 0);
+    VNPU_HIP(hipMemcpy(w->column_sums.data(), sums_dev, static_cast<size_t>(N) * 4,
+                       hipMemcpyDeviceToHost));
+    std::vector<uint8_t> zb(blocks);
+    VNPU_HIP(hipMemcpy(zb.data(), w->zero_blocks, blocks, hipMemcpyDeviceToHost));
+    w->zero_block_count = 0;
+    for (uint8_t z : zb) w->zero_block_count += z;
+    sg.finish();
+    VNPU_HIP(hipStreamSynchronize(st));
+    dev->dma_bytes.fetch_add(static_cast<uint64_t>(K) * N * 2);
+    return w.release();
+}
+
+void destroy_packed(vnpu_packed_weights_t *w)
+{
+    if (!w) return;
+    if (w->frag) (void)hipFree(w->frag);
+    if (w->scales_dev) (void)hipFree(w->scales_dev);
+    if (w->zero_blocks) (void)hipFree(w->zero_blocks);
+    delete w;
+}
+
+void release_device_tables(vnpu_device_t *dev)
+{
+    auto &c = inv_cache();
+    std::lock_guard<std::mutex> lock(c.mutex);
+    for (auto it = c.tables.begin(); it != c.tables.end();) {
+        if (std::get<0>(it->first) == dev) {
+            (void)hipFree(it->second);
+            it = c.tables.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
+
+}  // namespace vnpu

@@ -1,0 +1,336 @@
+// gemm_f32.hip - MATMUL_F32 / MTP_HEAD_F32 on gfx950.
+//
+// Semantics: the reference's store_c / zero_c_tile (src/kernels/kernels.cpp:
+// 43-62) with the defaults of prepare_matmul_f32 (src/core/scheduler.cpp:
+// 274-318):
+//   C = epi(alpha * op(A) op(B) + bias + beta * C_in)        (computed tile)
+//   C = epi(bias + beta * C_in)                             (Wildcat-culled)
+// applied once over the full K sum.  (The reference's default AVX2 packed NN
+// path applies the epilogue after the first 128-deep K block only,
+// kernels.cpp:313-323; this backend implements the documented semantics,
+// which its scalar, NT, row-stream and VNPU_PACK=0 paths also compute.)
+//
+// Two kernels:
+//   * gemm_f32_kernel: 128 x 128 workgroup tile, 2 x 2 waves of 64 x 64,
+//     v_mfma_f32_16x16x4_f32, both operands staged k-major in LDS (double
+//     buffered; row pitch 144 floats keeps fragment reads conflict free).
+//     trans_a / trans_b only change how a tile is fetched from HBM.
+//   * gemv_f32_kernel: M <= 8, NN (the MTP head and f32 decode GEMMs).  HBM
+//     bound: 256 columns x float4 per workgroup, waves and workgroups split K,
+//     activations read as wave-uniform scalars; partial sums reduced in a
+//     second deterministic pass when K is split across workgroups.
+#include "kernels.hpp"
+#include "device_math.hpp"
+
+namespace vnpu {
+namespace k {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int kThreads = 256;
+constexpr int kPitch = 144;
+
+// Loads 4 consecutive elements along the contiguous dimension of a matrix
+// stored with leading dimension ld: element (r, c0 + i), zero outside
+// rows x cols.
+__device__ __forceinline__ float4 load4(const float *base, uint32_t ld, uint32_t r, uint32_t c0,
+                                        uint32_t rows, uint32_t cols, bool vec)
+{
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r >= rows) return v;
+    const float *p = base + static_cast<uint64_t>(r) * ld + c0;
+    if (vec && c0 + 4 <= cols) return *reinterpret_cast<const float4 *>(p);
+    if (c0 + 0 < cols) v.x = p[0];
+    if (c0 + 1 < cols) v.y = p[1];
+    if (c0 + 2 < cols) v.z = p[2];
+    if (c0 + 3 < cols) v.w = p[3];
+    return v;
+}
+
+struct Stage {
+    float4 a0, a1, b0, b1;
+};
+
+// Fetch the (k0 .. k0+15) x tile slices of A (BM rows) and B (BN cols).
+// Thread mapping depends on which dimension is contiguous in memory.
+__device__ __forceinline__ void fetch(const F32Gemm &p, uint32_t m0, uint32_t n0, uint32_t k0,
+                                      int tid, bool va, bool vb, Stage &s)
+{
+    if (!p.trans_a) {  // A[m][k]: 128 rows x 4 float4 along k
+        const uint32_t r = tid >> 2, c = (tid & 3) * 4;
+        s.a0 = load4(p.A, p.lda, m0 + r, k0 + c, p.M, p.K, va);
+        s.a1 = load4(p.A, p.lda, m0 + r + 64, k0 + c, p.M, p.K, va);
+    } else {           // A[k][m]: 16 rows x 32 float4 along m
+        const uint32_t r = tid >> 5, c = (tid & 31) * 4;
+        s.a0 = load4(p.A, p.lda, k0 + r, m0 + c, p.K, p.M, va);
+        s.a1 = load4(p.A, p.lda, k0 + r + 8, m0 + c, p.K, p.M, va);
+    }
+    if (!p.trans_b) {  // B[k][n]: 16 rows x 32 float4 along n
+        const uint32_t r = tid >> 5, c = (tid & 31) * 4;
+        s.b0 = load4(p.B, p.ldb, k0 + r, n0 + c, p.K, p.N, vb);
+        s.b1 = load4(p.B, p.ldb, k0 + r + 8, n0 + c, p.K, p.N, vb);
+    } else {           // B[n][k]: 128 rows x 4 float4 along k
+        const uint32_t r = tid >> 2, c = (tid & 3) * 4;
+        s.b0 = load4(p.B, p.ldb, n0 + r, k0 + c, p.N, p.K, vb);
+        s.b1 = load4(p.B, p.ldb, n0 + r + 64, k0 + c, p.N, p.K, vb);
+    }
+}
+
+// Store a fetched stage k-major: As[k][m], Bs[k][n].
+__device__ __forceinline__ void stash(const F32Gemm &p, int tid, const Stage &s, float *As,
+                                      float *Bs)
+{
+    if (!p.trans_a) {
+        const uint32_t r = tid >> 2, c = (tid & 3) * 4;
+        As[(c + 0) * kPitch + r] = s.a0.x; As[(c + 1) * kPitch + r] = s.a0.y;
+        As[(c + 2) * kPitch + r] = s.a0.z; As[(c + 3) * kPitch + r] = s.a0.w;
+        As[(c + 0) * kPitch + r + 64] = s.a1.x; As[(c + 1) * kPitch + r + 64] = s.a1.y;
+        As[(c + 2) * kPitch + r + 64] = s.a1.z; As[(c + 3) * kPitch + r + 64] = s.a1.w;
+    } else {
+        const uint32_t r = tid >> 5, c = (tid & 31) * 4;
+        *reinterpret_cast<float4 *>(&As[r * kPitch + c]) = s.a0;
+        *reinterpret_cast<float4 *>(&As[(r + 8) * kPitch + c]) = s.a1;
+    }
+    if (!p.trans_b) {
+        const uint32_t r = tid >> 5, c = (tid & 31) * 4;
+        *reinterpret_cast<float4 *>(&Bs[r * kPitch + c]) = s.b0;
+        *reinterpret_cast<float4 *>(&Bs[(r + 8) * kPitch + c]) = s.b1;
+    } else {
+        const uint32_t r = tid >> 2, c = (tid & 3) * 4;
+        Bs[(c + 0) * kPitch + r] = s.b0.x; Bs[(c + 1) * kPitch + r] = s.b0.y;
+        Bs[(c + 2) * kPitch + r] = s.b0.z; Bs[(c + 3) * kPitch + r] = s.b0.w;
+        Bs[(c + 0) * kPitch + r + 64] = s.b1.x; Bs[(c + 1) * kPitch + r + 64] = s.b1.y;
+        Bs[(c + 2) * kPitch + r + 64] = s.b1.z; Bs[(c + 3) * kPitch + r + 64] = s.b1.w;
+    }
+}
+
+__device__ __forceinline__ bool culled(const F32Gemm &p, uint32_t m, uint32_t n)
+{
+    return p.cull[static_cast<uint64_t>(m / p.cull_tm) * p.cull_nt + n / p.cull_tn] != 0;
+}
+
+__device__ __forceinline__ void store_out(const F32Gemm &p, uint32_t m, uint32_t n, float acc,
+                                          bool cull)
+{
+    float *dst = p.C + static_cast<uint64_t>(m) * p.ldc + n;
+    float out;
+    if (cull) {
+        out = p.bias ? p.bias[n] : 0.0f;
+        if (p.beta != 0.0f) out += p.beta * *dst;
+    } else {
+        out = p.alpha * acc;
+        if (p.bias) out += p.bias[n];
+        if (p.beta != 0.0f) out += p.beta * *dst;
+    }
+    *dst = dev::epilogue(out, p.epilogue);
+}
+
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Gemm p)
+{
+    __shared__ __attribute__((aligned(16))) float As[2][BK * kPitch];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * kPitch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int fr = lane & 15, fg = lane >> 4;
+
+    uint8_t state = 0;
+    if (p.ktile_state) state = p.ktile_state[blockIdx.y * gridDim.x + blockIdx.x];
+
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    if (state != 1) {
+        const bool va = ((p.lda & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0);
+        const bool vb = ((p.ldb & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.B) & 15u) == 0);
+        const uint32_t KT = (p.K + BK - 1) / BK;
+        Stage st;
+        fetch(p, m0, n0, 0, tid, va, vb, st);
+        stash(p, tid, st, As[0], Bs[0]);
+        __syncthreads();
+        for (uint32_t kt = 0; kt < KT; ++kt) {
+            const int cur = kt & 1;
+            const bool more = kt + 1 < KT;
+            if (more) fetch(p, m0, n0, (kt + 1) * BK, tid, va, vb, st);
+            const float *as = As[cur];
+            const float *bs = Bs[cur];
+#pragma unroll
+            for (int kk = 0; kk < BK / 4; ++kk) {
+                float a[4], b[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = as[(kk * 4 + fg) * kPitch + wm * 64 + i * 16 + fr];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b[j] = bs[(kk * 4 + fg) * kPitch + wn * 64 + j * 16 + fr];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+            if (more) stash(p, tid, st, As[cur ^ 1], Bs[cur ^ 1]);
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t n = n0 + wn * 64 + j * 16 + fr;
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t m = m0 + wm * 64 + i * 16 + fg * 4 + r;
+                if (m >= p.M) continue;
+                const bool c = state == 1 ? true : (state == 2 ? culled(p, m, n) : false);
+                store_out(p, m, n, acc[i][j][r], c);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny NN path (M <= 8).
+// ---------------------------------------------------------------------------
+constexpr int kSkinnyCols = 256;  // 64 lanes x float4
+constexpr int kSkinnyUnroll = 8;
+
+template <int M>
+__global__ __launch_bounds__(kThreads) void gemv_f32_kernel(F32Gemm p, uint32_t k_per_split,
+                                                            float *ws, uint32_t splits)
+{
+    __shared__ float4 red[4][M][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t n = blockIdx.x * kSkinnyCols + lane * 4;
+    const uint32_t kb = blockIdx.y * k_per_split;
+    const uint32_t ke = min(p.K, kb + k_per_split);
+    const bool vb = ((p.ldb & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.B) & 15u) == 0);
+
+    float4 acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    for (uint32_t k = kb + wave; k < ke; k += 4 * kSkinnyUnroll) {
+        float4 b[kSkinnyUnroll];
+#pragma unroll
+        for (int u = 0; u < kSkinnyUnroll; ++u) {
+            const uint32_t kk = k + u * 4;
+            b[u] = kk < ke ? load4(p.B, p.ldb, kk, n, p.K, p.N, vb) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < kSkinnyUnroll; ++u) {
+            const uint32_t kk = k + u * 4;
+            if (kk >= ke) break;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float a = p.A[static_cast<uint64_t>(m) * p.lda + kk];
+                acc[m].x = fmaf(a, b[u].x, acc[m].x);
+                acc[m].y = fmaf(a, b[u].y, acc[m].y);
+                acc[m].z = fmaf(a, b[u].z, acc[m].z);
+                acc[m].w = fmaf(a, b[u].w, acc[m].w);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) red[tid >> 6][m][lane] = acc[m];
+    __syncthreads();
+    if (tid < 64) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float4 s = red[0][m][lane];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) {
+                const float4 t = red[w][m][lane];
+                s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+            }
+            const float v[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t nn = n + i;
+                if (nn >= p.N) continue;
+                if (splits > 1)
+                    ws[(static_cast<uint64_t>(blockIdx.y) * M + m) * p.N + nn] = v[i];
+                else
+                    store_out(p, m, nn, v[i], false);
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void gemv_f32_reduce(F32Gemm p, const float *ws,
+                                                            uint32_t splits)
+{
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
+    if (idx >= total) return;
+    const uint32_t m = static_cast<uint32_t>(idx / p.N), n = static_cast<uint32_t>(idx % p.N);
+    float s = 0.0f;
+    for (uint32_t i = 0; i < splits; ++i) s += ws[static_cast<uint64_t>(i) * total + idx];
+    store_out(p, m, n, s, false);
+}
+
+uint32_t skinny_splits(uint32_t N, uint32_t K)
+{
+    const uint32_t col_blocks = (N + kSkinnyCols - 1) / kSkinnyCols;
+    uint32_t splits = 1;
+    while (col_blocks * splits < 1024 && K / (splits * 2) >= 256) splits *= 2;
+    return splits;
+}
+
+template <int M>
+void launch_skinny(hipStream_t s, const F32Gemm &p, float *ws)
+{
+    const uint32_t splits = skinny_splits(p.N, p.K);
+    const uint32_t kps = (p.K + splits - 1) / splits;
+    dim3 grid((p.N + kSkinnyCols - 1) / kSkinnyCols, splits);
+    gemv_f32_kernel<M><<<grid, kThreads, 0, s>>>(p, kps, ws, splits);
+    if (splits > 1) {
+        const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
+        gemv_f32_reduce<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(p, ws, splits);
+    }
+}
+
+}  // namespace
+
+void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn)
+{
+    bm = BM;
+    bn = BN;
+}
+
+void gemm_f32(hipStream_t s, const F32Gemm &p)
+{
+    dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
+    gemm_f32_kernel<<<grid, kThreads, 0, s>>>(p);
+}
+
+size_t gemv_f32_ws_bytes(uint32_t M, uint32_t N, uint32_t K)
+{
+    const uint32_t splits = skinny_splits(N, K);
+    return splits > 1 ? static_cast<size_t>(splits) * M * N * sizeof(float) : 0;
+}
+
+void gemv_f32(hipStream_t s, const F32Gemm &p, float *ws)
+{
+    switch (p.M) {
+    case 1: launch_skinny<1>(s, p, ws); break;
+    case 2: launch_skinny<2>(s, p, ws); break;
+    case 3: launch_skinny<3>(s, p, ws); break;
+    case 4: launch_skinny<4>(s, p, ws); break;
+    case 5: launch_skinny<5>(s, p, ws); break;
+    case 6: launch_skinny<6>(s, p, ws); break;
+    case 7: launch_skinny<7>(s, p, ws); break;
+    case 8: launch_skinny<8>(s, p, ws); break;
+    default: break;
+    }
+}
+
+}  // namespace k
+}  // namespace vnpu

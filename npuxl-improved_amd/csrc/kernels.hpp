@@ -1,0 +1,103 @@
+// kernels.hpp - host-side launchers for the gfx950 kernels.
+//
+// Every launcher only enqueues work on the given stream; the command
+// processor (dispatch.cpp) has already validated shapes, so each launcher's
+// grid covers exactly the buffers described by its arguments.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace vnpu {
+namespace k {
+
+// ---- QUANTIZE_I8 (quantize.hip) ----
+void quantize_rows(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t rows,
+                   uint64_t cols);
+void quantize_cols(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t rows,
+                   uint64_t cols);
+// ws must hold quantize_tensor_ws_bytes() bytes.
+size_t quantize_tensor_ws_bytes();
+void quantize_tensor(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t count,
+                     float *ws);
+
+// ---- PACK_WEIGHTS_I8 (pack.hip) ----
+// Writes the fragment layout [Kp/64][Np/16][4][16][16] (zero padded), the
+// per-column sums [N] and the all-zero 1 KiB block map [Kp/64][Np/16].
+void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint32_t ldb,
+                    uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,
+                    int32_t *column_sums, uint8_t *zero_blocks);
+
+// ---- MATMUL_I8 (gemv_i8.hip, gemm_i8.hip) ----
+struct I8Gemm {
+    const int8_t *A = nullptr;   // [M][lda]
+    uint32_t lda = 0;
+    const int8_t *frag = nullptr;
+    const uint8_t *zero_blocks = nullptr;  // optional K-block skip map
+    uint32_t Kp = 0, Np = 0;
+    const float *scale_a = nullptr;  // [M] or null
+    const float *scale_b = nullptr;  // [Np]
+    const float *bias = nullptr;     // [N] or null
+    float *C = nullptr;              // [M][ldc]
+    uint32_t ldc = 0;
+    uint32_t M = 0, N = 0, K = 0;
+    uint32_t epilogue = 0;
+};
+void gemv_i8(hipStream_t s, const I8Gemm &p);  // M <= 8, no MFMA
+void gemm_i8(hipStream_t s, const I8Gemm &p);  // any M, v_mfma_i32_16x16x64_i8
+
+// ---- MATMUL_F32 (gemm_f32.hip) ----
+struct F32Gemm {
+    const float *A = nullptr, *B = nullptr, *bias = nullptr;
+    float *C = nullptr;
+    uint32_t M = 0, K = 0, N = 0;
+    uint32_t lda = 0, ldb = 0, ldc = 0;
+    uint32_t trans_a = 0, trans_b = 0;
+    float alpha = 1.0f, beta = 0.0f;
+    uint32_t epilogue = 0;
+    // Wildcat cull: a grid of (cull_tm x cull_tn) output tiles, cull_nt tiles
+    // per row of the grid, one byte per tile (1 = culled).  Null = no cull.
+    const uint8_t *cull = nullptr;
+    uint32_t cull_tm = 0, cull_tn = 0, cull_nt = 0;
+    // Per kernel-tile state derived from the cull grid: 0 compute, 1 fully
+    // culled (skip the K loop), 2 mixed.  Null when cull is null.
+    const uint8_t *ktile_state = nullptr;
+};
+void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn);
+void gemm_f32(hipStream_t s, const F32Gemm &p);
+// Skinny path: M <= 8, trans_a == 0, trans_b == 0, no cull.  ws holds
+// gemv_f32_ws_bytes(M, N, K) bytes.
+size_t gemv_f32_ws_bytes(uint32_t M, uint32_t N, uint32_t K);
+void gemv_f32(hipStream_t s, const F32Gemm &p, float *ws);
+
+// ---- transformer ops (ops.hip) ----
+void rmsnorm(hipStream_t s, const float *X, const float *W, float *Y, uint32_t rows,
+             uint32_t cols, float eps);
+void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t cols, float inv_t);
+// inv_freq: device table [head_dim/2] (half-rotation) or [head_dim/2] for the
+// interleaved pairs, computed on the host with the reference's powf expression.
+void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t batch,
+          uint32_t heads, uint32_t q_seq, uint32_t k_seq, uint32_t head_dim,
+          uint32_t position_offset, uint32_t interleaved, float scaling, const float *inv_freq);
+void swiglu(hipStream_t s, const float *g, const float *u, float *Y, uint64_t n, float alpha);
+void add(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha,
+         float beta);
+void mul(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha,
+         float beta);
+void gelu(hipStream_t s, const float *X, float *Y, uint64_t n);
+
+// ---- ATTENTION_F32 (attention.hip) ----
+struct Attn {
+    const float *Q = nullptr, *K = nullptr, *V = nullptr, *mask = nullptr;
+    float *O = nullptr;
+    uint32_t batch = 0, heads = 0, seq_q = 0, seq_k = 0, head_dim = 0, causal = 0;
+    float scale = 1.0f;
+};
+size_t attention_ws_bytes(const Attn &a);
+void attention(hipStream_t s, const Attn &a, float *ws);
+
+// ---- fills (ops.hip) ----
+void fill_u8(hipStream_t s, void *dst, uint8_t value, uint64_t bytes);
+
+}  // namespace k
+}  // namespace vnpu

@@ -1,0 +1,267 @@
+// ops.hip - bandwidth-bound transformer ops on gfx950.
+//
+// RMSNORM, SOFTMAX, ROPE, SWIGLU, ADD, MUL, GELU with the reference's
+// semantics and defaults (src/kernels/llm.cpp:64-330, 576-602;
+// src/core/scheduler.cpp:475-581).  Row ops use one workgroup per row with
+// wave-shuffle + LDS reductions; elementwise ops are grid-stride float4
+// streams.  All are HBM-bound: the algorithmic bytes are the reads and writes
+// of each element once (rows are re-read from cache between passes).
+#include "kernels.hpp"
+#include "device_math.hpp"
+
+namespace vnpu {
+namespace k {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float block_sum(float v, float *red)
+{
+    v = dev::wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) r += red[w];
+    return r;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red)
+{
+    v = dev::wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, red[w]);
+    return r;
+}
+
+// reference llm.cpp:64-108: inv = 1/sqrt(sum(x^2)/cols + eps); y = x*inv*w
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ X,
+                                                           const float *__restrict__ W,
+                                                           float *__restrict__ Y, uint32_t cols,
+                                                           float eps)
+{
+    __shared__ float red[kThreads / 64];
+    const uint64_t r = blockIdx.x;
+    const float *x = X + r * cols;
+    float *y = Y + r * cols;
+    float ss = 0.0f;
+    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) ss = fmaf(x[j], x[j], ss);
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) y[j] = x[j] * inv * (W ? W[j] : 1.0f);
+}
+
+__global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const float *__restrict__ X,
+                                                               const float *__restrict__ W,
+                                                               float *__restrict__ Y,
+                                                               uint32_t cols, float eps)
+{
+    __shared__ float red[kThreads / 64];
+    const uint64_t r = blockIdx.x;
+    const float4 *x = reinterpret_cast<const float4 *>(X + r * cols);
+    float4 *y = reinterpret_cast<float4 *>(Y + r * cols);
+    const float4 *w = reinterpret_cast<const float4 *>(W);
+    const uint32_t n4 = cols >> 2;
+    float ss = 0.0f;
+    for (uint32_t j = threadIdx.x; j < n4; j += kThreads) {
+        const float4 v = x[j];
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
+    ss = block_sum(ss, red);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    for (uint32_t j = threadIdx.x; j < n4; j += kThreads) {
+        const float4 v = x[j];
+        const float4 g = W ? w[j] : make_float4(1.f, 1.f, 1.f, 1.f);
+        y[j] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+    }
+}
+
+// reference llm.cpp:116-180 (exp is the reference's polynomial)
+__global__ __launch_bounds__(kThreads) void softmax_kernel(const float *__restrict__ X,
+                                                           float *__restrict__ Y, uint32_t cols,
+                                                           float inv_t)
+{
+    __shared__ float red[kThreads / 64];
+    const uint64_t r = blockIdx.x;
+    const float *x = X + r * cols;
+    float *y = Y + r * cols;
+    float mx = -__builtin_inff();
+    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) mx = fmaxf(mx, x[j]);
+    mx = block_max(mx, red);
+    float sum = 0.0f;
+    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) sum += dev::fast_expf((x[j] - mx) * inv_t);
+    sum = block_sum(sum, red);
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) y[j] = dev::fast_expf((x[j] - mx) * inv_t) * inv;
+}
+
+// reference llm.cpp:188-217, 576-602: one thread per rotated pair.
+__global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ Q, float *__restrict__ K,
+                                                        const int32_t *__restrict__ positions,
+                                                        uint64_t bh_count, uint32_t q_seq,
+                                                        uint32_t k_seq, uint32_t seq,
+                                                        uint32_t head_dim, uint32_t offset,
+                                                        uint32_t interleaved, float scaling,
+                                                        const float *__restrict__ inv_freq)
+{
+    const uint32_t half = head_dim / 2;
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const uint64_t total = bh_count * seq * half;
+    if (idx >= total) return;
+    const uint32_t j = static_cast<uint32_t>(idx % half);
+    const uint64_t tok = idx / half;
+    const uint32_t t = static_cast<uint32_t>(tok % seq);
+    const uint64_t bh = tok / seq;
+    const float pos = static_cast<float>(positions ? positions[t] : static_cast<int32_t>(t + offset));
+    const float angle = (pos * scaling) * inv_freq[j];
+    const float c = cosf(angle), s = sinf(angle);
+    const uint32_t i0 = interleaved ? 2 * j : j;
+    const uint32_t i1 = interleaved ? 2 * j + 1 : j + half;
+    if (Q && t < q_seq) {
+        float *x = Q + (bh * q_seq + t) * head_dim;
+        const float x0 = x[i0], x1 = x[i1];
+        x[i0] = x0 * c - x1 * s;
+        x[i1] = x0 * s + x1 * c;
+    }
+    if (K && t < k_seq) {
+        float *x = K + (bh * k_seq + t) * head_dim;
+        const float x0 = x[i0], x1 = x[i1];
+        x[i0] = x0 * c - x1 * s;
+        x[i1] = x0 * s + x1 * c;
+    }
+}
+
+enum EwOp { EW_SWIGLU = 0, EW_ADD = 1, EW_MUL = 2, EW_GELU = 3 };
+
+template <int OP>
+__device__ __forceinline__ float ew(float a, float b, float alpha, float beta)
+{
+    if (OP == EW_SWIGLU) return dev::silu(a) * b * alpha;        // llm.cpp:240-246
+    if (OP == EW_ADD) return fmaf(a, alpha, b * beta);           // llm.cpp:256-271
+    if (OP == EW_MUL) return fmaf(a * b, alpha, beta);           // llm.cpp:273-287
+    return dev::gelu_tanh(a);                                    // llm.cpp:248-253
+}
+
+template <int OP>
+__global__ __launch_bounds__(kThreads) void ew_vec_kernel(const float4 *__restrict__ A,
+                                                          const float4 *__restrict__ B,
+                                                          float4 *__restrict__ Y, uint64_t n4,
+                                                          float alpha, float beta)
+{
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4;
+         i += static_cast<uint64_t>(gridDim.x) * kThreads) {
+        const float4 a = A[i];
+        const float4 b = (OP == EW_GELU) ? a : B[i];
+        Y[i] = make_float4(ew<OP>(a.x, b.x, alpha, beta), ew<OP>(a.y, b.y, alpha, beta),
+                           ew<OP>(a.z, b.z, alpha, beta), ew<OP>(a.w, b.w, alpha, beta));
+    }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kThreads) void ew_kernel(const float *__restrict__ A,
+                                                      const float *__restrict__ B,
+                                                      float *__restrict__ Y, uint64_t n,
+                                                      float alpha, float beta)
+{
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * kThreads)
+        Y[i] = ew<OP>(A[i], (OP == EW_GELU) ? 0.0f : B[i], alpha, beta);
+}
+
+template <int OP>
+void launch_ew(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha,
+               float beta)
+{
+    const bool vec = (n % 4 == 0) && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(Y) |
+                                       (B ? reinterpret_cast<uintptr_t>(B) : 0)) % 16 == 0);
+    const uint64_t work = vec ? n / 4 : n;
+    uint64_t blocks = (work + kThreads - 1) / kThreads;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks == 0) blocks = 1;
+    if (vec)
+        ew_vec_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(
+            reinterpret_cast<const float4 *>(A), reinterpret_cast<const float4 *>(B),
+            reinterpret_cast<float4 *>(Y), n / 4, alpha, beta);
+    else
+        ew_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(A, B, Y, n, alpha, beta);
+}
+
+__global__ void fill_kernel(uint8_t *dst, uint8_t v, uint64_t n)
+{
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * kThreads)
+        dst[i] = v;
+}
+
+}  // namespace
+
+void rmsnorm(hipStream_t s, const float *X, const float *W, float *Y, uint32_t rows,
+             uint32_t cols, float eps)
+{
+    const bool vec = (cols % 4 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y) |
+                       (W ? reinterpret_cast<uintptr_t>(W) : 0)) % 16 == 0);
+    if (vec)
+        rmsnorm_vec_kernel<<<dim3(rows), kThreads, 0, s>>>(X, W, Y, cols, eps);
+    else
+        rmsnorm_kernel<<<dim3(rows), kThreads, 0, s>>>(X, W, Y, cols, eps);
+}
+
+void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t cols, float inv_t)
+{
+    softmax_kernel<<<dim3(rows), kThreads, 0, s>>>(X, Y, cols, inv_t);
+}
+
+void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t batch,
+          uint32_t heads, uint32_t q_seq, uint32_t k_seq, uint32_t head_dim,
+          uint32_t position_offset, uint32_t interleaved, float scaling, const float *inv_freq)
+{
+    const uint32_t seq = q_seq > k_seq ? q_seq : k_seq;
+    const uint64_t bh = static_cast<uint64_t>(batch) * heads;
+    const uint64_t total = bh * seq * (head_dim / 2);
+    if (!total) return;
+    rope_kernel<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
+        Q, K, positions, bh, q_seq, k_seq, seq, head_dim, position_offset, interleaved, scaling,
+        inv_freq);
+}
+
+void swiglu(hipStream_t s, const float *g, const float *u, float *Y, uint64_t n, float alpha)
+{
+    launch_ew<EW_SWIGLU>(s, g, u, Y, n, alpha, 0.0f);
+}
+
+void add(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha, float beta)
+{
+    launch_ew<EW_ADD>(s, A, B, Y, n, alpha, beta);
+}
+
+void mul(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha, float beta)
+{
+    launch_ew<EW_MUL>(s, A, B, Y, n, alpha, beta);
+}
+
+void gelu(hipStream_t s, const float *X, float *Y, uint64_t n)
+{
+    launch_ew<EW_GELU>(s, X, nullptr, Y, n, 0.0f, 0.0f);
+}
+
+void fill_u8(hipStream_t s, void *dst, uint8_t value, uint64_t bytes)
+{
+    uint64_t blocks = (bytes + kThreads - 1) / kThreads;
+    if (blocks > 8192) blocks = 8192;
+    if (!blocks) return;
+    fill_kernel<<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(static_cast<uint8_t *>(dst), value, bytes);
+}
+
+}  // namespace k
+}  // namespace vnpu

@@ -1,0 +1,203 @@
+// quantize.hip - QUANTIZE_I8 on gfx950 (symmetric int8, bit-exact).
+//
+// Semantics (reference src/kernels/llm.cpp:387-436, scheduler.cpp:430-473):
+//   scale = max|x| / 127 (zero or non-finite -> 1), inv = 1 / scale,
+//   q = clamp(round_half_away(x * inv), -128, 127).
+// Every step is an IEEE single operation with the reference's rounding:
+// __fdiv_rn / __fmul_rn pin the correctly rounded divide and multiply, and
+// roundf lowers to trunc + half-away adjust on AMDGPU.  Max ignores NaN
+// exactly as std::max(m, NaN) does (fmaxf returns the non-NaN operand).
+//
+// HBM-bound: per-row reads each element once (kept in registers between the
+// max pass and the quantize pass) and writes one byte, 5 bytes per element.
+#include "kernels.hpp"
+#include "device_math.hpp"
+
+namespace vnpu {
+namespace k {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ int8_t q8(float x, float inv)
+{
+    float q = roundf(__fmul_rn(x, inv));
+    // Plain compares, as the reference: a NaN passes both and converts to 0.
+    if (q > 127.0f) q = 127.0f;
+    if (q < -128.0f) q = -128.0f;
+    return q == q ? static_cast<int8_t>(static_cast<int>(q)) : static_cast<int8_t>(0);
+}
+
+__device__ __forceinline__ float scale_from_max(float maxabs)
+{
+    float scale = __fdiv_rn(maxabs, 127.0f);
+    if (!(scale > 0.0f) || !isfinite(scale)) scale = 1.0f;
+    return scale;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red)
+{
+    v = dev::wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) r = fmaxf(r, red[w]);
+    return r;
+}
+
+// One workgroup per row; the row stays in registers (VPT float4 per thread).
+template <int VPT>
+__global__ __launch_bounds__(kThreads) void quant_rows_reg(const float *__restrict__ X,
+                                                           int8_t *__restrict__ Y,
+                                                           float *__restrict__ scales,
+                                                           uint32_t cols)
+{
+    __shared__ float red[kThreads / 64];
+    const uint64_t r = blockIdx.x;
+    const float4 *row = reinterpret_cast<const float4 *>(X + r * cols);
+    const uint32_t n4 = cols >> 2;
+    float4 v[VPT];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const uint32_t j = threadIdx.x + i * kThreads;
+        v[i] = j < n4 ? row[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    const float scale = scale_from_max(block_max(m, red));
+    const float inv = __fdiv_rn(1.0f, scale);
+    if (threadIdx.x == 0) scales[r] = scale;
+    char4 *out = reinterpret_cast<char4 *>(Y + r * cols);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const uint32_t j = threadIdx.x + i * kThreads;
+        if (j < n4) out[j] = make_char4(q8(v[i].x, inv), q8(v[i].y, inv), q8(v[i].z, inv), q8(v[i].w, inv));
+    }
+}
+
+// Any row length / alignment: two passes over the row (second from cache).
+__global__ __launch_bounds__(kThreads) void quant_rows_any(const float *__restrict__ X,
+                                                           int8_t *__restrict__ Y,
+                                                           float *__restrict__ scales,
+                                                           uint64_t cols)
+{
+    __shared__ float red[kThreads / 64];
+    const uint64_t r = blockIdx.x;
+    const float *row = X + r * cols;
+    float m = 0.0f;
+    for (uint64_t j = threadIdx.x; j < cols; j += kThreads) m = fmaxf(m, fabsf(row[j]));
+    const float scale = scale_from_max(block_max(m, red));
+    const float inv = __fdiv_rn(1.0f, scale);
+    if (threadIdx.x == 0) scales[r] = scale;
+    for (uint64_t j = threadIdx.x; j < cols; j += kThreads) Y[r * cols + j] = q8(row[j], inv);
+}
+
+// 64 columns x 4 row groups per workgroup: per-column max, then quantize.
+__global__ __launch_bounds__(kThreads) void quant_cols(const float *__restrict__ X,
+                                                       int8_t *__restrict__ Y,
+                                                       float *__restrict__ scales,
+                                                       uint64_t rows, uint64_t cols)
+{
+    __shared__ float red[4][64];
+    __shared__ float inv_s[64];
+    const uint32_t cl = threadIdx.x & 63, rg = threadIdx.x >> 6;
+    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * 64 + cl;
+    float m = 0.0f;
+    if (c < cols)
+        for (uint64_t r = rg; r < rows; r += 4) m = fmaxf(m, fabsf(X[r * cols + c]));
+    red[rg][cl] = m;
+    __syncthreads();
+    if (rg == 0) {
+        const float mx = fmaxf(fmaxf(red[0][cl], red[1][cl]), fmaxf(red[2][cl], red[3][cl]));
+        const float scale = scale_from_max(mx);
+        inv_s[cl] = __fdiv_rn(1.0f, scale);
+        if (c < cols) scales[c] = scale;
+    }
+    __syncthreads();
+    const float inv = inv_s[cl];
+    if (c < cols)
+        for (uint64_t r = rg; r < rows; r += 4) Y[r * cols + c] = q8(X[r * cols + c], inv);
+}
+
+constexpr int kTensorBlocks = 1024;
+
+__global__ __launch_bounds__(kThreads) void tensor_partial_max(const float *__restrict__ X,
+                                                               uint64_t n, float *__restrict__ ws)
+{
+    __shared__ float red[kThreads / 64];
+    float m = 0.0f;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * kThreads)
+        m = fmaxf(m, fabsf(X[i]));
+    m = block_max(m, red);
+    if (threadIdx.x == 0) ws[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kThreads) void tensor_scale(const float *__restrict__ ws,
+                                                         float *__restrict__ scales)
+{
+    __shared__ float red[kThreads / 64];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < kTensorBlocks; i += kThreads) m = fmaxf(m, ws[i]);
+    m = block_max(m, red);
+    if (threadIdx.x == 0) scales[0] = scale_from_max(m);
+}
+
+// reference llm.cpp:430-436: inv = 1 / (scale > 0 ? scale : 1)
+__global__ __launch_bounds__(kThreads) void tensor_quant(const float *__restrict__ X,
+                                                         int8_t *__restrict__ Y, uint64_t n,
+                                                         const float *__restrict__ scales)
+{
+    const float s = scales[0];
+    const float inv = __fdiv_rn(1.0f, s > 0.0f ? s : 1.0f);
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+         i += static_cast<uint64_t>(gridDim.x) * kThreads)
+        Y[i] = q8(X[i], inv);
+}
+
+}  // namespace
+
+void quantize_rows(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t rows,
+                   uint64_t cols)
+{
+    const bool aligned = (cols % 4 == 0) && (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(Y) % 4 == 0);
+    const uint64_t n4 = cols / 4;
+    for (uint64_t r0 = 0; r0 < rows; r0 += 0x7fffffffull) {
+        const uint64_t nr = rows - r0 < 0x7fffffffull ? rows - r0 : 0x7fffffffull;
+        const float *x = X + r0 * cols;
+        int8_t *y = Y + r0 * cols;
+        float *sc = scales + r0;
+        dim3 grid(static_cast<uint32_t>(nr));
+        if (aligned && n4 <= kThreads * 1)
+            quant_rows_reg<1><<<grid, kThreads, 0, s>>>(x, y, sc, static_cast<uint32_t>(cols));
+        else if (aligned && n4 <= kThreads * 4)
+            quant_rows_reg<4><<<grid, kThreads, 0, s>>>(x, y, sc, static_cast<uint32_t>(cols));
+        else if (aligned && n4 <= kThreads * 12)
+            quant_rows_reg<12><<<grid, kThreads, 0, s>>>(x, y, sc, static_cast<uint32_t>(cols));
+        else
+            quant_rows_any<<<grid, kThreads, 0, s>>>(x, y, sc, cols);
+    }
+}
+
+void quantize_cols(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t rows,
+                   uint64_t cols)
+{
+    const uint64_t blocks = (cols + 63) / 64;
+    quant_cols<<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(X, Y, scales, rows, cols);
+}
+
+size_t quantize_tensor_ws_bytes() { return kTensorBlocks * sizeof(float); }
+
+void quantize_tensor(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t count,
+                     float *ws)
+{
+    tensor_partial_max<<<kTensorBlocks, kThreads, 0, s>>>(X, count, ws);
+    tensor_scale<<<1, kThreads, 0, s>>>(ws, scales);
+    tensor_quant<<<kTensorBlocks, kThreads, 0, s>>>(X, Y, count, scales);
+}
+
+}  // namespace k
+}  // namespace vnpu

@@ -1,0 +1,1195 @@
+// runtime.cpp - the vnpu C ABI on HIP (device, stream, event, buffer, trace).
+//
+// Replaces the reference runtime (src/core/runtime.cpp) and backend table
+// (src/core/backend.cpp).  The mapping:
+//   vnpu_device_create   -> a HIP device ordinal (VNPU_HIP_DEVICE, default 0)
+//   vnpu_stream_*        -> hipStream_t at default priority; submit enqueues
+//                           every command of the batch in order on the caller
+//                           thread, sync is hipStreamSynchronize
+//   vnpu_event_*         -> hipEvent_t recorded after the batch
+//   vnpu_buffer_*        -> hipMalloc'd HBM (zero filled, as the reference)
+//   Sherlock trace       -> hipEvent pairs around each command
+// Error behaviour follows the reference: submit only rejects a null stream or
+// an oversized batch; a failing command marks the batch event with its
+// status and makes every later sync of that stream return
+// VNPU_ERR_DEVICE_ERROR (sticky, runtime.cpp:1248-1254, 1281-1289).
+#include "vnpu_internal.hpp"
+#include "vnpu_backend.h"
+#include "kernels.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+#include <thread>
+
+namespace vnpu {
+
+void release_device_tables(vnpu_device_t *dev);
+
+bool debug_enabled()
+{
+    static const bool on = std::getenv("VNPU_DEBUG") != nullptr;
+    return on;
+}
+
+void debug_log(const char *fmt, ...)
+{
+    if (!debug_enabled()) return;
+    va_list ap;
+    va_start(ap, fmt);
+    std::fprintf(stderr, "[vnpu-mi355x] ");
+    std::vfprintf(stderr, fmt, ap);
+    std::fputc('\n', stderr);
+    va_end(ap);
+}
+
+static uint64_t now_ns()
+{
+    return static_cast<uint64_t>(std::chrono::duration_cast<std::chrono::nanoseconds>(
+                                     std::chrono::steady_clock::now().time_since_epoch())
+                                     .count());
+}
+
+void TraceState::reset()
+{
+    std::lock_guard<std::mutex> lock(mutex);
+    for (auto &r : records) {
+        if (r.start) (void)hipEventDestroy(r.start);
+        if (r.stop) (void)hipEventDestroy(r.stop);
+    }
+    records.clear();
+}
+
+void TraceState::resolve()
+{
+    std::lock_guard<std::mutex> lock(mutex);
+    for (auto &r : records) {
+        if (r.resolved) continue;
+        float ms = 0.0f;
+        if (r.start && r.stop && hipEventSynchronize(r.stop) == hipSuccess &&
+            hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess)
+            r.gpu_ns = static_cast<uint64_t>(static_cast<double>(ms) * 1e6);
+        else
+            (void)hipGetLastError();
+        if (r.start) (void)hipEventDestroy(r.start);
+        if (r.stop) (void)hipEventDestroy(r.stop);
+        r.start = r.stop = nullptr;
+        r.resolved = true;
+    }
+}
+
+static uint32_t trace_category(uint32_t opcode)
+{
+    if (opcode == VNPU_OP_COPY || opcode == VNPU_OP_MEMSET || opcode == VNPU_OP_PACK_WEIGHTS_I8)
+        return 1;  // memory
+    if (opcode == VNPU_OP_BARRIER || opcode == VNPU_OP_NOP) return 2;  // sync
+    return 0;  // compute
+}
+
+}  // namespace vnpu
+
+using namespace vnpu;
+
+void *vnpu_stream::ensure_workspace(size_t bytes)
+{
+    if (bytes == 0) return workspace;
+    if (bytes <= workspace_bytes) return workspace;
+    if (workspace) {
+        VNPU_HIP(hipStreamSynchronize(hip));
+        VNPU_HIP(hipFree(workspace));
+        workspace = nullptr;
+        workspace_bytes = 0;
+    }
+    size_t want = std::max<size_t>(bytes, 1u << 20);
+    VNPU_HIP(hipMalloc(&workspace, want));
+    workspace_bytes = want;
+    return workspace;
+}
+
+void vnpu_device::raise_irq(uint32_t bits)
+{
+    const uint32_t old = regs[VNPU_REG_IRQ_STATUS / 4].fetch_or(bits);
+    const uint32_t mask = regs[VNPU_REG_IRQ_MASK / 4].load();
+    if ((old & bits) == 0 && (mask & bits)) {
+        interrupts.fetch_add(1);
+        vnpu_interrupt_cb_t cb;
+        void *user;
+        {
+            std::lock_guard<std::mutex> lock(irq_mutex);
+            cb = irq_cb;
+            user = irq_user;
+        }
+        if (cb) cb(this, bits, user);
+    }
+}
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// Small helpers (reference runtime.cpp:636-815)
+// ---------------------------------------------------------------------------
+
+VNPU_API void VNPU_CALL vnpu_config_init(vnpu_config_t *config)
+{
+    if (!config) return;
+    std::memset(config, 0, sizeof(*config));
+    config->abi_version = VNPU_ABI_VERSION;
+    if (const char *t = std::getenv("VNPU_THREADS")) config->num_threads = static_cast<uint32_t>(std::atoi(t));
+    if (const char *t = std::getenv("VNPU_TRACE"))
+        if (std::atoi(t)) config->flags |= VNPU_CONFIG_TRACE;
+    if (const char *f = std::getenv("VNPU_TRACE_FILE")) config->trace_file = f;
+}
+
+VNPU_API const char *VNPU_CALL vnpu_status_string(vnpu_status_t status)
+{
+    switch (status) {
+    case VNPU_OK: return "OK";
+    case VNPU_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case VNPU_ERR_OUT_OF_MEMORY: return "out of memory";
+    case VNPU_ERR_UNSUPPORTED: return "unsupported";
+    case VNPU_ERR_INVALID_COMMAND: return "invalid command";
+    case VNPU_ERR_DEVICE_BUSY: return "device busy";
+    case VNPU_ERR_DEVICE_ERROR: return "device error";
+    case VNPU_ERR_TIMEOUT: return "timeout";
+    case VNPU_ERR_NETWORK: return "network error";
+    case VNPU_ERR_AUTH: return "authentication error";
+    case VNPU_ERR_PROTOCOL: return "protocol error";
+    case VNPU_ERR_NOT_FOUND: return "not found";
+    case VNPU_ERR_IO: return "I/O error";
+    default: return "internal error";
+    }
+}
+
+VNPU_API const char *VNPU_CALL vnpu_version_string(void) { return "vnpu 1.0.0 (MI355X gfx950)"; }
+
+VNPU_API uint32_t VNPU_CALL vnpu_abi_version(void) { return VNPU_ABI_VERSION; }
+
+VNPU_API const char *VNPU_CALL vnpu_opcode_name(uint32_t opcode)
+{
+    static const char *names[] = {"NOP", "MATMUL_F32", "MATMUL_I8", "RMSNORM_F32", "SOFTMAX_F32",
+                                  "ROPE_F32", "SWIGLU_F32", "GELU_F32", "ADD_F32", "MUL_F32",
+                                  "ATTENTION_F32", "QUANTIZE_I8", "PACK_WEIGHTS_I8",
+                                  "MTP_HEAD_F32", "COPY", "MEMSET", "BARRIER"};
+    return opcode < sizeof(names) / sizeof(names[0]) ? names[opcode] : "UNKNOWN";
+}
+
+VNPU_API const char *VNPU_CALL vnpu_unit_name(uint32_t unit)
+{
+    switch (unit) {
+    case VNPU_UNIT_AUTO: return "AUTO";
+    case VNPU_UNIT_VOODOO: return "VOODOO";
+    case VNPU_UNIT_WILDCAT: return "WILDCAT";
+    case VNPU_UNIT_CELL: return "CELL";
+    case VNPU_UNIT_GPU: return "GPU";
+    default: return "UNKNOWN";
+    }
+}
+
+// bf16: round to nearest even on the top 16 bits (reference runtime.cpp:730-736).
+VNPU_API uint16_t VNPU_CALL vnpu_float_to_bf16(float value)
+{
+    uint32_t u;
+    std::memcpy(&u, &value, 4);
+    return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+VNPU_API float VNPU_CALL vnpu_bf16_to_float(uint16_t value)
+{
+    const uint32_t u = static_cast<uint32_t>(value) << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// f16 conversions with the reference's rounding (runtime.cpp:746-785):
+// add half an ulp of the 13 dropped bits, then truncate.
+VNPU_API uint16_t VNPU_CALL vnpu_float_to_f16(float value)
+{
+    uint32_t f;
+    std::memcpy(&f, &value, 4);
+    const uint32_t sign = (f >> 16) & 0x8000u;
+    const int32_t e = static_cast<int32_t>((f >> 23) & 0xffu) - 112;
+    uint32_t mant = f & 0x7fffffu;
+    if (e <= 0) {
+        if (e < -10) return static_cast<uint16_t>(sign);
+        mant = (mant | 0x800000u) >> (1 - e);
+        return static_cast<uint16_t>(sign | ((mant + 0x1000u) >> 13));
+    }
+    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u | (mant ? 0x200u : 0u));
+    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(e) << 10) | ((mant + 0x1000u) >> 13));
+}
+
+VNPU_API float VNPU_CALL vnpu_f16_to_float(uint16_t value)
+{
+    const uint32_t sign = static_cast<uint32_t>(value & 0x8000u) << 16;
+    uint32_t e = (value >> 10) & 0x1fu;
+    uint32_t mant = value & 0x3ffu;
+    uint32_t f;
+    if (e == 0) {
+        if (mant == 0) {
+            f = sign;
+        } else {
+            e = 113;
+            while (!(mant & 0x400u)) {
+                mant <<= 1;
+                --e;
+            }
+            f = sign | (e << 23) | ((mant & 0x3ffu) << 13);
+        }
+    } else if (e == 31) {
+        f = sign | 0x7f800000u | (mant << 13);
+    } else {
+        f = sign | ((e + 112) << 23) | (mant << 13);
+    }
+    float out;
+    std::memcpy(&out, &f, 4);
+    return out;
+}
+
+VNPU_API void VNPU_CALL vnpu_cluster_config_init(vnpu_cluster_config_t *config)
+{
+    if (!config) return;
+    std::memset(config, 0, sizeof(*config));
+    config->abi_version = VNPU_ABI_VERSION;
+    config->num_streams = 1;
+    config->request_timeout_ms = 30000;
+    config->cluster_name = "vnpu-cluster";
+}
+
+VNPU_API void VNPU_CALL vnpu_speculative_config_init(vnpu_speculative_config_t *config)
+{
+    if (!config) return;
+    std::memset(config, 0, sizeof(*config));
+    config->abi_version = VNPU_ABI_VERSION;
+    config->gamma = 4;
+    config->vocab = 32000;
+    config->max_tokens = 16;
+    config->eos_token = 2;
+    config->seed = 1;
+}
+
+VNPU_API void VNPU_CALL vnpu_node_config_init(vnpu_node_config_t *config)
+{
+    if (!config) return;
+    std::memset(config, 0, sizeof(*config));
+    config->abi_version = VNPU_ABI_VERSION;
+    config->port = 9449;
+    config->bind_address = "0.0.0.0";
+    config->node_name = "vnpu-node";
+}
+
+// ---------------------------------------------------------------------------
+// Device lifecycle (reference runtime.cpp:817-1152)
+// ---------------------------------------------------------------------------
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_device_create(const vnpu_config_t *config,
+                                                    vnpu_device_t **out_device)
+{
+    if (!out_device) return VNPU_ERR_INVALID_ARGUMENT;
+    *out_device = nullptr;
+    return guard([&]() -> vnpu_status_t {
+        vnpu_config_t cfg;
+        vnpu_config_init(&cfg);
+        if (config) cfg = *config;
+        if (cfg.abi_version == 0) cfg.abi_version = VNPU_ABI_VERSION;
+        if (cfg.abi_version != VNPU_ABI_VERSION) return VNPU_ERR_UNSUPPORTED;
+
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+            (void)hipGetLastError();
+            debug_log("no HIP device visible: the MI355X backend needs a GPU");
+            return VNPU_ERR_UNSUPPORTED;
+        }
+        int ordinal = 0;
+        if (const char *e = std::getenv("VNPU_HIP_DEVICE")) ordinal = std::atoi(e);
+        if (ordinal < 0 || ordinal >= count) return VNPU_ERR_INVALID_ARGUMENT;
+        VNPU_HIP(hipSetDevice(ordinal));
+        hipDeviceProp_t prop;
+        VNPU_HIP(hipGetDeviceProperties(&prop, ordinal));
+
+        auto *d = new vnpu_device_t();
+        d->config = cfg;
+        d->hip_device = ordinal;
+        d->cu_count = static_cast<uint32_t>(prop.multiProcessorCount);
+        for (auto &r : d->regs) r.store(0);
+        d->name = cfg.node_name ? cfg.node_name : "vnpu0";
+
+        // The reference's AVX2 default tiles (runtime.cpp:923-933); on this
+        // backend they only shape Wildcat cull-mask sampling.
+        uint32_t tm = cfg.tile_m, tk = cfg.tile_k, tn = cfg.tile_n;
+        if (!tm || !tk || !tn) {
+            tm = 128;
+            tk = 128;
+            tn = 64;
+        }
+        d->tile_m.store(tm);
+        d->tile_k.store(tk);
+        d->tile_n.store(tn);
+        // "threads" = parallel units: the CU count unless the caller pins it.
+        const uint32_t units = cfg.num_threads ? cfg.num_threads : d->cu_count;
+
+        auto &info = d->info;
+        std::memset(&info, 0, sizeof(info));
+        info.abi_version = VNPU_ABI_VERSION;
+        std::snprintf(info.name, sizeof(info.name), "%s", d->name.c_str());
+        std::snprintf(info.vendor, sizeof(info.vendor), "AMD");
+        std::snprintf(info.cpu_arch, sizeof(info.cpu_arch), "%s", prop.gcnArchName);
+        std::snprintf(info.backend, sizeof(info.backend), "HIP %s (%s, %d CUs)", prop.gcnArchName,
+                      prop.name, prop.multiProcessorCount);
+        info.simd_bits = 64 * 32;  // one wave64 VGPR
+        info.num_threads = units;
+        info.num_compute_units = cfg.num_compute_units ? cfg.num_compute_units : d->cu_count;
+        info.local_store_bytes = static_cast<uint32_t>(prop.maxSharedMemoryPerMultiProcessor
+                                                           ? prop.maxSharedMemoryPerMultiProcessor
+                                                           : prop.sharedMemPerBlock);
+        info.tile_m = tm;
+        info.tile_k = tk;
+        info.tile_n = tn;
+        info.physical_cores = d->cu_count;
+        info.features = VNPU_FEATURE_THREADS | VNPU_FEATURE_TRACE | VNPU_FEATURE_GPU_FUTURE;
+        info.l1d_bytes = 32 * 1024;
+        info.l2_bytes = static_cast<uint64_t>(prop.l2CacheSize);
+        info.l3_bytes = 256ull << 20;  // Infinity Cache
+        info.total_memory_bytes = prop.totalGlobalMem;
+
+        d->regs[VNPU_REG_ID / 4].store(VNPU_MAGIC);
+        d->regs[VNPU_REG_VERSION / 4].store(VNPU_ABI_VERSION);
+        d->regs[VNPU_REG_CONTROL / 4].store(1);
+        d->regs[VNPU_REG_STATUS / 4].store(1);
+        d->regs[VNPU_REG_ACTIVE_CUS / 4].store(info.num_compute_units);
+        d->regs[VNPU_REG_CLOCK_MHZ / 4].store(static_cast<uint32_t>(prop.clockRate / 1000));
+        d->regs[VNPU_REG_FEATURE_LO / 4].store(static_cast<uint32_t>(info.features & 0xffffffffu));
+        d->regs[VNPU_REG_FEATURE_HI / 4].store(static_cast<uint32_t>(info.features >> 32));
+        d->regs[VNPU_REG_IRQ_MASK / 4].store(0xffffffffu);
+        d->trace.enabled.store((cfg.flags & VNPU_CONFIG_TRACE) != 0);
+        d->trace.trace_file = cfg.trace_file ? cfg.trace_file : "";
+        debug_log("created %s on HIP device %d (%s), %u CUs", d->name.c_str(), ordinal,
+                  prop.gcnArchName, d->cu_count);
+        *out_device = d;
+        return VNPU_OK;
+    });
+}
+
+static void destroy_stream_obj(vnpu_stream_t *s)
+{
+    if (!s) return;
+    if (s->hip) {
+        (void)hipStreamSynchronize(s->hip);
+        (void)hipStreamDestroy(s->hip);
+    }
+    if (s->workspace) (void)hipFree(s->workspace);
+    delete s;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_trace_write_chrome(const vnpu_device_t *device,
+                                                         const char *path);
+
+VNPU_API void VNPU_CALL vnpu_device_destroy(vnpu_device_t *device)
+{
+    if (!device) return;
+    std::vector<vnpu_stream_t *> streams;
+    {
+        std::lock_guard<std::mutex> lock(device->stream_mutex);
+        streams.swap(device->streams);
+    }
+    (void)hipSetDevice(device->hip_device);
+    for (auto *s : streams) destroy_stream_obj(s);
+    if ((device->config.flags & VNPU_CONFIG_TRACE_CHROME) && !device->trace.trace_file.empty())
+        vnpu_trace_write_chrome(device, device->trace.trace_file.c_str());
+    device->trace.reset();
+    release_device_tables(device);
+    delete device;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_device_get_info(const vnpu_device_t *device,
+                                                      vnpu_device_info_t *info)
+{
+    if (!device || !info) return VNPU_ERR_INVALID_ARGUMENT;
+    *info = device->info;
+    info->tile_m = device->tile_m.load();
+    info->tile_k = device->tile_k.load();
+    info->tile_n = device->tile_n.load();
+    return VNPU_OK;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_device_get_status(const vnpu_device_t *device,
+                                                        vnpu_device_status_t *status)
+{
+    if (!device || !status) return VNPU_ERR_INVALID_ARGUMENT;
+    std::memset(status, 0, sizeof(*status));
+    status->commands_submitted = device->commands_submitted.load();
+    status->commands_completed = device->commands_completed.load();
+    status->kernel_time_ns = device->kernel_ns.load();
+    status->dispatch_time_ns = device->dispatch_ns.load();
+    status->memory_time_ns = device->memory_ns.load();
+    status->sync_time_ns = device->sync_ns.load();
+    status->bytes_read = device->bytes_read.load();
+    status->bytes_written = device->bytes_written.load();
+    status->flops = device->flops.load();
+    status->tiles_dispatched = device->tiles_dispatched.load();
+    status->tiles_culled = device->tiles_culled.load();
+    status->dma_bytes = device->dma_bytes.load();
+    status->interrupts = device->interrupts.load();
+    status->busy = device->busy.load();
+    status->error = device->error.load();
+    status->last_opcode = device->last_opcode.load();
+    status->active_workers = device->active_workers.load();
+    return VNPU_OK;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_device_reset(vnpu_device_t *device)
+{
+    if (!device) return VNPU_ERR_INVALID_ARGUMENT;
+    if (device->busy.load()) return VNPU_ERR_DEVICE_BUSY;
+    for (auto *a : {&device->commands_submitted, &device->commands_completed, &device->kernel_ns,
+                    &device->dispatch_ns, &device->memory_ns, &device->sync_ns,
+                    &device->bytes_read, &device->bytes_written, &device->flops,
+                    &device->tiles_dispatched, &device->tiles_culled, &device->dma_bytes,
+                    &device->interrupts})
+        a->store(0);
+    device->error.store(0);
+    device->last_opcode.store(0);
+    device->regs[VNPU_REG_ERROR / 4].store(0);
+    device->regs[VNPU_REG_IRQ_STATUS / 4].store(0);
+    device->trace.reset();
+    return VNPU_OK;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_device_set_tiles(vnpu_device_t *device, uint32_t tile_m,
+                                                       uint32_t tile_k, uint32_t tile_n)
+{
+    if (!device || !tile_m || !tile_k || !tile_n) return VNPU_ERR_INVALID_ARGUMENT;
+    device->tile_m.store(tile_m);
+    device->tile_k.store(tile_k);
+    device->tile_n.store(tile_n);
+    device->info.tile_m = tile_m;
+    device->info.tile_k = tile_k;
+    device->info.tile_n = tile_n;
+    return VNPU_OK;
+}
+
+// MMIO register file (reference runtime.cpp:1102-1138)
+VNPU_API uint32_t VNPU_CALL vnpu_mmio_read32(vnpu_device_t *device, uint32_t offset)
+{
+    if (!device || (offset & 3u)) return 0xffffffffu;
+    const uint32_t idx = offset / 4;
+    if (idx >= VNPU_REG_COUNT) return 0xffffffffu;
+    switch (offset) {
+    case VNPU_REG_STATUS: return 1u | (device->busy.load() ? 2u : 0u);
+    case VNPU_REG_ERROR: return device->regs[idx].load() | (device->error.load() ? 1u : 0u);
+    case VNPU_REG_CMD_HEAD: return static_cast<uint32_t>(device->commands_completed.load());
+    case VNPU_REG_CMD_TAIL: return static_cast<uint32_t>(device->commands_submitted.load());
+    case VNPU_REG_ACTIVE_CUS: return device->active_workers.load();
+    case VNPU_REG_THERMAL: return 0;
+    default: return device->regs[idx].load();
+    }
+}
+
+VNPU_API void VNPU_CALL vnpu_mmio_write32(vnpu_device_t *device, uint32_t offset, uint32_t value)
+{
+    if (!device || (offset & 3u)) return;
+    const uint32_t idx = offset / 4;
+    if (idx >= VNPU_REG_COUNT) return;
+    device->regs[idx].store(value);
+    if (offset == VNPU_REG_DOORBELL && value)
+        device->raise_irq(1u << 0);
+    else if (offset == VNPU_REG_CONTROL && (value & 2u))
+        vnpu_device_reset(device);
+    else if (offset == VNPU_REG_IRQ_STATUS)
+        device->regs[idx].store(0);
+}
+
+VNPU_API void VNPU_CALL vnpu_device_set_interrupt_callback(vnpu_device_t *device,
+                                                           vnpu_interrupt_cb_t cb, void *user_data)
+{
+    if (!device) return;
+    std::lock_guard<std::mutex> lock(device->irq_mutex);
+    device->irq_cb = cb;
+    device->irq_user = user_data;
+}
+
+// ---------------------------------------------------------------------------
+// Events (reference runtime.cpp:1154-1209)
+// ---------------------------------------------------------------------------
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_event_create(vnpu_event_t **out_event)
+{
+    if (!out_event) return VNPU_ERR_INVALID_ARGUMENT;
+    *out_event = nullptr;
+    return guard([&]() -> vnpu_status_t {
+        *out_event = new vnpu_event_t();
+        return VNPU_OK;
+    });
+}
+
+VNPU_API void VNPU_CALL vnpu_event_destroy(vnpu_event_t *event)
+{
+    if (!event) return;
+    if (event->hip) {
+        (void)hipSetDevice(event->hip_device);
+        (void)hipEventSynchronize(event->hip);
+        (void)hipEventDestroy(event->hip);
+    }
+    delete event;
+}
+
+// Signalled = a batch was submitted with this event and the GPU passed it.
+static int event_ready(vnpu_event_t *e)
+{
+    if (e->host_signaled) return 1;
+    if (!e->submitted || !e->hip) return 0;
+    const hipError_t q = hipEventQuery(e->hip);
+    if (q == hipSuccess) return 1;
+    if (q == hipErrorNotReady) return 0;
+    (void)hipGetLastError();
+    return -1;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_event_wait(vnpu_event_t *event, uint32_t timeout_ms)
+{
+    if (!event) return VNPU_ERR_INVALID_ARGUMENT;
+    const auto deadline = std::chrono::steady_clock::now() + std::chrono::milliseconds(timeout_ms);
+    for (;;) {
+        {
+            std::lock_guard<std::mutex> lock(event->mutex);
+            const int r = event_ready(event);
+            if (r > 0) return event->status;
+            if (r < 0) return VNPU_ERR_DEVICE_ERROR;
+        }
+        if (std::chrono::steady_clock::now() >= deadline) return VNPU_ERR_TIMEOUT;
+        std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_event_query(const vnpu_event_t *event)
+{
+    if (!event) return VNPU_ERR_INVALID_ARGUMENT;
+    auto *e = const_cast<vnpu_event_t *>(event);
+    std::lock_guard<std::mutex> lock(e->mutex);
+    return event_ready(e) > 0 ? VNPU_OK : VNPU_ERR_DEVICE_BUSY;
+}
+
+// ---------------------------------------------------------------------------
+// Streams (reference runtime.cpp:1215-1361)
+// ---------------------------------------------------------------------------
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_create(vnpu_device_t *device, int priority,
+                                                    vnpu_stream_t **out_stream)
+{
+    if (!device || !out_stream) return VNPU_ERR_INVALID_ARGUMENT;
+    *out_stream = nullptr;
+    return guard([&]() -> vnpu_status_t {
+        VNPU_HIP(hipSetDevice(device->hip_device));
+        auto *s = new vnpu_stream_t();
+        s->device = device;
+        s->priority = priority;  // recorded only: every stream runs at default priority
+        hipError_t e = hipStreamCreate(&s->hip);
+        if (e != hipSuccess) {
+            delete s;
+            return VNPU_ERR_DEVICE_ERROR;
+        }
+        {
+            std::lock_guard<std::mutex> lock(device->stream_mutex);
+            device->streams.push_back(s);
+        }
+        *out_stream = s;
+        return VNPU_OK;
+    });
+}
+
+VNPU_API void VNPU_CALL vnpu_stream_destroy(vnpu_stream_t *stream)
+{
+    if (!stream) return;
+    if (vnpu_device_t *d = stream->device) {
+        std::lock_guard<std::mutex> lock(d->stream_mutex);
+        auto &v = d->streams;
+        v.erase(std::remove(v.begin(), v.end(), stream), v.end());
+        (void)hipSetDevice(d->hip_device);
+    }
+    destroy_stream_obj(stream);
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_sync(vnpu_stream_t *stream)
+{
+    if (!stream) return VNPU_ERR_INVALID_ARGUMENT;
+    const uint64_t t0 = now_ns();
+    hipError_t e;
+    {
+        std::lock_guard<std::mutex> lock(stream->mutex);
+        (void)hipSetDevice(stream->device->hip_device);
+        e = hipStreamSynchronize(stream->hip);
+    }
+    vnpu_device_t *d = stream->device;
+    d->sync_ns.fetch_add(now_ns() - t0);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        const uint32_t code = static_cast<uint32_t>(-VNPU_ERR_DEVICE_ERROR);
+        stream->last_error.store(code);
+        d->error.store(code);
+        d->regs[VNPU_REG_ERROR / 4].store(code);
+    }
+    const uint64_t pend = stream->pending.exchange(0);
+    d->commands_completed.fetch_add(pend);
+    d->regs[VNPU_REG_CMD_HEAD / 4].store(static_cast<uint32_t>(d->commands_completed.load()));
+    return stream->last_error.load() ? VNPU_ERR_DEVICE_ERROR : VNPU_OK;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
+                                                    const vnpu_command_t *commands, uint64_t count,
+                                                    vnpu_event_t *event)
+{
+    if (!stream || (!commands && count) || count > (1u << 24)) return VNPU_ERR_INVALID_ARGUMENT;
+    if (count == 0) {
+        if (event) {
+            std::lock_guard<std::mutex> lock(event->mutex);
+            event->host_signaled = true;
+            event->status = VNPU_OK;
+        }
+        return VNPU_OK;
+    }
+    return guard([&]() -> vnpu_status_t {
+        vnpu_device_t *d = stream->device;
+        uint32_t flags = 0;
+        for (uint64_t i = 0; i < count; ++i) flags |= commands[i].flags;
+        d->commands_submitted.fetch_add(count);
+        d->regs[VNPU_REG_CMD_TAIL / 4].store(static_cast<uint32_t>(d->commands_submitted.load()));
+        stream->pending.fetch_add(count);
+        vnpu_status_t batch_status = VNPU_OK;
+        const bool tracing = d->trace.enabled.load();
+        std::lock_guard<std::mutex> lock(stream->mutex);
+        VNPU_HIP(hipSetDevice(d->hip_device));
+        d->busy.fetch_add(1);
+        d->active_workers.fetch_add(1);
+        for (uint64_t i = 0; i < count; ++i) {
+            const vnpu_command_t &cmd = commands[i];
+            const uint64_t t0 = now_ns();
+            TraceRecord rec;
+            if (tracing) {
+                if (hipEventCreate(&rec.start) == hipSuccess) (void)hipEventRecord(rec.start, stream->hip);
+            }
+            ExecStats st;
+            vnpu_status_t rc = VNPU_OK;
+            if (cmd.opcode >= VNPU_OP_COUNT) {
+                rc = VNPU_ERR_INVALID_COMMAND;
+            } else {
+                try {
+                    d->last_opcode.store(cmd.opcode);
+                    execute_command(d, stream, cmd, flags, st);
+                } catch (const std::exception &ex) {
+                    debug_log("command %s failed: %s", vnpu_opcode_name(cmd.opcode), ex.what());
+                    (void)hipGetLastError();
+                    rc = VNPU_ERR_INTERNAL;
+                }
+            }
+            const uint64_t host = now_ns() - t0;
+            d->kernel_ns.fetch_add(host);
+            const uint32_t cat = trace_category(cmd.opcode);
+            if (cat == 1) d->memory_ns.fetch_add(host);
+            if (cat == 2) d->sync_ns.fetch_add(host);
+            d->bytes_read.fetch_add(st.bytes_read);
+            d->bytes_written.fetch_add(st.bytes_written);
+            d->flops.fetch_add(st.flops);
+            d->dma_bytes.fetch_add(st.dma_bytes);
+            d->tiles_dispatched.fetch_add(st.tiles_dispatched);
+            d->tiles_culled.fetch_add(st.tiles_culled);
+            if (tracing) {
+                if (hipEventCreate(&rec.stop) == hipSuccess) (void)hipEventRecord(rec.stop, stream->hip);
+                rec.opcode = cmd.opcode;
+                rec.unit = st.unit;
+                rec.id = cmd.id;
+                rec.bytes_read = st.bytes_read;
+                rec.bytes_written = st.bytes_written;
+                rec.flops = st.flops;
+                rec.host_ns = host;
+                if (rc != VNPU_OK) {
+                    if (rec.start) (void)hipEventDestroy(rec.start);
+                    if (rec.stop) (void)hipEventDestroy(rec.stop);
+                } else {
+                    std::lock_guard<std::mutex> tl(d->trace.mutex);
+                    if (d->trace.records.size() < 200000) d->trace.records.push_back(rec);
+                    else {
+                        (void)hipEventDestroy(rec.start);
+                        (void)hipEventDestroy(rec.stop);
+                    }
+                }
+            }
+            if (rc != VNPU_OK) {
+                batch_status = rc;
+                const uint32_t code = static_cast<uint32_t>(-rc);
+                d->error.store(code);
+                d->regs[VNPU_REG_ERROR / 4].store(code);
+                stream->last_error.store(code);
+            }
+        }
+        if (event) {
+            std::lock_guard<std::mutex> el(event->mutex);
+            if (event->hip && event->hip_device != d->hip_device) {
+                (void)hipEventDestroy(event->hip);
+                event->hip = nullptr;
+            }
+            if (!event->hip) {
+                VNPU_HIP(hipEventCreateWithFlags(&event->hip, hipEventDisableTiming));
+                event->hip_device = d->hip_device;
+            }
+            VNPU_HIP(hipEventRecord(event->hip, stream->hip));
+            event->submitted = true;
+            event->host_signaled = false;
+            event->status = batch_status;
+            event->command_count = count;
+        }
+        d->active_workers.fetch_sub(1);
+        d->busy.fetch_sub(1);
+        d->raise_irq(1u << 1);
+        return VNPU_OK;
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Buffers (reference runtime.cpp:1367-1440): HBM allocations.
+// ---------------------------------------------------------------------------
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_buffer_alloc(vnpu_device_t *device, uint64_t bytes,
+                                                   vnpu_buffer_t **out_buffer)
+{
+    if (!device || !bytes || !out_buffer) return VNPU_ERR_INVALID_ARGUMENT;
+    *out_buffer = nullptr;
+    return guard([&]() -> vnpu_status_t {
+        VNPU_HIP(hipSetDevice(device->hip_device));
+        void *p = nullptr;
+        if (hipMalloc(&p, static_cast<size_t>(bytes)) != hipSuccess) {
+            (void)hipGetLastError();
+            return VNPU_ERR_OUT_OF_MEMORY;
+        }
+        if (hipMemset(p, 0, static_cast<size_t>(bytes)) != hipSuccess) {
+            (void)hipFree(p);
+            return VNPU_ERR_DEVICE_ERROR;
+        }
+        auto *b = new vnpu_buffer_t();
+        b->device = device;
+        b->dev_ptr = p;
+        b->bytes = bytes;
+        static std::atomic<uint64_t> next{1};
+        b->handle = next.fetch_add(1);
+        *out_buffer = b;
+        return VNPU_OK;
+    });
+}
+
+VNPU_API void VNPU_CALL vnpu_buffer_free(vnpu_buffer_t *buffer)
+{
+    if (!buffer) return;
+    if (buffer->dev_ptr) {
+        (void)hipSetDevice(buffer->device->hip_device);
+        (void)hipFree(buffer->dev_ptr);
+    }
+    delete buffer;
+}
+
+VNPU_API void *VNPU_CALL vnpu_buffer_host_ptr(vnpu_buffer_t *buffer)
+{
+    return buffer ? buffer->dev_ptr : nullptr;
+}
+
+VNPU_API uint64_t VNPU_CALL vnpu_buffer_size(const vnpu_buffer_t *buffer)
+{
+    return buffer ? buffer->bytes : 0;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_buffer_copy(vnpu_stream_t *stream, void *dst, const void *src,
+                                                  uint64_t bytes, uint32_t direction)
+{
+    if (!stream || !dst || !src || !bytes) return VNPU_ERR_INVALID_ARGUMENT;
+    vnpu_command_t cmd{};
+    cmd.opcode = VNPU_OP_COPY;
+    cmd.args.copy.dst = dst;
+    cmd.args.copy.src = src;
+    cmd.args.copy.bytes = bytes;
+    cmd.args.copy.direction = direction;
+    vnpu_status_t rc = vnpu_stream_submit(stream, &cmd, 1, nullptr);
+    if (rc != VNPU_OK) return rc;
+    return vnpu_stream_sync(stream);
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_buffer_memset(vnpu_stream_t *stream, void *dst, uint32_t value,
+                                                    uint64_t bytes)
+{
+    if (!stream || !dst || !bytes) return VNPU_ERR_INVALID_ARGUMENT;
+    vnpu_command_t cmd{};
+    cmd.opcode = VNPU_OP_MEMSET;
+    cmd.args.memset.dst = dst;
+    cmd.args.memset.value = value;
+    cmd.args.memset.bytes = bytes;
+    vnpu_status_t rc = vnpu_stream_submit(stream, &cmd, 1, nullptr);
+    if (rc != VNPU_OK) return rc;
+    return vnpu_stream_sync(stream);
+}
+
+// ---------------------------------------------------------------------------
+// Packed weights
+// ---------------------------------------------------------------------------
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_pack_weights_i8(vnpu_device_t *device, const int8_t *B,
+                                                      const float *scales, uint32_t K, uint32_t N,
+                                                      uint32_t ldb, uint32_t trans_b,
+                                                      vnpu_packed_weights_t **out_weights)
+{
+    if (!device || !B || !out_weights || !K || !N || trans_b > 1) return VNPU_ERR_INVALID_ARGUMENT;
+    *out_weights = nullptr;
+    const uint32_t ld = ldb ? ldb : (trans_b ? K : N);
+    if (ld < (trans_b ? K : N)) return VNPU_ERR_INVALID_ARGUMENT;
+    return guard([&]() -> vnpu_status_t {
+        *out_weights = pack_weights(device, B, scales, K, N, ldb, trans_b);
+        return VNPU_OK;
+    });
+}
+
+VNPU_API void VNPU_CALL vnpu_packed_weights_destroy(vnpu_packed_weights_t *weights)
+{
+    destroy_packed(weights);
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_packed_weights_info(const vnpu_packed_weights_t *weights,
+                                                          uint32_t *K, uint32_t *N, uint64_t *bytes,
+                                                          const float **scales,
+                                                          const int32_t **column_sums)
+{
+    if (!weights) return VNPU_ERR_INVALID_ARGUMENT;
+    if (K) *K = weights->K;
+    if (N) *N = weights->N;
+    if (bytes) *bytes = weights->frag_bytes;
+    if (scales) *scales = weights->scales.data();
+    if (column_sums) *column_sums = weights->column_sums.data();
+    return VNPU_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Synchronous wrappers (reference scheduler.cpp:864-902)
+// ---------------------------------------------------------------------------
+
+#define VNPU_SYNC_WRAPPER(fn, op, field, type)                                \
+    VNPU_API vnpu_status_t VNPU_CALL fn(vnpu_stream_t *stream, const type *args) \
+    {                                                                          \
+        if (!stream || !args) return VNPU_ERR_INVALID_ARGUMENT;                \
+        vnpu_command_t cmd{};                                                  \
+        cmd.opcode = op;                                                       \
+        cmd.args.field = *args;                                                \
+        vnpu_status_t rc = vnpu_stream_submit(stream, &cmd, 1, nullptr);       \
+        if (rc != VNPU_OK) return rc;                                          \
+        return vnpu_stream_sync(stream);                                       \
+    }
+
+VNPU_SYNC_WRAPPER(vnpu_matmul_f32, VNPU_OP_MATMUL_F32, matmul_f32, vnpu_matmul_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_matmul_i8, VNPU_OP_MATMUL_I8, matmul_i8, vnpu_matmul_i8_args_t)
+VNPU_SYNC_WRAPPER(vnpu_quantize_i8, VNPU_OP_QUANTIZE_I8, quantize_i8, vnpu_quantize_i8_args_t)
+VNPU_SYNC_WRAPPER(vnpu_rmsnorm_f32, VNPU_OP_RMSNORM_F32, rmsnorm, vnpu_rmsnorm_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_softmax_f32, VNPU_OP_SOFTMAX_F32, softmax, vnpu_softmax_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_rope_f32, VNPU_OP_ROPE_F32, rope, vnpu_rope_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_swiglu_f32, VNPU_OP_SWIGLU_F32, swiglu, vnpu_swiglu_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_gelu_f32, VNPU_OP_GELU_F32, unary, vnpu_unary_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_add_f32, VNPU_OP_ADD_F32, binary, vnpu_binary_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_mul_f32, VNPU_OP_MUL_F32, binary, vnpu_binary_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_attention_f32, VNPU_OP_ATTENTION_F32, attention, vnpu_attention_f32_args_t)
+VNPU_SYNC_WRAPPER(vnpu_mtp_head_f32, VNPU_OP_MTP_HEAD_F32, mtp_head, vnpu_mtp_head_f32_args_t)
+
+#undef VNPU_SYNC_WRAPPER
+
+// ---------------------------------------------------------------------------
+// Sherlock trace (reference runtime.cpp:327-627, 1442-1479) on hipEvents.
+// ---------------------------------------------------------------------------
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_trace_enable(vnpu_device_t *device, int enable)
+{
+    if (!device) return VNPU_ERR_INVALID_ARGUMENT;
+    device->trace.enabled.store(enable != 0);
+    if (enable) device->trace.reset();
+    return VNPU_OK;
+}
+
+VNPU_API void VNPU_CALL vnpu_trace_reset(vnpu_device_t *device)
+{
+    if (device) device->trace.reset();
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_trace_get_summary(const vnpu_device_t *device,
+                                                        vnpu_trace_summary_t *summary)
+{
+    if (!device || !summary) return VNPU_ERR_INVALID_ARGUMENT;
+    auto &tr = const_cast<vnpu_device_t *>(device)->trace;
+    tr.resolve();
+    std::memset(summary, 0, sizeof(*summary));
+    std::lock_guard<std::mutex> lock(tr.mutex);
+    uint64_t per_op[VNPU_OP_COUNT] = {};
+    for (const auto &r : tr.records) {
+        summary->events++;
+        summary->total_time_ns += r.gpu_ns;
+        const uint32_t cat = trace_category(r.opcode);
+        if (cat == 0) summary->compute_time_ns += r.gpu_ns;
+        else if (cat == 1) summary->memory_time_ns += r.gpu_ns;
+        else summary->sync_time_ns += r.gpu_ns;
+        summary->dispatch_time_ns += r.host_ns > r.gpu_ns ? r.host_ns - r.gpu_ns : 0;
+        summary->bytes_read += r.bytes_read;
+        summary->bytes_written += r.bytes_written;
+        summary->flops += r.flops;
+        if (r.opcode < VNPU_OP_COUNT) per_op[r.opcode] += r.gpu_ns;
+    }
+    if (summary->total_time_ns) {
+        const double s = static_cast<double>(summary->total_time_ns) * 1e-9;
+        summary->achieved_gflops = static_cast<double>(summary->flops) / s * 1e-9;
+        summary->achieved_gbytes_s =
+            static_cast<double>(summary->bytes_read + summary->bytes_written) / s * 1e-9;
+    }
+    for (uint32_t op = 0; op < VNPU_OP_COUNT; ++op)
+        if (per_op[op] > summary->hot_time_ns) {
+            summary->hot_time_ns = per_op[op];
+            summary->hot_opcode = op;
+        }
+    summary->trace_overhead_ns = 0.0;
+    return VNPU_OK;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_trace_dump(const vnpu_device_t *device, const char *path)
+{
+    if (!device) return VNPU_ERR_INVALID_ARGUMENT;
+    vnpu_trace_summary_t s;
+    vnpu_trace_get_summary(device, &s);
+    std::ostringstream o;
+    o << "vnpu trace (" << device->info.backend << ")\n"
+      << "events " << s.events << ", gpu time " << s.total_time_ns / 1e6 << " ms\n"
+      << "compute " << s.compute_time_ns / 1e6 << " ms, memory " << s.memory_time_ns / 1e6
+      << " ms, sync " << s.sync_time_ns / 1e6 << " ms, host dispatch " << s.dispatch_time_ns / 1e6
+      << " ms\n"
+      << "achieved " << s.achieved_gflops << " GFLOP/s, " << s.achieved_gbytes_s << " GB/s\n"
+      << "hot opcode " << vnpu_opcode_name(s.hot_opcode) << " (" << s.hot_time_ns / 1e6 << " ms)\n";
+    const std::string text = o.str();
+    if (!path || !*path) {
+        std::fputs(text.c_str(), stderr);
+        return VNPU_OK;
+    }
+    std::ofstream f(path);
+    if (!f) return VNPU_ERR_IO;
+    f << text;
+    return f ? VNPU_OK : VNPU_ERR_IO;
+}
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_trace_write_chrome(const vnpu_device_t *device, const char *path)
+{
+    if (!device || !path) return VNPU_ERR_INVALID_ARGUMENT;
+    auto &tr = const_cast<vnpu_device_t *>(device)->trace;
+    tr.resolve();
+    std::ofstream f(path);
+    if (!f) return VNPU_ERR_IO;
+    std::lock_guard<std::mutex> lock(tr.mutex);
+    f << "{\"traceEvents\":[";
+    double ts = 0.0;
+    for (size_t i = 0; i < tr.records.size(); ++i) {
+        const auto &r = tr.records[i];
+        const double dur = static_cast<double>(r.gpu_ns) / 1000.0;
+        char buf[256];
+        std::snprintf(buf, sizeof(buf),
+                      "%s{\"name\":\"%s#%llu\",\"ph\":\"X\",\"pid\":0,\"tid\":0,\"ts\":%.3f,"
+                      "\"dur\":%.3f,\"args\":{\"bytes\":%llu,\"flops\":%llu}}",
+                      i ? "," : "", vnpu_opcode_name(r.opcode),
+                      static_cast<unsigned long long>(r.id), ts, dur,
+                      static_cast<unsigned long long>(r.bytes_read + r.bytes_written),
+                      static_cast<unsigned long long>(r.flops));
+        f << buf;
+        ts += dur;
+    }
+    f << "]}\n";
+    return f ? VNPU_OK : VNPU_ERR_IO;
+}
+
+// ---------------------------------------------------------------------------
+// Autotune (reference autotune.cpp:153-281): times the GPU GEMM for the
+// shape with hipEvents.  The kernel tile is fixed per dtype, so the sweep has
+// one candidate; the result reports it.
+// ---------------------------------------------------------------------------
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint32_t M, uint32_t K,
+                                                    uint32_t N, uint32_t iterations,
+                                                    vnpu_dtype_t dtype, vnpu_tune_result_t *result)
+{
+    if (!device || !result || !M || !K || !N) return VNPU_ERR_INVALID_ARGUMENT;
+    if (dtype != VNPU_DTYPE_F32 && dtype != VNPU_DTYPE_I8) return VNPU_ERR_UNSUPPORTED;
+    return guard([&]() -> vnpu_status_t {
+        std::memset(result, 0, sizeof(*result));
+        vnpu_stream_t *s = nullptr;
+        vnpu_status_t rc = vnpu_stream_create(device, 0, &s);
+        if (rc != VNPU_OK) return rc;
+        struct StreamGuard {
+            vnpu_stream_t *s;
+            ~StreamGuard() { vnpu_stream_destroy(s); }
+        } sgd{s};
+        const bool i8 = dtype == VNPU_DTYPE_I8;
+        const size_t ea = i8 ? 1 : 4;
+        void *A = nullptr, *B = nullptr, *C = nullptr;
+        VNPU_HIP(hipMalloc(&A, static_cast<size_t>(M) * K * ea));
+        VNPU_HIP(hipMalloc(&B, static_cast<size_t>(K) * N * ea));
+        VNPU_HIP(hipMalloc(&C, static_cast<size_t>(M) * N * 4));
+        VNPU_HIP(hipMemset(A, 1, static_cast<size_t>(M) * K * ea));
+        VNPU_HIP(hipMemset(B, 1, static_cast<size_t>(K) * N * ea));
+        vnpu_packed_weights_t *w = nullptr;
+        vnpu_command_t cmd{};
+        if (i8) {
+            w = pack_weights(device, static_cast<int8_t *>(B), nullptr, K, N, 0, 0);
+            cmd.opcode = VNPU_OP_MATMUL_I8;
+            cmd.args.matmul_i8.A = static_cast<int8_t *>(A);
+            cmd.args.matmul_i8.B = w;
+            cmd.args.matmul_i8.C = static_cast<float *>(C);
+            cmd.args.matmul_i8.M = M;
+            cmd.args.matmul_i8.K = K;
+            cmd.args.matmul_i8.N = N;
+        } else {
+            cmd.opcode = VNPU_OP_MATMUL_F32;
+            cmd.args.matmul_f32.A = static_cast<float *>(A);
+            cmd.args.matmul_f32.B = static_cast<float *>(B);
+            cmd.args.matmul_f32.C = static_cast<float *>(C);
+            cmd.args.matmul_f32.M = M;
+            cmd.args.matmul_f32.K = K;
+            cmd.args.matmul_f32.N = N;
+            cmd.args.matmul_f32.alpha = 1.0f;
+        }
+        const uint32_t iters = iterations ? iterations : 3;
+        hipEvent_t e0, e1;
+        VNPU_HIP(hipEventCreate(&e0));
+        VNPU_HIP(hipEventCreate(&e1));
+        rc = vnpu_stream_submit(s, &cmd, 1, nullptr);
+        if (rc == VNPU_OK) rc = vnpu_stream_sync(s);
+        double best = 1e30;
+        for (uint32_t i = 0; rc == VNPU_OK && i < iters; ++i) {
+            VNPU_HIP(hipEventRecord(e0, s->hip));
+            rc = vnpu_stream_submit(s, &cmd, 1, nullptr);
+            VNPU_HIP(hipEventRecord(e1, s->hip));
+            if (rc == VNPU_OK) rc = vnpu_stream_sync(s);
+            float ms = 0.0f;
+            VNPU_HIP(hipEventElapsedTime(&ms, e0, e1));
+            best = std::min(best, static_cast<double>(ms));
+        }
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        if (w) destroy_packed(w);
+        (void)hipFree(A);
+        (void)hipFree(B);
+        (void)hipFree(C);
+        if (rc != VNPU_OK) return rc;
+        result->tile_m = 128;
+        result->tile_k = i8 ? 64 : 16;
+        result->tile_n = 128;
+        result->unit = VNPU_UNIT_GPU;
+        result->threads = device->cu_count;
+        result->best_ms = best;
+        result->baseline_ms = best;
+        result->speedup = 1.0;
+        result->gflops = 2.0 * M * K * N / (best * 1e-3) * 1e-9;
+        result->bytes_read = static_cast<uint64_t>(M) * K * ea + static_cast<uint64_t>(K) * N * ea;
+        result->bytes_written = static_cast<uint64_t>(M) * N * 4;
+        return VNPU_OK;
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Multi-host cluster, remote node and speculative API: not provided by this
+// single-GPU backend (reference src/cluster/*).  Every entry point exists so
+// the ABI and the backend table are complete; each reports UNSUPPORTED.
+// ---------------------------------------------------------------------------
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_create(const vnpu_cluster_config_t *, vnpu_cluster_t **out)
+{
+    if (out) *out = nullptr;
+    return VNPU_ERR_UNSUPPORTED;
+}
+VNPU_API void VNPU_CALL vnpu_cluster_destroy(vnpu_cluster_t *) {}
+VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_add_device(vnpu_cluster_t *, vnpu_device_t *, uint32_t)
+{
+    return VNPU_ERR_UNSUPPORTED;
+}
+VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_add_remote(vnpu_cluster_t *, const vnpu_remote_node_config_t *,
+                                                         vnpu_remote_node_t **out)
+{
+    if (out) *out = nullptr;
+    return VNPU_ERR_UNSUPPORTED;
+}
+VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_get_stats(const vnpu_cluster_t *, vnpu_cluster_stats_t *)
+{
+    return VNPU_ERR_UNSUPPORTED;
+}
+VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_cache_weights_f32(vnpu_cluster_t *, const char *, const float *,
+                                                                uint32_t, uint32_t, uint32_t,
+                                                                vnpu_weight_handle_t **out)
+{
+    if (out) *out = nullptr;
+    return VNPU_ERR_UNSUPPORTED;
+}
+VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_matmul_f32(vnpu_cluster_t *, vnpu_weight_handle_t *, const float *,
+                                                         float *, uint32_t, uint32_t, uint32_t, uint32_t)
+{
+    return VNPU_ERR_UNSUPPORTED;
+}
+VNPU_API vnpu_status_t VNPU_CALL vnpu_node_run(const vnpu_node_config_t *) { return VNPU_ERR_UNSUPPORTED; }
+VNPU_API void VNPU_CALL vnpu_node_stop(void) {}
+VNPU_API vnpu_status_t VNPU_CALL vnpu_speculative_step(vnpu_cluster_t *, const vnpu_speculative_config_t *,
+                                                       const int32_t *, uint32_t, vnpu_logits_fn_t, void *,
+                                                       vnpu_logits_fn_t, void *, vnpu_speculative_result_t *)
+{
+    return VNPU_ERR_UNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
+// Backend table (reference src/core/backend.cpp:8-60), same entry order.
+// ---------------------------------------------------------------------------
+
+static const vnpu_backend_v1_t g_backend_v1 = {
+    VNPU_ABI_VERSION,
+    sizeof(vnpu_backend_v1_t),
+    "vnpu MI355X (gfx950 HIP)",
+    vnpu_device_create,
+    vnpu_device_destroy,
+    vnpu_device_get_info,
+    vnpu_device_get_status,
+    vnpu_stream_create,
+    vnpu_stream_destroy,
+    vnpu_stream_sync,
+    vnpu_stream_submit,
+    vnpu_event_create,
+    vnpu_event_destroy,
+    vnpu_event_wait,
+    vnpu_buffer_alloc,
+    vnpu_buffer_free,
+    vnpu_buffer_host_ptr,
+    vnpu_matmul_f32,
+    vnpu_matmul_i8,
+    vnpu_quantize_i8,
+    vnpu_pack_weights_i8,
+    vnpu_packed_weights_destroy,
+    vnpu_rmsnorm_f32,
+    vnpu_softmax_f32,
+    vnpu_rope_f32,
+    vnpu_swiglu_f32,
+    vnpu_gelu_f32,
+    vnpu_attention_f32,
+    vnpu_mtp_head_f32,
+    vnpu_trace_enable,
+    vnpu_trace_get_summary,
+    vnpu_trace_dump,
+    vnpu_trace_write_chrome,
+    vnpu_autotune_gemm,
+    vnpu_cluster_create,
+    vnpu_cluster_destroy,
+    vnpu_cluster_add_device,
+    vnpu_cluster_add_remote,
+    vnpu_cluster_cache_weights_f32,
+    vnpu_cluster_matmul_f32,
+    vnpu_cluster_get_stats,
+    vnpu_node_run,
+    vnpu_speculative_step,
+    vnpu_status_string,
+    vnpu_version_string,
+    {}};
+
+VNPU_API const vnpu_backend_v1_t *VNPU_CALL vnpu_get_backend_v1(void) { return &g_backend_v1; }
+
+}  // extern "C"

@@ -1,0 +1,193 @@
+// vnpu_internal.hpp - private object model of the MI355X vnpu backend.
+//
+// The reference runtime keeps its opaque objects in src/internal.h:618-725
+// (device with a CPU thread pool, stream with a worker thread, event with a
+// condition variable, host buffers).  Here the same handles wrap HIP objects:
+//   vnpu_device  -> one HIP device (ordinal), counters, trace, MMIO registers
+//   vnpu_stream  -> one hipStream_t plus a growable device workspace
+//   vnpu_event   -> one hipEvent_t recorded at the end of a submitted batch
+//   vnpu_buffer  -> one hipMalloc allocation in HBM
+//   vnpu_packed_weights -> int8 weights in HBM in the MFMA fragment layout
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "vnpu.h"
+
+namespace vnpu {
+
+// A HIP failure inside a command becomes a command failure (sticky stream
+// error), never an abort; no C++ exception crosses the C ABI.
+struct HipError : std::runtime_error {
+    explicit HipError(const std::string &s) : std::runtime_error(s) {}
+};
+
+#define VNPU_HIP(expr)                                                           \
+    do {                                                                         \
+        hipError_t _e = (expr);                                                  \
+        if (_e != hipSuccess)                                                    \
+            throw ::vnpu::HipError(std::string(#expr) + ": " + hipGetErrorString(_e)); \
+    } while (0)
+
+struct ArgError : std::runtime_error {
+    explicit ArgError(const char *s) : std::runtime_error(s) {}
+};
+
+bool debug_enabled();
+void debug_log(const char *fmt, ...);
+
+template <typename F>
+inline vnpu_status_t guard(F &&fn) noexcept
+{
+    try {
+        return fn();
+    } catch (const std::bad_alloc &) {
+        return VNPU_ERR_OUT_OF_MEMORY;
+    } catch (const std::exception &e) {
+        debug_log("exception: %s", e.what());
+        return VNPU_ERR_INTERNAL;
+    } catch (...) {
+        return VNPU_ERR_INTERNAL;
+    }
+}
+
+// One traced command: host-side accounting plus a pair of hipEvents on the
+// command's stream (resolved lazily when a summary is requested).
+struct TraceRecord {
+    uint32_t opcode = 0;
+    uint32_t unit = 0;
+    uint64_t id = 0;
+    uint64_t bytes_read = 0;
+    uint64_t bytes_written = 0;
+    uint64_t flops = 0;
+    uint64_t host_ns = 0;
+    uint64_t gpu_ns = 0;
+    bool resolved = false;
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
+struct TraceState {
+    std::atomic<bool> enabled{false};
+    std::mutex mutex;
+    std::vector<TraceRecord> records;
+    std::string trace_file;
+    void reset();
+    void resolve();  // waits for and converts pending hipEvent pairs
+};
+
+}  // namespace vnpu
+
+struct vnpu_event {
+    std::mutex mutex;
+    hipEvent_t hip = nullptr;      // recorded at the end of the last batch
+    int hip_device = -1;
+    bool submitted = false;        // a batch carrying this event was submitted
+    bool host_signaled = false;    // completed without GPU work (empty batch)
+    vnpu_status_t status = VNPU_OK;
+    uint64_t command_count = 0;
+};
+
+struct vnpu_buffer {
+    vnpu_device_t *device = nullptr;
+    void *dev_ptr = nullptr;
+    uint64_t bytes = 0;
+    uint64_t handle = 0;
+};
+
+struct vnpu_packed_weights {
+    vnpu_device_t *device = nullptr;
+    uint32_t K = 0, N = 0;
+    uint32_t Kp = 0;               // K rounded up to 64
+    uint32_t Np = 0;               // N rounded up to 16
+    int8_t *frag = nullptr;        // HBM, [Kp/64][Np/16][4][16][16] fragment layout
+    float *scales_dev = nullptr;   // HBM [Np], padding = 1
+    uint8_t *zero_blocks = nullptr;// HBM [Kp/64][Np/16]: 1 = all 1 KiB of the block zero
+    uint64_t zero_block_count = 0;
+    uint64_t frag_bytes = 0;
+    std::vector<float> scales;     // host copies for vnpu_packed_weights_info
+    std::vector<int32_t> column_sums;
+};
+
+struct vnpu_stream {
+    vnpu_device_t *device = nullptr;
+    int priority = 0;
+    hipStream_t hip = nullptr;
+    std::mutex mutex;              // one submitter at a time per stream
+    std::atomic<uint32_t> last_error{0};
+    std::atomic<uint64_t> pending{0};
+    void *workspace = nullptr;
+    size_t workspace_bytes = 0;
+    void *ensure_workspace(size_t bytes);
+};
+
+struct vnpu_device {
+    vnpu_config_t config{};
+    vnpu_device_info_t info{};
+    int hip_device = 0;
+    uint32_t cu_count = 0;
+    vnpu::TraceState trace;
+    std::atomic<uint32_t> regs[VNPU_REG_COUNT];
+    std::atomic<uint64_t> commands_submitted{0};
+    std::atomic<uint64_t> commands_completed{0};
+    std::atomic<uint64_t> kernel_ns{0};
+    std::atomic<uint64_t> dispatch_ns{0};
+    std::atomic<uint64_t> memory_ns{0};
+    std::atomic<uint64_t> sync_ns{0};
+    std::atomic<uint64_t> bytes_read{0};
+    std::atomic<uint64_t> bytes_written{0};
+    std::atomic<uint64_t> flops{0};
+    std::atomic<uint64_t> tiles_dispatched{0};
+    std::atomic<uint64_t> tiles_culled{0};
+    std::atomic<uint64_t> dma_bytes{0};
+    std::atomic<uint64_t> interrupts{0};
+    std::atomic<uint32_t> busy{0};
+    std::atomic<uint32_t> error{0};
+    std::atomic<uint32_t> active_workers{0};
+    std::atomic<uint32_t> last_opcode{0};
+    std::atomic<uint32_t> tile_m{0}, tile_k{0}, tile_n{0};
+    std::vector<vnpu_stream_t *> streams;
+    std::mutex stream_mutex;
+    vnpu_interrupt_cb_t irq_cb = nullptr;
+    void *irq_user = nullptr;
+    std::mutex irq_mutex;
+    std::string name;
+    void raise_irq(uint32_t bits);
+};
+
+namespace vnpu {
+
+// Accounting for one command, mirroring the reference's per-op byte/flop
+// model (src/core/scheduler.cpp execute_* functions).
+struct ExecStats {
+    uint64_t bytes_read = 0;
+    uint64_t bytes_written = 0;
+    uint64_t flops = 0;
+    uint64_t dma_bytes = 0;
+    uint64_t tiles_dispatched = 0;
+    uint64_t tiles_culled = 0;
+    uint32_t unit = 0;
+};
+
+// Executes one command on the stream (enqueue only).  Throws ArgError for
+// invalid arguments and HipError for runtime failures.
+void execute_command(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &cmd,
+                     uint32_t batch_flags, ExecStats &st);
+
+// Pack int8 weights (synchronous); B may be a host or a device pointer.
+vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const float *scales,
+                                    uint32_t K, uint32_t N, uint32_t ldb, uint32_t trans_b);
+void destroy_packed(vnpu_packed_weights_t *w);
+
+bool is_device_pointer(const void *p);
+
+}  // namespace vnpu

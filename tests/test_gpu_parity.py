@@ -1,0 +1,336 @@
+"""GPU parity: libvnpu.so (HIP, gfx950) against the C oracle, through the C ABI.
+
+Bars (from the task's parity contract):
+  * int8 tensors, scales and int32 accumulators bit-exact;
+  * MATMUL_I8 f32 output bit-exact without bias (same (acc*sa)*sb order),
+    rtol 1e-4 normalized with bias/epilogue;
+  * f32 ops max|d| / max(1, max|ref|) <= 1e-4; attention <= 2e-3.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+import gpu_ops as g
+from vnpu_mi355x import abi
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(20261201)
+
+
+def rel(a, b):
+    return oracle.rel_error(a, b)
+
+
+# ---------------------------------------------------------------- quantize
+@pytest.mark.parametrize("shape", [(1, 1), (3, 7), (17, 300), (64, 512), (5, 4099), (2, 4096),
+                                   (8, 11008), (3, 20000)])
+@pytest.mark.parametrize("axis", [0, 1, 2])
+def test_quantize_bit_exact(gpu, shape, axis):
+    X = RNG.standard_normal(shape).astype(np.float32) * 3
+    yg, sg = g.quantize(gpu, X, axis)
+    yo, so = oracle.quantize(X, axis)
+    assert np.array_equal(sg.view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(yg, yo)
+
+
+@pytest.mark.parametrize("axis", [0, 1, 2])
+def test_quantize_ties_zero_nonfinite(gpu, axis):
+    X = RNG.integers(-100, 100, size=(8, 33)).astype(np.float32) + 0.5
+    X[:, 0] = 127.0
+    X[2] = 0.0
+    X[3, 5] = np.inf
+    X[4, 7] = np.nan
+    X[5, 1] = -np.inf
+    yg, sg = g.quantize(gpu, X, axis)
+    yo, so = oracle.quantize(X, axis)
+    assert np.array_equal(sg.view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(yg, yo)
+
+
+def test_quantize_many_ties_full_row(gpu):
+    # 2048 x 4096 activation row block: counts the exact-tie elements and
+    # requires every byte to match (ties are where rint vs round differ).
+    X = RNG.standard_normal((256, 4096)).astype(np.float32)
+    yg, sg = g.quantize(gpu, X, 0)
+    yo, so = oracle.quantize(X, 0)
+    assert np.array_equal(sg.view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(yg, yo)
+
+
+# ---------------------------------------------------------------- pack
+@pytest.mark.parametrize("K,N,trans_b", [(37, 29, 0), (64, 16, 0), (100, 70, 1), (4096, 300, 0)])
+def test_pack_info(gpu, K, N, trans_b):
+    B = RNG.integers(-128, 128, size=(N, K) if trans_b else (K, N)).astype(np.int8)
+    scales = RNG.random(N).astype(np.float32) + 0.1
+    w = gpu.pack(B, K, N, scales=scales, trans_b=trans_b)
+    k, n, nbytes, sc, cs = gpu.unpack_info(w)
+    _, sums = oracle.pack_canonical(B, K, N, 0, trans_b)
+    assert (k, n) == (K, N)
+    assert nbytes == ((K + 63) // 64) * ((N + 15) // 16) * 1024
+    assert np.array_equal(cs, sums)
+    assert np.array_equal(sc, scales)
+    gpu.release_packed(w)
+
+
+# ---------------------------------------------------------------- matmul_i8
+I8_SHAPES = [(1, 64, 16), (1, 4096, 4096), (1, 300, 1100), (2, 257, 33), (3, 1000, 513),
+             (4, 4096, 11008), (5, 77, 19), (7, 129, 4000), (8, 4096, 1024),
+             (9, 64, 16), (16, 300, 200), (64, 128, 96), (130, 257, 129), (257, 1000, 300),
+             (512, 512, 512)]
+
+
+@pytest.mark.parametrize("M,K,N", I8_SHAPES)
+def test_matmul_i8_bit_exact(gpu, M, K, N):
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    w = gpu.pack(B, K, N, scales=sb)
+    got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa)
+    want = oracle.matmul_i8(A, B, sa, sb)
+    gpu.release_packed(w)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [1, 6, 40])
+def test_matmul_i8_accumulator_exact(gpu, M):
+    # scale 1 everywhere: C == (float)acc exactly while |acc| < 2^24
+    K, N = 1000, 257
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    w = gpu.pack(B, K, N)
+    got = g.matmul_i8(gpu, A, w, M, K, N)
+    gpu.release_packed(w)
+    acc = A.astype(np.int64) @ B.astype(np.int64)
+    assert np.array_equal(got.astype(np.int64), acc)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 33])
+@pytest.mark.parametrize("epi", [1, 2, 3, 4])
+def test_matmul_i8_bias_epilogue(gpu, M, epi):
+    K, N = 320, 200
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = RNG.random(M).astype(np.float32) / 127
+    sb = RNG.random(N).astype(np.float32) / 127
+    bias = RNG.standard_normal(N).astype(np.float32)
+    w = gpu.pack(B, K, N, scales=sb)
+    got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa, bias=bias, epilogue=epi)
+    gpu.release_packed(w)
+    assert rel(got, oracle.matmul_i8(A, B, sa, sb, bias, epi)) <= 1e-4
+
+
+@pytest.mark.parametrize("M", [2, 20])
+def test_matmul_i8_strided_and_trans_b(gpu, M):
+    K, N, lda, ldc = 200, 70, 256, 80
+    A = RNG.integers(-128, 128, size=(M, lda)).astype(np.int8)
+    Bt = RNG.integers(-128, 128, size=(N, K)).astype(np.int8)
+    w = gpu.pack(Bt, K, N, trans_b=1)
+    got = g.matmul_i8(gpu, A, w, M, K, N, lda=lda, ldc=ldc)
+    gpu.release_packed(w)
+    acc = A[:, :K].astype(np.int64) @ Bt.T.astype(np.int64)
+    assert np.array_equal(got.astype(np.int64), acc)
+
+
+def test_matmul_i8_zero_weight_blocks_skipped_exactly(gpu):
+    M, K, N = 64, 512, 256
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    keep = RNG.integers(0, 2, size=(K // 64, N // 64)).astype(bool)
+    B *= np.kron(keep, np.ones((64, 64), bool)).astype(np.int8)
+    for m in (M, 4):
+        w = gpu.pack(B, K, N)
+        got = g.matmul_i8(gpu, A[:m], w, m, K, N)
+        gpu.release_packed(w)
+        assert np.array_equal(got.astype(np.int64), A[:m].astype(np.int64) @ B.astype(np.int64))
+
+
+# ---------------------------------------------------------------- matmul_f32
+F32_CASES = [(37, 53, 29, 0, 0), (17, 41, 23, 0, 1), (9, 33, 18, 1, 0), (1, 512, 137, 0, 0),
+             (4, 4096, 1000, 0, 0), (8, 300, 33, 0, 1), (64, 128, 64, 1, 1), (200, 300, 130, 0, 0),
+             (256, 1024, 256, 0, 1)]
+
+
+@pytest.mark.parametrize("M,K,N,ta,tb", F32_CASES)
+@pytest.mark.parametrize("epi,beta,alpha", [(0, 0.0, 0.0), (2, 0.0, 1.0), (3, 0.5, 1.0), (1, 0.0, -2.0)])
+def test_matmul_f32(gpu, M, K, N, ta, tb, epi, beta, alpha):
+    A = RNG.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = RNG.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    bias = RNG.standard_normal(N).astype(np.float32)
+    C0 = RNG.standard_normal((M, N)).astype(np.float32)
+    got = g.matmul_f32(gpu, A, B, M, K, N, C_in=C0, bias=bias, trans_a=ta, trans_b=tb, beta=beta,
+                       alpha=alpha, epilogue=epi)
+    want = oracle.matmul_f32(A, B, C0, bias, M, K, N, ta, tb, alpha if alpha else 1.0, beta, epi,
+                             acc64=True)
+    assert rel(got, want) <= 1e-4
+
+
+@pytest.mark.parametrize("M,N,unit", [(256, 512, 2), (40, 96, 2), (128, 128, 1), (300, 200, 3),
+                                      (4, 300, 0)])
+def test_matmul_f32_wildcat_cull(gpu, M, N, unit):
+    K = 24
+    mask = RNG.integers(0, 2, size=(4, 6)).astype(np.uint8)
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    B = RNG.standard_normal((K, N)).astype(np.float32)
+    got = g.matmul_f32(gpu, A, B, M, K, N, mask=mask, unit=unit)
+    info = gpu.info()
+    cull, _ = oracle.cull_map(M, N, unit, info.tile_m, info.tile_n, info.num_threads, 1, mask)
+    assert np.array_equal(got == 0.0, cull.astype(bool))
+    want = oracle.matmul_f32(A, B, None, None, M, K, N, 0, 0, 1.0, 0.0, 0, cull=cull, acc64=False)
+    assert rel(got, want) <= 1e-4
+
+
+# ---------------------------------------------------------------- row / elementwise ops
+@pytest.mark.parametrize("rows,cols", [(1, 7), (7, 300), (64, 4096), (3, 32000)])
+def test_rmsnorm_softmax(gpu, rows, cols):
+    X = RNG.standard_normal((rows, cols)).astype(np.float32)
+    W = RNG.standard_normal(cols).astype(np.float32)
+    assert rel(g.unary_rows(gpu, abi.OP_RMSNORM_F32, X, W=W, eps=1e-5), oracle.rmsnorm(X, W, 1e-5)) <= 1e-4
+    assert rel(g.unary_rows(gpu, abi.OP_RMSNORM_F32, X, eps=0.0), oracle.rmsnorm(X, None, 1e-5)) <= 1e-4
+    sm = g.unary_rows(gpu, abi.OP_SOFTMAX_F32, X * 4, temperature=0.0)
+    assert rel(sm, oracle.softmax(X * 4, 1.0)) <= 1e-4
+    assert np.allclose(sm.sum(axis=1), 1.0, atol=1e-4)
+
+
+@pytest.mark.parametrize("n", [1, 1001, 4096 * 8 + 3, 2048 * 11008 // 64])
+def test_elementwise(gpu, n):
+    a = RNG.standard_normal(n).astype(np.float32)
+    b = RNG.standard_normal(n).astype(np.float32)
+    assert rel(g.elementwise(gpu, abi.OP_SWIGLU_F32, a, b, alpha=0.0), oracle.swiglu(a, b, 1.0)) <= 1e-4
+    assert rel(g.elementwise(gpu, abi.OP_GELU_F32, a), oracle.gelu(a)) <= 1e-4
+    assert rel(g.elementwise(gpu, abi.OP_ADD_F32, a, b, 0.0, 0.0), oracle.add(a, b, 1.0, 1.0)) <= 1e-6
+    assert rel(g.elementwise(gpu, abi.OP_ADD_F32, a, b, 0.5, -2.0), oracle.add(a, b, 0.5, -2.0)) <= 1e-6
+    assert rel(g.elementwise(gpu, abi.OP_MUL_F32, a, b, 0.0, 0.25), oracle.mul(a, b, 1.0, 0.25)) <= 1e-6
+
+
+@pytest.mark.parametrize("interleaved", [0, 1])
+@pytest.mark.parametrize("shape_q,shape_k,offset", [((2, 3, 40, 16), (2, 3, 24, 16), 100),
+                                                    ((1, 4, 2048, 128), (1, 4, 2048, 128), 0),
+                                                    ((8, 2, 1, 128), (8, 2, 1, 128), 4095)])
+def test_rope(gpu, interleaved, shape_q, shape_k, offset):
+    Q = RNG.standard_normal(shape_q).astype(np.float32)
+    K = RNG.standard_normal(shape_k).astype(np.float32)
+    gq, gk = g.rope(gpu, Q, K, position_offset=offset, interleaved=interleaved, theta=0.0)
+    oq, ok = oracle.rope(Q, K, position_offset=offset, interleaved=interleaved, theta=10000.0)
+    assert rel(gq, oq) <= 1e-4 and rel(gk, ok) <= 1e-4
+
+
+def test_rope_positions_and_identity(gpu):
+    Q = RNG.standard_normal((1, 2, 6, 8)).astype(np.float32)
+    pos = np.array([0, 5, 2, 0, 9, 1], np.int32)
+    gq, _ = g.rope(gpu, Q, None, positions=pos)
+    oq, _ = oracle.rope(Q, None, positions=pos)
+    assert rel(gq, oq) <= 1e-5
+    assert np.array_equal(gq[:, :, 0], Q[:, :, 0])  # position 0 is the identity
+    # pair norms are preserved
+    h = 4
+    n0 = Q[..., :h] ** 2 + Q[..., h:] ** 2
+    n1 = gq[..., :h] ** 2 + gq[..., h:] ** 2
+    assert np.allclose(n0, n1, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- attention
+@pytest.mark.parametrize("b,h,sq,sk,d,causal,use_mask", [
+    (1, 2, 5, 5, 16, 1, False), (1, 2, 33, 70, 16, 1, False), (1, 2, 16, 100, 16, 0, True),
+    (1, 2, 1, 130, 16, 1, False), (1, 4, 300, 300, 128, 1, False), (2, 2, 1, 4096, 128, 1, False),
+    (1, 1, 17, 9, 64, 1, False), (1, 2, 40, 40, 80, 0, False)])
+def test_attention(gpu, b, h, sq, sk, d, causal, use_mask):
+    Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
+    K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+    V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+    mask = RNG.standard_normal((b, h, sq, sk)).astype(np.float32) if use_mask else None
+    got = g.attention(gpu, Q, K, V, mask, causal)
+    want = oracle.attention(Q, K, V, mask, causal)
+    assert rel(got, want) <= 2e-3
+
+
+def test_attention_invariants(gpu):
+    # V constant -> O constant; causal row 0 attends only key 0 -> O[0] = V[0].
+    Q = RNG.standard_normal((1, 2, 20, 32)).astype(np.float32)
+    K = RNG.standard_normal((1, 2, 20, 32)).astype(np.float32)
+    V = np.full((1, 2, 20, 32), 0.75, np.float32)
+    assert np.allclose(g.attention(gpu, Q, K, V, None, 1), 0.75, atol=1e-6)
+    V = RNG.standard_normal((1, 2, 20, 32)).astype(np.float32)
+    O = g.attention(gpu, Q, K, V, None, 1)
+    assert np.allclose(O[:, :, 0], V[:, :, 0], atol=1e-6)
+
+
+# ---------------------------------------------------------------- runtime semantics
+def test_host_pointer_staging(gpu):
+    # The reference's tools pass host pointers everywhere: they are staged.
+    M, K, N = 3, 130, 70
+    X = RNG.standard_normal((M, K)).astype(np.float32)
+    A8 = np.empty((M, K), np.int8)
+    sa = np.empty(M, np.float32)
+    Bq = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    w = gpu.pack(Bq, K, N)
+    Cout = np.empty((M, N), np.float32)
+    p = lambda a: a.ctypes.data
+    gpu.run(abi.OP_QUANTIZE_I8, X=p(X), Y=p(A8), scales=p(sa), rows=M, cols=K, axis=0)
+    gpu.run(abi.OP_MATMUL_I8, A=p(A8), B=w, scale_a=p(sa), C=p(Cout), M=M, K=K, N=N)
+    yo, so = oracle.quantize(X, 0)
+    assert np.array_equal(A8, yo) and np.array_equal(sa, so)
+    assert np.array_equal(Cout.view(np.uint32), oracle.matmul_i8(yo, Bq, so, None).view(np.uint32))
+    gpu.release_packed(w)
+
+
+def test_batch_event_and_sticky_error():
+    from vnpu_mi355x import Session
+    s = Session()
+    try:
+        ev = C.c_void_p()
+        assert s.lib.vnpu_event_create(C.byref(ev)) == abi.OK
+        assert s.lib.vnpu_event_wait(ev, 0) == abi.ERR_TIMEOUT  # never submitted
+        nops = [s.command(abi.OP_NOP) for _ in range(8)]
+        assert s.submit(nops, ev) == abi.OK
+        assert s.lib.vnpu_event_wait(ev, 10000) == abi.OK
+        assert s.lib.vnpu_event_query(ev) == abi.OK
+        # ones(16x16) . ones(16x16) = 16 (reference selftest known answer)
+        ones = s.upload(np.ones((16, 16), np.float32))
+        out = s.alloc(16 * 16 * 4)
+        s.run(abi.OP_MATMUL_F32, A=ones, B=ones, C=out, M=16, K=16, N=16)
+        assert np.all(s.download(out, np.float32, (16, 16)) == 16.0)
+        # invalid command: submit still OK, event carries the failure, sync is sticky
+        bad = s.command(abi.OP_MATMUL_F32, A=None, B=None, C=None, M=0, K=0, N=0)
+        assert s.submit([bad], ev) == abi.OK
+        assert s.lib.vnpu_event_wait(ev, 10000) == abi.ERR_INTERNAL
+        assert s.sync() == abi.ERR_DEVICE_ERROR
+        assert s.sync() == abi.ERR_DEVICE_ERROR
+        assert s.submit([s.command(99)], None) == abi.OK
+        st = s.status()
+        assert st.error != 0
+        s.lib.vnpu_event_destroy(ev)
+    finally:
+        s.close()
+
+
+def test_two_streams_concurrent(gpu):
+    M, K, N = 192, 256, 256
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    B = RNG.standard_normal((K, N)).astype(np.float32)
+    want = oracle.matmul_f32(A, B, acc64=True)
+    s2 = C.c_void_p()
+    assert gpu.lib.vnpu_stream_create(gpu.dev, 0, C.byref(s2)) == abi.OK
+    ba, bb = gpu.upload(A), gpu.upload(B)
+    outs = [gpu.alloc(M * N * 4) for _ in range(8)]
+    cmds = [gpu.command(abi.OP_MATMUL_F32, A=ba, B=bb, C=o, M=M, K=K, N=N) for o in outs]
+    arr1 = (abi.Command * 4)(*cmds[:4])
+    arr2 = (abi.Command * 4)(*cmds[4:])
+    assert gpu.lib.vnpu_stream_submit(gpu.stream, arr1, 4, None) == abi.OK
+    assert gpu.lib.vnpu_stream_submit(s2, arr2, 4, None) == abi.OK
+    assert gpu.lib.vnpu_stream_sync(s2) == abi.OK and gpu.sync() == abi.OK
+    for o in outs:
+        assert rel(gpu.download(o, np.float32, (M, N)), want) <= 1e-4
+    gpu.lib.vnpu_stream_destroy(s2)
+
+
+def test_backend_table_and_info(gpu):
+    tbl = gpu.lib.vnpu_get_backend_v1()
+    raw = (C.c_uint32 * 2).from_address(tbl)
+    assert raw[0] == 1 and raw[1] == 416
+    info = gpu.info()
+    assert info.num_compute_units >= 1 and info.total_memory_bytes > 0
+    assert b"gfx950" in info.cpu_arch
+    assert gpu.lib.vnpu_mmio_read32(gpu.dev, 0) == 0x56504E55
