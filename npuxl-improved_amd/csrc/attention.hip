@@ -220,6 +220,14 @@ void attention(hipStream_t s, const Attn &a, float *ws)
     float *ws_acc = ws;
     float *ws_ml = ws ? ws + static_cast<uint64_t>(splits) * rows * D : nullptr;
     dim3 grid(qb, a.batch * a.heads, splits);
+    // Above 64 KiB of dynamic LDS the kernel must opt in (CDNA4 has 160 KiB).
+    static thread_local size_t lds_optin = 0;
+    if (lds > 65536 && lds > lds_optin) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds)) == hipSuccess)
+            lds_optin = lds;
+    }
     attn_kernel<<<grid, kThreads, lds, s>>>(a, kps, splits, ws_acc, ws_ml);
     if (splits > 1) {
         const uint64_t total = rows * D;
