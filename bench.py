@@ -182,6 +182,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--only", choices=["gemm_i8"], default=None,
+                    help="run one extra workload alone (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend benchmarks one GPU only; multi-GPU sharding is "
@@ -191,6 +193,11 @@ def main():
     M, K, N = 1, 4096, 32000
     s = Session()
     log("device", s.info().backend.decode())
+    if args.only == "gemm_i8":
+        for n in (4096, 14336):
+            log("gemm_i8", bench_gemm_i8(s, 2048, 4096, n, args.steps, args.warmup))
+        s.close()
+        return
     wq, ws = weights_for(s, K, N, f"w_{K}x{N}")
     head = bench_gemv(s, M, K, N, args.steps, args.warmup, wq, ws)
     log("headline", head)

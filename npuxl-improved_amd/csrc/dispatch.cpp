@@ -343,6 +343,7 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     p.ldc = in.ldc ? in.ldc : in.N;
     require(p.lda >= in.K && p.ldc >= in.N, "invalid int8 leading dimensions");
     p.frag = w->frag;
+    // The zero-block map only costs lookups when there are zero blocks.
     p.zero_blocks = w->zero_block_count ? w->zero_blocks : nullptr;
     p.Kp = w->Kp;
     p.Np = w->Np;

@@ -51,7 +51,7 @@ __device__ __forceinline__ v4i load_a_chunk(const I8Gemm &p, uint32_t m, uint32_
     return u.v;
 }
 
-__global__ __launch_bounds__(kThreads) void gemm_i8_kernel(I8Gemm p)
+__global__ __launch_bounds__(kThreads) void gemm_i8_generic(I8Gemm p)
 {
     __shared__ __attribute__((aligned(16))) int8_t a_lds[2][BM * kPitch];
 
@@ -154,12 +154,335 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(I8Gemm p)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined kernel (K % 64 == 0, 16-byte aligned rows of A).
+//
+//   * workgroup tile 256 x 128, 4 waves of 128 x 64 (8 x 4 MFMA blocks, 32
+//     independent accumulators per wave - enough to keep the matrix pipe
+//     issuing back to back);
+//   * a ring of kStages LDS stages, each holding one 64-deep k step of both
+//     operands as 1 KiB fragment blocks (16 of A, 8 of B), filled by
+//     global_load_lds_dwordx4: lane l of a wave writes bytes [16l, 16l+16) of
+//     a block, so A is fetched directly in fragment order (lane l reads row
+//     l%16, k 16*(l/16)..+16) and B is copied as packed;
+//   * kStages-1 k steps of DMA are in flight; each wave waits with an
+//     explicit vmcnt for only its own oldest stage and one s_barrier per k
+//     step publishes it;
+//   * fragments are software-pipelined through two register sets: the 12
+//     ds_read_b128 of step k+1 are in flight while the 32 MFMAs of step k
+//     issue, so LDS latency is hidden at one wave per SIMD;
+//   * the accumulators leave through LDS: a compact loop then applies the
+//     dequant epilogue with row-contiguous, coalesced stores (a fully
+//     unrolled per-lane epilogue would be tens of KiB of code per wave);
+//   * rows past M and column blocks past N are clamped to valid addresses
+//     (their results are never stored), so every DMA stays in bounds.
+// ---------------------------------------------------------------------------
+namespace pipe {
+constexpr int TM = 256, TN = 128;
+constexpr int kStages = 6;
+constexpr int kABlocks = TM / 16;                    // 16
+constexpr int kBBlocks = TN / 16;                    // 8
+constexpr int kBlocks = kABlocks + kBBlocks;         // 24 x 1 KiB per stage
+constexpr int kLoads = kBlocks / 4;                  // per wave per stage
+constexpr int kStageBytes = kBlocks * 1024;
+constexpr int kRing = kStages * kStageBytes;         // 144 KiB
+constexpr int kOutPitch = TN + 4;                    // int32 per staged row (pad vs bank conflicts)
+constexpr int kOut = TM * kOutPitch * 4;             // 132 KiB, row-major staged tile
+constexpr int kScaleOff = kOut;                      // 256 row scales after the tile
+constexpr size_t kLds = kRing;                       // 144 KiB (>= kOut + 1 KiB)
+static_assert(kOut + TM * 4 <= kRing, "staged tile + row scales fit in the ring");
+}  // namespace pipe
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8.  Issued through the builtin so the compiler's own wait
+// insertion knows which counters are already drained.
+constexpr int waitcnt_imm(int vm, int exp, int lgkm)
+{
+    return (vm & 0xF) | ((vm >> 4) << 14) | (exp << 4) | (lgkm << 8);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(N, 7, 15));
+}
+
+// Workgroup barrier that does not drain the DMA queue: only this wave's LDS
+// reads must be complete (the buffer they read may be refilled right after),
+// outstanding global->LDS loads keep flying.  The asm keeps memory accesses
+// from being moved across the barrier.
+__device__ __forceinline__ void block_barrier()
+{
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 7, 0));
+    asm volatile("s_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ void dma16(const void *src, int8_t *lds_dst)
+{
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds_dst), 16, 0, 0);
+}
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// One stage's operands for v_mfma_i32_32x32x32_i8, per 32-deep k half h:
+// lane l holds row (col) l%32 and k 16*(l/32)..+16 of that half.
+struct Frags {
+    v4i a[2][4], b[2][2];
+};
+
+// Dequant epilogue over the row-major staged tile: each thread writes 4
+// consecutive columns per row (one 16-byte store), 8 rows per pass.  One
+// instantiation per activation keeps the loop body small.  No contraction:
+// ((float)acc * sa) * sb + bias rounds each step, as the reference's
+// store_i8_c does.
+template <int EPI>
+__device__ void store_tile(const I8Gemm &p, const int32_t *tile, const float *sa_lds, uint32_t m0,
+                           uint32_t n0, int tid)
+{
+#pragma clang fp contract(off)
+    const uint32_t c4 = (tid & 31) * 4;  // first of this thread's 4 columns
+    const uint32_t n = n0 + c4;
+    float sb[4], bias[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const bool ok = n + q < p.N;
+        sb[q] = ok ? p.scale_b[n + q] : 0.0f;
+        bias[q] = (ok && p.bias) ? p.bias[n + q] : 0.0f;
+    }
+    const bool vec = (n + 3 < p.N) && ((p.ldc & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
+    const uint32_t rows = min(static_cast<uint32_t>(pipe::TM), p.M - m0);
+#pragma unroll 4
+    for (uint32_t r = tid >> 5; r < rows; r += 8) {
+        const v4i acc = *reinterpret_cast<const v4i *>(tile + r * pipe::kOutPitch + c4);
+        const float sa = sa_lds[r];
+        float o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float v = (static_cast<float>(acc[q]) * sa) * sb[q];
+            if (p.bias) v = v + bias[q];
+            o[q] = dev::epilogue(v, EPI);
+        }
+        float *dst = p.C + static_cast<uint64_t>(m0 + r) * p.ldc + n;
+        if (vec) {
+            *reinterpret_cast<float4 *>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (n + q < p.N) dst[q] = o[q];
+        }
+    }
+}
+
+template <bool kSkip>
+__global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
+{
+    using pipe::kABlocks;
+    using pipe::kBBlocks;
+    using pipe::kLoads;
+    using pipe::kStageBytes;
+    using pipe::kStages;
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int fr = lane & 15, fg = lane >> 4;
+
+    // XCD-aware tile order: workgroup g runs on XCD g % 8; give each XCD a
+    // contiguous run of tiles, M-fastest, so an XCD's L2 keeps its B columns.
+    const uint32_t total = tiles_m * tiles_n;
+    uint32_t g = blockIdx.x;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const uint32_t tmi = g % tiles_m, tni = g / tiles_m;
+    const uint32_t m0 = tmi * pipe::TM, n0 = tni * pipe::TN;
+    const uint32_t NT = p.Np >> 4;
+    const uint32_t KT = p.K >> 6;
+
+    // This wave's kLoads blocks of every stage: base address + per-k-step stride.
+    const int8_t *src[kLoads];
+    uint64_t stride[kLoads];
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+        const int b = wave * kLoads + j;
+        if (b < kABlocks) {
+            const uint32_t row = min(m0 + b * 16 + fr, p.M - 1);
+            src[j] = p.A + static_cast<uint64_t>(row) * p.lda + fg * 16;
+            stride[j] = 64;
+        } else {
+            const uint32_t nb = min((n0 >> 4) + (b - kABlocks), NT - 1);
+            src[j] = p.frag + (static_cast<uint64_t>(nb) << 10) + lane * 16;
+            stride[j] = static_cast<uint64_t>(NT) << 10;
+        }
+    }
+    auto issue = [&](uint32_t kt) {
+        int8_t *st = smem + (kt % kStages) * kStageBytes;
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) dma16(src[j] + kt * stride[j], st + (wave * kLoads + j) * 1024);
+    };
+    // A 32-row (32-column) operand is two 16-row fragment blocks of the
+    // stage: lane l takes block (l/16)%2, row l%16, k group 2h + l/32.
+    const int sub = (lane >> 4) & 1;
+    auto read_frags = [&](uint32_t kt, Frags &f) {
+        const int8_t *st = smem + (kt % kStages) * kStageBytes;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int off = ((2 * h + (lane >> 5)) * 16 + (lane & 15)) * 16;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+                f.b[h][nb] = *reinterpret_cast<const v4i *>(st + (kABlocks + wn * 4 + 2 * nb + sub) * 1024 + off);
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+                f.a[h][mb] = *reinterpret_cast<const v4i *>(st + (wm * 8 + 2 * mb + sub) * 1024 + off);
+        }
+    };
+
+    // All-zero weight-block flags of this tile's 8 column blocks, staged once
+    // in LDS (after the ring) so the k loop never waits on a global load.
+    uint8_t *zflags = reinterpret_cast<uint8_t *>(smem + pipe::kLds);
+    if (kSkip) {
+        for (uint32_t i = tid; i < KT * kBBlocks; i += kThreads) {
+            const uint32_t kt = i / kBBlocks, nb = (n0 >> 4) + (i % kBBlocks);
+            zflags[i] = nb < NT ? p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] : 1;
+        }
+        __syncthreads();
+    }
+
+    v16i acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i){0};
+
+    // 32x32x32 rather than 16x16x64: at one wave per SIMD it keeps the int8
+    // matrix pipe ~85% busy where the 16x16 shape issues at ~55%.
+    // A wave's 64 columns x 64 k of all-zero weights add nothing: the MFMAs
+    // of such a step are skipped (wave-uniform).  The flag is read before the
+    // next stage's fragments so waiting for it never waits for those.
+    auto zero_step = [&](uint32_t kt) -> bool {
+        return kSkip && *reinterpret_cast<const uint32_t *>(zflags + kt * kBBlocks + wn * 4) == 0x01010101u;
+    };
+    auto mma = [&](const Frags &f, bool skip) {
+        if (skip) return;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+    };
+
+    // Prologue: DMA every stage buffer, then stage 0's fragments.
+    const uint32_t pre = min(KT, static_cast<uint32_t>(kStages));
+    for (uint32_t s = 0; s < pre; ++s) issue(s);
+    if (KT > static_cast<uint32_t>(kStages)) wait_vmcnt<(kStages - 1) * kLoads>();
+    else wait_vmcnt<0>();
+    block_barrier();
+    Frags f0, f1;
+    read_frags(0, f0);
+
+    // Steady state, two k steps per trip so the fragment sets swap without
+    // copies, and no branch around the MFMAs.  Step kt: wait for this wave's
+    // DMA of stage kt+1 (kStages-2 later stages may stay in flight), barrier
+    // (stage kt+1 landed everywhere; every wave holds stage kt in registers,
+    // so its buffer is free), DMA stage kt+kStages into it, read stage kt+1,
+    // then issue stage kt's 32 MFMAs.
+    // sched_barrier(0) keeps the three phases of a step in order: the
+    // compiler would otherwise pull the next stage's reads into the MFMA
+    // sequence and stall it on lgkmcnt.
+    // A step's zero flag is read right after the previous step's MFMAs, so
+    // the next barrier's LDS drain covers it.
+    uint32_t kt = 0;
+    bool sk0 = zero_step(0), sk1 = false;
+    for (; kt + kStages + 1 < KT; kt += 2) {
+        wait_vmcnt<(kStages - 2) * kLoads>();
+        block_barrier();
+        issue(kt + kStages);
+        read_frags(kt + 1, f1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f0, sk0);
+        sk1 = zero_step(kt + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<(kStages - 2) * kLoads>();
+        block_barrier();
+        issue(kt + 1 + kStages);
+        read_frags(kt + 2, f0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f1, sk1);
+        sk0 = zero_step(kt + 2);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Drain: every remaining stage is already issued; wait for all of it once.
+    wait_vmcnt<0>();
+    block_barrier();
+    mma(f0, sk0);
+    for (++kt; kt < KT; ++kt) {
+        const bool sk = zero_step(kt);
+        read_frags(kt, f1);
+        mma(f1, sk);
+    }
+
+    // Stage the accumulators row-major (32x32 block: lane l holds column
+    // l%32, rows 8j + 4(l/32) + q in register 4j + q) and the row scales.
+    __syncthreads();
+    int32_t *tile = reinterpret_cast<int32_t *>(smem);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                tile[(wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * pipe::kOutPitch + wn * 64 +
+                     j * 32 + (lane & 31)] = acc[i][j][r];
+    float *sa_lds = reinterpret_cast<float *>(smem + pipe::kScaleOff);
+    {
+        const uint32_t m = m0 + tid;
+        sa_lds[tid] = (p.scale_a && m < p.M) ? p.scale_a[m] : 1.0f;
+    }
+    __syncthreads();
+    switch (p.epilogue) {
+    case 1: store_tile<1>(p, tile, sa_lds, m0, n0, tid); break;
+    case 2: store_tile<2>(p, tile, sa_lds, m0, n0, tid); break;
+    case 3:
+    case 4: store_tile<3>(p, tile, sa_lds, m0, n0, tid); break;
+    default: store_tile<0>(p, tile, sa_lds, m0, n0, tid); break;
+    }
+}
+
 }  // namespace
 
 void gemm_i8(hipStream_t s, const I8Gemm &p)
 {
+    // The zero-flag table must fit next to the staged tile (K <= 16384).
+    const bool aligned = (p.K % 64 == 0) && (p.lda % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64 &&
+                         p.K <= 16384;
+    if (aligned) {
+        static bool lds_optin = false;
+        if (!lds_optin) {
+            lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_i8_pipe<false>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            160 * 1024) == hipSuccess &&
+                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_i8_pipe<true>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            160 * 1024) == hipSuccess;
+        }
+        const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
+        const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
+        // Weights with all-zero 1 KiB blocks take the variant that skips
+        // their MFMAs; dense weights the one without the flag reads.
+        if (p.zero_blocks) {
+            const size_t lds = pipe::kLds + ((p.K / 64) * pipe::kBBlocks + 15) / 16 * 16;  // <= 160 KiB for K <= 16384
+            gemm_i8_pipe<true><<<dim3(tm * tn), kThreads, lds, s>>>(p, tm, tn);
+        } else {
+            gemm_i8_pipe<false><<<dim3(tm * tn), kThreads, pipe::kLds, s>>>(p, tm, tn);
+        }
+        return;
+    }
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
-    gemm_i8_kernel<<<grid, kThreads, 0, s>>>(p);
+    gemm_i8_generic<<<grid, kThreads, 0, s>>>(p);
 }
 
 }  // namespace k

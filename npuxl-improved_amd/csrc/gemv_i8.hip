@@ -27,10 +27,8 @@ namespace vnpu {
 namespace k {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr uint32_t kChunkK = 4096;  // activations staged per chunk of K
-constexpr int kUnroll = 4;          // k blocks in flight per wave
+constexpr int kUnroll = 8;           // k blocks per batch in flight per wave
+constexpr uint32_t kLdsA = 32768;    // bytes of LDS for staged activations
 
 __device__ __forceinline__ int dot16(const int4 a, const int4 b, int acc)
 {
@@ -41,11 +39,14 @@ __device__ __forceinline__ int dot16(const int4 a, const int4 b, int acc)
     return acc;
 }
 
-template <int M, int T>
-__global__ __launch_bounds__(kThreads) void gemv_i8_kernel(I8Gemm p)
+// M rows, T 16-column blocks per workgroup, W waves splitting K.
+template <int M, int T, int W>
+__global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p)
 {
+    constexpr int kThreads = 64 * W;
+    constexpr uint32_t kChunkK = (kLdsA / M) & ~63u;  // whole 64-deep k blocks
     __shared__ __attribute__((aligned(16))) int8_t a_lds[kChunkK * M];
-    __shared__ int red[kWaves][T][M][16];
+    __shared__ int red[W][T][M][16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -62,8 +63,32 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(I8Gemm p)
 
     for (uint32_t kc = 0; kc < p.Kp; kc += kChunkK) {
         const uint32_t kc_len = min(kChunkK, p.Kp - kc);
-        __syncthreads();
-        // Stage A[:, kc : kc + kc_len] as [k16][m][16] (zero beyond K).
+        const uint32_t kt_begin = kc >> 6, kt_end = (kc + kc_len) >> 6;
+        const uint32_t first = kt_begin + wave;
+        const uint32_t nsteps = first < kt_end ? (kt_end - first + W - 1) / W : 0;
+
+        // The weight stream does not depend on the activations: put the first
+        // batch in flight before staging them.
+        int4 bc[kUnroll][T], bn[kUnroll][T];
+        auto load_batch = [&](int4 (&b)[kUnroll][T], uint32_t i0) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const uint32_t step = i0 + u;
+                const uint32_t kt = first + step * W;
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    b[u][t] = make_int4(0, 0, 0, 0);
+                    if (step < nsteps && nt0 + t < NT) {
+                        const uint64_t blk = static_cast<uint64_t>(kt) * NT + nt0 + t;
+                        if (!p.zero_blocks || !p.zero_blocks[blk])
+                            b[u][t] = *reinterpret_cast<const int4 *>(p.frag + (blk << 10) + lane * 16);
+                    }
+                }
+            }
+        };
+        load_batch(bc, 0);
+
+        __syncthreads();  // previous chunk fully consumed
         const uint32_t chunks = (kc_len >> 4) * M;
         for (uint32_t i = tid; i < chunks; i += kThreads) {
             const uint32_t m = i % M, k16 = i / M;
@@ -85,35 +110,25 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(I8Gemm p)
         }
         __syncthreads();
 
-        const uint32_t kt_begin = kc >> 6, kt_end = (kc + kc_len) >> 6;
-        for (uint32_t kt = kt_begin + wave; kt < kt_end; kt += kWaves * kUnroll) {
-            int4 b[kUnroll][T];
+        for (uint32_t i = 0; i < nsteps; i += kUnroll) {
+            if (i + kUnroll < nsteps) load_batch(bn, i + kUnroll);
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
-                const uint32_t ktu = kt + u * kWaves;
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    b[u][t] = make_int4(0, 0, 0, 0);
-                    if (ktu < kt_end && nt0 + t < NT) {
-                        const bool skip = p.zero_blocks && p.zero_blocks[static_cast<uint64_t>(ktu) * NT + nt0 + t];
-                        if (!skip)
-                            b[u][t] = *reinterpret_cast<const int4 *>(
-                                p.frag + ((static_cast<uint64_t>(ktu) * NT + nt0 + t) << 10) + lane * 16);
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const uint32_t ktu = kt + u * kWaves;
-                if (ktu >= kt_end) break;
-                const int8_t *arow = a_lds + (((ktu - kt_begin) * 4 + kg) * M) * 16;
+                const uint32_t step = i + u;
+                if (step >= nsteps) break;
+                const uint32_t ktl = first + step * W - kt_begin;
+                const int8_t *arow = a_lds + ((ktl * 4 + kg) * M) * 16;
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     const int4 a = *reinterpret_cast<const int4 *>(arow + m * 16);
 #pragma unroll
-                    for (int t = 0; t < T; ++t) acc[t][m] = dot16(a, b[u][t], acc[t][m]);
+                    for (int t = 0; t < T; ++t) acc[t][m] = dot16(a, bc[u][t], acc[t][m]);
                 }
             }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+                for (int t = 0; t < T; ++t) bc[u][t] = bn[u][t];
         }
     }
 
@@ -134,15 +149,15 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(I8Gemm p)
             for (int m = 0; m < M; ++m) red[wave][t][m][lane] = acc[t][m];
     }
     __syncthreads();
-    if (tid < T * M * 16) {
-        const int c = tid & 15;
-        const int m = (tid >> 4) % M;
-        const int t = (tid >> 4) / M;
+    for (int o = tid; o < T * M * 16; o += kThreads) {
+        const int c = o & 15;
+        const int m = (o >> 4) % M;
+        const int t = (o >> 4) / M;
         const uint32_t n = (nt0 + t) * 16 + c;
         if (n < p.N) {
             int s = 0;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) s += red[w][t][m][c];
+            for (int w = 0; w < W; ++w) s += red[w][t][m][c];
             const float sa = p.scale_a ? p.scale_a[m] : 1.0f;
             float out = __fmul_rn(__fmul_rn(static_cast<float>(s), sa), p.scale_b[n]);
             if (p.bias) out = __fadd_rn(out, p.bias[n]);
@@ -151,15 +166,18 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(I8Gemm p)
     }
 }
 
+// Launch shape from the column count: two column blocks per workgroup once
+// there are enough of them, and eight waves when workgroups are scarce.
 template <int M>
 void launch_m(hipStream_t s, const I8Gemm &p)
 {
     const uint32_t NT = p.Np >> 4;
-    if (NT >= 1024) {
-        gemv_i8_kernel<M, 2><<<dim3((NT + 1) / 2), kThreads, 0, s>>>(p);
-    } else {
-        gemv_i8_kernel<M, 1><<<dim3(NT), kThreads, 0, s>>>(p);
-    }
+    if (NT >= 1024)
+        gemv_i8_kernel<M, 2, 4><<<dim3((NT + 1) / 2), 256, 0, s>>>(p);
+    else if (NT >= 512)
+        gemv_i8_kernel<M, 1, 4><<<dim3(NT), 256, 0, s>>>(p);
+    else
+        gemv_i8_kernel<M, 1, 8><<<dim3(NT), 512, 0, s>>>(p);
 }
 
 }  // namespace

@@ -78,7 +78,7 @@ def test_pack_info(gpu, K, N, trans_b):
 I8_SHAPES = [(1, 64, 16), (1, 4096, 4096), (1, 300, 1100), (2, 257, 33), (3, 1000, 513),
              (4, 4096, 11008), (5, 77, 19), (7, 129, 4000), (8, 4096, 1024),
              (9, 64, 16), (16, 300, 200), (64, 128, 96), (130, 257, 129), (257, 1000, 300),
-             (512, 512, 512)]
+             (512, 512, 512), (320, 4096, 700), (100, 1024, 2000), (513, 192, 130)]
 
 
 @pytest.mark.parametrize("M,K,N", I8_SHAPES)
