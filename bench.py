@@ -9,8 +9,9 @@ resident in HBM.  Bytes per call follow the reference's accounting
 
 Each step reads a different copy of the weights (rotation over > 768 MB) so
 the 256 MB Infinity Cache cannot serve them.  The timed region is bracketed
-by stream syncs; per-kernel durations come from the backend's Sherlock trace,
-i.e. hipEvents recorded around each command on the stream it runs on.
+by stream syncs (wall clock -> `value`) and by a hipEvent pair recorded on the
+vnpu stream's own hipStream_t (GPU time / launches -> the average kernel
+duration behind `roofline.achieved`).
 
 Also printed (same line, key "extras"): the rest of config 2 (M in {1,4,8} x
 N in {4096,11008,32000}) and the config-3 int8 prefill GEMM.  The CPU
@@ -71,22 +72,49 @@ class GemvCase:
             self.s.free(b)
 
 
+class HipEvents:
+    """hipEvent pair recorded on the vnpu stream's own hipStream_t (exported by
+    the backend as vnpu_stream_hip_handle), i.e. on the stream the kernels run on."""
+
+    def __init__(self, s: Session):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.stream = C.c_void_p(s.lib.vnpu_stream_hip_handle(s.stream))
+        self.e0, self.e1 = C.c_void_p(), C.c_void_p()
+        for e in (self.e0, self.e1):
+            assert self.hip.hipEventCreate(C.byref(e)) == 0
+
+    def record(self, ev):
+        assert self.hip.hipEventRecord(ev, self.stream) == 0
+
+    def elapsed_ms(self) -> float:
+        assert self.hip.hipEventSynchronize(self.e1) == 0
+        ms = C.c_float()
+        assert self.hip.hipEventElapsedTime(C.byref(ms), self.e0, self.e1) == 0
+        return ms.value
+
+    def close(self):
+        self.hip.hipEventDestroy(self.e0)
+        self.hip.hipEventDestroy(self.e1)
+
+
 def timed(s: Session, make_cmd, steps: int, warmup: int):
-    """Run warmup + steps commands; returns (wall seconds, avg GPU ns/command)."""
+    """Run warmup + steps commands.  Returns (wall seconds of the timed region,
+    average GPU ns per command): the region is bracketed by stream syncs for the
+    wall clock and by a hipEvent pair on the same stream for GPU time."""
     if warmup:
         s.check("submit", s.submit([make_cmd(i) for i in range(warmup)]))
         s.check("sync", s.sync())
     cmds = [make_cmd(i) for i in range(steps)]
-    s.lib.vnpu_trace_enable(s.dev, 1)
+    ev = HipEvents(s)
     s.check("sync", s.sync())
     t0 = time.perf_counter()
+    ev.record(ev.e0)
     s.check("submit", s.submit(cmds))
+    ev.record(ev.e1)
     s.check("sync", s.sync())
     wall = time.perf_counter() - t0
-    summ = abi.TraceSummary()
-    s.lib.vnpu_trace_get_summary(s.dev, C.byref(summ))
-    s.lib.vnpu_trace_enable(s.dev, 0)
-    gpu_ns = summ.total_time_ns / max(1, summ.events)
+    gpu_ns = ev.elapsed_ms() * 1e6 / steps
+    ev.close()
     return wall, gpu_ns
 
 

@@ -735,6 +735,12 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_speculative_step(vnpu_cluster_t *cluster,
                                                        void *verify_user,
                                                        vnpu_speculative_result_t *result);
 
+/* MI355X extension (additive, allowed by the ABI rules above; no reference
+ * counterpart): the hipStream_t behind a vnpu stream, so a caller can order
+ * its own HIP work or hipEvents with the stream's commands.  Returns NULL for
+ * a NULL stream. */
+VNPU_API void *VNPU_CALL vnpu_stream_hip_handle(vnpu_stream_t *stream);
+
 /* Helpers (reference include/vnpu.h:745-750). */
 VNPU_API uint16_t VNPU_CALL vnpu_float_to_bf16(float value);
 VNPU_API uint16_t VNPU_CALL vnpu_float_to_f16(float value);

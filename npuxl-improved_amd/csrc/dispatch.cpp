@@ -22,9 +22,45 @@
 
 namespace vnpu {
 
+namespace {
+struct RangeRegistry {
+    std::mutex mutex;
+    std::map<uintptr_t, size_t> ranges;  // start -> bytes
+};
+RangeRegistry &ranges()
+{
+    static RangeRegistry *r = new RangeRegistry();
+    return *r;
+}
+}  // namespace
+
+void register_device_range(const void *p, size_t bytes)
+{
+    auto &r = ranges();
+    std::lock_guard<std::mutex> lock(r.mutex);
+    r.ranges[reinterpret_cast<uintptr_t>(p)] = bytes;
+}
+
+void unregister_device_range(const void *p)
+{
+    auto &r = ranges();
+    std::lock_guard<std::mutex> lock(r.mutex);
+    r.ranges.erase(reinterpret_cast<uintptr_t>(p));
+}
+
 bool is_device_pointer(const void *p)
 {
     if (!p) return false;
+    {
+        auto &r = ranges();
+        std::lock_guard<std::mutex> lock(r.mutex);
+        const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+        auto it = r.ranges.upper_bound(a);
+        if (it != r.ranges.begin()) {
+            --it;
+            if (a < it->first + it->second) return true;
+        }
+    }
     hipPointerAttribute_t attr;
     std::memset(&attr, 0, sizeof(attr));
     hipError_t e = hipPointerGetAttributes(&attr, p);
@@ -671,6 +707,7 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
     const uint64_t blocks = static_cast<uint64_t>(w->Kp / 64) * (w->Np / 16);
     w->frag_bytes = blocks * 1024;
     VNPU_HIP(hipMalloc(&w->frag, w->frag_bytes));
+    register_device_range(w->frag, w->frag_bytes);
     VNPU_HIP(hipMalloc(&w->scales_dev, static_cast<size_t>(w->Np) * 4));
     VNPU_HIP(hipMalloc(&w->zero_blocks, blocks));
     int32_t *sums_dev = nullptr;
@@ -716,7 +753,10 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
 void destroy_packed(vnpu_packed_weights_t *w)
 {
     if (!w) return;
-    if (w->frag) (void)hipFree(w->frag);
+    if (w->frag) {
+        unregister_device_range(w->frag);
+        (void)hipFree(w->frag);
+    }
     if (w->scales_dev) (void)hipFree(w->scales_dev);
     if (w->zero_blocks) (void)hipFree(w->zero_blocks);
     delete w;

@@ -613,6 +613,11 @@ VNPU_API void VNPU_CALL vnpu_stream_destroy(vnpu_stream_t *stream)
     destroy_stream_obj(stream);
 }
 
+VNPU_API void *VNPU_CALL vnpu_stream_hip_handle(vnpu_stream_t *stream)
+{
+    return stream ? static_cast<void *>(stream->hip) : nullptr;
+}
+
 VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_sync(vnpu_stream_t *stream)
 {
     if (!stream) return VNPU_ERR_INVALID_ARGUMENT;
@@ -769,6 +774,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_buffer_alloc(vnpu_device_t *device, uint64
             return VNPU_ERR_DEVICE_ERROR;
         }
         auto *b = new vnpu_buffer_t();
+        register_device_range(p, static_cast<size_t>(bytes));
         b->device = device;
         b->dev_ptr = p;
         b->bytes = bytes;
@@ -783,6 +789,7 @@ VNPU_API void VNPU_CALL vnpu_buffer_free(vnpu_buffer_t *buffer)
 {
     if (!buffer) return;
     if (buffer->dev_ptr) {
+        unregister_device_range(buffer->dev_ptr);
         (void)hipSetDevice(buffer->device->hip_device);
         (void)hipFree(buffer->dev_ptr);
     }

@@ -189,5 +189,8 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
 void destroy_packed(vnpu_packed_weights_t *w);
 
 bool is_device_pointer(const void *p);
+// Ranges this library allocated in HBM: classified without a HIP query.
+void register_device_range(const void *p, size_t bytes);
+void unregister_device_range(const void *p);
 
 }  // namespace vnpu

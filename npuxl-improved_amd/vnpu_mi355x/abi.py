@@ -285,6 +285,7 @@ SIGNATURES = {
     "vnpu_opcode_name": (C.c_char_p, [u32]),
     "vnpu_unit_name": (C.c_char_p, [u32]),
     "vnpu_get_backend_v1": (vp, []),
+    "vnpu_stream_hip_handle": (vp, [vp]),  # MI355X additive extension
 }
 
 LAYOUT = {  # LP64 sizes measured on the reference header
