@@ -129,3 +129,19 @@ def attention(s, Q, K, V, mask=None, causal=0, scale=0.0):
         if x is not None:
             s.free(x)
     return out
+
+
+def mtp_head(s, hidden, W, bias=None, trans_w=0):
+    hidden = np.ascontiguousarray(hidden, np.float32)
+    gamma, hd = hidden.shape
+    vocab = W.shape[0] if trans_w else W.shape[1]
+    bh, bw = s.upload(hidden), s.upload(np.asarray(W, np.float32))
+    bb = s.upload(np.asarray(bias, np.float32)) if bias is not None else None
+    bl = s.alloc(4 * gamma * vocab)
+    s.run(abi.OP_MTP_HEAD_F32, hidden=bh, W=bw, bias=bb.ptr if bb else None, logits=bl,
+          gamma=gamma, hidden_dim=hd, vocab=vocab, trans_w=trans_w)
+    out = s.download(bl, np.float32, (gamma, vocab))
+    for x in (bh, bw, bb, bl):
+        if x is not None:
+            s.free(x)
+    return out

@@ -167,3 +167,51 @@ def test_wildcat_cull_geometry(ref, M, N, unit):
     want = oracle.matmul_f32(A, B, None, None, M, K, N, 0, 0, 1.0, 0.0, 0, cull=cull)
     assert np.array_equal(got == 0.0, cull.astype(bool))
     assert oracle.rel_error(got, want) <= 1e-4
+
+
+def _ref_session(env):
+    """A reference device created under extra environment settings (read by
+    the reference at device creation, src/core/runtime.cpp:889-903)."""
+    import os
+    from vnpu_mi355x import Session
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        cfg = abi.Config()
+        cfg.abi_version = 1
+        cfg.num_threads = 4
+        return Session(oracle.REF_LIB_PATH, cfg)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def test_matmul_f32_config1_epilogue_and_packed_defect(ref):
+    """Config 1's MATMUL_F32 (512^3, bias, alpha 1, beta 0, SiLU).
+
+    With VNPU_PACK=0 the reference computes the documented
+    silu(A.B + bias), which the oracle restates.  Its default packed AVX2
+    path (src/kernels/kernels.cpp:313-323) applies the epilogue after the
+    first 128-deep K block only; this test records that the defect is real
+    at this shape, and why the oracle does not follow the default path.
+    """
+    rng = np.random.default_rng(99)
+    M = K = N = 512
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.02 * rng.standard_normal((K, N))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    want = oracle.matmul_f32(A, B, None, bias, M, K, N, 0, 0, 1.0, 0.0, abi.EPI_SILU)
+    exact = oracle.matmul_f32(A, B, None, bias, M, K, N, 0, 0, 1.0, 0.0, abi.EPI_SILU,
+                              acc64=True)
+    assert oracle.rel_error(want, exact) <= 1e-5
+    unpacked = _ref_session({"VNPU_PACK": "0"})
+    try:
+        got = g.matmul_f32(unpacked, A, B, M, K, N, bias=bias, epilogue=abi.EPI_SILU)
+    finally:
+        unpacked.close()
+    assert oracle.rel_error(got, want) <= 1e-4
+    packed = g.matmul_f32(ref, A, B, M, K, N, bias=bias, epilogue=abi.EPI_SILU)
+    assert oracle.rel_error(packed, want) > 1e-2
