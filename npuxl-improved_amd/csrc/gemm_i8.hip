@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_generic(I8Gemm p)
             if (!z[j] && p.zero_blocks) z[j] = p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] != 0;
             b[j] = (v4i){0, 0, 0, 0};
             if (!z[j])
-                b[j] = *reinterpret_cast<const v4i *>(p.frag + ((static_cast<uint64_t>(kt) * NT + nb) << 10) + lane * 16);
+                b[j] = *reinterpret_cast<const v4i *>(p.frag + ((static_cast<uint64_t>(nb) * KT + kt) << 10) + lane * 16);
         }
     };
 
@@ -312,8 +312,8 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tile
             stride[j] = 64;
         } else {
             const uint32_t nb = min((n0 >> 4) + (b - kABlocks), NT - 1);
-            src[j] = p.frag + (static_cast<uint64_t>(nb) << 10) + lane * 16;
-            stride[j] = static_cast<uint64_t>(NT) << 10;
+            src[j] = p.frag + ((static_cast<uint64_t>(nb) * (p.Kp >> 6)) << 10) + lane * 16;
+            stride[j] = 1024;
         }
     }
     auto issue = [&](uint32_t kt) {

@@ -8,18 +8,26 @@
 //   acc = sum_k A[m][k] * B[k][n] in int32 (exact, so any order is bit-exact).
 //
 // Design (HBM-bound: every weight byte is read once, ~K*N bytes per call):
-//   * one workgroup = 4 waves owns T 16-column blocks over all of K;
-//   * the weights are read in the packed fragment layout: for each 64-deep
-//     k block one 1 KiB run per 16 columns; lane l = 16*kg + c loads 16 bytes
-//     = 16 consecutive k of column c (fully coalesced 16-byte loads);
-//   * waves stride over the k blocks (wave w takes kt = w, w+4, ...), with
-//     U k blocks of loads in flight per lane before any arithmetic;
-//   * the activations (M x K int8, tiny) are staged once per workgroup in LDS
-//     as [k/16][m][16], so lane kg reads its 16 bytes of every row with one
-//     ds_read_b128 per row;
+//   * one workgroup of W waves owns one 16-column strip over all of K; the
+//     packed layout stores a strip's Kp/64 blocks of 1 KiB contiguously, so
+//     the workgroup streams one sequential run;
+//   * lane l = 16*kg + c loads 16 bytes = 16 consecutive k of column c
+//     (one fully coalesced 1 KiB load per wave per block); waves interleave
+//     over the blocks (wave w takes blocks w, w+W, ...), with U blocks in
+//     flight per wave and the next U issued before the current U are used;
+//   * weight loads are raw buffer loads: the bounds check of the buffer
+//     resource turns loads past the wave's last block into zeros, so the
+//     load stream has no branches (branches around loads force the waitcnt
+//     pass into full drains), and they are nontemporal: the weights are read
+//     once and are not worth an L2 allocation;
+//   * the activations (M x K int8, tiny) are staged in LDS as [k/16][m][16]
+//     (dynamic LDS sized to the chunk actually used), so lane kg reads its
+//     16 bytes of every row with one ds_read_b128 per row;
 //   * v_dot4_i32_i8 (4 per 16 bytes per row) accumulates in int32;
 //   * lanes of equal c reduce over kg with two cross-lane shuffles, waves
-//     reduce through LDS, and 16*T*M threads apply the fused epilogue.
+//     reduce through LDS, and 16*M threads apply the fused epilogue.
+// Blocks flagged all-zero by PACK_WEIGHTS_I8 are streamed like any other: the
+// zero bytes are in memory, so skipping them would only save bandwidth.
 #include "kernels.hpp"
 #include "device_math.hpp"
 
@@ -27,8 +35,9 @@ namespace vnpu {
 namespace k {
 namespace {
 
-constexpr int kUnroll = 8;           // k blocks per batch in flight per wave
-constexpr uint32_t kLdsA = 32768;    // bytes of LDS for staged activations
+constexpr uint32_t kLdsA = 32768;   // max bytes of staged activations per chunk
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
+constexpr int kNontemporal = 2;           // cache policy bits of the weight loads
 
 __device__ __forceinline__ int dot16(const int4 a, const int4 b, int acc)
 {
@@ -39,58 +48,48 @@ __device__ __forceinline__ int dot16(const int4 a, const int4 b, int acc)
     return acc;
 }
 
-// M rows, T 16-column blocks per workgroup, W waves splitting K.
-template <int M, int T, int W>
-__global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p)
+// M rows, W waves, U blocks in flight per wave; chunk_k = k extent (multiple
+// of 64) of the activations staged at a time.
+template <int M, int W, int U>
+__global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chunk_k)
 {
-    constexpr int kThreads = 64 * W;
-    constexpr uint32_t kChunkK = (kLdsA / M) & ~63u;  // whole 64-deep k blocks
-    __shared__ __attribute__((aligned(16))) int8_t a_lds[kChunkK * M];
-    __shared__ int red[W][T][M][16];
+    extern __shared__ __attribute__((aligned(16))) int8_t a_lds[];  // [chunk_k/16][M][16]
+    __shared__ int red[W][M][16];
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave-uniform by construction; readfirstlane lets the compiler know
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kg = lane >> 4;
-    const uint32_t NT = p.Np >> 4;
-    const uint32_t nt0 = blockIdx.x * T;
+    const uint32_t nt = blockIdx.x;
+    const uint32_t KT = p.Kp >> 6;
+    const int8_t *strip = p.frag + static_cast<uint64_t>(nt) * KT * 1024;
     const bool vec_a = ((p.lda & 15u) == 0) && ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0);
 
-    int acc[T][M];
+    int acc[M];
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[t][m] = 0;
+    for (int m = 0; m < M; ++m) acc[m] = 0;
 
-    for (uint32_t kc = 0; kc < p.Kp; kc += kChunkK) {
-        const uint32_t kc_len = min(kChunkK, p.Kp - kc);
-        const uint32_t kt_begin = kc >> 6, kt_end = (kc + kc_len) >> 6;
-        const uint32_t first = kt_begin + wave;
-        const uint32_t nsteps = first < kt_end ? (kt_end - first + W - 1) / W : 0;
-
+    for (uint32_t kc = 0; kc < p.Kp; kc += chunk_k) {
+        const uint32_t kt0 = kc >> 6, kt1 = min(KT, (kc + chunk_k) >> 6);
+        const uint32_t first = kt0 + wave;
+        const uint32_t cnt = first < kt1 ? (kt1 - first + W - 1) / W : 0;
+        // This wave's blocks first, first + W, ... as one bounds-checked buffer.
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t *>(strip) + static_cast<uint64_t>(first) * 1024, 0,
+            cnt ? static_cast<int>(((cnt - 1) * W + 1) * 1024) : 0, kBufferWord3);
+        auto ld = [&](uint32_t i) {
+            return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(
+                rs, i * W * 1024 + lane * 16, 0, kNontemporal));
+        };
         // The weight stream does not depend on the activations: put the first
         // batch in flight before staging them.
-        int4 bc[kUnroll][T], bn[kUnroll][T];
-        auto load_batch = [&](int4 (&b)[kUnroll][T], uint32_t i0) {
+        int4 bc[U], bn[U];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const uint32_t step = i0 + u;
-                const uint32_t kt = first + step * W;
-#pragma unroll
-                for (int t = 0; t < T; ++t) {
-                    b[u][t] = make_int4(0, 0, 0, 0);
-                    if (step < nsteps && nt0 + t < NT) {
-                        const uint64_t blk = static_cast<uint64_t>(kt) * NT + nt0 + t;
-                        if (!p.zero_blocks || !p.zero_blocks[blk])
-                            b[u][t] = *reinterpret_cast<const int4 *>(p.frag + (blk << 10) + lane * 16);
-                    }
-                }
-            }
-        };
-        load_batch(bc, 0);
+        for (int u = 0; u < U; ++u) bc[u] = ld(u);
 
-        __syncthreads();  // previous chunk fully consumed
-        const uint32_t chunks = (kc_len >> 4) * M;
-        for (uint32_t i = tid; i < chunks; i += kThreads) {
+        if (kc) __syncthreads();  // previous chunk fully consumed
+        const uint32_t chunks = (kt1 - kt0) * 4 * M;
+        for (uint32_t i = tid; i < chunks; i += 64 * W) {
             const uint32_t m = i % M, k16 = i / M;
             const uint32_t k = kc + k16 * 16;
             const int8_t *src = p.A + static_cast<uint64_t>(m) * p.lda + k;
@@ -110,54 +109,44 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p)
         }
         __syncthreads();
 
-        for (uint32_t i = 0; i < nsteps; i += kUnroll) {
-            if (i + kUnroll < nsteps) load_batch(bn, i + kUnroll);
+        for (uint32_t i = 0; i < cnt; i += U) {
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const uint32_t step = i + u;
-                if (step >= nsteps) break;
-                const uint32_t ktl = first + step * W - kt_begin;
+            for (int u = 0; u < U; ++u) bn[u] = ld(i + U + u);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                // past the last block the weights read as zero; clamp the
+                // activation index so it stays inside the staged chunk
+                const uint32_t ktl = first + W * min(i + u, cnt - 1) - kt0;
                 const int8_t *arow = a_lds + ((ktl * 4 + kg) * M) * 16;
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const int4 a = *reinterpret_cast<const int4 *>(arow + m * 16);
-#pragma unroll
-                    for (int t = 0; t < T; ++t) acc[t][m] = dot16(a, bc[u][t], acc[t][m]);
-                }
+                for (int m = 0; m < M; ++m)
+                    acc[m] = dot16(*reinterpret_cast<const int4 *>(arow + m * 16), bc[u], acc[m]);
             }
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u)
-#pragma unroll
-                for (int t = 0; t < T; ++t) bc[u][t] = bn[u][t];
+            for (int u = 0; u < U; ++u) bc[u] = bn[u];
         }
     }
 
     // Reduce the four k groups (lanes c, c+16, c+32, c+48).
 #pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            int v = acc[t][m];
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            acc[t][m] = v;
-        }
+    for (int m = 0; m < M; ++m) {
+        int v = acc[m];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        acc[m] = v;
+    }
     if (lane < 16) {
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-#pragma unroll
-            for (int m = 0; m < M; ++m) red[wave][t][m][lane] = acc[t][m];
+        for (int m = 0; m < M; ++m) red[wave][m][lane] = acc[m];
     }
     __syncthreads();
-    for (int o = tid; o < T * M * 16; o += kThreads) {
-        const int c = o & 15;
-        const int m = (o >> 4) % M;
-        const int t = (o >> 4) / M;
-        const uint32_t n = (nt0 + t) * 16 + c;
+    for (int o = tid; o < M * 16; o += 64 * W) {
+        const int c = o & 15, m = o >> 4;
+        const uint32_t n = nt * 16 + c;
         if (n < p.N) {
             int s = 0;
 #pragma unroll
-            for (int w = 0; w < W; ++w) s += red[w][t][m][c];
+            for (int w = 0; w < W; ++w) s += red[w][m][c];
             const float sa = p.scale_a ? p.scale_a[m] : 1.0f;
             float out = __fmul_rn(__fmul_rn(static_cast<float>(s), sa), p.scale_b[n]);
             if (p.bias) out = __fadd_rn(out, p.bias[n]);
@@ -166,18 +155,23 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p)
     }
 }
 
-// Launch shape from the column count: two column blocks per workgroup once
-// there are enough of them, and eight waves when workgroups are scarce.
+// Launch shape (measured on MI355X with the weights streamed from HBM): four
+// waves with eight blocks in flight each for one or two rows; eight waves
+// when strips are few (the grid is one workgroup per strip); from three rows
+// up the activation reads from LDS grow with M, and eight waves with four
+// blocks each keep more of them overlapped.
 template <int M>
 void launch_m(hipStream_t s, const I8Gemm &p)
 {
     const uint32_t NT = p.Np >> 4;
-    if (NT >= 1024)
-        gemv_i8_kernel<M, 2, 4><<<dim3((NT + 1) / 2), 256, 0, s>>>(p);
-    else if (NT >= 512)
-        gemv_i8_kernel<M, 1, 4><<<dim3(NT), 256, 0, s>>>(p);
+    const uint32_t chunk_k = std::min<uint32_t>(p.Kp, (kLdsA / M) & ~63u);
+    const size_t lds = static_cast<size_t>(chunk_k) * M;
+    if (M <= 2 && NT >= 512)
+        gemv_i8_kernel<M, 4, 8><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
+    else if (M <= 2)
+        gemv_i8_kernel<M, 8, 8><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
     else
-        gemv_i8_kernel<M, 1, 8><<<dim3(NT), 512, 0, s>>>(p);
+        gemv_i8_kernel<M, 8, 4><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
 }
 
 }  // namespace

@@ -22,7 +22,7 @@ void quantize_tensor(hipStream_t s, const float *X, int8_t *Y, float *scales, ui
                      float *ws);
 
 // ---- PACK_WEIGHTS_I8 (pack.hip) ----
-// Writes the fragment layout [Kp/64][Np/16][4][16][16] (zero padded), the
+// Writes the fragment layout [Np/16][Kp/64][4][16][16] (zero padded), the
 // per-column sums [N] and the all-zero 1 KiB block map [Kp/64][Np/16].
 void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint32_t ldb,
                     uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,

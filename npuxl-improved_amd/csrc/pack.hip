@@ -4,16 +4,18 @@
 // AVX2 kernels never read (src/core/scheduler.cpp:763-836).  This backend
 // packs into the layout its gfx950 kernels consume directly:
 //
-//   frag[kt][nt][kg][c][j] = B[k = 64*kt + 16*kg + j][n = 16*nt + c]
+//   frag[nt][kt][kg][c][j] = B[k = 64*kt + 16*kg + j][n = 16*nt + c]
 //
-// with kt < Kp/64, nt < Np/16, kg < 4, c < 16, j < 16 (zero padded).  One
-// (kt, nt) block is 1 KiB and is exactly the B operand of one
-// v_mfma_i32_16x16x64_i8: lane l = 16*kg + c loads the 16 bytes at 16*l.
-// For a fixed kt the Np/16 blocks are contiguous, so a workgroup's B tile of
-// BN columns is one contiguous BN*64-byte run per k step.
+// with nt < Np/16, kt < Kp/64, kg < 4, c < 16, j < 16 (zero padded).  One
+// (kt, nt) block is 1 KiB: lane l = 16*kg + c of a wave loads the 16 bytes
+// at 16*l, i.e. 16 consecutive k of one column, which is the per-lane B
+// operand of the int8 MFMAs and four v_dot4 of the GEMV.  Blocks are stored
+// column-strip-major: the Kp/64 blocks of one 16-column strip are one
+// contiguous run, so the decode GEMV streams each strip sequentially.
 //
 // Also produced: per-column sums (reference scheduler.cpp:798-800) and a
-// per-block all-zero map that lets MATMUL_I8 skip zero weight blocks exactly.
+// [Kp/64][Np/16] all-zero block map that lets MATMUL_I8 skip zero weight
+// blocks exactly.
 #include "kernels.hpp"
 
 namespace vnpu {
@@ -22,17 +24,17 @@ namespace {
 
 __global__ __launch_bounds__(256) void pack_frag_kernel(const int8_t *__restrict__ B, uint32_t K,
                                                         uint32_t N, uint32_t ldb, uint32_t trans_b,
-                                                        int8_t *__restrict__ frag, uint32_t NT,
+                                                        int8_t *__restrict__ frag, uint32_t KT,
                                                         uint64_t chunks)
 {
     const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= chunks) return;
-    // idx = ((kt * NT + nt) * 4 + kg) * 16 + c
+    // idx = ((nt * KT + kt) * 4 + kg) * 16 + c
     const uint32_t c = idx & 15;
     const uint32_t kg = (idx >> 4) & 3;
     const uint64_t blk = idx >> 6;
-    const uint32_t nt = static_cast<uint32_t>(blk % NT);
-    const uint32_t kt = static_cast<uint32_t>(blk / NT);
+    const uint32_t kt = static_cast<uint32_t>(blk % KT);
+    const uint32_t nt = static_cast<uint32_t>(blk / KT);
     const uint32_t n = nt * 16 + c;
     const uint32_t k0 = kt * 64 + kg * 16;
     union {
@@ -50,32 +52,49 @@ __global__ __launch_bounds__(256) void pack_frag_kernel(const int8_t *__restrict
     reinterpret_cast<int4 *>(frag)[idx] = u.v;
 }
 
-__global__ __launch_bounds__(256) void column_sums_kernel(const int8_t *__restrict__ B, uint32_t K,
-                                                          uint32_t N, uint32_t ldb,
-                                                          uint32_t trans_b,
+// One workgroup per 16-column strip: the strip's blocks are contiguous, lane
+// 16*kg + c sums its 16 bytes of column c with one v_dot4 against ones, the
+// four k groups reduce by shuffles and the waves through LDS.  Padding is
+// zero, so the sums equal those over the K x N weights.
+__global__ __launch_bounds__(256) void column_sums_kernel(const int8_t *__restrict__ frag,
+                                                          uint32_t KT, uint32_t N,
                                                           int32_t *__restrict__ sums)
 {
-    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
-    if (n >= N) return;
-    int32_t s = 0;
-    if (trans_b) {
-        const int8_t *row = B + static_cast<uint64_t>(n) * ldb;
-        for (uint32_t k = 0; k < K; ++k) s += row[k];
-    } else {
-        for (uint32_t k = 0; k < K; ++k) s += B[static_cast<uint64_t>(k) * ldb + n];
+    __shared__ int red[4][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t nt = blockIdx.x;
+    const int4 *strip = reinterpret_cast<const int4 *>(frag + static_cast<uint64_t>(nt) * KT * 1024);
+    const int ones = 0x01010101;
+    int s = 0;
+    for (uint32_t kt = wave; kt < KT; kt += 4) {
+        const int4 v = strip[static_cast<uint64_t>(kt) * 64 + lane];
+        s = __builtin_amdgcn_sdot4(v.x, ones, s, false);
+        s = __builtin_amdgcn_sdot4(v.y, ones, s, false);
+        s = __builtin_amdgcn_sdot4(v.z, ones, s, false);
+        s = __builtin_amdgcn_sdot4(v.w, ones, s, false);
     }
-    sums[n] = s;
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+    if (lane < 16) red[wave][lane] = s;
+    __syncthreads();
+    if (tid < 16) {
+        const uint32_t n = nt * 16 + tid;
+        if (n < N) sums[n] = red[0][tid] + red[1][tid] + red[2][tid] + red[3][tid];
+    }
 }
 
-// One wave per 1 KiB block: 1 if every byte is zero.
+// One wave per 1 KiB block (frag order): 1 if every byte is zero, written
+// to the [kt][nt] map.
 __global__ __launch_bounds__(64) void zero_block_kernel(const int8_t *__restrict__ frag,
+                                                        uint32_t KT, uint32_t NT,
                                                         uint8_t *__restrict__ zero_blocks)
 {
     const uint64_t blk = blockIdx.x;
     const int4 v = reinterpret_cast<const int4 *>(frag + blk * 1024)[threadIdx.x];
     const int any = (v.x | v.y | v.z | v.w) != 0;
     const unsigned long long nz = __ballot(any);
-    if (threadIdx.x == 0) zero_blocks[blk] = nz == 0ull ? 1 : 0;
+    const uint32_t kt = static_cast<uint32_t>(blk % KT), nt = static_cast<uint32_t>(blk / KT);
+    if (threadIdx.x == 0) zero_blocks[static_cast<uint64_t>(kt) * NT + nt] = nz == 0ull ? 1 : 0;
 }
 
 }  // namespace
@@ -84,13 +103,13 @@ void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint
                     uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,
                     int32_t *column_sums, uint8_t *zero_blocks)
 {
-    const uint32_t NT = Np / 16;
-    const uint64_t blocks = static_cast<uint64_t>(Kp / 64) * NT;
+    const uint32_t NT = Np / 16, KT = Kp / 64;
+    const uint64_t blocks = static_cast<uint64_t>(KT) * NT;
     const uint64_t chunks = blocks * 64;
     pack_frag_kernel<<<dim3(static_cast<uint32_t>((chunks + 255) / 256)), 256, 0, s>>>(
-        B, K, N, ldb, trans_b, frag, NT, chunks);
-    column_sums_kernel<<<dim3((N + 255) / 256), 256, 0, s>>>(B, K, N, ldb, trans_b, column_sums);
-    zero_block_kernel<<<dim3(static_cast<uint32_t>(blocks)), 64, 0, s>>>(frag, zero_blocks);
+        B, K, N, ldb, trans_b, frag, KT, chunks);
+    column_sums_kernel<<<dim3(NT), 256, 0, s>>>(frag, KT, N, column_sums);
+    zero_block_kernel<<<dim3(static_cast<uint32_t>(blocks)), 64, 0, s>>>(frag, KT, NT, zero_blocks);
 }
 
 }  // namespace k

@@ -109,7 +109,7 @@ struct vnpu_packed_weights {
     uint32_t K = 0, N = 0;
     uint32_t Kp = 0;               // K rounded up to 64
     uint32_t Np = 0;               // N rounded up to 16
-    int8_t *frag = nullptr;        // HBM, [Kp/64][Np/16][4][16][16] fragment layout
+    int8_t *frag = nullptr;        // HBM, [Np/16][Kp/64][4][16][16] fragment layout
     float *scales_dev = nullptr;   // HBM [Np], padding = 1
     uint8_t *zero_blocks = nullptr;// HBM [Kp/64][Np/16]: 1 = all 1 KiB of the block zero
     uint64_t zero_block_count = 0;
