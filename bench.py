@@ -164,6 +164,152 @@ def bench_gemm_i8(s: Session, M, K, N, steps, warmup):
             "kernel_tops": ops / gpu_ns / 1e3, "frac_peak": ops / gpu_ns / 1e3 / I8_PEAK_TOPS}
 
 
+def gpu_timed(s: Session, enqueue, steps: int, warmup: int):
+    """Average GPU ms per step of an enqueue() that submits several commands:
+    a hipEvent pair on the vnpu stream around `steps` enqueues."""
+    for _ in range(warmup):
+        enqueue()
+    s.check("sync", s.sync())
+    ev = HipEvents(s)
+    t0 = time.perf_counter()
+    ev.record(ev.e0)
+    for _ in range(steps):
+        enqueue()
+    ev.record(ev.e1)
+    s.check("sync", s.sync())
+    wall = time.perf_counter() - t0
+    ms = ev.elapsed_ms() / steps
+    ev.close()
+    return ms, wall * 1e3 / steps
+
+
+def rounded(d, nd=4):
+    return {k: (round(v, nd) if isinstance(v, float) else v) for k, v in d.items()}
+
+
+def bench_config1(s: Session, steps: int):
+    """512^3 int8 (QUANTIZE rows -> MATMUL_I8 with packed per-column weights)
+    and MATMUL_F32 on the same A, B with bias, alpha 1, beta 0, SiLU."""
+    M = K = N = 512
+    a = synth.normal("c1/A", (M, K))
+    b = synth.normal("c1/B", (K, N), 0.02)
+    bias = synth.normal("c1/bias", (N,), 0.1)
+    ba, bb, bbias, bc = s.upload(a), s.upload(b), s.upload(bias), s.alloc(4 * M * N)
+    a8, sa, b8, sb = s.alloc(M * K), s.alloc(4 * M), s.alloc(K * N), s.alloc(4 * N)
+    s.run(abi.OP_QUANTIZE_I8, X=bb, Y=b8, scales=sb, rows=K, cols=N, axis=abi.QUANT_PER_COLUMN)
+    w = s.pack(b8, K, N, scales=sb)
+    q = lambda: s.command(abi.OP_QUANTIZE_I8, X=ba, Y=a8, scales=sa, rows=M, cols=K,
+                          axis=abi.QUANT_PER_ROW)
+    g = lambda: s.command(abi.OP_MATMUL_I8, A=a8, B=w, scale_a=sa, C=bc, M=M, K=K, N=N)
+    f = lambda: s.command(abi.OP_MATMUL_F32, A=ba, B=bb, bias=bbias, C=bc, M=M, K=K, N=N,
+                          alpha=1.0, beta=0.0, epilogue=abi.EPI_SILU)
+    i8_ms, _ = gpu_timed(s, lambda: s.check("submit", s.submit([q(), g()])), steps, 5)
+    f32_ms, _ = gpu_timed(s, lambda: s.check("submit", s.submit([f()])), steps, 5)
+    s.release_packed(w)
+    for x in (ba, bb, bbias, bc, a8, sa, b8, sb):
+        s.free(x)
+    ops = 2.0 * M * K * N
+    return {"shape": "512x512x512", "i8_quantize_plus_matmul_us": i8_ms * 1e3,
+            "i8_tops": ops / i8_ms / 1e9, "f32_silu_us": f32_ms * 1e3,
+            "f32_tflops": ops / f32_ms / 1e9}
+
+
+def bench_gemm_f32(s: Session, M, K, N, steps, warmup):
+    """Config 3 f32: B stored [N][K] (trans_b), bias, alpha 1, beta 0.5 onto C, GELU."""
+    a = synth.normal(f"c3/A_{M}x{K}", (M, K))
+    bt = synth.normal(f"c3/Bt_{N}x{K}", (N, K), 0.02)
+    bias = synth.normal(f"c3/bias_{N}", (N,), 0.1)
+    c0 = synth.normal(f"c3/C_{M}x{N}", (M, N))
+    ba, bb, bbias, bc = s.upload(a), s.upload(bt), s.upload(bias), s.upload(c0)
+    del a, bt, c0
+    mk = lambda i: s.command(abi.OP_MATMUL_F32, id=i, A=ba, B=bb, bias=bbias, C=bc, M=M, K=K, N=N,
+                             trans_b=1, alpha=1.0, beta=0.5, epilogue=abi.EPI_GELU_TANH)
+    wall, gpu_ns = timed(s, mk, steps, warmup)
+    for x in (ba, bb, bbias, bc):
+        s.free(x)
+    flops = 2.0 * M * K * N
+    return {"M": M, "K": K, "N": N, "kernel_us": gpu_ns / 1e3, "kernel_tflops": flops / gpu_ns / 1e3,
+            "frac_peak": flops / gpu_ns / 1e3 / F32_PEAK_TFLOPS}
+
+
+def bench_block(s: Session, steps: int):
+    """Config 4: one Llama-style layer, prefill B1 S2048 and decode B8 @ ctx 4096."""
+    from vnpu_mi355x.block import LLAMA_4096, Block, weights_f32
+
+    sh = LLAMA_4096
+    blk = Block(s, sh, weights_f32(sh, "config4"))
+    out = {}
+    try:
+        blk.prepare(1, 2048)
+        blk.set_input(synth.normal("config4/prefill/x", (2048, sh.d_model)))
+        ms, wall = gpu_timed(s, lambda: blk.enqueue(True), max(3, steps // 4), 1)
+        out["prefill_b1_s2048"] = {"ms": ms, "wall_ms": wall, "tok_s": 2048 / ms * 1e3}
+        ctx = 4096
+        blk.prepare(8, 1, past=ctx - 1, cache_len=ctx)
+        kv = (8, sh.heads, ctx, sh.head_dim)
+        blk.set_input(synth.normal("config4/decode/x", (8, sh.d_model)),
+                      synth.normal("config4/decode/k_cache", kv), synth.normal("config4/decode/v_cache", kv))
+        ms, wall = gpu_timed(s, lambda: blk.enqueue(True), steps, 3)
+        out["decode_b8_ctx4096"] = {"ms": ms, "wall_ms": wall, "tok_s": 8 / ms * 1e3}
+    finally:
+        blk.close()
+    return out
+
+
+def bench_config5(s: Session, steps: int):
+    """Config 5: int8 4096^3 with half of the 64x64 weight tiles zero (seeded
+    Bernoulli), and the MTP head [4,4096] x [4096,32000] f32 + softmax."""
+    M = K = N = 4096
+    w = synth.normal("c5/W", (K, N), 0.02)
+    keep = synth.bernoulli_mask("c5/tiles", (K // 64, N // 64), 0.5)
+    w *= np.kron(keep, np.ones((64, 64), np.uint8)).astype(np.float32)
+    bw = s.upload(w)
+    del w
+    wq, ws = s.alloc(K * N), s.alloc(4 * N)
+    s.run(abi.OP_QUANTIZE_I8, X=bw, Y=wq, scales=ws, rows=K, cols=N, axis=abi.QUANT_PER_COLUMN)
+    s.free(bw)
+    packed = s.pack(wq, K, N, scales=ws)
+    s.free(wq)
+    s.free(ws)
+    x = synth.normal("c5/A", (M, K))
+    bx = s.upload(x)
+    a8, sa, c = s.alloc(M * K), s.alloc(4 * M), s.alloc(4 * M * N)
+    s.run(abi.OP_QUANTIZE_I8, X=bx, Y=a8, scales=sa, rows=M, cols=K, axis=abi.QUANT_PER_ROW)
+    s.free(bx)
+    mk = lambda i: s.command(abi.OP_MATMUL_I8, id=i, A=a8, B=packed, scale_a=sa, C=c, M=M, K=K, N=N)
+    _, gpu_ns = timed(s, mk, steps, 3)
+    s.release_packed(packed)
+    for b in (a8, sa, c):
+        s.free(b)
+    dense = 2.0 * M * K * N
+    out = {"cull_i8_4096": {"kernel_us": gpu_ns / 1e3, "zero_tiles": int(keep.size - keep.sum()),
+                            "dense_equiv_tops": dense / gpu_ns / 1e3,
+                            "useful_tops": dense * keep.mean() / gpu_ns / 1e3}}
+    G, H, V = 4, 4096, 32000
+    hid = s.upload(synth.normal("c5/hidden", (G, H)))
+    wm = synth.normal("c5/mtp_W", (H, V), 0.02)
+    copies = [s.upload(wm) for _ in range(2)]   # 2 x 524 MB: past the 256 MB MALL
+    del wm
+    logits, probs = s.alloc(4 * G * V), s.alloc(4 * G * V)
+    state = {"i": 0}
+
+    def step():
+        wcur = copies[state["i"] % 2]
+        state["i"] += 1
+        s.check("submit", s.submit([
+            s.command(abi.OP_MTP_HEAD_F32, hidden=hid, W=wcur, logits=logits, gamma=G, hidden_dim=H,
+                      vocab=V),
+            s.command(abi.OP_SOFTMAX_F32, X=logits, Y=probs, rows=G, cols=V)]))
+
+    ms, _ = gpu_timed(s, step, steps, 3)
+    for b in copies + [hid, logits, probs]:
+        s.free(b)
+    mtp_bytes = 4.0 * (G * H + H * V + 2 * G * V) + 8.0 * G * V
+    out["mtp_head_softmax"] = {"us": ms * 1e3, "gbs": mtp_bytes / ms / 1e6,
+                               "frac_hbm": mtp_bytes / ms / 1e6 / HBM_PEAK_GBS}
+    return out
+
+
 def cpu_baseline(M, K, N, budget_s: float):
     """The reference runtime (built from its own sources) on this host."""
     import oracle  # checker/baseline infrastructure, used only here
@@ -210,8 +356,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=["gemm_i8"], default=None,
-                    help="run one extra workload alone (for profiling)")
+    ap.add_argument("--only", choices=["gemm_i8", "gemm_f32", "block", "config1", "config5"],
+                    default=None, help="run one extra workload alone (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this backend benchmarks one GPU only; multi-GPU sharding is "
@@ -221,9 +367,19 @@ def main():
     M, K, N = 1, 4096, 32000
     s = Session()
     log("device", s.info().backend.decode())
-    if args.only == "gemm_i8":
-        for n in (4096, 14336):
-            log("gemm_i8", bench_gemm_i8(s, 2048, 4096, n, args.steps, args.warmup))
+    if args.only:
+        if args.only == "gemm_i8":
+            for n in (4096, 14336):
+                log("gemm_i8", bench_gemm_i8(s, 2048, 4096, n, args.steps, args.warmup))
+        elif args.only == "gemm_f32":
+            for n in (4096, 14336):
+                log("gemm_f32", bench_gemm_f32(s, 2048, 4096, n, args.steps, args.warmup))
+        elif args.only == "block":
+            log("block", bench_block(s, args.steps))
+        elif args.only == "config1":
+            log("config1", bench_config1(s, args.steps))
+        else:
+            log("config5", bench_config5(s, args.steps))
         s.close()
         return
     wq, ws = weights_for(s, K, N, f"w_{K}x{N}")
@@ -251,8 +407,22 @@ def main():
             gemm.append({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()})
             log("gemm_i8", gemm[-1])
         extras["config3_gemm_i8"] = gemm
-    s.free(wq)
-    s.free(ws)
+        s.free(wq)
+        s.free(ws)
+        wq = ws = None
+        extras["config1"] = rounded(bench_config1(s, 50), 3)
+        log("config1", extras["config1"])
+        extras["config3_gemm_f32"] = []
+        for n in (4096, 14336):
+            extras["config3_gemm_f32"].append(rounded(bench_gemm_f32(s, 2048, 4096, n, 5, 2)))
+            log("gemm_f32", extras["config3_gemm_f32"][-1])
+        extras["config4_block"] = {k: rounded(v, 3) for k, v in bench_block(s, 20).items()}
+        log("block", extras["config4_block"])
+        extras["config5"] = {k: rounded(v, 3) for k, v in bench_config5(s, 10).items()}
+        log("config5", extras["config5"])
+    if wq is not None:
+        s.free(wq)
+        s.free(ws)
     s.close()
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(M, K, N, args.cpu_budget)

@@ -78,7 +78,10 @@ def test_pack_info(gpu, K, N, trans_b):
 I8_SHAPES = [(1, 64, 16), (1, 4096, 4096), (1, 300, 1100), (2, 257, 33), (3, 1000, 513),
              (4, 4096, 11008), (5, 77, 19), (7, 129, 4000), (8, 4096, 1024),
              (9, 64, 16), (16, 300, 200), (64, 128, 96), (130, 257, 129), (257, 1000, 300),
-             (512, 512, 512), (320, 4096, 700), (100, 1024, 2000), (513, 192, 130)]
+             (512, 512, 512), (320, 4096, 700), (100, 1024, 2000), (513, 192, 130),
+             # decode shapes of the config-4 block: the activations of K = 11008
+             # (M=8) and K = 40000 (M=1) are staged in several LDS chunks
+             (8, 11008, 4096), (8, 4096, 12288), (1, 11008, 4096), (1, 40000, 48), (5, 9000, 33)]
 
 
 @pytest.mark.parametrize("M,K,N", I8_SHAPES)
@@ -235,6 +238,7 @@ def test_rope_positions_and_identity(gpu):
 @pytest.mark.parametrize("b,h,sq,sk,d,causal,use_mask", [
     (1, 2, 5, 5, 16, 1, False), (1, 2, 33, 70, 16, 1, False), (1, 2, 16, 100, 16, 0, True),
     (1, 2, 1, 130, 16, 1, False), (1, 4, 300, 300, 128, 1, False), (2, 2, 1, 4096, 128, 1, False),
+    (8, 32, 1, 4096, 128, 1, False),   # config-4 decode: batch 8, 32 heads, context 4096
     (1, 1, 17, 9, 64, 1, False), (1, 2, 40, 40, 80, 0, False)])
 def test_attention(gpu, b, h, sq, sk, d, causal, use_mask):
     Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
