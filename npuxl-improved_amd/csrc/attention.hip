@@ -18,6 +18,8 @@
 #include "kernels.hpp"
 #include "device_math.hpp"
 
+#include <algorithm>
+
 namespace vnpu {
 namespace k {
 namespace {
@@ -164,6 +166,195 @@ __global__ __launch_bounds__(kThreads) void attn_kernel(Attn a, uint32_t keys_pe
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode kernel (seq_q <= 4, head_dim a multiple of 32): streams K and V.
+//
+// Eight lanes own one key at a time: lane r of a group reads float4 r, r+8,
+// r+16, ... of the key's K and V rows (one contiguous 128-byte segment per
+// float4 index), so a wave reads 8 whole rows per step.  Every group runs its
+// own online softmax (m, l, acc) over the keys it owns (keys kbeg + 32*i +
+// its stream index), so steps need no cross-group reduction; the 32 streams
+// of the workgroup are merged once at the end.  Loads are clamped and
+// flagged rather than branched, and the next key's rows are in flight while
+// the current key is consumed.
+// ---------------------------------------------------------------------------
+constexpr int kStreams = 32;   // 4 waves x 8 groups
+
+__device__ __forceinline__ void merge_stream(float &m, float &l, float &mo, float &lo, float &a,
+                                             float &b)
+{
+    const float M = fmaxf(m, mo);
+    a = (m == -__builtin_inff()) ? 0.0f : dev::fast_expf(m - M);
+    b = (mo == -__builtin_inff()) ? 0.0f : dev::fast_expf(mo - M);
+    l = l * a + lo * b;
+    m = M;
+}
+
+template <int QN, int V4>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t keys_per_split,
+                                                               uint32_t splits, float *ws_acc,
+                                                               float *ws_ml)
+{
+    __shared__ float red_ml[4][QN][2];
+    __shared__ float4 red_acc[4][QN][8][V4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 3, r = lane & 7;
+    const uint32_t D = a.head_dim;
+    const uint64_t bh = blockIdx.y;
+    const uint32_t q0 = blockIdx.x * QN, split = blockIdx.z;
+    const uint32_t sq = a.seq_q, sk = a.seq_k;
+    const uint32_t off = sk > sq ? sk - sq : 0;
+    const uint32_t nq = min(static_cast<uint32_t>(QN), sq - q0);
+    const float4 *Kh = reinterpret_cast<const float4 *>(a.K + bh * sk * D);
+    const float4 *Vh = reinterpret_cast<const float4 *>(a.V + bh * sk * D);
+    const uint32_t D4 = D >> 2;
+
+    float4 q[QN][V4];
+#pragma unroll
+    for (int i = 0; i < QN; ++i)
+#pragma unroll
+        for (int t = 0; t < V4; ++t) {
+            const uint32_t qi = min(q0 + i, sq - 1);
+            q[i][t] = reinterpret_cast<const float4 *>(a.Q + (bh * sq + qi) * D)[r + 8 * t];
+        }
+
+    const uint32_t kbeg = split * keys_per_split;
+    uint32_t kend = min(sk, kbeg + keys_per_split);
+    if (a.causal) kend = min(kend, q0 + nq - 1 + off + 1);
+    const uint32_t stream = wave * 8 + g;
+    const uint32_t nsteps = kend > kbeg ? (kend - kbeg + kStreams - 1) / kStreams : 0;
+
+    float m[QN], l[QN];
+    float4 acc[QN][V4];
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+        m[i] = -__builtin_inff();
+        l[i] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < V4; ++t) acc[i][t] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    auto load = [&](uint32_t step, float4 (&kr)[V4], float4 (&vr)[V4]) {
+        const uint32_t key = min(kbeg + stream + step * kStreams, kend - 1);
+#pragma unroll
+        for (int t = 0; t < V4; ++t) {
+            kr[t] = Kh[static_cast<uint64_t>(key) * D4 + r + 8 * t];
+            vr[t] = Vh[static_cast<uint64_t>(key) * D4 + r + 8 * t];
+        }
+    };
+    float4 kc[V4], vc[V4], kn[V4], vn[V4];
+    if (nsteps) load(0, kc, vc);
+    for (uint32_t step = 0; step < nsteps; ++step) {
+        if (step + 1 < nsteps) load(step + 1, kn, vn);
+        const uint32_t key = kbeg + stream + step * kStreams;
+#pragma unroll
+        for (int i = 0; i < QN; ++i) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int t = 0; t < V4; ++t) {
+                dot = fmaf(q[i][t].x, kc[t].x, dot);
+                dot = fmaf(q[i][t].y, kc[t].y, dot);
+                dot = fmaf(q[i][t].z, kc[t].z, dot);
+                dot = fmaf(q[i][t].w, kc[t].w, dot);
+            }
+            dot += __shfl_xor(dot, 1, 64);
+            dot += __shfl_xor(dot, 2, 64);
+            dot += __shfl_xor(dot, 4, 64);
+            const uint32_t qi = q0 + i;
+            const bool live = key < kend && i < static_cast<int>(nq) && !(a.causal && key > qi + off);
+            if (live) {   // uniform over the 8 lanes of the group
+                float s = dot * a.scale;
+                if (a.mask) s += a.mask[(bh * sq + qi) * sk + key];
+                const float mn = fmaxf(m[i], s);
+                const float al = (m[i] == -__builtin_inff()) ? 0.0f : dev::fast_expf(m[i] - mn);
+                const float p = dev::fast_expf(s - mn);
+                l[i] = fmaf(l[i], al, p);
+#pragma unroll
+                for (int t = 0; t < V4; ++t) {
+                    acc[i][t].x = fmaf(p, vc[t].x, acc[i][t].x * al);
+                    acc[i][t].y = fmaf(p, vc[t].y, acc[i][t].y * al);
+                    acc[i][t].z = fmaf(p, vc[t].z, acc[i][t].z * al);
+                    acc[i][t].w = fmaf(p, vc[t].w, acc[i][t].w * al);
+                }
+                m[i] = mn;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < V4; ++t) {
+            kc[t] = kn[t];
+            vc[t] = vn[t];
+        }
+    }
+
+    // Merge the 8 groups of the wave (lanes differing in bits 3..5), then
+    // the 4 waves through LDS.
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+#pragma unroll
+        for (int sh = 8; sh < 64; sh <<= 1) {
+            float mo = __shfl_xor(m[i], sh, 64), lo = __shfl_xor(l[i], sh, 64), wa, wb;
+            merge_stream(m[i], l[i], mo, lo, wa, wb);
+#pragma unroll
+            for (int t = 0; t < V4; ++t) {
+                float4 o;
+                o.x = __shfl_xor(acc[i][t].x, sh, 64);
+                o.y = __shfl_xor(acc[i][t].y, sh, 64);
+                o.z = __shfl_xor(acc[i][t].z, sh, 64);
+                o.w = __shfl_xor(acc[i][t].w, sh, 64);
+                acc[i][t].x = acc[i][t].x * wa + o.x * wb;
+                acc[i][t].y = acc[i][t].y * wa + o.y * wb;
+                acc[i][t].z = acc[i][t].z * wa + o.z * wb;
+                acc[i][t].w = acc[i][t].w * wa + o.w * wb;
+            }
+        }
+        if (g == 0) {
+            if (r == 0) {
+                red_ml[wave][i][0] = m[i];
+                red_ml[wave][i][1] = l[i];
+            }
+#pragma unroll
+            for (int t = 0; t < V4; ++t) red_acc[wave][i][r][t] = acc[i][t];
+        }
+    }
+    __syncthreads();
+    if (wave != 0 || g != 0) return;
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+        if (i >= static_cast<int>(nq)) break;
+        for (int w = 1; w < 4; ++w) {
+            float mo = red_ml[w][i][0], lo = red_ml[w][i][1], wa, wb;
+            merge_stream(m[i], l[i], mo, lo, wa, wb);
+#pragma unroll
+            for (int t = 0; t < V4; ++t) {
+                const float4 o = red_acc[w][i][r][t];
+                acc[i][t].x = acc[i][t].x * wa + o.x * wb;
+                acc[i][t].y = acc[i][t].y * wa + o.y * wb;
+                acc[i][t].z = acc[i][t].z * wa + o.z * wb;
+                acc[i][t].w = acc[i][t].w * wa + o.w * wb;
+            }
+        }
+        const uint32_t qi = q0 + i;
+        if (splits == 1) {
+            const float inv = l[i] > 0.0f ? 1.0f / l[i] : 0.0f;
+            float4 *o = reinterpret_cast<float4 *>(a.O + (bh * sq + qi) * D);
+#pragma unroll
+            for (int t = 0; t < V4; ++t)
+                o[r + 8 * t] = make_float4(acc[i][t].x * inv, acc[i][t].y * inv, acc[i][t].z * inv,
+                                           acc[i][t].w * inv);
+        } else {
+            const uint64_t row = (static_cast<uint64_t>(split) * gridDim.y + bh) * sq + qi;
+            float4 *o = reinterpret_cast<float4 *>(ws_acc + row * D);
+#pragma unroll
+            for (int t = 0; t < V4; ++t) o[r + 8 * t] = acc[i][t];
+            if (r == 0) {
+                ws_ml[row * 2 + 0] = m[i];
+                ws_ml[row * 2 + 1] = l[i];
+            }
+        }
+    }
+}
+
 // Merge split partials: O = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
 __global__ __launch_bounds__(kThreads) void attn_merge(Attn a, uint32_t splits, uint64_t rows,
                                                        const float *ws_acc, const float *ws_ml)
@@ -188,8 +379,48 @@ __global__ __launch_bounds__(kThreads) void attn_merge(Attn a, uint32_t splits, 
     a.O[row * D + d] = den > 0.0f ? num / den : 0.0f;
 }
 
+template <int QN>
+void decode_launch_v(int v4, dim3 grid, hipStream_t s, const Attn &a, uint32_t kps,
+                     uint32_t splits, float *ws_acc, float *ws_ml)
+{
+    switch (v4) {
+    case 1: attn_decode_kernel<QN, 1><<<grid, kThreads, 0, s>>>(a, kps, splits, ws_acc, ws_ml); break;
+    case 2: attn_decode_kernel<QN, 2><<<grid, kThreads, 0, s>>>(a, kps, splits, ws_acc, ws_ml); break;
+    case 3: attn_decode_kernel<QN, 3><<<grid, kThreads, 0, s>>>(a, kps, splits, ws_acc, ws_ml); break;
+    case 4: attn_decode_kernel<QN, 4><<<grid, kThreads, 0, s>>>(a, kps, splits, ws_acc, ws_ml); break;
+    case 5: attn_decode_kernel<QN, 5><<<grid, kThreads, 0, s>>>(a, kps, splits, ws_acc, ws_ml); break;
+    case 6: attn_decode_kernel<QN, 6><<<grid, kThreads, 0, s>>>(a, kps, splits, ws_acc, ws_ml); break;
+    case 7: attn_decode_kernel<QN, 7><<<grid, kThreads, 0, s>>>(a, kps, splits, ws_acc, ws_ml); break;
+    default: attn_decode_kernel<QN, 8><<<grid, kThreads, 0, s>>>(a, kps, splits, ws_acc, ws_ml); break;
+    }
+}
+
+void decode_launch(int qn, int v4, dim3 grid, hipStream_t s, const Attn &a, uint32_t kps,
+                   uint32_t splits, float *ws_acc, float *ws_ml)
+{
+    if (qn == 1) decode_launch_v<1>(v4, grid, s, a, kps, splits, ws_acc, ws_ml);
+    else if (qn == 2) decode_launch_v<2>(v4, grid, s, a, kps, splits, ws_acc, ws_ml);
+    else decode_launch_v<4>(v4, grid, s, a, kps, splits, ws_acc, ws_ml);
+}
+
+bool use_decode(const Attn &a)
+{
+    return a.seq_q <= 4 && (a.head_dim % 32) == 0 && a.head_dim <= 256;
+}
+
 void plan(const Attn &a, uint32_t &qblocks, uint32_t &splits, uint32_t &kps)
 {
+    if (use_decode(a)) {
+        // One workgroup per (batch, head) and key range: enough ranges for
+        // ~2048 workgroups, each at least 256 keys (8 per stream).
+        qblocks = 1;
+        const uint64_t bh = static_cast<uint64_t>(a.batch) * a.heads;
+        const uint32_t max_splits = std::max<uint32_t>(1, (a.seq_k + 255) / 256);
+        splits = static_cast<uint32_t>(std::min<uint64_t>(max_splits, std::max<uint64_t>(1, (2048 + bh - 1) / bh)));
+        kps = ((a.seq_k + splits - 1) / splits + kStreams - 1) / kStreams * kStreams;
+        splits = (a.seq_k + kps - 1) / kps;
+        return;
+    }
     qblocks = (a.seq_q + BQ - 1) / BQ;
     const uint64_t tiles = static_cast<uint64_t>(qblocks) * a.batch * a.heads;
     splits = 1;
@@ -220,15 +451,21 @@ void attention(hipStream_t s, const Attn &a, float *ws)
     float *ws_acc = ws;
     float *ws_ml = ws ? ws + static_cast<uint64_t>(splits) * rows * D : nullptr;
     dim3 grid(qb, a.batch * a.heads, splits);
-    // Above 64 KiB of dynamic LDS the kernel must opt in (CDNA4 has 160 KiB).
-    static thread_local size_t lds_optin = 0;
-    if (lds > 65536 && lds > lds_optin) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                static_cast<int>(lds)) == hipSuccess)
-            lds_optin = lds;
+    if (use_decode(a)) {
+        const int qn = a.seq_q == 1 ? 1 : a.seq_q == 2 ? 2 : 4;
+        const int v4 = static_cast<int>(D / 32);
+        decode_launch(qn, v4, grid, s, a, kps, splits, ws_acc, ws_ml);
+    } else {
+        // Above 64 KiB of dynamic LDS the kernel must opt in (CDNA4 has 160 KiB).
+        static thread_local size_t lds_optin = 0;
+        if (lds > 65536 && lds > lds_optin) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void *>(attn_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(lds)) == hipSuccess)
+                lds_optin = lds;
+        }
+        attn_kernel<<<grid, kThreads, lds, s>>>(a, kps, splits, ws_acc, ws_ml);
     }
-    attn_kernel<<<grid, kThreads, lds, s>>>(a, kps, splits, ws_acc, ws_ml);
     if (splits > 1) {
         const uint64_t total = rows * D;
         attn_merge<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(

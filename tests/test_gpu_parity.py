@@ -239,6 +239,9 @@ def test_rope_positions_and_identity(gpu):
     (1, 2, 5, 5, 16, 1, False), (1, 2, 33, 70, 16, 1, False), (1, 2, 16, 100, 16, 0, True),
     (1, 2, 1, 130, 16, 1, False), (1, 4, 300, 300, 128, 1, False), (2, 2, 1, 4096, 128, 1, False),
     (8, 32, 1, 4096, 128, 1, False),   # config-4 decode: batch 8, 32 heads, context 4096
+    # decode kernel (seq_q <= 4, head_dim % 32 == 0): query counts, widths, masks
+    (2, 3, 1, 777, 64, 1, True), (1, 2, 3, 300, 96, 1, False), (1, 2, 4, 1000, 256, 1, True),
+    (2, 2, 2, 64, 32, 0, False), (1, 1, 4, 3, 160, 1, False), (3, 1, 1, 1, 128, 1, False),
     (1, 1, 17, 9, 64, 1, False), (1, 2, 40, 40, 80, 0, False)])
 def test_attention(gpu, b, h, sq, sk, d, causal, use_mask):
     Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
