@@ -451,6 +451,211 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tile
     }
 }
 
+// ---------------------------------------------------------------------------
+// 128-deep pipelined kernel (K % 128 == 0): same 256 x 128 tile, 4 waves of
+// 128 x 64 and 32x32x32 MFMAs, but each LDS stage holds a 128-deep k slab,
+// so every row of A is fetched as one full 128-byte line (the 64-deep stage
+// fetched half lines and doubled the L2 requests for A):
+//   * stage = A 256 rows x 128 B (32 KiB) + B 16 fragment blocks (2 k
+//     blocks x 8 column blocks, 16 KiB); 3 stages = 144 KiB of LDS;
+//   * one DMA instruction moves 8 rows of A (lane l: row l/8, 16-byte slot
+//     l%8); the lane fetches k chunk slot ^ ((row >> 1) & 7), so chunk c of
+//     row r sits at r*128 + 16*(c ^ ((r >> 1) & 7)) and the fragment reads
+//     (16 rows at one chunk per quarter wave) hit 16 distinct bank groups;
+//   * one barrier per stage: the wave reads the stage's second half while
+//     the first half's MFMAs issue, then waits for the next stage's DMA.
+// ---------------------------------------------------------------------------
+namespace pipe128 {
+constexpr int TM = 256, TN = 128, SK = 128;  // k depth of one stage
+constexpr int kStages = 3;
+constexpr int kAInstr = TM / 8;                      // 32 x 1 KiB of A per stage
+constexpr int kBInstr = (TN / 16) * (SK / 64);       // 16 x 1 KiB of B per stage
+constexpr int kLoads = (kAInstr + kBInstr) / 4;      // 12 per wave per stage
+constexpr int kAPerWave = kAInstr / 4;               // 8
+constexpr int kStageBytes = (kAInstr + kBInstr) * 1024;  // 48 KiB
+constexpr int kBOff = kAInstr * 1024;
+constexpr size_t kLds = static_cast<size_t>(kStages) * kStageBytes;  // 144 KiB
+static_assert(pipe::kOut + TM * 4 <= static_cast<int>(kLds), "staged tile + row scales fit");
+}  // namespace pipe128
+
+template <bool kSkip>
+__global__ __launch_bounds__(kThreads) void gemm_i8_k128(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
+{
+    using namespace pipe128;
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    const uint32_t total = tiles_m * tiles_n;
+    uint32_t g = blockIdx.x;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const uint32_t tmi = g % tiles_m, tni = g / tiles_m;
+    const uint32_t m0 = tmi * TM, n0 = tni * TN;
+    const uint32_t NT = p.Np >> 4;
+    const uint32_t KS = p.K / SK;          // stages
+    const uint32_t KT = p.K >> 6;          // 64-deep steps
+    const uint64_t KTp = p.Kp >> 6;
+
+    // This wave's DMA sources: 8 A instructions (rows 64*wave .. +63) and 4
+    // B blocks; each advances by a fixed stride per stage.
+    const int8_t *src[kLoads];
+    uint32_t stride[kLoads];
+#pragma unroll
+    for (int j = 0; j < kAPerWave; ++j) {
+        const uint32_t r = (wave * kAPerWave + j) * 8 + (lane >> 3);
+        const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);
+        const uint32_t row = min(m0 + r, p.M - 1);
+        src[j] = p.A + static_cast<uint64_t>(row) * p.lda + c * 16;
+        stride[j] = SK;
+    }
+#pragma unroll
+    for (int j = 0; j < kLoads - kAPerWave; ++j) {
+        const int bi = wave * (kLoads - kAPerWave) + j;   // 0..15: column block bi/2, k block bi%2
+        const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
+        src[kAPerWave + j] = p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + lane * 16;
+        stride[kAPerWave + j] = 2048;
+    }
+    auto issue = [&](uint32_t s) {
+        int8_t *st = smem + (s % kStages) * kStageBytes;
+#pragma unroll
+        for (int j = 0; j < kAPerWave; ++j) dma16(src[j] + s * stride[j], st + (wave * kAPerWave + j) * 1024);
+#pragma unroll
+        for (int j = 0; j < kLoads - kAPerWave; ++j)
+            dma16(src[kAPerWave + j] + static_cast<uint64_t>(s) * stride[kAPerWave + j],
+                  st + kBOff + (wave * (kLoads - kAPerWave) + j) * 1024);
+    };
+
+    // Fragment read offsets (bytes within a stage) for half hh of the stage.
+    // A: rows wm*128 + mb*32 + l%32, k chunk c = 4*hh + 2*h + l/32.
+    // B: column block wn*4 + 2*nb + (l/16)%2, k block hh, k group 2h + l/32.
+    const int sub = (lane >> 4) & 1;
+    int a_row_off[4];
+    uint32_t a_sw[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+        const uint32_t r = wm * 128 + mb * 32 + (lane & 31);
+        a_row_off[mb] = r * 128;
+        a_sw[mb] = (r >> 1) & 7;
+    }
+    auto read_frags = [&](uint32_t s, int hh, Frags &f) {
+        const int8_t *st = smem + (s % kStages) * kStageBytes;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t c = 4 * hh + 2 * h + (lane >> 5);
+            const int boff = kBOff + (((wn * 4 + sub) * 2 + hh) << 10) + (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+                f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+                f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_row_off[mb] + ((c ^ a_sw[mb]) << 4));
+        }
+    };
+
+    uint8_t *zflags = reinterpret_cast<uint8_t *>(smem + kLds);
+    if (kSkip) {
+        for (uint32_t i = tid; i < KT * pipe::kBBlocks; i += kThreads) {
+            const uint32_t kt = i / pipe::kBBlocks, nb = (n0 >> 4) + (i % pipe::kBBlocks);
+            zflags[i] = nb < NT ? p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] : 1;
+        }
+        __syncthreads();
+    }
+    auto zero_step = [&](uint32_t kt) -> bool {
+        return kSkip && *reinterpret_cast<const uint32_t *>(zflags + kt * pipe::kBBlocks + wn * 4) == 0x01010101u;
+    };
+
+    v16i acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i){0};
+    auto mma = [&](const Frags &f, bool skip) {
+        if (skip) return;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+    };
+
+    // Prologue: DMA every stage buffer, wait for stage 0, read its first half.
+    const uint32_t pre = min(KS, static_cast<uint32_t>(kStages));
+    for (uint32_t s = 0; s < pre; ++s) issue(s);
+    if (KS >= 3) wait_vmcnt<2 * kLoads>();
+    else wait_vmcnt<0>();
+    block_barrier();
+    Frags f0, f1;
+    read_frags(0, 0, f0);
+
+    // Steady state, one stage per trip: read the second half while the first
+    // half's MFMAs issue; wait for this wave's DMA of stage s+1 (stage s+2
+    // may stay in flight); barrier (stage s+1 landed everywhere, every wave
+    // holds stage s in registers); refill stage s's buffer with s+3; read
+    // stage s+1's first half while the second half's MFMAs issue.
+    uint32_t s = 0;
+    bool sk0 = zero_step(0), sk1 = false;
+    for (; s + kStages < KS; ++s) {
+        read_frags(s, 1, f1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f0, sk0);
+        sk1 = zero_step(2 * s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<kLoads>();
+        block_barrier();
+        issue(s + kStages);
+        read_frags(s + 1, 0, f0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f1, sk1);
+        sk0 = zero_step(2 * s + 2);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Drain: every remaining stage is in flight or landed; wait once.
+    wait_vmcnt<0>();
+    block_barrier();
+    for (; s < KS; ++s) {
+        read_frags(s, 1, f1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f0, sk0);
+        sk1 = zero_step(2 * s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 1 < KS) {
+            read_frags(s + 1, 0, f0);
+            sk0 = zero_step(2 * s + 2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f1, sk1);
+    }
+
+    __syncthreads();
+    int32_t *tile = reinterpret_cast<int32_t *>(smem);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                tile[(wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * pipe::kOutPitch + wn * 64 +
+                     j * 32 + (lane & 31)] = acc[i][j][r];
+    float *sa_lds = reinterpret_cast<float *>(smem + pipe::kScaleOff);
+    {
+        const uint32_t m = m0 + tid;
+        sa_lds[tid] = (p.scale_a && m < p.M) ? p.scale_a[m] : 1.0f;
+    }
+    __syncthreads();
+    switch (p.epilogue) {
+    case 1: store_tile<1>(p, tile, sa_lds, m0, n0, tid); break;
+    case 2: store_tile<2>(p, tile, sa_lds, m0, n0, tid); break;
+    case 3:
+    case 4: store_tile<3>(p, tile, sa_lds, m0, n0, tid); break;
+    default: store_tile<0>(p, tile, sa_lds, m0, n0, tid); break;
+    }
+}
+
 }  // namespace
 
 void gemm_i8(hipStream_t s, const I8Gemm &p)
@@ -462,15 +667,26 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
     if (aligned) {
         static bool lds_optin = false;
         if (!lds_optin) {
-            lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_i8_pipe<false>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            160 * 1024) == hipSuccess &&
-                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_i8_pipe<true>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            160 * 1024) == hipSuccess;
+            bool ok = true;
+            for (const void *fn : {reinterpret_cast<const void *>(gemm_i8_pipe<false>),
+                                   reinterpret_cast<const void *>(gemm_i8_pipe<true>),
+                                   reinterpret_cast<const void *>(gemm_i8_k128<false>),
+                                   reinterpret_cast<const void *>(gemm_i8_k128<true>)})
+                ok = ok && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               160 * 1024) == hipSuccess;
+            lds_optin = ok;
         }
         const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
         const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
+        if (p.K % pipe128::SK == 0) {
+            if (p.zero_blocks) {
+                const size_t lds = pipe128::kLds + ((p.K / 64) * pipe::kBBlocks + 15) / 16 * 16;
+                gemm_i8_k128<true><<<dim3(tm * tn), kThreads, lds, s>>>(p, tm, tn);
+            } else {
+                gemm_i8_k128<false><<<dim3(tm * tn), kThreads, pipe128::kLds, s>>>(p, tm, tn);
+            }
+            return;
+        }
         // Weights with all-zero 1 KiB blocks take the variant that skips
         // their MFMAs; dense weights the one without the flag reads.
         if (p.zero_blocks) {
