@@ -355,6 +355,189 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill kernel on the f32 matrix cores (head_dim 64 or 128, seq_q > 4).
+//
+// A workgroup of 4 waves owns 128 queries of one (batch, head); wave w owns
+// queries q0 + 32w .. +31.  Keys stream through LDS in blocks of 32 (K
+// transposed to [d][key], V as [key][d], double buffered, the next block
+// prefetched into registers while the current one is multiplied).  Per key
+// block each wave runs v_mfma_f32_32x32x2_f32:
+//   S^T (32 keys x 32 queries) = K . Q^T   (D/2 MFMAs; Q^T stays in VGPRs)
+//   O^T (D x 32 queries)     += V^T . P^T  (D/2 MFMAs)
+// In the accumulator layout lane l holds query l%32 and keys 8j + 4(l/32) + q
+// (register 4j + q), so a query's block max and sum need one cross-lane step
+// (lane l ^ 32), and the P^T operand of PV step s is the lane's own score
+// register s once the key order of that product is chosen as
+// key(s, h) = 8(s/4) + 4h + s%4 (h = l/32).  Online softmax as in the
+// reference (a query whose block is fully masked skips the block), with the
+// reference's fast_expf.  O leaves through LDS for coalesced rows.
+// ---------------------------------------------------------------------------
+typedef float v16f __attribute__((ext_vector_type(16)));
+constexpr int PQ = 128;   // queries per workgroup
+constexpr int PK = 32;    // keys per block
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_prefill_kernel(Attn a)
+{
+    constexpr int D4 = D / 4;
+    constexpr int NS = D / 2;          // QK MFMA steps (2 d per step)
+    constexpr int DB = D / 32;         // 32-wide d blocks of O^T
+    constexpr int KV4 = PK * D4 / kThreads;   // float4 of K (and of V) per thread per block
+    // [2 buffers][D][PK] transposed K, then [2 buffers][PK][D] V; reused for
+    // the output staging (4 waves x 32 x D) after the key loop.
+    __shared__ float lds[4 * PK * D];
+    auto Kt = [&](int buf, int d, int key) -> float & { return lds[(buf * D + d) * PK + key]; };
+    auto Vs = [&](int buf, int key, int d) -> float & { return lds[2 * PK * D + (buf * PK + key) * D + d]; };
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, qc = lane & 31;
+    const uint64_t bh = blockIdx.y;
+    const uint32_t nqb = gridDim.x;
+    const uint32_t q0 = (nqb - 1 - blockIdx.x) * PQ;        // heaviest causal blocks first
+    const uint32_t sq = a.seq_q, sk = a.seq_k;
+    const uint32_t off = sk > sq ? sk - sq : 0;
+    const float *Qh = a.Q + bh * sq * D;
+    const float *Kh = a.K + bh * sk * D;
+    const float *Vh = a.V + bh * sk * D;
+    const float *Mh = a.mask ? a.mask + bh * sq * sk : nullptr;
+
+    const uint32_t qw = q0 + wave * 32;                     // this wave's first query
+    const uint32_t myq = qw + qc;                            // this lane's query
+    // Q^T operand: step s = 2t + e uses d = 4t + 2h + e.
+    float qf[NS];
+    {
+        const float *qrow = Qh + static_cast<uint64_t>(min(myq, sq - 1)) * D;
+#pragma unroll
+        for (int t = 0; t < NS / 2; ++t) {
+            const float2 v = *reinterpret_cast<const float2 *>(qrow + 4 * t + 2 * h);
+            qf[2 * t] = v.x;
+            qf[2 * t + 1] = v.y;
+        }
+    }
+
+    // Keys this workgroup needs (causal: up to its last query's limit).
+    uint32_t kend = sk;
+    if (a.causal) kend = min(sk, min(q0 + PQ, sq) - 1 + off + 1);
+    const uint32_t nblk = (kend + PK - 1) / PK;
+    // This wave's causal limit: its blocks past it contribute nothing.
+    const uint32_t wave_kend = a.causal ? min(kend, min(qw + 32, sq) - 1 + off + 1) : kend;
+
+    // Block loads: K as (key = t % 32, float4 d4 = t / 32 + 8i) so that the
+    // transposed LDS writes of a half wave hit consecutive keys; V row-major.
+    float4 kr[KV4], vr[KV4];
+    auto load_blk = [&](uint32_t kb) {
+#pragma unroll
+        for (int i = 0; i < KV4; ++i) {
+            const uint32_t key = kb * PK + (tid & 31);
+            const uint32_t d4 = (tid >> 5) + 8 * i;
+            kr[i] = key < kend ? reinterpret_cast<const float4 *>(Kh + static_cast<uint64_t>(key) * D)[d4]
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            const uint32_t vi = tid + kThreads * i;          // float4 index in the [32][D] block
+            const uint32_t vkey = kb * PK + vi / D4;
+            vr[i] = vkey < kend ? reinterpret_cast<const float4 *>(Vh + static_cast<uint64_t>(vkey) * D)[vi % D4]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_blk = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < KV4; ++i) {
+            const uint32_t key = tid & 31;
+            const uint32_t d = 4 * ((tid >> 5) + 8 * i);
+            Kt(buf, d + 0, key) = kr[i].x;
+            Kt(buf, d + 1, key) = kr[i].y;
+            Kt(buf, d + 2, key) = kr[i].z;
+            Kt(buf, d + 3, key) = kr[i].w;
+            reinterpret_cast<float4 *>(&Vs(buf, 0, 0))[tid + kThreads * i] = vr[i];
+        }
+    };
+
+    v16f o[DB];
+#pragma unroll
+    for (int b = 0; b < DB; ++b) o[b] = (v16f){0.f};
+    float m = -__builtin_inff(), l = 0.0f;
+
+    if (nblk) {
+        load_blk(0);
+        store_blk(0);
+    }
+    for (uint32_t kb = 0; kb < nblk; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < nblk) load_blk(kb + 1);
+        __syncthreads();   // block kb visible; block kb-1's buffer free for kb+1
+        if (kb * PK < wave_kend) {   // wave-uniform
+            // S^T = K . Q^T
+            v16f s = (v16f){0.f};
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                const int d = 4 * (st >> 1) + 2 * h + (st & 1);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(Kt(buf, d, qc), qf[st], s, 0, 0, 0);
+            }
+            // scores of query myq for keys kb*32 + 8j + 4h + q (register 4j+q)
+            float bmax = -__builtin_inff();
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t key = kb * PK + 8 * (r >> 2) + 4 * h + (r & 3);
+                float v = s[r] * a.scale;
+                if (Mh && key < sk && myq < sq) v += Mh[static_cast<uint64_t>(myq) * sk + key];
+                if (key >= kend || myq >= sq || (a.causal && key > myq + off)) v = -__builtin_inff();
+                s[r] = v;
+                bmax = fmaxf(bmax, v);
+            }
+            bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+            float alpha = 1.0f, psum = 0.0f;
+            if (bmax != -__builtin_inff()) {
+                const float mn = fmaxf(m, bmax);
+                alpha = (m == -__builtin_inff()) ? 0.0f : dev::fast_expf(m - mn);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float p = (s[r] == -__builtin_inff()) ? 0.0f : dev::fast_expf(s[r] - mn);
+                    s[r] = p;
+                    psum += p;
+                }
+                m = mn;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+            }
+            psum += __shfl_xor(psum, 32, 64);
+            l = l * alpha + psum;
+#pragma unroll
+            for (int b = 0; b < DB; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+            // O^T += V^T . P^T, key order key(st, h) = 8(st/4) + 4h + st%4
+#pragma unroll
+            for (int st = 0; st < 16; ++st) {
+                const int key = 8 * (st >> 2) + 4 * h + (st & 3);
+#pragma unroll
+                for (int b = 0; b < DB; ++b)
+                    o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs(buf, key, 32 * b + qc), s[st], o[b], 0, 0, 0);
+            }
+        }
+        if (kb + 1 < nblk) store_blk(buf ^ 1);
+    }
+
+    // O = O^T / l through LDS: this wave's 32 x D tile (reuses the K/V
+    // buffers), column c of row r stored at c ^ r so that the 32 rows of a
+    // register's write land in distinct banks.
+    __syncthreads();
+    float *ot = lds + wave * 32 * D;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int b = 0; b < DB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            ot[qc * D + ((32 * b + 8 * (r >> 2) + 4 * h + (r & 3)) ^ qc)] = o[b][r] * inv;
+    __syncthreads();
+    for (int i = lane; i < 32 * D; i += 64) {
+        const uint32_t row = i / D, col = i % D;
+        const uint32_t q = qw + row;
+        if (q < sq) a.O[(bh * sq + q) * D + col] = ot[row * D + (col ^ row)];
+    }
+}
+
 // Merge split partials: O = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
 __global__ __launch_bounds__(kThreads) void attn_merge(Attn a, uint32_t splits, uint64_t rows,
                                                        const float *ws_acc, const float *ws_ml)
@@ -408,8 +591,19 @@ bool use_decode(const Attn &a)
     return a.seq_q <= 4 && (a.head_dim % 32) == 0 && a.head_dim <= 256;
 }
 
+bool use_prefill(const Attn &a)
+{
+    return !use_decode(a) && (a.head_dim == 64 || a.head_dim == 128);
+}
+
 void plan(const Attn &a, uint32_t &qblocks, uint32_t &splits, uint32_t &kps)
 {
+    if (use_prefill(a)) {
+        qblocks = (a.seq_q + PQ - 1) / PQ;
+        splits = 1;
+        kps = a.seq_k;
+        return;
+    }
     if (use_decode(a)) {
         // One workgroup per (batch, head) and key range: enough ranges for
         // ~2048 workgroups, each at least 256 keys (8 per stream).
@@ -451,6 +645,13 @@ void attention(hipStream_t s, const Attn &a, float *ws)
     float *ws_acc = ws;
     float *ws_ml = ws ? ws + static_cast<uint64_t>(splits) * rows * D : nullptr;
     dim3 grid(qb, a.batch * a.heads, splits);
+    if (use_prefill(a)) {
+        if (D == 128)
+            attn_prefill_kernel<128><<<grid, kThreads, 0, s>>>(a);
+        else
+            attn_prefill_kernel<64><<<grid, kThreads, 0, s>>>(a);
+        return;
+    }
     if (use_decode(a)) {
         const int qn = a.seq_q == 1 ? 1 : a.seq_q == 2 ? 2 : 4;
         const int v4 = static_cast<int>(D / 32);

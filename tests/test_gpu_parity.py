@@ -242,6 +242,9 @@ def test_rope_positions_and_identity(gpu):
     # decode kernel (seq_q <= 4, head_dim % 32 == 0): query counts, widths, masks
     (2, 3, 1, 777, 64, 1, True), (1, 2, 3, 300, 96, 1, False), (1, 2, 4, 1000, 256, 1, True),
     (2, 2, 2, 64, 32, 0, False), (1, 1, 4, 3, 160, 1, False), (3, 1, 1, 1, 128, 1, False),
+    # prefill kernel (f32 MFMA, head_dim 64/128): ragged lengths, masks, offsets
+    (2, 3, 129, 200, 64, 0, True), (1, 2, 256, 256, 128, 1, True), (1, 2, 100, 1000, 128, 1, False),
+    (1, 1, 5, 5, 128, 1, False), (1, 2, 300, 120, 64, 1, False), (1, 1, 640, 640, 128, 1, False),
     (1, 1, 17, 9, 64, 1, False), (1, 2, 40, 40, 80, 0, False)])
 def test_attention(gpu, b, h, sq, sk, d, causal, use_mask):
     Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
