@@ -428,8 +428,9 @@ void exec_quantize(vnpu_device_t *, vnpu_stream_t *s, const vnpu_quantize_i8_arg
     if (a.axis == VNPU_QUANT_PER_ROW) {
         k::quantize_rows(s->hip, X, Y, sc, a.rows, a.cols);
     } else if (a.axis == VNPU_QUANT_PER_COLUMN) {
-        require(a.cols <= 0xffffffffull * 64ull, "quantize column count too large");
-        k::quantize_cols(s->hip, X, Y, sc, a.rows, a.cols);
+        require(a.cols <= 0xffffffffull * 256ull, "quantize column count too large");
+        uint32_t *ws = static_cast<uint32_t *>(s->ensure_workspace(k::quantize_cols_ws_bytes(a.cols)));
+        k::quantize_cols(s->hip, X, Y, sc, a.rows, a.cols, ws);
     } else {
         float *ws = static_cast<float *>(s->ensure_workspace(k::quantize_tensor_ws_bytes()));
         k::quantize_tensor(s->hip, X, Y, sc, total, ws);

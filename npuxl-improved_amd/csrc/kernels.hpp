@@ -14,8 +14,10 @@ namespace k {
 // ---- QUANTIZE_I8 (quantize.hip) ----
 void quantize_rows(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t rows,
                    uint64_t cols);
+// ws must hold quantize_cols_ws_bytes(cols) bytes (per-column maxima).
+size_t quantize_cols_ws_bytes(uint64_t cols);
 void quantize_cols(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t rows,
-                   uint64_t cols);
+                   uint64_t cols, uint32_t *ws);
 // ws must hold quantize_tensor_ws_bytes() bytes.
 size_t quantize_tensor_ws_bytes();
 void quantize_tensor(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t count,
@@ -44,7 +46,7 @@ struct I8Gemm {
     uint32_t epilogue = 0;
 };
 void gemv_i8(hipStream_t s, const I8Gemm &p);  // M <= 8, no MFMA
-void gemm_i8(hipStream_t s, const I8Gemm &p);  // any M, v_mfma_i32_16x16x64_i8
+void gemm_i8(hipStream_t s, const I8Gemm &p);  // any M, int8 MFMA
 
 // ---- MATMUL_F32 (gemm_f32.hip) ----
 struct F32Gemm {

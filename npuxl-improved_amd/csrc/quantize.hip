@@ -13,6 +13,8 @@
 #include "kernels.hpp"
 #include "device_math.hpp"
 
+#include <algorithm>
+
 namespace vnpu {
 namespace k {
 namespace {
@@ -94,31 +96,52 @@ __global__ __launch_bounds__(kThreads) void quant_rows_any(const float *__restri
     for (uint64_t j = threadIdx.x; j < cols; j += kThreads) Y[r * cols + j] = q8(row[j], inv);
 }
 
-// 64 columns x 4 row groups per workgroup: per-column max, then quantize.
-__global__ __launch_bounds__(kThreads) void quant_cols(const float *__restrict__ X,
-                                                       int8_t *__restrict__ Y,
-                                                       float *__restrict__ scales,
-                                                       uint64_t rows, uint64_t cols)
+// Per-column quantization in two bandwidth-shaped passes over a grid of
+// (256-column chunk) x (row range): every thread owns one column, so each
+// row of a chunk is one coalesced 1 KiB read.
+//   1. partial maxima of |x| (fmaxf ignores NaN, as the reference's max does)
+//      folded into colmax[] with an integer atomicMax on the float's bits,
+//      which orders non-negative floats exactly - the result does not depend
+//      on the order the row ranges arrive in;
+//   2. scale = max/127 (0 or non-finite -> 1), q = round(x * (1/scale)).
+__global__ __launch_bounds__(kThreads) void quant_cols_max(const float *__restrict__ X,
+                                                           uint64_t rows, uint64_t cols,
+                                                           uint64_t rows_per,
+                                                           uint32_t *__restrict__ colmax)
 {
-    __shared__ float red[4][64];
-    __shared__ float inv_s[64];
-    const uint32_t cl = threadIdx.x & 63, rg = threadIdx.x >> 6;
-    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * 64 + cl;
-    float m = 0.0f;
-    if (c < cols)
-        for (uint64_t r = rg; r < rows; r += 4) m = fmaxf(m, fabsf(X[r * cols + c]));
-    red[rg][cl] = m;
-    __syncthreads();
-    if (rg == 0) {
-        const float mx = fmaxf(fmaxf(red[0][cl], red[1][cl]), fmaxf(red[2][cl], red[3][cl]));
-        const float scale = scale_from_max(mx);
-        inv_s[cl] = __fdiv_rn(1.0f, scale);
-        if (c < cols) scales[c] = scale;
+    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (c >= cols) return;
+    const uint64_t r0 = static_cast<uint64_t>(blockIdx.y) * rows_per;
+    const uint64_t r1 = min(rows, r0 + rows_per);
+    float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
+    uint64_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+        m0 = fmaxf(m0, fabsf(X[(r + 0) * cols + c]));
+        m1 = fmaxf(m1, fabsf(X[(r + 1) * cols + c]));
+        m2 = fmaxf(m2, fabsf(X[(r + 2) * cols + c]));
+        m3 = fmaxf(m3, fabsf(X[(r + 3) * cols + c]));
     }
-    __syncthreads();
-    const float inv = inv_s[cl];
-    if (c < cols)
-        for (uint64_t r = rg; r < rows; r += 4) Y[r * cols + c] = q8(X[r * cols + c], inv);
+    for (; r < r1; ++r) m0 = fmaxf(m0, fabsf(X[r * cols + c]));
+    const float m = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+    atomicMax(colmax + c, __float_as_uint(m));
+}
+
+__global__ __launch_bounds__(kThreads) void quant_cols_apply(const float *__restrict__ X,
+                                                             int8_t *__restrict__ Y,
+                                                             float *__restrict__ scales,
+                                                             uint64_t rows, uint64_t cols,
+                                                             uint64_t rows_per,
+                                                             const uint32_t *__restrict__ colmax)
+{
+    const uint64_t c = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (c >= cols) return;
+    const float scale = scale_from_max(__uint_as_float(colmax[c]));
+    const float inv = __fdiv_rn(1.0f, scale);
+    if (blockIdx.y == 0) scales[c] = scale;
+    const uint64_t r0 = static_cast<uint64_t>(blockIdx.y) * rows_per;
+    const uint64_t r1 = min(rows, r0 + rows_per);
+#pragma unroll 4
+    for (uint64_t r = r0; r < r1; ++r) Y[r * cols + c] = q8(X[r * cols + c], inv);
 }
 
 constexpr int kTensorBlocks = 1024;
@@ -182,11 +205,21 @@ void quantize_rows(hipStream_t s, const float *X, int8_t *Y, float *scales, uint
     }
 }
 
+size_t quantize_cols_ws_bytes(uint64_t cols) { return static_cast<size_t>(cols) * sizeof(uint32_t); }
+
 void quantize_cols(hipStream_t s, const float *X, int8_t *Y, float *scales, uint64_t rows,
-                   uint64_t cols)
+                   uint64_t cols, uint32_t *ws)
 {
-    const uint64_t blocks = (cols + 63) / 64;
-    quant_cols<<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(X, Y, scales, rows, cols);
+    // ~2048 workgroups, at least 16 rows each.
+    const uint64_t chunks = (cols + kThreads - 1) / kThreads;
+    const uint64_t max_splits = (rows + 15) / 16;
+    const uint64_t splits = std::max<uint64_t>(1, std::min<uint64_t>(max_splits, (2048 + chunks - 1) / chunks));
+    const uint64_t rows_per = (rows + splits - 1) / splits;
+    const uint64_t ysplits = (rows + rows_per - 1) / rows_per;
+    fill_u8(s, ws, 0, quantize_cols_ws_bytes(cols));   // a kernel, not a memset
+    const dim3 grid(static_cast<uint32_t>(chunks), static_cast<uint32_t>(ysplits));
+    quant_cols_max<<<grid, kThreads, 0, s>>>(X, rows, cols, rows_per, ws);
+    quant_cols_apply<<<grid, kThreads, 0, s>>>(X, Y, scales, rows, cols, rows_per, ws);
 }
 
 size_t quantize_tensor_ws_bytes() { return kTensorBlocks * sizeof(float); }

@@ -25,7 +25,7 @@ def rel(a, b):
 
 # ---------------------------------------------------------------- quantize
 @pytest.mark.parametrize("shape", [(1, 1), (3, 7), (17, 300), (64, 512), (5, 4099), (2, 4096),
-                                   (8, 11008), (3, 20000)])
+                                   (8, 11008), (3, 20000), (4096, 1000), (3000, 257), (33, 70000)])
 @pytest.mark.parametrize("axis", [0, 1, 2])
 def test_quantize_bit_exact(gpu, shape, axis):
     X = RNG.standard_normal(shape).astype(np.float32) * 3
