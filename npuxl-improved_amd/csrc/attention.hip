@@ -358,180 +358,205 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
 // ---------------------------------------------------------------------------
 // Prefill kernel on the f32 matrix cores (head_dim 64 or 128, seq_q > 4).
 //
-// A workgroup of 4 waves owns 128 queries of one (batch, head); wave w owns
-// queries q0 + 32w .. +31.  Keys stream through LDS in blocks of 32 (K
-// transposed to [d][key], V as [key][d], double buffered, the next block
-// prefetched into registers while the current one is multiplied).  Per key
-// block each wave runs v_mfma_f32_32x32x2_f32:
-//   S^T (32 keys x 32 queries) = K . Q^T   (D/2 MFMAs; Q^T stays in VGPRs)
-//   O^T (D x 32 queries)     += V^T . P^T  (D/2 MFMAs)
-// In the accumulator layout lane l holds query l%32 and keys 8j + 4(l/32) + q
-// (register 4j + q), so a query's block max and sum need one cross-lane step
-// (lane l ^ 32), and the P^T operand of PV step s is the lane's own score
-// register s once the key order of that product is chosen as
-// key(s, h) = 8(s/4) + 4h + s%4 (h = l/32).  Online softmax as in the
-// reference (a query whose block is fully masked skips the block), with the
-// reference's fast_expf.  O leaves through LDS for coalesced rows.
+// A workgroup of 8 waves owns 128 queries of one (batch, head); wave w owns
+// queries q0 + 16w .. +15 (two waves per SIMD).  Keys stream through LDS in
+// blocks of 32, double buffered and filled by 16-byte DMA of whole rows: V as
+// [key][d], K as [key][d] with 16-byte chunk c of key k at slot c ^ k (mod the
+// chunks per row).  Per block each wave runs v_mfma_f32_16x16x4_f32:
+//   S^T (16 keys x 16 queries, two tiles) = K . Q^T   (Q^T in VGPRs)
+//   O^T (D x 16 queries)                += V^T . P^T
+// Index maps chosen so every lane's operands are contiguous (one
+// ds_read_b128 feeds four MFMAs):
+//   * QK step st of lane group g = l/16 sums d = (D/4)g + st, so a lane reads
+//     its key's K row in 16-byte chunks (the swizzle keeps the 16 keys of a
+//     quarter wave in distinct banks) and holds Q[q][(D/4)g .. +D/4];
+//   * O^T tile dt, row i stands for d = 64(dt/4) + 4i + dt%4, so one chunk of
+//     a V row feeds four tiles;
+//   * the accumulator layout puts query l%16 and keys 4g + q of a tile in
+//     lane l, so a query's block max and sum combine four lanes (l^16, l^32),
+//     and the P^T operand of PV step s of tile t is the lane's own score
+//     register s when that product's key order is 16t + 4g + s.
+// Online softmax as in the reference (a query whose block is fully masked
+// skips the block), with the reference's fast_expf.  Keys past the range are
+// clamped to a valid row and masked in the scores.  O leaves through LDS so
+// every global row write is coalesced.
 // ---------------------------------------------------------------------------
-typedef float v16f __attribute__((ext_vector_type(16)));
-constexpr int PQ = 128;   // queries per workgroup
-constexpr int PK = 32;    // keys per block
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int PQ = 128;          // queries per workgroup
+constexpr int PK = 32;           // keys per block
+constexpr int PThreads = 512;    // 8 waves
+
+__device__ __forceinline__ void lds_dma16(const void *src, float *lds_dst)
+{
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds_dst), 16, 0, 0);
+}
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_prefill_kernel(Attn a)
+struct PrefillLds {
+    static constexpr int kK = PK * D;            // floats
+    static constexpr int kBuf = 2 * PK * D;      // K + V
+    static constexpr size_t kBytes = static_cast<size_t>(2 * kBuf) * 4;
+    static_assert(8 * 16 * D <= 2 * kBuf, "output staging fits in the key buffers");
+};
+
+template <int D>
+__global__ __launch_bounds__(PThreads) void attn_prefill_kernel(Attn a)
 {
-    constexpr int D4 = D / 4;
-    constexpr int NS = D / 2;          // QK MFMA steps (2 d per step)
-    constexpr int DB = D / 32;         // 32-wide d blocks of O^T
-    constexpr int KV4 = PK * D4 / kThreads;   // float4 of K (and of V) per thread per block
-    // [2 buffers][D][PK] transposed K, then [2 buffers][PK][D] V; reused for
-    // the output staging (4 waves x 32 x D) after the key loop.
-    __shared__ float lds[4 * PK * D];
-    auto Kt = [&](int buf, int d, int key) -> float & { return lds[(buf * D + d) * PK + key]; };
-    auto Vs = [&](int buf, int key, int d) -> float & { return lds[2 * PK * D + (buf * PK + key) * D + d]; };
+    using L = PrefillLds<D>;
+    constexpr int NS = D / 4;          // QK MFMA steps per tile (4 d each)
+    constexpr int NCH = D / 4;         // 16-byte chunks per row
+    constexpr int DT = D / 16;         // 16-wide d tiles of O^T
+    constexpr int HI = DT / 4;         // V chunks read per key
+    extern __shared__ __attribute__((aligned(16))) float lds[];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane >> 5, qc = lane & 31;
+    const int g = lane >> 4, qc = lane & 15;
     const uint64_t bh = blockIdx.y;
     const uint32_t nqb = gridDim.x;
     const uint32_t q0 = (nqb - 1 - blockIdx.x) * PQ;        // heaviest causal blocks first
     const uint32_t sq = a.seq_q, sk = a.seq_k;
     const uint32_t off = sk > sq ? sk - sq : 0;
-    const float *Qh = a.Q + bh * sq * D;
     const float *Kh = a.K + bh * sk * D;
     const float *Vh = a.V + bh * sk * D;
     const float *Mh = a.mask ? a.mask + bh * sq * sk : nullptr;
-
-    const uint32_t qw = q0 + wave * 32;                     // this wave's first query
+    const uint32_t qw = q0 + wave * 16;                      // this wave's first query
     const uint32_t myq = qw + qc;                            // this lane's query
-    // Q^T operand: step s = 2t + e uses d = 4t + 2h + e.
-    float qf[NS];
-    {
-        const float *qrow = Qh + static_cast<uint64_t>(min(myq, sq - 1)) * D;
-#pragma unroll
-        for (int t = 0; t < NS / 2; ++t) {
-            const float2 v = *reinterpret_cast<const float2 *>(qrow + 4 * t + 2 * h);
-            qf[2 * t] = v.x;
-            qf[2 * t + 1] = v.y;
-        }
-    }
 
-    // Keys this workgroup needs (causal: up to its last query's limit).
     uint32_t kend = sk;
     if (a.causal) kend = min(sk, min(q0 + PQ, sq) - 1 + off + 1);
     const uint32_t nblk = (kend + PK - 1) / PK;
-    // This wave's causal limit: its blocks past it contribute nothing.
-    const uint32_t wave_kend = a.causal ? min(kend, min(qw + 32, sq) - 1 + off + 1) : kend;
+    const uint32_t wave_kend = a.causal ? min(kend, min(qw + 16, sq) - 1 + off + 1) : kend;
 
-    // Block loads: K as (key = t % 32, float4 d4 = t / 32 + 8i) so that the
-    // transposed LDS writes of a half wave hit consecutive keys; V row-major.
-    float4 kr[KV4], vr[KV4];
-    auto load_blk = [&](uint32_t kb) {
+    // Q^T operand: lane (query qc, group g) holds Q[myq][NS*g .. NS*g + NS).
+    float qf[NS];
+    {
+        const float4 *qrow = reinterpret_cast<const float4 *>(a.Q + (bh * sq + min(myq, sq - 1)) * D + NS * g);
 #pragma unroll
-        for (int i = 0; i < KV4; ++i) {
-            const uint32_t key = kb * PK + (tid & 31);
-            const uint32_t d4 = (tid >> 5) + 8 * i;
-            kr[i] = key < kend ? reinterpret_cast<const float4 *>(Kh + static_cast<uint64_t>(key) * D)[d4]
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-            const uint32_t vi = tid + kThreads * i;          // float4 index in the [32][D] block
-            const uint32_t vkey = kb * PK + vi / D4;
-            vr[i] = vkey < kend ? reinterpret_cast<const float4 *>(Vh + static_cast<uint64_t>(vkey) * D)[vi % D4]
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int u = 0; u < NS / 4; ++u) {
+            const float4 v = qrow[u];
+            qf[4 * u] = v.x;
+            qf[4 * u + 1] = v.y;
+            qf[4 * u + 2] = v.z;
+            qf[4 * u + 3] = v.w;
+        }
+    }
+
+    // DMA of key block kb into buffer buf: K and V, 16-byte chunks, 64 per
+    // instruction, PK*NCH/64 instructions each, spread over the 8 waves.
+    auto issue = [&](uint32_t kb, int buf) {
+        float *ks = lds + buf * L::kBuf;
+        float *vs = ks + L::kK;
+        constexpr int kInstr = PK * NCH / 64;
+#pragma unroll
+        for (int i = 0; i < kInstr / 8; ++i) {
+            const int ins = wave * (kInstr / 8) + i;
+            const uint32_t f = ins * 64 + lane;              // chunk slot in the block
+            const uint32_t k = f / NCH, slot = f % NCH;
+            const uint32_t key = min(kb * PK + k, kend - 1);
+            const uint32_t c = slot ^ (k & (NCH - 1));       // K chunk stored in this slot
+            lds_dma16(Kh + static_cast<uint64_t>(key) * D + 4 * c, ks + ins * 256);
+            lds_dma16(Vh + static_cast<uint64_t>(key) * D + 4 * slot, vs + ins * 256);
         }
     };
-    auto store_blk = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < KV4; ++i) {
-            const uint32_t key = tid & 31;
-            const uint32_t d = 4 * ((tid >> 5) + 8 * i);
-            Kt(buf, d + 0, key) = kr[i].x;
-            Kt(buf, d + 1, key) = kr[i].y;
-            Kt(buf, d + 2, key) = kr[i].z;
-            Kt(buf, d + 3, key) = kr[i].w;
-            reinterpret_cast<float4 *>(&Vs(buf, 0, 0))[tid + kThreads * i] = vr[i];
-        }
-    };
+    if (nblk) issue(0, 0);
 
-    v16f o[DB];
+    v4f o[DT];
 #pragma unroll
-    for (int b = 0; b < DB; ++b) o[b] = (v16f){0.f};
+    for (int t = 0; t < DT; ++t) o[t] = (v4f){0.f, 0.f, 0.f, 0.f};
     float m = -__builtin_inff(), l = 0.0f;
 
-    if (nblk) {
-        load_blk(0);
-        store_blk(0);
-    }
     for (uint32_t kb = 0; kb < nblk; ++kb) {
         const int buf = kb & 1;
-        if (kb + 1 < nblk) load_blk(kb + 1);
-        __syncthreads();   // block kb visible; block kb-1's buffer free for kb+1
-        if (kb * PK < wave_kend) {   // wave-uniform
-            // S^T = K . Q^T
-            v16f s = (v16f){0.f};
+        __builtin_amdgcn_s_waitcnt(0xF70);   // vmcnt(0): this wave's DMA of block kb
+        __syncthreads();                     // block kb landed everywhere; block kb-1's buffer free
+        if (kb + 1 < nblk) issue(kb + 1, buf ^ 1);
+        if (kb * PK >= wave_kend) continue;  // wave-uniform: past this wave's causal limit
+        const float *ks = lds + buf * L::kBuf;
+        const float *vs = ks + L::kK;
+
+        // S^T tiles (keys 16t + row) = K . Q^T
+        v4f sc[2];
 #pragma unroll
-            for (int st = 0; st < NS; ++st) {
-                const int d = 4 * (st >> 1) + 2 * h + (st & 1);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(Kt(buf, d, qc), qf[st], s, 0, 0, 0);
-            }
-            // scores of query myq for keys kb*32 + 8j + 4h + q (register 4j+q)
-            float bmax = -__builtin_inff();
+        for (int t = 0; t < 2; ++t) {
+            const int kk = 16 * t + qc;
+            const float *krow = ks + kk * D;
+            sc[t] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t key = kb * PK + 8 * (r >> 2) + 4 * h + (r & 3);
-                float v = s[r] * a.scale;
-                if (Mh && key < sk && myq < sq) v += Mh[static_cast<uint64_t>(myq) * sk + key];
-                if (key >= kend || myq >= sq || (a.causal && key > myq + off)) v = -__builtin_inff();
-                s[r] = v;
-                bmax = fmaxf(bmax, v);
-            }
-            bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-            float alpha = 1.0f, psum = 0.0f;
-            if (bmax != -__builtin_inff()) {
-                const float mn = fmaxf(m, bmax);
-                alpha = (m == -__builtin_inff()) ? 0.0f : dev::fast_expf(m - mn);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float p = (s[r] == -__builtin_inff()) ? 0.0f : dev::fast_expf(s[r] - mn);
-                    s[r] = p;
-                    psum += p;
-                }
-                m = mn;
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) s[r] = 0.0f;
-            }
-            psum += __shfl_xor(psum, 32, 64);
-            l = l * alpha + psum;
-#pragma unroll
-            for (int b = 0; b < DB; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
-            // O^T += V^T . P^T, key order key(st, h) = 8(st/4) + 4h + st%4
-#pragma unroll
-            for (int st = 0; st < 16; ++st) {
-                const int key = 8 * (st >> 2) + 4 * h + (st & 3);
-#pragma unroll
-                for (int b = 0; b < DB; ++b)
-                    o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs(buf, key, 32 * b + qc), s[st], o[b], 0, 0, 0);
+            for (int u = 0; u < NS / 4; ++u) {
+                const int c = (NS / 4) * g + u;
+                const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * (c ^ (kk & (NCH - 1))));
+                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qf[4 * u + 0], sc[t], 0, 0, 0);
+                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qf[4 * u + 1], sc[t], 0, 0, 0);
+                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qf[4 * u + 2], sc[t], 0, 0, 0);
+                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qf[4 * u + 3], sc[t], 0, 0, 0);
             }
         }
-        if (kb + 1 < nblk) store_blk(buf ^ 1);
+        // Scores of query myq for keys kb*32 + 16t + 4g + q.
+        float bmax = -__builtin_inff();
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t key = kb * PK + 16 * t + 4 * g + r;
+                float v = sc[t][r] * a.scale;
+                if (Mh) v += Mh[static_cast<uint64_t>(min(myq, sq - 1)) * sk + min(key, sk - 1)];
+                const bool dead = key >= kend || myq >= sq || (a.causal && key > myq + off);
+                v = dead ? -__builtin_inff() : v;
+                sc[t][r] = v;
+                bmax = fmaxf(bmax, v);
+            }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        const bool live = bmax != -__builtin_inff();      // else the block is skipped for this query
+        const float mn = live ? fmaxf(m, bmax) : m;
+        const float alpha = (!live || m == -__builtin_inff()) ? (live ? 0.0f : 1.0f) : dev::fast_expf(m - mn);
+        float psum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = (sc[t][r] == -__builtin_inff()) ? 0.0f : dev::fast_expf(sc[t][r] - mn);
+                sc[t][r] = p;
+                psum += p;
+            }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        m = mn;
+        l = l * alpha + psum;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) o[t] *= alpha;
+        // O^T += V^T . P^T, key 16t + 4g + st: P^T is the lane's register st;
+        // tile dt row qc is d = 64(dt/4) + 4qc + dt%4.
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const float *vrow = vs + (16 * t + 4 * g + st) * D + 4 * qc;
+#pragma unroll
+                for (int hi = 0; hi < HI; ++hi) {
+                    const float4 vv = *reinterpret_cast<const float4 *>(vrow + 64 * hi);
+                    o[4 * hi + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sc[t][st], o[4 * hi + 0], 0, 0, 0);
+                    o[4 * hi + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sc[t][st], o[4 * hi + 1], 0, 0, 0);
+                    o[4 * hi + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sc[t][st], o[4 * hi + 2], 0, 0, 0);
+                    o[4 * hi + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sc[t][st], o[4 * hi + 3], 0, 0, 0);
+                }
+            }
     }
 
-    // O = O^T / l through LDS: this wave's 32 x D tile (reuses the K/V
-    // buffers), column c of row r stored at c ^ r so that the 32 rows of a
-    // register's write land in distinct banks.
+    // O = O^T / l through LDS (the key buffers): this wave's 16 x D tile; the
+    // lane holds query qc, d = 64(dt/4) + 16g + 4r + dt%4 (register r of tile
+    // dt); column c of row q stored at c ^ q (distinct banks per register).
     __syncthreads();
-    float *ot = lds + wave * 32 * D;
+    float *ot = lds + wave * 16 * D;
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-    for (int b = 0; b < DB; ++b)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            ot[qc * D + ((32 * b + 8 * (r >> 2) + 4 * h + (r & 3)) ^ qc)] = o[b][r] * inv;
+        for (int r = 0; r < 4; ++r)
+            ot[qc * D + ((64 * (dt >> 2) + 16 * g + 4 * r + (dt & 3)) ^ qc)] = o[dt][r] * inv;
     __syncthreads();
-    for (int i = lane; i < 32 * D; i += 64) {
+    for (int i = lane; i < 16 * D; i += 64) {
         const uint32_t row = i / D, col = i % D;
         const uint32_t q = qw + row;
         if (q < sq) a.O[(bh * sq + q) * D + col] = ot[row * D + (col ^ row)];
@@ -647,9 +672,9 @@ void attention(hipStream_t s, const Attn &a, float *ws)
     dim3 grid(qb, a.batch * a.heads, splits);
     if (use_prefill(a)) {
         if (D == 128)
-            attn_prefill_kernel<128><<<grid, kThreads, 0, s>>>(a);
+            attn_prefill_kernel<128><<<grid, PThreads, PrefillLds<128>::kBytes, s>>>(a);
         else
-            attn_prefill_kernel<64><<<grid, kThreads, 0, s>>>(a);
+            attn_prefill_kernel<64><<<grid, PThreads, PrefillLds<64>::kBytes, s>>>(a);
         return;
     }
     if (use_decode(a)) {
