@@ -14,7 +14,10 @@ vnpu stream's own hipStream_t (GPU time / launches -> the average kernel
 duration behind `roofline.achieved`).
 
 Also printed (same line, key "extras"): the rest of config 2 (M in {1,4,8} x
-N in {4096,11008,32000}) and the config-3 int8 prefill GEMM.  The CPU
+N in {4096,11008,32000}), config 1 (512^3 int8 and f32+SiLU), config 3 (int8
+and f32 prefill GEMMs), config 4 (one Llama-style layer: prefill tokens/s at
+batch 1 x 2048 and decode tokens/s at batch 8, context 4096) and config 5
+(int8 GEMM over half-zero weight tiles, MTP head + softmax).  The CPU
 baseline is the reference runtime built from its own sources, timed on this
 host's cores on a bounded sample of the same GEMV.
 """
@@ -38,6 +41,12 @@ HBM_PEAK_GBS = 8000.0
 I8_PEAK_TOPS = 5000.0
 F32_PEAK_TFLOPS = 157.3
 ROTATE_BYTES = 800 << 20
+# HBM bytes per headline GEMV launch from two rocprofv3 PMC passes (FETCH_SIZE,
+# WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for a
+# copy kernel of known size (FETCH x2.000, WRITE x1.000):
+# 64,169.1 KiB x 2 + 125 KiB.  Measured offline with the commands in
+# profiles/gemv_i8_m1_k4096_n32000_traffic.md; re-measure when the kernel changes.
+GEMV_TRAFFIC_BYTES = 131_546_317
 
 
 def log(*a):
@@ -360,8 +369,8 @@ def main():
                     default=None, help="run one extra workload alone (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this backend benchmarks one GPU only; multi-GPU sharding is "
-                                   "design-only (see DESIGN.md)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build benchmarks one GPU only: how the path shards across "
+                                   "GPUs is a design, not a measured run", "n_gpus": args.gpus}))
         sys.exit(2)
 
     M, K, N = 1, 4096, 32000
@@ -444,7 +453,7 @@ def main():
                                f"{head['copies']} HBM copies", "M": M, "K": K, "N": N},
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "gemv_i8_kernel", "kernel_us": round(head["kernel_us"], 3),
+                     "traffic": GEMV_TRAFFIC_BYTES, "kernel": "gemv_i8_kernel", "kernel_us": round(head["kernel_us"], 3),
                      "algorithmic_bytes": b},
         "cpu_baseline": cpu,
         "extras": extras,
