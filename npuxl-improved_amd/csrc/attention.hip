@@ -386,9 +386,20 @@ constexpr int PQ = 128;          // queries per workgroup
 constexpr int PK = 32;           // keys per block
 constexpr int PThreads = 512;    // 8 waves
 
+// 16-byte-per-lane global->LDS copy (lane l writes lds_dst + 16 l bytes).
+// Written as asm on purpose: for the builtin form the compiler cannot tell the
+// in-flight copy of the next key block from the buffer being read, and waits
+// vmcnt(0) before the first ds_read of every block, which serialises the copy
+// with the compute.  The kernel's own vmcnt(0) + barrier at the top of each
+// key block is what orders the copy before its readers.
 __device__ __forceinline__ void lds_dma16(const void *src, float *lds_dst)
 {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds_dst), 16, 0, 0);
+    const uint32_t lds = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) float *)(lds_dst)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory", "m0");
 }
 
 template <int D>

@@ -471,7 +471,9 @@ void exec_softmax(vnpu_stream_t *s, const vnpu_softmax_f32_args_t &a, ExecStats 
     const float *X = sg.in(a.X, n * 4);
     float *Y = (a.Y == a.X) ? sg.inout(a.Y, n * 4) : sg.out(a.Y, n * 4);
     if (a.Y == a.X && !is_device_pointer(a.X)) X = Y;
-    k::softmax(s->hip, X, Y, a.rows, a.cols, inv_t);
+    const size_t ws_bytes = k::softmax_ws_bytes(a.rows, a.cols);
+    float *ws = ws_bytes ? static_cast<float *>(s->ensure_workspace(ws_bytes)) : nullptr;
+    k::softmax(s->hip, X, Y, a.rows, a.cols, inv_t, ws);
     VNPU_HIP(hipGetLastError());
     sg.finish();
     st.bytes_read += n * 4;

@@ -31,6 +31,7 @@ namespace k {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int kThreads = 256;
@@ -218,9 +219,21 @@ __device__ __forceinline__ void block_barrier()
     asm volatile("s_barrier" ::: "memory");
 }
 
+// 16-byte-per-lane global->LDS copy (lane l writes lds_dst + 16 l).  Written
+// as asm on purpose: the compiler books the builtin form as an LDS-counter
+// event that may complete out of order, and then waits lgkmcnt(0) before
+// every MFMA that uses earlier ds_reads, which serialises each half stage
+// behind the next one's fragment reads.  Every consumer of DMA'd data waits
+// for it explicitly (vmcnt + barrier); the compiler's own vmcnt waits for its
+// own loads only get more conservative by not seeing these.
 __device__ __forceinline__ void dma16(const void *src, int8_t *lds_dst)
 {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds_dst), 16, 0, 0);
+    const uint32_t lds = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(lds_dst)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory", "m0");
 }
 
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -265,7 +278,8 @@ __device__ void store_tile(const I8Gemm &p, const int32_t *tile, const float *sa
         }
         float *dst = p.C + static_cast<uint64_t>(m0 + r) * p.ldc + n;
         if (vec) {
-            *reinterpret_cast<float4 *>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+            // Streaming store: C is written once and not re-read by this kernel.
+            __builtin_nontemporal_store((v4f){o[0], o[1], o[2], o[3]}, reinterpret_cast<v4f *>(dst));
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -518,14 +532,18 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_k128(I8Gemm p, uint32_t tile
         src[kAPerWave + j] = p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + lane * 16;
         stride[kAPerWave + j] = 2048;
     }
-    auto issue = [&](uint32_t s) {
+    // DMA instruction k (0..11) of stage s.
+    auto issue_one = [&](uint32_t s, int k) {
         int8_t *st = smem + (s % kStages) * kStageBytes;
+        if (k < kAPerWave)
+            dma16(src[k] + s * stride[k], st + (wave * kAPerWave + k) * 1024);
+        else
+            dma16(src[k] + static_cast<uint64_t>(s) * stride[k],
+                  st + kBOff + (wave * (kLoads - kAPerWave) + (k - kAPerWave)) * 1024);
+    };
+    auto issue = [&](uint32_t s) {
 #pragma unroll
-        for (int j = 0; j < kAPerWave; ++j) dma16(src[j] + s * stride[j], st + (wave * kAPerWave + j) * 1024);
-#pragma unroll
-        for (int j = 0; j < kLoads - kAPerWave; ++j)
-            dma16(src[kAPerWave + j] + static_cast<uint64_t>(s) * stride[kAPerWave + j],
-                  st + kBOff + (wave * (kLoads - kAPerWave) + j) * 1024);
+        for (int k = 0; k < kLoads; ++k) issue_one(s, k);
     };
 
     // Fragment read offsets (bytes within a stage) for half hh of the stage.
@@ -540,19 +558,25 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_k128(I8Gemm p, uint32_t tile
         a_row_off[mb] = r * 128;
         a_sw[mb] = (r >> 1) & 7;
     }
-    auto read_frags = [&](uint32_t s, int hh, Frags &f) {
+    // Fragment read k (0..11) of half hh of stage s, in the order the MFMAs
+    // consume them: per 32-deep h, b[h][0], a[h][0..3], b[h][1].
+    auto read_one = [&](uint32_t s, int hh, Frags &f, int k) {
         const int8_t *st = smem + (s % kStages) * kStageBytes;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        const int h = k / 6, r = k % 6;
+        if (r == 0 || r == 5) {
+            const int nb = r == 5;
+            const int boff = kBOff + (((wn * 4 + sub) * 2 + hh) << 10) +
+                             (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
+            f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
+        } else {
+            const int mb = r - 1;
             const uint32_t c = 4 * hh + 2 * h + (lane >> 5);
-            const int boff = kBOff + (((wn * 4 + sub) * 2 + hh) << 10) + (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
-                f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
-                f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_row_off[mb] + ((c ^ a_sw[mb]) << 4));
+            f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_row_off[mb] + ((c ^ a_sw[mb]) << 4));
         }
+    };
+    auto read_frags = [&](uint32_t s, int hh, Frags &f) {
+#pragma unroll
+        for (int k = 0; k < 12; ++k) read_one(s, hh, f, k);
     };
 
     uint8_t *zflags = reinterpret_cast<uint8_t *>(smem + kLds);
@@ -572,16 +596,25 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_k128(I8Gemm p, uint32_t tile
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = (v16i){0};
-    auto mma = [&](const Frags &f, bool skip) {
-        if (skip) return;
+    // The 16 MFMAs of one 64-deep half with side work threaded between them:
+    // side(k) runs after MFMA k, so DMA issue and fragment reads (which a
+    // wave issues in order) proceed while the matrix pipe works instead of
+    // stalling it.  A skipped (all-zero) half still does its side work.
+    auto mma = [&](const Frags &f, bool skip, auto &&side) {
+        if (kSkip && skip) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+            for (int k = 0; k < 16; ++k) side(k);
+            return;
+        }
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+        for (int k = 0; k < 16; ++k) {
+            const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+            side(k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
+    auto nothing = [](int) {};
 
     // Prologue: DMA every stage buffer, wait for stage 0, read its first half.
     const uint32_t pre = min(KS, static_cast<uint32_t>(kStages));
@@ -595,22 +628,21 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_k128(I8Gemm p, uint32_t tile
     // Steady state, one stage per trip: read the second half while the first
     // half's MFMAs issue; wait for this wave's DMA of stage s+1 (stage s+2
     // may stay in flight); barrier (stage s+1 landed everywhere, every wave
-    // holds stage s in registers); refill stage s's buffer with s+3; read
+    // holds stage s in registers); refill stage s's buffer with s+3 and read
     // stage s+1's first half while the second half's MFMAs issue.
     uint32_t s = 0;
     bool sk0 = zero_step(0), sk1 = false;
     for (; s + kStages < KS; ++s) {
-        read_frags(s, 1, f1);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, sk0);
+        mma(f0, sk0, [&](int k) { if (k < 12) read_one(s, 1, f1, k); });
         sk1 = zero_step(2 * s + 1);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<kLoads>();
         block_barrier();
-        issue(s + kStages);
-        read_frags(s + 1, 0, f0);
-        __builtin_amdgcn_sched_barrier(0);
-        mma(f1, sk1);
+        mma(f1, sk1, [&](int k) {
+            if (k < kLoads) issue_one(s + kStages, k);
+            if (k >= 4) read_one(s + 1, 0, f0, k - 4);
+        });
         sk0 = zero_step(2 * s + 2);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -618,17 +650,16 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_k128(I8Gemm p, uint32_t tile
     wait_vmcnt<0>();
     block_barrier();
     for (; s < KS; ++s) {
-        read_frags(s, 1, f1);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, sk0);
+        mma(f0, sk0, [&](int k) { if (k < 12) read_one(s, 1, f1, k); });
         sk1 = zero_step(2 * s + 1);
         __builtin_amdgcn_sched_barrier(0);
         if (s + 1 < KS) {
-            read_frags(s + 1, 0, f0);
+            mma(f1, sk1, [&](int k) { if (k >= 4) read_one(s + 1, 0, f0, k - 4); });
             sk0 = zero_step(2 * s + 2);
+        } else {
+            mma(f1, sk1, nothing);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        mma(f1, sk1);
     }
 
     __syncthreads();

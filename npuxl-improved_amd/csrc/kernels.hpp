@@ -75,7 +75,11 @@ void gemv_f32(hipStream_t s, const F32Gemm &p, float *ws);
 // ---- transformer ops (ops.hip) ----
 void rmsnorm(hipStream_t s, const float *X, const float *W, float *Y, uint32_t rows,
              uint32_t cols, float eps);
-void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t cols, float inv_t);
+// Few long rows are split over workgroups: ws holds softmax_ws_bytes(rows,
+// cols) bytes (0 when one workgroup per row is used).
+size_t softmax_ws_bytes(uint32_t rows, uint32_t cols);
+void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t cols, float inv_t,
+             float *ws);
 // inv_freq: device table [head_dim/2] (half-rotation) or [head_dim/2] for the
 // interleaved pairs, computed on the host with the reference's powf expression.
 void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t batch,

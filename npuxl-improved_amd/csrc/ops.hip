@@ -105,6 +105,71 @@ __global__ __launch_bounds__(kThreads) void softmax_kernel(const float *__restri
     for (uint32_t j = threadIdx.x; j < cols; j += kThreads) y[j] = dev::fast_expf((x[j] - mx) * inv_t) * inv;
 }
 
+// Few long rows (e.g. the MTP head's [4, 32000] logits): each row is split
+// into chunks over many workgroups, in three passes that keep the
+// reference's terms exactly: chunk maxima -> the row max M; chunk sums of
+// fast_expf((x - M) * inv_t) -> the row sum L; y = fast_expf((x - M) * inv_t)
+// * (1 / L).  ws holds rows x chunks x 2 floats.
+__device__ __forceinline__ float row_max_of(const float *part, uint32_t chunks, float *red)
+{
+    float m = -__builtin_inff();
+    for (uint32_t c = threadIdx.x; c < chunks; c += kThreads) m = fmaxf(m, part[2 * c]);
+    return block_max(m, red);
+}
+
+__device__ __forceinline__ float row_sum_of(const float *part, uint32_t chunks, float *red)
+{
+    float s = 0.0f;
+    for (uint32_t c = threadIdx.x; c < chunks; c += kThreads) s += part[2 * c + 1];
+    return block_sum(s, red);
+}
+
+__global__ __launch_bounds__(kThreads) void softmax_chunk_max(const float *__restrict__ X,
+                                                              uint32_t cols, uint32_t chunk,
+                                                              float *__restrict__ ws)
+{
+    __shared__ float red[kThreads / 64];
+    const uint64_t r = blockIdx.y;
+    const uint32_t c0 = blockIdx.x * chunk, c1 = min(cols, c0 + chunk);
+    const float *x = X + r * cols;
+    float mx = -__builtin_inff();
+    for (uint32_t j = c0 + threadIdx.x; j < c1; j += kThreads) mx = fmaxf(mx, x[j]);
+    mx = block_max(mx, red);
+    if (threadIdx.x == 0) ws[(r * gridDim.x + blockIdx.x) * 2] = mx;
+}
+
+__global__ __launch_bounds__(kThreads) void softmax_chunk_sum(const float *__restrict__ X,
+                                                              uint32_t cols, uint32_t chunk,
+                                                              float inv_t, float *__restrict__ ws)
+{
+    __shared__ float red[kThreads / 64];
+    const uint64_t r = blockIdx.y;
+    const uint32_t c0 = blockIdx.x * chunk, c1 = min(cols, c0 + chunk);
+    const float *x = X + r * cols;
+    const float mx = row_max_of(ws + r * gridDim.x * 2, gridDim.x, red);
+    float sum = 0.0f;
+    for (uint32_t j = c0 + threadIdx.x; j < c1; j += kThreads) sum += dev::fast_expf((x[j] - mx) * inv_t);
+    sum = block_sum(sum, red);
+    if (threadIdx.x == 0) ws[(r * gridDim.x + blockIdx.x) * 2 + 1] = sum;
+}
+
+__global__ __launch_bounds__(kThreads) void softmax_chunk_norm(const float *__restrict__ X,
+                                                               float *__restrict__ Y, uint32_t cols,
+                                                               uint32_t chunk, float inv_t,
+                                                               const float *__restrict__ ws)
+{
+    __shared__ float red[kThreads / 64];
+    const uint64_t r = blockIdx.y;
+    const uint32_t c0 = blockIdx.x * chunk, c1 = min(cols, c0 + chunk);
+    const float *part = ws + r * gridDim.x * 2;
+    const float mx = row_max_of(part, gridDim.x, red);
+    const float sum = row_sum_of(part, gridDim.x, red);
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    const float *x = X + r * cols;
+    float *y = Y + r * cols;
+    for (uint32_t j = c0 + threadIdx.x; j < c1; j += kThreads) y[j] = dev::fast_expf((x[j] - mx) * inv_t) * inv;
+}
+
 // reference llm.cpp:188-217, 576-602: one thread per rotated pair.
 __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ Q, float *__restrict__ K,
                                                         const int32_t *__restrict__ positions,
@@ -217,9 +282,34 @@ void rmsnorm(hipStream_t s, const float *X, const float *W, float *Y, uint32_t r
         rmsnorm_kernel<<<dim3(rows), kThreads, 0, s>>>(X, W, Y, cols, eps);
 }
 
-void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t cols, float inv_t)
+// Rows below this count leave most CUs idle with one workgroup per row.
+constexpr uint32_t kSplitRows = 512;
+constexpr uint32_t kSplitChunk = 1024;  // columns per workgroup (4 per thread)
+
+static uint32_t softmax_chunks(uint32_t rows, uint32_t cols)
 {
-    softmax_kernel<<<dim3(rows), kThreads, 0, s>>>(X, Y, cols, inv_t);
+    if (rows >= kSplitRows || cols < 2 * kSplitChunk) return 1;
+    return (cols + kSplitChunk - 1) / kSplitChunk;
+}
+
+size_t softmax_ws_bytes(uint32_t rows, uint32_t cols)
+{
+    const uint32_t chunks = softmax_chunks(rows, cols);
+    return chunks > 1 ? static_cast<size_t>(rows) * chunks * 2 * sizeof(float) : 0;
+}
+
+void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t cols, float inv_t,
+             float *ws)
+{
+    const uint32_t chunks = softmax_chunks(rows, cols);
+    if (chunks == 1) {
+        softmax_kernel<<<dim3(rows), kThreads, 0, s>>>(X, Y, cols, inv_t);
+        return;
+    }
+    const dim3 grid(chunks, rows);
+    softmax_chunk_max<<<grid, kThreads, 0, s>>>(X, cols, kSplitChunk, ws);
+    softmax_chunk_sum<<<grid, kThreads, 0, s>>>(X, cols, kSplitChunk, inv_t, ws);
+    softmax_chunk_norm<<<grid, kThreads, 0, s>>>(X, Y, cols, kSplitChunk, inv_t, ws);
 }
 
 void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t batch,

@@ -197,6 +197,29 @@ def test_rmsnorm_softmax(gpu, rows, cols):
     assert np.allclose(sm.sum(axis=1), 1.0, atol=1e-4)
 
 
+@pytest.mark.parametrize("rows,cols", [(4, 2049), (2, 300000), (511, 3000), (4, 32000)])
+def test_softmax_split_rows(gpu, rows, cols):
+    """Few long rows are split over workgroups; includes a temperature, a
+    chunk that is -inf throughout (masked logits) and a ragged last chunk.
+
+    The reference sums a row's exponentials one after another in float32;
+    over 300000 columns that sum is itself off by more than 1e-4 (relative),
+    so the bar is 1e-4 or twice the reference's own distance from the float64
+    softmax, whichever is larger, and the GPU must be within 1e-4 of float64."""
+    X = (RNG.standard_normal((rows, cols)) * 3).astype(np.float32)
+    X[0, :1500] = -np.inf
+    for t in (0.0, 0.7):
+        sm = g.unary_rows(gpu, abi.OP_SOFTMAX_F32, X, temperature=t)
+        want = oracle.softmax(X, 1.0 if t == 0.0 else t)
+        x64 = X.astype(np.float64) * (1.0 if t == 0.0 else 1.0 / t)
+        e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+        exact = e / e.sum(axis=1, keepdims=True)
+        assert rel(sm, want) <= max(1e-4, 2 * rel(want, exact))
+        assert rel(sm, exact) <= 1e-4
+        assert np.all(sm[0, :1500] == 0.0)
+        assert np.allclose(sm.sum(axis=1), 1.0, atol=1e-4)
+
+
 @pytest.mark.parametrize("n", [1, 1001, 4096 * 8 + 3, 2048 * 11008 // 64])
 def test_elementwise(gpu, n):
     a = RNG.standard_normal(n).astype(np.float32)
