@@ -5,25 +5,26 @@
 // reference's store_i8_c (kernels.cpp:526-535): exact int32 accumulation,
 // then C = epi(((float)acc * scale_a[m]) * scale_b[n] + bias[n]).
 //
-// Structure:
-//   * workgroup tile BM x BN = 128 x 128, 4 waves in a 2 x 2 grid, wave tile
-//     64 x 64 = 4 x 4 v_mfma_i32_16x16x64_i8 blocks (64 accumulator VGPRs);
-//   * k step 64 = one MFMA depth;
-//   * A (row-major int8 from QUANTIZE_I8) is staged through LDS, double
-//     buffered, rows padded to 80 bytes so each ds_read_b128 fragment read is
-//     bank-conflict free;
-//   * B needs no LDS: the packed fragment layout stores each 16 x 64 operand
-//     block as the 1 KiB a wave loads with one 16-byte load per lane;
-//   * the next k step's global loads are issued before the current step's
-//     MFMAs, one barrier per k step;
-//   * a 1 KiB weight block known to be all zero (PACK_WEIGHTS_I8's zero map)
-//     is neither loaded nor multiplied: exact, it only adds zeros.
+// Kernels, chosen by gemm_i8() at the end of the file:
+//   * gemm_i8_wide   - 256 x 256 tiles, dense weights, M % 256 == 0,
+//                      K % 128 == 0, >= 384 tiles;
+//   * gemm_i8_k128w8 - 256 x 128 tiles, 8 waves, K % 128 == 0;
+//   * gemm_i8_pipe   - 256 x 128 tiles, 64-deep stages, K % 64 == 0;
+//   * gemm_i8_generic - any shape and alignment (below).
+// All of them multiply int8 fragments read from the packed weight layout and
+// accumulate exactly in int32; a 64-deep weight block known to be all zero
+// (PACK_WEIGHTS_I8's zero map) may be skipped: exact, it only adds zeros.
 //
-// Fragment convention (both operands use the same k order, so the integer
-// result is exact whatever order the hardware sums in): lane l = 16*g + r
-// holds row/column r and k = 16*g .. 16*g + 15 of the 64-deep block.
-// Output: lane l holds C[4*(l/16) + i][l%16], i = 0..3.
+// Generic kernel: workgroup tile BM x BN = 128 x 128, 4 waves in a 2 x 2
+// grid, wave tile 64 x 64 = 4 x 4 v_mfma_i32_16x16x64_i8 blocks; A staged
+// through LDS (rows padded to 80 bytes, conflict-free ds_read_b128), B loaded
+// straight from the packed layout (one 16-byte load per lane per 1 KiB
+// operand block).  Fragment convention (both operands use the same k order,
+// so the integer result is exact whatever order the hardware sums in):
+// lane l = 16*g + r holds row/column r and k = 16*g .. 16*g + 15 of the
+// 64-deep block.  Output: lane l holds C[4*(l/16) + i][l%16], i = 0..3.
 #include "kernels.hpp"
+#include <type_traits>
 #include "device_math.hpp"
 
 namespace vnpu {
@@ -236,6 +237,18 @@ __device__ __forceinline__ void dma16(const void *src, int8_t *lds_dst)
                  : "memory", "m0");
 }
 
+// The same copy with a wave-uniform 64-bit base (SGPRs) and a 32-bit
+// per-lane byte offset: lane l reads base + voff and writes lds_dst + 16 l.
+__device__ __forceinline__ void dma16_s(const int8_t *base, uint32_t voff, int8_t *lds_dst)
+{
+    const uint32_t lds = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(lds_dst)));
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 // One stage's operands for v_mfma_i32_32x32x32_i8, per 32-deep k half h:
@@ -244,17 +257,19 @@ struct Frags {
     v4i a[2][4], b[2][2];
 };
 
-// Dequant epilogue over the row-major staged tile: each thread writes 4
-// consecutive columns per row (one 16-byte store), 8 rows per pass.  One
-// instantiation per activation keeps the loop body small.  No contraction:
+// Dequant epilogue over a row-major staged tile of kRows x kCols int32 (row
+// pitch kPitch): each thread writes 4 consecutive columns per row (one
+// 16-byte store), kT/(kCols/4) rows per pass.  One instantiation per
+// activation keeps the loop body small.  No contraction:
 // ((float)acc * sa) * sb + bias rounds each step, as the reference's
 // store_i8_c does.
-template <int EPI>
+template <int EPI, int kT = kThreads, int kCols = pipe::TN, int kPitch = pipe::kOutPitch, int kRows = pipe::TM>
 __device__ void store_tile(const I8Gemm &p, const int32_t *tile, const float *sa_lds, uint32_t m0,
                            uint32_t n0, int tid)
 {
 #pragma clang fp contract(off)
-    const uint32_t c4 = (tid & 31) * 4;  // first of this thread's 4 columns
+    constexpr int kPerRow = kCols / 4;   // threads per row
+    const uint32_t c4 = (tid % kPerRow) * 4;  // first of this thread's 4 columns
     const uint32_t n = n0 + c4;
     float sb[4], bias[4];
 #pragma unroll
@@ -264,10 +279,10 @@ __device__ void store_tile(const I8Gemm &p, const int32_t *tile, const float *sa
         bias[q] = (ok && p.bias) ? p.bias[n + q] : 0.0f;
     }
     const bool vec = (n + 3 < p.N) && ((p.ldc & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
-    const uint32_t rows = min(static_cast<uint32_t>(pipe::TM), p.M - m0);
+    const uint32_t rows = min(static_cast<uint32_t>(kRows), p.M - m0);
 #pragma unroll 4
-    for (uint32_t r = tid >> 5; r < rows; r += 8) {
-        const v4i acc = *reinterpret_cast<const v4i *>(tile + r * pipe::kOutPitch + c4);
+    for (uint32_t r = tid / kPerRow; r < rows; r += kT / kPerRow) {
+        const v4i acc = *reinterpret_cast<const v4i *>(tile + r * kPitch + c4);
         const float sa = sa_lds[r];
         float o[4];
 #pragma unroll
@@ -466,36 +481,242 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tile
 }
 
 // ---------------------------------------------------------------------------
-// 128-deep pipelined kernel (K % 128 == 0): same 256 x 128 tile, 4 waves of
-// 128 x 64 and 32x32x32 MFMAs, but each LDS stage holds a 128-deep k slab,
-// so every row of A is fetched as one full 128-byte line (the 64-deep stage
-// fetched half lines and doubled the L2 requests for A):
+// 128-deep LDS stages (K % 128 == 0) for the 256 x 128 tile: each stage holds
+// a 128-deep k slab, so every row of A is fetched as one full 128-byte line
+// (64-deep stages fetched half lines and doubled the L2 requests for A):
 //   * stage = A 256 rows x 128 B (32 KiB) + B 16 fragment blocks (2 k
 //     blocks x 8 column blocks, 16 KiB); 3 stages = 144 KiB of LDS;
 //   * one DMA instruction moves 8 rows of A (lane l: row l/8, 16-byte slot
 //     l%8); the lane fetches k chunk slot ^ ((row >> 1) & 7), so chunk c of
 //     row r sits at r*128 + 16*(c ^ ((r >> 1) & 7)) and the fragment reads
-//     (16 rows at one chunk per quarter wave) hit 16 distinct bank groups;
-//   * one barrier per stage: the wave reads the stage's second half while
-//     the first half's MFMAs issue, then waits for the next stage's DMA.
+//     (16 rows at one chunk per quarter wave) hit 16 distinct bank groups.
 // ---------------------------------------------------------------------------
 namespace pipe128 {
 constexpr int TM = 256, TN = 128, SK = 128;  // k depth of one stage
 constexpr int kStages = 3;
 constexpr int kAInstr = TM / 8;                      // 32 x 1 KiB of A per stage
 constexpr int kBInstr = (TN / 16) * (SK / 64);       // 16 x 1 KiB of B per stage
-constexpr int kLoads = (kAInstr + kBInstr) / 4;      // 12 per wave per stage
-constexpr int kAPerWave = kAInstr / 4;               // 8
 constexpr int kStageBytes = (kAInstr + kBInstr) * 1024;  // 48 KiB
 constexpr int kBOff = kAInstr * 1024;
 constexpr size_t kLds = static_cast<size_t>(kStages) * kStageBytes;  // 144 KiB
 static_assert(pipe::kOut + TM * 4 <= static_cast<int>(kLds), "staged tile + row scales fit");
 }  // namespace pipe128
 
+// ---------------------------------------------------------------------------
+// Two waves per SIMD (K % 128 == 0): the 256 x 128 tile over the 128-deep
+// LDS stages above, with 8 waves.  Waves w and w+4 own the same
+// 128 x 64 output block and split every stage by k half (wave group gk takes
+// the 64-deep half gk), so LDS traffic per MFMA is unchanged while each SIMD
+// has a second wave to issue MFMAs whenever the other waits on its fragment
+// reads or the barrier.  The two partial accumulators are summed through LDS
+// (exact int32) before the shared epilogue.
+//   * 3 LDS stages; stage s+2 is copied while stage s is multiplied; each
+//     wave issues 6 of the 48 DMA instructions of a stage;
+//   * per stage and wave: vmcnt wait for its own copy of stage s, one
+//     barrier (stage s visible; stage s-1's buffer free), 12 fragment reads,
+//     16 MFMAs that each wait only for their own operands.
+// ---------------------------------------------------------------------------
+namespace w8 {
+constexpr int kThreads8 = 512;
+constexpr int kAPer = 4;                 // A DMA instructions per wave per stage
+constexpr int kBPer = 2;                 // B DMA instructions per wave per stage
+constexpr int kLoads = kAPer + kBPer;
+constexpr int kStages = pipe128::kStages;
+}  // namespace w8
+
 template <bool kSkip>
-__global__ __launch_bounds__(kThreads) void gemm_i8_k128(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
+__global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
 {
-    using namespace pipe128;
+    using pipe128::kBOff;
+    using pipe128::kStageBytes;
+    using pipe128::SK;
+    using pipe128::TM;
+    using pipe128::TN;
+    using w8::kAPer;
+    using w8::kBPer;
+    using w8::kLoads;
+    using w8::kStages;
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gk = wave >> 2;                    // k half of every stage
+    const int wm = (wave >> 1) & 1, wn = wave & 1;
+
+    const uint32_t total = tiles_m * tiles_n;
+    uint32_t g = blockIdx.x;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const uint32_t tmi = g % tiles_m, tni = g / tiles_m;
+    const uint32_t m0 = tmi * TM, n0 = tni * TN;
+    const uint32_t NT = p.Np >> 4;
+    const uint32_t KS = p.K / SK;
+    const uint32_t KT = p.K >> 6;
+    const uint64_t KTp = p.Kp >> 6;
+
+    // DMA sources: A instructions 4*wave + j (8 rows each), B instructions
+    // 2*wave + j (column block bi/2, k block bi%2).
+    const int8_t *src[kLoads];
+#pragma unroll
+    for (int j = 0; j < kAPer; ++j) {
+        const uint32_t r = (wave * kAPer + j) * 8 + (lane >> 3);
+        const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);
+        const uint32_t row = min(m0 + r, p.M - 1);
+        src[j] = p.A + static_cast<uint64_t>(row) * p.lda + c * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < kBPer; ++j) {
+        const int bi = wave * kBPer + j;
+        const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
+        src[kAPer + j] = p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + lane * 16;
+    }
+    auto issue = [&](uint32_t s) {
+        int8_t *st = smem + (s % kStages) * kStageBytes;
+#pragma unroll
+        for (int j = 0; j < kAPer; ++j) dma16(src[j] + s * SK, st + (wave * kAPer + j) * 1024);
+#pragma unroll
+        for (int j = 0; j < kBPer; ++j)
+            dma16(src[kAPer + j] + static_cast<uint64_t>(s) * 2048, st + kBOff + (wave * kBPer + j) * 1024);
+    };
+
+    // Fragment reads of half gk of a stage, in MFMA consumption order.
+    const int sub = (lane >> 4) & 1;
+    int a_off[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+        const uint32_t r = wm * 128 + mb * 32 + (lane & 31);
+        a_off[mb] = r * 128;
+    }
+    auto read_frags = [&](uint32_t s, Frags &f) {
+        const int8_t *st = smem + (s % kStages) * kStageBytes;
+#pragma unroll
+        for (int k = 0; k < 12; ++k) {
+            const int h = k / 6, r = k % 6;
+            if (r == 0 || r == 5) {
+                const int nb = r == 5;
+                const int boff = kBOff + (((wn * 4 + sub) * 2 + gk) << 10) +
+                                 (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
+                f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
+            } else {
+                const int mb = r - 1;
+                const uint32_t row = wm * 128 + mb * 32 + (lane & 31);
+                const uint32_t c = 4 * gk + 2 * h + (lane >> 5);
+                f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_off[mb] + ((c ^ ((row >> 1) & 7)) << 4));
+            }
+        }
+    };
+
+    uint8_t *zflags = reinterpret_cast<uint8_t *>(smem + pipe128::kLds);
+    if (kSkip) {
+        for (uint32_t i = tid; i < KT * pipe::kBBlocks; i += w8::kThreads8) {
+            const uint32_t kt = i / pipe::kBBlocks, nb = (n0 >> 4) + (i % pipe::kBBlocks);
+            zflags[i] = nb < NT ? p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] : 1;
+        }
+        __syncthreads();
+    }
+
+    v16i acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i){0};
+
+    issue(0);
+    if (KS > 1) issue(1);
+    for (uint32_t s = 0; s < KS; ++s) {
+        if (s + 1 < KS) wait_vmcnt<kLoads>();
+        else wait_vmcnt<0>();
+        block_barrier();
+        if (s + 2 < KS) issue(s + 2);
+        const bool skip = kSkip && *reinterpret_cast<const uint32_t *>(zflags + (2 * s + gk) * pipe::kBBlocks + wn * 4) ==
+                                       0x01010101u;
+        if (!skip) {
+            Frags f;
+            read_frags(s, f);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    // Sum the two k halves in the staged tile, then the shared epilogue.
+    __syncthreads();
+    int32_t *tile = reinterpret_cast<int32_t *>(smem);
+    auto tile_at = [&](int i, int j, int r) -> int32_t & {
+        return tile[(wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * pipe::kOutPitch + wn * 64 +
+                    j * 32 + (lane & 31)];
+    };
+    if (gk == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) tile_at(i, j, r) = acc[i][j][r];
+    }
+    float *sa_lds = reinterpret_cast<float *>(smem + pipe::kScaleOff);
+    if (tid < TM) {
+        const uint32_t m = m0 + tid;
+        sa_lds[tid] = (p.scale_a && m < p.M) ? p.scale_a[m] : 1.0f;
+    }
+    __syncthreads();
+    if (gk == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) tile_at(i, j, r) += acc[i][j][r];
+    }
+    __syncthreads();
+    switch (p.epilogue) {
+    case 1: store_tile<1, w8::kThreads8>(p, tile, sa_lds, m0, n0, tid); break;
+    case 2: store_tile<2, w8::kThreads8>(p, tile, sa_lds, m0, n0, tid); break;
+    case 3:
+    case 4: store_tile<3, w8::kThreads8>(p, tile, sa_lds, m0, n0, tid); break;
+    default: store_tile<0, w8::kThreads8>(p, tile, sa_lds, m0, n0, tid); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Wide tile (K % 128 == 0, dense weights, grids of many tiles): 256 x 256 per
+// workgroup, 4 waves of 128 x 128 (4 x 4 MFMA tiles, 256 accumulator
+// registers at one wave per SIMD).  Per MFMA it copies a third fewer bytes
+// from L2 into LDS and reads a third fewer fragment bytes from LDS than the
+// 256 x 128 tile, at twice the work per tile, so it pays only when the grid
+// holds well over one tile per CU.
+//   * stage = A 256 x 128 B (32 KiB, swizzled as above) + B 32 fragment
+//     blocks (16 column blocks x 2 k blocks, 32 KiB); 2 stages = 128 KiB;
+//   * per stage: 32 MFMAs on half 0 with half 1's 16 fragment reads threaded
+//     between them; vmcnt(0) (stage s+1 landed) and one barrier (stage s
+//     fully read); 32 MFMAs on half 1 with stage s+2's 16 DMA instructions
+//     and stage s+1's half-0 reads threaded between them;
+//   * the epilogue stages 128 rows at a time through LDS.
+// ---------------------------------------------------------------------------
+namespace wide {
+constexpr int TM = 256, TN = 256, SK = 128;
+constexpr int kALoads = 8, kBLoads = 8;               // per wave per stage
+constexpr int kLoads = kALoads + kBLoads;
+constexpr int kStageBytes = 64 * 1024;
+constexpr int kBOff = 32 * 1024;
+constexpr int kRing = 2 * kStageBytes;                // 128 KiB
+constexpr int kOutRows = 128;                         // rows staged at a time
+constexpr int kOutPitch = TN + 4;                     // int32 per staged row
+constexpr int kOut = kOutRows * kOutPitch * 4;        // 130 KiB
+constexpr int kScaleOff = kOut;
+constexpr size_t kLds = kOut + TM * 4;
+static_assert(kLds >= static_cast<size_t>(kRing) && kLds <= 160 * 1024, "LDS plan");
+}  // namespace wide
+
+struct FragsW {
+    v4i a[2][4], b[2][4];
+};
+
+__global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
+{
+    using namespace wide;
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
 
     const int tid = threadIdx.x;
@@ -509,181 +730,149 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_k128(I8Gemm p, uint32_t tile
     const uint32_t tmi = g % tiles_m, tni = g / tiles_m;
     const uint32_t m0 = tmi * TM, n0 = tni * TN;
     const uint32_t NT = p.Np >> 4;
-    const uint32_t KS = p.K / SK;          // stages
-    const uint32_t KT = p.K >> 6;          // 64-deep steps
+    const uint32_t KS = p.K / SK;
     const uint64_t KTp = p.Kp >> 6;
 
-    // This wave's DMA sources: 8 A instructions (rows 64*wave .. +63) and 4
-    // B blocks; each advances by a fixed stride per stage.
-    const int8_t *src[kLoads];
-    uint32_t stride[kLoads];
-#pragma unroll
-    for (int j = 0; j < kAPerWave; ++j) {
-        const uint32_t r = (wave * kAPerWave + j) * 8 + (lane >> 3);
-        const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);
-        const uint32_t row = min(m0 + r, p.M - 1);
-        src[j] = p.A + static_cast<uint64_t>(row) * p.lda + c * 16;
-        stride[j] = SK;
-    }
-#pragma unroll
-    for (int j = 0; j < kLoads - kAPerWave; ++j) {
-        const int bi = wave * (kLoads - kAPerWave) + j;   // 0..15: column block bi/2, k block bi%2
-        const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
-        src[kAPerWave + j] = p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + lane * 16;
-        stride[kAPerWave + j] = 2048;
-    }
-    // DMA instruction k (0..11) of stage s.
+    // DMA: A instruction 8*wave + j copies rows 64*wave + 8j + l/8 (M is a
+    // multiple of 256 here, so no row clamp); lane l fetches k chunk
+    // (l%8) ^ ((row >> 1) & 7) = (l%8) ^ (l/16) ^ 4(j%2).  B block
+    // bi = 8*wave + j is column block bi/2, k block bi%2.  Bases are
+    // wave-uniform (SGPRs); per-lane parts are 32-bit offsets.
+    const int q = lane >> 3;
+    const int8_t *a_base = p.A + static_cast<uint64_t>(m0 + wave * 64) * p.lda;
+    const uint32_t a_lo = q * p.lda + 16 * ((lane & 7) ^ (q >> 1));
+    const uint32_t a_lo_odd = q * p.lda + 16 * ((lane & 7) ^ (q >> 1) ^ 4);
+    const uint32_t b_lo = lane * 16;
     auto issue_one = [&](uint32_t s, int k) {
-        int8_t *st = smem + (s % kStages) * kStageBytes;
-        if (k < kAPerWave)
-            dma16(src[k] + s * stride[k], st + (wave * kAPerWave + k) * 1024);
-        else
-            dma16(src[k] + static_cast<uint64_t>(s) * stride[k],
-                  st + kBOff + (wave * (kLoads - kAPerWave) + (k - kAPerWave)) * 1024);
-    };
-    auto issue = [&](uint32_t s) {
-#pragma unroll
-        for (int k = 0; k < kLoads; ++k) issue_one(s, k);
-    };
-
-    // Fragment read offsets (bytes within a stage) for half hh of the stage.
-    // A: rows wm*128 + mb*32 + l%32, k chunk c = 4*hh + 2*h + l/32.
-    // B: column block wn*4 + 2*nb + (l/16)%2, k block hh, k group 2h + l/32.
-    const int sub = (lane >> 4) & 1;
-    int a_row_off[4];
-    uint32_t a_sw[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-        const uint32_t r = wm * 128 + mb * 32 + (lane & 31);
-        a_row_off[mb] = r * 128;
-        a_sw[mb] = (r >> 1) & 7;
-    }
-    // Fragment read k (0..11) of half hh of stage s, in the order the MFMAs
-    // consume them: per 32-deep h, b[h][0], a[h][0..3], b[h][1].
-    auto read_one = [&](uint32_t s, int hh, Frags &f, int k) {
-        const int8_t *st = smem + (s % kStages) * kStageBytes;
-        const int h = k / 6, r = k % 6;
-        if (r == 0 || r == 5) {
-            const int nb = r == 5;
-            const int boff = kBOff + (((wn * 4 + sub) * 2 + hh) << 10) +
-                             (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
-            f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
+        int8_t *st = smem + (s & 1) * kStageBytes;
+        if (k < kALoads) {
+            dma16_s(a_base + static_cast<uint64_t>(8 * k) * p.lda + s * SK, (k & 1) ? a_lo_odd : a_lo,
+                    st + (wave * kALoads + k) * 1024);
         } else {
-            const int mb = r - 1;
-            const uint32_t c = 4 * hh + 2 * h + (lane >> 5);
-            f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_row_off[mb] + ((c ^ a_sw[mb]) << 4));
+            const int bi = wave * kBLoads + (k - kALoads);
+            const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
+            dma16_s(p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + static_cast<uint64_t>(s) * 2048,
+                    b_lo, st + kBOff + bi * 1024);
         }
     };
-    auto read_frags = [&](uint32_t s, int hh, Frags &f) {
+
+    // Fragment read k (0..15) of half hh of the stage at byte offset st, in
+    // MFMA order: per 32-deep h, b[h][0], a[h][0..3], b[h][1..3].  A row
+    // wm*128 + 32i + l%32 has swizzle ((l%32) >> 1) & 7 whatever i is, so one
+    // per-lane base per (hh, h) plus the constant 4096 i addresses it; B needs
+    // one per-lane base plus constants.  With st a constant every read is
+    // base + immediate.
+    const int sub = (lane >> 4) & 1;
+    uint32_t a_rd[2][2];
 #pragma unroll
-        for (int k = 0; k < 12; ++k) read_one(s, hh, f, k);
-    };
-
-    uint8_t *zflags = reinterpret_cast<uint8_t *>(smem + kLds);
-    if (kSkip) {
-        for (uint32_t i = tid; i < KT * pipe::kBBlocks; i += kThreads) {
-            const uint32_t kt = i / pipe::kBBlocks, nb = (n0 >> 4) + (i % pipe::kBBlocks);
-            zflags[i] = nb < NT ? p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] : 1;
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            a_rd[hh][h] = (wm * 128 + (lane & 31)) * 128 +
+                          (((4 * hh + 2 * h + (lane >> 5)) ^ (((lane & 31) >> 1) & 7)) << 4);
+    const uint32_t b_rd = kBOff + ((wn * 16 + 2 * sub) << 10) + (((lane >> 5) * 16 + (lane & 15)) << 4);
+    auto read_one = [&](uint32_t st, int hh, FragsW &f, int k) {
+        const int h = k >> 3, r = k & 7;
+        if (r >= 1 && r <= 4) {
+            const int i = r - 1;
+            f.a[h][i] = *reinterpret_cast<const v4i *>(smem + st + a_rd[hh][h] + i * 4096);
+        } else {
+            const int j = r == 0 ? 0 : r - 4;
+            f.b[h][j] = *reinterpret_cast<const v4i *>(smem + st + b_rd + j * 4096 + hh * 1024 + h * 512);
         }
-        __syncthreads();
-    }
-    auto zero_step = [&](uint32_t kt) -> bool {
-        return kSkip && *reinterpret_cast<const uint32_t *>(zflags + kt * pipe::kBBlocks + wn * 4) == 0x01010101u;
     };
 
-    v16i acc[4][2];
+    v16i acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i){0};
-    // The 16 MFMAs of one 64-deep half with side work threaded between them:
-    // side(k) runs after MFMA k, so DMA issue and fragment reads (which a
-    // wave issues in order) proceed while the matrix pipe works instead of
-    // stalling it.  A skipped (all-zero) half still does its side work.
-    auto mma = [&](const Frags &f, bool skip, auto &&side) {
-        if (kSkip && skip) {
+        for (int j = 0; j < 4; ++j) acc[i][j] = (v16i){0};
+    // The 32 MFMAs of one 64-deep half; side(k) runs after MFMA k.
+    auto mma = [&](const FragsW &f, auto &&side) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) side(k);
-            return;
-        }
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
+        for (int k = 0; k < 32; ++k) {
+            const int h = k >> 4, j = (k >> 2) & 3, i = k & 3;
             acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
             side(k);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto nothing = [](int) {};
 
-    // Prologue: DMA every stage buffer, wait for stage 0, read its first half.
-    const uint32_t pre = min(KS, static_cast<uint32_t>(kStages));
-    for (uint32_t s = 0; s < pre; ++s) issue(s);
-    if (KS >= 3) wait_vmcnt<2 * kLoads>();
-    else wait_vmcnt<0>();
-    block_barrier();
-    Frags f0, f1;
-    read_frags(0, 0, f0);
-
-    // Steady state, one stage per trip: read the second half while the first
-    // half's MFMAs issue; wait for this wave's DMA of stage s+1 (stage s+2
-    // may stay in flight); barrier (stage s+1 landed everywhere, every wave
-    // holds stage s in registers); refill stage s's buffer with s+3 and read
-    // stage s+1's first half while the second half's MFMAs issue.
-    uint32_t s = 0;
-    bool sk0 = zero_step(0), sk1 = false;
-    for (; s + kStages < KS; ++s) {
-        __builtin_amdgcn_sched_barrier(0);
-        mma(f0, sk0, [&](int k) { if (k < 12) read_one(s, 1, f1, k); });
-        sk1 = zero_step(2 * s + 1);
-        __builtin_amdgcn_sched_barrier(0);
+    // Prologue: stages 0 and 1 in flight, wait for 0, read its first half.
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) issue_one(0, k);
+    if (KS > 1) {
+#pragma unroll
+        for (int k = 0; k < kLoads; ++k) issue_one(1, k);
         wait_vmcnt<kLoads>();
-        block_barrier();
-        mma(f1, sk1, [&](int k) {
-            if (k < kLoads) issue_one(s + kStages, k);
-            if (k >= 4) read_one(s + 1, 0, f0, k - 4);
-        });
-        sk0 = zero_step(2 * s + 2);
-        __builtin_amdgcn_sched_barrier(0);
+    } else {
+        wait_vmcnt<0>();
     }
-    // Drain: every remaining stage is in flight or landed; wait once.
-    wait_vmcnt<0>();
     block_barrier();
-    for (; s < KS; ++s) {
+    FragsW f0, f1;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) read_one(0, 0, f0, k);
+
+    uint32_t s = 0;
+    for (; s + 2 < KS; ++s) {
+        const uint32_t cur = (s & 1) * kStageBytes, nxt = kStageBytes - cur;
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, sk0, [&](int k) { if (k < 12) read_one(s, 1, f1, k); });
-        sk1 = zero_step(2 * s + 1);
+        mma(f0, [&](int k) { if (k < 16) read_one(cur, 1, f1, k); });
+        wait_vmcnt<0>();
+        block_barrier();
+        mma(f1, [&](int k) {
+            if (k < 16) issue_one(s + 2, k);
+            else read_one(nxt, 0, f0, k - 16);
+        });
+    }
+    if (s + 1 < KS) {
+        const uint32_t cur = (s & 1) * kStageBytes, nxt = ((s + 1) & 1) * kStageBytes;
         __builtin_amdgcn_sched_barrier(0);
-        if (s + 1 < KS) {
-            mma(f1, sk1, [&](int k) { if (k >= 4) read_one(s + 1, 0, f0, k - 4); });
-            sk0 = zero_step(2 * s + 2);
-        } else {
-            mma(f1, sk1, nothing);
-        }
+        mma(f0, [&](int k) { if (k < 16) read_one(cur, 1, f1, k); });
+        wait_vmcnt<0>();
+        block_barrier();
+        mma(f1, [&](int k) { if (k >= 16) read_one(nxt, 0, f0, k - 16); });
+        ++s;
+    }
+    {
+        const uint32_t cur = (s & 1) * kStageBytes;
+        __builtin_amdgcn_sched_barrier(0);
+        mma(f0, [&](int k) { if (k < 16) read_one(cur, 1, f1, k); });
+        mma(f1, [](int) {});
     }
 
+    // Epilogue, 128 rows (the rows of waves with wm == half) at a time.
     __syncthreads();
     int32_t *tile = reinterpret_cast<int32_t *>(smem);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                tile[(wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * pipe::kOutPitch + wn * 64 +
-                     j * 32 + (lane & 31)] = acc[i][j][r];
-    float *sa_lds = reinterpret_cast<float *>(smem + pipe::kScaleOff);
+    float *sa_lds = reinterpret_cast<float *>(smem + kScaleOff);
     {
         const uint32_t m = m0 + tid;
         sa_lds[tid] = (p.scale_a && m < p.M) ? p.scale_a[m] : 1.0f;
     }
-    __syncthreads();
-    switch (p.epilogue) {
-    case 1: store_tile<1>(p, tile, sa_lds, m0, n0, tid); break;
-    case 2: store_tile<2>(p, tile, sa_lds, m0, n0, tid); break;
-    case 3:
-    case 4: store_tile<3>(p, tile, sa_lds, m0, n0, tid); break;
-    default: store_tile<0>(p, tile, sa_lds, m0, n0, tid); break;
+    for (int half = 0; half < 2; ++half) {
+        const uint32_t mh = m0 + half * kOutRows;
+        if (wm == half) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        tile[(i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kOutPitch + wn * 128 + j * 32 +
+                             (lane & 31)] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (mh < p.M) {
+            const float *sa = sa_lds + half * kOutRows;
+            switch (p.epilogue) {
+            case 1: store_tile<1, kThreads, TN, kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
+            case 2: store_tile<2, kThreads, TN, kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
+            case 3:
+            case 4: store_tile<3, kThreads, TN, kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
+            default: store_tile<0, kThreads, TN, kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -701,8 +890,9 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
             bool ok = true;
             for (const void *fn : {reinterpret_cast<const void *>(gemm_i8_pipe<false>),
                                    reinterpret_cast<const void *>(gemm_i8_pipe<true>),
-                                   reinterpret_cast<const void *>(gemm_i8_k128<false>),
-                                   reinterpret_cast<const void *>(gemm_i8_k128<true>)})
+                                   reinterpret_cast<const void *>(gemm_i8_k128w8<false>),
+                                   reinterpret_cast<const void *>(gemm_i8_k128w8<true>),
+                                   reinterpret_cast<const void *>(gemm_i8_wide)})
                 ok = ok && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                160 * 1024) == hipSuccess;
             lds_optin = ok;
@@ -710,11 +900,18 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
         const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
         const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
         if (p.K % pipe128::SK == 0) {
+            // Dense weights, whole 256-row tiles and a grid of at least ~1.5
+            // wide tiles per CU (256 CUs): the 256 x 256 tile.
+            const uint32_t wm_ = p.M / wide::TM, wn_ = (p.N + wide::TN - 1) / wide::TN;
+            if (!p.zero_blocks && p.M % wide::TM == 0 && wm_ * wn_ >= 384) {
+                gemm_i8_wide<<<dim3(wm_ * wn_), kThreads, wide::kLds, s>>>(p, wm_, wn_);
+                return;
+            }
             if (p.zero_blocks) {
                 const size_t lds = pipe128::kLds + ((p.K / 64) * pipe::kBBlocks + 15) / 16 * 16;
-                gemm_i8_k128<true><<<dim3(tm * tn), kThreads, lds, s>>>(p, tm, tn);
+                gemm_i8_k128w8<true><<<dim3(tm * tn), w8::kThreads8, lds, s>>>(p, tm, tn);
             } else {
-                gemm_i8_k128<false><<<dim3(tm * tn), kThreads, pipe128::kLds, s>>>(p, tm, tn);
+                gemm_i8_k128w8<false><<<dim3(tm * tn), w8::kThreads8, pipe128::kLds, s>>>(p, tm, tn);
             }
             return;
         }

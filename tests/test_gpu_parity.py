@@ -97,6 +97,25 @@ def test_matmul_i8_bit_exact(gpu, M, K, N):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,K,N", [(2048, 256, 12288), (2304, 384, 11000), (2048, 128, 12288)])
+def test_matmul_i8_wide_tile(gpu, M, K, N):
+    """Grids of >= 384 whole 256 x 256 tiles take the wide-tile kernel
+    (1, 2 and 3 k stages; a ragged last column tile).  Every output is
+    checked: the float64 product of int8 matrices is the exact int32
+    accumulator here, and C = ((float)acc * sa) * sb rounds each product
+    once in float32, as the oracle's matmul_i8 does."""
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    w = gpu.pack(B, K, N, scales=sb)
+    got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa)
+    gpu.release_packed(w)
+    acc = A.astype(np.float64) @ B.astype(np.float64)
+    want = (acc.astype(np.float32) * sa[:, None]) * sb[None, :]
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
 @pytest.mark.parametrize("M", [1, 6, 40])
 def test_matmul_i8_accumulator_exact(gpu, M):
     # scale 1 everywhere: C == (float)acc exactly while |acc| < 2^24
