@@ -347,7 +347,8 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
         float *w = static_cast<float *>(s->ensure_workspace(ws));
         k::gemv_f32(s->hip, p, w);
     } else {
-        k::gemm_f32(s->hip, p);
+        const size_t ws = k::gemm_f32_ws_bytes(p);
+        k::gemm_f32(s->hip, p, ws ? static_cast<float *>(s->ensure_workspace(ws)) : nullptr);
     }
     VNPU_HIP(hipGetLastError());
     sg.finish();

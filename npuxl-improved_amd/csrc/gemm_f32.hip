@@ -127,7 +127,10 @@ __device__ __forceinline__ void store_out(const F32Gemm &p, uint32_t m, uint32_t
     *dst = dev::epilogue(out, p.epilogue);
 }
 
-__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Gemm p)
+// blockIdx.z selects a k range of k_per_split (a multiple of BK) when K is
+// split over workgroups; then the raw sums go to ws[z][m][n] and
+// gemm_f32_splitk_reduce applies alpha, bias, beta and the epilogue once.
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Gemm p, uint32_t k_per_split, float *ws)
 {
     __shared__ __attribute__((aligned(16))) float As[2][BK * kPitch];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK * kPitch];
@@ -150,15 +153,17 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Gemm p)
     if (state != 1) {
         const bool va = ((p.lda & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0);
         const bool vb = ((p.ldb & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.B) & 15u) == 0);
-        const uint32_t KT = (p.K + BK - 1) / BK;
+        const uint32_t kb = blockIdx.z * k_per_split;
+        const uint32_t ke = min(p.K, kb + k_per_split);
+        const uint32_t KT = (ke - kb + BK - 1) / BK;
         Stage st;
-        fetch(p, m0, n0, 0, tid, va, vb, st);
+        fetch(p, m0, n0, kb, tid, va, vb, st);
         stash(p, tid, st, As[0], Bs[0]);
         __syncthreads();
         for (uint32_t kt = 0; kt < KT; ++kt) {
             const int cur = kt & 1;
             const bool more = kt + 1 < KT;
-            if (more) fetch(p, m0, n0, (kt + 1) * BK, tid, va, vb, st);
+            if (more) fetch(p, m0, n0, kb + (kt + 1) * BK, tid, va, vb, st);
             const float *as = As[cur];
             const float *bs = Bs[cur];
 #pragma unroll
@@ -189,10 +194,25 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Gemm p)
             for (int r = 0; r < 4; ++r) {
                 const uint32_t m = m0 + wm * 64 + i * 16 + fg * 4 + r;
                 if (m >= p.M) continue;
+                if (ws) {
+                    ws[(static_cast<uint64_t>(blockIdx.z) * p.M + m) * p.N + n] = acc[i][j][r];
+                    continue;
+                }
                 const bool c = state == 1 ? true : (state == 2 ? culled(p, m, n) : false);
                 store_out(p, m, n, acc[i][j][r], c);
             }
     }
+}
+
+__global__ __launch_bounds__(kThreads) void gemm_f32_splitk_reduce(F32Gemm p, const float *ws, uint32_t splits)
+{
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
+    if (idx >= total) return;
+    const uint32_t m = static_cast<uint32_t>(idx / p.N), n = static_cast<uint32_t>(idx % p.N);
+    float s = 0.0f;
+    for (uint32_t i = 0; i < splits; ++i) s += ws[static_cast<uint64_t>(i) * total + idx];
+    store_out(p, m, n, s, false);
 }
 
 // ---------------------------------------------------------------------------
@@ -305,10 +325,37 @@ void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn)
     bn = BN;
 }
 
-void gemm_f32(hipStream_t s, const F32Gemm &p)
+// Grids of fewer than 128 tiles leave most CUs idle: split K over up to
+// 256 workgroups, at least 64 deep each (not with a cull map, whose per-tile
+// state is read by the single-pass kernel).
+static uint32_t gemm_f32_splits(const F32Gemm &p)
 {
-    dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
-    gemm_f32_kernel<<<grid, kThreads, 0, s>>>(p);
+    if (p.ktile_state || p.cull) return 1;
+    const uint32_t tiles = ((p.N + BN - 1) / BN) * ((p.M + BM - 1) / BM);
+    uint32_t splits = 1;
+    while (tiles * splits < 256 && p.K / (splits * 2) >= 64) splits *= 2;
+    return tiles >= 128 ? 1 : splits;
+}
+
+size_t gemm_f32_ws_bytes(const F32Gemm &p)
+{
+    const uint32_t splits = gemm_f32_splits(p);
+    return splits > 1 ? static_cast<size_t>(splits) * p.M * p.N * sizeof(float) : 0;
+}
+
+void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
+{
+    const uint32_t want = gemm_f32_splits(p);
+    const uint32_t kps = want > 1 ? ((p.K + want - 1) / want + BK - 1) / BK * BK : p.K;
+    // Every z slice starts below K (rounding kps up may leave fewer slices).
+    const uint32_t splits = want > 1 ? (p.K + kps - 1) / kps : 1;
+    dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, splits);
+    gemm_f32_kernel<<<grid, kThreads, 0, s>>>(p, kps, splits > 1 ? ws : nullptr);
+    if (splits > 1) {
+        const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
+        gemm_f32_splitk_reduce<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
+            p, ws, splits);
+    }
 }
 
 size_t gemv_f32_ws_bytes(uint32_t M, uint32_t N, uint32_t K)

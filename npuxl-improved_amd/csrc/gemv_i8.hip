@@ -8,9 +8,10 @@
 //   acc = sum_k A[m][k] * B[k][n] in int32 (exact, so any order is bit-exact).
 //
 // Design (HBM-bound: every weight byte is read once, ~K*N bytes per call):
-//   * one workgroup of W waves owns one 16-column strip over all of K; the
-//     packed layout stores a strip's Kp/64 blocks of 1 KiB contiguously, so
-//     the workgroup streams one sequential run;
+//   * one workgroup of W waves owns T 16-column strips (T = 1, or 4 for many
+//     rows and strips) over all of K; the packed layout stores a strip's
+//     Kp/64 blocks of 1 KiB contiguously, so each strip is one sequential
+//     run;
 //   * lane l = 16*kg + c loads 16 bytes = 16 consecutive k of column c
 //     (one fully coalesced 1 KiB load per wave per block); waves interleave
 //     over the blocks (wave w takes blocks w, w+W, ...), with U blocks in
@@ -48,44 +49,56 @@ __device__ __forceinline__ int dot16(const int4 a, const int4 b, int acc)
     return acc;
 }
 
-// M rows, W waves, U blocks in flight per wave; chunk_k = k extent (multiple
-// of 64) of the activations staged at a time.
-template <int M, int W, int U>
+// M rows, W waves, U blocks in flight per wave, T strips per workgroup (each
+// activation read from LDS feeds T weight blocks); chunk_k = k extent
+// (multiple of 64) of the activations staged at a time.
+template <int M, int W, int U, int T>
 __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chunk_k)
 {
     extern __shared__ __attribute__((aligned(16))) int8_t a_lds[];  // [chunk_k/16][M][16]
-    __shared__ int red[W][M][16];
+    __shared__ int red[W][T][M][16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     // wave-uniform by construction; readfirstlane lets the compiler know
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kg = lane >> 4;
-    const uint32_t nt = blockIdx.x;
+    const uint32_t NT = p.Np >> 4;
+    const uint32_t nt0 = blockIdx.x * T;
     const uint32_t KT = p.Kp >> 6;
-    const int8_t *strip = p.frag + static_cast<uint64_t>(nt) * KT * 1024;
     const bool vec_a = ((p.lda & 15u) == 0) && ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0);
 
-    int acc[M];
+    int acc[T][M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = 0;
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[t][m] = 0;
 
     for (uint32_t kc = 0; kc < p.Kp; kc += chunk_k) {
         const uint32_t kt0 = kc >> 6, kt1 = min(KT, (kc + chunk_k) >> 6);
         const uint32_t first = kt0 + wave;
         const uint32_t cnt = first < kt1 ? (kt1 - first + W - 1) / W : 0;
-        // This wave's blocks first, first + W, ... as one bounds-checked buffer.
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int8_t *>(strip) + static_cast<uint64_t>(first) * 1024, 0,
-            cnt ? static_cast<int>(((cnt - 1) * W + 1) * 1024) : 0, kBufferWord3);
-        auto ld = [&](uint32_t i) {
+        // This wave's blocks first, first + W, ... of each strip as one
+        // bounds-checked buffer (empty for a strip past the last one).
+        __amdgpu_buffer_rsrc_t rs[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint32_t nt = min(nt0 + t, NT - 1);
+            const int8_t *strip = p.frag + static_cast<uint64_t>(nt) * KT * 1024;
+            const int bytes = (cnt && nt0 + t < NT) ? static_cast<int>(((cnt - 1) * W + 1) * 1024) : 0;
+            rs[t] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(strip) + static_cast<uint64_t>(first) * 1024,
+                                                      0, bytes, kBufferWord3);
+        }
+        auto ld = [&](int t, uint32_t i) {
             return __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(
-                rs, i * W * 1024 + lane * 16, 0, kNontemporal));
+                rs[t], i * W * 1024 + lane * 16, 0, kNontemporal));
         };
         // The weight stream does not depend on the activations: put the first
         // batch in flight before staging them.
-        int4 bc[U], bn[U];
+        int4 bc[U][T], bn[U][T];
 #pragma unroll
-        for (int u = 0; u < U; ++u) bc[u] = ld(u);
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int t = 0; t < T; ++t) bc[u][t] = ld(t, u);
 
         if (kc) __syncthreads();  // previous chunk fully consumed
         const uint32_t chunks = (kt1 - kt0) * 4 * M;
@@ -111,7 +124,9 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chun
 
         for (uint32_t i = 0; i < cnt; i += U) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) bn[u] = ld(i + U + u);
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int t = 0; t < T; ++t) bn[u][t] = ld(t, i + U + u);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 // past the last block the weights read as zero; clamp the
@@ -119,39 +134,47 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chun
                 const uint32_t ktl = first + W * min(i + u, cnt - 1) - kt0;
                 const int8_t *arow = a_lds + ((ktl * 4 + kg) * M) * 16;
 #pragma unroll
-                for (int m = 0; m < M; ++m)
-                    acc[m] = dot16(*reinterpret_cast<const int4 *>(arow + m * 16), bc[u], acc[m]);
+                for (int m = 0; m < M; ++m) {
+                    const int4 a = *reinterpret_cast<const int4 *>(arow + m * 16);
+#pragma unroll
+                    for (int t = 0; t < T; ++t) acc[t][m] = dot16(a, bc[u][t], acc[t][m]);
+                }
             }
 #pragma unroll
-            for (int u = 0; u < U; ++u) bc[u] = bn[u];
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int t = 0; t < T; ++t) bc[u][t] = bn[u][t];
         }
     }
 
     // Reduce the four k groups (lanes c, c+16, c+32, c+48).
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        int v = acc[m];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        acc[m] = v;
-    }
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            int v = acc[t][m];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            acc[t][m] = v;
+        }
     if (lane < 16) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) red[wave][m][lane] = acc[m];
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int m = 0; m < M; ++m) red[wave][t][m][lane] = acc[t][m];
     }
     __syncthreads();
-    for (int o = tid; o < M * 16; o += 64 * W) {
-        const int c = o & 15, m = o >> 4;
-        const uint32_t n = nt * 16 + c;
-        if (n < p.N) {
-            int s = 0;
+    for (int o = tid; o < T * M * 16; o += 64 * W) {
+        const int c = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
+        const uint32_t n = (nt0 + t) * 16 + c;
+        if (nt0 + t >= NT || n >= p.N) continue;
+        int s = 0;
 #pragma unroll
-            for (int w = 0; w < W; ++w) s += red[w][m][c];
-            const float sa = p.scale_a ? p.scale_a[m] : 1.0f;
-            float out = __fmul_rn(__fmul_rn(static_cast<float>(s), sa), p.scale_b[n]);
-            if (p.bias) out = __fadd_rn(out, p.bias[n]);
-            p.C[static_cast<uint64_t>(m) * p.ldc + n] = dev::epilogue(out, p.epilogue);
-        }
+        for (int w = 0; w < W; ++w) s += red[w][t][m][c];
+        const float sa = p.scale_a ? p.scale_a[m] : 1.0f;
+        float out = __fmul_rn(__fmul_rn(static_cast<float>(s), sa), p.scale_b[n]);
+        if (p.bias) out = __fadd_rn(out, p.bias[n]);
+        p.C[static_cast<uint64_t>(m) * p.ldc + n] = dev::epilogue(out, p.epilogue);
     }
 }
 
@@ -159,19 +182,23 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chun
 // waves with eight blocks in flight each for one or two rows; eight waves
 // when strips are few (the grid is one workgroup per strip); from three rows
 // up the activation reads from LDS grow with M, and eight waves with four
-// blocks each keep more of them overlapped.
+// blocks each keep more of them overlapped; from six rows up, with at least
+// 1024 strips, each workgroup takes four strips so that one activation read
+// from LDS feeds four weight blocks (M=8, N=32000: 30 -> 25-28 us).
 template <int M>
 void launch_m(hipStream_t s, const I8Gemm &p)
 {
     const uint32_t NT = p.Np >> 4;
     const uint32_t chunk_k = std::min<uint32_t>(p.Kp, (kLdsA / M) & ~63u);
     const size_t lds = static_cast<size_t>(chunk_k) * M;
-    if (M <= 2 && NT >= 512)
-        gemv_i8_kernel<M, 4, 8><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
+    if (M >= 6 && NT >= 1024)
+        gemv_i8_kernel<M, 4, 4, 4><<<dim3((NT + 3) / 4), 256, lds, s>>>(p, chunk_k);
+    else if (M <= 2 && NT >= 512)
+        gemv_i8_kernel<M, 4, 8, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
     else if (M <= 2)
-        gemv_i8_kernel<M, 8, 8><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+        gemv_i8_kernel<M, 8, 8, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
     else
-        gemv_i8_kernel<M, 8, 4><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+        gemv_i8_kernel<M, 8, 4, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
 }
 
 }  // namespace

@@ -81,7 +81,10 @@ I8_SHAPES = [(1, 64, 16), (1, 4096, 4096), (1, 300, 1100), (2, 257, 33), (3, 100
              (512, 512, 512), (320, 4096, 700), (100, 1024, 2000), (513, 192, 130),
              # decode shapes of the config-4 block: the activations of K = 11008
              # (M=8) and K = 40000 (M=1) are staged in several LDS chunks
-             (8, 11008, 4096), (8, 4096, 12288), (1, 11008, 4096), (1, 40000, 48), (5, 9000, 33)]
+             (8, 11008, 4096), (8, 4096, 12288), (1, 11008, 4096), (1, 40000, 48), (5, 9000, 33),
+             # six or more rows over >= 1024 column strips: four strips per
+             # workgroup (a ragged last group; K not a multiple of 64)
+             (8, 1000, 16400), (6, 4096, 32000), (7, 130, 20000)]
 
 
 @pytest.mark.parametrize("M,K,N", I8_SHAPES)
