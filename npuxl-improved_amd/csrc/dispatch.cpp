@@ -342,8 +342,8 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
     const size_t c_bytes = span(in.M, in.N, p.ldc, 4);
     p.C = c_in ? sg.inout(in.C, c_bytes) : sg.out(in.C, c_bytes);
 
-    if (!has_mask && in.M <= 8 && !in.trans_a && !in.trans_b) {
-        const size_t ws = k::gemv_f32_ws_bytes(in.M, in.N, in.K);
+    if (!has_mask && in.M <= 8 && !in.trans_a && !in.trans_b && k::gemv_f32_supported(p)) {
+        const size_t ws = k::gemv_f32_ws_bytes(p);
         float *w = static_cast<float *>(s->ensure_workspace(ws));
         k::gemv_f32(s->hip, p, w);
     } else {

@@ -17,6 +17,7 @@
 //     trans_a / trans_b only change how a tile is fetched from HBM.
 //   * gemv_f32_kernel: M <= 8, NN (the MTP head and f32 decode GEMMs).  HBM
 //     bound: 256 columns x float4 per workgroup, waves and workgroups split K,
+//     weights streamed with branch-free bounds-checked buffer loads,
 //     activations read as wave-uniform scalars; partial sums reduced in a
 //     second deterministic pass when K is split across workgroups.
 #include "kernels.hpp"
@@ -220,7 +221,15 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_splitk_reduce(F32Gemm p, co
 // ---------------------------------------------------------------------------
 constexpr int kSkinnyCols = 256;  // 64 lanes x float4
 constexpr int kSkinnyUnroll = 8;
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
+constexpr int kNontemporal = 2;           // weights are streamed once
 
+// Rows kb..ke of B in this workgroup's 256 columns, as one bounds-checked
+// buffer: lane l of wave w reads row kb + w + 4i at byte (row - kb) * ldb * 4
+// + 16 l.  Rows past ke and columns past N in the last row read as zero, so
+// the load stream has no branches (a branch around a load makes the waitcnt
+// pass drain every load in flight).  Activations are wave-uniform scalars,
+// zero for rows past ke.
 template <int M>
 __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(F32Gemm p, uint32_t k_per_split,
                                                             float *ws, uint32_t splits)
@@ -228,10 +237,16 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(F32Gemm p, uint32_t 
     __shared__ float4 red[4][M][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t n = blockIdx.x * kSkinnyCols + lane * 4;
+    const uint32_t n0 = blockIdx.x * kSkinnyCols;
+    const uint32_t n = n0 + lane * 4;
     const uint32_t kb = blockIdx.y * k_per_split;
     const uint32_t ke = min(p.K, kb + k_per_split);
-    const bool vb = ((p.ldb & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.B) & 15u) == 0);
+
+    const uint64_t row_bytes = static_cast<uint64_t>(p.ldb) * 4;
+    const uint64_t span = ke > kb ? (ke - kb - 1) * row_bytes + static_cast<uint64_t>(p.N - n0) * 4 : 0;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(p.B) + static_cast<uint64_t>(kb) * p.ldb + n0, 0,
+        static_cast<int>(span), kBufferWord3);
 
     float4 acc[M];
 #pragma unroll
@@ -241,16 +256,15 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(F32Gemm p, uint32_t 
         float4 b[kSkinnyUnroll];
 #pragma unroll
         for (int u = 0; u < kSkinnyUnroll; ++u) {
-            const uint32_t kk = k + u * 4;
-            b[u] = kk < ke ? load4(p.B, p.ldb, kk, n, p.K, p.N, vb) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const uint32_t off = static_cast<uint32_t>((k - kb + u * 4) * row_bytes) + lane * 16;
+            b[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kNontemporal));
         }
 #pragma unroll
         for (int u = 0; u < kSkinnyUnroll; ++u) {
             const uint32_t kk = k + u * 4;
-            if (kk >= ke) break;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float a = p.A[static_cast<uint64_t>(m) * p.lda + kk];
+                const float a = kk < ke ? p.A[static_cast<uint64_t>(m) * p.lda + kk] : 0.0f;
                 acc[m].x = fmaf(a, b[u].x, acc[m].x);
                 acc[m].y = fmaf(a, b[u].y, acc[m].y);
                 acc[m].z = fmaf(a, b[u].z, acc[m].z);
@@ -296,24 +310,38 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_reduce(F32Gemm p, const flo
     store_out(p, m, n, s, false);
 }
 
-uint32_t skinny_splits(uint32_t N, uint32_t K)
+// K split: enough workgroups to keep the weight stream in flight, and each
+// workgroup's buffer (its rows of B, plus the rows a final partial batch
+// reads past them) addressable with 32-bit offsets.
+struct SkinnyPlan {
+    uint32_t splits, kps;
+};
+
+SkinnyPlan skinny_plan(const F32Gemm &p)
 {
-    const uint32_t col_blocks = (N + kSkinnyCols - 1) / kSkinnyCols;
-    uint32_t splits = 1;
-    while (col_blocks * splits < 1024 && K / (splits * 2) >= 256) splits *= 2;
-    return splits;
+    const uint32_t col_blocks = (p.N + kSkinnyCols - 1) / kSkinnyCols;
+    uint32_t want = 1;
+    while (col_blocks * want < 1024 && p.K / (want * 2) >= 256) want *= 2;
+    const uint64_t row_bytes = static_cast<uint64_t>(p.ldb) * 4;
+    const uint64_t max_rows = (0x7fffffffull / row_bytes) - 4 * kSkinnyUnroll;
+    uint64_t kps = (p.K + want - 1) / want;
+    if (kps > max_rows) kps = max_rows;
+    SkinnyPlan plan;
+    plan.kps = static_cast<uint32_t>(kps);
+    plan.splits = static_cast<uint32_t>((p.K + kps - 1) / kps);
+    return plan;
 }
 
 template <int M>
 void launch_skinny(hipStream_t s, const F32Gemm &p, float *ws)
 {
-    const uint32_t splits = skinny_splits(p.N, p.K);
-    const uint32_t kps = (p.K + splits - 1) / splits;
-    dim3 grid((p.N + kSkinnyCols - 1) / kSkinnyCols, splits);
-    gemv_f32_kernel<M><<<grid, kThreads, 0, s>>>(p, kps, ws, splits);
-    if (splits > 1) {
+    const SkinnyPlan plan = skinny_plan(p);
+    dim3 grid((p.N + kSkinnyCols - 1) / kSkinnyCols, plan.splits);
+    gemv_f32_kernel<M><<<grid, kThreads, 0, s>>>(p, plan.kps, ws, plan.splits);
+    if (plan.splits > 1) {
         const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
-        gemv_f32_reduce<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(p, ws, splits);
+        gemv_f32_reduce<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
+            p, ws, plan.splits);
     }
 }
 
@@ -358,10 +386,16 @@ void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
     }
 }
 
-size_t gemv_f32_ws_bytes(uint32_t M, uint32_t N, uint32_t K)
+size_t gemv_f32_ws_bytes(const F32Gemm &p)
 {
-    const uint32_t splits = skinny_splits(N, K);
-    return splits > 1 ? static_cast<size_t>(splits) * M * N * sizeof(float) : 0;
+    const SkinnyPlan plan = skinny_plan(p);
+    return plan.splits > 1 ? static_cast<size_t>(plan.splits) * p.M * p.N * sizeof(float) : 0;
+}
+
+bool gemv_f32_supported(const F32Gemm &p)
+{
+    // 33 rows of B must be addressable with 32-bit offsets
+    return static_cast<uint64_t>(p.ldb) * 4 * (4 * kSkinnyUnroll + 1) < 0x7fffffffull;
 }
 
 void gemv_f32(hipStream_t s, const F32Gemm &p, float *ws)

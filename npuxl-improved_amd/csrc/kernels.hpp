@@ -70,9 +70,11 @@ void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn);
 // bytes (0 when the single-pass kernel is used).
 size_t gemm_f32_ws_bytes(const F32Gemm &p);
 void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws);
-// Skinny path: M <= 8, trans_a == 0, trans_b == 0, no cull.  ws holds
-// gemv_f32_ws_bytes(M, N, K) bytes.
-size_t gemv_f32_ws_bytes(uint32_t M, uint32_t N, uint32_t K);
+// Skinny path: M <= 8, trans_a == 0, trans_b == 0, no cull, and
+// gemv_f32_supported(p) (rows of B short enough for 32-bit buffer offsets).
+// ws holds gemv_f32_ws_bytes(p) bytes.
+size_t gemv_f32_ws_bytes(const F32Gemm &p);
+bool gemv_f32_supported(const F32Gemm &p);
 void gemv_f32(hipStream_t s, const F32Gemm &p, float *ws);
 
 // ---- transformer ops (ops.hip) ----
