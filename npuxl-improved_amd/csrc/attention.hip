@@ -410,22 +410,19 @@ struct PrefillLds {
     static_assert(8 * 16 * D <= 2 * kBuf, "output staging fits in the key buffers");
 };
 
+// One block of PQ queries starting at q0, for (batch, head) bh.
 template <int D>
-__global__ __launch_bounds__(PThreads) void attn_prefill_kernel(Attn a)
+__device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64_t bh, float *lds)
 {
     using L = PrefillLds<D>;
     constexpr int NS = D / 4;          // QK MFMA steps per tile (4 d each)
     constexpr int NCH = D / 4;         // 16-byte chunks per row
     constexpr int DT = D / 16;         // 16-wide d tiles of O^T
     constexpr int HI = DT / 4;         // V chunks read per key
-    extern __shared__ __attribute__((aligned(16))) float lds[];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, qc = lane & 15;
-    const uint64_t bh = blockIdx.y;
-    const uint32_t nqb = gridDim.x;
-    const uint32_t q0 = (nqb - 1 - blockIdx.x) * PQ;        // heaviest causal blocks first
     const uint32_t sq = a.seq_q, sk = a.seq_k;
     const uint32_t off = sk > sq ? sk - sq : 0;
     const float *Kh = a.K + bh * sk * D;
@@ -574,6 +571,24 @@ __global__ __launch_bounds__(PThreads) void attn_prefill_kernel(Attn a)
     }
 }
 
+// Causal blocks cost in proportion to their position, so with nqb blocks per
+// head the grid has ceil(nqb/2) workgroups per head and workgroup x takes
+// block nqb-1-x and then block x: every workgroup does the same work (the
+// grid otherwise runs as long as its last, heaviest block).  Without a
+// causal mask every block costs the same and each workgroup takes one.
+template <int D>
+__global__ __launch_bounds__(PThreads) void attn_prefill_kernel(Attn a, uint32_t nqb)
+{
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const uint64_t bh = blockIdx.y;
+    const uint32_t heavy = nqb - 1 - blockIdx.x;
+    prefill_block<D>(a, heavy * PQ, bh, lds);
+    if (gridDim.x < nqb && blockIdx.x != heavy) {
+        __syncthreads();  // the output staging of the first block is read out
+        prefill_block<D>(a, blockIdx.x * PQ, bh, lds);
+    }
+}
+
 // Merge split partials: O = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
 __global__ __launch_bounds__(kThreads) void attn_merge(Attn a, uint32_t splits, uint64_t rows,
                                                        const float *ws_acc, const float *ws_ml)
@@ -682,10 +697,12 @@ void attention(hipStream_t s, const Attn &a, float *ws)
     float *ws_ml = ws ? ws + static_cast<uint64_t>(splits) * rows * D : nullptr;
     dim3 grid(qb, a.batch * a.heads, splits);
     if (use_prefill(a)) {
+        const uint32_t nqb = qb;
+        if (a.causal) grid.x = (nqb + 1) / 2;
         if (D == 128)
-            attn_prefill_kernel<128><<<grid, PThreads, PrefillLds<128>::kBytes, s>>>(a);
+            attn_prefill_kernel<128><<<grid, PThreads, PrefillLds<128>::kBytes, s>>>(a, nqb);
         else
-            attn_prefill_kernel<64><<<grid, PThreads, PrefillLds<64>::kBytes, s>>>(a);
+            attn_prefill_kernel<64><<<grid, PThreads, PrefillLds<64>::kBytes, s>>>(a, nqb);
         return;
     }
     if (use_decode(a)) {

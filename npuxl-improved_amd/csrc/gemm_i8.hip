@@ -7,7 +7,7 @@
 //
 // Kernels, chosen by gemm_i8() at the end of the file:
 //   * gemm_i8_wide   - 256 x 256 tiles, dense weights, M % 256 == 0,
-//                      K % 128 == 0, >= 384 tiles;
+//                      K % 128 == 0, >= 256 tiles;
 //   * gemm_i8_k128w8 - 256 x 128 tiles, 8 waves, K % 128 == 0;
 //   * gemm_i8_pipe   - 256 x 128 tiles, 64-deep stages, K % 64 == 0;
 //   * gemm_i8_generic - any shape and alignment (below).
@@ -24,7 +24,6 @@
 // lane l = 16*g + r holds row/column r and k = 16*g .. 16*g + 15 of the
 // 64-deep block.  Output: lane l holds C[4*(l/16) + i][l%16], i = 0..3.
 #include "kernels.hpp"
-#include <type_traits>
 #include "device_math.hpp"
 
 namespace vnpu {
@@ -681,12 +680,12 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
 }
 
 // ---------------------------------------------------------------------------
-// Wide tile (K % 128 == 0, dense weights, grids of many tiles): 256 x 256 per
+// Wide tile (K % 128 == 0, dense weights, >= 256 tiles): 256 x 256 per
 // workgroup, 4 waves of 128 x 128 (4 x 4 MFMA tiles, 256 accumulator
 // registers at one wave per SIMD).  Per MFMA it copies a third fewer bytes
 // from L2 into LDS and reads a third fewer fragment bytes from LDS than the
 // 256 x 128 tile, at twice the work per tile, so it pays only when the grid
-// holds well over one tile per CU.
+// holds at least one tile per CU.
 //   * stage = A 256 x 128 B (32 KiB, swizzled as above) + B 32 fragment
 //     blocks (16 column blocks x 2 k blocks, 32 KiB); 2 stages = 128 KiB;
 //   * per stage: 32 MFMAs on half 0 with half 1's 16 fragment reads threaded
@@ -900,10 +899,12 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
         const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
         const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
         if (p.K % pipe128::SK == 0) {
-            // Dense weights, whole 256-row tiles and a grid of at least ~1.5
-            // wide tiles per CU (256 CUs): the 256 x 256 tile.
+            // Dense weights, whole 256-row tiles and at least one wide tile
+            // per CU (256 CUs): the 256 x 256 tile (measured: 2048x4096x8192
+            // 57 vs 78 us, x11008 108 vs 112 us; with 128 wide tiles half the
+            // CUs idle and the 256 x 128 tile wins, 84 vs 115 us).
             const uint32_t wm_ = p.M / wide::TM, wn_ = (p.N + wide::TN - 1) / wide::TN;
-            if (!p.zero_blocks && p.M % wide::TM == 0 && wm_ * wn_ >= 384) {
+            if (!p.zero_blocks && p.M % wide::TM == 0 && wm_ * wn_ >= 256) {
                 gemm_i8_wide<<<dim3(wm_ * wn_), kThreads, wide::kLds, s>>>(p, wm_, wn_);
                 return;
             }

@@ -100,9 +100,10 @@ def test_matmul_i8_bit_exact(gpu, M, K, N):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,K,N", [(2048, 256, 12288), (2304, 384, 11000), (2048, 128, 12288)])
+@pytest.mark.parametrize("M,K,N", [(2048, 256, 12288), (2304, 384, 11000), (2048, 128, 12288),
+                                   (4096, 256, 4096)])
 def test_matmul_i8_wide_tile(gpu, M, K, N):
-    """Grids of >= 384 whole 256 x 256 tiles take the wide-tile kernel
+    """Grids of >= 256 whole 256 x 256 tiles take the wide-tile kernel
     (1, 2 and 3 k stages; a ragged last column tile).  Every output is
     checked: the float64 product of int8 matrices is the exact int32
     accumulator here, and C = ((float)acc * sa) * sb rounds each product
