@@ -410,6 +410,16 @@ struct PrefillLds {
     static_assert(8 * 16 * D <= 2 * kBuf, "output staging fits in the key buffers");
 };
 
+// e^x through the hardware exp2 (v_exp_f32).  The prefill kernel is matrix-
+// bound and this is its softmax's cost: the reference's degree-5 polynomial
+// (dev::fast_expf) spends ~10 VALU ops per weight.  The two differ by at most
+// ~1.5e-4 relative (the polynomial's own truncation error), far inside the
+// attention bar of 2e-3; the decode kernel keeps the polynomial.
+__device__ __forceinline__ float fast_exp_hw(float x)
+{
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
 // One block of PQ queries starting at q0, for (batch, head) bh.
 template <int D>
 __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64_t bh, float *lds)
@@ -500,7 +510,11 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
                 sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qf[4 * u + 3], sc[t], 0, 0, 0);
             }
         }
-        // Scores of query myq for keys kb*32 + 16t + 4g + q.
+        // Scores of query myq for keys kb*32 + 16t + 4g + q.  A block whose
+        // keys are all below every query's causal limit and kend (wave-
+        // uniform) needs no masking.
+        const bool interior = (kb + 1) * PK <= kend && qw + 15 < sq &&
+                              (!a.causal || (kb + 1) * PK - 1 <= qw + off);
         float bmax = -__builtin_inff();
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -509,8 +523,10 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
                 const uint32_t key = kb * PK + 16 * t + 4 * g + r;
                 float v = sc[t][r] * a.scale;
                 if (Mh) v += Mh[static_cast<uint64_t>(min(myq, sq - 1)) * sk + min(key, sk - 1)];
-                const bool dead = key >= kend || myq >= sq || (a.causal && key > myq + off);
-                v = dead ? -__builtin_inff() : v;
+                if (!interior) {
+                    const bool dead = key >= kend || myq >= sq || (a.causal && key > myq + off);
+                    v = dead ? -__builtin_inff() : v;
+                }
                 sc[t][r] = v;
                 bmax = fmaxf(bmax, v);
             }
@@ -518,13 +534,13 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
         const bool live = bmax != -__builtin_inff();      // else the block is skipped for this query
         const float mn = live ? fmaxf(m, bmax) : m;
-        const float alpha = (!live || m == -__builtin_inff()) ? (live ? 0.0f : 1.0f) : dev::fast_expf(m - mn);
+        const float alpha = (!live || m == -__builtin_inff()) ? (live ? 0.0f : 1.0f) : fast_exp_hw(m - mn);
         float psum = 0.0f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = (sc[t][r] == -__builtin_inff()) ? 0.0f : dev::fast_expf(sc[t][r] - mn);
+                const float p = (sc[t][r] == -__builtin_inff()) ? 0.0f : fast_exp_hw(sc[t][r] - mn);
                 sc[t][r] = p;
                 psum += p;
             }
