@@ -62,6 +62,8 @@ void TraceState::reset()
         if (r.stop) (void)hipEventDestroy(r.stop);
     }
     records.clear();
+    if (epoch) (void)hipEventDestroy(epoch);
+    epoch = nullptr;
 }
 
 void TraceState::resolve()
@@ -69,10 +71,14 @@ void TraceState::resolve()
     std::lock_guard<std::mutex> lock(mutex);
     for (auto &r : records) {
         if (r.resolved) continue;
-        float ms = 0.0f;
+        float ms = 0.0f, ms0 = 0.0f;
         if (r.start && r.stop && hipEventSynchronize(r.stop) == hipSuccess &&
             hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess)
             r.gpu_ns = static_cast<uint64_t>(static_cast<double>(ms) * 1e6);
+        else
+            (void)hipGetLastError();
+        if (epoch && r.start && hipEventElapsedTime(&ms0, epoch, r.start) == hipSuccess)
+            r.gpu_start_ns = ms0 > 0.0f ? static_cast<uint64_t>(static_cast<double>(ms0) * 1e6) : 0;
         else
             (void)hipGetLastError();
         if (r.start) (void)hipEventDestroy(r.start);
@@ -108,6 +114,42 @@ void *vnpu_stream::ensure_workspace(size_t bytes)
     VNPU_HIP(hipMalloc(&workspace, want));
     workspace_bytes = want;
     return workspace;
+}
+
+hipEvent_t vnpu_stream::acquire_event()
+{
+    if (!event_pool.empty()) {
+        hipEvent_t e = event_pool.back();
+        event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return e;
+}
+
+void vnpu_stream::resolve_timing(bool wait_all)
+{
+    size_t keep = 0;
+    for (size_t i = 0; i < batch_timing.size(); ++i) {
+        auto &pr = batch_timing[i];
+        if (!wait_all && hipEventQuery(pr.second) != hipSuccess) {
+            (void)hipGetLastError();
+            batch_timing[keep++] = pr;
+            continue;
+        }
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, pr.first, pr.second) == hipSuccess && ms > 0.0f)
+            device->kernel_ns.fetch_add(static_cast<uint64_t>(static_cast<double>(ms) * 1e6));
+        else
+            (void)hipGetLastError();
+        event_pool.push_back(pr.first);
+        event_pool.push_back(pr.second);
+    }
+    batch_timing.resize(keep);
 }
 
 void vnpu_device::raise_irq(uint32_t bits)
@@ -379,8 +421,10 @@ static void destroy_stream_obj(vnpu_stream_t *s)
     if (!s) return;
     if (s->hip) {
         (void)hipStreamSynchronize(s->hip);
+        s->resolve_timing(true);
         (void)hipStreamDestroy(s->hip);
     }
+    for (hipEvent_t e : s->event_pool) (void)hipEventDestroy(e);
     if (s->workspace) (void)hipFree(s->workspace);
     delete s;
 }
@@ -627,6 +671,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_sync(vnpu_stream_t *stream)
         std::lock_guard<std::mutex> lock(stream->mutex);
         (void)hipSetDevice(stream->device->hip_device);
         e = hipStreamSynchronize(stream->hip);
+        if (e == hipSuccess) stream->resolve_timing(true);
     }
     vnpu_device_t *d = stream->device;
     d->sync_ns.fetch_add(now_ns() - t0);
@@ -669,11 +714,19 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
         VNPU_HIP(hipSetDevice(d->hip_device));
         d->busy.fetch_add(1);
         d->active_workers.fetch_add(1);
+        if (stream->batch_timing.size() >= 256) stream->resolve_timing(false);
+        hipEvent_t batch_start = stream->acquire_event();
+        if (batch_start) (void)hipEventRecord(batch_start, stream->hip);
         for (uint64_t i = 0; i < count; ++i) {
             const vnpu_command_t &cmd = commands[i];
             const uint64_t t0 = now_ns();
             TraceRecord rec;
             if (tracing) {
+                {
+                    std::lock_guard<std::mutex> tl(d->trace.mutex);
+                    if (!d->trace.epoch && hipEventCreate(&d->trace.epoch) == hipSuccess)
+                        (void)hipEventRecord(d->trace.epoch, stream->hip);
+                }
                 if (hipEventCreate(&rec.start) == hipSuccess) (void)hipEventRecord(rec.start, stream->hip);
             }
             ExecStats st;
@@ -691,7 +744,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
                 }
             }
             const uint64_t host = now_ns() - t0;
-            d->kernel_ns.fetch_add(host);
+            d->dispatch_ns.fetch_add(host);
             const uint32_t cat = trace_category(cmd.opcode);
             if (cat == 1) d->memory_ns.fetch_add(host);
             if (cat == 2) d->sync_ns.fetch_add(host);
@@ -728,6 +781,15 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
                 d->error.store(code);
                 d->regs[VNPU_REG_ERROR / 4].store(code);
                 stream->last_error.store(code);
+            }
+        }
+        if (batch_start) {
+            hipEvent_t batch_stop = stream->acquire_event();
+            if (batch_stop) {
+                (void)hipEventRecord(batch_stop, stream->hip);
+                stream->batch_timing.emplace_back(batch_start, batch_stop);
+            } else {
+                stream->event_pool.push_back(batch_start);
             }
         }
         if (event) {
@@ -984,29 +1046,40 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_trace_dump(const vnpu_device_t *device, co
 
 VNPU_API vnpu_status_t VNPU_CALL vnpu_trace_write_chrome(const vnpu_device_t *device, const char *path)
 {
+    // The reference's Chrome trace layout (src/core/runtime.cpp:530-580):
+    // complete events named OPCODE#id with a category, timestamps relative to
+    // the first event at 1 ns resolution, args {op, unit, bytes_read,
+    // bytes_written, flops}.  Start times and durations here are the GPU's
+    // (hipEvent pairs around each command on its stream).
     if (!device || !path) return VNPU_ERR_INVALID_ARGUMENT;
     auto &tr = const_cast<vnpu_device_t *>(device)->trace;
     tr.resolve();
     std::ofstream f(path);
     if (!f) return VNPU_ERR_IO;
     std::lock_guard<std::mutex> lock(tr.mutex);
-    f << "{\"traceEvents\":[";
-    double ts = 0.0;
+    uint64_t t0 = tr.records.empty() ? 0u : tr.records[0].gpu_start_ns;
+    for (const auto &r : tr.records) t0 = std::min(t0, r.gpu_start_ns);
+    static const char *cats[] = {"compute", "memory", "sync"};
+    f << "{\n\"traceEvents\":[\n";
+    f << "{\"name\":\"process_name\",\"ph\":\"M\",\"pid\":1,\"tid\":0,\"args\":{\"name\":\"VNPU "
+      << device->info.name << "\"}}" << (tr.records.empty() ? "" : ",") << "\n";
     for (size_t i = 0; i < tr.records.size(); ++i) {
         const auto &r = tr.records[i];
-        const double dur = static_cast<double>(r.gpu_ns) / 1000.0;
-        char buf[256];
+        char buf[512];
         std::snprintf(buf, sizeof(buf),
-                      "%s{\"name\":\"%s#%llu\",\"ph\":\"X\",\"pid\":0,\"tid\":0,\"ts\":%.3f,"
-                      "\"dur\":%.3f,\"args\":{\"bytes\":%llu,\"flops\":%llu}}",
-                      i ? "," : "", vnpu_opcode_name(r.opcode),
-                      static_cast<unsigned long long>(r.id), ts, dur,
-                      static_cast<unsigned long long>(r.bytes_read + r.bytes_written),
-                      static_cast<unsigned long long>(r.flops));
+                      "{\"name\":\"%s#%llu\",\"cat\":\"%s\",\"ph\":\"X\",\"ts\":%.3f,\"dur\":%.3f,"
+                      "\"pid\":1,\"tid\":0,\"args\":{\"op\":\"%s\",\"unit\":\"%s\",\"bytes_read\":%llu,"
+                      "\"bytes_written\":%llu,\"flops\":%llu}}%s\n",
+                      vnpu_opcode_name(r.opcode), static_cast<unsigned long long>(r.id),
+                      cats[trace_category(r.opcode)], static_cast<double>(r.gpu_start_ns - t0) / 1000.0,
+                      static_cast<double>(r.gpu_ns) / 1000.0, vnpu_opcode_name(r.opcode),
+                      vnpu_unit_name(r.unit), static_cast<unsigned long long>(r.bytes_read),
+                      static_cast<unsigned long long>(r.bytes_written),
+                      static_cast<unsigned long long>(r.flops), i + 1 < tr.records.size() ? "," : "");
         f << buf;
-        ts += dur;
     }
-    f << "]}\n";
+    f << "],\n\"displayTimeUnit\":\"ns\",\"otherData\":{\"version\":\"" << vnpu_version_string()
+      << "\"}}\n";
     return f ? VNPU_OK : VNPU_ERR_IO;
 }
 

@@ -71,6 +71,7 @@ struct TraceRecord {
     uint64_t flops = 0;
     uint64_t host_ns = 0;
     uint64_t gpu_ns = 0;
+    uint64_t gpu_start_ns = 0;   // GPU start relative to the trace epoch
     bool resolved = false;
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
@@ -80,6 +81,7 @@ struct TraceState {
     std::atomic<bool> enabled{false};
     std::mutex mutex;
     std::vector<TraceRecord> records;
+    hipEvent_t epoch = nullptr;   // recorded before the first traced command
     std::string trace_file;
     void reset();
     void resolve();  // waits for and converts pending hipEvent pairs
@@ -128,6 +130,13 @@ struct vnpu_stream {
     void *workspace = nullptr;
     size_t workspace_bytes = 0;
     void *ensure_workspace(size_t bytes);
+    // GPU time of submitted batches: one hipEvent pair per batch, recorded on
+    // the stream and folded into the device's kernel time once complete.
+    // Guarded by mutex.
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> batch_timing;
+    std::vector<hipEvent_t> event_pool;
+    hipEvent_t acquire_event();
+    void resolve_timing(bool wait_all);   // adds finished pairs to kernel_ns
 };
 
 struct vnpu_device {

@@ -1,0 +1,210 @@
+"""GPU telemetry through the C ABI: device status counters, the trace summary,
+the text and Chrome-JSON traces, MMIO registers and interrupts, autotune.
+
+Semantics follow the reference runtime: status counters and the per-op byte /
+flop accounting of src/core/scheduler.cpp (execute_*), the trace layout of
+src/core/runtime.cpp:530-580, the register file and doorbell / batch-done
+interrupts of src/core/runtime.cpp:1102-1138.  Where the reference build
+(oracle/_ref, CPU) is present, the accounting is compared with it command by
+command.
+"""
+import ctypes as C
+import json
+
+import numpy as np
+import pytest
+
+from vnpu_mi355x import abi
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(20261202)
+
+
+def _reset(s):
+    assert s.lib.vnpu_device_reset(s.dev) == abi.OK
+
+
+def _commands(s):
+    """One command per hot-path opcode on fresh buffers of session s.
+    Returns (commands, keep-alive list)."""
+    M, K, N = 48, 192, 80
+    keep = []
+
+    def up(a):
+        b = s.upload(np.ascontiguousarray(a))
+        keep.append(b)
+        return b
+
+    def out(nbytes):
+        b = s.alloc(nbytes)
+        keep.append(b)
+        return b
+
+    a8 = RNG.integers(-128, 128, (M, K)).astype(np.int8)
+    b8 = RNG.integers(-128, 128, (K, N)).astype(np.int8)
+    w = s.pack(b8, K, N, scales=(RNG.random(N).astype(np.float32) + 0.5) / 127)
+    keep.append(("packed", w))
+    af, bf = RNG.standard_normal((M, K)).astype(np.float32), RNG.standard_normal((K, N)).astype(np.float32)
+    x = RNG.standard_normal((M, K)).astype(np.float32)
+    q = RNG.standard_normal((1, 2, 24, 32)).astype(np.float32)
+    cmds = [
+        s.command(abi.OP_MATMUL_I8, id=1, A=up(a8), B=w, scale_a=up(np.full(M, 0.01, np.float32)).ptr,
+                  C=out(4 * M * N), M=M, K=K, N=N),
+        s.command(abi.OP_MATMUL_F32, id=2, A=up(af), B=up(bf), bias=up(np.ones(N, np.float32)).ptr,
+                  C=up(np.ones((M, N), np.float32)), M=M, K=K, N=N, alpha=1.0, beta=0.5, epilogue=1),
+        s.command(abi.OP_RMSNORM_F32, id=3, X=up(x), W=up(np.ones(K, np.float32)).ptr, Y=out(4 * M * K),
+                  rows=M, cols=K, eps=1e-5),
+        s.command(abi.OP_SOFTMAX_F32, id=4, X=up(x), Y=out(4 * M * K), rows=M, cols=K),
+        s.command(abi.OP_SWIGLU_F32, id=5, gate=up(x), up=up(x), Y=out(4 * M * K), count=M * K),
+        s.command(abi.OP_ADD_F32, id=6, A=up(x), B=up(x), Y=out(4 * M * K), count=M * K),
+        s.command(abi.OP_QUANTIZE_I8, id=7, X=up(x), Y=out(M * K), scales=out(4 * M), rows=M, cols=K,
+                  axis=abi.QUANT_PER_ROW),
+        s.command(abi.OP_ROPE_F32, id=8, Q=up(q), K=up(q), batch=1, heads=2, q_seq=24, k_seq=24,
+                  head_dim=32),
+        s.command(abi.OP_ATTENTION_F32, id=9, Q=up(q), K=up(q), V=up(q), O=out(q.nbytes), batch=1,
+                  heads=2, seq_q=24, seq_k=24, head_dim=32, causal=1),
+    ]
+    return cmds, keep
+
+
+def _release(s, keep):
+    for b in keep:
+        if isinstance(b, tuple):
+            s.release_packed(b[1])
+        else:
+            s.free(b)
+
+
+def _status_after(s, cmds):
+    _reset(s)
+    assert s.submit(cmds) == abi.OK
+    assert s.sync() == abi.OK
+    return s.status()
+
+
+def test_status_counters_follow_the_reference_accounting(gpu):
+    M, K, N = 64, 256, 192
+    A = RNG.integers(-128, 128, (M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, (K, N)).astype(np.int8)
+    w = gpu.pack(B, K, N)
+    ba, bsa, bc = gpu.upload(A), gpu.upload(np.ones(M, np.float32)), gpu.alloc(4 * M * N)
+    cmds = [gpu.command(abi.OP_MATMUL_I8, A=ba, B=w, scale_a=bsa.ptr, C=bc, M=M, K=K, N=N)
+            for _ in range(3)]
+    st = _status_after(gpu, cmds)
+    assert st.commands_submitted == 3 and st.commands_completed == 3
+    # execute_matmul_i8 (scheduler.cpp:420-426): MK + KN + 4(N + M) read, 4MN written
+    assert st.flops == 3 * 2 * M * K * N
+    assert st.bytes_read == 3 * (M * K + K * N + 4 * (N + M))
+    assert st.bytes_written == 3 * 4 * M * N
+    assert st.kernel_time_ns > 0 and st.dispatch_time_ns > 0
+    assert st.busy == 0 and st.error == 0 and st.last_opcode == abi.OP_MATMUL_I8
+    # the GPU time of the three launches is a plausible fraction of a second
+    assert st.kernel_time_ns < 10**9
+    for b in (ba, bsa, bc):
+        gpu.free(b)
+    gpu.release_packed(w)
+
+
+def test_accounting_matches_the_reference_build(gpu, ref):
+    """Same commands on the reference runtime (CPU, built from its sources)
+    and on this backend: identical byte and flop counts per command."""
+    for i in range(9):
+        counts = []
+        for s in (ref, gpu):
+            cmds, keep = _commands(s)
+            st = _status_after(s, [cmds[i]])
+            counts.append((st.bytes_read, st.bytes_written, st.flops, st.commands_completed))
+            _release(s, keep)
+        assert counts[0] == counts[1], (int(cmds[i].opcode), counts)
+
+
+def test_trace_summary_chrome_and_text(gpu, tmp_path):
+    cmds, keep = _commands(gpu)
+    lib = gpu.lib
+    _reset(gpu)
+    assert lib.vnpu_trace_enable(gpu.dev, 1) == abi.OK
+    assert gpu.submit(cmds) == abi.OK and gpu.sync() == abi.OK
+    st = gpu.status()
+    summ = abi.TraceSummary()
+    assert lib.vnpu_trace_get_summary(gpu.dev, C.byref(summ)) == abi.OK
+    assert summ.events == len(cmds)
+    assert summ.flops == st.flops and summ.bytes_read == st.bytes_read
+    assert summ.bytes_written == st.bytes_written
+    assert summ.total_time_ns > 0 and summ.compute_time_ns == summ.total_time_ns
+    assert summ.hot_time_ns > 0 and summ.hot_opcode in (abi.OP_MATMUL_F32, abi.OP_MATMUL_I8,
+                                                         abi.OP_ATTENTION_F32, abi.OP_QUANTIZE_I8,
+                                                         abi.OP_RMSNORM_F32, abi.OP_SOFTMAX_F32,
+                                                         abi.OP_SWIGLU_F32, abi.OP_ADD_F32,
+                                                         abi.OP_ROPE_F32)
+    assert summ.achieved_gflops > 0 and summ.achieved_gbytes_s > 0
+
+    path = tmp_path / "trace.json"
+    assert lib.vnpu_trace_write_chrome(gpu.dev, str(path).encode()) == abi.OK
+    doc = json.loads(path.read_text())
+    assert doc["displayTimeUnit"] == "ns" and "version" in doc["otherData"]
+    ev = [e for e in doc["traceEvents"] if e["ph"] == "X"]
+    names = ["MATMUL_I8#1", "MATMUL_F32#2", "RMSNORM_F32#3", "SOFTMAX_F32#4", "SWIGLU_F32#5",
+             "ADD_F32#6", "QUANTIZE_I8#7", "ROPE_F32#8", "ATTENTION_F32#9"]
+    assert [e["name"] for e in ev] == names
+    assert all(e["cat"] == "compute" and e["dur"] > 0 for e in ev)
+    assert ev[0]["ts"] == 0.0
+    # one stream: GPU start times follow submission order and do not overlap
+    for e0, e1 in zip(ev, ev[1:]):
+        assert e1["ts"] >= e0["ts"] + e0["dur"] - 1e-3
+    assert sum(e["args"]["flops"] for e in ev) == st.flops
+    assert [e["args"]["op"] for e in ev] == [n.split("#")[0] for n in names]
+
+    text = tmp_path / "trace.txt"
+    assert lib.vnpu_trace_dump(gpu.dev, str(text).encode()) == abi.OK
+    assert f"events {len(cmds)}" in text.read_text()
+
+    assert lib.vnpu_trace_enable(gpu.dev, 0) == abi.OK
+    lib.vnpu_trace_reset(gpu.dev)
+    assert lib.vnpu_trace_get_summary(gpu.dev, C.byref(summ)) == abi.OK and summ.events == 0
+    _release(gpu, keep)
+
+
+def test_mmio_registers_and_interrupts(gpu):
+    lib = gpu.lib
+    dev = gpu.dev
+    lib.vnpu_mmio_read32.restype = C.c_uint32
+    lib.vnpu_mmio_write32.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32]
+    _reset(gpu)
+    fired = []
+    CB = C.CFUNCTYPE(None, C.c_void_p, C.c_uint32, C.c_void_p)
+    cb = CB(lambda d, irq, user: fired.append(irq))
+    lib.vnpu_device_set_interrupt_callback(dev, cb, None)
+    try:
+        assert lib.vnpu_mmio_read32(dev, 0x00) == 0x56504E55          # ID
+        assert lib.vnpu_mmio_read32(dev, 0x0c) & 1                    # STATUS: ready
+        lib.vnpu_mmio_write32(dev, 0x20, 0xffffffff)                  # clear IRQ_STATUS
+        assert lib.vnpu_mmio_read32(dev, 0x20) == 0
+        lib.vnpu_mmio_write32(dev, 0x1c, 1)                           # doorbell -> IRQ0
+        assert lib.vnpu_mmio_read32(dev, 0x20) & 1
+        nops = [gpu.command(abi.OP_NOP) for _ in range(5)]
+        assert gpu.submit(nops) == abi.OK and gpu.sync() == abi.OK    # batch done -> IRQ1
+        assert lib.vnpu_mmio_read32(dev, 0x20) & 2
+        assert lib.vnpu_mmio_read32(dev, 0x18) == 5                   # CMD_TAIL = submitted
+        assert lib.vnpu_mmio_read32(dev, 0x14) == 5                   # CMD_HEAD = completed
+        # the callback gets the IRQ_STATUS bits: doorbell (bit 0), batch done (bit 1)
+        assert any(v & 1 for v in fired) and any(v & 2 for v in fired)
+        lib.vnpu_mmio_write32(dev, 0x08, 2)                           # CONTROL bit 1: reset
+        assert gpu.status().commands_submitted == 0
+        assert lib.vnpu_mmio_read32(dev, 0x20) == 0
+        assert lib.vnpu_mmio_read32(dev, 0x40) == 0xffffffff          # past the register file
+    finally:
+        lib.vnpu_device_set_interrupt_callback(dev, None, None)
+
+
+def test_set_tiles_and_autotune(gpu):
+    lib = gpu.lib
+    info0 = gpu.info()
+    assert lib.vnpu_device_set_tiles(gpu.dev, 64, 32, 96) == abi.OK
+    info = gpu.info()
+    assert (info.tile_m, info.tile_k, info.tile_n) == (64, 32, 96)
+    assert lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n) == abi.OK
+    for dtype in (3, 0):  # VNPU_DTYPE_I8, VNPU_DTYPE_F32
+        res = abi.TuneResult()
+        assert lib.vnpu_autotune_gemm(gpu.dev, 256, 512, 384, 3, dtype, C.byref(res)) == abi.OK
+        assert res.best_ms > 0 and res.gflops > 0 and res.unit == abi.UNIT_GPU
+        assert res.bytes_written == 256 * 384 * 4
