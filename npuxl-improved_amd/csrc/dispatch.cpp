@@ -283,6 +283,10 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
     p.alpha = in.alpha == 0.0f ? 1.0f : in.alpha;
     p.beta = in.beta;
     p.epilogue = in.epilogue;
+    // Device tiles 128 x depth x 128 (vnpu_device_set_tiles, autotune) fix
+    // the K depth per workgroup; other tiles leave the choice automatic.
+    if (dev->tile_m.load() == 128 && dev->tile_n.load() == 128 && dev->tile_k.load() % 16 == 0)
+        p.k_split_depth = dev->tile_k.load();
 
     Stager sg(s->hip);
     p.A = sg.in(in.A, in.trans_a ? span(in.K, in.M, p.lda, 4) : span(in.M, in.K, p.lda, 4));
@@ -386,6 +390,7 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     p.Np = w->Np;
     p.scale_b = w->scales_dev;
     p.epilogue = in.epilogue;
+    p.variant = k::gemm_i8_variant_for_tiles(dev->tile_m.load(), dev->tile_k.load(), dev->tile_n.load());
     require(in.epilogue <= VNPU_EPILOGUE_GELU_ERF, "invalid matmul_i8 epilogue");
 
     Stager sg(s->hip);

@@ -23,6 +23,8 @@
 #include "kernels.hpp"
 #include "device_math.hpp"
 
+#include <algorithm>
+
 namespace vnpu {
 namespace k {
 namespace {
@@ -359,6 +361,9 @@ void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn)
 static uint32_t gemm_f32_splits(const F32Gemm &p)
 {
     if (p.ktile_state || p.cull) return 1;
+    if (p.k_split_depth >= BK && p.k_split_depth < p.K)
+        return std::min<uint32_t>(256, (p.K + p.k_split_depth - 1) / p.k_split_depth);
+    if (p.k_split_depth >= p.K) return 1;
     const uint32_t tiles = ((p.N + BN - 1) / BN) * ((p.M + BM - 1) / BM);
     uint32_t splits = 1;
     while (tiles * splits < 256 && p.K / (splits * 2) >= 64) splits *= 2;

@@ -877,13 +877,36 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tile
 
 }  // namespace
 
+uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t tile_n)
+{
+    if (tile_m == 256 && tile_k == 128 && tile_n == 256) return kI8Wide;
+    if (tile_m == 256 && tile_k == 128 && tile_n == 128) return kI8Wave8;
+    if (tile_m == 256 && tile_k == 64 && tile_n == 128) return kI8Pipe;
+    if (tile_m == 128 && tile_k == 64 && tile_n == 128) return kI8Generic;
+    return kI8Auto;
+}
+
 void gemm_i8(hipStream_t s, const I8Gemm &p)
 {
     // The zero-flag table must fit next to the staged tile (K <= 16384).
     const bool aligned = (p.K % 64 == 0) && (p.lda % 16 == 0) &&
                          (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64 &&
                          p.K <= 16384;
-    if (aligned) {
+    const bool k128 = aligned && p.K % pipe128::SK == 0;
+    const bool wide_ok = k128 && !p.zero_blocks && p.M % wide::TM == 0;
+    const uint32_t wm_ = p.M / wide::TM, wn_ = (p.N + wide::TN - 1) / wide::TN;
+    // A requested kernel that cannot take this shape falls back to the
+    // automatic choice.
+    uint32_t v = p.variant;
+    if ((v == kI8Wide && !wide_ok) || (v == kI8Wave8 && !k128) || (v == kI8Pipe && !aligned)) v = kI8Auto;
+    if (v == kI8Auto) {
+        // Dense weights, whole 256-row tiles and at least one wide tile per
+        // CU (256 CUs): the 256 x 256 tile (measured: 2048x4096x8192 57 vs
+        // 78 us, x11008 108 vs 112 us; with 128 wide tiles half the CUs idle
+        // and the 256 x 128 tile wins, 84 vs 115 us).
+        v = (wide_ok && wm_ * wn_ >= 256) ? kI8Wide : k128 ? kI8Wave8 : aligned ? kI8Pipe : kI8Generic;
+    }
+    if (v != kI8Generic) {
         static bool lds_optin = false;
         if (!lds_optin) {
             bool ok = true;
@@ -896,26 +919,22 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
                                                160 * 1024) == hipSuccess;
             lds_optin = ok;
         }
-        const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
-        const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
-        if (p.K % pipe128::SK == 0) {
-            // Dense weights, whole 256-row tiles and at least one wide tile
-            // per CU (256 CUs): the 256 x 256 tile (measured: 2048x4096x8192
-            // 57 vs 78 us, x11008 108 vs 112 us; with 128 wide tiles half the
-            // CUs idle and the 256 x 128 tile wins, 84 vs 115 us).
-            const uint32_t wm_ = p.M / wide::TM, wn_ = (p.N + wide::TN - 1) / wide::TN;
-            if (!p.zero_blocks && p.M % wide::TM == 0 && wm_ * wn_ >= 256) {
-                gemm_i8_wide<<<dim3(wm_ * wn_), kThreads, wide::kLds, s>>>(p, wm_, wn_);
-                return;
-            }
-            if (p.zero_blocks) {
-                const size_t lds = pipe128::kLds + ((p.K / 64) * pipe::kBBlocks + 15) / 16 * 16;
-                gemm_i8_k128w8<true><<<dim3(tm * tn), w8::kThreads8, lds, s>>>(p, tm, tn);
-            } else {
-                gemm_i8_k128w8<false><<<dim3(tm * tn), w8::kThreads8, pipe128::kLds, s>>>(p, tm, tn);
-            }
-            return;
+    }
+    const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
+    const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
+    switch (v) {
+    case kI8Wide:
+        gemm_i8_wide<<<dim3(wm_ * wn_), kThreads, wide::kLds, s>>>(p, wm_, wn_);
+        return;
+    case kI8Wave8:
+        if (p.zero_blocks) {
+            const size_t lds = pipe128::kLds + ((p.K / 64) * pipe::kBBlocks + 15) / 16 * 16;
+            gemm_i8_k128w8<true><<<dim3(tm * tn), w8::kThreads8, lds, s>>>(p, tm, tn);
+        } else {
+            gemm_i8_k128w8<false><<<dim3(tm * tn), w8::kThreads8, pipe128::kLds, s>>>(p, tm, tn);
         }
+        return;
+    case kI8Pipe:
         // Weights with all-zero 1 KiB blocks take the variant that skips
         // their MFMAs; dense weights the one without the flag reads.
         if (p.zero_blocks) {
@@ -925,9 +944,12 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
             gemm_i8_pipe<false><<<dim3(tm * tn), kThreads, pipe::kLds, s>>>(p, tm, tn);
         }
         return;
+    default: {
+        dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
+        gemm_i8_generic<<<grid, kThreads, 0, s>>>(p);
+        return;
     }
-    dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
-    gemm_i8_generic<<<grid, kThreads, 0, s>>>(p);
+    }
 }
 
 }  // namespace k

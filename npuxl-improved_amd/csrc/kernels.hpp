@@ -44,7 +44,15 @@ struct I8Gemm {
     uint32_t ldc = 0;
     uint32_t M = 0, N = 0, K = 0;
     uint32_t epilogue = 0;
+    uint32_t variant = 0;            // kI8*: which prefill kernel (0 = choose)
 };
+// Prefill kernels (gemm_i8.hip): a requested one that cannot take the shape
+// falls back to the automatic choice.
+enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generic = 4 };
+// vnpu_device_set_tiles / autotune: tile triples (M, K, N) that name a kernel
+// select it: 256x128x256 wide, 256x128x128 8-wave, 256x64x128 64-deep,
+// 128x64x128 generic; anything else chooses automatically.
+uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t tile_n);
 void gemv_i8(hipStream_t s, const I8Gemm &p);  // M <= 8, no MFMA
 void gemm_i8(hipStream_t s, const I8Gemm &p);  // any M, int8 MFMA
 
@@ -64,6 +72,9 @@ struct F32Gemm {
     // Per kernel-tile state derived from the cull grid: 0 compute, 1 fully
     // culled (skip the K loop), 2 mixed.  Null when cull is null.
     const uint8_t *ktile_state = nullptr;
+    // K depth per workgroup when a 128 x 128 x depth tile was requested
+    // (vnpu_device_set_tiles / autotune); 0 = choose the split automatically.
+    uint32_t k_split_depth = 0;
 };
 void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn);
 // Grids of few tiles split K over workgroups: ws holds gemm_f32_ws_bytes(p)

@@ -1084,9 +1084,15 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_trace_write_chrome(const vnpu_device_t *de
 }
 
 // ---------------------------------------------------------------------------
-// Autotune (reference autotune.cpp:153-281): times the GPU GEMM for the
-// shape with hipEvents.  The kernel tile is fixed per dtype, so the sweep has
-// one candidate; the result reports it.
+// Autotune (reference autotune.cpp:153-281): the candidates are this
+// backend's GEMM kernels, named by tile triples that vnpu_device_set_tiles
+// understands (int8: 256x128x256 wide, 256x128x128 8-wave, 256x64x128 64-deep,
+// 128x64x128 generic; f32: 128 x depth x 128 with the K depth per workgroup).
+// Each candidate the shape admits is timed on the GPU (hipEvents, best of
+// `iterations`), the baseline is the automatic choice with the tiles the
+// device had, and the fastest is written back with vnpu_device_set_tiles.
+// As in the reference, tracing is off while tuning, iterations are clamped
+// to 1..20 (0 means 3) and bytes_read counts 4-byte elements.
 // ---------------------------------------------------------------------------
 
 VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint32_t M, uint32_t K,
@@ -1095,8 +1101,18 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
 {
     if (!device || !result || !M || !K || !N) return VNPU_ERR_INVALID_ARGUMENT;
     if (dtype != VNPU_DTYPE_F32 && dtype != VNPU_DTYPE_I8) return VNPU_ERR_UNSUPPORTED;
+    if (iterations == 0) iterations = 3;
+    if (iterations > 20) iterations = 20;
     return guard([&]() -> vnpu_status_t {
         std::memset(result, 0, sizeof(*result));
+        const uint32_t orig_tm = device->tile_m.load(), orig_tk = device->tile_k.load(),
+                       orig_tn = device->tile_n.load();
+        const bool trace_was_on = device->trace.enabled.exchange(false);
+        struct Restore {
+            vnpu_device_t *d;
+            bool trace;
+            ~Restore() { d->trace.enabled.store(trace); }
+        } restore{device, trace_was_on};
         vnpu_stream_t *s = nullptr;
         vnpu_status_t rc = vnpu_stream_create(device, 0, &s);
         if (rc != VNPU_OK) return rc;
@@ -1110,6 +1126,10 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
         VNPU_HIP(hipMalloc(&A, static_cast<size_t>(M) * K * ea));
         VNPU_HIP(hipMalloc(&B, static_cast<size_t>(K) * N * ea));
         VNPU_HIP(hipMalloc(&C, static_cast<size_t>(M) * N * 4));
+        struct Free {
+            void *a, *b, *c;
+            ~Free() { (void)hipFree(a); (void)hipFree(b); (void)hipFree(c); }
+        } freer{A, B, C};
         VNPU_HIP(hipMemset(A, 1, static_cast<size_t>(M) * K * ea));
         VNPU_HIP(hipMemset(B, 1, static_cast<size_t>(K) * N * ea));
         vnpu_packed_weights_t *w = nullptr;
@@ -1133,39 +1153,72 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
             cmd.args.matmul_f32.N = N;
             cmd.args.matmul_f32.alpha = 1.0f;
         }
-        const uint32_t iters = iterations ? iterations : 3;
+        struct Pack {
+            vnpu_packed_weights_t *w;
+            ~Pack() { if (w) destroy_packed(w); }
+        } packguard{w};
+
         hipEvent_t e0, e1;
         VNPU_HIP(hipEventCreate(&e0));
         VNPU_HIP(hipEventCreate(&e1));
-        rc = vnpu_stream_submit(s, &cmd, 1, nullptr);
-        if (rc == VNPU_OK) rc = vnpu_stream_sync(s);
-        double best = 1e30;
-        for (uint32_t i = 0; rc == VNPU_OK && i < iters; ++i) {
-            VNPU_HIP(hipEventRecord(e0, s->hip));
-            rc = vnpu_stream_submit(s, &cmd, 1, nullptr);
-            VNPU_HIP(hipEventRecord(e1, s->hip));
-            if (rc == VNPU_OK) rc = vnpu_stream_sync(s);
-            float ms = 0.0f;
-            VNPU_HIP(hipEventElapsedTime(&ms, e0, e1));
-            best = std::min(best, static_cast<double>(ms));
+        auto time_tiles = [&](uint32_t tm, uint32_t tk, uint32_t tn, double &best) -> vnpu_status_t {
+            vnpu_status_t r = vnpu_device_set_tiles(device, tm, tk, tn);
+            if (r == VNPU_OK) r = vnpu_stream_submit(s, &cmd, 1, nullptr);   // warm-up
+            if (r == VNPU_OK) r = vnpu_stream_sync(s);
+            best = 1e30;
+            for (uint32_t i = 0; r == VNPU_OK && i < iterations; ++i) {
+                VNPU_HIP(hipEventRecord(e0, s->hip));
+                r = vnpu_stream_submit(s, &cmd, 1, nullptr);
+                VNPU_HIP(hipEventRecord(e1, s->hip));
+                if (r == VNPU_OK) r = vnpu_stream_sync(s);
+                float ms = 0.0f;
+                VNPU_HIP(hipEventElapsedTime(&ms, e0, e1));
+                best = std::min(best, static_cast<double>(ms));
+            }
+            return r;
+        };
+        struct Cand {
+            uint32_t tm, tk, tn;
+        };
+        std::vector<Cand> cands;
+        if (i8) {
+            if (M % 256 == 0 && K % 128 == 0) cands.push_back({256, 128, 256});
+            if (K % 128 == 0) cands.push_back({256, 128, 128});
+            if (K % 64 == 0) cands.push_back({256, 64, 128});
+            cands.push_back({128, 64, 128});
+        } else {
+            cands.push_back({128, (K + 15) / 16 * 16, 128});                 // no K split
+            for (uint32_t d = (K / 2) / 16 * 16; d >= 64; d = (d / 2) / 16 * 16) cands.push_back({128, d, 128});
+        }
+        double baseline = 0.0;
+        rc = time_tiles(orig_tm, orig_tk, orig_tn, baseline);
+        double best_ms = baseline;
+        Cand best{orig_tm, orig_tk, orig_tn};
+        for (size_t i = 0; rc == VNPU_OK && i < cands.size(); ++i) {
+            double ms = 0.0;
+            rc = time_tiles(cands[i].tm, cands[i].tk, cands[i].tn, ms);
+            if (rc == VNPU_OK && ms < best_ms) {
+                best_ms = ms;
+                best = cands[i];
+            }
         }
         (void)hipEventDestroy(e0);
         (void)hipEventDestroy(e1);
-        if (w) destroy_packed(w);
-        (void)hipFree(A);
-        (void)hipFree(B);
-        (void)hipFree(C);
-        if (rc != VNPU_OK) return rc;
-        result->tile_m = 128;
-        result->tile_k = i8 ? 64 : 16;
-        result->tile_n = 128;
+        if (rc != VNPU_OK) {
+            vnpu_device_set_tiles(device, orig_tm, orig_tk, orig_tn);
+            return rc;
+        }
+        vnpu_device_set_tiles(device, best.tm, best.tk, best.tn);
+        result->tile_m = best.tm;
+        result->tile_k = best.tk;
+        result->tile_n = best.tn;
         result->unit = VNPU_UNIT_GPU;
         result->threads = device->cu_count;
-        result->best_ms = best;
-        result->baseline_ms = best;
-        result->speedup = 1.0;
-        result->gflops = 2.0 * M * K * N / (best * 1e-3) * 1e-9;
-        result->bytes_read = static_cast<uint64_t>(M) * K * ea + static_cast<uint64_t>(K) * N * ea;
+        result->best_ms = best_ms;
+        result->baseline_ms = baseline;
+        result->speedup = best_ms > 0.0 ? baseline / best_ms : 0.0;
+        result->gflops = 2.0 * M * K * N / (best_ms * 1e-3) * 1e-9;
+        result->bytes_read = static_cast<uint64_t>(M) * K * 4 + static_cast<uint64_t>(K) * N * 4;
         result->bytes_written = static_cast<uint64_t>(M) * N * 4;
         return VNPU_OK;
     });

@@ -202,9 +202,65 @@ def test_set_tiles_and_autotune(gpu):
     assert lib.vnpu_device_set_tiles(gpu.dev, 64, 32, 96) == abi.OK
     info = gpu.info()
     assert (info.tile_m, info.tile_k, info.tile_n) == (64, 32, 96)
-    assert lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n) == abi.OK
-    for dtype in (3, 0):  # VNPU_DTYPE_I8, VNPU_DTYPE_F32
-        res = abi.TuneResult()
-        assert lib.vnpu_autotune_gemm(gpu.dev, 256, 512, 384, 3, dtype, C.byref(res)) == abi.OK
-        assert res.best_ms > 0 and res.gflops > 0 and res.unit == abi.UNIT_GPU
-        assert res.bytes_written == 256 * 384 * 4
+    try:
+        for dtype, shape in ((3, (512, 1024, 768)), (0, (256, 2048, 256))):  # VNPU_DTYPE_I8, _F32
+            res = abi.TuneResult()
+            assert lib.vnpu_autotune_gemm(gpu.dev, *shape, 3, dtype, C.byref(res)) == abi.OK
+            assert res.best_ms > 0 and res.gflops > 0 and res.unit == abi.UNIT_GPU
+            assert res.best_ms <= res.baseline_ms and res.speedup >= 1.0
+            assert res.bytes_written == shape[0] * shape[2] * 4
+            # the winner is left on the device
+            info = gpu.info()
+            assert (info.tile_m, info.tile_k, info.tile_n) == (res.tile_m, res.tile_k, res.tile_n)
+    finally:
+        assert lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n) == abi.OK
+
+
+@pytest.mark.parametrize("tiles", [(256, 128, 256), (256, 128, 128), (256, 64, 128), (128, 64, 128),
+                                   (128, 128, 64)])
+def test_forced_int8_kernels_are_bit_exact(gpu, tiles):
+    """Every int8 prefill kernel a tile triple can select gives the oracle's
+    bits (the last triple is the automatic choice)."""
+    import oracle
+    M, K, N = 512, 384, 520
+    A = RNG.integers(-128, 128, (M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, (K, N)).astype(np.int8)
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    w = gpu.pack(B, K, N, scales=sb)
+    info0 = gpu.info()
+    assert gpu.lib.vnpu_device_set_tiles(gpu.dev, *tiles) == abi.OK
+    try:
+        ba, bsa, bc = gpu.upload(A), gpu.upload(sa), gpu.alloc(4 * M * N)
+        gpu.run(abi.OP_MATMUL_I8, A=ba, B=w, scale_a=bsa.ptr, C=bc, M=M, K=K, N=N)
+        got = gpu.download(bc, np.float32, (M, N))
+        for b in (ba, bsa, bc):
+            gpu.free(b)
+    finally:
+        gpu.lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n)
+        gpu.release_packed(w)
+    want = oracle.matmul_i8(A, B, sa, sb)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("depth", [64, 256, 1024])
+def test_forced_f32_split_depths(gpu, depth):
+    import oracle
+    M, K, N = 256, 1024, 200
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    B = RNG.standard_normal((K, N)).astype(np.float32)
+    bias = RNG.standard_normal(N).astype(np.float32)
+    Cin = RNG.standard_normal((M, N)).astype(np.float32)
+    info0 = gpu.info()
+    assert gpu.lib.vnpu_device_set_tiles(gpu.dev, 128, depth, 128) == abi.OK
+    try:
+        ba, bb, bbias, bc = gpu.upload(A), gpu.upload(B), gpu.upload(bias), gpu.upload(Cin)
+        gpu.run(abi.OP_MATMUL_F32, A=ba, B=bb, bias=bbias.ptr, C=bc, M=M, K=K, N=N, alpha=1.0,
+                beta=0.5, epilogue=3)
+        got = gpu.download(bc, np.float32, (M, N))
+        for b in (ba, bb, bbias, bc):
+            gpu.free(b)
+    finally:
+        gpu.lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n)
+    want = oracle.matmul_f32(A, B, Cin, bias, M, K, N, 0, 0, 1.0, 0.5, 3, acc64=True)
+    assert oracle.rel_error(got, want) <= 1e-4
