@@ -725,6 +725,11 @@ typedef struct vnpu_speculative_result_t {
 } vnpu_speculative_result_t;
 
 VNPU_API void VNPU_CALL vnpu_speculative_config_init(vnpu_speculative_config_t *config);
+/* Implemented (reference src/cluster/cluster.cpp:552-646): gamma one-position
+ * draft calls, one verify call over gamma + 1 positions, greedy acceptance,
+ * a bonus token sampled with the reference's xorshift64 stream.  The cluster
+ * may be NULL.  The callbacks are the caller's (e.g. OP_MTP_HEAD_F32 on this
+ * device); they run on the calling thread. */
 VNPU_API vnpu_status_t VNPU_CALL vnpu_speculative_step(vnpu_cluster_t *cluster,
                                                        const vnpu_speculative_config_t *config,
                                                        const int32_t *context,

@@ -18,6 +18,8 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <vector>
+#include <limits>
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
@@ -1225,9 +1227,9 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
 }
 
 // ---------------------------------------------------------------------------
-// Multi-host cluster, remote node and speculative API: not provided by this
-// single-GPU backend (reference src/cluster/*).  Every entry point exists so
-// the ABI and the backend table are complete; each reports UNSUPPORTED.
+// Multi-host cluster and remote node API: not provided by this single-GPU
+// backend (reference src/cluster/*).  Every entry point exists so the ABI and
+// the backend table are complete; each reports UNSUPPORTED.
 // ---------------------------------------------------------------------------
 
 VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_create(const vnpu_cluster_config_t *, vnpu_cluster_t **out)
@@ -1264,11 +1266,144 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_matmul_f32(vnpu_cluster_t *, vnpu_
 }
 VNPU_API vnpu_status_t VNPU_CALL vnpu_node_run(const vnpu_node_config_t *) { return VNPU_ERR_UNSUPPORTED; }
 VNPU_API void VNPU_CALL vnpu_node_stop(void) {}
-VNPU_API vnpu_status_t VNPU_CALL vnpu_speculative_step(vnpu_cluster_t *, const vnpu_speculative_config_t *,
-                                                       const int32_t *, uint32_t, vnpu_logits_fn_t, void *,
-                                                       vnpu_logits_fn_t, void *, vnpu_speculative_result_t *)
+// ---------------------------------------------------------------------------
+// Speculative step (reference src/cluster/cluster.cpp:552-646): draft gamma
+// tokens one position at a time through draft_fn, score the gamma + 1
+// positions with one verify_fn call, accept drafts while they equal the
+// verifier's argmax (greedy acceptance, as the reference's v1), then sample a
+// bonus token from the first rejected position.  The cluster handle is
+// optional (no cluster is needed on one GPU).  The logits callbacks are the
+// caller's; on this backend they would run MTP_HEAD_F32 / SOFTMAX_F32 on the
+// GPU.  Sampling reproduces the reference's exactly: softmax weights from the
+// same exp polynomial accumulated in double, one xorshift64 draw, the first
+// index whose cumulative weight reaches u * sum.
+// ---------------------------------------------------------------------------
+namespace {
+
+float host_fast_expf(float x)
 {
-    return VNPU_ERR_UNSUPPORTED;
+    // The reference's 2^f polynomial (src/internal.h:87-108).  Unfused
+    // multiply-then-add in each Horner step, as the reference's x86-64 build
+    // evaluates it (no FMA in its target), so the sampling CDF and therefore
+    // the sampled token agree bit for bit.
+#pragma clang fp contract(off)
+    if (x < -80.0f) return 0.0f;
+    if (x > 80.0f) return std::numeric_limits<float>::infinity();
+    const float z = x * 1.4426950408889634f;
+    const float zi = std::floor(z);
+    const float f = z - zi;
+    float p = 0.0013333558146428443f;
+    p = p * f + 0.009618129107628477f;
+    p = p * f + 0.05550410866482158f;
+    p = p * f + 0.2402265069591007f;
+    p = p * f + 0.6931471805599453f;
+    p = p * f + 1.0f;
+    return std::ldexp(p, static_cast<int>(zi));
+}
+
+uint32_t argmax_finite(const float *logits, uint32_t vocab)
+{
+    uint32_t best = 0;
+    float best_v = -std::numeric_limits<float>::infinity();
+    for (uint32_t i = 0; i < vocab; ++i)
+        if (std::isfinite(logits[i]) && logits[i] > best_v) {
+            best_v = logits[i];
+            best = i;
+        }
+    return best;
+}
+
+uint64_t next_xorshift64(uint64_t &state)
+{
+    state ^= state << 13;
+    state ^= state >> 7;
+    state ^= state << 17;
+    return state;
+}
+
+int32_t draw_token(const float *logits, uint32_t vocab, float temperature, uint64_t &rng)
+{
+    if (temperature <= 0.0f) return static_cast<int32_t>(argmax_finite(logits, vocab));
+    float top = -std::numeric_limits<float>::infinity();
+    for (uint32_t i = 0; i < vocab; ++i)
+        if (std::isfinite(logits[i])) top = std::max(top, logits[i]);
+    const float inv_t = 1.0f / temperature;
+    std::vector<double> cum(vocab);
+    double total = 0.0;
+    for (uint32_t i = 0; i < vocab; ++i) {
+        total += std::isfinite(logits[i]) ? host_fast_expf((logits[i] - top) * inv_t) : 0.0f;
+        cum[i] = total;
+    }
+    if (total <= 0.0) return static_cast<int32_t>(argmax_finite(logits, vocab));
+    const double u = static_cast<double>(next_xorshift64(rng) >> 11) / static_cast<double>(1ull << 53);
+    const auto it = std::lower_bound(cum.begin(), cum.end(), u * total);
+    return static_cast<int32_t>(std::min<size_t>(static_cast<size_t>(it - cum.begin()), vocab - 1));
+}
+
+}  // namespace
+
+VNPU_API vnpu_status_t VNPU_CALL vnpu_speculative_step(vnpu_cluster_t *, const vnpu_speculative_config_t *config,
+                                                       const int32_t *context, uint32_t context_len,
+                                                       vnpu_logits_fn_t draft_fn, void *draft_user,
+                                                       vnpu_logits_fn_t verify_fn, void *verify_user,
+                                                       vnpu_speculative_result_t *result)
+{
+    if (!config || (!context && context_len) || !draft_fn || !verify_fn || !result || !config->vocab)
+        return VNPU_ERR_INVALID_ARGUMENT;
+    if (config->gamma == 0 || config->gamma >= VNPU_MAX_TOKENS) return VNPU_ERR_INVALID_ARGUMENT;
+    return guard([&]() -> vnpu_status_t {
+        std::memset(result, 0, sizeof(*result));
+        const uint32_t gamma = config->gamma, vocab = config->vocab;
+        std::vector<int32_t> seq(context, context + context_len);
+        seq.reserve(context_len + gamma + 1);
+        std::vector<int32_t> drafts(gamma);
+        std::vector<float> logits(vocab);
+        uint64_t rng = static_cast<uint64_t>(config->seed ? config->seed : 1) ^ 0x9e3779b97f4a7c15ull;
+        const uint64_t t_begin = now_ns();
+        for (uint32_t j = 0; j < gamma; ++j) {
+            const vnpu_status_t rc = draft_fn(draft_user, seq.data(), static_cast<uint32_t>(seq.size()),
+                                              context_len + j, 1, logits.data(), vocab);
+            if (rc != VNPU_OK) return rc;
+            drafts[j] = draw_token(logits.data(), vocab, config->temperature, rng);
+            seq.push_back(drafts[j]);
+        }
+        const uint64_t t_drafted = now_ns();
+        std::vector<float> scored(static_cast<size_t>(gamma + 1) * vocab, 0.0f);
+        const vnpu_status_t rc = verify_fn(verify_user, seq.data(), static_cast<uint32_t>(seq.size()),
+                                           context_len, gamma + 1, scored.data(), vocab);
+        if (rc != VNPU_OK) return rc;
+        const uint64_t t_verified = now_ns();
+        uint32_t accepted = 0;
+        while (accepted < gamma &&
+               static_cast<int32_t>(argmax_finite(scored.data() + static_cast<size_t>(accepted) * vocab,
+                                                  vocab)) == drafts[accepted])
+            ++accepted;
+        const int32_t bonus = draw_token(scored.data() + static_cast<size_t>(accepted) * vocab, vocab,
+                                         config->temperature, rng);
+        const uint32_t produced = accepted + 1;
+        const uint32_t limit = config->max_tokens ? std::min(config->max_tokens, produced) : produced;
+        for (uint32_t j = 0; j < limit; ++j) result->tokens[j] = j < accepted ? drafts[j] : bonus;
+        result->accepted = std::min(accepted, limit);
+        result->produced = limit;
+        for (uint32_t j = 0; j < limit; ++j)
+            if (result->tokens[j] == static_cast<int32_t>(config->eos_token)) {
+                result->produced = j + 1;
+                result->accepted = std::min(result->accepted, j + 1);
+                result->eos = 1;
+                break;
+            }
+        const double draft_ms = static_cast<double>(t_drafted - t_begin) / 1e6;
+        const double verify_ms = static_cast<double>(t_verified - t_drafted) / 1e6;
+        const double total_ms = static_cast<double>(now_ns() - t_begin) / 1e6;
+        result->draft_time_ms = draft_ms;
+        result->verify_time_ms = verify_ms;
+        result->total_time_ms = total_ms;
+        result->tokens_per_second = total_ms > 0.0 ? result->produced * 1000.0 / total_ms : 0.0;
+        // produced tokens per (one verify + gamma drafts), in verify units
+        result->theoretical_speedup =
+            result->produced / (1.0 + gamma * (draft_ms / gamma) / std::max(verify_ms, 1e-6));
+        return VNPU_OK;
+    });
 }
 
 // ---------------------------------------------------------------------------

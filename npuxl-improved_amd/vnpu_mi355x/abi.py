@@ -94,6 +94,27 @@ class TuneResult(C.Structure):
                 ("bytes_read", C.c_uint64), ("bytes_written", C.c_uint64)]
 
 
+MAX_TOKENS = 64  # VNPU_MAX_TOKENS (vnpu.h)
+
+
+class SpeculativeConfig(C.Structure):
+    _fields_ = [("abi_version", C.c_uint32), ("gamma", C.c_uint32), ("vocab", C.c_uint32),
+                ("max_tokens", C.c_uint32), ("eos_token", C.c_uint32), ("flags", C.c_uint32),
+                ("temperature", C.c_float), ("seed", C.c_uint32)]
+
+
+class SpeculativeResult(C.Structure):
+    _fields_ = [("accepted", C.c_uint32), ("produced", C.c_uint32), ("eos", C.c_uint32),
+                ("tokens", C.c_int32 * MAX_TOKENS), ("draft_time_ms", C.c_double),
+                ("verify_time_ms", C.c_double), ("total_time_ms", C.c_double),
+                ("tokens_per_second", C.c_double), ("theoretical_speedup", C.c_double)]
+
+
+# vnpu_logits_fn_t(user, tokens, num_tokens, first_position, num_positions, logits, vocab)
+LOGITS_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_int32), C.c_uint32, C.c_uint32,
+                        C.c_uint32, C.POINTER(C.c_float), C.c_uint32)
+
+
 class MatmulF32Args(C.Structure):
     _fields_ = [("A", C.c_void_p), ("B", C.c_void_p), ("bias", C.c_void_p), ("C", C.c_void_p),
                 ("M", C.c_uint32), ("K", C.c_uint32), ("N", C.c_uint32),
@@ -277,7 +298,7 @@ SIGNATURES = {
     "vnpu_node_run": (st, [vp]),
     "vnpu_node_stop": (None, []),
     "vnpu_speculative_config_init": (None, [vp]),
-    "vnpu_speculative_step": (st, [vp, vp, vp, u32, vp, vp, vp, vp, vp]),
+    "vnpu_speculative_step": (st, [vp, vp, vp, u32, LOGITS_FN, vp, LOGITS_FN, vp, vp]),
     "vnpu_float_to_bf16": (C.c_uint16, [f32]),
     "vnpu_float_to_f16": (C.c_uint16, [f32]),
     "vnpu_bf16_to_float": (f32, [C.c_uint16]),
@@ -291,7 +312,7 @@ SIGNATURES = {
 LAYOUT = {  # LP64 sizes measured on the reference header
     Command: 208, MatmulF32Args: 104, MatmulI8Args: 72, AttentionArgs: 88, RopeArgs: 64,
     QuantizeArgs: 48, Config: 48, DeviceInfo: 304, DeviceStatus: 152, TraceSummary: 112,
-    TuneResult: 72,
+    TuneResult: 72, SpeculativeConfig: 32, SpeculativeResult: 312,
 }
 
 
