@@ -356,35 +356,131 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
 }
 
 // ---------------------------------------------------------------------------
-// Prefill kernel on the f32 matrix cores (head_dim 64 or 128, seq_q > 4).
+// Prefill (head_dim 64 or 128, seq_q > 4) on the bf16 matrix cores with
+// three-term split products.
 //
-// A workgroup of 8 waves owns 128 queries of one (batch, head); wave w owns
-// queries q0 + 16w .. +15 (two waves per SIMD).  Keys stream through LDS in
-// blocks of 32, double buffered and filled by 16-byte DMA of whole rows: V as
-// [key][d], K as [key][d] with 16-byte chunk c of key k at slot c ^ k (mod the
-// chunks per row).  Per block each wave runs v_mfma_f32_16x16x4_f32:
-//   S^T (16 keys x 16 queries, two tiles) = K . Q^T   (Q^T in VGPRs)
-//   O^T (D x 16 queries)                += V^T . P^T
-// Index maps chosen so every lane's operands are contiguous (one
-// ds_read_b128 feeds four MFMAs):
-//   * QK step st of lane group g = l/16 sums d = (D/4)g + st, so a lane reads
-//     its key's K row in 16-byte chunks (the swizzle keeps the 16 keys of a
-//     quarter wave in distinct banks) and holds Q[q][(D/4)g .. +D/4];
-//   * O^T tile dt, row i stands for d = 64(dt/4) + 4i + dt%4, so one chunk of
-//     a V row feeds four tiles;
-//   * the accumulator layout puts query l%16 and keys 4g + q of a tile in
-//     lane l, so a query's block max and sum combine four lanes (l^16, l^32),
-//     and the P^T operand of PV step s of tile t is the lane's own score
-//     register s when that product's key order is 16t + 4g + s.
+// gfx950 multiplies bf16 ~11x faster than f32 on its matrix cores (measured
+// with random operands: v_mfma_f32_32x32x16_bf16 1.8 PFLOP/s against
+// v_mfma_f32_16x16x4_f32 157 TFLOP/s).  Every f32 operand x is split into
+// hi = bf16(x) and lo = bf16(x - hi) (x - hi is exact in f32), and a product
+// is taken as hi*hi + hi*lo + lo*hi with f32 accumulation: the dropped lo*lo
+// term and the rounding of lo leave a relative error of about 2^-16 per
+// product, far inside the attention bar of 2e-3 (the f32 kernel's own
+// softmax exponent differs from the reference's by 1.5e-4).
+//
+// A pre-pass (attn_split_kv) writes K and V of every 32-key block, split and
+// laid out for the fragment reads, as one contiguous 32 KiB (D = 128) block:
+//   K hi | K lo : [key][d] bf16, 16-byte chunk c of key k at slot c ^ (k % C)
+//                 (C = chunks per row), so 8 lanes reading 8 keys at one d
+//                 offset hit distinct banks;
+//   V^T hi | lo : [d][position] bf16, 32 positions per row in the key order
+//                 that the PV step consumes (vt_key), chunk c of row d at
+//                 slot c ^ ((d >> 1) & 3).
+// Keys past seq_k are written as zeros (their scores are masked anyway).
+//
+// Main kernel: a workgroup of 8 waves owns 128 queries of one (batch, head):
+// waves w and w+4 own queries q0 + 32(w%4) .. +31 and take the even and the
+// odd 32-key blocks of every 64-key super block (two waves per SIMD, one
+// barrier per super block, the next super block's 64 KiB in flight by DMA
+// while this one is multiplied).  Per 32-key block a wave runs
+// v_mfma_f32_32x32x16_bf16:
+//   S^T (32 keys x 32 queries) = K . Q^T      (Q^T hi/lo in VGPRs)
+//   O^T (D x 32 queries)      += V^T . P^T    (P^T from the lane's scores)
+// The 32 x 32 accumulator puts query l%32 and keys 8j + 4(l/32) + i
+// (register 4j + i) in lane l, so a query's block max and sum combine two
+// lanes (l, l^32), and the PV step over keys 16t..16t+15 takes the lane's
+// score registers 8t..8t+7 as its P^T operand when V^T's positions follow
+// the same key order.  The two key halves are merged through LDS at the end,
+// O leaves through LDS so every global row write is coalesced.
 // Online softmax as in the reference (a query whose block is fully masked
-// skips the block), with the reference's fast_expf.  Keys past the range are
-// clamped to a valid row and masked in the scores.  O leaves through LDS so
-// every global row write is coalesced.
+// skips the block).
 // ---------------------------------------------------------------------------
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+constexpr int XQ = 32;           // queries per wave
+constexpr int XK = 32;           // keys per block
 constexpr int PQ = 128;          // queries per workgroup
-constexpr int PK = 32;           // keys per block
-constexpr int PThreads = 512;    // 8 waves
+constexpr int PThreads = 512;    // 8 waves: 4 query groups x 2 key halves
+
+template <int D>
+struct SplitBlk {
+    static constexpr int kHalfK = XK * D * 2;                    // bytes of K hi (or lo)
+    static constexpr int kHalfV = D * XK * 2;                    // bytes of V^T hi (or lo)
+    static constexpr int kVOff = 2 * kHalfK;
+    static constexpr int kBytes = 2 * kHalfK + 2 * kHalfV;       // one 32-key block
+    static constexpr int kChunks = D / 8;                        // 16-byte chunks per K row
+    static constexpr size_t kLds = 4 * static_cast<size_t>(kBytes);  // 2 super blocks of 2 blocks
+    static constexpr int kOPitch = D + 4;                        // floats per staged row
+    static_assert(4 * XQ * kOPitch * 4 + 4 * XQ * 2 * 4 <= static_cast<int>(kLds), "merge staging fits");
+};
+
+// Key (within its 32-key block) at V^T position p: the PV step t = p/16 of
+// lane half h = (p/8)%2 multiplies element e = p%8 with the lane's score
+// register 8t + e, which holds key 16t + 4h + e (e < 4) or 16t + 8 + 4h +
+// e - 4 (e >= 4).
+__device__ __forceinline__ uint32_t vt_key(uint32_t p)
+{
+    const uint32_t t = p >> 4, h = (p >> 3) & 1, e = p & 7;
+    return 16 * t + (e < 4 ? 4 * h + e : 8 + 4 * h + (e - 4));
+}
+
+__device__ __forceinline__ void split_bf16(const float (&x)[8], v8bf &hi, v8bf &lo)
+{
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        hi[e] = static_cast<__bf16>(x[e]);
+        lo[e] = static_cast<__bf16>(x[e] - static_cast<float>(hi[e]));
+    }
+}
+
+// One (32-key block, batch*head) per workgroup of 256 threads.
+template <int D>
+__global__ __launch_bounds__(256) void attn_split_kv(Attn a, uint32_t nkb, int8_t *split)
+{
+    using S = SplitBlk<D>;
+    constexpr int C = S::kChunks;
+    const uint32_t kb = blockIdx.x;
+    const uint64_t bh = blockIdx.y;
+    const uint32_t sk = a.seq_k;
+    int8_t *blk = split + (bh * nkb + kb) * S::kBytes;
+    const float *Kh = a.K + bh * sk * D;
+    const float *Vh = a.V + bh * sk * D;
+    for (uint32_t it = threadIdx.x; it < XK * C; it += 256) {
+        const uint32_t key = it / C, c = it % C;
+        const uint32_t gk = kb * XK + key;
+        float x[8];
+        if (gk < sk) {
+            const float4 *src = reinterpret_cast<const float4 *>(Kh + static_cast<uint64_t>(gk) * D + 8 * c);
+            const float4 u = src[0], v = src[1];
+            x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+            x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+        }
+        v8bf hi, lo;
+        split_bf16(x, hi, lo);
+        const uint32_t off = key * (D * 2) + ((c ^ (key & (C - 1))) << 4);
+        *reinterpret_cast<v8bf *>(blk + off) = hi;
+        *reinterpret_cast<v8bf *>(blk + S::kHalfK + off) = lo;
+    }
+    // V^T: lanes take consecutive d, so each key's reads are coalesced.
+    for (uint32_t it = threadIdx.x; it < 4 * D; it += 256) {
+        const uint32_t d = it % D, ch = it / D;
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t gk = kb * XK + vt_key(8 * ch + e);
+            x[e] = gk < sk ? Vh[static_cast<uint64_t>(gk) * D + d] : 0.0f;
+        }
+        v8bf hi, lo;
+        split_bf16(x, hi, lo);
+        const uint32_t off = d * (XK * 2) + ((ch ^ ((d >> 1) & 3)) << 4);
+        *reinterpret_cast<v8bf *>(blk + S::kVOff + off) = hi;
+        *reinterpret_cast<v8bf *>(blk + S::kVOff + S::kHalfV + off) = lo;
+    }
+}
 
 // 16-byte-per-lane global->LDS copy (lane l writes lds_dst + 16 l bytes).
 // Written as asm on purpose: for the builtin form the compiler cannot tell the
@@ -392,198 +488,221 @@ constexpr int PThreads = 512;    // 8 waves
 // vmcnt(0) before the first ds_read of every block, which serialises the copy
 // with the compute.  The kernel's own vmcnt(0) + barrier at the top of each
 // key block is what orders the copy before its readers.
-__device__ __forceinline__ void lds_dma16(const void *src, float *lds_dst)
+__device__ __forceinline__ void lds_dma16(const void *src, int8_t *lds_dst)
 {
     const uint32_t lds = static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) float *)(lds_dst)));
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(lds_dst)));
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :
                  : "v"(src), "s"(lds)
                  : "memory", "m0");
 }
 
-template <int D>
-struct PrefillLds {
-    static constexpr int kK = PK * D;            // floats
-    static constexpr int kBuf = 2 * PK * D;      // K + V
-    static constexpr size_t kBytes = static_cast<size_t>(2 * kBuf) * 4;
-    static_assert(8 * 16 * D <= 2 * kBuf, "output staging fits in the key buffers");
-};
-
-// e^x through the hardware exp2 (v_exp_f32).  The prefill kernel is matrix-
-// bound and this is its softmax's cost: the reference's degree-5 polynomial
-// (dev::fast_expf) spends ~10 VALU ops per weight.  The two differ by at most
-// ~1.5e-4 relative (the polynomial's own truncation error), far inside the
-// attention bar of 2e-3; the decode kernel keeps the polynomial.
+// e^x through the hardware exp2 (v_exp_f32).  The reference's degree-5
+// polynomial (dev::fast_expf) spends ~10 VALU ops per weight; the two differ
+// by at most ~1.5e-4 relative (the polynomial's own truncation error), far
+// inside the attention bar of 2e-3; the decode kernel keeps the polynomial.
 __device__ __forceinline__ float fast_exp_hw(float x)
 {
     return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
+__device__ __forceinline__ v16f mfma_bf16(const v8bf &a, const v8bf &b, const v16f &c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
 // One block of PQ queries starting at q0, for (batch, head) bh.
 template <int D>
-__device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64_t bh, float *lds)
+__device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64_t bh, uint32_t nkb,
+                                              const int8_t *split, int8_t *lds)
 {
-    using L = PrefillLds<D>;
-    constexpr int NS = D / 4;          // QK MFMA steps per tile (4 d each)
-    constexpr int NCH = D / 4;         // 16-byte chunks per row
-    constexpr int DT = D / 16;         // 16-wide d tiles of O^T
-    constexpr int HI = DT / 4;         // V chunks read per key
+    using S = SplitBlk<D>;
+    constexpr int NS = D / 16;          // QK steps (16 d each)
+    constexpr int DT = D / 32;          // 32-row tiles of O^T
+    constexpr int C = S::kChunks;
+    constexpr int kInstr = 2 * S::kBytes / 1024;   // DMA instructions per super block
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 4, qc = lane & 15;
+    const int wq = wave & 3, wk = wave >> 2;
+    const int h = lane >> 5, col = lane & 31;
     const uint32_t sq = a.seq_q, sk = a.seq_k;
     const uint32_t off = sk > sq ? sk - sq : 0;
-    const float *Kh = a.K + bh * sk * D;
-    const float *Vh = a.V + bh * sk * D;
     const float *Mh = a.mask ? a.mask + bh * sq * sk : nullptr;
-    const uint32_t qw = q0 + wave * 16;                      // this wave's first query
-    const uint32_t myq = qw + qc;                            // this lane's query
+    const uint32_t qw = q0 + wq * XQ;                         // this wave's first query
+    const uint32_t myq = qw + col;                            // this lane's query
+    const int8_t *src = split + bh * nkb * S::kBytes;
 
     uint32_t kend = sk;
     if (a.causal) kend = min(sk, min(q0 + PQ, sq) - 1 + off + 1);
-    const uint32_t nblk = (kend + PK - 1) / PK;
-    const uint32_t wave_kend = a.causal ? min(kend, min(qw + 16, sq) - 1 + off + 1) : kend;
+    const uint32_t nblk = (kend + XK - 1) / XK;
+    const uint32_t nsb = (nblk + 1) / 2;
+    const uint32_t wave_kend = a.causal ? min(kend, min(qw + XQ, sq) - 1 + off + 1) : kend;
 
-    // Q^T operand: lane (query qc, group g) holds Q[myq][NS*g .. NS*g + NS).
-    float qf[NS];
+    // Q^T operand of step s: lane (query col, half h) holds d = 16s + 8h .. +8.
+    v8bf qh[NS], ql[NS];
     {
-        const float4 *qrow = reinterpret_cast<const float4 *>(a.Q + (bh * sq + min(myq, sq - 1)) * D + NS * g);
+        const float4 *qrow = reinterpret_cast<const float4 *>(a.Q + (bh * sq + min(myq, sq - 1)) * D + 8 * h);
 #pragma unroll
-        for (int u = 0; u < NS / 4; ++u) {
-            const float4 v = qrow[u];
-            qf[4 * u] = v.x;
-            qf[4 * u + 1] = v.y;
-            qf[4 * u + 2] = v.z;
-            qf[4 * u + 3] = v.w;
+        for (int s = 0; s < NS; ++s) {
+            const float4 u = qrow[4 * s], v = qrow[4 * s + 1];
+            const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+            split_bf16(x, qh[s], ql[s]);
         }
     }
 
-    // DMA of key block kb into buffer buf: K and V, 16-byte chunks, 64 per
-    // instruction, PK*NCH/64 instructions each, spread over the 8 waves.
-    auto issue = [&](uint32_t kb, int buf) {
-        float *ks = lds + buf * L::kBuf;
-        float *vs = ks + L::kK;
-        constexpr int kInstr = PK * NCH / 64;
+    // DMA of super block sb (blocks 2sb, 2sb+1) into ring slot sb%2; waves
+    // 0-3 copy the even block, 4-7 the odd one (skipped past nblk).
+    auto issue = [&](uint32_t sb) {
+        const uint32_t blk = 2 * sb + wk;
+        if (blk >= nblk) return;                                  // wave-uniform
+        int8_t *dst = lds + (sb & 1) * 2 * S::kBytes + wk * S::kBytes;
+        const int8_t *from = src + static_cast<uint64_t>(blk) * S::kBytes + lane * 16;
 #pragma unroll
         for (int i = 0; i < kInstr / 8; ++i) {
-            const int ins = wave * (kInstr / 8) + i;
-            const uint32_t f = ins * 64 + lane;              // chunk slot in the block
-            const uint32_t k = f / NCH, slot = f % NCH;
-            const uint32_t key = min(kb * PK + k, kend - 1);
-            const uint32_t c = slot ^ (k & (NCH - 1));       // K chunk stored in this slot
-            lds_dma16(Kh + static_cast<uint64_t>(key) * D + 4 * c, ks + ins * 256);
-            lds_dma16(Vh + static_cast<uint64_t>(key) * D + 4 * slot, vs + ins * 256);
+            const int ins = wq * (kInstr / 8) + i;                // 1 KiB piece of the block
+            lds_dma16(from + ins * 1024, dst + ins * 1024);
         }
     };
-    if (nblk) issue(0, 0);
+    if (nsb) issue(0);
 
-    v4f o[DT];
+    v16f o[DT];
 #pragma unroll
-    for (int t = 0; t < DT; ++t) o[t] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < DT; ++t) o[t] = (v16f){0.f};
     float m = -__builtin_inff(), l = 0.0f;
 
-    for (uint32_t kb = 0; kb < nblk; ++kb) {
-        const int buf = kb & 1;
-        __builtin_amdgcn_s_waitcnt(0xF70);   // vmcnt(0): this wave's DMA of block kb
-        __syncthreads();                     // block kb landed everywhere; block kb-1's buffer free
-        if (kb + 1 < nblk) issue(kb + 1, buf ^ 1);
-        if (kb * PK >= wave_kend) continue;  // wave-uniform: past this wave's causal limit
-        const float *ks = lds + buf * L::kBuf;
-        const float *vs = ks + L::kK;
+    for (uint32_t sb = 0; sb < nsb; ++sb) {
+        __builtin_amdgcn_s_waitcnt(0xF70);   // vmcnt(0): this wave's DMA of super block sb
+        __syncthreads();                     // landed everywhere; super block sb-1's slot free
+        if (sb + 1 < nsb) issue(sb + 1);
+        const uint32_t kb = 2 * sb + wk;
+        if (kb * XK >= wave_kend) continue;  // wave-uniform: past this wave's causal limit
+        const int8_t *blk = lds + (sb & 1) * 2 * S::kBytes + wk * S::kBytes;
 
-        // S^T tiles (keys 16t + row) = K . Q^T
-        v4f sc[2];
+        // S^T = K . Q^T: hi*hi on one chain, the two cross terms on another.
+        v16f s0 = (v16f){0.f}, s1 = (v16f){0.f};
+        const int8_t *krow = blk + col * (D * 2);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int kk = 16 * t + qc;
-            const float *krow = ks + kk * D;
-            sc[t] = (v4f){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int u = 0; u < NS / 4; ++u) {
-                const int c = (NS / 4) * g + u;
-                const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * (c ^ (kk & (NCH - 1))));
-                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qf[4 * u + 0], sc[t], 0, 0, 0);
-                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qf[4 * u + 1], sc[t], 0, 0, 0);
-                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qf[4 * u + 2], sc[t], 0, 0, 0);
-                sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qf[4 * u + 3], sc[t], 0, 0, 0);
-            }
+        for (int s = 0; s < NS; ++s) {
+            const uint32_t koff = ((2 * s + h) ^ (col & (C - 1))) << 4;
+            const v8bf kh = *reinterpret_cast<const v8bf *>(krow + koff);
+            const v8bf kl = *reinterpret_cast<const v8bf *>(krow + S::kHalfK + koff);
+            s1 = mfma_bf16(kl, qh[s], s1);
+            s0 = mfma_bf16(kh, qh[s], s0);
+            s1 = mfma_bf16(kh, ql[s], s1);
         }
-        // Scores of query myq for keys kb*32 + 16t + 4g + q.  A block whose
-        // keys are all below every query's causal limit and kend (wave-
-        // uniform) needs no masking.
-        const bool interior = (kb + 1) * PK <= kend && qw + 15 < sq &&
-                              (!a.causal || (kb + 1) * PK - 1 <= qw + off);
+        // Scores of query myq for keys kb*32 + 8j + 4h + i (register 4j + i).
+        // A block whose keys are all below every query's causal limit and
+        // kend (wave-uniform) needs no masking.
+        const bool interior = (kb + 1) * XK <= kend && qw + XQ - 1 < sq &&
+                              (!a.causal || (kb + 1) * XK - 1 <= qw + off);
+        float sc[16];
         float bmax = -__builtin_inff();
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t key = kb * PK + 16 * t + 4 * g + r;
-                float v = sc[t][r] * a.scale;
-                if (Mh) v += Mh[static_cast<uint64_t>(min(myq, sq - 1)) * sk + min(key, sk - 1)];
-                if (!interior) {
-                    const bool dead = key >= kend || myq >= sq || (a.causal && key > myq + off);
-                    v = dead ? -__builtin_inff() : v;
-                }
-                sc[t][r] = v;
-                bmax = fmaxf(bmax, v);
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t key = kb * XK + 8 * (r >> 2) + 4 * h + (r & 3);
+            float v = (s0[r] + s1[r]) * a.scale;
+            if (Mh) v += Mh[static_cast<uint64_t>(min(myq, sq - 1)) * sk + min(key, sk - 1)];
+            if (!interior) {
+                const bool dead = key >= kend || myq >= sq || (a.causal && key > myq + off);
+                v = dead ? -__builtin_inff() : v;
             }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+            sc[r] = v;
+            bmax = fmaxf(bmax, v);
+        }
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
         const bool live = bmax != -__builtin_inff();      // else the block is skipped for this query
         const float mn = live ? fmaxf(m, bmax) : m;
         const float alpha = (!live || m == -__builtin_inff()) ? (live ? 0.0f : 1.0f) : fast_exp_hw(m - mn);
         float psum = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float p = (sc[t][r] == -__builtin_inff()) ? 0.0f : fast_exp_hw(sc[t][r] - mn);
-                sc[t][r] = p;
-                psum += p;
-            }
-        psum += __shfl_xor(psum, 16, 64);
+        for (int r = 0; r < 16; ++r) {
+            const float p = (sc[r] == -__builtin_inff()) ? 0.0f : fast_exp_hw(sc[r] - mn);
+            sc[r] = p;
+            psum += p;
+        }
         psum += __shfl_xor(psum, 32, 64);
         m = mn;
         l = l * alpha + psum;
 #pragma unroll
         for (int t = 0; t < DT; ++t) o[t] *= alpha;
-        // O^T += V^T . P^T, key 16t + 4g + st: P^T is the lane's register st;
-        // tile dt row qc is d = 64(dt/4) + 4qc + dt%4.
+
+        // O^T += V^T . P^T over keys 16t..16t+15: P^T = score registers 8t..8t+7.
+        v8bf ph[2], pl[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t) {
+            const float x[8] = {sc[8 * t], sc[8 * t + 1], sc[8 * t + 2], sc[8 * t + 3],
+                                sc[8 * t + 4], sc[8 * t + 5], sc[8 * t + 6], sc[8 * t + 7]};
+            split_bf16(x, ph[t], pl[t]);
+        }
+        const int8_t *vt = blk + S::kVOff;
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const float *vrow = vs + (16 * t + 4 * g + st) * D + 4 * qc;
+        for (int t = 0; t < 2; ++t) {
+            v8bf vh[DT], vl[DT];
 #pragma unroll
-                for (int hi = 0; hi < HI; ++hi) {
-                    const float4 vv = *reinterpret_cast<const float4 *>(vrow + 64 * hi);
-                    o[4 * hi + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sc[t][st], o[4 * hi + 0], 0, 0, 0);
-                    o[4 * hi + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sc[t][st], o[4 * hi + 1], 0, 0, 0);
-                    o[4 * hi + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sc[t][st], o[4 * hi + 2], 0, 0, 0);
-                    o[4 * hi + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sc[t][st], o[4 * hi + 3], 0, 0, 0);
-                }
+            for (int dt = 0; dt < DT; ++dt) {
+                const uint32_t d = 32 * dt + col;
+                const uint32_t voff = d * (XK * 2) + (((2 * t + h) ^ ((d >> 1) & 3)) << 4);
+                vh[dt] = *reinterpret_cast<const v8bf *>(vt + voff);
+                vl[dt] = *reinterpret_cast<const v8bf *>(vt + S::kHalfV + voff);
             }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] = mfma_bf16(vl[dt], ph[t], o[dt]);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] = mfma_bf16(vh[dt], pl[t], o[dt]);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] = mfma_bf16(vh[dt], ph[t], o[dt]);
+        }
     }
 
-    // O = O^T / l through LDS (the key buffers): this wave's 16 x D tile; the
-    // lane holds query qc, d = 64(dt/4) + 16g + 4r + dt%4 (register r of tile
-    // dt); column c of row q stored at c ^ q (distinct banks per register).
+    // Merge the two key halves: waves 4-7 stage (m, l, O^T) in LDS, waves 0-3
+    // combine them with their own, normalise, and stage O row-major; then all
+    // waves write the 128 rows.  Lane (query col, half h) holds O^T rows
+    // d = 32dt + 8j + 4h + i in register 4j + i of tile dt: one float4 per
+    // (dt, j), stored at row col of the wave's [32][D + 4] tile.
     __syncthreads();
-    float *ot = lds + wave * 16 * D;
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float *ot = reinterpret_cast<float *>(lds) + wq * XQ * S::kOPitch;
+    float *ml = reinterpret_cast<float *>(lds) + 4 * XQ * S::kOPitch + wq * XQ * 2;
+    if (wk == 1) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            ot[qc * D + ((64 * (dt >> 2) + 16 * g + 4 * r + (dt & 3)) ^ qc)] = o[dt][r] * inv;
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<v4f *>(ot + col * S::kOPitch + 32 * dt + 8 * j + 4 * h) =
+                    (v4f){o[dt][4 * j], o[dt][4 * j + 1], o[dt][4 * j + 2], o[dt][4 * j + 3]};
+        if (h == 0) {
+            ml[2 * col] = m;
+            ml[2 * col + 1] = l;
+        }
+    }
     __syncthreads();
-    for (int i = lane; i < 16 * D; i += 64) {
-        const uint32_t row = i / D, col = i % D;
-        const uint32_t q = qw + row;
-        if (q < sq) a.O[(bh * sq + q) * D + col] = ot[row * D + (col ^ row)];
+    if (wk == 0) {
+        const float m1 = ml[2 * col], l1 = ml[2 * col + 1];
+        const float M = fmaxf(m, m1);
+        const float a0 = m == -__builtin_inff() ? 0.0f : fast_exp_hw(m - M);
+        const float a1 = m1 == -__builtin_inff() ? 0.0f : fast_exp_hw(m1 - M);
+        const float L = a0 * l + a1 * l1;
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const float w0 = a0 * inv, w1 = a1 * inv;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v4f *p = reinterpret_cast<v4f *>(ot + col * S::kOPitch + 32 * dt + 8 * j + 4 * h);
+                const v4f other = *p;
+                *p = (v4f){o[dt][4 * j] * w0 + other[0] * w1, o[dt][4 * j + 1] * w0 + other[1] * w1,
+                           o[dt][4 * j + 2] * w0 + other[2] * w1, o[dt][4 * j + 3] * w0 + other[3] * w1};
+            }
+    }
+    __syncthreads();
+    const float *stage = reinterpret_cast<const float *>(lds);
+    for (uint32_t i = tid; i < PQ * D / 4; i += PThreads) {
+        const uint32_t row = i / (D / 4), c4 = i % (D / 4);
+        const uint32_t q = q0 + row;
+        if (q < sq)
+            *reinterpret_cast<v4f *>(a.O + (bh * sq + q) * D + 4 * c4) =
+                *reinterpret_cast<const v4f *>(stage + row * S::kOPitch + 4 * c4);
     }
 }
 
@@ -593,15 +712,16 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
 // grid otherwise runs as long as its last, heaviest block).  Without a
 // causal mask every block costs the same and each workgroup takes one.
 template <int D>
-__global__ __launch_bounds__(PThreads) void attn_prefill_kernel(Attn a, uint32_t nqb)
+__global__ __launch_bounds__(PThreads) void attn_prefill_kernel(Attn a, uint32_t nqb, uint32_t nkb,
+                                                                const int8_t *split)
 {
-    extern __shared__ __attribute__((aligned(16))) float lds[];
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
     const uint64_t bh = blockIdx.y;
     const uint32_t heavy = nqb - 1 - blockIdx.x;
-    prefill_block<D>(a, heavy * PQ, bh, lds);
+    prefill_block<D>(a, heavy * PQ, bh, nkb, split, lds);
     if (gridDim.x < nqb && blockIdx.x != heavy) {
         __syncthreads();  // the output staging of the first block is read out
-        prefill_block<D>(a, blockIdx.x * PQ, bh, lds);
+        prefill_block<D>(a, blockIdx.x * PQ, bh, nkb, split, lds);
     }
 }
 
@@ -697,6 +817,12 @@ size_t attention_ws_bytes(const Attn &a)
 {
     uint32_t qb, splits, kps;
     plan(a, qb, splits, kps);
+    if (use_prefill(a)) {
+        // the split K / V^T blocks of the bf16 prefill kernel
+        const uint64_t nkb = (a.seq_k + XK - 1) / XK;
+        const uint64_t blk = a.head_dim == 128 ? SplitBlk<128>::kBytes : SplitBlk<64>::kBytes;
+        return static_cast<size_t>(static_cast<uint64_t>(a.batch) * a.heads * nkb * blk);
+    }
     if (splits <= 1) return 0;
     const uint64_t rows = static_cast<uint64_t>(a.batch) * a.heads * a.seq_q;
     return static_cast<size_t>(splits) * rows * (a.head_dim + 2) * sizeof(float);
@@ -713,12 +839,27 @@ void attention(hipStream_t s, const Attn &a, float *ws)
     float *ws_ml = ws ? ws + static_cast<uint64_t>(splits) * rows * D : nullptr;
     dim3 grid(qb, a.batch * a.heads, splits);
     if (use_prefill(a)) {
+        // ws holds attention_ws_bytes(a): the split K / V^T blocks.
+        int8_t *split = reinterpret_cast<int8_t *>(ws);
         const uint32_t nqb = qb;
+        const uint32_t nkb = (a.seq_k + XK - 1) / XK;
+        const dim3 sgrid(nkb, a.batch * a.heads);
         if (a.causal) grid.x = (nqb + 1) / 2;
-        if (D == 128)
-            attn_prefill_kernel<128><<<grid, PThreads, PrefillLds<128>::kBytes, s>>>(a, nqb);
-        else
-            attn_prefill_kernel<64><<<grid, PThreads, PrefillLds<64>::kBytes, s>>>(a, nqb);
+        static bool lds_optin = false;
+        if (!lds_optin)
+            lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_prefill_kernel<128>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(SplitBlk<128>::kLds)) == hipSuccess &&
+                        hipFuncSetAttribute(reinterpret_cast<const void *>(attn_prefill_kernel<64>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(SplitBlk<64>::kLds)) == hipSuccess;
+        if (D == 128) {
+            attn_split_kv<128><<<sgrid, 256, 0, s>>>(a, nkb, split);
+            attn_prefill_kernel<128><<<grid, PThreads, SplitBlk<128>::kLds, s>>>(a, nqb, nkb, split);
+        } else {
+            attn_split_kv<64><<<sgrid, 256, 0, s>>>(a, nkb, split);
+            attn_prefill_kernel<64><<<grid, PThreads, SplitBlk<64>::kLds, s>>>(a, nqb, nkb, split);
+        }
         return;
     }
     if (use_decode(a)) {
