@@ -427,11 +427,21 @@ __device__ __forceinline__ uint32_t vt_key(uint32_t p)
 
 __device__ __forceinline__ void split_bf16(const float (&x)[8], v8bf &hi, v8bf &lo)
 {
+    // hi rounded to nearest even, two per v_cvt_pk_bf16_f32; its f32 value is
+    // the packed word's halves moved to the top; lo = bf16(x - hi).
+    typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    uint32_t hw[4], lw[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        hi[e] = static_cast<__bf16>(x[e]);
-        lo[e] = static_cast<__bf16>(x[e] - static_cast<float>(hi[e]));
+    for (int e = 0; e < 4; ++e) {
+        hw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){x[2 * e], x[2 * e + 1]}, v2bf));
+        const float h0 = __builtin_bit_cast(float, hw[e] << 16);
+        const float h1 = __builtin_bit_cast(float, hw[e] & 0xFFFF0000u);
+        lw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){x[2 * e] - h0, x[2 * e + 1] - h1}, v2bf));
     }
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    hi = __builtin_bit_cast(v8bf, (v4u){hw[0], hw[1], hw[2], hw[3]});
+    lo = __builtin_bit_cast(v8bf, (v4u){lw[0], lw[1], lw[2], lw[3]});
 }
 
 // One (32-key block, batch*head) per workgroup of 256 threads.
@@ -498,15 +508,11 @@ __device__ __forceinline__ void lds_dma16(const void *src, int8_t *lds_dst)
                  : "memory", "m0");
 }
 
-// e^x through the hardware exp2 (v_exp_f32).  The reference's degree-5
-// polynomial (dev::fast_expf) spends ~10 VALU ops per weight; the two differ
-// by at most ~1.5e-4 relative (the polynomial's own truncation error), far
-// inside the attention bar of 2e-3; the decode kernel keeps the polynomial.
-__device__ __forceinline__ float fast_exp_hw(float x)
-{
-    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
-}
-
+// Softmax weights use the hardware exp2 (v_exp_f32) on base-2 scores (Q is
+// pre-scaled by log2 e).  The reference's degree-5 polynomial
+// (dev::fast_expf) spends ~10 VALU ops per weight; the two differ by at most
+// ~1.5e-4 relative (the polynomial's own truncation error), far inside the
+// attention bar of 2e-3; the decode kernel keeps the polynomial.
 __device__ __forceinline__ v16f mfma_bf16(const v8bf &a, const v8bf &b, const v16f &c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -540,24 +546,32 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
     const uint32_t nsb = (nblk + 1) / 2;
     const uint32_t wave_kend = a.causal ? min(kend, min(qw + XQ, sq) - 1 + off + 1) : kend;
 
-    // Q^T operand of step s: lane (query col, half h) holds d = 16s + 8h .. +8.
+    // Q^T operand of step s: lane (query col, half h) holds d = 16s + 8h .. +8,
+    // pre-multiplied by scale * log2(e) so scores come out in base-2 units
+    // (softmax weights are exp2(s - m); m, alpha and the merge use base 2).
+    constexpr float kLog2e = 1.4426950408889634f;
     v8bf qh[NS], ql[NS];
     {
+        const float qs = a.scale * kLog2e;
         const float4 *qrow = reinterpret_cast<const float4 *>(a.Q + (bh * sq + min(myq, sq - 1)) * D + 8 * h);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const float4 u = qrow[4 * s], v = qrow[4 * s + 1];
-            const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+            const float x[8] = {u.x * qs, u.y * qs, u.z * qs, u.w * qs, v.x * qs, v.y * qs, v.z * qs, v.w * qs};
             split_bf16(x, qh[s], ql[s]);
         }
     }
 
-    // DMA of super block sb (blocks 2sb, 2sb+1) into ring slot sb%2; waves
-    // 0-3 copy the even block, 4-7 the odd one (skipped past nblk).
+    // LDS slot of block 2sb + wk: super block sb sits in ring slot sb % 2.
+    auto slot = [&](uint32_t sb) -> int8_t * {
+        return lds + ((sb & 1) * 2 + wk) * S::kBytes;
+    };
+    // DMA of block 2sb + wk: waves 0-3 copy the even block, 4-7 the odd one
+    // (skipped past nblk).
     auto issue = [&](uint32_t sb) {
         const uint32_t blk = 2 * sb + wk;
         if (blk >= nblk) return;                                  // wave-uniform
-        int8_t *dst = lds + (sb & 1) * 2 * S::kBytes + wk * S::kBytes;
+        int8_t *dst = slot(sb);
         const int8_t *from = src + static_cast<uint64_t>(blk) * S::kBytes + lane * 16;
 #pragma unroll
         for (int i = 0; i < kInstr / 8; ++i) {
@@ -565,46 +579,42 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
             lds_dma16(from + ins * 1024, dst + ins * 1024);
         }
     };
-    if (nsb) issue(0);
 
     v16f o[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] = (v16f){0.f};
     float m = -__builtin_inff(), l = 0.0f;
 
-    for (uint32_t sb = 0; sb < nsb; ++sb) {
-        __builtin_amdgcn_s_waitcnt(0xF70);   // vmcnt(0): this wave's DMA of super block sb
-        __syncthreads();                     // landed everywhere; super block sb-1's slot free
-        if (sb + 1 < nsb) issue(sb + 1);
-        const uint32_t kb = 2 * sb + wk;
-        if (kb * XK >= wave_kend) continue;  // wave-uniform: past this wave's causal limit
-        const int8_t *blk = lds + (sb & 1) * 2 * S::kBytes + wk * S::kBytes;
-
-        // S^T = K . Q^T: hi*hi on one chain, the two cross terms on another.
-        v16f s0 = (v16f){0.f}, s1 = (v16f){0.f};
+    // S^T = K . Q^T, one accumulator chain (the cross terms first).
+    auto qk = [&](const int8_t *blk, v16f &sa) {
+        sa = (v16f){0.f};
         const int8_t *krow = blk + col * (D * 2);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             const uint32_t koff = ((2 * s + h) ^ (col & (C - 1))) << 4;
             const v8bf kh = *reinterpret_cast<const v8bf *>(krow + koff);
             const v8bf kl = *reinterpret_cast<const v8bf *>(krow + S::kHalfK + koff);
-            s1 = mfma_bf16(kl, qh[s], s1);
-            s0 = mfma_bf16(kh, qh[s], s0);
-            s1 = mfma_bf16(kh, ql[s], s1);
+            sa = mfma_bf16(kl, qh[s], sa);
+            sa = mfma_bf16(kh, ql[s], sa);
+            sa = mfma_bf16(kh, qh[s], sa);
         }
-        // Scores of query myq for keys kb*32 + 8j + 4h + i (register 4j + i).
-        // A block whose keys are all below every query's causal limit and
-        // kend (wave-uniform) needs no masking.
+    };
+
+    // Online softmax of block kb: scores of query myq for keys kb*32 + 8j +
+    // 4h + i (register 4j + i) -> split weights ph/pl, rescaled O^T.  A block
+    // whose keys are all below every query's causal limit and kend (wave-
+    // uniform) needs no masking.
+    auto softmax = [&](uint32_t kb, const v16f &sa, v8bf (&ph)[2], v8bf (&pl)[2]) {
         const bool interior = (kb + 1) * XK <= kend && qw + XQ - 1 < sq &&
                               (!a.causal || (kb + 1) * XK - 1 <= qw + off);
         float sc[16];
         float bmax = -__builtin_inff();
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t key = kb * XK + 8 * (r >> 2) + 4 * h + (r & 3);
-            float v = (s0[r] + s1[r]) * a.scale;
-            if (Mh) v += Mh[static_cast<uint64_t>(min(myq, sq - 1)) * sk + min(key, sk - 1)];
-            if (!interior) {
+            float v = sa[r];
+            if (!interior || Mh) {
+                const uint32_t key = kb * XK + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (Mh) v += Mh[static_cast<uint64_t>(min(myq, sq - 1)) * sk + min(key, sk - 1)] * kLog2e;
                 const bool dead = key >= kend || myq >= sq || (a.causal && key > myq + off);
                 v = dead ? -__builtin_inff() : v;
             }
@@ -612,48 +622,65 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
             bmax = fmaxf(bmax, v);
         }
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-        const bool live = bmax != -__builtin_inff();      // else the block is skipped for this query
-        const float mn = live ? fmaxf(m, bmax) : m;
-        const float alpha = (!live || m == -__builtin_inff()) ? (live ? 0.0f : 1.0f) : fast_exp_hw(m - mn);
+        // Lazy reference point: weights are exp2(s - m) with m moved only when
+        // the block max exceeds it by more than 8 (weights stay <= 256), so
+        // O^T is rescaled only on those rare blocks; softmax is invariant to
+        // the reference point.  A block whose max is not finite adds nothing.
+        const bool grow = bmax > m + 8.0f;                // also the first live block (m = -inf)
+        const float mn = grow ? bmax : m;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;   // 0 when m = -inf
+        const float ref = mn == -__builtin_inff() ? 0.0f : mn;             // exp2(-inf - 0) = 0
         float psum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float p = (sc[r] == -__builtin_inff()) ? 0.0f : fast_exp_hw(sc[r] - mn);
+            const float p = __builtin_amdgcn_exp2f(sc[r] - ref);
             sc[r] = p;
             psum += p;
         }
         psum += __shfl_xor(psum, 32, 64);
-        m = mn;
         l = l * alpha + psum;
+        if (__ballot(grow && m != -__builtin_inff())) {   // wave-uniform; O^T is 0 before the first
 #pragma unroll
-        for (int t = 0; t < DT; ++t) o[t] *= alpha;
-
-        // O^T += V^T . P^T over keys 16t..16t+15: P^T = score registers 8t..8t+7.
-        v8bf ph[2], pl[2];
+            for (int t = 0; t < DT; ++t) o[t] *= alpha;
+        }
+        m = mn;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const float x[8] = {sc[8 * t], sc[8 * t + 1], sc[8 * t + 2], sc[8 * t + 3],
                                 sc[8 * t + 4], sc[8 * t + 5], sc[8 * t + 6], sc[8 * t + 7]};
             split_bf16(x, ph[t], pl[t]);
         }
-        const int8_t *vt = blk + S::kVOff;
+    };
+
+    // O^T += V^T . P^T over keys 16t..16t+15: P^T = score registers 8t..8t+7.
+    auto pv = [&](const int8_t *vt, const v8bf (&ph)[2], const v8bf (&pl)[2]) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            v8bf vh[DT], vl[DT];
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const uint32_t d = 32 * dt + col;
                 const uint32_t voff = d * (XK * 2) + (((2 * t + h) ^ ((d >> 1) & 3)) << 4);
-                vh[dt] = *reinterpret_cast<const v8bf *>(vt + voff);
-                vl[dt] = *reinterpret_cast<const v8bf *>(vt + S::kHalfV + voff);
+                const v8bf vh = *reinterpret_cast<const v8bf *>(vt + voff);
+                const v8bf vl = *reinterpret_cast<const v8bf *>(vt + S::kHalfV + voff);
+                o[dt] = mfma_bf16(vl, ph[t], o[dt]);
+                o[dt] = mfma_bf16(vh, pl[t], o[dt]);
+                o[dt] = mfma_bf16(vh, ph[t], o[dt]);
             }
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt] = mfma_bf16(vl[dt], ph[t], o[dt]);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt] = mfma_bf16(vh[dt], pl[t], o[dt]);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o[dt] = mfma_bf16(vh[dt], ph[t], o[dt]);
-        }
+    };
+
+    if (nsb) issue(0);
+    for (uint32_t sb = 0; sb < nsb; ++sb) {
+        __builtin_amdgcn_s_waitcnt(0xF70);   // vmcnt(0): this wave's DMA of super block sb
+        __syncthreads();                     // landed everywhere; super block sb-1's slot free
+        if (sb + 1 < nsb) issue(sb + 1);
+        const uint32_t kb = 2 * sb + wk;
+        if (kb * XK >= wave_kend) continue;  // wave-uniform: past this wave's causal limit
+        const int8_t *blk = slot(sb);
+        v16f sa;
+        qk(blk, sa);
+        v8bf ph[2], pl[2];
+        softmax(kb, sa, ph, pl);
+        pv(blk + S::kVOff, ph, pl);
     }
 
     // Merge the two key halves: waves 4-7 stage (m, l, O^T) in LDS, waves 0-3
@@ -680,8 +707,8 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
     if (wk == 0) {
         const float m1 = ml[2 * col], l1 = ml[2 * col + 1];
         const float M = fmaxf(m, m1);
-        const float a0 = m == -__builtin_inff() ? 0.0f : fast_exp_hw(m - M);
-        const float a1 = m1 == -__builtin_inff() ? 0.0f : fast_exp_hw(m1 - M);
+        const float a0 = m == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+        const float a1 = m1 == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
         const float L = a0 * l + a1 * l1;
         const float inv = L > 0.0f ? 1.0f / L : 0.0f;
         const float w0 = a0 * inv, w1 = a1 * inv;
