@@ -475,20 +475,30 @@ __global__ __launch_bounds__(256) void attn_split_kv(Attn a, uint32_t nkb, int8_
         *reinterpret_cast<v8bf *>(blk + off) = hi;
         *reinterpret_cast<v8bf *>(blk + S::kHalfK + off) = lo;
     }
-    // V^T: lanes take consecutive d, so each key's reads are coalesced.
-    for (uint32_t it = threadIdx.x; it < 4 * D; it += 256) {
-        const uint32_t d = it % D, ch = it / D;
-        float x[8];
+    // V^T: a thread takes 4 columns (one float4) of the 8 keys of position
+    // chunk ch and writes those 4 rows' chunk; lanes take consecutive float4
+    // of a key row, so the reads are coalesced.
+    for (uint32_t it = threadIdx.x; it < D; it += 256) {
+        const uint32_t d4 = it % (D / 4), ch = it / (D / 4);
+        float4 v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const uint32_t gk = kb * XK + vt_key(8 * ch + e);
-            x[e] = gk < sk ? Vh[static_cast<uint64_t>(gk) * D + d] : 0.0f;
+            v[e] = gk < sk ? *reinterpret_cast<const float4 *>(Vh + static_cast<uint64_t>(gk) * D + 4 * d4)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        v8bf hi, lo;
-        split_bf16(x, hi, lo);
-        const uint32_t off = d * (XK * 2) + ((ch ^ ((d >> 1) & 3)) << 4);
-        *reinterpret_cast<v8bf *>(blk + S::kVOff + off) = hi;
-        *reinterpret_cast<v8bf *>(blk + S::kVOff + S::kHalfV + off) = lo;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t d = 4 * d4 + q;
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = q == 0 ? v[e].x : q == 1 ? v[e].y : q == 2 ? v[e].z : v[e].w;
+            v8bf hi, lo;
+            split_bf16(x, hi, lo);
+            const uint32_t off = d * (XK * 2) + ((ch ^ ((d >> 1) & 3)) << 4);
+            *reinterpret_cast<v8bf *>(blk + S::kVOff + off) = hi;
+            *reinterpret_cast<v8bf *>(blk + S::kVOff + S::kHalfV + off) = lo;
+        }
     }
 }
 

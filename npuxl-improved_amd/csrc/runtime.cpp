@@ -118,6 +118,14 @@ void *vnpu_stream::ensure_workspace(size_t bytes)
     return workspace;
 }
 
+// Events that only time GPU work: no system-scope fence when they complete
+// (the default event writes back and invalidates the caches, which costs
+// several microseconds per record and slows the kernels that follow).
+static hipError_t create_timing_event(hipEvent_t *e)
+{
+    return hipEventCreateWithFlags(e, hipEventDisableSystemFence);
+}
+
 hipEvent_t vnpu_stream::acquire_event()
 {
     if (!event_pool.empty()) {
@@ -126,7 +134,7 @@ hipEvent_t vnpu_stream::acquire_event()
         return e;
     }
     hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) {
+    if (create_timing_event(&e) != hipSuccess) {
         (void)hipGetLastError();
         return nullptr;
     }
@@ -726,10 +734,10 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
             if (tracing) {
                 {
                     std::lock_guard<std::mutex> tl(d->trace.mutex);
-                    if (!d->trace.epoch && hipEventCreate(&d->trace.epoch) == hipSuccess)
+                    if (!d->trace.epoch && create_timing_event(&d->trace.epoch) == hipSuccess)
                         (void)hipEventRecord(d->trace.epoch, stream->hip);
                 }
-                if (hipEventCreate(&rec.start) == hipSuccess) (void)hipEventRecord(rec.start, stream->hip);
+                if (create_timing_event(&rec.start) == hipSuccess) (void)hipEventRecord(rec.start, stream->hip);
             }
             ExecStats st;
             vnpu_status_t rc = VNPU_OK;
@@ -757,7 +765,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
             d->tiles_dispatched.fetch_add(st.tiles_dispatched);
             d->tiles_culled.fetch_add(st.tiles_culled);
             if (tracing) {
-                if (hipEventCreate(&rec.stop) == hipSuccess) (void)hipEventRecord(rec.stop, stream->hip);
+                if (create_timing_event(&rec.stop) == hipSuccess) (void)hipEventRecord(rec.stop, stream->hip);
                 rec.opcode = cmd.opcode;
                 rec.unit = st.unit;
                 rec.id = cmd.id;
@@ -1161,8 +1169,8 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
         } packguard{w};
 
         hipEvent_t e0, e1;
-        VNPU_HIP(hipEventCreate(&e0));
-        VNPU_HIP(hipEventCreate(&e1));
+        VNPU_HIP(create_timing_event(&e0));
+        VNPU_HIP(create_timing_event(&e1));
         auto time_tiles = [&](uint32_t tm, uint32_t tk, uint32_t tn, double &best) -> vnpu_status_t {
             vnpu_status_t r = vnpu_device_set_tiles(device, tm, tk, tn);
             if (r == VNPU_OK) r = vnpu_stream_submit(s, &cmd, 1, nullptr);   // warm-up
