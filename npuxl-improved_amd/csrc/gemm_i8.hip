@@ -268,6 +268,8 @@ __device__ void store_tile(const I8Gemm &p, const int32_t *tile, const float *sa
 {
 #pragma clang fp contract(off)
     constexpr int kPerRow = kCols / 4;   // threads per row
+    constexpr int kRowStep = kT / kPerRow;
+    if (tid >= kRowStep * kPerRow) return;    // kT need not be a multiple of kPerRow
     const uint32_t c4 = (tid % kPerRow) * 4;  // first of this thread's 4 columns
     const uint32_t n = n0 + c4;
     float sb[4], bias[4];
@@ -280,7 +282,7 @@ __device__ void store_tile(const I8Gemm &p, const int32_t *tile, const float *sa
     const bool vec = (n + 3 < p.N) && ((p.ldc & 3u) == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
     const uint32_t rows = min(static_cast<uint32_t>(kRows), p.M - m0);
 #pragma unroll 4
-    for (uint32_t r = tid / kPerRow; r < rows; r += kT / kPerRow) {
+    for (uint32_t r = tid / kPerRow; r < rows; r += kRowStep) {
         const v4i acc = *reinterpret_cast<const v4i *>(tile + r * kPitch + c4);
         const float sa = sa_lds[r];
         float o[4];
@@ -680,42 +682,56 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
 }
 
 // ---------------------------------------------------------------------------
-// Wide tile (K % 128 == 0, dense weights, >= 256 tiles): 256 x 256 per
-// workgroup, 4 waves of 128 x 128 (4 x 4 MFMA tiles, 256 accumulator
-// registers at one wave per SIMD).  Per MFMA it copies a third fewer bytes
-// from L2 into LDS and reads a third fewer fragment bytes from LDS than the
-// 256 x 128 tile, at twice the work per tile, so it pays only when the grid
-// holds at least one tile per CU.
-//   * stage = A 256 x 128 B (32 KiB, swizzled as above) + B 32 fragment
-//     blocks (16 column blocks x 2 k blocks, 32 KiB); 2 stages = 128 KiB;
-//   * per stage: 32 MFMAs on half 0 with half 1's 16 fragment reads threaded
+// Wide tiles (K % 128 == 0, dense weights, M % 256 == 0): 256 x TN per
+// workgroup with TN = 256 or 192, 4 waves of 128 x TN/2 (4 x TN/64 MFMA
+// tiles; 256 or 192 accumulator registers at one wave per SIMD).  Per MFMA
+// the 256 x 256 tile copies a third fewer bytes from L2 into LDS and reads a
+// third fewer fragment bytes from LDS than the 256 x 128 tile; 256 x 192 sits
+// between them and fills whole rounds of 256 CUs where 256-wide tiles leave a
+// half-empty last round (N = 11008 and 12288 at M = 2048).
+//   * stage = A 256 x 128 B (32 KiB, swizzled as above) + B TN/8 fragment
+//     blocks (TN/16 column blocks x 2 k blocks); 2 stages (128 or 112 KiB);
+//   * per stage: the MFMAs of k half 0 with half 1's fragment reads threaded
 //     between them; vmcnt(0) (stage s+1 landed) and one barrier (stage s
-//     fully read); 32 MFMAs on half 1 with stage s+2's 16 DMA instructions
-//     and stage s+1's half-0 reads threaded between them;
+//     fully read); the MFMAs of half 1 with stage s+2's DMA instructions and
+//     stage s+1's half-0 reads threaded between them;
 //   * the epilogue stages 128 rows at a time through LDS.
 // ---------------------------------------------------------------------------
 namespace wide {
-constexpr int TM = 256, TN = 256, SK = 128;
-constexpr int kALoads = 8, kBLoads = 8;               // per wave per stage
-constexpr int kLoads = kALoads + kBLoads;
-constexpr int kStageBytes = 64 * 1024;
-constexpr int kBOff = 32 * 1024;
-constexpr int kRing = 2 * kStageBytes;                // 128 KiB
+constexpr int TM = 256, SK = 128;
+constexpr int kALoads = 8;                            // A DMA per wave per stage
+constexpr int kBOff = 32 * 1024;                      // B's offset in a stage
 constexpr int kOutRows = 128;                         // rows staged at a time
-constexpr int kOutPitch = TN + 4;                     // int32 per staged row
-constexpr int kOut = kOutRows * kOutPitch * 4;        // 130 KiB
-constexpr int kScaleOff = kOut;
-constexpr size_t kLds = kOut + TM * 4;
-static_assert(kLds >= static_cast<size_t>(kRing) && kLds <= 160 * 1024, "LDS plan");
+template <int TN>
+struct Cfg {
+    static constexpr int NB = TN / 64;                // 32-column MFMA tiles per wave
+    static constexpr int kBBlocks = TN / 8;           // 1 KiB B blocks per stage
+    static constexpr int kBLoads = kBBlocks / 4;      // B DMA per wave per stage
+    static constexpr int kLoads = kALoads + kBLoads;
+    static constexpr int kStageBytes = kBOff + kBBlocks * 1024;
+    static constexpr int kRing = 2 * kStageBytes;
+    static constexpr int kOutPitch = TN + 4;          // int32 per staged row
+    static constexpr int kOut = kOutRows * kOutPitch * 4;
+    static constexpr int kScaleOff = kOut;
+    static constexpr size_t kLds = static_cast<size_t>(kOut + TM * 4 > kRing ? kOut + TM * 4 : kRing);
+    static constexpr int kReads = 2 * (4 + NB);       // fragment reads per 64-deep half
+    static constexpr int kMfma = 2 * 4 * NB;          // MFMAs per 64-deep half
+    static_assert(kLds <= 160 * 1024, "LDS plan");
+    static_assert(kLoads + kReads <= 2 * kMfma, "side work fits the MFMA slots");
+};
 }  // namespace wide
 
+template <int NB>
 struct FragsW {
-    v4i a[2][4], b[2][4];
+    v4i a[2][4], b[2][NB];
 };
 
+template <int TN>
 __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
 {
     using namespace wide;
+    using G = Cfg<TN>;
+    constexpr int NB = G::NB;
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
 
     const int tid = threadIdx.x;
@@ -735,7 +751,8 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tile
     // DMA: A instruction 8*wave + j copies rows 64*wave + 8j + l/8 (M is a
     // multiple of 256 here, so no row clamp); lane l fetches k chunk
     // (l%8) ^ ((row >> 1) & 7) = (l%8) ^ (l/16) ^ 4(j%2).  B block
-    // bi = 8*wave + j is column block bi/2, k block bi%2.  Bases are
+    // bi = kBLoads*wave + j is column block bi/2, k block bi%2 (column blocks
+    // past N are clamped: their results are never stored).  Bases are
     // wave-uniform (SGPRs); per-lane parts are 32-bit offsets.
     const int q = lane >> 3;
     const int8_t *a_base = p.A + static_cast<uint64_t>(m0 + wave * 64) * p.lda;
@@ -743,20 +760,20 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tile
     const uint32_t a_lo_odd = q * p.lda + 16 * ((lane & 7) ^ (q >> 1) ^ 4);
     const uint32_t b_lo = lane * 16;
     auto issue_one = [&](uint32_t s, int k) {
-        int8_t *st = smem + (s & 1) * kStageBytes;
+        int8_t *st = smem + (s & 1) * G::kStageBytes;
         if (k < kALoads) {
             dma16_s(a_base + static_cast<uint64_t>(8 * k) * p.lda + s * SK, (k & 1) ? a_lo_odd : a_lo,
                     st + (wave * kALoads + k) * 1024);
         } else {
-            const int bi = wave * kBLoads + (k - kALoads);
+            const int bi = wave * G::kBLoads + (k - kALoads);
             const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
             dma16_s(p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + static_cast<uint64_t>(s) * 2048,
                     b_lo, st + kBOff + bi * 1024);
         }
     };
 
-    // Fragment read k (0..15) of half hh of the stage at byte offset st, in
-    // MFMA order: per 32-deep h, b[h][0], a[h][0..3], b[h][1..3].  A row
+    // Fragment read k of half hh of the stage at byte offset st, in MFMA
+    // order: per 32-deep h, b[h][0], a[h][0..3], b[h][1..NB-1].  A row
     // wm*128 + 32i + l%32 has swizzle ((l%32) >> 1) & 7 whatever i is, so one
     // per-lane base per (hh, h) plus the constant 4096 i addresses it; B needs
     // one per-lane base plus constants.  With st a constant every read is
@@ -769,9 +786,9 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tile
         for (int h = 0; h < 2; ++h)
             a_rd[hh][h] = (wm * 128 + (lane & 31)) * 128 +
                           (((4 * hh + 2 * h + (lane >> 5)) ^ (((lane & 31) >> 1) & 7)) << 4);
-    const uint32_t b_rd = kBOff + ((wn * 16 + 2 * sub) << 10) + (((lane >> 5) * 16 + (lane & 15)) << 4);
-    auto read_one = [&](uint32_t st, int hh, FragsW &f, int k) {
-        const int h = k >> 3, r = k & 7;
+    const uint32_t b_rd = kBOff + ((wn * (TN / 16) + 2 * sub) << 10) + (((lane >> 5) * 16 + (lane & 15)) << 4);
+    auto read_one = [&](uint32_t st, int hh, FragsW<NB> &f, int k) {
+        const int h = k / (4 + NB), r = k % (4 + NB);
         if (r >= 1 && r <= 4) {
             const int i = r - 1;
             f.a[h][i] = *reinterpret_cast<const v4i *>(smem + st + a_rd[hh][h] + i * 4096);
@@ -781,69 +798,75 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tile
         }
     };
 
-    v16i acc[4][4];
+    v16i acc[4][NB];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (v16i){0};
-    // The 32 MFMAs of one 64-deep half; side(k) runs after MFMA k.
-    auto mma = [&](const FragsW &f, auto &&side) {
+        for (int j = 0; j < NB; ++j) acc[i][j] = (v16i){0};
+    // The MFMAs of one 64-deep half; side(k) runs after MFMA k.
+    auto mma = [&](const FragsW<NB> &f, auto &&side) {
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {
-            const int h = k >> 4, j = (k >> 2) & 3, i = k & 3;
+        for (int k = 0; k < G::kMfma; ++k) {
+            const int h = k / (4 * NB), j = (k / 4) % NB, i = k % 4;
             acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
             side(k);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
+    // Second half's side work: the stage s+2 DMA, one per MFMA slot, then the
+    // next stage's half-0 reads spread over the remaining slots.
+    constexpr int kTail = G::kMfma - G::kLoads;
+    auto side2 = [&](int k, uint32_t s, uint32_t nxt, FragsW<NB> &f, bool dma) {
+        if (dma && k < G::kLoads) issue_one(s, k);
+#pragma unroll
+        for (int r = 0; r < G::kReads; ++r)
+            if (G::kLoads + (r * kTail) / G::kReads == k) read_one(nxt, 0, f, r);
+    };
 
     // Prologue: stages 0 and 1 in flight, wait for 0, read its first half.
 #pragma unroll
-    for (int k = 0; k < kLoads; ++k) issue_one(0, k);
+    for (int k = 0; k < G::kLoads; ++k) issue_one(0, k);
     if (KS > 1) {
 #pragma unroll
-        for (int k = 0; k < kLoads; ++k) issue_one(1, k);
-        wait_vmcnt<kLoads>();
+        for (int k = 0; k < G::kLoads; ++k) issue_one(1, k);
+        wait_vmcnt<G::kLoads>();
     } else {
         wait_vmcnt<0>();
     }
     block_barrier();
-    FragsW f0, f1;
+    FragsW<NB> f0, f1;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) read_one(0, 0, f0, k);
+    for (int k = 0; k < G::kReads; ++k) read_one(0, 0, f0, k);
 
     uint32_t s = 0;
     for (; s + 2 < KS; ++s) {
-        const uint32_t cur = (s & 1) * kStageBytes, nxt = kStageBytes - cur;
+        const uint32_t cur = (s & 1) * G::kStageBytes, nxt = G::kStageBytes - cur;
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < 16) read_one(cur, 1, f1, k); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
         wait_vmcnt<0>();
         block_barrier();
-        mma(f1, [&](int k) {
-            if (k < 16) issue_one(s + 2, k);
-            else read_one(nxt, 0, f0, k - 16);
-        });
+        mma(f1, [&](int k) { side2(k, s + 2, nxt, f0, true); });
     }
     if (s + 1 < KS) {
-        const uint32_t cur = (s & 1) * kStageBytes, nxt = ((s + 1) & 1) * kStageBytes;
+        const uint32_t cur = (s & 1) * G::kStageBytes, nxt = ((s + 1) & 1) * G::kStageBytes;
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < 16) read_one(cur, 1, f1, k); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
         wait_vmcnt<0>();
         block_barrier();
-        mma(f1, [&](int k) { if (k >= 16) read_one(nxt, 0, f0, k - 16); });
+        mma(f1, [&](int k) { side2(k, 0, nxt, f0, false); });
         ++s;
     }
     {
-        const uint32_t cur = (s & 1) * kStageBytes;
+        const uint32_t cur = (s & 1) * G::kStageBytes;
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < 16) read_one(cur, 1, f1, k); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
         mma(f1, [](int) {});
     }
 
     // Epilogue, 128 rows (the rows of waves with wm == half) at a time.
     __syncthreads();
     int32_t *tile = reinterpret_cast<int32_t *>(smem);
-    float *sa_lds = reinterpret_cast<float *>(smem + kScaleOff);
+    float *sa_lds = reinterpret_cast<float *>(smem + G::kScaleOff);
     {
         const uint32_t m = m0 + tid;
         sa_lds[tid] = (p.scale_a && m < p.M) ? p.scale_a[m] : 1.0f;
@@ -854,21 +877,21 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tile
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < NB; ++j)
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        tile[(i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kOutPitch + wn * 128 + j * 32 +
-                             (lane & 31)] = acc[i][j][r];
+                        tile[(i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * G::kOutPitch + wn * (TN / 2) +
+                             j * 32 + (lane & 31)] = acc[i][j][r];
         }
         __syncthreads();
         if (mh < p.M) {
             const float *sa = sa_lds + half * kOutRows;
             switch (p.epilogue) {
-            case 1: store_tile<1, kThreads, TN, kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
-            case 2: store_tile<2, kThreads, TN, kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
+            case 1: store_tile<1, kThreads, TN, G::kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
+            case 2: store_tile<2, kThreads, TN, G::kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
             case 3:
-            case 4: store_tile<3, kThreads, TN, kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
-            default: store_tile<0, kThreads, TN, kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
+            case 4: store_tile<3, kThreads, TN, G::kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
+            default: store_tile<0, kThreads, TN, G::kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
             }
         }
         __syncthreads();
@@ -880,11 +903,40 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tile
 uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t tile_n)
 {
     if (tile_m == 256 && tile_k == 128 && tile_n == 256) return kI8Wide;
+    if (tile_m == 256 && tile_k == 128 && tile_n == 192) return kI8Wide192;
     if (tile_m == 256 && tile_k == 128 && tile_n == 128) return kI8Wave8;
     if (tile_m == 256 && tile_k == 64 && tile_n == 128) return kI8Pipe;
     if (tile_m == 128 && tile_k == 64 && tile_n == 128) return kI8Generic;
     return kI8Auto;
 }
+
+namespace {
+
+uint32_t cu_count()
+{
+    static const uint32_t n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+            (void)hipGetLastError();
+            return 256u;
+        }
+        return static_cast<uint32_t>(cus);
+    }();
+    return n;
+}
+
+// Estimated time of a grid of `tiles` tiles of area tm x tn on `cus` CUs:
+// whole rounds of one tile per CU, each tile costing its area times the
+// kernel's measured time per unit area (relative: 256 x 256 tile 1.0,
+// 256 x 192 1.2, 256 x 128 8-wave 1.4; from 2048 x 4096 x N runs).
+double tile_cost(uint64_t tiles, uint32_t cus, uint32_t tm, uint32_t tn, double per_area)
+{
+    const uint64_t rounds = (tiles + cus - 1) / cus;
+    return static_cast<double>(rounds) * tm * tn * per_area;
+}
+
+}  // namespace
 
 void gemm_i8(hipStream_t s, const I8Gemm &p)
 {
@@ -894,17 +946,28 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
                          p.K <= 16384;
     const bool k128 = aligned && p.K % pipe128::SK == 0;
     const bool wide_ok = k128 && !p.zero_blocks && p.M % wide::TM == 0;
-    const uint32_t wm_ = p.M / wide::TM, wn_ = (p.N + wide::TN - 1) / wide::TN;
+    const uint32_t wm_ = p.M / wide::TM;
+    const uint32_t wn256 = (p.N + 255) / 256, wn192 = (p.N + 191) / 192;
+    const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
+    const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
     // A requested kernel that cannot take this shape falls back to the
     // automatic choice.
     uint32_t v = p.variant;
-    if ((v == kI8Wide && !wide_ok) || (v == kI8Wave8 && !k128) || (v == kI8Pipe && !aligned)) v = kI8Auto;
+    if (((v == kI8Wide || v == kI8Wide192) && !wide_ok) || (v == kI8Wave8 && !k128) || (v == kI8Pipe && !aligned))
+        v = kI8Auto;
     if (v == kI8Auto) {
-        // Dense weights, whole 256-row tiles and at least one wide tile per
-        // CU (256 CUs): the 256 x 256 tile (measured: 2048x4096x8192 57 vs
-        // 78 us, x11008 108 vs 112 us; with 128 wide tiles half the CUs idle
-        // and the 256 x 128 tile wins, 84 vs 115 us).
-        v = (wide_ok && wm_ * wn_ >= 256) ? kI8Wide : k128 ? kI8Wave8 : aligned ? kI8Pipe : kI8Generic;
+        // The tile that finishes first: whole rounds of one tile per CU times
+        // the tile's cost (a 256-wide grid of 344 or 384 tiles runs two
+        // rounds, the second half empty; 256 x 192 tiles fill both).
+        v = k128 ? kI8Wave8 : aligned ? kI8Pipe : kI8Generic;
+        if (wide_ok) {
+            const uint32_t cus = cu_count();
+            const double c8 = tile_cost(static_cast<uint64_t>(tm) * tn, cus, 256, 128, 1.4);
+            const double c256 = tile_cost(static_cast<uint64_t>(wm_) * wn256, cus, 256, 256, 1.0);
+            const double c192 = tile_cost(static_cast<uint64_t>(wm_) * wn192, cus, 256, 192, 1.2);
+            if (c256 <= c192 && c256 < c8) v = kI8Wide;
+            else if (c192 < c8) v = kI8Wide192;
+        }
     }
     if (v != kI8Generic) {
         static bool lds_optin = false;
@@ -914,17 +977,19 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
                                    reinterpret_cast<const void *>(gemm_i8_pipe<true>),
                                    reinterpret_cast<const void *>(gemm_i8_k128w8<false>),
                                    reinterpret_cast<const void *>(gemm_i8_k128w8<true>),
-                                   reinterpret_cast<const void *>(gemm_i8_wide)})
+                                   reinterpret_cast<const void *>(gemm_i8_wide<256>),
+                                   reinterpret_cast<const void *>(gemm_i8_wide<192>)})
                 ok = ok && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                160 * 1024) == hipSuccess;
             lds_optin = ok;
         }
     }
-    const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
-    const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
     switch (v) {
     case kI8Wide:
-        gemm_i8_wide<<<dim3(wm_ * wn_), kThreads, wide::kLds, s>>>(p, wm_, wn_);
+        gemm_i8_wide<256><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds, s>>>(p, wm_, wn256);
+        return;
+    case kI8Wide192:
+        gemm_i8_wide<192><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds, s>>>(p, wm_, wn192);
         return;
     case kI8Wave8:
         if (p.zero_blocks) {

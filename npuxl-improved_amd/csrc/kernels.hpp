@@ -48,7 +48,7 @@ struct I8Gemm {
 };
 // Prefill kernels (gemm_i8.hip): a requested one that cannot take the shape
 // falls back to the automatic choice.
-enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generic = 4 };
+enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generic = 4, kI8Wide192 = 5 };
 // vnpu_device_set_tiles / autotune: tile triples (M, K, N) that name a kernel
 // select it: 256x128x256 wide, 256x128x128 8-wave, 256x64x128 64-deep,
 // 128x64x128 generic; anything else chooses automatically.

@@ -1193,6 +1193,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
         std::vector<Cand> cands;
         if (i8) {
             if (M % 256 == 0 && K % 128 == 0) cands.push_back({256, 128, 256});
+            if (M % 256 == 0 && K % 128 == 0) cands.push_back({256, 128, 192});
             if (K % 128 == 0) cands.push_back({256, 128, 128});
             if (K % 64 == 0) cands.push_back({256, 64, 128});
             cands.push_back({128, 64, 128});

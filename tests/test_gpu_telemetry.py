@@ -216,8 +216,8 @@ def test_set_tiles_and_autotune(gpu):
         assert lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n) == abi.OK
 
 
-@pytest.mark.parametrize("tiles", [(256, 128, 256), (256, 128, 128), (256, 64, 128), (128, 64, 128),
-                                   (128, 128, 64)])
+@pytest.mark.parametrize("tiles", [(256, 128, 256), (256, 128, 192), (256, 128, 128), (256, 64, 128),
+                                   (128, 64, 128), (128, 128, 64)])
 def test_forced_int8_kernels_are_bit_exact(gpu, tiles):
     """Every int8 prefill kernel a tile triple can select gives the oracle's
     bits (the last triple is the automatic choice)."""
