@@ -370,12 +370,14 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
 //
 // A pre-pass (attn_split_kv) writes K and V of every 32-key block, split and
 // laid out for the fragment reads, as one contiguous 32 KiB (D = 128) block:
-//   K hi | K lo : [key][d] bf16, 16-byte chunk c of key k at slot c ^ (k % C)
-//                 (C = chunks per row), so 8 lanes reading 8 keys at one d
-//                 offset hit distinct banks;
+//   K hi | K lo : [key][d] bf16, 16-byte chunk c of key k at slot
+//                 c ^ k_swizzle(k);
 //   V^T hi | lo : [d][position] bf16, 32 positions per row in the key order
 //                 that the PV step consumes (vt_key), chunk c of row d at
-//                 slot c ^ ((d >> 1) & 3).
+//                 slot c ^ ((d >> 2) & 3).
+// ds_read_b128 serves 16 lanes at a time from one 256-byte window of banks;
+// the swizzles put the 16 rows a quarter wave reads at one chunk in 16
+// distinct 16-byte slots of that window.
 // Keys past seq_k are written as zeros (their scores are masked anyway).
 //
 // Main kernel: a workgroup of 8 waves owns 128 queries of one (batch, head):
@@ -419,6 +421,15 @@ struct SplitBlk {
 // lane half h = (p/8)%2 multiplies element e = p%8 with the lane's score
 // register 8t + e, which holds key 16t + 4h + e (e < 4) or 16t + 8 + 4h +
 // e - 4 (e >= 4).
+// K rows are 2D bytes: 256 (D = 128) rows differ in all 16 slots of a
+// window by k % 16; 128-byte rows (D = 64) pair up in a window, so the slot
+// varies with k / 2.
+template <int D>
+__device__ __forceinline__ uint32_t k_swizzle(uint32_t k)
+{
+    return D == 128 ? (k & 15) : ((k >> 1) & 7);
+}
+
 __device__ __forceinline__ uint32_t vt_key(uint32_t p)
 {
     const uint32_t t = p >> 4, h = (p >> 3) & 1, e = p & 7;
@@ -471,7 +482,7 @@ __global__ __launch_bounds__(256) void attn_split_kv(Attn a, uint32_t nkb, int8_
         }
         v8bf hi, lo;
         split_bf16(x, hi, lo);
-        const uint32_t off = key * (D * 2) + ((c ^ (key & (C - 1))) << 4);
+        const uint32_t off = key * (D * 2) + ((c ^ k_swizzle<D>(key)) << 4);
         *reinterpret_cast<v8bf *>(blk + off) = hi;
         *reinterpret_cast<v8bf *>(blk + S::kHalfK + off) = lo;
     }
@@ -495,7 +506,7 @@ __global__ __launch_bounds__(256) void attn_split_kv(Attn a, uint32_t nkb, int8_
             for (int e = 0; e < 8; ++e) x[e] = q == 0 ? v[e].x : q == 1 ? v[e].y : q == 2 ? v[e].z : v[e].w;
             v8bf hi, lo;
             split_bf16(x, hi, lo);
-            const uint32_t off = d * (XK * 2) + ((ch ^ ((d >> 1) & 3)) << 4);
+            const uint32_t off = d * (XK * 2) + ((ch ^ ((d >> 2) & 3)) << 4);
             *reinterpret_cast<v8bf *>(blk + S::kVOff + off) = hi;
             *reinterpret_cast<v8bf *>(blk + S::kVOff + S::kHalfV + off) = lo;
         }
@@ -601,7 +612,7 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
         const int8_t *krow = blk + col * (D * 2);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-            const uint32_t koff = ((2 * s + h) ^ (col & (C - 1))) << 4;
+            const uint32_t koff = ((2 * s + h) ^ k_swizzle<D>(col)) << 4;
             const v8bf kh = *reinterpret_cast<const v8bf *>(krow + koff);
             const v8bf kl = *reinterpret_cast<const v8bf *>(krow + S::kHalfK + koff);
             sa = mfma_bf16(kl, qh[s], sa);
@@ -669,7 +680,7 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const uint32_t d = 32 * dt + col;
-                const uint32_t voff = d * (XK * 2) + (((2 * t + h) ^ ((d >> 1) & 3)) << 4);
+                const uint32_t voff = d * (XK * 2) + (((2 * t + h) ^ ((d >> 2) & 3)) << 4);
                 const v8bf vh = *reinterpret_cast<const v8bf *>(vt + voff);
                 const v8bf vl = *reinterpret_cast<const v8bf *>(vt + S::kHalfV + voff);
                 o[dt] = mfma_bf16(vl, ph[t], o[dt]);

@@ -219,6 +219,225 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_splitk_reduce(F32Gemm p, co
 }
 
 // ---------------------------------------------------------------------------
+// Split-bf16 prefill kernel (no cull, 16-byte aligned operands).
+//
+// gfx950's bf16 matrix cores run ~11x faster than its f32 ones (measured with
+// random operands: v_mfma_f32_32x32x16_bf16 1.8 PFLOP/s, v_mfma_f32_16x16x4_f32
+// 157 TFLOP/s).  Each f32 element x is split into hi = bf16(x) and
+// lo = bf16(x - hi) (x - hi is exact) and every product is taken as
+// hi*hi + hi*lo + lo*hi in f32 accumulation: the dropped lo*lo term and the
+// rounding of lo leave ~2^-16 relative error per product, an order of
+// magnitude inside the MATMUL_F32 bar (1e-4 of the output's largest value).
+//   * 128 x 128 workgroup tile, 2 x 2 waves of 64 x 64 (2 x 2 tiles of
+//     32 x 32), 32-deep k stages, two workgroups per CU;
+//   * the next stage's f32 slices are loaded into registers while the
+//     current stage is multiplied, then split and written to the other LDS
+//     buffer: per operand row (m for A, n for B) 32 k of bf16 as 4 chunks of
+//     16 bytes, hi and lo in separate planes, chunk c of row r at slot
+//     c ^ ((r >> 2) & 3): ds_read_b128 serves 16 lanes at a time from one
+//     256-byte window of banks, and the 16 rows of a quarter wave at one
+//     chunk then hit 16 distinct 16-byte slots of it (measured: the
+//     (r >> 1) & 3 swizzle that only separates 8 rows costs 1.6x);
+//   * an operand stored k-contiguous (A, or B with trans_b) is fetched as 8
+//     consecutive k of one row per item; one stored the other way (B, or A
+//     with trans_a) as 8 rows of k by 2 adjacent columns, so a lane's chunk
+//     is one column's 8 k either way.
+// ---------------------------------------------------------------------------
+namespace x3 {
+constexpr int TM = 128, TN = 128, BK = 32;
+constexpr int kPlane = 128 * BK * 2;                 // bytes of one bf16 plane (128 rows x 32 k)
+constexpr int kStage = 4 * kPlane;                   // A hi, A lo, B hi, B lo
+constexpr int kLds = 2 * kStage;                     // 64 KiB: two stages
+}  // namespace x3
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void split8(const float (&x)[8], v8bf &hi, v8bf &lo)
+{
+    typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        hw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){x[2 * e], x[2 * e + 1]}, v2bf));
+        const float h0 = __builtin_bit_cast(float, hw[e] << 16);
+        const float h1 = __builtin_bit_cast(float, hw[e] & 0xFFFF0000u);
+        lw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){x[2 * e] - h0, x[2 * e + 1] - h1}, v2bf));
+    }
+    hi = __builtin_bit_cast(v8bf, (v4u){hw[0], hw[1], hw[2], hw[3]});
+    lo = __builtin_bit_cast(v8bf, (v4u){lw[0], lw[1], lw[2], lw[3]});
+}
+
+// One operand's share of a stage: two chunks (8 k of one row each).
+struct X3Slice {
+    float x[2][8];
+};
+
+// Operand op(X) viewed as rows (m of A, n of B) x k.  KCONTIG: X[row][k]
+// with leading dimension ld; otherwise X[k][row].
+template <bool KCONTIG>
+__device__ __forceinline__ void x3_fetch(const float *X, uint32_t ld, uint32_t rows, uint32_t K,
+                                         uint32_t r0, uint32_t k0, int tid, X3Slice &s)
+{
+    if (KCONTIG) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t item = tid + 256 * u, r = r0 + (item >> 2), k = k0 + 8 * (item & 3);
+            const float *p = X + static_cast<uint64_t>(r) * ld + k;
+            if (r < rows && k + 8 <= K) {
+                const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+                s.x[u][0] = a.x; s.x[u][1] = a.y; s.x[u][2] = a.z; s.x[u][3] = a.w;
+                s.x[u][4] = b.x; s.x[u][5] = b.y; s.x[u][6] = b.z; s.x[u][7] = b.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s.x[u][e] = (r < rows && k + e < K) ? p[e] : 0.0f;
+            }
+        }
+    } else {
+        const uint32_t r = r0 + 2 * (tid & 63), k = k0 + 8 * (tid >> 6);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float *p = X + static_cast<uint64_t>(k + e) * ld + r;
+            if (k + e < K && r + 1 < rows) {
+                const float2 v = *reinterpret_cast<const float2 *>(p);
+                s.x[0][e] = v.x;
+                s.x[1][e] = v.y;
+            } else {
+                s.x[0][e] = (k + e < K && r < rows) ? p[0] : 0.0f;
+                s.x[1][e] = (k + e < K && r + 1 < rows) ? p[1] : 0.0f;
+            }
+        }
+    }
+}
+
+// Row and chunk of chunk u of this thread's slice (see x3_fetch).
+template <bool KCONTIG>
+__device__ __forceinline__ void x3_chunk(int tid, int u, uint32_t &row, uint32_t &c)
+{
+    if (KCONTIG) {
+        const uint32_t item = tid + 256 * u;
+        row = item >> 2;
+        c = item & 3;
+    } else {
+        row = 2 * (tid & 63) + u;
+        c = tid >> 6;
+    }
+}
+
+template <bool KCONTIG>
+__device__ __forceinline__ void x3_stash(const X3Slice &s, int tid, int8_t *hi_plane)
+{
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        uint32_t row, c;
+        x3_chunk<KCONTIG>(tid, u, row, c);
+        v8bf h, l;
+        split8(s.x[u], h, l);
+        const uint32_t off = row * (x3::BK * 2) + ((c ^ ((row >> 2) & 3)) << 4);
+        *reinterpret_cast<v8bf *>(hi_plane + off) = h;
+        *reinterpret_cast<v8bf *>(hi_plane + x3::kPlane + off) = l;
+    }
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_x3(F32Gemm p)
+{
+    constexpr uint32_t TM = x3::TM, TN = x3::TN, XBK = x3::BK;
+    constexpr int kPlane = x3::kPlane, kStage = x3::kStage;
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    // Tiles run M-fastest, and each XCD (workgroup g runs on XCD g % 8) takes
+    // a contiguous run of them: the XCD's resident workgroups share A's rows
+    // and a few of B's column tiles through its L2.
+    const uint32_t tiles_m = (p.M + TM - 1) / TM, total = tiles_m * ((p.N + TN - 1) / TN);
+    uint32_t g = blockIdx.x;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const uint32_t m0 = (g % tiles_m) * TM, n0 = (g / tiles_m) * TN;
+    const uint32_t KT = (p.K + XBK - 1) / XBK;
+    const int h = lane >> 5, col = lane & 31;
+
+    X3Slice sa, sb;
+    auto fetch = [&](uint32_t kt) {
+        x3_fetch<!TA>(p.A, p.lda, p.M, p.K, m0, kt * XBK, tid, sa);
+        x3_fetch<TB>(p.B, p.ldb, p.N, p.K, n0, kt * XBK, tid, sb);
+    };
+    auto stash = [&](uint32_t kt) {
+        int8_t *st = smem + (kt & 1) * kStage;
+        x3_stash<!TA>(sa, tid, st);
+        x3_stash<TB>(sb, tid, st + 2 * kPlane);
+    };
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16f){0.f};
+
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < KT; ++kt) {
+        const bool more = kt + 1 < KT;
+        if (more) fetch(kt + 1);
+        const int8_t *st = smem + (kt & 1) * kStage;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            // lane (row l%32, half h) reads k 16s + 8h .. +8 of its row
+            v8bf ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t r = wm * 64 + 32 * i + col;
+                const uint32_t off = r * (XBK * 2) + (((2 * s + h) ^ ((r >> 2) & 3)) << 4);
+                ah[i] = *reinterpret_cast<const v8bf *>(st + off);
+                al[i] = *reinterpret_cast<const v8bf *>(st + kPlane + off);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t r = wn * 64 + 32 * j + col;
+                const uint32_t off = r * (XBK * 2) + (((2 * s + h) ^ ((r >> 2) & 3)) << 4);
+                bh[j] = *reinterpret_cast<const v8bf *>(st + 2 * kPlane + off);
+                bl[j] = *reinterpret_cast<const v8bf *>(st + 3 * kPlane + off);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+        }
+        // The other buffer was last read in step kt-1, before the barrier
+        // that ended it; the next barrier publishes the new stage.
+        if (more) stash(kt + 1);
+        __syncthreads();
+    }
+
+    // 32 x 32 accumulator: lane l holds column l%32, rows 8j' + 4(l/32) + i'
+    // in register 4j' + i'; a store instruction writes two 128-byte row runs.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t n = n0 + wn * 64 + 32 * j + col;
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < p.M) store_out(p, m, n, acc[i][j][r], false);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Skinny NN path (M <= 8).
 // ---------------------------------------------------------------------------
 constexpr int kSkinnyCols = 256;  // 64 lanes x float4
@@ -370,14 +589,43 @@ static uint32_t gemm_f32_splits(const F32Gemm &p)
     return tiles >= 128 ? 1 : splits;
 }
 
+// The split-bf16 kernel takes grids of at least 128 tiles without a cull map
+// or a requested K depth, on 16-byte aligned operands.
+static bool use_x3(const F32Gemm &p)
+{
+    const uint64_t tiles = static_cast<uint64_t>((p.M + x3::TM - 1) / x3::TM) * ((p.N + x3::TN - 1) / x3::TN);
+    const bool al = (p.lda % 4 == 0) && (p.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) &&
+                    (reinterpret_cast<uintptr_t>(p.B) % 16 == 0);
+    return !p.cull && !p.ktile_state && p.k_split_depth == 0 && tiles >= 128 && al;
+}
+
 size_t gemm_f32_ws_bytes(const F32Gemm &p)
 {
+    if (use_x3(p)) return 0;
     const uint32_t splits = gemm_f32_splits(p);
     return splits > 1 ? static_cast<size_t>(splits) * p.M * p.N * sizeof(float) : 0;
 }
 
 void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
 {
+    if (use_x3(p)) {
+        static bool lds_optin = false;
+        if (!lds_optin)
+            lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<false, false>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, x3::kLds) == hipSuccess &&
+                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<false, true>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, x3::kLds) == hipSuccess &&
+                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<true, false>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, x3::kLds) == hipSuccess &&
+                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<true, true>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, x3::kLds) == hipSuccess;
+        const dim3 grid(((p.N + x3::TN - 1) / x3::TN) * ((p.M + x3::TM - 1) / x3::TM));
+        if (!p.trans_a && !p.trans_b) gemm_f32_x3<false, false><<<grid, kThreads, x3::kLds, s>>>(p);
+        else if (!p.trans_a) gemm_f32_x3<false, true><<<grid, kThreads, x3::kLds, s>>>(p);
+        else if (!p.trans_b) gemm_f32_x3<true, false><<<grid, kThreads, x3::kLds, s>>>(p);
+        else gemm_f32_x3<true, true><<<grid, kThreads, x3::kLds, s>>>(p);
+        return;
+    }
     const uint32_t want = gemm_f32_splits(p);
     const uint32_t kps = want > 1 ? ((p.K + want - 1) / want + BK - 1) / BK * BK : p.K;
     // Every z slice starts below K (rounding kps up may leave fewer slices).

@@ -193,6 +193,23 @@ def test_matmul_f32(gpu, M, K, N, ta, tb, epi, beta, alpha):
     assert rel(got, want) <= 1e-4
 
 
+@pytest.mark.parametrize("M,K,N,ta,tb,epi,beta", [
+    (1024, 1000, 2176, 0, 0, 2, 0.0), (1024, 1000, 2176, 0, 1, 3, 0.5), (1100, 520, 1920, 1, 0, 1, 0.0),
+    (1100, 520, 1920, 1, 1, 0, 0.5), (2048, 4096, 1024, 0, 1, 3, 0.5), (1030, 37, 2050, 0, 0, 0, 0.0)])
+def test_matmul_f32_split_bf16(gpu, M, K, N, ta, tb, epi, beta):
+    """Grids of >= 128 tiles run the split-bf16 kernel (hi*hi + hi*lo + lo*hi
+    on the bf16 matrix cores): every transpose combination, ragged M / N / K,
+    the config-3 epilogue (bias, beta 0.5 onto C, GELU), to the f32 bar."""
+    A = RNG.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    B = RNG.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    bias = RNG.standard_normal(N).astype(np.float32)
+    C0 = RNG.standard_normal((M, N)).astype(np.float32)
+    got = g.matmul_f32(gpu, A, B, M, K, N, C_in=C0, bias=bias, trans_a=ta, trans_b=tb, beta=beta,
+                       alpha=1.0, epilogue=epi)
+    want = oracle.matmul_f32(A, B, C0, bias, M, K, N, ta, tb, 1.0, beta, epi, acc64=True)
+    assert rel(got, want) <= 1e-4
+
+
 @pytest.mark.parametrize("M,N,unit", [(256, 512, 2), (40, 96, 2), (128, 128, 1), (300, 200, 3),
                                       (4, 300, 0)])
 def test_matmul_f32_wildcat_cull(gpu, M, N, unit):
