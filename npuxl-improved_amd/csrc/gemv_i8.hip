@@ -1,4 +1,4 @@
-// gemv_i8.hip - MATMUL_I8 decode path (M <= 8): HBM-streaming GEMV, no MFMA.
+// gemv_i8.hip - MATMUL_I8 decode path (M <= 8): HBM-streaming GEMV.
 //
 // Replaces the reference's rank-1/rank-R AVX2 decode kernels
 // (src/kernels/kernels.cpp:581-632, 702-767) and their tile rules
@@ -24,7 +24,9 @@
 //   * the activations (M x K int8, tiny) are staged in LDS as [k/16][m][16]
 //     (dynamic LDS sized to the chunk actually used), so lane kg reads its
 //     16 bytes of every row with one ds_read_b128 per row;
-//   * v_dot4_i32_i8 (4 per 16 bytes per row) accumulates in int32;
+//   * v_dot4_i32_i8 (4 per 16 bytes per row) accumulates in int32 for up
+//     to four rows; from five rows one v_mfma_i32_16x16x64_i8 per block
+//     does it (gemv_i8_mfma below);
 //   * lanes of equal c reduce over kg with two cross-lane shuffles, waves
 //     reduce through LDS, and 16*M threads apply the fused epilogue.
 // Blocks flagged all-zero by PACK_WEIGHTS_I8 are streamed like any other: the
@@ -178,27 +180,151 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chun
     }
 }
 
+// The same stream for 3..8 rows with the int8 matrix core doing the math: a
+// packed 1 KiB weight block is exactly the B operand of one
+// v_mfma_i32_16x16x64_i8 (lane 16kg + c holds k 16kg..16kg+15 of column c),
+// and the A operand is the staged activations (lane l: row l%16, the same 16
+// k; rows past M are zero).  One MFMA per block replaces 4M v_dot4 and M
+// ds_read_b128 per lane, which at M = 8 made the VALU the bottleneck.  The
+// 16 x 16 result leaves row 4(l/16) + i, column l%16 in lane l, register i.
+template <int M, int W, int U, int T>
+__global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8Gemm p, uint32_t chunk_k)
+{
+    static_assert(M <= 16, "rows of one 16 x 16 tile");
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    extern __shared__ __attribute__((aligned(16))) int8_t a_lds[];  // [chunk_k/16][M][16]
+    __shared__ int red[W][T][M][16];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = lane >> 4, row = lane & 15;
+    const uint32_t NT = p.Np >> 4;
+    const uint32_t nt0 = blockIdx.x * T;
+    const uint32_t KT = p.Kp >> 6;
+    const bool vec_a = ((p.lda & 15u) == 0) && ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0);
+
+    v4i acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = (v4i){0, 0, 0, 0};
+
+    for (uint32_t kc = 0; kc < p.Kp; kc += chunk_k) {
+        const uint32_t kt0 = kc >> 6, kt1 = min(KT, (kc + chunk_k) >> 6);
+        const uint32_t first = kt0 + wave;
+        const uint32_t cnt = first < kt1 ? (kt1 - first + W - 1) / W : 0;
+        __amdgpu_buffer_rsrc_t rs[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint32_t nt = min(nt0 + t, NT - 1);
+            const int8_t *strip = p.frag + static_cast<uint64_t>(nt) * KT * 1024;
+            const int bytes = (cnt && nt0 + t < NT) ? static_cast<int>(((cnt - 1) * W + 1) * 1024) : 0;
+            rs[t] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(strip) + static_cast<uint64_t>(first) * 1024,
+                                                      0, bytes, kBufferWord3);
+        }
+        auto ld = [&](int t, uint32_t i) {
+            return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                rs[t], i * W * 1024 + lane * 16, 0, kNontemporal));
+        };
+        v4i bc[U][T], bn[U][T];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int t = 0; t < T; ++t) bc[u][t] = ld(t, u);
+
+        if (kc) __syncthreads();  // previous chunk fully consumed
+        const uint32_t chunks = (kt1 - kt0) * 4 * M;
+        for (uint32_t i = tid; i < chunks; i += 64 * W) {
+            const uint32_t m = i % M, k16 = i / M;
+            const uint32_t k = kc + k16 * 16;
+            const int8_t *src = p.A + static_cast<uint64_t>(m) * p.lda + k;
+            int4 v;
+            if (vec_a && k + 16 <= p.K) {
+                v = *reinterpret_cast<const int4 *>(src);
+            } else {
+                union {
+                    int8_t b[16];
+                    int4 v;
+                } u;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) u.b[j] = (k + j < p.K) ? src[j] : 0;
+                v = u.v;
+            }
+            *reinterpret_cast<int4 *>(a_lds + (k16 * M + m) * 16) = v;
+        }
+        __syncthreads();
+
+        for (uint32_t i = 0; i < cnt; i += U) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int t = 0; t < T; ++t) bn[u][t] = ld(t, i + U + u);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t ktl = first + W * min(i + u, cnt - 1) - kt0;
+                v4i a = (v4i){0, 0, 0, 0};
+                if (row < M) a = *reinterpret_cast<const v4i *>(a_lds + ((ktl * 4 + kg) * M + row) * 16);
+#pragma unroll
+                for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bc[u][t], acc[t], 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int t = 0; t < T; ++t) bc[u][t] = bn[u][t];
+        }
+    }
+
+    // Lane l holds rows 4(l/16) + i of column l%16; sum the waves in LDS.
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * kg + i;
+            if (m < M) red[wave][t][m][row] = acc[t][i];
+        }
+    __syncthreads();
+    for (int o = tid; o < T * M * 16; o += 64 * W) {
+        const int c = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
+        const uint32_t n = (nt0 + t) * 16 + c;
+        if (nt0 + t >= NT || n >= p.N) continue;
+        int s = 0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) s += red[w][t][m][c];
+        const float sa = p.scale_a ? p.scale_a[m] : 1.0f;
+        float out = __fmul_rn(__fmul_rn(static_cast<float>(s), sa), p.scale_b[n]);
+        if (p.bias) out = __fadd_rn(out, p.bias[n]);
+        p.C[static_cast<uint64_t>(m) * p.ldc + n] = dev::epilogue(out, p.epilogue);
+    }
+}
+
 // Launch shape (measured on MI355X with the weights streamed from HBM): four
 // waves with eight blocks in flight each for one or two rows; eight waves
-// when strips are few (the grid is one workgroup per strip); from three rows
-// up the activation reads from LDS grow with M, and eight waves with four
-// blocks each keep more of them overlapped; from six rows up, with at least
-// 1024 strips, each workgroup takes four strips so that one activation read
-// from LDS feeds four weight blocks (M=8, N=32000: 30 -> 25-28 us).
+// when strips are few (the grid is one workgroup per strip); for three or
+// four rows eight waves with four blocks each.  From five rows up the matrix
+// core does the math (M=8: N=4096 7.5 -> 6.9 us, 11008 13.2 -> 11.8 us,
+// 32000 27.0 -> 24.3 us; at three and four rows the v_dot4 kernel is as fast
+// or faster), with four strips per workgroup over at least 1024 strips so one
+// staged activation chunk serves four weight streams (two strips per
+// workgroup at 512-1023 strips measured slower: fewer workgroups than CUs).
 template <int M>
 void launch_m(hipStream_t s, const I8Gemm &p)
 {
     const uint32_t NT = p.Np >> 4;
     const uint32_t chunk_k = std::min<uint32_t>(p.Kp, (kLdsA / M) & ~63u);
     const size_t lds = static_cast<size_t>(chunk_k) * M;
-    if (M >= 6 && NT >= 1024)
-        gemv_i8_kernel<M, 4, 4, 4><<<dim3((NT + 3) / 4), 256, lds, s>>>(p, chunk_k);
-    else if (M <= 2 && NT >= 512)
-        gemv_i8_kernel<M, 4, 8, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
-    else if (M <= 2)
-        gemv_i8_kernel<M, 8, 8, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
-    else
+    if constexpr (M >= 5) {
+        if (NT >= 1024)
+            gemv_i8_mfma<M, 4, 4, 4><<<dim3((NT + 3) / 4), 256, lds, s>>>(p, chunk_k);
+        else if (NT >= 512)
+            gemv_i8_mfma<M, 4, 8, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
+        else
+            gemv_i8_mfma<M, 8, 8, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+    } else if constexpr (M >= 3) {
         gemv_i8_kernel<M, 8, 4, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+    } else {
+        if (NT >= 512)
+            gemv_i8_kernel<M, 4, 8, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
+        else
+            gemv_i8_kernel<M, 8, 8, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+    }
 }
 
 }  // namespace
