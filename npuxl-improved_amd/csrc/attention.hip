@@ -190,6 +190,20 @@ __device__ __forceinline__ void merge_stream(float &m, float &l, float &mo, floa
     m = M;
 }
 
+// K and V rows are read once per call: nontemporal loads keep them from
+// displacing the L2's reusable lines.
+__device__ __forceinline__ float4 load_stream(const float4 *p)
+{
+    typedef float nv4 __attribute__((ext_vector_type(4)));
+    const nv4 v = __builtin_nontemporal_load(reinterpret_cast<const nv4 *>(p));
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// A stream's reference point m moves only when a score exceeds it by more
+// than this (weights stay below e^5.5 ~ 256), so acc is rescaled on rare
+// keys only; softmax is invariant to the reference point.
+constexpr float kDecodeLazy = 5.5f;
+
 template <int QN, int V4>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t keys_per_split,
                                                                uint32_t splits, float *ws_acc,
@@ -239,8 +253,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
         const uint32_t key = min(kbeg + stream + step * kStreams, kend - 1);
 #pragma unroll
         for (int t = 0; t < V4; ++t) {
-            kr[t] = Kh[static_cast<uint64_t>(key) * D4 + r + 8 * t];
-            vr[t] = Vh[static_cast<uint64_t>(key) * D4 + r + 8 * t];
+            kr[t] = load_stream(Kh + static_cast<uint64_t>(key) * D4 + r + 8 * t);
+            vr[t] = load_stream(Vh + static_cast<uint64_t>(key) * D4 + r + 8 * t);
         }
     };
     float4 kc[V4], vc[V4], kn[V4], vn[V4];
@@ -266,18 +280,27 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
             if (live) {   // uniform over the 8 lanes of the group
                 float s = dot * a.scale;
                 if (a.mask) s += a.mask[(bh * sq + qi) * sk + key];
-                const float mn = fmaxf(m[i], s);
-                const float al = (m[i] == -__builtin_inff()) ? 0.0f : dev::fast_expf(m[i] - mn);
-                const float p = dev::fast_expf(s - mn);
-                l[i] = fmaf(l[i], al, p);
+                if (s > m[i] + kDecodeLazy) {   // also the first key (m = -inf)
+                    const float al = (m[i] == -__builtin_inff()) ? 0.0f : dev::fast_expf(m[i] - s);
+                    l[i] *= al;
+#pragma unroll
+                    for (int t = 0; t < V4; ++t) {
+                        acc[i][t].x *= al;
+                        acc[i][t].y *= al;
+                        acc[i][t].z *= al;
+                        acc[i][t].w *= al;
+                    }
+                    m[i] = s;
+                }
+                const float p = dev::fast_expf(s - m[i]);
+                l[i] += p;
 #pragma unroll
                 for (int t = 0; t < V4; ++t) {
-                    acc[i][t].x = fmaf(p, vc[t].x, acc[i][t].x * al);
-                    acc[i][t].y = fmaf(p, vc[t].y, acc[i][t].y * al);
-                    acc[i][t].z = fmaf(p, vc[t].z, acc[i][t].z * al);
-                    acc[i][t].w = fmaf(p, vc[t].w, acc[i][t].w * al);
+                    acc[i][t].x = fmaf(p, vc[t].x, acc[i][t].x);
+                    acc[i][t].y = fmaf(p, vc[t].y, acc[i][t].y);
+                    acc[i][t].z = fmaf(p, vc[t].z, acc[i][t].z);
+                    acc[i][t].w = fmaf(p, vc[t].w, acc[i][t].w);
                 }
-                m[i] = mn;
             }
         }
 #pragma unroll
