@@ -257,10 +257,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
             vr[t] = load_stream(Vh + static_cast<uint64_t>(key) * D4 + r + 8 * t);
         }
     };
-    float4 kc[V4], vc[V4], kn[V4], vn[V4];
-    if (nsteps) load(0, kc, vc);
-    for (uint32_t step = 0; step < nsteps; ++step) {
-        if (step + 1 < nsteps) load(step + 1, kn, vn);
+    // One key step: this stream's key kbeg + stream + 32 step.
+    auto consume = [&](uint32_t step, const float4 (&kc)[V4], const float4 (&vc)[V4]) {
         const uint32_t key = kbeg + stream + step * kStreams;
 #pragma unroll
         for (int i = 0; i < QN; ++i) {
@@ -303,11 +301,22 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
                 }
             }
         }
-#pragma unroll
-        for (int t = 0; t < V4; ++t) {
-            kc[t] = kn[t];
-            vc[t] = vn[t];
-        }
+    };
+    // Three register sets in rotation: while one step is consumed the next
+    // two are in flight.
+    float4 k0[V4], v0[V4], k1[V4], v1[V4], k2[V4], v2[V4];
+    if (nsteps > 0) load(0, k0, v0);
+    if (nsteps > 1) load(1, k1, v1);
+    if (nsteps > 2) load(2, k2, v2);
+    for (uint32_t step = 0; step < nsteps; step += 3) {
+        consume(step, k0, v0);
+        if (step + 3 < nsteps) load(step + 3, k0, v0);
+        if (step + 1 >= nsteps) break;
+        consume(step + 1, k1, v1);
+        if (step + 4 < nsteps) load(step + 4, k1, v1);
+        if (step + 2 >= nsteps) break;
+        consume(step + 2, k2, v2);
+        if (step + 5 < nsteps) load(step + 5, k2, v2);
     }
 
     // Merge the 8 groups of the wave (lanes differing in bits 3..5), then
