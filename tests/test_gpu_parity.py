@@ -103,8 +103,9 @@ def test_matmul_i8_bit_exact(gpu, M, K, N):
 @pytest.mark.parametrize("M,K,N", [(2048, 256, 12288), (2304, 384, 11000), (2048, 128, 12288),
                                    (4096, 256, 4096)])
 def test_matmul_i8_wide_tile(gpu, M, K, N):
-    """Grids of >= 256 whole 256 x 256 tiles take the wide-tile kernel
-    (1, 2 and 3 k stages; a ragged last column tile).  Every output is
+    """Whole 256-row tiles take the wide-tile kernels (256 x 256 for 4096 and
+    11000 columns, 256 x 192 for 12288; 1, 2 and 3 k stages; a ragged last
+    column tile).  Every output is
     checked: the float64 product of int8 matrices is the exact int32
     accumulator here, and C = ((float)acc * sa) * sb rounds each product
     once in float32, as the oracle's matmul_i8 does."""
@@ -226,7 +227,8 @@ def test_matmul_f32_wildcat_cull(gpu, M, N, unit):
 
 
 # ---------------------------------------------------------------- row / elementwise ops
-@pytest.mark.parametrize("rows,cols", [(1, 7), (7, 300), (64, 4096), (3, 32000)])
+@pytest.mark.parametrize("rows,cols", [(1, 7), (7, 300), (64, 4096), (3, 32000), (5, 11008), (2, 12288),
+                                       (3, 12292)])
 def test_rmsnorm_softmax(gpu, rows, cols):
     X = RNG.standard_normal((rows, cols)).astype(np.float32)
     W = RNG.standard_normal(cols).astype(np.float32)
