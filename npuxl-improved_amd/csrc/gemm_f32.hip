@@ -244,10 +244,10 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_splitk_reduce(F32Gemm p, co
 //     is one column's 8 k either way.
 // ---------------------------------------------------------------------------
 namespace x3 {
-constexpr int TM = 128, TN = 128, BK = 32;
-constexpr int kPlane = 128 * BK * 2;                 // bytes of one bf16 plane (128 rows x 32 k)
-constexpr int kStage = 4 * kPlane;                   // A hi, A lo, B hi, B lo
-constexpr int kLds = 2 * kStage;                     // 64 KiB: two stages
+constexpr int TN = 128, BK = 32;
+// Two stages of A hi, A lo (64*WM rows) and B hi, B lo (128 rows), 32 k of
+// bf16 per row: 64 KiB for WM = 2, 96 KiB for WM = 4.
+constexpr int lds_bytes(int wm) { return 2 * (2 * 64 * wm + 2 * TN) * BK * 2; }
 }  // namespace x3
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -270,21 +270,53 @@ __device__ __forceinline__ void split8(const float (&x)[8], v8bf &hi, v8bf &lo)
     lo = __builtin_bit_cast(v8bf, (v4u){lw[0], lw[1], lw[2], lw[3]});
 }
 
-// One operand's share of a stage: two chunks (8 k of one row each).
+// One operand's share of a stage: up to two chunks (8 k of one row each).
 struct X3Slice {
     float x[2][8];
 };
 
-// Operand op(X) viewed as rows (m of A, n of B) x k.  KCONTIG: X[row][k]
-// with leading dimension ld; otherwise X[k][row].
-template <bool KCONTIG>
+// Operand op(X) viewed as R rows (m of A, n of B) x k, fetched by NT
+// threads.  KCONTIG: X[row][k] with leading dimension ld, item i = (row i/4,
+// chunk i%4), 4R/NT items per thread.  Otherwise X[k][row]: item i = (rows
+// 2p, 2p+1 with p = i % (R/2), chunk i / (R/2)), two chunks per item, one item
+// per thread for the first 2R threads.
+template <bool KCONTIG, int R, int NT>
+__device__ __forceinline__ constexpr int x3_chunks()
+{
+    return KCONTIG ? 4 * R / NT : 2;
+}
+
+template <bool KCONTIG, int R, int NT>
+__device__ __forceinline__ bool x3_active(int tid)
+{
+    return KCONTIG || tid < 2 * R;
+}
+
+template <bool KCONTIG, int R, int NT>
+__device__ __forceinline__ void x3_chunk(int tid, int u, uint32_t &row, uint32_t &c)
+{
+    if (KCONTIG) {
+        const uint32_t item = tid + NT * u;
+        row = item >> 2;
+        c = item & 3;
+    } else {
+        row = 2 * (tid % (R / 2)) + u;
+        c = tid / (R / 2);
+    }
+}
+
+template <bool KCONTIG, int R, int NT>
 __device__ __forceinline__ void x3_fetch(const float *X, uint32_t ld, uint32_t rows, uint32_t K,
                                          uint32_t r0, uint32_t k0, int tid, X3Slice &s)
 {
+    static_assert(x3_chunks<KCONTIG, R, NT>() >= 1 && x3_chunks<KCONTIG, R, NT>() <= 2, "slice size");
+    if (!x3_active<KCONTIG, R, NT>(tid)) return;
     if (KCONTIG) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const uint32_t item = tid + 256 * u, r = r0 + (item >> 2), k = k0 + 8 * (item & 3);
+        for (int u = 0; u < x3_chunks<KCONTIG, R, NT>(); ++u) {
+            uint32_t row, c;
+            x3_chunk<KCONTIG, R, NT>(tid, u, row, c);
+            const uint32_t r = r0 + row, k = k0 + 8 * c;
             const float *p = X + static_cast<uint64_t>(r) * ld + k;
             if (r < rows && k + 8 <= K) {
                 const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
@@ -296,7 +328,9 @@ __device__ __forceinline__ void x3_fetch(const float *X, uint32_t ld, uint32_t r
             }
         }
     } else {
-        const uint32_t r = r0 + 2 * (tid & 63), k = k0 + 8 * (tid >> 6);
+        uint32_t row, c;
+        x3_chunk<KCONTIG, R, NT>(tid, 0, row, c);
+        const uint32_t r = r0 + row, k = k0 + 8 * c;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const float *p = X + static_cast<uint64_t>(k + e) * ld + r;
@@ -312,40 +346,33 @@ __device__ __forceinline__ void x3_fetch(const float *X, uint32_t ld, uint32_t r
     }
 }
 
-// Row and chunk of chunk u of this thread's slice (see x3_fetch).
-template <bool KCONTIG>
-__device__ __forceinline__ void x3_chunk(int tid, int u, uint32_t &row, uint32_t &c)
+// hi plane at hi_plane, lo plane plane_bytes after it.
+template <bool KCONTIG, int R, int NT>
+__device__ __forceinline__ void x3_stash(const X3Slice &s, int tid, int8_t *hi_plane, int plane_bytes)
 {
-    if (KCONTIG) {
-        const uint32_t item = tid + 256 * u;
-        row = item >> 2;
-        c = item & 3;
-    } else {
-        row = 2 * (tid & 63) + u;
-        c = tid >> 6;
-    }
-}
-
-template <bool KCONTIG>
-__device__ __forceinline__ void x3_stash(const X3Slice &s, int tid, int8_t *hi_plane)
-{
+    if (!x3_active<KCONTIG, R, NT>(tid)) return;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < x3_chunks<KCONTIG, R, NT>(); ++u) {
         uint32_t row, c;
-        x3_chunk<KCONTIG>(tid, u, row, c);
+        x3_chunk<KCONTIG, R, NT>(tid, u, row, c);
         v8bf h, l;
         split8(s.x[u], h, l);
         const uint32_t off = row * (x3::BK * 2) + ((c ^ ((row >> 2) & 3)) << 4);
         *reinterpret_cast<v8bf *>(hi_plane + off) = h;
-        *reinterpret_cast<v8bf *>(hi_plane + x3::kPlane + off) = l;
+        *reinterpret_cast<v8bf *>(hi_plane + plane_bytes + off) = l;
     }
 }
 
-template <bool TA, bool TB>
-__global__ __launch_bounds__(kThreads, 2) void gemm_f32_x3(F32Gemm p)
+// WM wave rows: the tile is 64*WM x 128 (WM = 2: four waves, two workgroups
+// per CU; WM = 4: eight waves, one workgroup per CU, each A slice converted
+// once for twice the columns... the B slice once for twice the rows).
+template <bool TA, bool TB, int WM>
+__global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p)
 {
-    constexpr uint32_t TM = x3::TM, TN = x3::TN, XBK = x3::BK;
-    constexpr int kPlane = x3::kPlane, kStage = x3::kStage;
+    constexpr uint32_t TM = 64 * WM, TN = x3::TN, XBK = x3::BK;
+    constexpr int NT = 128 * WM;
+    constexpr int kPlaneA = TM * XBK * 2, kPlaneB = TN * XBK * 2;
+    constexpr int kStage = 2 * kPlaneA + 2 * kPlaneB;
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -360,15 +387,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_x3(F32Gemm p)
     const uint32_t KT = (p.K + XBK - 1) / XBK;
     const int h = lane >> 5, col = lane & 31;
 
+    // The next stage's f32 slices load into registers while this stage is
+    // multiplied, then are split into the other LDS buffer.
     X3Slice sa, sb;
     auto fetch = [&](uint32_t kt) {
-        x3_fetch<!TA>(p.A, p.lda, p.M, p.K, m0, kt * XBK, tid, sa);
-        x3_fetch<TB>(p.B, p.ldb, p.N, p.K, n0, kt * XBK, tid, sb);
+        x3_fetch<!TA, TM, NT>(p.A, p.lda, p.M, p.K, m0, kt * XBK, tid, sa);
+        x3_fetch<TB, TN, NT>(p.B, p.ldb, p.N, p.K, n0, kt * XBK, tid, sb);
     };
     auto stash = [&](uint32_t kt) {
         int8_t *st = smem + (kt & 1) * kStage;
-        x3_stash<!TA>(sa, tid, st);
-        x3_stash<TB>(sb, tid, st + 2 * kPlane);
+        x3_stash<!TA, TM, NT>(sa, tid, st, kPlaneA);
+        x3_stash<TB, TN, NT>(sb, tid, st + 2 * kPlaneA, kPlaneB);
     };
 
     v16f acc[2][2];
@@ -393,14 +422,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_x3(F32Gemm p)
                 const uint32_t r = wm * 64 + 32 * i + col;
                 const uint32_t off = r * (XBK * 2) + (((2 * s + h) ^ ((r >> 2) & 3)) << 4);
                 ah[i] = *reinterpret_cast<const v8bf *>(st + off);
-                al[i] = *reinterpret_cast<const v8bf *>(st + kPlane + off);
+                al[i] = *reinterpret_cast<const v8bf *>(st + kPlaneA + off);
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const uint32_t r = wn * 64 + 32 * j + col;
                 const uint32_t off = r * (XBK * 2) + (((2 * s + h) ^ ((r >> 2) & 3)) << 4);
-                bh[j] = *reinterpret_cast<const v8bf *>(st + 2 * kPlane + off);
-                bl[j] = *reinterpret_cast<const v8bf *>(st + 3 * kPlane + off);
+                bh[j] = *reinterpret_cast<const v8bf *>(st + 2 * kPlaneA + off);
+                bl[j] = *reinterpret_cast<const v8bf *>(st + 2 * kPlaneA + kPlaneB + off);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -589,14 +618,36 @@ static uint32_t gemm_f32_splits(const F32Gemm &p)
     return tiles >= 128 ? 1 : splits;
 }
 
-// The split-bf16 kernel takes grids of at least 128 tiles without a cull map
-// or a requested K depth, on 16-byte aligned operands.
+// The split-bf16 kernel takes grids of at least 128 tiles of 128 x 128
+// without a cull map or a requested K depth, on 16-byte aligned operands.
 static bool use_x3(const F32Gemm &p)
 {
-    const uint64_t tiles = static_cast<uint64_t>((p.M + x3::TM - 1) / x3::TM) * ((p.N + x3::TN - 1) / x3::TN);
+    const uint64_t tiles = static_cast<uint64_t>((p.M + 127) / 128) * ((p.N + x3::TN - 1) / x3::TN);
     const bool al = (p.lda % 4 == 0) && (p.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) &&
                     (reinterpret_cast<uintptr_t>(p.B) % 16 == 0);
     return !p.cull && !p.ktile_state && p.k_split_depth == 0 && tiles >= 128 && al;
+}
+
+template <int WM>
+static void launch_x3(hipStream_t s, const F32Gemm &p)
+{
+    static bool lds_optin = false;
+    constexpr int lds = x3::lds_bytes(WM);
+    if (!lds_optin)
+        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<false, false, WM>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<false, true, WM>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<true, false, WM>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<true, true, WM>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess;
+    const dim3 grid(((p.N + x3::TN - 1) / x3::TN) * ((p.M + 64 * WM - 1) / (64 * WM)));
+    const dim3 block(128 * WM);
+    if (!p.trans_a && !p.trans_b) gemm_f32_x3<false, false, WM><<<grid, block, lds, s>>>(p);
+    else if (!p.trans_a) gemm_f32_x3<false, true, WM><<<grid, block, lds, s>>>(p);
+    else if (!p.trans_b) gemm_f32_x3<true, false, WM><<<grid, block, lds, s>>>(p);
+    else gemm_f32_x3<true, true, WM><<<grid, block, lds, s>>>(p);
 }
 
 size_t gemm_f32_ws_bytes(const F32Gemm &p)
@@ -609,21 +660,12 @@ size_t gemm_f32_ws_bytes(const F32Gemm &p)
 void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
 {
     if (use_x3(p)) {
-        static bool lds_optin = false;
-        if (!lds_optin)
-            lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<false, false>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, x3::kLds) == hipSuccess &&
-                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<false, true>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, x3::kLds) == hipSuccess &&
-                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<true, false>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, x3::kLds) == hipSuccess &&
-                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<true, true>),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, x3::kLds) == hipSuccess;
-        const dim3 grid(((p.N + x3::TN - 1) / x3::TN) * ((p.M + x3::TM - 1) / x3::TM));
-        if (!p.trans_a && !p.trans_b) gemm_f32_x3<false, false><<<grid, kThreads, x3::kLds, s>>>(p);
-        else if (!p.trans_a) gemm_f32_x3<false, true><<<grid, kThreads, x3::kLds, s>>>(p);
-        else if (!p.trans_b) gemm_f32_x3<true, false><<<grid, kThreads, x3::kLds, s>>>(p);
-        else gemm_f32_x3<true, true><<<grid, kThreads, x3::kLds, s>>>(p);
+        // 256 x 128 tiles (eight waves) when they still give every CU one:
+        // each workgroup splits an A slice once for 128 columns and a B slice
+        // once for 256 rows (a quarter less conversion per MFMA).
+        const uint64_t tiles256 = static_cast<uint64_t>((p.M + 255) / 256) * ((p.N + x3::TN - 1) / x3::TN);
+        if (tiles256 >= 256) launch_x3<4>(s, p);
+        else launch_x3<2>(s, p);
         return;
     }
     const uint32_t want = gemm_f32_splits(p);
