@@ -796,12 +796,19 @@ __global__ __launch_bounds__(PThreads) void attn_prefill_kernel(Attn a, uint32_t
                                                                 const int8_t *split)
 {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
-    const uint64_t bh = blockIdx.y;
-    const uint32_t heavy = nqb - 1 - blockIdx.x;
+    // Workgroup g runs on XCD g % 8: give each XCD a contiguous run of
+    // (query block, head) pairs, so the workgroups of one head share its
+    // split K / V blocks through one L2 instead of fetching them once per XCD.
+    const uint32_t nx = gridDim.x, total = nx * gridDim.y;
+    uint32_t g = blockIdx.x + nx * blockIdx.y;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const uint32_t bx = g % nx;
+    const uint64_t bh = g / nx;
+    const uint32_t heavy = nqb - 1 - bx;
     prefill_block<D>(a, heavy * PQ, bh, nkb, split, lds);
-    if (gridDim.x < nqb && blockIdx.x != heavy) {
+    if (nx < nqb && bx != heavy) {
         __syncthreads();  // the output staging of the first block is read out
-        prefill_block<D>(a, blockIdx.x * PQ, bh, nkb, split, lds);
+        prefill_block<D>(a, bx * PQ, bh, nkb, split, lds);
     }
 }
 
