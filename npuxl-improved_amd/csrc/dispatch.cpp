@@ -417,6 +417,75 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     st.flops += 2ull * in.M * in.K * in.N;
 }
 
+}  // namespace
+
+// Two MATMUL_I8 commands in a row, on device-resident data, with the same M
+// and neither reading nor writing what the other writes (the block's gate and
+// up projections): one wide-tile grid when that runs fewer whole rounds of
+// tiles (k::gemm_i8_pair).  Returns false, having launched nothing, when the
+// pair does not qualify; the commands then run one by one as usual.
+bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &c0,
+                      const vnpu_command_t &c1, uint32_t flags, ExecStats &st0, ExecStats &st1)
+{
+    if (c0.opcode != VNPU_OP_MATMUL_I8 || c1.opcode != VNPU_OP_MATMUL_I8) return false;
+    const vnpu_matmul_i8_args_t *in[2] = {&c0.args.matmul_i8, &c1.args.matmul_i8};
+    k::I8Gemm p[2];
+    struct Range {
+        uintptr_t lo = 0, hi = 0;
+        bool overlaps(const Range &o) const { return lo < o.hi && o.lo < hi; }
+    };
+    Range ra[2], rc[2], rs[2], rb[2];
+    const uint32_t variant =
+        k::gemm_i8_variant_for_tiles(dev->tile_m.load(), dev->tile_k.load(), dev->tile_n.load());
+    for (int i = 0; i < 2; ++i) {
+        const vnpu_matmul_i8_args_t &a = *in[i];
+        const vnpu_packed_weights_t *w = a.B;
+        if (!a.A || !w || !a.C || a.M <= 8 || !a.K || !a.N) return false;
+        if (w->K != a.K || w->N != a.N || a.epilogue > VNPU_EPILOGUE_GELU_ERF) return false;
+        if (w->device && w->device->hip_device != dev->hip_device) return false;
+        const uint32_t lda = a.lda ? a.lda : a.K, ldc = a.ldc ? a.ldc : a.N;
+        if (lda < a.K || ldc < a.N) return false;
+        if (!is_device_pointer(a.A) || !is_device_pointer(a.C) || (a.scale_a && !is_device_pointer(a.scale_a)) ||
+            (a.bias && !is_device_pointer(a.bias)))
+            return false;
+        k::I8Gemm &q = p[i];
+        q.A = a.A; q.lda = lda; q.frag = w->frag;
+        q.zero_blocks = w->zero_block_count ? w->zero_blocks : nullptr;
+        q.Kp = w->Kp; q.Np = w->Np; q.scale_a = a.scale_a; q.scale_b = w->scales_dev; q.bias = a.bias;
+        q.C = a.C; q.ldc = ldc; q.M = a.M; q.N = a.N; q.K = a.K; q.epilogue = a.epilogue; q.variant = variant;
+        auto range = [](const void *ptr, size_t bytes) {
+            Range r;
+            r.lo = reinterpret_cast<uintptr_t>(ptr);
+            r.hi = r.lo + bytes;
+            return r;
+        };
+        ra[i] = range(a.A, span(a.M, a.K, lda, 1));
+        rc[i] = range(a.C, span(a.M, a.N, ldc, 4));
+        rs[i] = a.scale_a ? range(a.scale_a, static_cast<size_t>(a.M) * 4) : Range{};
+        rb[i] = a.bias ? range(a.bias, static_cast<size_t>(a.N) * 4) : Range{};
+    }
+    for (int i = 0; i < 2; ++i) {
+        const int o = 1 - i;
+        if (rc[i].overlaps(ra[o]) || rc[i].overlaps(rs[o]) || rc[i].overlaps(rb[o]) || rc[i].overlaps(rc[o]))
+            return false;
+    }
+    if (!k::gemm_i8_pair(s->hip, p[0], p[1])) return false;
+    VNPU_HIP(hipGetLastError());
+    ExecStats *st[2] = {&st0, &st1};
+    for (int i = 0; i < 2; ++i) {
+        const vnpu_matmul_i8_args_t &a = *in[i];
+        st[i]->unit = choose_unit(a.unit, false, flags);
+        st[i]->tiles_dispatched += 1;
+        st[i]->bytes_read += static_cast<uint64_t>(a.M) * a.K + static_cast<uint64_t>(a.K) * a.N +
+                             static_cast<uint64_t>(a.N + (a.scale_a ? a.M : 0)) * 4;
+        st[i]->bytes_written += static_cast<uint64_t>(a.M) * a.N * 4;
+        st[i]->flops += 2ull * a.M * a.K * a.N;
+    }
+    return true;
+}
+
+namespace {
+
 void exec_quantize(vnpu_device_t *, vnpu_stream_t *s, const vnpu_quantize_i8_args_t &a,
                    ExecStats &st)
 {

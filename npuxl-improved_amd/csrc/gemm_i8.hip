@@ -727,7 +727,11 @@ struct FragsW {
 };
 
 template <int TN>
-__global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
+// ps[0] and ps[1]: up to two independent problems with the same M in one
+// grid (tiles_n0 and tiles_n1 column tiles; tiles_n1 = 0 for one problem),
+// so the tiles of both fill whole rounds of CUs together.
+__global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t tiles_m, uint32_t tiles_n0,
+                                                         uint32_t tiles_n1)
 {
     using namespace wide;
     using G = Cfg<TN>;
@@ -739,9 +743,12 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8Gemm p, uint32_t tile
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
 
-    const uint32_t total = tiles_m * tiles_n;
+    const uint32_t first = tiles_m * tiles_n0, total = first + tiles_m * tiles_n1;
     uint32_t g = blockIdx.x;
     if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const bool second = g >= first;
+    const I8Gemm &p = second ? ps.p[1] : ps.p[0];
+    if (second) g -= first;
     const uint32_t tmi = g % tiles_m, tni = g / tiles_m;
     const uint32_t m0 = tmi * TM, n0 = tni * TN;
     const uint32_t NT = p.Np >> 4;
@@ -986,10 +993,12 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
     }
     switch (v) {
     case kI8Wide:
-        gemm_i8_wide<256><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds, s>>>(p, wm_, wn256);
+        gemm_i8_wide<256><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
+                                                                                   wn256, 0);
         return;
     case kI8Wide192:
-        gemm_i8_wide<192><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds, s>>>(p, wm_, wn192);
+        gemm_i8_wide<192><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
+                                                                                   wn192, 0);
         return;
     case kI8Wave8:
         if (p.zero_blocks) {
@@ -1015,6 +1024,37 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
         return;
     }
     }
+}
+
+bool gemm_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1)
+{
+    auto wide_ok = [](const I8Gemm &p) {
+        return p.K % 64 == 0 && p.lda % 16 == 0 && reinterpret_cast<uintptr_t>(p.A) % 16 == 0 && p.M >= 64 &&
+               p.K <= 16384 && p.K % pipe128::SK == 0 && !p.zero_blocks && p.M % wide::TM == 0 &&
+               p.variant == kI8Auto;
+    };
+    if (p0.M != p1.M || !wide_ok(p0) || !wide_ok(p1)) return false;
+    // One grid of 256 x 256 tiles only when its whole rounds beat the two
+    // grids the automatic choice would run one after the other.
+    const uint32_t cus = cu_count();
+    const uint32_t wm_ = p0.M / wide::TM;
+    auto alone = [&](const I8Gemm &p) {
+        const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM, tn = (p.N + pipe::TN - 1) / pipe::TN;
+        const double c8 = tile_cost(static_cast<uint64_t>(tm) * tn, cus, 256, 128, 1.4);
+        const double c256 = tile_cost(static_cast<uint64_t>(wm_) * ((p.N + 255) / 256), cus, 256, 256, 1.0);
+        const double c192 = tile_cost(static_cast<uint64_t>(wm_) * ((p.N + 191) / 192), cus, 256, 192, 1.2);
+        return std::min(c8, std::min(c256, c192));
+    };
+    const uint32_t tn0 = (p0.N + 255) / 256, tn1 = (p1.N + 255) / 256;
+    const double together = tile_cost(static_cast<uint64_t>(wm_) * (tn0 + tn1), cus, 256, 256, 1.0);
+    if (together >= alone(p0) + alone(p1)) return false;
+    static bool lds_optin = false;
+    if (!lds_optin)
+        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_i8_wide<256>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    gemm_i8_wide<256><<<dim3(wm_ * (tn0 + tn1)), kThreads, wide::Cfg<256>::kLds, s>>>(I8GemmPair{{p0, p1}}, wm_,
+                                                                                      tn0, tn1);
+    return true;
 }
 
 }  // namespace k

@@ -46,6 +46,9 @@ struct I8Gemm {
     uint32_t epilogue = 0;
     uint32_t variant = 0;            // kI8*: which prefill kernel (0 = choose)
 };
+struct I8GemmPair {
+    I8Gemm p[2];
+};
 // Prefill kernels (gemm_i8.hip): a requested one that cannot take the shape
 // falls back to the automatic choice.
 enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generic = 4, kI8Wide192 = 5 };
@@ -55,6 +58,10 @@ enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generi
 uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t tile_n);
 void gemv_i8(hipStream_t s, const I8Gemm &p);  // M <= 8, no MFMA
 void gemm_i8(hipStream_t s, const I8Gemm &p);  // any M, int8 MFMA
+// Two independent MATMUL_I8 problems with the same M in one wide-tile grid
+// when that runs fewer whole rounds of tiles; false (nothing launched) when
+// either cannot take the wide kernel or one grid would not be faster.
+bool gemm_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1);
 
 // ---- MATMUL_F32 (gemm_f32.hip) ----
 struct F32Gemm {

@@ -727,9 +727,46 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
         if (stream->batch_timing.size() >= 256) stream->resolve_timing(false);
         hipEvent_t batch_start = stream->acquire_event();
         if (batch_start) (void)hipEventRecord(batch_start, stream->hip);
+        auto account = [&](const ExecStats &st, uint64_t host) {
+            d->dispatch_ns.fetch_add(host);
+            d->bytes_read.fetch_add(st.bytes_read);
+            d->bytes_written.fetch_add(st.bytes_written);
+            d->flops.fetch_add(st.flops);
+            d->dma_bytes.fetch_add(st.dma_bytes);
+            d->tiles_dispatched.fetch_add(st.tiles_dispatched);
+            d->tiles_culled.fetch_add(st.tiles_culled);
+        };
         for (uint64_t i = 0; i < count; ++i) {
             const vnpu_command_t &cmd = commands[i];
             const uint64_t t0 = now_ns();
+            // Two independent MATMUL_I8 in a row may share one launch (not
+            // while tracing, which times every command on the GPU).
+            if (!tracing && i + 1 < count && cmd.opcode == VNPU_OP_MATMUL_I8 &&
+                commands[i + 1].opcode == VNPU_OP_MATMUL_I8) {
+                ExecStats s0, s1;
+                bool paired = false;
+                try {
+                    paired = try_execute_pair(d, stream, cmd, commands[i + 1], flags, s0, s1);
+                } catch (const std::exception &ex) {
+                    debug_log("paired matmul_i8 failed: %s", ex.what());
+                    (void)hipGetLastError();
+                    batch_status = VNPU_ERR_INTERNAL;
+                    const uint32_t code = static_cast<uint32_t>(-VNPU_ERR_INTERNAL);
+                    d->error.store(code);
+                    d->regs[VNPU_REG_ERROR / 4].store(code);
+                    stream->last_error.store(code);
+                    ++i;
+                    continue;
+                }
+                if (paired) {
+                    d->last_opcode.store(VNPU_OP_MATMUL_I8);
+                    const uint64_t host = now_ns() - t0;
+                    account(s0, host / 2);
+                    account(s1, host - host / 2);
+                    ++i;
+                    continue;
+                }
+            }
             TraceRecord rec;
             if (tracing) {
                 {
@@ -754,16 +791,10 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
                 }
             }
             const uint64_t host = now_ns() - t0;
-            d->dispatch_ns.fetch_add(host);
             const uint32_t cat = trace_category(cmd.opcode);
             if (cat == 1) d->memory_ns.fetch_add(host);
             if (cat == 2) d->sync_ns.fetch_add(host);
-            d->bytes_read.fetch_add(st.bytes_read);
-            d->bytes_written.fetch_add(st.bytes_written);
-            d->flops.fetch_add(st.flops);
-            d->dma_bytes.fetch_add(st.dma_bytes);
-            d->tiles_dispatched.fetch_add(st.tiles_dispatched);
-            d->tiles_culled.fetch_add(st.tiles_culled);
+            account(st, host);
             if (tracing) {
                 if (create_timing_event(&rec.stop) == hipSuccess) (void)hipEventRecord(rec.stop, stream->hip);
                 rec.opcode = cmd.opcode;

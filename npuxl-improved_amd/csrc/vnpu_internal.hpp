@@ -189,6 +189,8 @@ struct ExecStats {
 
 // Executes one command on the stream (enqueue only).  Throws ArgError for
 // invalid arguments and HipError for runtime failures.
+bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &c0,
+                      const vnpu_command_t &c1, uint32_t flags, ExecStats &st0, ExecStats &st1);
 void execute_command(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &cmd,
                      uint32_t batch_flags, ExecStats &st);
 

@@ -121,6 +121,43 @@ def test_matmul_i8_wide_tile(gpu, M, K, N):
     assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("N0,N1,alias", [(3000, 2000, False), (11008, 11008, False), (1000, 700, True)])
+def test_matmul_i8_pair_in_one_batch(gpu, N0, N1, alias):
+    """Two MATMUL_I8 commands in one batch with the same M (the block's gate
+    and up projections) may share one wide-tile launch; both outputs must be
+    the oracle's bits, with their own bias and epilogue.  With `alias` the
+    second command reads the first one's output as its A (a dependency),
+    which must keep them in order."""
+    M, K = 512, 256
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B0 = RNG.integers(-128, 128, size=(K, N0)).astype(np.int8)
+    B1 = RNG.integers(-128, 128, size=(K if not alias else 256, N1)).astype(np.int8)
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb0 = (RNG.random(N0).astype(np.float32) + 0.5) / 127
+    sb1 = (RNG.random(N1).astype(np.float32) + 0.5) / 127
+    bias1 = RNG.standard_normal(N1).astype(np.float32)
+    w0, w1 = gpu.pack(B0, K, N0, scales=sb0), gpu.pack(B1, 256, N1, scales=sb1)
+    ba, bsa = gpu.upload(A), gpu.upload(sa)
+    bc0, bc1, bb1 = gpu.alloc(4 * M * N0), gpu.alloc(4 * M * N1), gpu.upload(bias1)
+    # alias: the second GEMM's A is the first GEMM's output bytes (int8 view)
+    a1 = bc0 if alias else ba
+    cmds = [gpu.command(abi.OP_MATMUL_I8, A=ba, B=w0, scale_a=bsa.ptr, C=bc0, M=M, K=K, N=N0),
+            gpu.command(abi.OP_MATMUL_I8, A=a1, B=w1, scale_a=bsa.ptr, bias=bb1.ptr, C=bc1, M=M, K=256,
+                        N=N1, lda=4 * N0 if alias else 0, epilogue=2)]
+    assert gpu.submit(cmds) == abi.OK and gpu.sync() == abi.OK
+    c0 = gpu.download(bc0, np.float32, (M, N0))
+    c1 = gpu.download(bc1, np.float32, (M, N1))
+    for b in (ba, bsa, bc0, bc1, bb1):
+        gpu.free(b)
+    gpu.release_packed(w0)
+    gpu.release_packed(w1)
+    want0 = oracle.matmul_i8(A, B0, sa, sb0)
+    assert np.array_equal(c0.view(np.uint32), want0.view(np.uint32))
+    A1 = want0.view(np.int8).reshape(M, 4 * N0)[:, :256] if alias else A
+    want1 = oracle.matmul_i8(A1, B1, sa, sb1, bias1, 2)
+    assert rel(c1, want1) <= 1e-4
+
+
 @pytest.mark.parametrize("M", [1, 6, 40])
 def test_matmul_i8_accumulator_exact(gpu, M):
     # scale 1 everywhere: C == (float)acc exactly while |acc| < 2^24
