@@ -15,7 +15,8 @@ duration behind `roofline.achieved`).
 
 Also printed (same line, key "extras"): the rest of config 2 (M in {1,4,8} x
 N in {4096,11008,32000}), config 1 (512^3 int8 and f32+SiLU), config 3 (int8
-and f32 prefill GEMMs), config 4 (one Llama-style layer: prefill tokens/s at
+and f32 prefill GEMMs), config 4 (its attention calls alone, and one Llama-style
+layer: prefill tokens/s at
 batch 1 x 2048 and decode tokens/s at batch 8, context 4096) and config 5
 (int8 GEMM over half-zero weight tiles, MTP head + softmax).  The CPU
 baseline is the reference runtime built from its own sources, timed on this
@@ -248,6 +249,30 @@ def bench_gemm_f32(s: Session, M, K, N, steps, warmup):
             "frac_bound": tf / F32_SPLIT_BOUND_TFLOPS, "vs_f32_matrix_peak": tf / F32_PEAK_TFLOPS}
 
 
+def bench_attention(s: Session, steps: int, warmup: int):
+    """Config 4's ATTENTION_F32 calls alone: prefill B1 x 32 heads x 2048 causal
+    and decode B8 x 32 heads x 1 query over a 4096-entry KV cache (D = 128)."""
+    out = {}
+    h, d = 32, 128
+    for name, b, sq, sk in (("prefill_b1_s2048", 1, 2048, 2048), ("decode_b8_ctx4096", 8, 1, 4096)):
+        q = s.upload(synth.normal(f"c4att/{name}/q", (b, h, sq, d)))
+        k = s.upload(synth.normal(f"c4att/{name}/k", (b, h, sk, d)))
+        v = s.upload(synth.normal(f"c4att/{name}/v", (b, h, sk, d)))
+        o = s.alloc(4 * b * h * sq * d)
+        mk = lambda i: s.command(abi.OP_ATTENTION_F32, id=i, Q=q, K=k, V=v, O=o, batch=b, heads=h, seq_q=sq,
+                                 seq_k=sk, head_dim=d, causal=1)
+        wall, gpu_ns = timed(s, mk, steps, warmup)
+        for x in (q, k, v, o):
+            s.free(x)
+        r = {"kernel_us": gpu_ns / 1e3}
+        if sq > 1:
+            r["tflops_causal"] = 4.0 * b * h * sq * sk * d / 2 / gpu_ns / 1e3
+        else:
+            r["kv_gbs"] = 2.0 * b * h * sk * d * 4 / gpu_ns
+        out[name] = r
+    return out
+
+
 def bench_block(s: Session, steps: int):
     """Config 4: one Llama-style layer, prefill B1 S2048 and decode B8 @ ctx 4096."""
     from vnpu_mi355x.block import LLAMA_4096, Block, weights_f32
@@ -372,7 +397,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=["gemm_i8", "gemm_f32", "block", "config1", "config5"],
+    ap.add_argument("--only", choices=["gemm_i8", "gemm_f32", "attention", "block", "config1", "config5"],
                     default=None, help="run one extra workload alone (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -390,6 +415,8 @@ def main():
         elif args.only == "gemm_f32":
             for n in (4096, 14336):
                 log("gemm_f32", bench_gemm_f32(s, 2048, 4096, n, args.steps, args.warmup))
+        elif args.only == "attention":
+            log("attention", bench_attention(s, args.steps, args.warmup))
         elif args.only == "block":
             log("block", bench_block(s, args.steps))
         elif args.only == "config1":
@@ -432,6 +459,8 @@ def main():
         for n in (4096, 14336):
             extras["config3_gemm_f32"].append(rounded(bench_gemm_f32(s, 2048, 4096, n, 5, 2)))
             log("gemm_f32", extras["config3_gemm_f32"][-1])
+        extras["config4_attention"] = {k: rounded(v, 3) for k, v in bench_attention(s, 20, 3).items()}
+        log("attention", extras["config4_attention"])
         extras["config4_block"] = {k: rounded(v, 3) for k, v in bench_block(s, 20).items()}
         log("block", extras["config4_block"])
         extras["config5"] = {k: rounded(v, 3) for k, v in bench_config5(s, 10).items()}
