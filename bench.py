@@ -273,6 +273,21 @@ def bench_attention(s: Session, steps: int, warmup: int):
     return out
 
 
+def bench_copy(s: Session, steps: int):
+    """A device-to-device COPY of 256 MiB, `steps` times: a plain copy kernel of
+    known size that calibrates the FETCH_SIZE / WRITE_SIZE counters behind
+    GEMV_TRAFFIC_BYTES (KiB per dispatch against 262,144 KiB read and written)."""
+    n = 256 << 20
+    a, b = s.alloc(n), s.alloc(n)
+    s.run(abi.OP_MEMSET, dst=a, value=1, bytes=n)
+    mk = lambda i: s.command(abi.OP_COPY, id=i, dst=b if i % 2 == 0 else a, src=a if i % 2 == 0 else b, bytes=n,
+                             direction=abi.COPY_D2D)
+    wall, gpu_ns = timed(s, mk, steps, 0)
+    s.free(a)
+    s.free(b)
+    return {"bytes": n, "copies": steps, "kernel_us": gpu_ns / 1e3, "gbs": 2.0 * n / gpu_ns}
+
+
 def bench_block(s: Session, steps: int):
     """Config 4: one Llama-style layer, prefill B1 S2048 and decode B8 @ ctx 4096."""
     from vnpu_mi355x.block import LLAMA_4096, Block, weights_f32
@@ -397,7 +412,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
-    ap.add_argument("--only", choices=["gemm_i8", "gemm_f32", "attention", "block", "config1", "config5"],
+    ap.add_argument("--only", choices=["gemm_i8", "gemm_f32", "attention", "block", "config1", "config5",
+                                       "copy"],
                     default=None, help="run one extra workload alone (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -415,6 +431,8 @@ def main():
         elif args.only == "gemm_f32":
             for n in (4096, 14336):
                 log("gemm_f32", bench_gemm_f32(s, 2048, 4096, n, args.steps, args.warmup))
+        elif args.only == "copy":
+            log("copy", bench_copy(s, 5))
         elif args.only == "attention":
             log("attention", bench_attention(s, args.steps, args.warmup))
         elif args.only == "block":
