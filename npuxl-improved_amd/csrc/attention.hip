@@ -579,7 +579,6 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
     using S = SplitBlk<D>;
     constexpr int NS = D / 16;          // QK steps (16 d each)
     constexpr int DT = D / 32;          // 32-row tiles of O^T
-    constexpr int C = S::kChunks;
     constexpr int kInstr = 2 * S::kBytes / 1024;   // DMA instructions per super block
 
     const int tid = threadIdx.x, lane = tid & 63;

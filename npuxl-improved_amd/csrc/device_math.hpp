@@ -55,6 +55,25 @@ __device__ __forceinline__ float epilogue(float v, uint32_t epi)
     }
 }
 
+// QUANTIZE_I8 element and scale rules (reference src/kernels/llm.cpp:387-436):
+// q = clamp(round_half_away(x * inv), -128, 127) with the correctly rounded
+// multiply; scale = max|x| / 127, zero or non-finite -> 1.
+__device__ __forceinline__ int8_t q8(float x, float inv)
+{
+    float q = roundf(__fmul_rn(x, inv));
+    // Plain compares, as the reference: a NaN passes both and converts to 0.
+    if (q > 127.0f) q = 127.0f;
+    if (q < -128.0f) q = -128.0f;
+    return q == q ? static_cast<int8_t>(static_cast<int>(q)) : static_cast<int8_t>(0);
+}
+
+__device__ __forceinline__ float scale_from_max(float maxabs)
+{
+    float scale = __fdiv_rn(maxabs, 127.0f);
+    if (!(scale > 0.0f) || !isfinite(scale)) scale = 1.0f;
+    return scale;
+}
+
 // Wave-wide reductions (wave64).
 __device__ __forceinline__ float wave_max(float v)
 {

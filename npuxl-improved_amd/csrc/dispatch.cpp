@@ -484,6 +484,142 @@ bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t
     return true;
 }
 
+uint32_t try_execute_chain(vnpu_stream_t *s, const vnpu_command_t *c, uint64_t n,
+                           uint32_t *matched, ExecStats *st)
+{
+    *matched = 0;
+    if (n < 2) return 0;
+    k::RowChain p;
+    uint32_t used = 0;
+    const vnpu_rmsnorm_f32_args_t *norm = nullptr;
+    const vnpu_quantize_i8_args_t *quant = nullptr;
+    uint64_t pre_count = 0;
+    const uint32_t op0 = c[0].opcode;
+    if (op0 == VNPU_OP_ADD_F32 || op0 == VNPU_OP_SWIGLU_F32) {
+        if (op0 == VNPU_OP_ADD_F32) {
+            const auto &a = c[0].args.binary;  // scheduler.cpp:564-581
+            const bool both0 = a.alpha == 0.0f && a.beta == 0.0f;
+            p.pre = k::kChainAdd;
+            p.A = a.A; p.B = a.B; p.Y = a.Y; pre_count = a.count;
+            p.alpha = both0 ? 1.0f : a.alpha;
+            p.beta = both0 ? 1.0f : a.beta;
+            if (c[1].opcode != VNPU_OP_RMSNORM_F32 || c[1].args.rmsnorm.X != a.Y) return 0;
+            norm = &c[1].args.rmsnorm;
+            used = 2;
+            if (n > 2 && c[2].opcode == VNPU_OP_QUANTIZE_I8) {
+                quant = &c[2].args.quantize_i8;
+                used = 3;
+            }
+        } else {
+            const auto &a = c[0].args.swiglu;  // scheduler.cpp:536-548
+            p.pre = k::kChainSwiglu;
+            p.A = a.gate; p.B = a.up; p.Y = a.Y; pre_count = a.count;
+            p.alpha = a.alpha == 0.0f ? 1.0f : a.alpha;
+            if (c[1].opcode != VNPU_OP_QUANTIZE_I8 || c[1].args.quantize_i8.X != a.Y) return 0;
+            quant = &c[1].args.quantize_i8;
+            used = 2;
+        }
+        if (!p.A || !p.B || !p.Y || !pre_count) return 0;
+    } else if (op0 == VNPU_OP_RMSNORM_F32) {
+        if (c[1].opcode != VNPU_OP_QUANTIZE_I8) return 0;
+        norm = &c[0].args.rmsnorm;
+        quant = &c[1].args.quantize_i8;
+        p.A = norm->X;
+        used = 2;
+    } else {
+        return 0;
+    }
+    if (norm) {
+        if (!norm->X || !norm->Y || !norm->rows || !norm->cols) return 0;  // scheduler.cpp:475-492
+        p.rows = norm->rows;
+        p.cols = norm->cols;
+        p.W = norm->W;
+        p.Nrm = norm->Y;
+        p.eps = norm->eps > 0.0f ? norm->eps : 1e-5f;
+    }
+    if (quant) {
+        const float *qx = norm ? norm->Y : p.Y;
+        if (quant->X != qx || !quant->Y || !quant->scales || quant->axis != VNPU_QUANT_PER_ROW ||
+            !quant->rows || !quant->cols || quant->rows > 0xffffffffull || quant->cols > 0xffffffffull)
+            quant = nullptr;
+        else if (norm && (quant->rows != norm->rows || quant->cols != norm->cols))
+            quant = nullptr;
+        if (!quant) {
+            if (op0 != VNPU_OP_ADD_F32) return 0;
+            used = 2;  // ADD -> RMSNORM without the quantize
+        } else {
+            p.rows = static_cast<uint32_t>(quant->rows);
+            p.cols = static_cast<uint32_t>(quant->cols);
+            p.Q = quant->Y;
+            p.scales = quant->scales;
+        }
+    }
+    const uint64_t elems = static_cast<uint64_t>(p.rows) * p.cols;
+    if (pre_count && pre_count != elems) return 0;
+
+    // Aliasing: every output must be disjoint from every other buffer of the
+    // chain, except that float rows (A, B, Y, Nrm) may be the same buffer;
+    // then each workgroup reads its row before writing it and the result is
+    // the one of the commands run in order.
+    struct Buf {
+        const void *p;
+        size_t bytes;
+        bool row, out;
+    };
+    const size_t rb = elems * 4;
+    Buf bufs[7];
+    int nb = 0;
+    auto add = [&](const void *q, size_t bytes, bool row, bool out) {
+        if (q) bufs[nb++] = Buf{q, bytes, row, out};
+    };
+    add(p.A, rb, true, false);
+    add(p.B, rb, true, false);
+    add(p.Y, rb, true, true);
+    add(p.W, static_cast<size_t>(p.cols) * 4, false, false);
+    add(p.Nrm, rb, true, true);
+    add(p.Q, elems, false, true);
+    add(p.scales, static_cast<size_t>(p.rows) * 4, false, true);
+    for (int i = 0; i < nb; ++i) {
+        if (!is_device_pointer(bufs[i].p)) return 0;
+        if (!bufs[i].out) continue;
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(bufs[i].p), hi = lo + bufs[i].bytes;
+        for (int j = 0; j < nb; ++j) {
+            if (j == i) continue;
+            const uintptr_t lo2 = reinterpret_cast<uintptr_t>(bufs[j].p), hi2 = lo2 + bufs[j].bytes;
+            if (lo < hi2 && lo2 < hi && !(bufs[i].row && bufs[j].row && lo == lo2)) return 0;
+        }
+    }
+
+    *matched = used;
+    if (!k::row_chain(s->hip, p)) {
+        *matched = 0;
+        return 0;
+    }
+    VNPU_HIP(hipGetLastError());
+    // Per-command accounting as the unfused commands count it.
+    uint32_t k = 0;
+    if (p.pre == k::kChainAdd) {
+        st[k].bytes_read += elems * 8;
+        st[k].bytes_written += elems * 4;
+        st[k++].flops += elems * 3;
+    } else if (p.pre == k::kChainSwiglu) {
+        st[k].bytes_read += elems * 8;
+        st[k].bytes_written += elems * 4;
+        st[k++].flops += elems * 8;
+    }
+    if (p.Nrm) {
+        st[k].bytes_read += elems * 4 + (p.W ? static_cast<uint64_t>(p.cols) * 4 : 0);
+        st[k].bytes_written += elems * 4;
+        st[k++].flops += elems * 5;
+    }
+    if (p.Q) {
+        st[k].bytes_read += elems * 4;
+        st[k].bytes_written += elems;
+        st[k++].flops += elems * 3;
+    }
+    return used;
+}
+
 namespace {
 
 void exec_quantize(vnpu_device_t *, vnpu_stream_t *s, const vnpu_quantize_i8_args_t &a,

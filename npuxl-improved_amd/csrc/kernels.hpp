@@ -115,6 +115,31 @@ void mul(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, fl
          float beta);
 void gelu(hipStream_t s, const float *X, float *Y, uint64_t n);
 
+// A run of row-wise commands over the same rows x cols float rows, executed
+// per row in one workgroup with the row held in registers: an optional first
+// stage (ADD: Y = A*alpha + B*beta, or SWIGLU: Y = silu(A)*B*alpha), an
+// optional RMSNORM (Nrm = X*inv*W, X being Y or, without a first stage, A),
+// and an optional per-row QUANTIZE_I8 of the last stage's output.  Every
+// stage's output is written, and each stage is the arithmetic of its own
+// kernel in the same order, so the results equal the commands run one by one.
+// Needs cols % 4 == 0, cols / 4 <= kRowChainMaxVec4, 16-byte aligned float
+// rows and W, a 4-byte aligned Q; returns false (nothing launched) otherwise.
+enum RowChainPre : uint32_t { kChainNone = 0, kChainAdd = 1, kChainSwiglu = 2 };
+constexpr uint32_t kRowChainMaxVec4 = 3072;
+struct RowChain {
+    uint32_t pre = kChainNone;
+    const float *A = nullptr, *B = nullptr;
+    float *Y = nullptr;
+    float alpha = 1.0f, beta = 1.0f;
+    const float *W = nullptr;
+    float *Nrm = nullptr;  // null: no RMSNORM
+    float eps = 1e-5f;
+    int8_t *Q = nullptr;   // null: no QUANTIZE_I8
+    float *scales = nullptr;
+    uint32_t rows = 0, cols = 0;
+};
+bool row_chain(hipStream_t s, const RowChain &p);
+
 // ---- ATTENTION_F32 (attention.hip) ----
 struct Attn {
     const float *Q = nullptr, *K = nullptr, *V = nullptr, *mask = nullptr;

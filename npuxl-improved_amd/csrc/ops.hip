@@ -297,6 +297,128 @@ void launch_ew(hipStream_t s, const float *A, const float *B, float *Y, uint64_t
         ew_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(A, B, Y, n, alpha, beta);
 }
 
+// One row of a RowChain per workgroup (no __restrict__: a stage's output may
+// be the very buffer an input row came from; every thread reads its elements
+// of the row before it writes them, and writes the stages in command order).
+// The RMSNORM sum runs over the same thread/element mapping and block_sum as
+// rmsnorm_reg_kernel, hence the same float sum; the max of the quantize stage
+// does not depend on order.
+template <int NT>
+__device__ __forceinline__ float block_max_n(float v, float *red)
+{
+    v = dev::wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) r = fmaxf(r, red[w]);
+    return r;
+}
+
+// NT threads per row: 256 whenever the chain has an RMSNORM (its sum order is
+// rmsnorm_reg_kernel's); SWIGLU -> QUANTIZE_I8 (a max, any order) uses 1024,
+// four times the lanes for the SiLU of a long row.
+template <int VPT, uint32_t PRE, bool NORM, bool QUANT, int NT = kThreads>
+__global__ __launch_bounds__(NT) void row_chain_kernel(RowChain p)
+{
+    static_assert(!NORM || NT == kThreads, "RMSNORM sums in rmsnorm_reg_kernel's order");
+    __shared__ float red[NT / 64];
+    const uint32_t n4 = p.cols >> 2;
+    const uint64_t off = static_cast<uint64_t>(blockIdx.x) * n4;
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v[VPT];
+    if (PRE == kChainNone) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const uint32_t j = threadIdx.x + i * NT;
+            v[i] = j < n4 ? reinterpret_cast<const float4 *>(p.A)[off + j] : zero;
+        }
+    } else {
+        float4 b[VPT];
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const uint32_t j = threadIdx.x + i * NT;
+            v[i] = j < n4 ? reinterpret_cast<const float4 *>(p.A)[off + j] : zero;
+            b[i] = j < n4 ? reinterpret_cast<const float4 *>(p.B)[off + j] : zero;
+        }
+        constexpr int OP = PRE == kChainAdd ? EW_ADD : EW_SWIGLU;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const uint32_t j = threadIdx.x + i * NT;
+            if (j >= n4) continue;
+            v[i] = make_float4(ew<OP>(v[i].x, b[i].x, p.alpha, p.beta), ew<OP>(v[i].y, b[i].y, p.alpha, p.beta),
+                               ew<OP>(v[i].z, b[i].z, p.alpha, p.beta), ew<OP>(v[i].w, b[i].w, p.alpha, p.beta));
+            reinterpret_cast<float4 *>(p.Y)[off + j] = v[i];
+        }
+    }
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            ss = fmaf(v[i].x, v[i].x, ss);
+            ss = fmaf(v[i].y, v[i].y, ss);
+            ss = fmaf(v[i].z, v[i].z, ss);
+            ss = fmaf(v[i].w, v[i].w, ss);
+        }
+        ss = block_sum(ss, red);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(p.cols) + p.eps);
+        const float4 *w = reinterpret_cast<const float4 *>(p.W);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const uint32_t j = threadIdx.x + i * NT;
+            if (j >= n4) continue;
+            const float4 g = w ? w[j] : make_float4(1.f, 1.f, 1.f, 1.f);
+            v[i] = make_float4(v[i].x * inv * g.x, v[i].y * inv * g.y, v[i].z * inv * g.z, v[i].w * inv * g.w);
+            reinterpret_cast<float4 *>(p.Nrm)[off + j] = v[i];
+        }
+    }
+    if (QUANT) {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        const float scale = dev::scale_from_max(block_max_n<NT>(m, red));
+        const float inv = __fdiv_rn(1.0f, scale);
+        if (threadIdx.x == 0) p.scales[blockIdx.x] = scale;
+        char4 *out = reinterpret_cast<char4 *>(p.Q) + off;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const uint32_t j = threadIdx.x + i * NT;
+            if (j < n4)
+                out[j] = make_char4(dev::q8(v[i].x, inv), dev::q8(v[i].y, inv), dev::q8(v[i].z, inv),
+                                    dev::q8(v[i].w, inv));
+        }
+    }
+}
+
+template <int VPT>
+bool launch_row_chain(hipStream_t s, const RowChain &p)
+{
+    const dim3 grid(p.rows), block(kThreads);
+    const bool norm = p.Nrm != nullptr, quant = p.Q != nullptr;
+    if (p.pre == kChainAdd && norm && quant)
+        row_chain_kernel<VPT, kChainAdd, true, true><<<grid, block, 0, s>>>(p);
+    else if (p.pre == kChainAdd && norm)
+        row_chain_kernel<VPT, kChainAdd, true, false><<<grid, block, 0, s>>>(p);
+    else if (p.pre == kChainNone && norm && quant)
+        row_chain_kernel<VPT, kChainNone, true, true><<<grid, block, 0, s>>>(p);
+    else
+        return false;
+    return true;
+}
+
+bool launch_swiglu_chain(hipStream_t s, const RowChain &p)
+{
+    const dim3 grid(p.rows), block(1024);
+    if (p.cols / 4 <= 1024)
+        row_chain_kernel<1, kChainSwiglu, false, true, 1024><<<grid, block, 0, s>>>(p);
+    else
+        row_chain_kernel<3, kChainSwiglu, false, true, 1024><<<grid, block, 0, s>>>(p);
+    return true;
+}
+
 __global__ void fill_kernel(uint8_t *dst, uint8_t v, uint64_t n)
 {
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
@@ -384,6 +506,19 @@ void mul(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, fl
 void gelu(hipStream_t s, const float *X, float *Y, uint64_t n)
 {
     launch_ew<EW_GELU>(s, X, nullptr, Y, n, 0.0f, 0.0f);
+}
+
+bool row_chain(hipStream_t s, const RowChain &p)
+{
+    auto al = [](const void *q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q) % a == 0; };
+    if (!p.rows || !p.cols || p.cols % 4 || p.cols / 4 > kRowChainMaxVec4 || p.rows > (1u << 22))
+        return false;
+    if (!p.A || !al(p.A, 16) || (p.pre != kChainNone && (!p.B || !p.Y || !al(p.B, 16) || !al(p.Y, 16))))
+        return false;
+    if ((p.W && !al(p.W, 16)) || (p.Nrm && !al(p.Nrm, 16)) || (p.Q && (!al(p.Q, 4) || !p.scales)))
+        return false;
+    if (p.pre == kChainSwiglu) return !p.Nrm && p.Q && launch_swiglu_chain(s, p);
+    return p.cols / 4 <= kThreads * 4 ? launch_row_chain<4>(s, p) : launch_row_chain<12>(s, p);
 }
 
 void fill_u8(hipStream_t s, void *dst, uint8_t value, uint64_t bytes)

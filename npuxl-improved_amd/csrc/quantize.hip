@@ -21,21 +21,8 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ int8_t q8(float x, float inv)
-{
-    float q = roundf(__fmul_rn(x, inv));
-    // Plain compares, as the reference: a NaN passes both and converts to 0.
-    if (q > 127.0f) q = 127.0f;
-    if (q < -128.0f) q = -128.0f;
-    return q == q ? static_cast<int8_t>(static_cast<int>(q)) : static_cast<int8_t>(0);
-}
-
-__device__ __forceinline__ float scale_from_max(float maxabs)
-{
-    float scale = __fdiv_rn(maxabs, 127.0f);
-    if (!(scale > 0.0f) || !isfinite(scale)) scale = 1.0f;
-    return scale;
-}
+using dev::q8;
+using dev::scale_from_max;
 
 __device__ __forceinline__ float block_max(float v, float *red)
 {

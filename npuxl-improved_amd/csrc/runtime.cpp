@@ -767,6 +767,34 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
                     continue;
                 }
             }
+            // ADD / SWIGLU / RMSNORM followed by the row commands that consume
+            // their output may run as one row-chain kernel (not while tracing).
+            if (!tracing && i + 1 < count &&
+                (cmd.opcode == VNPU_OP_ADD_F32 || cmd.opcode == VNPU_OP_SWIGLU_F32 ||
+                 cmd.opcode == VNPU_OP_RMSNORM_F32)) {
+                ExecStats cs[3];
+                uint32_t matched = 0, used = 0;
+                try {
+                    used = try_execute_chain(stream, commands + i, count - i, &matched, cs);
+                } catch (const std::exception &ex) {
+                    debug_log("row chain failed: %s", ex.what());
+                    (void)hipGetLastError();
+                    batch_status = VNPU_ERR_INTERNAL;
+                    const uint32_t code = static_cast<uint32_t>(-VNPU_ERR_INTERNAL);
+                    d->error.store(code);
+                    d->regs[VNPU_REG_ERROR / 4].store(code);
+                    stream->last_error.store(code);
+                    i += matched ? matched - 1 : 0;
+                    continue;
+                }
+                if (used) {
+                    d->last_opcode.store(commands[i + used - 1].opcode);
+                    const uint64_t host = now_ns() - t0;
+                    for (uint32_t k = 0; k < used; ++k) account(cs[k], k + 1 < used ? host / used : host - (used - 1) * (host / used));
+                    i += used - 1;
+                    continue;
+                }
+            }
             TraceRecord rec;
             if (tracing) {
                 {

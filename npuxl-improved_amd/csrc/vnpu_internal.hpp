@@ -187,10 +187,19 @@ struct ExecStats {
     uint32_t unit = 0;
 };
 
-// Executes one command on the stream (enqueue only).  Throws ArgError for
-// invalid arguments and HipError for runtime failures.
+// Two independent MATMUL_I8 commands in one grid; false: run them one by one.
 bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &c0,
                       const vnpu_command_t &c1, uint32_t flags, ExecStats &st0, ExecStats &st1);
+// A row chain at the head of c[0..n): ADD -> RMSNORM [-> QUANTIZE_I8 per row],
+// RMSNORM -> QUANTIZE_I8 or SWIGLU -> QUANTIZE_I8 over the same rows, device
+// buffers only, run as one kernel.  Returns the number of commands executed
+// (0: none, run them one by one); *matched is set before the launch so a
+// caller that catches a HipError knows how many commands it covered.  st[]
+// holds one entry per executed command.
+uint32_t try_execute_chain(vnpu_stream_t *s, const vnpu_command_t *c, uint64_t n,
+                           uint32_t *matched, ExecStats *st);
+// Executes one command on the stream (enqueue only).  Throws ArgError for
+// invalid arguments and HipError for runtime failures.
 void execute_command(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &cmd,
                      uint32_t batch_flags, ExecStats &st);
 
