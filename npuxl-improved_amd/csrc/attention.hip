@@ -17,6 +17,7 @@
 // limit are never loaded.
 #include "kernels.hpp"
 #include "device_math.hpp"
+#include "lds_dma.hpp"
 
 #include <algorithm>
 
@@ -545,21 +546,7 @@ __global__ __launch_bounds__(256) void attn_split_kv(Attn a, uint32_t nkb, int8_
     }
 }
 
-// 16-byte-per-lane global->LDS copy (lane l writes lds_dst + 16 l bytes).
-// Written as asm on purpose: for the builtin form the compiler cannot tell the
-// in-flight copy of the next key block from the buffer being read, and waits
-// vmcnt(0) before the first ds_read of every block, which serialises the copy
-// with the compute.  The kernel's own vmcnt(0) + barrier at the top of each
-// key block is what orders the copy before its readers.
-__device__ __forceinline__ void lds_dma16(const void *src, int8_t *lds_dst)
-{
-    const uint32_t lds = static_cast<uint32_t>(
-        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(lds_dst)));
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 :
-                 : "v"(src), "s"(lds)
-                 : "memory", "m0");
-}
+using lds::dma16;
 
 // Softmax weights use the hardware exp2 (v_exp_f32) on base-2 scores (Q is
 // pre-scaled by log2 e).  The reference's degree-5 polynomial
@@ -628,7 +615,7 @@ __device__ __forceinline__ void prefill_block(const Attn &a, uint32_t q0, uint64
 #pragma unroll
         for (int i = 0; i < kInstr / 8; ++i) {
             const int ins = wq * (kInstr / 8) + i;                // 1 KiB piece of the block
-            lds_dma16(from + ins * 1024, dst + ins * 1024);
+            dma16(from + ins * 1024, dst + ins * 1024);
         }
     };
 

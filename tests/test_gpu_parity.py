@@ -233,11 +233,15 @@ def test_matmul_f32(gpu, M, K, N, ta, tb, epi, beta, alpha):
 
 @pytest.mark.parametrize("M,K,N,ta,tb,epi,beta", [
     (1024, 1000, 2176, 0, 0, 2, 0.0), (1024, 1000, 2176, 0, 1, 3, 0.5), (1100, 520, 1920, 1, 0, 1, 0.0),
-    (1100, 520, 1920, 1, 1, 0, 0.5), (2048, 4096, 1024, 0, 1, 3, 0.5), (1030, 37, 2050, 0, 0, 0, 0.0)])
+    (1100, 520, 1920, 1, 1, 0, 0.5), (2048, 4096, 1024, 0, 1, 3, 0.5), (1030, 37, 2050, 0, 0, 0, 0.0),
+    (1100, 100, 6600, 0, 0, 2, 0.0), (1100, 37, 6600, 1, 1, 3, 0.5), (1300, 520, 6200, 0, 1, 3, 0.5),
+    (1300, 520, 6200, 1, 0, 0, 0.0), (2048, 1000, 4096, 0, 1, 3, 0.5)])
 def test_matmul_f32_split_bf16(gpu, M, K, N, ta, tb, epi, beta):
     """Grids of >= 128 tiles run the split-bf16 kernel (hi*hi + hi*lo + lo*hi
     on the bf16 matrix cores): every transpose combination, ragged M / N / K,
-    the config-3 epilogue (bias, beta 0.5 onto C, GELU), to the f32 bar."""
+    the config-3 epilogue (bias, beta 0.5 onto C, GELU), to the f32 bar.  The
+    last five have at least 256 tiles of 256 x 128, which take the eight-wave
+    256 x 128 tile (the others the four-wave 128 x 128 one)."""
     A = RNG.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
     B = RNG.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
     bias = RNG.standard_normal(N).astype(np.float32)
