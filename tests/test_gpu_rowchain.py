@@ -160,3 +160,22 @@ def test_chain_nan_and_zero_rows(gpu):
     p["y"][3, 7] = np.inf
     _same_bits(_run(gpu, "add_norm_quant", rows, cols, True, True, p),
                _run(gpu, "add_norm_quant", rows, cols, True, False, p))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_chain_counters_match_commands_one_by_one(gpu, kind):
+    """Device counters (bytes, flops, commands) after a chained batch equal
+    those after the same commands submitted one per batch: the reference's
+    per-command accounting (scheduler.cpp:430-581) does not see the chain."""
+    rows, cols = 32, 4096
+    p = _params(kind, rows, cols)
+
+    def delta(fused):
+        s0 = gpu.status()
+        before = (s0.bytes_read, s0.bytes_written, s0.flops, s0.commands_completed)
+        _run(gpu, kind, rows, cols, False, fused, p)
+        s1 = gpu.status()
+        return tuple(a - b for a, b in zip((s1.bytes_read, s1.bytes_written, s1.flops, s1.commands_completed),
+                                           before))
+
+    assert delta(True) == delta(False)
