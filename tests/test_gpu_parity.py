@@ -317,8 +317,12 @@ def test_elementwise(gpu, n):
 @pytest.mark.parametrize("interleaved", [0, 1])
 @pytest.mark.parametrize("shape_q,shape_k,offset", [((2, 3, 40, 16), (2, 3, 24, 16), 100),
                                                     ((1, 4, 2048, 128), (1, 4, 2048, 128), 0),
-                                                    ((8, 2, 1, 128), (8, 2, 1, 128), 4095)])
+                                                    ((8, 2, 1, 128), (8, 2, 1, 128), 4095),
+                                                    ((1, 32, 2048, 128), (1, 32, 2048, 128), 0),
+                                                    ((1, 13, 2600, 128), (1, 13, 2000, 128), 7)])
 def test_rope(gpu, interleaved, shape_q, shape_k, offset):
+    """Includes config 4's prefill shape (32 heads x 2048 tokens) and unequal
+    Q / K lengths at scale."""
     Q = RNG.standard_normal(shape_q).astype(np.float32)
     K = RNG.standard_normal(shape_k).astype(np.float32)
     gq, gk = g.rope(gpu, Q, K, position_offset=offset, interleaved=interleaved, theta=0.0)
