@@ -807,16 +807,38 @@ __global__ __launch_bounds__(kThreads) void attn_merge(Attn a, uint32_t splits, 
     if (idx >= rows * D) return;
     const uint64_t row = idx / D;
     const uint32_t d = static_cast<uint32_t>(idx % D);
+    // Splits in groups of eight whose loads are all issued before any is used
+    // (one L2 round trip per group, not two per split); the sums run in split
+    // order, skipping splits with no unmasked key.
+    constexpr uint32_t G = 8;
     float M = -__builtin_inff();
-    for (uint32_t s = 0; s < splits; ++s) M = fmaxf(M, ws_ml[(s * rows + row) * 2]);
+    for (uint32_t s0 = 0; s0 < splits; s0 += G) {
+        float ms[G];
+#pragma unroll
+        for (uint32_t u = 0; u < G; ++u)
+            ms[u] = s0 + u < splits ? ws_ml[((s0 + u) * rows + row) * 2] : -__builtin_inff();
+#pragma unroll
+        for (uint32_t u = 0; u < G; ++u) M = fmaxf(M, ms[u]);
+    }
     float num = 0.0f, den = 0.0f;
     if (isfinite(M)) {
-        for (uint32_t s = 0; s < splits; ++s) {
-            const float ms = ws_ml[(s * rows + row) * 2];
-            if (!isfinite(ms)) continue;
-            const float w = dev::fast_expf(ms - M);
-            num = fmaf(w, ws_acc[(s * rows + row) * D + d], num);
-            den = fmaf(w, ws_ml[(s * rows + row) * 2 + 1], den);
+        for (uint32_t s0 = 0; s0 < splits; s0 += G) {
+            float ms[G], acc[G], l[G];
+#pragma unroll
+            for (uint32_t u = 0; u < G; ++u) {
+                const bool in = s0 + u < splits;
+                const uint64_t r = static_cast<uint64_t>(s0 + u) * rows + row;
+                ms[u] = in ? ws_ml[r * 2] : -__builtin_inff();
+                acc[u] = in ? ws_acc[r * D + d] : 0.0f;
+                l[u] = in ? ws_ml[r * 2 + 1] : 0.0f;
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < G; ++u) {
+                if (!isfinite(ms[u])) continue;
+                const float w = dev::fast_expf(ms[u] - M);
+                num = fmaf(w, acc[u], num);
+                den = fmaf(w, l[u], den);
+            }
         }
     }
     a.O[row * D + d] = den > 0.0f ? num / den : 0.0f;
