@@ -242,6 +242,46 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ Q, f
     }
 }
 
+// Half-rotation layout with head_dim % 8 == 0 and 16-byte aligned rows: one
+// thread rotates pairs j..j+3 with one float4 from each half of the row.
+__device__ __forceinline__ void rotate4(float *row, uint32_t j4, uint32_t half4, const float (&c)[4],
+                                        const float (&s)[4])
+{
+    float4 *x = reinterpret_cast<float4 *>(row);
+    const float4 a = x[j4], b = x[half4 + j4];
+    x[j4] = make_float4(a.x * c[0] - b.x * s[0], a.y * c[1] - b.y * s[1], a.z * c[2] - b.z * s[2],
+                        a.w * c[3] - b.w * s[3]);
+    x[half4 + j4] = make_float4(a.x * s[0] + b.x * c[0], a.y * s[1] + b.y * c[1], a.z * s[2] + b.z * c[2],
+                                a.w * s[3] + b.w * c[3]);
+}
+
+__global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ Q, float *__restrict__ K,
+                                                            const int32_t *__restrict__ positions,
+                                                            uint64_t bh_count, uint32_t q_seq,
+                                                            uint32_t k_seq, uint32_t seq,
+                                                            uint32_t head_dim, uint32_t offset,
+                                                            float scaling,
+                                                            const float *__restrict__ inv_freq)
+{
+    const uint32_t half4 = head_dim / 8;
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (idx >= bh_count * seq * half4) return;
+    const uint32_t j4 = static_cast<uint32_t>(idx % half4);
+    const uint64_t tok = idx / half4;
+    const uint32_t t = static_cast<uint32_t>(tok % seq);
+    const uint64_t bh = tok / seq;
+    const float pos = static_cast<float>(positions ? positions[t] : static_cast<int32_t>(t + offset));
+    float c[4], s[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float angle = (pos * scaling) * inv_freq[4 * j4 + e];
+        c[e] = cosf(angle);
+        s[e] = sinf(angle);
+    }
+    if (Q && t < q_seq) rotate4(Q + (bh * q_seq + t) * head_dim, j4, half4, c, s);
+    if (K && t < k_seq) rotate4(K + (bh * k_seq + t) * head_dim, j4, half4, c, s);
+}
+
 enum EwOp { EW_SWIGLU = 0, EW_ADD = 1, EW_MUL = 2, EW_GELU = 3 };
 
 template <int OP>
@@ -483,6 +523,14 @@ void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t 
     const uint64_t bh = static_cast<uint64_t>(batch) * heads;
     const uint64_t total = bh * seq * (head_dim / 2);
     if (!total) return;
+    const bool vec = !interleaved && head_dim % 8 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K)) % 16 == 0);
+    if (vec) {
+        const uint64_t t4 = total / 4;
+        rope_vec_kernel<<<dim3(static_cast<uint32_t>((t4 + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
+            Q, K, positions, bh, q_seq, k_seq, seq, head_dim, position_offset, scaling, inv_freq);
+        return;
+    }
     rope_kernel<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
         Q, K, positions, bh, q_seq, k_seq, seq, head_dim, position_offset, interleaved, scaling,
         inv_freq);
