@@ -422,8 +422,9 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
 // Two MATMUL_I8 commands in a row, on device-resident data, with the same M
 // and neither reading nor writing what the other writes (the block's gate and
 // up projections): one wide-tile grid when that runs fewer whole rounds of
-// tiles (k::gemm_i8_pair).  Returns false, having launched nothing, when the
-// pair does not qualify; the commands then run one by one as usual.
+// tiles (k::gemm_i8_pair), or at M <= 8 one matrix-core GEMV grid
+// (k::gemv_i8_pair).  Returns false, having launched nothing, when the pair
+// does not qualify; the commands then run one by one as usual.
 bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &c0,
                       const vnpu_command_t &c1, uint32_t flags, ExecStats &st0, ExecStats &st1)
 {
@@ -440,7 +441,7 @@ bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t
     for (int i = 0; i < 2; ++i) {
         const vnpu_matmul_i8_args_t &a = *in[i];
         const vnpu_packed_weights_t *w = a.B;
-        if (!a.A || !w || !a.C || a.M <= 8 || !a.K || !a.N) return false;
+        if (!a.A || !w || !a.C || !a.M || !a.K || !a.N || (a.M <= 8) != (in[0]->M <= 8)) return false;
         if (w->K != a.K || w->N != a.N || a.epilogue > VNPU_EPILOGUE_GELU_ERF) return false;
         if (w->device && w->device->hip_device != dev->hip_device) return false;
         const uint32_t lda = a.lda ? a.lda : a.K, ldc = a.ldc ? a.ldc : a.N;
@@ -469,7 +470,8 @@ bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t
         if (rc[i].overlaps(ra[o]) || rc[i].overlaps(rs[o]) || rc[i].overlaps(rb[o]) || rc[i].overlaps(rc[o]))
             return false;
     }
-    if (!k::gemm_i8_pair(s->hip, p[0], p[1])) return false;
+    if (!(in[0]->M <= 8 ? k::gemv_i8_pair(s->hip, p[0], p[1]) : k::gemm_i8_pair(s->hip, p[0], p[1])))
+        return false;
     VNPU_HIP(hipGetLastError());
     ExecStats *st[2] = {&st0, &st1};
     for (int i = 0; i < 2; ++i) {

@@ -188,8 +188,13 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chun
 // ds_read_b128 per lane, which at M = 8 made the VALU the bottleneck.  The
 // 16 x 16 result leaves row 4(l/16) + i, column l%16 in lane l, register i.
 template <int M, int W, int U, int T>
-__global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8Gemm p, uint32_t chunk_k)
+__global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t grid0, uint32_t chunk_k)
 {
+    // Workgroups from grid0 on serve the second problem of a pair (same M
+    // and K, so the same chunk_k and LDS size).
+    const bool second = blockIdx.x >= grid0;
+    const I8Gemm &p = ps.p[second ? 1 : 0];
+    const uint32_t bx = second ? blockIdx.x - grid0 : blockIdx.x;
     static_assert(M <= 16, "rows of one 16 x 16 tile");
     typedef int v4i __attribute__((ext_vector_type(4)));
     extern __shared__ __attribute__((aligned(16))) int8_t a_lds[];  // [chunk_k/16][M][16]
@@ -199,7 +204,7 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8Gemm p, uint32_t chunk_
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kg = lane >> 4, row = lane & 15;
     const uint32_t NT = p.Np >> 4;
-    const uint32_t nt0 = blockIdx.x * T;
+    const uint32_t nt0 = bx * T;
     const uint32_t KT = p.Kp >> 6;
     const bool vec_a = ((p.lda & 15u) == 0) && ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0);
 
@@ -304,6 +309,25 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8Gemm p, uint32_t chunk_
 // or faster), with four strips per workgroup over at least 1024 strips so one
 // staged activation chunk serves four weight streams (two strips per
 // workgroup at 512-1023 strips measured slower: fewer workgroups than CUs).
+// MFMA variants by strip count: <4,4,4> from 1024 strips, <4,8,1> from 512,
+// <8,8,1> below.
+int mfma_variant(uint32_t NT) { return NT >= 1024 ? 0 : NT >= 512 ? 1 : 2; }
+uint32_t mfma_grid(uint32_t NT) { return mfma_variant(NT) == 0 ? (NT + 3) / 4 : NT; }
+
+template <int M>
+void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t grid0, uint32_t grid1,
+                      uint32_t chunk_k)
+{
+    const size_t lds = static_cast<size_t>(chunk_k) * M;
+    const dim3 grid(grid0 + grid1);
+    if (variant == 0)
+        gemv_i8_mfma<M, 4, 4, 4><<<grid, 256, lds, s>>>(ps, grid0, chunk_k);
+    else if (variant == 1)
+        gemv_i8_mfma<M, 4, 8, 1><<<grid, 256, lds, s>>>(ps, grid0, chunk_k);
+    else
+        gemv_i8_mfma<M, 8, 8, 1><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
+}
+
 template <int M>
 void launch_m(hipStream_t s, const I8Gemm &p)
 {
@@ -311,12 +335,9 @@ void launch_m(hipStream_t s, const I8Gemm &p)
     const uint32_t chunk_k = std::min<uint32_t>(p.Kp, (kLdsA / M) & ~63u);
     const size_t lds = static_cast<size_t>(chunk_k) * M;
     if constexpr (M >= 5) {
-        if (NT >= 1024)
-            gemv_i8_mfma<M, 4, 4, 4><<<dim3((NT + 3) / 4), 256, lds, s>>>(p, chunk_k);
-        else if (NT >= 512)
-            gemv_i8_mfma<M, 4, 8, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
-        else
-            gemv_i8_mfma<M, 8, 8, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+        I8GemmPair ps;
+        ps.p[0] = ps.p[1] = p;
+        launch_mfma_pair<M>(s, ps, mfma_variant(NT), mfma_grid(NT), 0, chunk_k);
     } else if constexpr (M >= 3) {
         gemv_i8_kernel<M, 8, 4, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
     } else {
@@ -342,6 +363,22 @@ void gemv_i8(hipStream_t s, const I8Gemm &p)
     case 8: launch_m<8>(s, p); break;
     default: break;
     }
+}
+
+bool gemv_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1)
+{
+    if (p0.M != p1.M || p0.M < 5 || p0.M > 8 || p0.Kp != p1.Kp) return false;
+    const uint32_t nt0 = p0.Np >> 4, nt1 = p1.Np >> 4;
+    if (mfma_variant(nt0) != mfma_variant(nt1)) return false;
+    const uint32_t chunk_k = std::min<uint32_t>(p0.Kp, (kLdsA / p0.M) & ~63u);
+    const I8GemmPair ps{{p0, p1}};
+    switch (p0.M) {
+    case 5: launch_mfma_pair<5>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;
+    case 6: launch_mfma_pair<6>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;
+    case 7: launch_mfma_pair<7>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;
+    default: launch_mfma_pair<8>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;
+    }
+    return true;
 }
 
 }  // namespace k

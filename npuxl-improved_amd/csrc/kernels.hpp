@@ -56,12 +56,15 @@ enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generi
 // select it: 256x128x256 wide, 256x128x128 8-wave, 256x64x128 64-deep,
 // 128x64x128 generic; anything else chooses automatically.
 uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t tile_n);
-void gemv_i8(hipStream_t s, const I8Gemm &p);  // M <= 8, no MFMA
+void gemv_i8(hipStream_t s, const I8Gemm &p);  // M <= 8 (matrix core from 5 rows)
 void gemm_i8(hipStream_t s, const I8Gemm &p);  // any M, int8 MFMA
 // Two independent MATMUL_I8 problems with the same M in one wide-tile grid
 // when that runs fewer whole rounds of tiles; false (nothing launched) when
 // either cannot take the wide kernel or one grid would not be faster.
 bool gemm_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1);
+// Two M <= 8 problems with the same M (5..8) and K, whose strip counts take
+// the same matrix-core GEMV variant, in one grid; false: nothing launched.
+bool gemv_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1);
 
 // ---- MATMUL_F32 (gemm_f32.hip) ----
 struct F32Gemm {

@@ -121,14 +121,18 @@ def test_matmul_i8_wide_tile(gpu, M, K, N):
     assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
 
 
-@pytest.mark.parametrize("N0,N1,alias", [(3000, 2000, False), (11008, 11008, False), (1000, 700, True)])
-def test_matmul_i8_pair_in_one_batch(gpu, N0, N1, alias):
+@pytest.mark.parametrize("M,N0,N1,alias", [(512, 3000, 2000, False), (512, 11008, 11008, False),
+                                           (512, 1000, 700, True), (8, 11008, 11008, False),
+                                           (6, 3000, 2000, False), (8, 1000, 700, True),
+                                           (8, 20000, 700, False)])
+def test_matmul_i8_pair_in_one_batch(gpu, M, N0, N1, alias):
     """Two MATMUL_I8 commands in one batch with the same M (the block's gate
-    and up projections) may share one wide-tile launch; both outputs must be
-    the oracle's bits, with their own bias and epilogue.  With `alias` the
-    second command reads the first one's output as its A (a dependency),
-    which must keep them in order."""
-    M, K = 512, 256
+    and up projections) may share one launch (a wide-tile grid, or one
+    matrix-core GEMV grid at M <= 8); both outputs must be the oracle's bits,
+    with their own bias and epilogue.  With `alias` the second command reads
+    the first one's output as its A (a dependency), which must keep them in
+    order; 20000 and 700 columns take different GEMV variants (not paired)."""
+    K = 256
     A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
     B0 = RNG.integers(-128, 128, size=(K, N0)).astype(np.int8)
     B1 = RNG.integers(-128, 128, size=(K if not alias else 256, N1)).astype(np.int8)
