@@ -16,6 +16,8 @@
 // runs with lanes over the head dimension.  Keys past a query block's causal
 // limit are never loaded.
 #include "kernels.hpp"
+
+#include <atomic>
 #include "device_math.hpp"
 #include "lds_dma.hpp"
 
@@ -940,7 +942,7 @@ void attention(hipStream_t s, const Attn &a, float *ws)
         const uint32_t nkb = (a.seq_k + XK - 1) / XK;
         const dim3 sgrid(nkb, a.batch * a.heads);
         if (a.causal) grid.x = (nqb + 1) / 2;
-        static bool lds_optin = false;
+        static std::atomic<bool> lds_optin{false};  // launches may come from several host threads
         if (!lds_optin)
             lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_prefill_kernel<128>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -21,6 +21,8 @@
 //     activations read as wave-uniform scalars; partial sums reduced in a
 //     second deterministic pass when K is split across workgroups.
 #include "kernels.hpp"
+
+#include <atomic>
 #include "device_math.hpp"
 
 #include <algorithm>
@@ -631,7 +633,7 @@ static bool use_x3(const F32Gemm &p)
 template <int WM>
 static void launch_x3(hipStream_t s, const F32Gemm &p)
 {
-    static bool lds_optin = false;
+    static std::atomic<bool> lds_optin{false};  // launches may come from several host threads
     constexpr int lds = x3::lds_bytes(WM);
     if (!lds_optin)
         lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<false, false, WM>),

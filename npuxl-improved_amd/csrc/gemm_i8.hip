@@ -24,6 +24,8 @@
 // lane l = 16*g + r holds row/column r and k = 16*g .. 16*g + 15 of the
 // 64-deep block.  Output: lane l holds C[4*(l/16) + i][l%16], i = 0..3.
 #include "kernels.hpp"
+
+#include <atomic>
 #include "device_math.hpp"
 #include "lds_dma.hpp"
 
@@ -930,7 +932,7 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
         }
     }
     if (v != kI8Generic) {
-        static bool lds_optin = false;
+        static std::atomic<bool> lds_optin{false};  // launches may come from several host threads
         if (!lds_optin) {
             bool ok = true;
             for (const void *fn : {reinterpret_cast<const void *>(gemm_i8_pipe<false>),
@@ -1001,7 +1003,7 @@ bool gemm_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1)
     const uint32_t tn0 = (p0.N + 255) / 256, tn1 = (p1.N + 255) / 256;
     const double together = tile_cost(static_cast<uint64_t>(wm_) * (tn0 + tn1), cus, 256, 256, 1.0);
     if (together >= alone(p0) + alone(p1)) return false;
-    static bool lds_optin = false;
+    static std::atomic<bool> lds_optin{false};  // launches may come from several host threads
     if (!lds_optin)
         lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_i8_wide<256>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
