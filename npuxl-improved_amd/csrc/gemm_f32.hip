@@ -215,8 +215,19 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_splitk_reduce(F32Gemm p, co
     const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
     if (idx >= total) return;
     const uint32_t m = static_cast<uint32_t>(idx / p.N), n = static_cast<uint32_t>(idx % p.N);
+    // Partials in groups of eight whose loads are issued together (one round
+    // trip per group), summed in split order.
+    constexpr uint32_t G = 8;
     float s = 0.0f;
-    for (uint32_t i = 0; i < splits; ++i) s += ws[static_cast<uint64_t>(i) * total + idx];
+    for (uint32_t i0 = 0; i0 < splits; i0 += G) {
+        float v[G];
+#pragma unroll
+        for (uint32_t u = 0; u < G; ++u)
+            v[u] = i0 + u < splits ? ws[static_cast<uint64_t>(i0 + u) * total + idx] : 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < G; ++u)
+            if (i0 + u < splits) s += v[u];
+    }
     store_out(p, m, n, s, false);
 }
 
@@ -557,8 +568,19 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_reduce(F32Gemm p, const flo
     const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
     if (idx >= total) return;
     const uint32_t m = static_cast<uint32_t>(idx / p.N), n = static_cast<uint32_t>(idx % p.N);
+    // Partials in groups of eight whose loads are issued together (one round
+    // trip per group), summed in split order.
+    constexpr uint32_t G = 8;
     float s = 0.0f;
-    for (uint32_t i = 0; i < splits; ++i) s += ws[static_cast<uint64_t>(i) * total + idx];
+    for (uint32_t i0 = 0; i0 < splits; i0 += G) {
+        float v[G];
+#pragma unroll
+        for (uint32_t u = 0; u < G; ++u)
+            v[u] = i0 + u < splits ? ws[static_cast<uint64_t>(i0 + u) * total + idx] : 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < G; ++u)
+            if (i0 + u < splits) s += v[u];
+    }
     store_out(p, m, n, s, false);
 }
 

@@ -337,12 +337,6 @@ void launch_ew(hipStream_t s, const float *A, const float *B, float *Y, uint64_t
         ew_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(A, B, Y, n, alpha, beta);
 }
 
-// One row of a RowChain per workgroup (no __restrict__: a stage's output may
-// be the very buffer an input row came from; every thread reads its elements
-// of the row before it writes them, and writes the stages in command order).
-// The RMSNORM sum runs over the same thread/element mapping and block_sum as
-// rmsnorm_reg_kernel, hence the same float sum; the max of the quantize stage
-// does not depend on order.
 template <int NT>
 __device__ __forceinline__ float block_max_n(float v, float *red)
 {
@@ -357,6 +351,72 @@ __device__ __forceinline__ float block_max_n(float v, float *red)
     return r;
 }
 
+template <int NT>
+__device__ __forceinline__ float block_sum_n(float v, float *red)
+{
+    v = dev::wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) r += red[w];
+    return r;
+}
+
+// Softmax of few long rows (the MTP head's [gamma, vocab] logits) in one
+// launch: a 1024-thread workgroup per row keeps the row in registers, takes
+// the max, then each e = fast_expf((x - max) * inv_t) once (kept for the
+// output) and their sum; y = e * (1 / sum), the reference's terms
+// (llm.cpp:116-134) with a tree sum.
+template <int VPT>
+__global__ __launch_bounds__(1024) void softmax_reg_kernel(const float *__restrict__ X, float *__restrict__ Y,
+                                                          uint32_t cols, float inv_t)
+{
+    __shared__ float red[1024 / 64];
+    const uint64_t r = blockIdx.x;
+    const float4 *x = reinterpret_cast<const float4 *>(X + r * cols);
+    float4 *y = reinterpret_cast<float4 *>(Y + r * cols);
+    const uint32_t n4 = cols >> 2;
+    const float ninf = -__builtin_inff();
+    float4 v[VPT];
+    float mx = ninf;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const uint32_t j = threadIdx.x + i * 1024;
+        v[i] = j < n4 ? x[j] : make_float4(ninf, ninf, ninf, ninf);
+        mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    }
+    mx = block_max_n<1024>(mx, red);
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const uint32_t j = threadIdx.x + i * 1024;
+        if (j >= n4) continue;
+        v[i] = make_float4(dev::fast_expf((v[i].x - mx) * inv_t), dev::fast_expf((v[i].y - mx) * inv_t),
+                           dev::fast_expf((v[i].z - mx) * inv_t), dev::fast_expf((v[i].w - mx) * inv_t));
+        sum += v[i].x;
+        sum += v[i].y;
+        sum += v[i].z;
+        sum += v[i].w;
+    }
+    sum = block_sum_n<1024>(sum, red);
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const uint32_t j = threadIdx.x + i * 1024;
+        if (j < n4) y[j] = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+    }
+}
+
+
+// One row of a RowChain per workgroup (no __restrict__: a stage's output may
+// be the very buffer an input row came from; every thread reads its elements
+// of the row before it writes them, and writes the stages in command order).
+// The RMSNORM sum runs over the same thread/element mapping and block_sum as
+// rmsnorm_reg_kernel, hence the same float sum; the max of the quantize stage
+// does not depend on order.
 // NT threads per row: 256 whenever the chain has an RMSNORM (its sum order is
 // rmsnorm_reg_kernel's); SWIGLU -> QUANTIZE_I8 (a max, any order) uses 1024,
 // four times the lanes for the SiLU of a long row.
@@ -507,6 +567,11 @@ void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t co
     const uint32_t chunks = softmax_chunks(rows, cols);
     if (chunks == 1) {
         softmax_kernel<<<dim3(rows), kThreads, 0, s>>>(X, Y, cols, inv_t);
+        return;
+    }
+    const bool vec = cols % 4 == 0 && ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y)) % 16 == 0);
+    if (vec && cols / 4 <= 1024 * 8) {
+        softmax_reg_kernel<8><<<dim3(rows), 1024, 0, s>>>(X, Y, cols, inv_t);
         return;
     }
     const dim3 grid(chunks, rows);
