@@ -736,6 +736,15 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
             d->tiles_dispatched.fetch_add(st.tiles_dispatched);
             d->tiles_culled.fetch_add(st.tiles_culled);
         };
+        // A failed command marks the batch, the device error register and the
+        // stream's sticky error.
+        auto fail = [&](vnpu_status_t rc) {
+            batch_status = rc;
+            const uint32_t code = static_cast<uint32_t>(-rc);
+            d->error.store(code);
+            d->regs[VNPU_REG_ERROR / 4].store(code);
+            stream->last_error.store(code);
+        };
         for (uint64_t i = 0; i < count; ++i) {
             const vnpu_command_t &cmd = commands[i];
             const uint64_t t0 = now_ns();
@@ -750,11 +759,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
                 } catch (const std::exception &ex) {
                     debug_log("paired matmul_i8 failed: %s", ex.what());
                     (void)hipGetLastError();
-                    batch_status = VNPU_ERR_INTERNAL;
-                    const uint32_t code = static_cast<uint32_t>(-VNPU_ERR_INTERNAL);
-                    d->error.store(code);
-                    d->regs[VNPU_REG_ERROR / 4].store(code);
-                    stream->last_error.store(code);
+                    fail(VNPU_ERR_INTERNAL);
                     ++i;
                     continue;
                 }
@@ -779,18 +784,15 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
                 } catch (const std::exception &ex) {
                     debug_log("row chain failed: %s", ex.what());
                     (void)hipGetLastError();
-                    batch_status = VNPU_ERR_INTERNAL;
-                    const uint32_t code = static_cast<uint32_t>(-VNPU_ERR_INTERNAL);
-                    d->error.store(code);
-                    d->regs[VNPU_REG_ERROR / 4].store(code);
-                    stream->last_error.store(code);
+                    fail(VNPU_ERR_INTERNAL);
                     i += matched ? matched - 1 : 0;
                     continue;
                 }
                 if (used) {
                     d->last_opcode.store(commands[i + used - 1].opcode);
                     const uint64_t host = now_ns() - t0;
-                    for (uint32_t k = 0; k < used; ++k) account(cs[k], k + 1 < used ? host / used : host - (used - 1) * (host / used));
+                    const uint64_t share = host / used;
+                    for (uint32_t k = 0; k < used; ++k) account(cs[k], k + 1 < used ? share : host - share * (used - 1));
                     i += used - 1;
                     continue;
                 }
@@ -844,13 +846,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
                     }
                 }
             }
-            if (rc != VNPU_OK) {
-                batch_status = rc;
-                const uint32_t code = static_cast<uint32_t>(-rc);
-                d->error.store(code);
-                d->regs[VNPU_REG_ERROR / 4].store(code);
-                stream->last_error.store(code);
-            }
+            if (rc != VNPU_OK) fail(rc);
         }
         if (batch_start) {
             hipEvent_t batch_stop = stream->acquire_event();
