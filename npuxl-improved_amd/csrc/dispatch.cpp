@@ -599,25 +599,25 @@ uint32_t try_execute_chain(vnpu_stream_t *s, const vnpu_command_t *c, uint64_t n
     }
     VNPU_HIP(hipGetLastError());
     // Per-command accounting as the unfused commands count it.
-    uint32_t k = 0;
+    uint32_t slot = 0;
     if (p.pre == k::kChainAdd) {
-        st[k].bytes_read += elems * 8;
-        st[k].bytes_written += elems * 4;
-        st[k++].flops += elems * 3;
+        st[slot].bytes_read += elems * 8;
+        st[slot].bytes_written += elems * 4;
+        st[slot++].flops += elems * 3;
     } else if (p.pre == k::kChainSwiglu) {
-        st[k].bytes_read += elems * 8;
-        st[k].bytes_written += elems * 4;
-        st[k++].flops += elems * 8;
+        st[slot].bytes_read += elems * 8;
+        st[slot].bytes_written += elems * 4;
+        st[slot++].flops += elems * 8;
     }
     if (p.Nrm) {
-        st[k].bytes_read += elems * 4 + (p.W ? static_cast<uint64_t>(p.cols) * 4 : 0);
-        st[k].bytes_written += elems * 4;
-        st[k++].flops += elems * 5;
+        st[slot].bytes_read += elems * 4 + (p.W ? static_cast<uint64_t>(p.cols) * 4 : 0);
+        st[slot].bytes_written += elems * 4;
+        st[slot++].flops += elems * 5;
     }
     if (p.Q) {
-        st[k].bytes_read += elems * 4;
-        st[k].bytes_written += elems;
-        st[k++].flops += elems * 3;
+        st[slot].bytes_read += elems * 4;
+        st[slot].bytes_written += elems;
+        st[slot++].flops += elems * 3;
     }
     return used;
 }
