@@ -124,7 +124,8 @@ def test_matmul_i8_wide_tile(gpu, M, K, N):
 @pytest.mark.parametrize("M,N0,N1,alias", [(512, 3000, 2000, False), (512, 11008, 11008, False),
                                            (512, 1000, 700, True), (8, 11008, 11008, False),
                                            (6, 3000, 2000, False), (8, 1000, 700, True),
-                                           (8, 20000, 700, False)])
+                                           (8, 20000, 700, False), (5, 4096, 4096, False),
+                                           (7, 1500, 1500, False)])
 def test_matmul_i8_pair_in_one_batch(gpu, M, N0, N1, alias):
     """Two MATMUL_I8 commands in one batch with the same M (the block's gate
     and up projections) may share one launch (a wide-tile grid, or one
