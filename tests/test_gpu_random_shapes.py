@@ -1,0 +1,54 @@
+"""Seeded random shapes through the batch-level paths of the MI355X backend:
+row chains (ADD -> RMSNORM -> QUANTIZE_I8, RMSNORM -> QUANTIZE_I8,
+SWIGLU -> QUANTIZE_I8) at random rows, columns and aliasing must give the
+bits of the same commands submitted one per batch, and pairs of MATMUL_I8
+commands at M <= 8 with random K and N the oracle's bits (reference
+src/kernels/kernels.cpp:922-978 accumulation and store_i8_c order)."""
+import numpy as np
+import pytest
+
+import oracle
+import test_gpu_rowchain as rc
+from vnpu_mi355x import abi
+
+pytestmark = pytest.mark.gpu
+
+
+def test_random_row_chains(gpu):
+    rng = np.random.default_rng(20261208)
+    for _ in range(40):
+        kind = rc.KINDS[rng.integers(4)]
+        rows = int(rng.integers(1, 200))
+        cols = 4 * int(rng.integers(1, 3200))   # past 12288 columns: commands one by one
+        alias = bool(rng.integers(2))
+        p = rc._params(kind, rows, cols)
+        fused = rc._run(gpu, kind, rows, cols, alias, True, p)
+        single = rc._run(gpu, kind, rows, cols, alias, False, p)
+        for k in fused:
+            assert np.array_equal(fused[k].view(np.uint8), single[k].view(np.uint8)), (kind, rows, cols, alias, k)
+
+
+def test_random_matmul_i8_pairs_small_m(gpu):
+    rng = np.random.default_rng(20261209)
+    for _ in range(24):
+        M, K = int(rng.integers(1, 9)), int(rng.integers(1, 3000))
+        N0 = int(rng.integers(1, 20000))
+        N1 = N0 if rng.integers(2) else int(rng.integers(1, 20000))
+        A = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
+        Bs = [rng.integers(-128, 128, size=(K, n)).astype(np.int8) for n in (N0, N1)]
+        sa = (rng.random(M).astype(np.float32) + 0.5) / 127
+        ss = [(rng.random(n).astype(np.float32) + 0.5) / 127 for n in (N0, N1)]
+        ws = [gpu.pack(B, K, n, scales=s) for B, n, s in zip(Bs, (N0, N1), ss)]
+        ba, bsa = gpu.upload(A), gpu.upload(sa)
+        cs = [gpu.alloc(4 * M * n) for n in (N0, N1)]
+        cmds = [gpu.command(abi.OP_MATMUL_I8, A=ba, B=w, scale_a=bsa.ptr, C=c, M=M, K=K, N=n)
+                for w, c, n in zip(ws, cs, (N0, N1))]
+        assert gpu.submit(cmds) == abi.OK and gpu.sync() == abi.OK
+        got = [gpu.download(c, np.float32, (M, n)) for c, n in zip(cs, (N0, N1))]
+        for b in [ba, bsa] + cs:
+            gpu.free(b)
+        for w in ws:
+            gpu.release_packed(w)
+        for g_, B, s in zip(got, Bs, ss):
+            want = oracle.matmul_i8(A, B, sa, s)
+            assert np.array_equal(g_.view(np.uint32), want.view(np.uint32)), (M, K, N0, N1)
