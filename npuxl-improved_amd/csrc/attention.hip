@@ -293,7 +293,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(Attn a, uint32_t 
                     }
                     m[i] = s;
                 }
-                const float p = dev::fast_expf(s - m[i]);
+                // m is still -inf only if every key so far, this one included,
+                // scored -inf (an additive -inf mask): such a key weighs 0, as
+                // fast_expf(-inf - m) does for any finite m.
+                const float p = (m[i] == -__builtin_inff()) ? 0.0f : dev::fast_expf(s - m[i]);
                 l[i] += p;
 #pragma unroll
                 for (int t = 0; t < V4; ++t) {

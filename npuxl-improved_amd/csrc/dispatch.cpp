@@ -283,10 +283,9 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
     p.alpha = in.alpha == 0.0f ? 1.0f : in.alpha;
     p.beta = in.beta;
     p.epilogue = in.epilogue;
-    // Device tiles 128 x depth x 128 (vnpu_device_set_tiles, autotune) fix
-    // the K depth per workgroup; other tiles leave the choice automatic.
-    if (dev->tile_m.load() == 128 && dev->tile_n.load() == 128 && dev->tile_k.load() % 16 == 0)
-        p.k_split_depth = dev->tile_k.load();
+    // Device tiles 128 x depth x 128 (vnpu_device_set_tiles, an f32 autotune)
+    // fix the K depth per workgroup; other tiles leave the choice automatic.
+    p.k_split_depth = dev->f32_depth.load();
 
     Stager sg(s->hip);
     p.A = sg.in(in.A, in.trans_a ? span(in.K, in.M, p.lda, 4) : span(in.M, in.K, p.lda, 4));
@@ -390,7 +389,7 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     p.Np = w->Np;
     p.scale_b = w->scales_dev;
     p.epilogue = in.epilogue;
-    p.variant = k::gemm_i8_variant_for_tiles(dev->tile_m.load(), dev->tile_k.load(), dev->tile_n.load());
+    p.variant = dev->i8_variant.load();
     require(in.epilogue <= VNPU_EPILOGUE_GELU_ERF, "invalid matmul_i8 epilogue");
 
     Stager sg(s->hip);
@@ -436,8 +435,7 @@ bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t
         bool overlaps(const Range &o) const { return lo < o.hi && o.lo < hi; }
     };
     Range ra[2], rc[2], rs[2], rb[2];
-    const uint32_t variant =
-        k::gemm_i8_variant_for_tiles(dev->tile_m.load(), dev->tile_k.load(), dev->tile_n.load());
+    const uint32_t variant = dev->i8_variant.load();
     for (int i = 0; i < 2; ++i) {
         const vnpu_matmul_i8_args_t &a = *in[i];
         const vnpu_packed_weights_t *w = a.B;

@@ -266,15 +266,23 @@ constexpr int lds_bytes(int wm) { return 2 * (2 * 64 * wm + 2 * TN) * BK * 2; }
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
+// hi = bf16(x) rounded to nearest even, lo = bf16(x - hi).  hi is rounded
+// from x clamped to the largest finite bf16 (3.3895e38), so it is finite for
+// every finite x and x - hi stays exact; an infinite x leaves its infinity in
+// lo (hi*b + hi*lo_b + lo*b is then +-inf with the sign of x*b, as the f32
+// product), and a NaN x gives lo = NaN, which propagates.
 __device__ __forceinline__ void split8(const float (&x)[8], v8bf &hi, v8bf &lo)
 {
     typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
     typedef float v2f __attribute__((ext_vector_type(2)));
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    constexpr float kBf16Max = 3.38953139e38f;   // 0x7F7F0000
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        hw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){x[2 * e], x[2 * e + 1]}, v2bf));
+        const float c0 = fminf(fmaxf(x[2 * e], -kBf16Max), kBf16Max);
+        const float c1 = fminf(fmaxf(x[2 * e + 1], -kBf16Max), kBf16Max);
+        hw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){c0, c1}, v2bf));
         const float h0 = __builtin_bit_cast(float, hw[e] << 16);
         const float h1 = __builtin_bit_cast(float, hw[e] & 0xFFFF0000u);
         lw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){x[2 * e] - h0, x[2 * e + 1] - h1}, v2bf));
@@ -630,11 +638,19 @@ void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn)
 // Grids of fewer than 128 tiles leave most CUs idle: split K over up to
 // 256 workgroups, at least 64 deep each (not with a cull map, whose per-tile
 // state is read by the single-pass kernel).
+// A requested K depth (device tiles 128 x depth x 128) is honoured up to a
+// split-K workspace of kMaxSplitWs bytes; deeper slices beyond that.
+constexpr uint64_t kMaxSplitWs = 256ull << 20;
+
 static uint32_t gemm_f32_splits(const F32Gemm &p)
 {
     if (p.ktile_state || p.cull) return 1;
-    if (p.k_split_depth >= BK && p.k_split_depth < p.K)
-        return std::min<uint32_t>(256, (p.K + p.k_split_depth - 1) / p.k_split_depth);
+    if (p.k_split_depth >= BK && p.k_split_depth < p.K) {
+        const uint64_t per_split = static_cast<uint64_t>(p.M) * p.N * sizeof(float);
+        const uint64_t cap = std::max<uint64_t>(1, kMaxSplitWs / per_split);
+        return static_cast<uint32_t>(
+            std::min<uint64_t>(std::min<uint64_t>(256, cap), (p.K + p.k_split_depth - 1) / p.k_split_depth));
+    }
     if (p.k_split_depth >= p.K) return 1;
     const uint32_t tiles = ((p.N + BN - 1) / BN) * ((p.M + BM - 1) / BM);
     uint32_t splits = 1;

@@ -338,6 +338,28 @@ VNPU_API void VNPU_CALL vnpu_node_config_init(vnpu_node_config_t *config)
 // Device lifecycle (reference runtime.cpp:817-1152)
 // ---------------------------------------------------------------------------
 
+namespace {
+
+enum : uint32_t { kTilesI8 = 1, kTilesF32 = 2 };
+
+// Stores a tile triple (cull-mask sampling, device info) and derives the GEMM
+// kernels it forces for the dtypes in `which`; the other dtype keeps its
+// forced choice.  int8: the kernel named by gemm_i8_variant_for_tiles.  f32:
+// 128 x depth x 128 fixes the K depth per workgroup of the split-K kernel.
+void apply_tiles(vnpu_device_t *device, uint32_t tm, uint32_t tk, uint32_t tn, uint32_t which)
+{
+    device->tile_m.store(tm);
+    device->tile_k.store(tk);
+    device->tile_n.store(tn);
+    device->info.tile_m = tm;
+    device->info.tile_k = tk;
+    device->info.tile_n = tn;
+    if (which & kTilesI8) device->i8_variant.store(vnpu::k::gemm_i8_variant_for_tiles(tm, tk, tn));
+    if (which & kTilesF32) device->f32_depth.store(tm == 128 && tn == 128 && tk % 16 == 0 ? tk : 0);
+}
+
+}  // namespace
+
 VNPU_API vnpu_status_t VNPU_CALL vnpu_device_create(const vnpu_config_t *config,
                                                     vnpu_device_t **out_device)
 {
@@ -378,9 +400,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_device_create(const vnpu_config_t *config,
             tk = 128;
             tn = 64;
         }
-        d->tile_m.store(tm);
-        d->tile_k.store(tk);
-        d->tile_n.store(tn);
+        apply_tiles(d, tm, tk, tn, kTilesI8 | kTilesF32);
         // "threads" = parallel units: the CU count unless the caller pins it.
         const uint32_t units = cfg.num_threads ? cfg.num_threads : d->cu_count;
 
@@ -513,16 +533,12 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_device_reset(vnpu_device_t *device)
     return VNPU_OK;
 }
 
+
 VNPU_API vnpu_status_t VNPU_CALL vnpu_device_set_tiles(vnpu_device_t *device, uint32_t tile_m,
                                                        uint32_t tile_k, uint32_t tile_n)
 {
     if (!device || !tile_m || !tile_k || !tile_n) return VNPU_ERR_INVALID_ARGUMENT;
-    device->tile_m.store(tile_m);
-    device->tile_k.store(tile_k);
-    device->tile_n.store(tile_n);
-    device->info.tile_m = tile_m;
-    device->info.tile_k = tile_k;
-    device->info.tile_n = tile_n;
+    apply_tiles(device, tile_m, tile_k, tile_n, kTilesI8 | kTilesF32);
     return VNPU_OK;
 }
 
@@ -1172,6 +1188,15 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
         std::memset(result, 0, sizeof(*result));
         const uint32_t orig_tm = device->tile_m.load(), orig_tk = device->tile_k.load(),
                        orig_tn = device->tile_n.load();
+        // Only the tuned dtype's forced kernel changes; the other dtype's
+        // choice is left as it was.
+        const uint32_t which = dtype == VNPU_DTYPE_I8 ? kTilesI8 : kTilesF32;
+        const uint32_t orig_i8 = device->i8_variant.load(), orig_f32 = device->f32_depth.load();
+        auto restore_tiles = [&]() {
+            apply_tiles(device, orig_tm, orig_tk, orig_tn, 0);
+            device->i8_variant.store(orig_i8);
+            device->f32_depth.store(orig_f32);
+        };
         const bool trace_was_on = device->trace.enabled.exchange(false);
         struct Restore {
             vnpu_device_t *d;
@@ -1227,8 +1252,8 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
         VNPU_HIP(create_timing_event(&e0));
         VNPU_HIP(create_timing_event(&e1));
         auto time_tiles = [&](uint32_t tm, uint32_t tk, uint32_t tn, double &best) -> vnpu_status_t {
-            vnpu_status_t r = vnpu_device_set_tiles(device, tm, tk, tn);
-            if (r == VNPU_OK) r = vnpu_stream_submit(s, &cmd, 1, nullptr);   // warm-up
+            apply_tiles(device, tm, tk, tn, which);
+            vnpu_status_t r = vnpu_stream_submit(s, &cmd, 1, nullptr);   // warm-up
             if (r == VNPU_OK) r = vnpu_stream_sync(s);
             best = 1e30;
             for (uint32_t i = 0; r == VNPU_OK && i < iterations; ++i) {
@@ -1256,25 +1281,39 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
             cands.push_back({128, (K + 15) / 16 * 16, 128});                 // no K split
             for (uint32_t d = (K / 2) / 16 * 16; d >= 64; d = (d / 2) / 16 * 16) cands.push_back({128, d, 128});
         }
+        // The baseline is the kernel the device would run without the tune.
         double baseline = 0.0;
-        rc = time_tiles(orig_tm, orig_tk, orig_tn, baseline);
+        {
+            rc = vnpu_stream_submit(s, &cmd, 1, nullptr);
+            if (rc == VNPU_OK) rc = vnpu_stream_sync(s);
+            baseline = 1e30;
+            for (uint32_t i = 0; rc == VNPU_OK && i < iterations; ++i) {
+                VNPU_HIP(hipEventRecord(e0, s->hip));
+                rc = vnpu_stream_submit(s, &cmd, 1, nullptr);
+                VNPU_HIP(hipEventRecord(e1, s->hip));
+                if (rc == VNPU_OK) rc = vnpu_stream_sync(s);
+                float ms = 0.0f;
+                VNPU_HIP(hipEventElapsedTime(&ms, e0, e1));
+                baseline = std::min(baseline, static_cast<double>(ms));
+            }
+        }
         double best_ms = baseline;
         Cand best{orig_tm, orig_tk, orig_tn};
+        bool improved = false;
         for (size_t i = 0; rc == VNPU_OK && i < cands.size(); ++i) {
             double ms = 0.0;
             rc = time_tiles(cands[i].tm, cands[i].tk, cands[i].tn, ms);
             if (rc == VNPU_OK && ms < best_ms) {
                 best_ms = ms;
                 best = cands[i];
+                improved = true;
             }
         }
         (void)hipEventDestroy(e0);
         (void)hipEventDestroy(e1);
-        if (rc != VNPU_OK) {
-            vnpu_device_set_tiles(device, orig_tm, orig_tk, orig_tn);
-            return rc;
-        }
-        vnpu_device_set_tiles(device, best.tm, best.tk, best.tn);
+        restore_tiles();
+        if (rc != VNPU_OK) return rc;
+        if (improved) apply_tiles(device, best.tm, best.tk, best.tn, which);
         result->tile_m = best.tm;
         result->tile_k = best.tk;
         result->tile_n = best.tn;

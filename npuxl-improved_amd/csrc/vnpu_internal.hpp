@@ -164,6 +164,11 @@ struct vnpu_device {
     std::atomic<uint32_t> active_workers{0};
     std::atomic<uint32_t> last_opcode{0};
     std::atomic<uint32_t> tile_m{0}, tile_k{0}, tile_n{0};
+    // GEMM kernels forced by tile triples, one choice per dtype: set together
+    // by vnpu_device_set_tiles, but vnpu_autotune_gemm writes only the choice
+    // of the dtype it tuned.  0 = automatic.
+    std::atomic<uint32_t> i8_variant{0};   // int8 GEMM kernel (gemm_i8_variant_for_tiles)
+    std::atomic<uint32_t> f32_depth{0};    // f32 K depth per workgroup (split-K)
     std::vector<vnpu_stream_t *> streams;
     std::mutex stream_mutex;
     vnpu_interrupt_cb_t irq_cb = nullptr;

@@ -37,6 +37,8 @@ def lib() -> C.CDLL:
             "vo_pack_canonical": (None, [vp, u32, u32, u32, u32, vp, vp]),
             "vo_gemm_i8_acc": (None, [vp, u32, vp, u32, u32, u32, vp]),
             "vo_matmul_i8": (None, [vp, u32, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32]),
+            "vo_store_i8": (None, [vp, vp, vp, vp, vp, u32, u32, u32]),
+            "vo_store_f32": (None, [vp, vp, vp, u32, u32, f32, f32, u32]),
             "vo_matmul_f32": (None, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, u32,
                                      f32, f32, u32, vp]),
             "vo_matmul_f32_acc64": (None, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32,
@@ -117,6 +119,34 @@ def matmul_i8(A, Bkn, scale_a=None, scale_b=None, bias=None, epilogue: int = 0):
     lib().vo_matmul_i8(_p(A), K, _p(Bkn), _p(_c(scale_a, np.float32)), _p(_c(scale_b, np.float32)),
                        _p(_c(bias, np.float32)), _p(C_), N, M, K, N, epilogue)
     return C_
+
+
+def matmul_i8_blas(A, Bkn, scale_a=None, scale_b=None, bias=None, epilogue: int = 0):
+    """matmul_i8 for large shapes: the int32 accumulator is the float64 BLAS
+    product of the int8 matrices (exact: every partial sum is an integer below
+    2^53), then the C store step vo_store_i8 (the same rounding order as
+    vo_matmul_i8; tests/test_oracle_blas.py checks the two agree bit for bit)."""
+    A, Bkn = _c(A, np.int8), _c(Bkn, np.int8)
+    M, N = A.shape[0], Bkn.shape[1]
+    acc = np.ascontiguousarray((A.astype(np.float64) @ Bkn.astype(np.float64)).astype(np.int32))
+    C_ = np.empty((M, N), np.float32)
+    lib().vo_store_i8(_p(acc), _p(_c(scale_a, np.float32)), _p(_c(scale_b, np.float32)),
+                      _p(_c(bias, np.float32)), _p(C_), M, N, epilogue)
+    return C_
+
+
+def matmul_f32_blas(A, B, C_in=None, bias=None, trans_a=0, trans_b=0, alpha=1.0, beta=0.0,
+                    epilogue=0):
+    """matmul_f32 with a float64 accumulator (vo_matmul_f32_acc64's semantics)
+    for large shapes: the float64 BLAS product, then the C store step
+    vo_store_f32."""
+    A64 = np.asarray(A, np.float64)
+    B64 = np.asarray(B, np.float64)
+    acc = np.ascontiguousarray((A64.T if trans_a else A64) @ (B64.T if trans_b else B64))
+    M, N = acc.shape
+    out = np.zeros((M, N), np.float32) if C_in is None else np.array(C_in, np.float32, copy=True)
+    lib().vo_store_f32(_p(acc), _p(_c(bias, np.float32)), _p(out), M, N, alpha, beta, epilogue)
+    return out
 
 
 def matmul_f32(A, B, C_in=None, bias=None, M=None, K=None, N=None, trans_a=0, trans_b=0,

@@ -189,6 +189,24 @@ void vo_matmul_i8(const int8_t *A, uint32_t lda, const int8_t *Bkn, const float 
     free(acc);
 }
 
+/* The store_i8_c step above for accumulators computed elsewhere (an exact
+ * float64 product of int8 matrices is the int32 accumulator): lets the tests
+ * check full-size GEMMs through BLAS with this file's rounding order. */
+void vo_store_i8(const int32_t *acc, const float *scale_a, const float *scale_b,
+                 const float *bias, float *C, uint32_t M, uint32_t N, uint32_t epilogue)
+{
+    for (uint32_t m = 0; m < M; ++m) {
+        float sa = scale_a ? scale_a[m] : 1.0f;
+        for (uint32_t n = 0; n < N; ++n) {
+            float sb = scale_b ? scale_b[n] : 1.0f;
+            float out = (float)acc[(size_t)m * N + n] * sa;
+            out = out * sb;
+            if (bias) out += bias[n];
+            C[(size_t)m * N + n] = vo_apply_epilogue(out, epilogue);
+        }
+    }
+}
+
 /* ----------------------------------------------------------------------- */
 /* F32 GEMM: kernels.cpp:43-75 (store_c, zero_c_tile, scalar tile) with the   */
 /* defaults of scheduler.cpp:274-318 (alpha 0 -> 1, ld 0 -> dense).           */
@@ -256,6 +274,23 @@ void vo_matmul_f32_acc64(const float *A, const float *B, const float *bias, floa
                        (double)load_b(B, ldb, trans_b, k, n);
             float *dst = C + (size_t)m * ldc + n;
             float out = alpha * (float)acc;
+            if (bias) out += bias[n];
+            if (beta != 0.0f) out += beta * *dst;
+            *dst = vo_apply_epilogue(out, epilogue);
+        }
+}
+
+/* The store step of vo_matmul_f32_acc64 for double accumulators computed
+ * elsewhere (float64 BLAS in the tests): C = epi(alpha*(float)acc + bias +
+ * beta*C), C dense [M][N]. */
+void vo_store_f32(const double *acc, const float *bias, float *C, uint32_t M, uint32_t N,
+                  float alpha, float beta, uint32_t epilogue)
+{
+    if (alpha == 0.0f) alpha = 1.0f;
+    for (uint32_t m = 0; m < M; ++m)
+        for (uint32_t n = 0; n < N; ++n) {
+            float *dst = C + (size_t)m * N + n;
+            float out = alpha * (float)acc[(size_t)m * N + n];
             if (bias) out += bias[n];
             if (beta != 0.0f) out += beta * *dst;
             *dst = vo_apply_epilogue(out, epilogue);

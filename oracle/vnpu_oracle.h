@@ -36,6 +36,11 @@ void vo_matmul_i8(const int8_t *A, uint32_t lda, const int8_t *Bkn, const float 
                   const float *scale_b, const float *bias, float *C, uint32_t ldc, uint32_t M,
                   uint32_t K, uint32_t N, uint32_t epilogue);
 
+void vo_store_i8(const int32_t *acc, const float *scale_a, const float *scale_b,
+                 const float *bias, float *C, uint32_t M, uint32_t N, uint32_t epilogue);
+void vo_store_f32(const double *acc, const float *bias, float *C, uint32_t M, uint32_t N,
+                  float alpha, float beta, uint32_t epilogue);
+
 void vo_matmul_f32(const float *A, const float *B, const float *bias, float *C, uint32_t M,
                    uint32_t K, uint32_t N, uint32_t lda, uint32_t ldb, uint32_t ldc,
                    uint32_t trans_a, uint32_t trans_b, float alpha, float beta, uint32_t epilogue,

@@ -6,6 +6,8 @@ the oracle's restatement, the layout steps are numpy transposes.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 import oracle
@@ -14,6 +16,77 @@ import oracle
 def gemm(x, wq, ws):
     a8, sa = oracle.quantize(x, 0)
     return oracle.matmul_i8(a8, wq, sa, ws)
+
+
+def attention_threaded(q, K, V, causal=1, workers=None):
+    """oracle.attention over (batch, head) slices on a thread pool (the C call
+    releases the GIL); each slice is the same C restatement, so the result
+    equals one oracle.attention call."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    B, H = q.shape[:2]
+    out = np.empty_like(q)
+
+    def one(i):
+        b, h = divmod(i, H)
+        out[b, h] = oracle.attention(q[b:b + 1, h:h + 1], K[b:b + 1, h:h + 1],
+                                     V[b:b + 1, h:h + 1], None, causal)[0, 0]
+
+    with ThreadPoolExecutor(max_workers=workers or min(16, os.cpu_count() or 1)) as ex:
+        list(ex.map(one, range(B * H)))
+    return out
+
+
+def block_stages(shape, wq, norm_attn, norm_ffn, x, batch, tokens, past=0, k_cache=None,
+                 v_cache=None, eps=1e-5, theta=10000.0):
+    """The block of block() at any size, keeping every stage: the int8 GEMMs
+    through oracle.matmul_i8_blas (bit-identical to oracle.matmul_i8) and
+    attention per (batch, head) on threads.  Returns name -> array, with the
+    inputs of the four per-row quantize stages under xn1, att, xn2, ff."""
+    d, H, D = shape.d_model, shape.heads, shape.head_dim
+    B, T = batch, tokens
+    st = {}
+    x = np.array(x, np.float32, copy=True)
+    st["xn1"] = oracle.rmsnorm(x, norm_attn, eps)
+
+    def g(name, a):
+        a8, sa = oracle.quantize(a, 0)
+        return oracle.matmul_i8_blas(a8, wq[name][0], sa, wq[name][1])
+
+    st["qkv"] = qkv = g("qkv", st["xn1"])
+
+    def heads(part):
+        return np.ascontiguousarray(part.reshape(B, T, H, D).transpose(0, 2, 1, 3))
+
+    q, k, v = heads(qkv[:, :d]), heads(qkv[:, d:2 * d]), heads(qkv[:, 2 * d:])
+    q, k = oracle.rope(q, k, position_offset=past, theta=theta, scaling=1.0)
+    st["q"], st["k"], st["v"] = q, k, v
+    if k_cache is not None:
+        Kc = np.array(k_cache, np.float32, copy=True)
+        Vc = np.array(v_cache, np.float32, copy=True)
+        Kc[:, :, past:past + T] = k
+        Vc[:, :, past:past + T] = v
+    else:
+        Kc, Vc = k, v
+    st["o"] = o = attention_threaded(q, Kc, Vc, 1)
+    st["att"] = att = np.ascontiguousarray(o.transpose(0, 2, 1, 3).reshape(B * T, d))
+    st["x1"] = x1 = oracle.add(x, g("o", att), 1.0, 1.0)
+    st["xn2"] = xn2 = oracle.rmsnorm(x1, norm_ffn, eps)
+    a8, sa = oracle.quantize(xn2, 0)
+    st["gate"] = gate = oracle.matmul_i8_blas(a8, wq["gate"][0], sa, wq["gate"][1])
+    st["up"] = up = oracle.matmul_i8_blas(a8, wq["up"][0], sa, wq["up"][1])
+    st["ff"] = ff = oracle.swiglu(gate, up, 1.0)
+    st["out"] = oracle.add(x1, g("down", ff), 1.0, 1.0)
+    return st
+
+
+def flips(a, b):
+    """Number of int8 elements that differ between the per-row quantizations
+    of two f32 tensors (the scales are compared too: a differing scale counts
+    its whole row)."""
+    qa, sa = oracle.quantize(np.asarray(a, np.float32), 0)
+    qb, sb = oracle.quantize(np.asarray(b, np.float32), 0)
+    return int(np.count_nonzero(qa != qb)), int(np.count_nonzero(sa != sb))
 
 
 def block(shape, wq, norm_attn, norm_ffn, x, batch, tokens, past=0, k_cache=None, v_cache=None,

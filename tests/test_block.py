@@ -88,67 +88,135 @@ def test_gpu_block_matches_oracle(gpu, shape, batch, tokens, past, cache_len):
     assert oracle.rel_error(got, want) <= TOL
 
 
-@pytest.mark.gpu
-def test_gpu_block_full_decode_stagewise(gpu):
-    """Config 4 decode at full size (batch 8, context 4096, new token at 4095),
-    stage by stage: each op's GPU output against the oracle applied to the
-    GPU's own input of that stage (integer stages bit-exact, f32 stages within
-    their op tolerance).
+def test_block_stages_equals_block():
+    """The staged oracle the full-size tests use (BLAS int8 GEMMs, threaded
+    attention) is bit-identical to the plain composition."""
+    w32 = weights_f32(TINY, "test/stages")
+    wq = {n: oracle.quantize(w32[n], 1) for n in PROJECTIONS}
+    for batch, tokens, past, cache_len in ((1, 37, 0, 0), (3, 2, 20, 22)):
+        x, kc, vc = _inputs(TINY, batch, tokens, cache_len, "test/stages")
+        a = block_oracle.block(TINY, wq, w32["norm_attn"], w32["norm_ffn"], x, batch, tokens,
+                               past=past, k_cache=kc, v_cache=vc)
+        st = block_oracle.block_stages(TINY, wq, w32["norm_attn"], w32["norm_ffn"], x, batch, tokens,
+                                       past=past, k_cache=kc, v_cache=vc)
+        assert np.array_equal(a.view(np.uint32), st["out"].view(np.uint32))
 
-    End to end the block is not compared at this size: it re-quantizes its
-    activations to int8 four times, and f32 differences of ~1e-5 in the
-    attention output (summation order) flip ~0.3% of the next int8 roundings;
-    the flips compound through the O projection and the FFN until the input of
-    the down projection differs in hundreds of +-1 steps per row, ~4e-2 on
-    outputs of magnitude ~5.  The reference and the oracle agree end to end
-    only because both are the same CPU f32 arithmetic.
-    """
-    shape, B, T, ctx = LLAMA_4096, 8, 1, 4096
+
+# End-to-end bound of the full-size block against the oracle: every stage
+# matches its own bar, but the four per-row re-quantizations amplify f32
+# rounding differences.  Measured on MI355X: decode 9.9e-3 (int8 flips per
+# quantize stage 0 / 56 / 37 / 843 of 32768..88064 elements), prefill
+# 1.53e-2 (6 / 5628 / 44635 / 433199 of 8.4M..22.5M); the bounds are twice
+# that.
+FULL_E2E_BOUND = {"decode": 0.02, "prefill": 0.03}
+
+
+def _full_block(gpu, B, T, past, ctx, tag):
+    shape = LLAMA_4096
     d, H, D, F = shape.d_model, shape.heads, shape.head_dim, shape.ffn
     w32 = weights_f32(shape, "config4")
     blk = Block(gpu, shape, w32)
     try:
-        blk.prepare(B, T, past=ctx - 1, cache_len=ctx)
-        x0, kc0, vc0 = _inputs(shape, B, T, ctx, "config4/decode")
+        blk.prepare(B, T, past=past, cache_len=ctx)
+        x0, kc0, vc0 = _inputs(shape, B, T, ctx, tag)
         blk.set_input(x0, kc0, vc0)
         blk.run(True)
+        rows = B * T
         get = lambda n, shp: gpu.download(blk.bufs[n], np.float32, shp)
         wq = {n: blk.quantized_weights(n) for n in PROJECTIONS}
-        qkv, q, k, v = (get("qkv", (B, 3 * d)), get("q", (B, H, T, D)), get("k", (B, H, T, D)),
-                        get("v", (B, H, T, D)))
-        kv = (B, H, ctx, D)
-        kc, vc, o, att = get("k_cache", kv), get("v_cache", kv), get("o", (B, H, T, D)), get("att", (B, d))
-        gate, up, ff, down, x = (get("gate", (B, F)), get("up", (B, F)), get("ff", (B, F)),
-                                 get("proj", (B, d)), get("x", (B, d)))
-        xn2 = get("xn", (B, d))
+        out = {"qkv": get("qkv", (rows, 3 * d)), "q": get("q", (B, H, T, D)), "k": get("k", (B, H, T, D)),
+               "v": get("v", (B, H, T, D)), "o": get("o", (B, H, T, D)), "att": get("att", (rows, d)),
+               "gate": get("gate", (rows, F)), "up": get("up", (rows, F)), "ff": get("ff", (rows, F)),
+               "down": get("proj", (rows, d)), "x": get("x", (rows, d)), "xn2": get("xn", (rows, d))}
+        if ctx:
+            kv = (B, H, ctx, D)
+            out["k_cache"], out["v_cache"] = get("k_cache", kv), get("v_cache", kv)
     finally:
         blk.close()
+    # The first RMSNorm's output is overwritten by the second inside the
+    # block: the same op alone on the GPU (its row kernel is the block's, bit
+    # for bit, tests/test_gpu_rowchain.py) gives the GPU's first quantize input.
+    import gpu_ops as g
+    out["xn1"] = g.unary_rows(gpu, abi.OP_RMSNORM_F32, x0, W=w32["norm_attn"], eps=1e-5)
+    return shape, w32, wq, (x0, kc0, vc0), out
+
+
+def _check_stages(shape, w32, wq, inputs, gpu_out, B, T, past, ctx):
+    """Each op's GPU output against the oracle applied to the GPU's own input
+    of that stage; then the whole block against the oracle's chain from the
+    same x.  Returns (end-to-end error, per-stage flip counts)."""
+    d, H, D = shape.d_model, shape.heads, shape.head_dim
+    x0, kc0, vc0 = inputs
+    G = gpu_out
 
     def gemm(a, name):
         a8, sa = oracle.quantize(a, 0)
-        return oracle.matmul_i8(a8, wq[name][0], sa, wq[name][1])
+        return oracle.matmul_i8_blas(a8, wq[name][0], sa, wq[name][1])
 
     def heads(part):
         return np.ascontiguousarray(part.reshape(B, T, H, D).transpose(0, 2, 1, 3))
 
-    xn1 = oracle.rmsnorm(x0, w32["norm_attn"], 1e-5)
-    assert oracle.rel_error(qkv, gemm(xn1, "qkv")) <= 1e-4
-    qr, kr = oracle.rope(heads(qkv[:, :d]), heads(qkv[:, d:2 * d]), position_offset=ctx - 1)
-    assert oracle.rel_error(q, qr) <= 1e-4 and oracle.rel_error(k, kr) <= 1e-4
-    assert np.array_equal(v, heads(qkv[:, 2 * d:]))
-    assert np.array_equal(kc[:, :, ctx - 1:], k) and np.array_equal(vc[:, :, ctx - 1:], v)
-    assert np.array_equal(kc[:, :, :ctx - 1], kc0[:, :, :ctx - 1])
-    assert oracle.rel_error(o, oracle.attention(q, kc, vc, None, 1)) <= TOL
-    assert np.array_equal(att, o.transpose(0, 2, 1, 3).reshape(B, d))
+    bits = lambda a, b: np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert oracle.rel_error(G["xn1"], oracle.rmsnorm(x0, w32["norm_attn"], 1e-5)) <= 1e-4
+    assert bits(G["qkv"], gemm(G["xn1"], "qkv"))
+    qr, kr = oracle.rope(heads(G["qkv"][:, :d]), heads(G["qkv"][:, d:2 * d]), position_offset=past)
+    assert oracle.rel_error(G["q"], qr) <= 1e-4 and oracle.rel_error(G["k"], kr) <= 1e-4
+    assert np.array_equal(G["v"], heads(G["qkv"][:, 2 * d:]))
+    if ctx:
+        kc, vc = G["k_cache"], G["v_cache"]
+        assert np.array_equal(kc[:, :, past:past + T], G["k"]) and np.array_equal(vc[:, :, past:past + T], G["v"])
+        assert np.array_equal(kc[:, :, :past], kc0[:, :, :past])
+    else:
+        kc, vc = G["k"], G["v"]
+    att_err = oracle.rel_error(G["o"], block_oracle.attention_threaded(G["q"], kc, vc, 1))
+    assert att_err <= TOL
+    assert np.array_equal(G["att"], G["o"].transpose(0, 2, 1, 3).reshape(B * T, d))
     # x after the attention residual is not kept by the harness: rebuild it
-    # from the GPU's attention output (integer GEMM and exact add), then
-    # check the FFN stages from the GPU's own normalized input.
-    x1 = oracle.add(x0, gemm(att, "o"), 1.0, 1.0)
-    assert oracle.rel_error(xn2, oracle.rmsnorm(x1, w32["norm_ffn"], 1e-5)) <= 1e-4
-    a8, sa = oracle.quantize(xn2, 0)
-    assert np.array_equal(gate, oracle.matmul_i8(a8, wq["gate"][0], sa, wq["gate"][1]))
-    assert np.array_equal(up, oracle.matmul_i8(a8, wq["up"][0], sa, wq["up"][1]))
-    assert oracle.rel_error(ff, oracle.swiglu(gate, up, 1.0)) <= 1e-4
-    a8, sa = oracle.quantize(ff, 0)
-    assert np.array_equal(down, oracle.matmul_i8(a8, wq["down"][0], sa, wq["down"][1]))
-    assert np.isfinite(x).all()
+    # from the GPU's attention output (exact integer GEMM, the oracle's add).
+    x1 = oracle.add(x0, gemm(G["att"], "o"), 1.0, 1.0)
+    assert oracle.rel_error(G["xn2"], oracle.rmsnorm(x1, w32["norm_ffn"], 1e-5)) <= 1e-4
+    assert bits(G["gate"], gemm(G["xn2"], "gate")) and bits(G["up"], gemm(G["xn2"], "up"))
+    assert oracle.rel_error(G["ff"], oracle.swiglu(G["gate"], G["up"], 1.0)) <= 1e-4
+    assert bits(G["down"], gemm(G["ff"], "down"))
+    assert oracle.rel_error(G["x"], oracle.add(x1, G["down"], 1.0, 1.0)) <= 1e-6
+    assert np.isfinite(G["x"]).all()
+
+    st = block_oracle.block_stages(shape, wq, w32["norm_attn"], w32["norm_ffn"], x0, B, T, past=past,
+                                   k_cache=kc0, v_cache=vc0)
+    e2e = oracle.rel_error(G["x"], st["out"])
+    fl = {n: block_oracle.flips(G[n], st[n]) for n in ("xn1", "att", "xn2", "ff")}
+    return e2e, fl, att_err
+
+
+@pytest.mark.gpu
+def test_gpu_block_full_decode_stagewise(gpu):
+    """Config 4 decode at full size (batch 8, context 4096, new token at 4095).
+
+    Stage by stage, each op's GPU output against the oracle applied to the
+    GPU's own input of that stage: integer stages (QKV, gate/up, down GEMMs,
+    the layout steps) bit-exact, f32 stages within their op bar, attention
+    within 2e-3.  End to end the block is compared with the oracle's chain
+    from the same input, and the number of int8 elements that differ at each
+    of the four per-row quantize stages is printed: f32 rounding differences
+    of ~1e-7..1e-6 (summation order in RMSNorm and attention, libm in RoPE)
+    flip a few int8 roundings, and each flip moves later stages by a whole
+    int8 step, so the end-to-end error is the flips', not the ops'.
+    """
+    B, T, ctx = 8, 1, 4096
+    shape, w32, wq, inputs, G = _full_block(gpu, B, T, ctx - 1, ctx, "config4/decode")
+    e2e, fl, att_err = _check_stages(shape, w32, wq, inputs, G, B, T, ctx - 1, ctx)
+    print(f"\n[block decode B8 ctx4096] attention {att_err:.3g}, end to end {e2e:.3g}, "
+          f"int8 flips per stage (elements, scales): {fl}", flush=True)
+    assert e2e <= FULL_E2E_BOUND["decode"]
+
+
+@pytest.mark.gpu
+def test_gpu_block_full_prefill_stagewise(gpu):
+    """Config 4 prefill at full size (batch 1, 2048 tokens, causal), with the
+    same stage-by-stage bars and end-to-end report as the decode test."""
+    B, T = 1, 2048
+    shape, w32, wq, inputs, G = _full_block(gpu, B, T, 0, 0, "config4/prefill")
+    e2e, fl, att_err = _check_stages(shape, w32, wq, inputs, G, B, T, 0, 0)
+    print(f"\n[block prefill B1 S2048] attention {att_err:.3g}, end to end {e2e:.3g}, "
+          f"int8 flips per stage (elements, scales): {fl}", flush=True)
+    assert e2e <= FULL_E2E_BOUND["prefill"]
