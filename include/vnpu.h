@@ -746,6 +746,20 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_speculative_step(vnpu_cluster_t *cluster,
  * a NULL stream. */
 VNPU_API void *VNPU_CALL vnpu_stream_hip_handle(vnpu_stream_t *stream);
 
+/* MI355X extension (additive; no counterpart in the reference): ATTENTION_F32
+ * that allocates nothing, for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops).  Same arguments and kernels
+ * as vnpu_attention_f32, but Q, K, V, mask and O must be device memory
+ * (vnpu_buffer_host_ptr or hipMalloc), the call only enqueues on the stream
+ * (completion: vnpu_stream_sync or later work on the stream), and its
+ * scratch is one 64 MiB device array per GPU held for the life of the
+ * process: shapes needing more (the split K/V^T blocks of prefill beyond
+ * 64 MiB, e.g. 32 heads x more than 2048 keys at head_dim 128) return
+ * VNPU_ERR_INVALID_ARGUMENT, as do host pointers.  Every call on a GPU shares
+ * that array, so calls that overlap on one GPU race. */
+VNPU_API vnpu_status_t VNPU_CALL vnpu_attention_f32_noalloc(vnpu_stream_t *stream,
+                                                            const vnpu_attention_f32_args_t *args);
+
 /* Helpers (reference include/vnpu.h:745-750). */
 VNPU_API uint16_t VNPU_CALL vnpu_float_to_bf16(float value);
 VNPU_API uint16_t VNPU_CALL vnpu_float_to_f16(float value);

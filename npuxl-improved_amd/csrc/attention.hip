@@ -20,8 +20,17 @@
 #include <atomic>
 #include "device_math.hpp"
 #include "lds_dma.hpp"
+#include "vnpu_internal.hpp"
 
 #include <algorithm>
+#include <mutex>
+
+// Device scratch of vnpu_attention_f32_noalloc (partial (m, l, acc) triples of
+// split decode, the split K / V^T blocks of prefill): 64 MiB, the prefill
+// need of B1 x 32 heads x 2048 keys at head_dim 128.  Each GPU holds its own
+// copy for the life of the process; host code uses only the address
+// hipGetSymbolAddress returns for the current device, never this name.
+static __device__ __align__(256) float scratch[vnpu::k::kAttnScratchBytes / sizeof(float)];
 
 namespace vnpu {
 namespace k {
@@ -912,6 +921,32 @@ void plan(const Attn &a, uint32_t &qblocks, uint32_t &splits, uint32_t &kps)
 }
 
 }  // namespace
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch[kMaxScratchDevices] = {};
+}  // namespace
+
+void attention_scratch_setup(int hip_device)
+{
+    if (hip_device < 0 || hip_device >= kMaxScratchDevices)
+        throw HipError("attention scratch: device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[hip_device]) return;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        throw HipError(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch[hip_device] = static_cast<float *>(ptr);
+}
+
+float *attention_scratch(int hip_device)
+{
+    if (hip_device < 0 || hip_device >= kMaxScratchDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch[hip_device];
+}
 
 size_t attention_ws_bytes(const Attn &a)
 {

@@ -760,9 +760,10 @@ void exec_elementwise(vnpu_stream_t *s, const vnpu_command_t &cmd, ExecStats &st
     sg.finish();
 }
 
-void exec_attention(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecStats &st)
+// execute_attention (scheduler.cpp:583-608), scale default llm.cpp:452-453:
+// validation and the kernel parameters, pointers left to the caller.
+k::Attn attention_params(const vnpu_attention_f32_args_t &a)
 {
-    // execute_attention (scheduler.cpp:583-608), scale default llm.cpp:452-453
     require(a.Q && a.K && a.V && a.O && a.batch && a.heads && a.seq_q && a.seq_k && a.head_dim,
             "invalid attention arguments");
     require(a.head_dim <= 256, "attention head_dim above 256 is not supported on this backend");
@@ -772,6 +773,22 @@ void exec_attention(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecSt
     p.batch = a.batch; p.heads = a.heads; p.seq_q = a.seq_q; p.seq_k = a.seq_k;
     p.head_dim = a.head_dim; p.causal = a.causal;
     p.scale = a.scale > 0.0f ? a.scale : 1.0f / std::sqrt(static_cast<float>(a.head_dim));
+    return p;
+}
+
+void account_attention(const vnpu_attention_f32_args_t &a, ExecStats &st)
+{
+    const uint64_t bh = static_cast<uint64_t>(a.batch) * a.heads;
+    const uint64_t qn = bh * a.seq_q * a.head_dim, kn = bh * a.seq_k * a.head_dim;
+    const uint64_t mn = a.mask ? bh * a.seq_q * a.seq_k : 0;
+    st.bytes_read += (qn + 2 * kn + mn) * 4;
+    st.bytes_written += qn * 4;
+    st.flops += 4ull * a.batch * a.heads * a.seq_q * a.seq_k * a.head_dim;
+}
+
+void exec_attention(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecStats &st)
+{
+    k::Attn p = attention_params(a);
     const uint64_t bh = static_cast<uint64_t>(a.batch) * a.heads;
     const uint64_t qn = bh * a.seq_q * a.head_dim, kn = bh * a.seq_k * a.head_dim;
     const uint64_t mn = a.mask ? bh * a.seq_q * a.seq_k : 0;
@@ -785,9 +802,7 @@ void exec_attention(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecSt
     k::attention(s->hip, p, ws);
     VNPU_HIP(hipGetLastError());
     sg.finish();
-    st.bytes_read += (qn + 2 * kn + mn) * 4;
-    st.bytes_written += qn * 4;
-    st.flops += 4ull * a.batch * a.heads * a.seq_q * a.seq_k * a.head_dim;
+    account_attention(a, st);
 }
 
 void exec_copy(vnpu_stream_t *s, const vnpu_copy_args_t &a, ExecStats &st)
@@ -823,6 +838,30 @@ void exec_memset(vnpu_stream_t *s, const vnpu_memset_args_t &a, ExecStats &st)
 }
 
 }  // namespace
+
+void enqueue_attention_noalloc(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecStats &st)
+{
+    k::Attn p = attention_params(a);
+    // No staging: every tensor must already be device memory.
+    require(is_device_pointer(a.Q) && is_device_pointer(a.K) && is_device_pointer(a.V) &&
+                is_device_pointer(a.O) && (!a.mask || is_device_pointer(a.mask)),
+            "attention without allocation needs device-resident Q, K, V, mask and O");
+    p.Q = a.Q; p.K = a.K; p.V = a.V; p.mask = a.mask; p.O = a.O;
+    const size_t need = k::attention_ws_bytes(p);
+    if (need > k::kAttnScratchBytes) {
+        debug_log("attention without allocation: this call needs %zu bytes of scratch, above the "
+                  "%zu-byte device scratch", need, k::kAttnScratchBytes);
+        throw ArgError("attention scratch requirement above the device scratch size");
+    }
+    float *ws = nullptr;
+    if (need) {
+        ws = k::attention_scratch(s->device->hip_device);
+        if (!ws) throw HipError("attention scratch not set up on this device");
+    }
+    k::attention(s->hip, p, ws);
+    VNPU_HIP(hipGetLastError());
+    account_attention(a, st);
+}
 
 void execute_command(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &cmd,
                      uint32_t flags, ExecStats &st)

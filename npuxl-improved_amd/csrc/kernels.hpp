@@ -152,6 +152,13 @@ struct Attn {
 };
 size_t attention_ws_bytes(const Attn &a);
 void attention(hipStream_t s, const Attn &a, float *ws);
+// The allocation-free attention entry point's device scratch: a file-scope
+// array of kAttnScratchBytes in attention.hip, one copy per GPU.  Setup looks
+// its address up once per device (that device current) and keeps it;
+// attention_scratch returns it (nullptr before setup).
+constexpr size_t kAttnScratchBytes = 64ull << 20;
+void attention_scratch_setup(int hip_device);
+float *attention_scratch(int hip_device);
 
 // ---- fills (ops.hip) ----
 void fill_u8(hipStream_t s, void *dst, uint8_t value, uint64_t bytes);

@@ -385,6 +385,10 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_device_create(const vnpu_config_t *config,
         hipDeviceProp_t prop;
         VNPU_HIP(hipGetDeviceProperties(&prop, ordinal));
 
+        // The allocation-free attention entry point's scratch address on
+        // this device (the device is current).
+        vnpu::k::attention_scratch_setup(ordinal);
+
         auto *d = new vnpu_device_t();
         d->config = cfg;
         d->hip_device = ordinal;
@@ -686,6 +690,45 @@ VNPU_API void VNPU_CALL vnpu_stream_destroy(vnpu_stream_t *stream)
 VNPU_API void *VNPU_CALL vnpu_stream_hip_handle(vnpu_stream_t *stream)
 {
     return stream ? static_cast<void *>(stream->hip) : nullptr;
+}
+
+// ATTENTION_F32 that allocates nothing (no reference counterpart): for
+// callers that cannot allocate device memory, such as code under HIP graph
+// capture or a serving loop.  The kernels are vnpu_attention_f32's; their
+// scratch is the per-GPU device array of attention.hip (set up by
+// vnpu_device_create), shared by every call on that GPU, so calls that
+// overlap on one GPU (two streams, two threads) race.  Enqueues only.
+VNPU_API vnpu_status_t VNPU_CALL vnpu_attention_f32_noalloc(vnpu_stream_t *stream,
+                                                            const vnpu_attention_f32_args_t *args)
+{
+    if (!stream || !args) return VNPU_ERR_INVALID_ARGUMENT;
+    vnpu_device_t *d = stream->device;
+    try {
+        ExecStats st;
+        std::lock_guard<std::mutex> lock(stream->mutex);
+        VNPU_HIP(hipSetDevice(d->hip_device));
+        enqueue_attention_noalloc(stream, *args, st);
+        d->bytes_read.fetch_add(st.bytes_read);
+        d->bytes_written.fetch_add(st.bytes_written);
+        d->flops.fetch_add(st.flops);
+        d->last_opcode.store(VNPU_OP_ATTENTION_F32);
+        return VNPU_OK;
+    } catch (const ArgError &e) {
+        debug_log("vnpu_attention_f32_noalloc: %s", e.what());
+        return VNPU_ERR_INVALID_ARGUMENT;
+    } catch (const std::exception &e) {
+        // A launch failure: the stream's error becomes sticky, as for a
+        // failed command of a batch.
+        debug_log("vnpu_attention_f32_noalloc: %s", e.what());
+        (void)hipGetLastError();
+        const uint32_t code = static_cast<uint32_t>(-VNPU_ERR_INTERNAL);
+        d->error.store(code);
+        d->regs[VNPU_REG_ERROR / 4].store(code);
+        stream->last_error.store(code);
+        return VNPU_ERR_INTERNAL;
+    } catch (...) {
+        return VNPU_ERR_INTERNAL;
+    }
 }
 
 VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_sync(vnpu_stream_t *stream)

@@ -208,6 +208,11 @@ uint32_t try_execute_chain(vnpu_stream_t *s, const vnpu_command_t *c, uint64_t n
 void execute_command(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &cmd,
                      uint32_t batch_flags, ExecStats &st);
 
+// ATTENTION_F32 on device-resident tensors with the device scratch of
+// attention.hip instead of the stream workspace: enqueues only, allocates
+// nothing.  Throws ArgError for invalid arguments, host pointers or a
+// scratch need above k::kAttnScratchBytes.
+void enqueue_attention_noalloc(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecStats &st);
 // Pack int8 weights (synchronous); B may be a host or a device pointer.
 vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const float *scales,
                                     uint32_t K, uint32_t N, uint32_t ldb, uint32_t trans_b);

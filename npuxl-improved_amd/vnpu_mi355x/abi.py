@@ -307,6 +307,7 @@ SIGNATURES = {
     "vnpu_unit_name": (C.c_char_p, [u32]),
     "vnpu_get_backend_v1": (vp, []),
     "vnpu_stream_hip_handle": (vp, [vp]),  # MI355X additive extension
+    "vnpu_attention_f32_noalloc": (st, [vp, vp]),  # MI355X additive extension
 }
 
 LAYOUT = {  # LP64 sizes measured on the reference header

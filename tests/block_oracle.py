@@ -18,7 +18,7 @@ def gemm(x, wq, ws):
     return oracle.matmul_i8(a8, wq, sa, ws)
 
 
-def attention_threaded(q, K, V, causal=1, workers=None):
+def attention_threaded(q, K, V, causal=1, workers=None, mask=None):
     """oracle.attention over (batch, head) slices on a thread pool (the C call
     releases the GIL); each slice is the same C restatement, so the result
     equals one oracle.attention call."""
@@ -29,8 +29,9 @@ def attention_threaded(q, K, V, causal=1, workers=None):
 
     def one(i):
         b, h = divmod(i, H)
+        m = None if mask is None else mask[b:b + 1, h:h + 1]
         out[b, h] = oracle.attention(q[b:b + 1, h:h + 1], K[b:b + 1, h:h + 1],
-                                     V[b:b + 1, h:h + 1], None, causal)[0, 0]
+                                     V[b:b + 1, h:h + 1], m, causal)[0, 0]
 
     with ThreadPoolExecutor(max_workers=workers or min(16, os.cpu_count() or 1)) as ex:
         list(ex.map(one, range(B * H)))
