@@ -366,16 +366,38 @@ def bench_config5(s: Session, steps: int):
     return out
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(M, K, N, budget_s: float):
     """The reference runtime (built from its own sources) on this host."""
     import oracle  # checker/baseline infrastructure, used only here
 
     if not os.path.exists(oracle.REF_LIB_PATH):
         return None
-    threads = min(16, os.cpu_count() or 1)
+    # The reference's default thread count is the host's physical core count
+    # (src/core/runtime.cpp:862-866): read it from the reference itself, then
+    # run at that count unless it exceeds this process's CPU share (the GPU
+    # box gives one GPU's job 16 CPUs).
     cfg = abi.Config()
     cfg.abi_version = 1
+    with Session(oracle.REF_LIB_PATH, cfg) as probe:
+        pinfo = probe.info()
+        ref_default = int(pinfo.num_threads)
+        physical = int(pinfo.physical_cores)
+    share = min(16, len(os.sched_getaffinity(0)))
+    threads = min(ref_default, share)
     cfg.num_threads = threads
+    host = {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "physical_cores": physical, "reference_default_threads": ref_default}
     with Session(oracle.REF_LIB_PATH, cfg) as r:
         info = r.info()
         w = synth.normal(f"w_{K}x{N}", (K, N), 0.02)
@@ -397,11 +419,15 @@ def cpu_baseline(M, K, N, budget_s: float):
             r.check("sync", r.sync())
             times.append(time.perf_counter() - t0)
         med = float(np.median(times))
+        capped = "" if threads == ref_default else (
+            f" (the reference default is {ref_default} threads, one per physical core; capped at "
+            f"this job's CPU share of {share})")
         return {"value": i8_bytes(M, K, N) / med / 1e9, "unit": "GB/s",
                 "cores": int(info.num_threads), "kind": "reference",
                 "sample": f"MATMUL_I8 M={M} K={K} N={N} decode GEMV, {len(times)} calls "
                           f"(median {med * 1e3:.3f} ms, best {min(times) * 1e3:.3f} ms), "
-                          f"reference AVX2 path, {info.num_threads} threads"}
+                          f"reference AVX2 path, {info.num_threads} threads{capped}",
+                "host": host}
 
 
 def main():

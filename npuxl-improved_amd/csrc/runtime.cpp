@@ -1372,46 +1372,8 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_autotune_gemm(vnpu_device_t *device, uint3
     });
 }
 
-// ---------------------------------------------------------------------------
-// Multi-host cluster and remote node API: not provided by this single-GPU
-// backend (reference src/cluster/*).  Every entry point exists so the ABI and
-// the backend table are complete; each reports UNSUPPORTED.
-// ---------------------------------------------------------------------------
+// The cluster client and the vnpu-node server are in cluster.cpp.
 
-VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_create(const vnpu_cluster_config_t *, vnpu_cluster_t **out)
-{
-    if (out) *out = nullptr;
-    return VNPU_ERR_UNSUPPORTED;
-}
-VNPU_API void VNPU_CALL vnpu_cluster_destroy(vnpu_cluster_t *) {}
-VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_add_device(vnpu_cluster_t *, vnpu_device_t *, uint32_t)
-{
-    return VNPU_ERR_UNSUPPORTED;
-}
-VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_add_remote(vnpu_cluster_t *, const vnpu_remote_node_config_t *,
-                                                         vnpu_remote_node_t **out)
-{
-    if (out) *out = nullptr;
-    return VNPU_ERR_UNSUPPORTED;
-}
-VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_get_stats(const vnpu_cluster_t *, vnpu_cluster_stats_t *)
-{
-    return VNPU_ERR_UNSUPPORTED;
-}
-VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_cache_weights_f32(vnpu_cluster_t *, const char *, const float *,
-                                                                uint32_t, uint32_t, uint32_t,
-                                                                vnpu_weight_handle_t **out)
-{
-    if (out) *out = nullptr;
-    return VNPU_ERR_UNSUPPORTED;
-}
-VNPU_API vnpu_status_t VNPU_CALL vnpu_cluster_matmul_f32(vnpu_cluster_t *, vnpu_weight_handle_t *, const float *,
-                                                         float *, uint32_t, uint32_t, uint32_t, uint32_t)
-{
-    return VNPU_ERR_UNSUPPORTED;
-}
-VNPU_API vnpu_status_t VNPU_CALL vnpu_node_run(const vnpu_node_config_t *) { return VNPU_ERR_UNSUPPORTED; }
-VNPU_API void VNPU_CALL vnpu_node_stop(void) {}
 // ---------------------------------------------------------------------------
 // Speculative step (reference src/cluster/cluster.cpp:552-646): draft gamma
 // tokens one position at a time through draft_fn, score the gamma + 1

@@ -27,6 +27,11 @@ ERR_INVALID_COMMAND = -4
 ERR_DEVICE_BUSY = -5
 ERR_DEVICE_ERROR = -6
 ERR_TIMEOUT = -7
+ERR_NETWORK = -8
+ERR_AUTH = -9
+ERR_PROTOCOL = -10
+ERR_NOT_FOUND = -11
+ERR_IO = -12
 ERR_INTERNAL = -100
 
 # opcodes (vnpu.h:164-184)
@@ -108,6 +113,29 @@ class SpeculativeResult(C.Structure):
                 ("tokens", C.c_int32 * MAX_TOKENS), ("draft_time_ms", C.c_double),
                 ("verify_time_ms", C.c_double), ("total_time_ms", C.c_double),
                 ("tokens_per_second", C.c_double), ("theoretical_speedup", C.c_double)]
+
+
+class ClusterConfig(C.Structure):
+    _fields_ = [("abi_version", C.c_uint32), ("num_streams", C.c_uint32), ("flags", C.c_uint32),
+                ("request_timeout_ms", C.c_uint32), ("auth_token", C.c_char_p), ("cluster_name", C.c_char_p)]
+
+
+class RemoteNodeConfig(C.Structure):
+    _fields_ = [("host", C.c_char_p), ("port", C.c_uint16), ("auth_token", C.c_char_p),
+                ("weight", C.c_uint32), ("flags", C.c_uint32)]
+
+
+class ClusterStats(C.Structure):
+    _fields_ = [("local_jobs", C.c_uint64), ("remote_jobs", C.c_uint64), ("total_jobs", C.c_uint64),
+                ("network_bytes_sent", C.c_uint64), ("network_bytes_received", C.c_uint64),
+                ("failed_jobs", C.c_uint64), ("culled_tiles", C.c_uint64), ("local_time_ns", C.c_double),
+                ("remote_time_ns", C.c_double), ("speedup_estimate", C.c_double)]
+
+
+class NodeConfig(C.Structure):
+    _fields_ = [("abi_version", C.c_uint32), ("port", C.c_uint16), ("reserved0", C.c_uint16),
+                ("num_threads", C.c_uint32), ("flags", C.c_uint32), ("bind_address", C.c_char_p),
+                ("auth_token", C.c_char_p), ("node_name", C.c_char_p)]
 
 
 # vnpu_logits_fn_t(user, tokens, num_tokens, first_position, num_positions, logits, vocab)
@@ -313,7 +341,8 @@ SIGNATURES = {
 LAYOUT = {  # LP64 sizes measured on the reference header
     Command: 208, MatmulF32Args: 104, MatmulI8Args: 72, AttentionArgs: 88, RopeArgs: 64,
     QuantizeArgs: 48, Config: 48, DeviceInfo: 304, DeviceStatus: 152, TraceSummary: 112,
-    TuneResult: 72, SpeculativeConfig: 32, SpeculativeResult: 312,
+    TuneResult: 72, SpeculativeConfig: 32, SpeculativeResult: 312, ClusterConfig: 32,
+    RemoteNodeConfig: 32, ClusterStats: 80, NodeConfig: 40,
 }
 
 
