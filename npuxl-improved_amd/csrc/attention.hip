@@ -882,6 +882,77 @@ void decode_launch(int qn, int v4, dim3 grid, hipStream_t s, const Attn &a, uint
     else decode_launch_v<4>(v4, grid, s, a, kps, splits, ws_acc, ws_ml);
 }
 
+// ---------------------------------------------------------------------------
+// Row-wise kernel for the shapes the tiled kernels do not take: head_dim above
+// 256 or more than 65535 (batch, head) pairs.  One workgroup per query row
+// (a 1-D grid, so any number of rows), 64-key blocks with the reference's
+// online softmax (a block whose max is not finite is skipped), scores by wave
+// dot products over the whole head dimension, and the running output kept in
+// the output row itself (no register or LDS bound on head_dim).  Every thread
+// owns the same output elements throughout, so the row needs no barrier
+// between its read-modify-write steps.
+// ---------------------------------------------------------------------------
+constexpr int RW_KEYS = 64;
+
+__global__ __launch_bounds__(kThreads) void attn_rowwise_kernel(Attn a, uint64_t row0)
+{
+    __shared__ float sc[RW_KEYS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t row = row0 + blockIdx.x;
+    const uint32_t sq = a.seq_q, sk = a.seq_k, D = a.head_dim;
+    const uint64_t bh = row / sq;
+    const uint32_t qi = static_cast<uint32_t>(row % sq);
+    const uint32_t off = sk > sq ? sk - sq : 0;
+    const float *q = a.Q + row * D;
+    const float *Kh = a.K + bh * sk * D;
+    const float *Vh = a.V + bh * sk * D;
+    float *o = a.O + row * D;
+    for (uint32_t d = tid; d < D; d += kThreads) o[d] = 0.0f;
+    float m = -__builtin_inff(), l = 0.0f;
+    uint32_t kend = sk;
+    if (a.causal) kend = min(sk, qi + off + 1);
+    for (uint32_t k0 = 0; k0 < kend; k0 += RW_KEYS) {
+        const uint32_t kc = min(static_cast<uint32_t>(RW_KEYS), kend - k0);
+        __syncthreads();   // the previous block's scores are consumed
+        for (uint32_t j = wave; j < kc; j += 4) {
+            const float *kr = Kh + static_cast<uint64_t>(k0 + j) * D;
+            float dot = 0.0f;
+            for (uint32_t d = lane; d < D; d += 64) dot = fmaf(q[d], kr[d], dot);
+            dot = dev::wave_sum(dot);
+            if (lane == 0) {
+                float s = dot * a.scale;
+                if (a.mask) s += a.mask[row * sk + k0 + j];
+                sc[j] = s;
+            }
+        }
+        __syncthreads();
+        float bmax = -__builtin_inff();
+        for (uint32_t j = 0; j < kc; ++j) bmax = fmaxf(bmax, sc[j]);
+        if (!isfinite(bmax)) continue;   // uniform over the workgroup
+        const float nm = fmaxf(m, bmax);
+        const float alpha = dev::fast_expf(m - nm);
+        float psum = 0.0f;
+        for (uint32_t j = 0; j < kc; ++j) psum += dev::fast_expf(sc[j] - nm);
+        l = l * alpha + psum;
+        for (uint32_t d = tid; d < D; d += kThreads) {
+            float acc = o[d] * alpha;
+            for (uint32_t j = 0; j < kc; ++j) {
+                const float p = dev::fast_expf(sc[j] - nm);
+                if (p != 0.0f) acc = fmaf(p, Vh[static_cast<uint64_t>(k0 + j) * D + d], acc);
+            }
+            o[d] = acc;
+        }
+        m = nm;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    for (uint32_t d = tid; d < D; d += kThreads) o[d] *= inv;
+}
+
+bool use_rowwise(const Attn &a)
+{
+    return a.head_dim > 256 || static_cast<uint64_t>(a.batch) * a.heads > 65535u;
+}
+
 bool use_decode(const Attn &a)
 {
     return a.seq_q <= 4 && (a.head_dim % 32) == 0 && a.head_dim <= 256;
@@ -894,6 +965,12 @@ bool use_prefill(const Attn &a)
 
 void plan(const Attn &a, uint32_t &qblocks, uint32_t &splits, uint32_t &kps)
 {
+    if (use_rowwise(a)) {
+        qblocks = 1;
+        splits = 1;
+        kps = a.seq_k;
+        return;
+    }
     if (use_prefill(a)) {
         qblocks = (a.seq_q + PQ - 1) / PQ;
         splits = 1;
@@ -950,6 +1027,7 @@ float *attention_scratch(int hip_device)
 
 size_t attention_ws_bytes(const Attn &a)
 {
+    if (use_rowwise(a)) return 0;
     uint32_t qb, splits, kps;
     plan(a, qb, splits, kps);
     if (use_prefill(a)) {
@@ -965,6 +1043,14 @@ size_t attention_ws_bytes(const Attn &a)
 
 void attention(hipStream_t s, const Attn &a, float *ws)
 {
+    if (use_rowwise(a)) {
+        const uint64_t rows = static_cast<uint64_t>(a.batch) * a.heads * a.seq_q;
+        for (uint64_t r0 = 0; r0 < rows; r0 += 0x7fffffffull) {
+            const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(rows - r0, 0x7fffffffull));
+            attn_rowwise_kernel<<<n, kThreads, 0, s>>>(a, r0);
+        }
+        return;
+    }
     uint32_t qb, splits, kps;
     plan(a, qb, splits, kps);
     const uint32_t D = a.head_dim;

@@ -16,6 +16,10 @@ namespace dev {
 
 __device__ __forceinline__ float fast_expf(float x)
 {
+    // z = x*log2e and f = z - floor(z) round separately, as in every build of
+    // the reference (z has a second use, so it is never fused); only the
+    // Horner steps are FMAs.
+#pragma clang fp contract(off)
     if (x < -80.0f) return 0.0f;
     if (x > 80.0f) return __builtin_inff();
     const float z = x * 1.4426950408889634f;
@@ -27,6 +31,23 @@ __device__ __forceinline__ float fast_expf(float x)
     p = fmaf(p, f, 0.6931471805599453f);
     p = fmaf(p, f, 1.0f);
     return ldexpf(p, static_cast<int>(zi));
+}
+
+// Correctly rounded f32 multiply and add that the compiler may not fuse
+// into an FMA with a neighbouring operation (HIP's __fmul_rn / __fadd_rn are
+// plain operators and can be contracted).  Used wherever the result must
+// round like the reference's separate multiply and add, e.g. the int8
+// dequantize ((float)acc * sa) * sb + bias.
+__device__ __forceinline__ float mul_rn(float a, float b)
+{
+#pragma clang fp contract(off)
+    return a * b;
+}
+
+__device__ __forceinline__ float add_rn(float a, float b)
+{
+#pragma clang fp contract(off)
+    return a + b;
 }
 
 // reference src/internal.h:112
@@ -60,7 +81,7 @@ __device__ __forceinline__ float epilogue(float v, uint32_t epi)
 // multiply; scale = max|x| / 127, zero or non-finite -> 1.
 __device__ __forceinline__ int8_t q8(float x, float inv)
 {
-    float q = roundf(__fmul_rn(x, inv));
+    float q = roundf(mul_rn(x, inv));
     // Plain compares, as the reference: a NaN passes both and converts to 0.
     if (q > 127.0f) q = 127.0f;
     if (q < -128.0f) q = -128.0f;

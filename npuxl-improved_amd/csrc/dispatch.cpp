@@ -766,9 +766,6 @@ k::Attn attention_params(const vnpu_attention_f32_args_t &a)
 {
     require(a.Q && a.K && a.V && a.O && a.batch && a.heads && a.seq_q && a.seq_k && a.head_dim,
             "invalid attention arguments");
-    require(a.head_dim <= 256, "attention head_dim above 256 is not supported on this backend");
-    require(static_cast<uint64_t>(a.batch) * a.heads <= 65535u,
-            "attention batch*heads above 65535 is not supported on this backend");
     k::Attn p;
     p.batch = a.batch; p.heads = a.heads; p.seq_q = a.seq_q; p.seq_k = a.seq_k;
     p.head_dim = a.head_dim; p.causal = a.causal;

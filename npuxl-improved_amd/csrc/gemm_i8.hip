@@ -150,8 +150,8 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_generic(I8Gemm p)
                 const uint32_t m = m0 + wm * 64 + i * 16 + fg * 4 + r;
                 if (m >= p.M) continue;
                 const float sa = p.scale_a ? p.scale_a[m] : 1.0f;
-                float out = __fmul_rn(__fmul_rn(static_cast<float>(acc[i][j][r]), sa), sb);
-                if (p.bias) out = __fadd_rn(out, bias);
+                float out = dev::mul_rn(dev::mul_rn(static_cast<float>(acc[i][j][r]), sa), sb);
+                if (p.bias) out = dev::add_rn(out, bias);
                 p.C[static_cast<uint64_t>(m) * p.ldc + n] = dev::epilogue(out, p.epilogue);
             }
         }

@@ -51,6 +51,48 @@ __device__ __forceinline__ int dot16(const int4 a, const int4 b, int acc)
     return acc;
 }
 
+// The epilogue's scales and bias for the outputs this thread stores (o = tid,
+// tid + NTH, ... below NO), loaded when the workgroup starts so their memory
+// latency overlaps the weight stream instead of following it.  The store
+// keeps the reference's order ((float)acc * sa) * sb (+ bias) -> epilogue.
+template <int NO, int NTH>
+struct EpiOperands {
+    static constexpr int S = (NO + NTH - 1) / NTH;
+    float sa[S], sb[S], bias[S];
+    __device__ __forceinline__ EpiOperands(const I8Gemm &p, uint32_t nt0, int M, int tid)
+    {
+        const uint32_t NT = p.Np >> 4;
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const int o = tid + j * NTH;
+            const int c = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
+            const uint32_t n = (nt0 + t) * 16 + c;
+            const bool live = o < NO && nt0 + t < NT && n < p.N;
+            sa[j] = live && p.scale_a ? p.scale_a[m] : 1.0f;
+            sb[j] = live ? p.scale_b[n] : 1.0f;
+            bias[j] = live && p.bias ? p.bias[n] : 0.0f;
+        }
+    }
+    template <int W, int T, int M>
+    __device__ __forceinline__ void store(const I8Gemm &p, const int (&red)[W][T][M][16], uint32_t nt0,
+                                          uint32_t NT, int tid) const
+    {
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const int o = tid + j * NTH;
+            const int c = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
+            const uint32_t n = (nt0 + t) * 16 + c;
+            if (o >= NO || nt0 + t >= NT || n >= p.N) continue;
+            int s = 0;
+#pragma unroll
+            for (int w = 0; w < W; ++w) s += red[w][t][m][c];
+            float out = dev::mul_rn(dev::mul_rn(static_cast<float>(s), sa[j]), sb[j]);
+            if (p.bias) out = dev::add_rn(out, bias[j]);
+            p.C[static_cast<uint64_t>(m) * p.ldc + n] = dev::epilogue(out, p.epilogue);
+        }
+    }
+};
+
 // M rows, W waves, U blocks in flight per wave, T strips per workgroup (each
 // activation read from LDS feeds T weight blocks); chunk_k = k extent
 // (multiple of 64) of the activations staged at a time.
@@ -74,6 +116,7 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chun
     for (int t = 0; t < T; ++t)
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[t][m] = 0;
+    const EpiOperands<T * M * 16, 64 * W> epi(p, nt0, M, tid);
 
     for (uint32_t kc = 0; kc < p.Kp; kc += chunk_k) {
         const uint32_t kt0 = kc >> 6, kt1 = min(KT, (kc + chunk_k) >> 6);
@@ -166,18 +209,7 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chun
             for (int m = 0; m < M; ++m) red[wave][t][m][lane] = acc[t][m];
     }
     __syncthreads();
-    for (int o = tid; o < T * M * 16; o += 64 * W) {
-        const int c = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
-        const uint32_t n = (nt0 + t) * 16 + c;
-        if (nt0 + t >= NT || n >= p.N) continue;
-        int s = 0;
-#pragma unroll
-        for (int w = 0; w < W; ++w) s += red[w][t][m][c];
-        const float sa = p.scale_a ? p.scale_a[m] : 1.0f;
-        float out = __fmul_rn(__fmul_rn(static_cast<float>(s), sa), p.scale_b[n]);
-        if (p.bias) out = __fadd_rn(out, p.bias[n]);
-        p.C[static_cast<uint64_t>(m) * p.ldc + n] = dev::epilogue(out, p.epilogue);
-    }
+    epi.template store<W, T, M>(p, red, nt0, NT, tid);
 }
 
 // The same stream for 3..8 rows with the int8 matrix core doing the math: a
@@ -211,6 +243,7 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
     v4i acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = (v4i){0, 0, 0, 0};
+    const EpiOperands<T * M * 16, 64 * W> epi(p, nt0, M, tid);
 
     for (uint32_t kc = 0; kc < p.Kp; kc += chunk_k) {
         const uint32_t kt0 = kc >> 6, kt1 = min(KT, (kc + chunk_k) >> 6);
@@ -286,31 +319,22 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
             if (m < M) red[wave][t][m][row] = acc[t][i];
         }
     __syncthreads();
-    for (int o = tid; o < T * M * 16; o += 64 * W) {
-        const int c = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
-        const uint32_t n = (nt0 + t) * 16 + c;
-        if (nt0 + t >= NT || n >= p.N) continue;
-        int s = 0;
-#pragma unroll
-        for (int w = 0; w < W; ++w) s += red[w][t][m][c];
-        const float sa = p.scale_a ? p.scale_a[m] : 1.0f;
-        float out = __fmul_rn(__fmul_rn(static_cast<float>(s), sa), p.scale_b[n]);
-        if (p.bias) out = __fadd_rn(out, p.bias[n]);
-        p.C[static_cast<uint64_t>(m) * p.ldc + n] = dev::epilogue(out, p.epilogue);
-    }
+    epi.template store<W, T, M>(p, red, nt0, NT, tid);
 }
 
-// Launch shape (measured on MI355X with the weights streamed from HBM): four
-// waves with eight blocks in flight each for one or two rows; eight waves
-// when strips are few (the grid is one workgroup per strip); for three or
-// four rows eight waves with four blocks each.  From five rows up the matrix
-// core does the math (M=8: N=4096 7.5 -> 6.9 us, 11008 13.2 -> 11.8 us,
-// 32000 27.0 -> 24.3 us; at three and four rows the v_dot4 kernel is as fast
-// or faster), with four strips per workgroup over at least 1024 strips so one
-// staged activation chunk serves four weight streams (two strips per
-// workgroup at 512-1023 strips measured slower: fewer workgroups than CUs).
-// MFMA variants by strip count: <4,4,4> from 1024 strips, <4,8,1> from 512,
-// <8,8,1> below.
+// Launch shapes (swept on MI355X at K = 4096 with the weights streamed from
+// HBM; waves W x blocks in flight U per wave).  Fewer registers per wave buy
+// more resident waves, which matters more than deeper per-wave prefetch:
+//   * v_dot4 kernel (M <= 4), from 512 strips: M = 1, 3, 4 eight waves with two
+//     blocks (M=1 N=32000 21.7 -> 20.4 us, N=11008 9.7 -> 8.5 us; M=4 N=32000
+//     25.5 -> 22.2 us), M = 2 four waves with two; below 512 strips (one
+//     workgroup per strip, at most 256 workgroups) sixteen waves with four
+//     (M = 1) or two blocks (M=1 N=4096 5.2 -> 4.8 us).
+//   * matrix-core kernel (M >= 5; at three and four rows v_dot4 is as fast):
+//     from 1024 strips four strips per workgroup so one staged activation
+//     chunk serves four weight streams, <W,U,T> = <4,4,4>; 512-1023 strips
+//     <8,4,1> (M=8 N=11008 11.9 -> 11.1 us); below, <16,2,1> (M=8 N=4096
+//     6.9 -> 6.2 us).
 int mfma_variant(uint32_t NT) { return NT >= 1024 ? 0 : NT >= 512 ? 1 : 2; }
 uint32_t mfma_grid(uint32_t NT) { return mfma_variant(NT) == 0 ? (NT + 3) / 4 : NT; }
 
@@ -323,9 +347,9 @@ void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t
     if (variant == 0)
         gemv_i8_mfma<M, 4, 4, 4><<<grid, 256, lds, s>>>(ps, grid0, chunk_k);
     else if (variant == 1)
-        gemv_i8_mfma<M, 4, 8, 1><<<grid, 256, lds, s>>>(ps, grid0, chunk_k);
+        gemv_i8_mfma<M, 8, 4, 1><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
     else
-        gemv_i8_mfma<M, 8, 8, 1><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
+        gemv_i8_mfma<M, 16, 2, 1><<<grid, 1024, lds, s>>>(ps, grid0, chunk_k);
 }
 
 template <int M>
@@ -338,13 +362,18 @@ void launch_m(hipStream_t s, const I8Gemm &p)
         I8GemmPair ps;
         ps.p[0] = ps.p[1] = p;
         launch_mfma_pair<M>(s, ps, mfma_variant(NT), mfma_grid(NT), 0, chunk_k);
-    } else if constexpr (M >= 3) {
-        gemv_i8_kernel<M, 8, 4, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+    } else if constexpr (M == 2) {
+        if (NT >= 512)
+            gemv_i8_kernel<M, 4, 2, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
+        else
+            gemv_i8_kernel<M, 16, 2, 1><<<dim3(NT), 1024, lds, s>>>(p, chunk_k);
     } else {
         if (NT >= 512)
-            gemv_i8_kernel<M, 4, 8, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
+            gemv_i8_kernel<M, 8, 2, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+        else if constexpr (M == 1)
+            gemv_i8_kernel<M, 16, 4, 1><<<dim3(NT), 1024, lds, s>>>(p, chunk_k);
         else
-            gemv_i8_kernel<M, 8, 8, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+            gemv_i8_kernel<M, 16, 2, 1><<<dim3(NT), 1024, lds, s>>>(p, chunk_k);
     }
 }
 

@@ -246,3 +246,22 @@ def test_forced_f32_depth_large_grid(gpu):
     finally:
         gpu.lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n)
     assert oracle.rel_error(got, oracle.matmul_f32_blas(A, B)) <= 1e-4
+
+
+@pytest.mark.parametrize("b,h,sq,sk,d,causal,use_mask", [
+    (1, 2, 5, 40, 320, 1, False), (2, 1, 3, 150, 1024, 0, True), (1, 2, 70, 70, 264, 1, True),
+    (1, 70000, 1, 5, 8, 1, False), (2, 40000, 2, 3, 32, 0, True)])
+def test_attention_wide_heads_and_many_heads(gpu, b, h, sq, sk, d, causal, use_mask):
+    """head_dim above 256 and more than 65535 (batch, head) pairs: the
+    row-wise kernel (the reference takes any head_dim and any count)."""
+    import gpu_ops as g
+    Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
+    K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+    V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+    mask = RNG.standard_normal((b, h, sq, sk)).astype(np.float32) if use_mask else None
+    if use_mask:
+        mask[..., 0] = -np.inf
+    got = g.attention(gpu, Q, K, V, mask, causal)
+    want = oracle.attention(Q, K, V, mask, causal)
+    assert np.isfinite(got).all()
+    assert oracle.rel_error(got, want) <= 2e-3
