@@ -87,6 +87,10 @@ extern "C" {
 #define VNPU_CONFIG_EAGER_SYNC      (1u << 4)
 #define VNPU_CONFIG_LOW_LATENCY     (1u << 5)
 #define VNPU_CONFIG_HIGH_THROUGHPUT (1u << 6)
+/* MI355X extension (additive; no reference counterpart): ATTENTION_F32 in the
+ * reference CPU build's order of roundings, bit for bit (slower for prefill).
+ * The environment variable VNPU_REFERENCE_ORDER=1 sets it for every device. */
+#define VNPU_CONFIG_REFERENCE_ORDER (1u << 7)
 
 /* Command flags: reference include/vnpu.h:95-100.  They are OR-ed over a
  * submitted batch, as in the reference (src/core/runtime.cpp:1345-1347). */

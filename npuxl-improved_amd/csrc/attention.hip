@@ -883,21 +883,46 @@ void decode_launch(int qn, int v4, dim3 grid, hipStream_t s, const Attn &a, uint
 }
 
 // ---------------------------------------------------------------------------
-// Row-wise kernel for the shapes the tiled kernels do not take: head_dim above
-// 256 or more than 65535 (batch, head) pairs.  One workgroup per query row
-// (a 1-D grid, so any number of rows), 64-key blocks with the reference's
-// online softmax (a block whose max is not finite is skipped), scores by wave
-// dot products over the whole head dimension, and the running output kept in
-// the output row itself (no register or LDS bound on head_dim).  Every thread
-// owns the same output elements throughout, so the row needs no barrier
-// between its read-modify-write steps.
+// Reference-order attention: the reference's attention_range
+// (llm.cpp:442-546) rounding for rounding, so the output is its output bit
+// for bit.  Per query row, keys in 64-key blocks from key 0:
+//   * s = dot(q, k) * scale (+ mask), dot in dot_avx2's order (eight FMA
+//     chains over the 8-wide steps, hsum256, then the tail unfused);
+//   * block max m_b; a block whose max is not finite is skipped; new_m =
+//     max(m, m_b), alpha = fast_expf(m - new_m), p_j = fast_expf(s_j - new_m)
+//     with the reference's unfused scalar polynomial (dev::fast_expf_unfused);
+//   * sum_p adds the block's p_j in key order, l = l * alpha + sum_p;
+//   * acc = acc * alpha, then acc = fma(v_j, p_j, acc) in key order (p_j != 0);
+//   * out = acc * (1 / l), 0 when l == 0.
+// The sums over keys are sequential chains: lanes split the score work and
+// the head dimension, never a chain.
 // ---------------------------------------------------------------------------
-constexpr int RW_KEYS = 64;
+constexpr int RK = 64;   // keys per block (the reference's BK)
 
+// dot_avx2 over d in [0, D): chains c = 0..7 over d = 8i + c, hsum256, tail.
+__device__ __forceinline__ float dot_ref(const float *q, const float *k, uint32_t D)
+{
+#pragma clang fp contract(off)
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint32_t D8 = D & ~7u;
+    for (uint32_t i = 0; i < D8; i += 8) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = fmaf(q[i + c], k[i + c], acc[c]);
+    }
+    float sum = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+    for (uint32_t i = D8; i < D; ++i) sum = sum + q[i] * k[i];
+    return sum;
+}
+
+// Any head_dim and any number of (batch, head) pairs: one workgroup per
+// query row (a 1-D grid), the scores of a block by the lanes of wave 0 (one
+// key each), the running output in the output row itself (no bound on
+// head_dim; every thread owns the same elements throughout).
 __global__ __launch_bounds__(kThreads) void attn_rowwise_kernel(Attn a, uint64_t row0)
 {
-    __shared__ float sc[RW_KEYS];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma clang fp contract(off)
+    __shared__ float pw[RK];
+    const int tid = threadIdx.x;
     const uint64_t row = row0 + blockIdx.x;
     const uint32_t sq = a.seq_q, sk = a.seq_k, D = a.head_dim;
     const uint64_t bh = row / sq;
@@ -911,46 +936,244 @@ __global__ __launch_bounds__(kThreads) void attn_rowwise_kernel(Attn a, uint64_t
     float m = -__builtin_inff(), l = 0.0f;
     uint32_t kend = sk;
     if (a.causal) kend = min(sk, qi + off + 1);
-    for (uint32_t k0 = 0; k0 < kend; k0 += RW_KEYS) {
-        const uint32_t kc = min(static_cast<uint32_t>(RW_KEYS), kend - k0);
-        __syncthreads();   // the previous block's scores are consumed
-        for (uint32_t j = wave; j < kc; j += 4) {
-            const float *kr = Kh + static_cast<uint64_t>(k0 + j) * D;
-            float dot = 0.0f;
-            for (uint32_t d = lane; d < D; d += 64) dot = fmaf(q[d], kr[d], dot);
-            dot = dev::wave_sum(dot);
-            if (lane == 0) {
-                float s = dot * a.scale;
-                if (a.mask) s += a.mask[row * sk + k0 + j];
-                sc[j] = s;
-            }
+    for (uint32_t k0 = 0; k0 < kend; k0 += RK) {
+        const uint32_t kc = min(static_cast<uint32_t>(RK), kend - k0);
+        __syncthreads();   // the previous block's weights are consumed
+        if (tid < static_cast<int>(kc)) {
+            float sc = dot_ref(q, Kh + static_cast<uint64_t>(k0 + tid) * D, D) * a.scale;
+            if (a.mask) sc = sc + a.mask[row * sk + k0 + tid];
+            pw[tid] = sc;
         }
         __syncthreads();
         float bmax = -__builtin_inff();
-        for (uint32_t j = 0; j < kc; ++j) bmax = fmaxf(bmax, sc[j]);
+        for (uint32_t j = 0; j < kc; ++j) bmax = bmax < pw[j] ? pw[j] : bmax;
         if (!isfinite(bmax)) continue;   // uniform over the workgroup
-        const float nm = fmaxf(m, bmax);
-        const float alpha = dev::fast_expf(m - nm);
+        const float nm = m < bmax ? bmax : m;
+        const float alpha = dev::fast_expf_unfused(m - nm);
+        __syncthreads();   // every thread has read the scores
+        if (tid < static_cast<int>(kc)) pw[tid] = dev::fast_expf_unfused(pw[tid] - nm);
+        __syncthreads();
         float psum = 0.0f;
-        for (uint32_t j = 0; j < kc; ++j) psum += dev::fast_expf(sc[j] - nm);
+        for (uint32_t j = 0; j < kc; ++j) psum = psum + pw[j];
         l = l * alpha + psum;
         for (uint32_t d = tid; d < D; d += kThreads) {
             float acc = o[d] * alpha;
             for (uint32_t j = 0; j < kc; ++j) {
-                const float p = dev::fast_expf(sc[j] - nm);
-                if (p != 0.0f) acc = fmaf(p, Vh[static_cast<uint64_t>(k0 + j) * D + d], acc);
+                const float p = pw[j];
+                if (p != 0.0f) acc = fmaf(Vh[static_cast<uint64_t>(k0 + j) * D + d], p, acc);
             }
             o[d] = acc;
         }
         m = nm;
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    for (uint32_t d = tid; d < D; d += kThreads) o[d] *= inv;
+    for (uint32_t d = tid; d < D; d += kThreads) o[d] = o[d] * inv;
+}
+
+// The same arithmetic tiled for head_dim 64 or 128 and at most 65535
+// (batch, head) pairs: one workgroup of 256 threads per (batch, head) and QT
+// query rows.  Per 64-key block the K (row pitch D + 1 floats: lane j reads
+// key j's element i with no bank conflict) and V tiles are staged in LDS,
+// the next block's tiles already in flight in registers.
+//   scores: thread (key j = tid % 64, query group tid / 64) runs the eight
+//           dot chains for its QPT queries, each K element read once;
+//   softmax: wave w owns queries w, w + 4, ...: block max and the weights by
+//           lane j, the weight sum by lane 0 in key order;
+//   output: thread (d slot tid % (D / DPT), query group) keeps QPT x DPT
+//           accumulators and walks the block's keys in order.
+// QT = 1 (decode: one workgroup per query row) or 16 (prefill).
+template <int QT, int D>
+struct ExactCfg {
+    static constexpr int P = D + 1;                 // K row pitch in LDS (floats)
+    static constexpr int QG = QT == 1 ? 1 : 4;      // query groups (waves) in the score/output phases
+    static constexpr int QPT = QT / QG;             // queries per thread
+    static constexpr int DS = QT == 1 ? D : 64;     // output d slots
+    static constexpr int DPT = D / DS;              // d per thread
+    static constexpr int kFloats = RK * P + RK * D + QT * D + QT * RK + 4 * QT;
+    static constexpr size_t kLds = static_cast<size_t>(kFloats) * sizeof(float);
+    static constexpr int kPre = RK * D / 4 / kThreads;   // float4s of K (and of V) per thread per block
+};
+
+template <int QT, int D>
+__global__ __launch_bounds__(kThreads) void attn_exact_kernel(Attn a)
+{
+#pragma clang fp contract(off)
+    using G = ExactCfg<QT, D>;
+    extern __shared__ float sm[];
+    float *Ks = sm;                          // [64][P]
+    float *Vs = Ks + RK * G::P;              // [64][D]
+    float *Qs = Vs + RK * D;                 // [QT][D]
+    float *W = Qs + QT * D;                  // [QT][64] scores, then weights
+    float *Ml = W + QT * RK;                 // [QT] running max
+    float *Ll = Ml + QT;                     // [QT] running sum
+    float *Al = Ll + QT;                     // [QT] this block's alpha
+    float *Sk = Al + QT;                     // [QT] 1 = block skipped for the row
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t bh = blockIdx.y;
+    const uint32_t sq = a.seq_q, sk = a.seq_k;
+    const uint32_t off = sk > sq ? sk - sq : 0;
+    const uint32_t q0 = blockIdx.x * QT;
+    const uint32_t nq = min(static_cast<uint32_t>(QT), sq - q0);
+    const float *Kh = a.K + bh * sk * D;
+    const float *Vh = a.V + bh * sk * D;
+    const float *Mh = a.mask ? a.mask + bh * sq * sk : nullptr;
+
+    for (int i = tid; i < QT * D; i += kThreads) {
+        const uint32_t r = i / D;
+        Qs[i] = r < nq ? a.Q[(bh * sq + q0 + r) * D + (i % D)] : 0.0f;
+    }
+    if (tid < QT) {
+        Ml[tid] = -__builtin_inff();
+        Ll[tid] = 0.0f;
+    }
+    uint32_t kend = sk;
+    if (a.causal) kend = min(sk, q0 + nq - 1 + off + 1);
+    const uint32_t nblk = (kend + RK - 1) / RK;
+
+    // Staging of block b's K and V: float4 f = tid + kThreads * u of the
+    // block's 64 x D floats (rows past kend read as zero).
+    float4 pk[G::kPre], pv[G::kPre];
+    auto fetch = [&](uint32_t b) {
+#pragma unroll
+        for (int u = 0; u < G::kPre; ++u) {
+            const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);
+            const uint32_t key = b * RK + j;
+            const bool in = key < kend;
+            const uint64_t at = static_cast<uint64_t>(in ? key : 0) * (D / 4) + c4;
+            pk[u] = in ? reinterpret_cast<const float4 *>(Kh)[at] : make_float4(0.f, 0.f, 0.f, 0.f);
+            pv[u] = in ? reinterpret_cast<const float4 *>(Vh)[at] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int u = 0; u < G::kPre; ++u) {
+            const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);
+            float *kr = Ks + j * G::P + 4 * c4;
+            kr[0] = pk[u].x;
+            kr[1] = pk[u].y;
+            kr[2] = pk[u].z;
+            kr[3] = pk[u].w;
+            reinterpret_cast<float4 *>(Vs)[f] = pv[u];
+        }
+    };
+
+    float acc[G::QPT][G::DPT];
+#pragma unroll
+    for (int i = 0; i < G::QPT; ++i)
+#pragma unroll
+        for (int e = 0; e < G::DPT; ++e) acc[i][e] = 0.0f;
+
+    if (nblk) fetch(0);
+    for (uint32_t b = 0; b < nblk; ++b) {
+        const uint32_t k0 = b * RK, kc = min(static_cast<uint32_t>(RK), kend - k0);
+        __syncthreads();   // the previous block's tiles and weights are consumed
+        stage();
+        __syncthreads();
+        if (b + 1 < nblk) fetch(b + 1);
+
+        // Scores.
+        if (QT > 1 || wave == 0) {
+            const int j = lane, g = QT > 1 ? wave : 0;
+            float ch[G::QPT][8];
+#pragma unroll
+            for (int i = 0; i < G::QPT; ++i)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) ch[i][c] = 0.0f;
+            const float *kr = Ks + j * G::P;
+            for (int d = 0; d < D; d += 8) {
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const float kv = kr[d + c];
+#pragma unroll
+                    for (int i = 0; i < G::QPT; ++i) ch[i][c] = fmaf(Qs[(g * G::QPT + i) * D + d + c], kv, ch[i][c]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < G::QPT; ++i) {
+                const uint32_t r = g * G::QPT + i, qi = q0 + r;
+                float sc = -__builtin_inff();
+                const uint32_t key = k0 + j;
+                if (j < static_cast<int>(kc) && r < nq && !(a.causal && key > qi + off)) {
+                    const float dot = ((ch[i][0] + ch[i][4]) + (ch[i][1] + ch[i][5])) +
+                                      ((ch[i][2] + ch[i][6]) + (ch[i][3] + ch[i][7]));
+                    sc = dot * a.scale;
+                    if (Mh) sc = sc + Mh[static_cast<uint64_t>(qi) * sk + key];
+                }
+                W[r * RK + j] = sc;
+            }
+        }
+        __syncthreads();
+
+        // Softmax state per row: wave w takes rows w, w + 4, ...
+        for (int r = wave; r < static_cast<int>(nq); r += 4) {
+            const float sc = W[r * RK + lane];
+            const float bmax = dev::wave_max(sc);
+            if (!isfinite(bmax)) {   // uniform over the wave
+                if (lane == 0) Sk[r] = 1.0f;
+                continue;
+            }
+            const float m = Ml[r];
+            const float nm = m < bmax ? bmax : m;
+            W[r * RK + lane] = dev::fast_expf_unfused(sc - nm);   // -inf scores give 0
+            if (lane == 0) {
+                const float alpha = dev::fast_expf_unfused(m - nm);
+                float psum = 0.0f;
+                for (uint32_t j = 0; j < kc; ++j) psum = psum + W[r * RK + j];
+                Ll[r] = Ll[r] * alpha + psum;
+                Ml[r] = nm;
+                Al[r] = alpha;
+                Sk[r] = 0.0f;
+            }
+        }
+        __syncthreads();
+
+        // Output accumulators.
+        if (QT > 1 || tid < D) {
+            const int ds = QT == 1 ? tid : lane, g = QT > 1 ? wave : 0;
+#pragma unroll
+            for (int i = 0; i < G::QPT; ++i) {
+                const int r = g * G::QPT + i;
+                if (r >= static_cast<int>(nq) || Sk[r] != 0.0f) continue;
+                const float alpha = Al[r];
+#pragma unroll
+                for (int e = 0; e < G::DPT; ++e) acc[i][e] = acc[i][e] * alpha;
+                for (uint32_t j = 0; j < kc; ++j) {
+                    const float p = W[r * RK + j];
+                    if (p == 0.0f) continue;
+#pragma unroll
+                    for (int e = 0; e < G::DPT; ++e)
+                        acc[i][e] = fmaf(Vs[j * D + ds * G::DPT + e], p, acc[i][e]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (QT > 1 || tid < D) {
+        const int ds = QT == 1 ? tid : lane, g = QT > 1 ? wave : 0;
+#pragma unroll
+        for (int i = 0; i < G::QPT; ++i) {
+            const int r = g * G::QPT + i;
+            if (r >= static_cast<int>(nq)) continue;
+            const float l = Ll[r];
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            float *o = a.O + (bh * sq + q0 + r) * D + ds * G::DPT;
+#pragma unroll
+            for (int e = 0; e < G::DPT; ++e) o[e] = acc[i][e] * inv;
+        }
+    }
 }
 
 bool use_rowwise(const Attn &a)
 {
-    return a.head_dim > 256 || static_cast<uint64_t>(a.batch) * a.heads > 65535u;
+    return a.head_dim > 256 || static_cast<uint64_t>(a.batch) * a.heads > 65535u ||
+           (a.exact && a.head_dim != 64 && a.head_dim != 128);
+}
+
+// Reference-order tiled kernel (exact mode, head_dim 64 or 128).
+bool use_exact_tiled(const Attn &a)
+{
+    return a.exact && !use_rowwise(a);
 }
 
 bool use_decode(const Attn &a)
@@ -1027,7 +1250,7 @@ float *attention_scratch(int hip_device)
 
 size_t attention_ws_bytes(const Attn &a)
 {
-    if (use_rowwise(a)) return 0;
+    if (use_rowwise(a) || use_exact_tiled(a)) return 0;
     uint32_t qb, splits, kps;
     plan(a, qb, splits, kps);
     if (use_prefill(a)) {
@@ -1041,8 +1264,27 @@ size_t attention_ws_bytes(const Attn &a)
     return static_cast<size_t>(splits) * rows * (a.head_dim + 2) * sizeof(float);
 }
 
+template <int QT, int D>
+void launch_exact(hipStream_t s, const Attn &a)
+{
+    using G = ExactCfg<QT, D>;
+    static std::atomic<bool> lds_optin{false};
+    if (!lds_optin && G::kLds > 65536)
+        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_exact_kernel<QT, D>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(G::kLds)) == hipSuccess;
+    const dim3 grid((a.seq_q + QT - 1) / QT, a.batch * a.heads);
+    attn_exact_kernel<QT, D><<<grid, kThreads, G::kLds, s>>>(a);
+}
+
 void attention(hipStream_t s, const Attn &a, float *ws)
 {
+    if (use_exact_tiled(a)) {
+        const bool decode = a.seq_q <= 4;
+        if (a.head_dim == 128) decode ? launch_exact<1, 128>(s, a) : launch_exact<16, 128>(s, a);
+        else decode ? launch_exact<1, 64>(s, a) : launch_exact<16, 64>(s, a);
+        return;
+    }
     if (use_rowwise(a)) {
         const uint64_t rows = static_cast<uint64_t>(a.batch) * a.heads * a.seq_q;
         for (uint64_t r0 = 0; r0 < rows; r0 += 0x7fffffffull) {

@@ -50,6 +50,63 @@ __device__ __forceinline__ float add_rn(float a, float b)
     return a + b;
 }
 
+// fast_expf as the reference's baseline x86-64 build evaluates it in code
+// without an AVX2 target (its attention_range, llm.cpp:442-546): the same
+// steps with every multiply and add of the polynomial rounded separately.
+__device__ __forceinline__ float fast_expf_unfused(float x)
+{
+#pragma clang fp contract(off)
+    if (x < -80.0f) return 0.0f;
+    if (x > 80.0f) return __builtin_inff();
+    const float z = x * 1.4426950408889634f;
+    const float zi = floorf(z);
+    const float f = z - zi;
+    const float p = 1.0f + f * (0.6931471805599453f +
+                    f * (0.2402265069591007f +
+                    f * (0.05550410866482158f +
+                    f * (0.009618129107628477f +
+                    f * 0.0013333558146428443f))));
+    return ldexpf(p, static_cast<int>(zi));
+}
+
+// exp256_ps (reference src/kernels/llm.cpp:31-56), the vector exp of the
+// reference's AVX2 SWIGLU / GELU / SOFTMAX: x clamped to [-80, 80] (a NaN
+// becomes 80, as min_ps/max_ps give), then fast_expf's steps.
+__device__ __forceinline__ float exp_avx2(float x)
+{
+#pragma clang fp contract(off)
+    x = fmaxf(fminf(x, 80.0f), -80.0f);
+    const float z = x * 1.4426950408889634f;
+    const float zi = floorf(z);
+    const float f = z - zi;
+    float p = fmaf(0.0013333558146428443f, f, 0.009618129107628477f);
+    p = fmaf(p, f, 0.05550410866482158f);
+    p = fmaf(p, f, 0.2402265069591007f);
+    p = fmaf(p, f, 0.6931471805599453f);
+    p = fmaf(p, f, 1.0f);
+    return ldexpf(p, static_cast<int>(zi));
+}
+
+// swiglu_avx2_range (llm.cpp:289-306): s = g / (1 + exp256(-g)), (s*u)*alpha.
+__device__ __forceinline__ float swiglu_avx2(float g, float u, float alpha)
+{
+#pragma clang fp contract(off)
+    const float s = g / (1.0f + exp_avx2(-g));
+    return (s * u) * alpha;
+}
+
+// gelu_avx2_range (llm.cpp:308-330): inner = k0 * fma(k1, x^3, x),
+// t = 2 / (1 + exp256(-2 inner)) - 1, y = (0.5 x)(1 + t).
+__device__ __forceinline__ float gelu_avx2(float x)
+{
+#pragma clang fp contract(off)
+    const float x3 = (x * x) * x;
+    const float inner = 0.7978845608028654f * fmaf(0.035677408136300125f, x3, x);
+    const float e = exp_avx2(-2.0f * inner);
+    const float t = 2.0f / (1.0f + e) - 1.0f;
+    return (0.5f * x) * (1.0f + t);
+}
+
 // reference src/internal.h:112
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + fast_expf(-x)); }
 

@@ -257,6 +257,68 @@ const float *rope_table(vnpu_device_t *dev, float theta, uint32_t dim)
     return d;
 }
 
+// RoPE cos/sin table: rows of (cos, sin) of (p * scaling) * inv[j] for the
+// positions p = 0 .. rows-1, computed on the host with the C library's
+// cosf / sinf - the very calls of the reference's rotate_vector
+// (llm.cpp:195-211) - so the rotation is the reference's bit for bit.  One
+// table per (device, theta, dim, scaling), grown to a power of two of
+// positions as calls need more (at most kRopeMaxRows); a replaced table is
+// kept until the device goes away, since kernels enqueued earlier may still
+// read it.
+constexpr uint32_t kRopeMaxRows = 65536;
+
+struct RopeCs {
+    float2 *table = nullptr;
+    uint32_t rows = 0;
+    std::vector<float2 *> retired;
+};
+struct RopeCsCache {
+    std::mutex mutex;
+    std::map<std::tuple<vnpu_device_t *, uint32_t, uint32_t, uint32_t>, RopeCs> tables;
+};
+RopeCsCache &rope_cs_cache()
+{
+    static RopeCsCache *c = new RopeCsCache();
+    return *c;
+}
+
+const float2 *rope_cos_sin_table(vnpu_device_t *dev, float theta, uint32_t dim, float scaling, uint32_t need,
+                                 uint32_t &rows)
+{
+    uint32_t tb, sb;
+    std::memcpy(&tb, &theta, 4);
+    std::memcpy(&sb, &scaling, 4);
+    auto &c = rope_cs_cache();
+    std::lock_guard<std::mutex> lock(c.mutex);
+    RopeCs &t = c.tables[std::make_tuple(dev, tb, dim, sb)];
+    need = std::min(need, kRopeMaxRows);
+    if (need > t.rows) {
+        uint32_t n = 64;
+        while (n < need) n *= 2;
+        n = std::min(n, kRopeMaxRows);
+        const uint32_t half = dim / 2;
+        std::vector<float> inv(half);
+        for (uint32_t j = 0; j < half; ++j)
+            inv[j] = 1.0f / std::pow(theta, 2.0f * static_cast<float>(j) / static_cast<float>(dim));
+        std::vector<float2> host(static_cast<size_t>(n) * half);
+        for (uint32_t p = 0; p < n; ++p) {
+            const float pos = static_cast<float>(static_cast<int32_t>(p)) * scaling;
+            for (uint32_t j = 0; j < half; ++j) {
+                const float angle = pos * inv[j];
+                host[static_cast<size_t>(p) * half + j] = make_float2(std::cos(angle), std::sin(angle));
+            }
+        }
+        float2 *d = nullptr;
+        VNPU_HIP(hipMalloc(&d, host.size() * sizeof(float2)));
+        VNPU_HIP(hipMemcpy(d, host.data(), host.size() * sizeof(float2), hipMemcpyHostToDevice));
+        if (t.table) t.retired.push_back(t.table);
+        t.table = d;
+        t.rows = n;
+    }
+    rows = t.rows;
+    return t.table;
+}
+
 // ---------------------------------------------------------------------------
 
 void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32_args_t &in,
@@ -704,12 +766,25 @@ void exec_rope(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_rope_f32_args_t 
     const uint64_t qn = bh * a.q_seq * a.head_dim, kn = bh * a.k_seq * a.head_dim;
     const uint32_t seq = std::max(a.q_seq, a.k_seq);
     const float *inv = rope_table(dev, theta, a.head_dim);
+    // Positions the table must cover: known on the host for offset-based
+    // positions and host position arrays; a device position array uses the
+    // rows the table already has (other positions compute cos/sin on the GPU).
+    uint64_t need = 0;
+    if (!a.positions) {
+        need = static_cast<uint64_t>(a.position_offset) + seq;
+    } else if (!is_device_pointer(a.positions)) {
+        for (uint32_t t = 0; t < seq; ++t)
+            if (a.positions[t] >= 0) need = std::max<uint64_t>(need, static_cast<uint64_t>(a.positions[t]) + 1);
+    }
+    uint32_t cs_rows = 0;
+    const float2 *cs = rope_cos_sin_table(dev, theta, a.head_dim, scaling,
+                                          static_cast<uint32_t>(std::min<uint64_t>(need, kRopeMaxRows)), cs_rows);
     Stager sg(s->hip);
     float *Q = a.Q && a.q_seq ? sg.inout(a.Q, qn * 4) : nullptr;
     float *K = a.K && a.k_seq ? sg.inout(a.K, kn * 4) : nullptr;
     const int32_t *pos = sg.in(a.positions, a.positions ? static_cast<size_t>(seq) * 4 : 0);
     k::rope(s->hip, Q, K, pos, a.batch, a.heads, Q ? a.q_seq : 0, K ? a.k_seq : 0, a.head_dim,
-            a.position_offset, a.interleaved, scaling, inv);
+            a.position_offset, a.interleaved, scaling, inv, cs, cs_rows);
     VNPU_HIP(hipGetLastError());
     sg.finish();
     st.bytes_read += (qn + kn) * 4;
@@ -786,6 +861,7 @@ void account_attention(const vnpu_attention_f32_args_t &a, ExecStats &st)
 void exec_attention(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecStats &st)
 {
     k::Attn p = attention_params(a);
+    p.exact = s->device->reference_order;
     const uint64_t bh = static_cast<uint64_t>(a.batch) * a.heads;
     const uint64_t qn = bh * a.seq_q * a.head_dim, kn = bh * a.seq_k * a.head_dim;
     const uint64_t mn = a.mask ? bh * a.seq_q * a.seq_k : 0;
@@ -839,6 +915,7 @@ void exec_memset(vnpu_stream_t *s, const vnpu_memset_args_t &a, ExecStats &st)
 void enqueue_attention_noalloc(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecStats &st)
 {
     k::Attn p = attention_params(a);
+    p.exact = s->device->reference_order;
     // No staging: every tensor must already be device memory.
     require(is_device_pointer(a.Q) && is_device_pointer(a.K) && is_device_pointer(a.V) &&
                 is_device_pointer(a.O) && (!a.mask || is_device_pointer(a.mask)),
@@ -1014,11 +1091,24 @@ void destroy_packed(vnpu_packed_weights_t *w)
 
 void release_device_tables(vnpu_device_t *dev)
 {
-    auto &c = inv_cache();
+    {
+        auto &c = inv_cache();
+        std::lock_guard<std::mutex> lock(c.mutex);
+        for (auto it = c.tables.begin(); it != c.tables.end();) {
+            if (std::get<0>(it->first) == dev) {
+                (void)hipFree(it->second);
+                it = c.tables.erase(it);
+            } else {
+                ++it;
+            }
+        }
+    }
+    auto &c = rope_cs_cache();
     std::lock_guard<std::mutex> lock(c.mutex);
     for (auto it = c.tables.begin(); it != c.tables.end();) {
         if (std::get<0>(it->first) == dev) {
-            (void)hipFree(it->second);
+            (void)hipFree(it->second.table);
+            for (float2 *r : it->second.retired) (void)hipFree(r);
             it = c.tables.erase(it);
         } else {
             ++it;

@@ -110,7 +110,8 @@ void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t co
 // interleaved pairs, computed on the host with the reference's powf expression.
 void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t batch,
           uint32_t heads, uint32_t q_seq, uint32_t k_seq, uint32_t head_dim,
-          uint32_t position_offset, uint32_t interleaved, float scaling, const float *inv_freq);
+          uint32_t position_offset, uint32_t interleaved, float scaling, const float *inv_freq,
+          const float2 *cs, uint32_t cs_rows);
 void swiglu(hipStream_t s, const float *g, const float *u, float *Y, uint64_t n, float alpha);
 void add(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha,
          float beta);
@@ -149,6 +150,7 @@ struct Attn {
     float *O = nullptr;
     uint32_t batch = 0, heads = 0, seq_q = 0, seq_k = 0, head_dim = 0, causal = 0;
     float scale = 1.0f;
+    bool exact = false;   // the reference's order of roundings (bit for bit)
 };
 size_t attention_ws_bytes(const Attn &a);
 void attention(hipStream_t s, const Attn &a, float *ws);

@@ -41,84 +41,128 @@ __device__ __forceinline__ float block_max(float v, float *red)
     return r;
 }
 
-// reference llm.cpp:64-108: inv = 1/sqrt(sum(x^2)/cols + eps); y = x*inv*w
+// RMSNORM in the rounding order of the reference's AVX2 build
+// (rmsnorm_avx2_rows, llm.cpp:80-108), so the result is the reference's bit
+// for bit:
+//   * the sum of squares runs as eight FMA chains, chain c over elements c,
+//     c + 8, c + 16, ... in order; the eight sums combine as
+//     ((s0 + s4) + (s1 + s5)) + ((s2 + s6) + (s3 + s7)) (hsum256), and the
+//     cols % 8 tail elements follow one FMA each;
+//   * inv = 1 / sqrt(sum / cols + eps), correctly rounded;
+//   * y = (x * w) * inv on the 8-wide part, (x * inv) * w on the tail.
+// A chain is one sequential dependency (cols / 8 FMAs), so eight lanes walk
+// the row staged in LDS while the other lanes wait; rows run in parallel
+// across workgroups.  kChainFloats bounds the LDS staging of one pass.
+constexpr uint32_t kChainFloats = 12288;
+
+// Eight chain lanes accumulate row[0 .. n) (n a multiple of 8, staged in LDS)
+// into acc; call with every thread, between barriers.
+__device__ __forceinline__ void chain_sumsq(const float *row, uint32_t n, float &acc)
+{
+    const uint32_t c = threadIdx.x;
+    if (c >= 8) return;
+    uint32_t s = 0;
+    for (; s + 8 <= n / 8; s += 8) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = row[(s + u) * 8 + c];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(x[u], x[u], acc);
+    }
+    for (; s < n / 8; ++s) {
+        const float x = row[s * 8 + c];
+        acc = fmaf(x, x, acc);
+    }
+}
+
+// Combines the chain sums (red8, written by lanes 0..7) and the tail
+// row_tail[0 .. tail) the way hsum256 and the scalar tail do; every thread
+// gets the result.  Call after a barrier that follows the chains' writes.
+__device__ __forceinline__ float chain_total(const float *red8, const float *row_tail, uint32_t tail)
+{
+    float sum = ((red8[0] + red8[4]) + (red8[1] + red8[5])) + ((red8[2] + red8[6]) + (red8[3] + red8[7]));
+    for (uint32_t j = 0; j < tail; ++j) sum = fmaf(row_tail[j], row_tail[j], sum);
+    return sum;
+}
+
+__device__ __forceinline__ float rms_inv(float sum, uint32_t cols, float eps)
+{
+    return 1.0f / sqrtf(sum / static_cast<float>(cols) + eps);
+}
+
+// Element e of a row of `cols`: (x*w)*inv inside the 8-wide part, else
+// (x*inv)*w.
+__device__ __forceinline__ float rms_scale(float x, float w, float inv, uint32_t e, uint32_t cols8)
+{
+    return e < cols8 ? dev::mul_rn(dev::mul_rn(x, w), inv) : dev::mul_rn(dev::mul_rn(x, inv), w);
+}
+
+// Any row length and alignment: the row streams through LDS in passes of
+// kChainFloats for the sum, then is read again for the scaling.
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ X,
                                                            const float *__restrict__ W,
                                                            float *__restrict__ Y, uint32_t cols,
                                                            float eps)
 {
-    __shared__ float red[kThreads / 64];
+    extern __shared__ float row_lds[];   // min(cols, kChainFloats) floats
+    __shared__ float red8[8];
     const uint64_t r = blockIdx.x;
     const float *x = X + r * cols;
     float *y = Y + r * cols;
-    float ss = 0.0f;
-    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) ss = fmaf(x[j], x[j], ss);
-    ss = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
-    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) y[j] = x[j] * inv * (W ? W[j] : 1.0f);
-}
-
-__global__ __launch_bounds__(kThreads) void rmsnorm_vec_kernel(const float *__restrict__ X,
-                                                               const float *__restrict__ W,
-                                                               float *__restrict__ Y,
-                                                               uint32_t cols, float eps)
-{
-    __shared__ float red[kThreads / 64];
-    const uint64_t r = blockIdx.x;
-    const float4 *x = reinterpret_cast<const float4 *>(X + r * cols);
-    float4 *y = reinterpret_cast<float4 *>(Y + r * cols);
-    const float4 *w = reinterpret_cast<const float4 *>(W);
-    const uint32_t n4 = cols >> 2;
-    float ss = 0.0f;
-    for (uint32_t j = threadIdx.x; j < n4; j += kThreads) {
-        const float4 v = x[j];
-        ss = fmaf(v.x, v.x, ss);
-        ss = fmaf(v.y, v.y, ss);
-        ss = fmaf(v.z, v.z, ss);
-        ss = fmaf(v.w, v.w, ss);
+    const uint32_t cols8 = cols & ~7u;
+    float acc = 0.0f;
+    for (uint32_t c0 = 0; c0 < cols8; c0 += kChainFloats) {
+        const uint32_t n = min(kChainFloats, cols8 - c0);
+        __syncthreads();
+        for (uint32_t j = threadIdx.x; j < n; j += kThreads) row_lds[j] = x[c0 + j];
+        __syncthreads();
+        chain_sumsq(row_lds, n, acc);
     }
-    ss = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
-    for (uint32_t j = threadIdx.x; j < n4; j += kThreads) {
-        const float4 v = x[j];
-        const float4 g = W ? w[j] : make_float4(1.f, 1.f, 1.f, 1.f);
-        y[j] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
-    }
+    __syncthreads();
+    if (threadIdx.x < 8) red8[threadIdx.x] = acc;
+    __syncthreads();
+    const float inv = rms_inv(chain_total(red8, x + cols8, cols - cols8), cols, eps);
+    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) y[j] = rms_scale(x[j], W ? W[j] : 1.0f, inv, j, cols8);
 }
 
 // Rows of up to VPT*1024 floats, 16-byte aligned: the row stays in registers
-// between the sum of squares and the scaling (one HBM read instead of two).
+// between the sum of squares and the scaling (one HBM read instead of two)
+// and is staged once in LDS for the chain lanes.
 template <int VPT>
 __global__ __launch_bounds__(kThreads) void rmsnorm_reg_kernel(const float *__restrict__ X,
                                                                const float *__restrict__ W,
                                                                float *__restrict__ Y, uint32_t cols,
                                                                float eps)
 {
-    __shared__ float red[kThreads / 64];
+    extern __shared__ float4 row4[];   // cols floats
+    __shared__ float red8[8];
     const uint64_t r = blockIdx.x;
     const float4 *x = reinterpret_cast<const float4 *>(X + r * cols);
     float4 *y = reinterpret_cast<float4 *>(Y + r * cols);
     const float4 *w = reinterpret_cast<const float4 *>(W);
-    const uint32_t n4 = cols >> 2;
+    const uint32_t n4 = cols >> 2, cols8 = cols & ~7u;
     float4 v[VPT];
-    float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * kThreads;
         v[i] = j < n4 ? x[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-        ss = fmaf(v[i].x, v[i].x, ss);
-        ss = fmaf(v[i].y, v[i].y, ss);
-        ss = fmaf(v[i].z, v[i].z, ss);
-        ss = fmaf(v[i].w, v[i].w, ss);
+        if (j < n4) row4[j] = v[i];
     }
-    ss = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    __syncthreads();
+    const float *row = reinterpret_cast<const float *>(row4);
+    float acc = 0.0f;
+    chain_sumsq(row, cols8, acc);
+    if (threadIdx.x < 8) red8[threadIdx.x] = acc;
+    __syncthreads();
+    const float inv = rms_inv(chain_total(red8, row + cols8, cols - cols8), cols, eps);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * kThreads;
         if (j >= n4) continue;
         const float4 g = W ? w[j] : make_float4(1.f, 1.f, 1.f, 1.f);
-        y[j] = make_float4(v[i].x * inv * g.x, v[i].y * inv * g.y, v[i].z * inv * g.z, v[i].w * inv * g.w);
+        const uint32_t e = 4 * j;
+        y[j] = make_float4(rms_scale(v[i].x, g.x, inv, e, cols8), rms_scale(v[i].y, g.y, inv, e + 1, cols8),
+                           rms_scale(v[i].z, g.z, inv, e + 2, cols8), rms_scale(v[i].w, g.w, inv, e + 3, cols8));
     }
 }
 
@@ -207,13 +251,43 @@ __global__ __launch_bounds__(kThreads) void softmax_chunk_norm(const float *__re
 }
 
 // reference llm.cpp:188-217, 576-602: one thread per rotated pair.
+// cos and sin of pair j at position p: from the host table (the reference's
+// libm cosf/sinf of (p * scaling) * inv[j], llm.cpp:195-211) where it covers
+// p, else computed here (positions the table does not cover: a device-side
+// position array beyond the positions seen so far, or a negative position).
+__device__ __forceinline__ void rope_cos_sin(int32_t p, uint32_t j, uint32_t half, float scaling,
+                                             const float *inv_freq, const float2 *cs, uint32_t cs_rows,
+                                             float &c, float &s)
+{
+    if (cs && p >= 0 && static_cast<uint32_t>(p) < cs_rows) {
+        const float2 v = cs[static_cast<uint64_t>(p) * half + j];
+        c = v.x;
+        s = v.y;
+        return;
+    }
+    const float angle = dev::mul_rn(dev::mul_rn(static_cast<float>(p), scaling), inv_freq[j]);
+    c = cosf(angle);
+    s = sinf(angle);
+}
+
+// rotate_vector's pair update (llm.cpp:202-213): products and the
+// difference / sum round separately.
+__device__ __forceinline__ void rotate_pair(float *x, uint32_t i0, uint32_t i1, float c, float s)
+{
+#pragma clang fp contract(off)
+    const float x0 = x[i0], x1 = x[i1];
+    x[i0] = x0 * c - x1 * s;
+    x[i1] = x0 * s + x1 * c;
+}
+
 __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ Q, float *__restrict__ K,
                                                         const int32_t *__restrict__ positions,
                                                         uint64_t bh_count, uint32_t q_seq,
                                                         uint32_t k_seq, uint32_t seq,
                                                         uint32_t head_dim, uint32_t offset,
                                                         uint32_t interleaved, float scaling,
-                                                        const float *__restrict__ inv_freq)
+                                                        const float *__restrict__ inv_freq,
+                                                        const float2 *__restrict__ cs, uint32_t cs_rows)
 {
     const uint32_t half = head_dim / 2;
     const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -223,23 +297,13 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ Q, f
     const uint64_t tok = idx / half;
     const uint32_t t = static_cast<uint32_t>(tok % seq);
     const uint64_t bh = tok / seq;
-    const float pos = static_cast<float>(positions ? positions[t] : static_cast<int32_t>(t + offset));
-    const float angle = (pos * scaling) * inv_freq[j];
-    const float c = cosf(angle), s = sinf(angle);
+    const int32_t p = positions ? positions[t] : static_cast<int32_t>(t + offset);
+    float c, s;
+    rope_cos_sin(p, j, half, scaling, inv_freq, cs, cs_rows, c, s);
     const uint32_t i0 = interleaved ? 2 * j : j;
     const uint32_t i1 = interleaved ? 2 * j + 1 : j + half;
-    if (Q && t < q_seq) {
-        float *x = Q + (bh * q_seq + t) * head_dim;
-        const float x0 = x[i0], x1 = x[i1];
-        x[i0] = x0 * c - x1 * s;
-        x[i1] = x0 * s + x1 * c;
-    }
-    if (K && t < k_seq) {
-        float *x = K + (bh * k_seq + t) * head_dim;
-        const float x0 = x[i0], x1 = x[i1];
-        x[i0] = x0 * c - x1 * s;
-        x[i1] = x0 * s + x1 * c;
-    }
+    if (Q && t < q_seq) rotate_pair(Q + (bh * q_seq + t) * head_dim, i0, i1, c, s);
+    if (K && t < k_seq) rotate_pair(K + (bh * k_seq + t) * head_dim, i0, i1, c, s);
 }
 
 // Half-rotation layout with head_dim % 8 == 0 and 16-byte aligned rows: one
@@ -247,6 +311,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ Q, f
 __device__ __forceinline__ void rotate4(float *row, uint32_t j4, uint32_t half4, const float (&c)[4],
                                         const float (&s)[4])
 {
+#pragma clang fp contract(off)
     float4 *x = reinterpret_cast<float4 *>(row);
     const float4 a = x[j4], b = x[half4 + j4];
     x[j4] = make_float4(a.x * c[0] - b.x * s[0], a.y * c[1] - b.y * s[1], a.z * c[2] - b.z * s[2],
@@ -261,7 +326,8 @@ __global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ 
                                                             uint32_t k_seq, uint32_t seq,
                                                             uint32_t head_dim, uint32_t offset,
                                                             float scaling,
-                                                            const float *__restrict__ inv_freq)
+                                                            const float *__restrict__ inv_freq,
+                                                            const float2 *__restrict__ cs, uint32_t cs_rows)
 {
     const uint32_t half4 = head_dim / 8;
     const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -270,14 +336,10 @@ __global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ 
     const uint64_t tok = idx / half4;
     const uint32_t t = static_cast<uint32_t>(tok % seq);
     const uint64_t bh = tok / seq;
-    const float pos = static_cast<float>(positions ? positions[t] : static_cast<int32_t>(t + offset));
+    const int32_t p = positions ? positions[t] : static_cast<int32_t>(t + offset);
     float c[4], s[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float angle = (pos * scaling) * inv_freq[4 * j4 + e];
-        c[e] = cosf(angle);
-        s[e] = sinf(angle);
-    }
+    for (int e = 0; e < 4; ++e) rope_cos_sin(p, 4 * j4 + e, head_dim / 2, scaling, inv_freq, cs, cs_rows, c[e], s[e]);
     if (Q && t < q_seq) rotate4(Q + (bh * q_seq + t) * head_dim, j4, half4, c, s);
     if (K && t < k_seq) rotate4(K + (bh * k_seq + t) * head_dim, j4, half4, c, s);
 }
@@ -287,10 +349,11 @@ enum EwOp { EW_SWIGLU = 0, EW_ADD = 1, EW_MUL = 2, EW_GELU = 3 };
 template <int OP>
 __device__ __forceinline__ float ew(float a, float b, float alpha, float beta)
 {
-    if (OP == EW_SWIGLU) return dev::silu(a) * b * alpha;        // llm.cpp:240-246
-    if (OP == EW_ADD) return fmaf(a, alpha, b * beta);           // llm.cpp:256-271
-    if (OP == EW_MUL) return fmaf(a * b, alpha, beta);           // llm.cpp:273-287
-    return dev::gelu_tanh(a);                                    // llm.cpp:248-253
+    // the reference's AVX2 builds (llm.cpp:256-330), rounding for rounding
+    if (OP == EW_SWIGLU) return dev::swiglu_avx2(a, b, alpha);
+    if (OP == EW_ADD) return fmaf(a, alpha, dev::mul_rn(b, beta));
+    if (OP == EW_MUL) return fmaf(dev::mul_rn(a, b), alpha, beta);
+    return dev::gelu_avx2(a);
 }
 
 template <int OP>
@@ -423,7 +486,7 @@ __global__ __launch_bounds__(1024) void softmax_reg_kernel(const float *__restri
 template <int VPT, uint32_t PRE, bool NORM, bool QUANT, int NT = kThreads>
 __global__ __launch_bounds__(NT) void row_chain_kernel(RowChain p)
 {
-    static_assert(!NORM || NT == kThreads, "RMSNORM sums in rmsnorm_reg_kernel's order");
+    static_assert(!NORM || NT == kThreads, "RMSNORM as rmsnorm_reg_kernel computes it");
     __shared__ float red[NT / 64];
     const uint32_t n4 = p.cols >> 2;
     const uint64_t off = static_cast<uint64_t>(blockIdx.x) * n4;
@@ -454,23 +517,31 @@ __global__ __launch_bounds__(NT) void row_chain_kernel(RowChain p)
         }
     }
     if (NORM) {
-        float ss = 0.0f;
+        // rmsnorm_reg_kernel's arithmetic (the reference's AVX2 order)
+        extern __shared__ float4 row4[];   // cols floats
+        __shared__ float red8[8];
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
-            ss = fmaf(v[i].x, v[i].x, ss);
-            ss = fmaf(v[i].y, v[i].y, ss);
-            ss = fmaf(v[i].z, v[i].z, ss);
-            ss = fmaf(v[i].w, v[i].w, ss);
+            const uint32_t j = threadIdx.x + i * NT;
+            if (j < n4) row4[j] = v[i];
         }
-        ss = block_sum(ss, red);
-        const float inv = 1.0f / sqrtf(ss / static_cast<float>(p.cols) + p.eps);
+        __syncthreads();
+        const float *row = reinterpret_cast<const float *>(row4);
+        const uint32_t cols8 = p.cols & ~7u;
+        float acc = 0.0f;
+        chain_sumsq(row, cols8, acc);
+        if (threadIdx.x < 8) red8[threadIdx.x] = acc;
+        __syncthreads();
+        const float inv = rms_inv(chain_total(red8, row + cols8, p.cols - cols8), p.cols, p.eps);
         const float4 *w = reinterpret_cast<const float4 *>(p.W);
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const uint32_t j = threadIdx.x + i * NT;
             if (j >= n4) continue;
             const float4 g = w ? w[j] : make_float4(1.f, 1.f, 1.f, 1.f);
-            v[i] = make_float4(v[i].x * inv * g.x, v[i].y * inv * g.y, v[i].z * inv * g.z, v[i].w * inv * g.w);
+            const uint32_t e = 4 * j;
+            v[i] = make_float4(rms_scale(v[i].x, g.x, inv, e, cols8), rms_scale(v[i].y, g.y, inv, e + 1, cols8),
+                               rms_scale(v[i].z, g.z, inv, e + 2, cols8), rms_scale(v[i].w, g.w, inv, e + 3, cols8));
             reinterpret_cast<float4 *>(p.Nrm)[off + j] = v[i];
         }
     }
@@ -498,12 +569,13 @@ bool launch_row_chain(hipStream_t s, const RowChain &p)
 {
     const dim3 grid(p.rows), block(kThreads);
     const bool norm = p.Nrm != nullptr, quant = p.Q != nullptr;
+    const size_t lds = norm ? static_cast<size_t>(p.cols) * sizeof(float) : 0;
     if (p.pre == kChainAdd && norm && quant)
-        row_chain_kernel<VPT, kChainAdd, true, true><<<grid, block, 0, s>>>(p);
+        row_chain_kernel<VPT, kChainAdd, true, true><<<grid, block, lds, s>>>(p);
     else if (p.pre == kChainAdd && norm)
-        row_chain_kernel<VPT, kChainAdd, true, false><<<grid, block, 0, s>>>(p);
+        row_chain_kernel<VPT, kChainAdd, true, false><<<grid, block, lds, s>>>(p);
     else if (p.pre == kChainNone && norm && quant)
-        row_chain_kernel<VPT, kChainNone, true, true><<<grid, block, 0, s>>>(p);
+        row_chain_kernel<VPT, kChainNone, true, true><<<grid, block, lds, s>>>(p);
     else
         return false;
     return true;
@@ -535,14 +607,14 @@ void rmsnorm(hipStream_t s, const float *X, const float *W, float *Y, uint32_t r
                      ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y) |
                        (W ? reinterpret_cast<uintptr_t>(W) : 0)) % 16 == 0);
     const uint32_t n4 = cols / 4;
+    const size_t row_bytes = static_cast<size_t>(cols) * sizeof(float);
     if (vec && n4 <= kThreads * 4)
-        rmsnorm_reg_kernel<4><<<dim3(rows), kThreads, 0, s>>>(X, W, Y, cols, eps);
+        rmsnorm_reg_kernel<4><<<dim3(rows), kThreads, row_bytes, s>>>(X, W, Y, cols, eps);
     else if (vec && n4 <= kThreads * 12)
-        rmsnorm_reg_kernel<12><<<dim3(rows), kThreads, 0, s>>>(X, W, Y, cols, eps);
-    else if (vec)
-        rmsnorm_vec_kernel<<<dim3(rows), kThreads, 0, s>>>(X, W, Y, cols, eps);
+        rmsnorm_reg_kernel<12><<<dim3(rows), kThreads, row_bytes, s>>>(X, W, Y, cols, eps);
     else
-        rmsnorm_kernel<<<dim3(rows), kThreads, 0, s>>>(X, W, Y, cols, eps);
+        rmsnorm_kernel<<<dim3(rows), kThreads, std::min<size_t>(row_bytes, kChainFloats * sizeof(float)), s>>>(
+            X, W, Y, cols, eps);
 }
 
 // Rows below this count leave most CUs idle with one workgroup per row.
@@ -582,7 +654,8 @@ void softmax(hipStream_t s, const float *X, float *Y, uint32_t rows, uint32_t co
 
 void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t batch,
           uint32_t heads, uint32_t q_seq, uint32_t k_seq, uint32_t head_dim,
-          uint32_t position_offset, uint32_t interleaved, float scaling, const float *inv_freq)
+          uint32_t position_offset, uint32_t interleaved, float scaling, const float *inv_freq,
+          const float2 *cs, uint32_t cs_rows)
 {
     const uint32_t seq = q_seq > k_seq ? q_seq : k_seq;
     const uint64_t bh = static_cast<uint64_t>(batch) * heads;
@@ -593,12 +666,12 @@ void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t 
     if (vec) {
         const uint64_t t4 = total / 4;
         rope_vec_kernel<<<dim3(static_cast<uint32_t>((t4 + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
-            Q, K, positions, bh, q_seq, k_seq, seq, head_dim, position_offset, scaling, inv_freq);
+            Q, K, positions, bh, q_seq, k_seq, seq, head_dim, position_offset, scaling, inv_freq, cs, cs_rows);
         return;
     }
     rope_kernel<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
         Q, K, positions, bh, q_seq, k_seq, seq, head_dim, position_offset, interleaved, scaling,
-        inv_freq);
+        inv_freq, cs, cs_rows);
 }
 
 void swiglu(hipStream_t s, const float *g, const float *u, float *Y, uint64_t n, float alpha)

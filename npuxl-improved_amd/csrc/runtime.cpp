@@ -405,6 +405,8 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_device_create(const vnpu_config_t *config,
             tn = 64;
         }
         apply_tiles(d, tm, tk, tn, kTilesI8 | kTilesF32);
+        const char *ro = std::getenv("VNPU_REFERENCE_ORDER");
+        d->reference_order = (cfg.flags & VNPU_CONFIG_REFERENCE_ORDER) != 0 || (ro && ro[0] == '1');
         // "threads" = parallel units: the CU count unless the caller pins it.
         const uint32_t units = cfg.num_threads ? cfg.num_threads : d->cu_count;
 

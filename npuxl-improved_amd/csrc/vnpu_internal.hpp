@@ -169,6 +169,7 @@ struct vnpu_device {
     // of the dtype it tuned.  0 = automatic.
     std::atomic<uint32_t> i8_variant{0};   // int8 GEMM kernel (gemm_i8_variant_for_tiles)
     std::atomic<uint32_t> f32_depth{0};    // f32 K depth per workgroup (split-K)
+    bool reference_order = false;          // VNPU_CONFIG_REFERENCE_ORDER: attention bit-exact
     std::vector<vnpu_stream_t *> streams;
     std::mutex stream_mutex;
     vnpu_interrupt_cb_t irq_cb = nullptr;

@@ -52,6 +52,12 @@ def lib() -> C.CDLL:
             "vo_mul": (None, [vp, vp, vp, u64, f32, f32]),
             "vo_gelu": (None, [vp, vp, u64]),
             "vo_attention": (None, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32]),
+            "vo_rmsnorm_avx2": (None, [vp, vp, vp, u32, u32, f32]),
+            "vo_exp_avx2": (f32, [f32]),
+            "vo_swiglu_avx2": (None, [vp, vp, vp, u64, f32]),
+            "vo_gelu_avx2": (None, [vp, vp, u64]),
+            "vo_mul_avx2": (None, [vp, vp, vp, u64, f32, f32]),
+            "vo_attention_avx2": (None, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(_lib, name)
@@ -237,6 +243,49 @@ def attention(Q, K, V, mask=None, causal=0, scale=0.0):
     O = np.empty_like(Q)
     lib().vo_attention(_p(Q), _p(K), _p(V), _p(_c(mask, np.float32)), _p(O), b, h, sq, sk, d,
                        causal, scale)
+    return O
+
+
+def rmsnorm_avx2(X, W=None, eps=1e-5):
+    """RMSNORM in the order of the reference's AVX2 build (bit for bit)."""
+    X = _c(X, np.float32)
+    Y = np.empty_like(X)
+    lib().vo_rmsnorm_avx2(_p(X), _p(_c(W, np.float32)), _p(Y), X.shape[0], X.shape[1], eps)
+    return Y
+
+
+def swiglu_avx2(g, u, alpha=1.0):
+    """SWIGLU in the order of the reference's AVX2 build (bit for bit)."""
+    g, u = _c(g, np.float32), _c(u, np.float32)
+    Y = np.empty_like(g)
+    lib().vo_swiglu_avx2(_p(g), _p(u), _p(Y), g.size, alpha)
+    return Y
+
+
+def gelu_avx2(x):
+    """GELU in the order of the reference's AVX2 build (bit for bit)."""
+    x = _c(x, np.float32)
+    Y = np.empty_like(x)
+    lib().vo_gelu_avx2(_p(x), _p(Y), x.size)
+    return Y
+
+
+def mul_avx2(a, b, alpha=1.0, beta=0.0):
+    """MUL in the order of the reference's AVX2 build (bit for bit)."""
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    Y = np.empty_like(a)
+    lib().vo_mul_avx2(_p(a), _p(b), _p(Y), a.size, alpha, beta)
+    return Y
+
+
+def attention_avx2(Q, K, V, mask=None, causal=0, scale=0.0):
+    """ATTENTION_F32 in the order of the reference's AVX2 build (bit for bit)."""
+    Q, K, V = _c(Q, np.float32), _c(K, np.float32), _c(V, np.float32)
+    b, h, sq, d = Q.shape
+    sk = K.shape[2]
+    O = np.empty_like(Q)
+    lib().vo_attention_avx2(_p(Q), _p(K), _p(V), _p(_c(mask, np.float32)), _p(O), b, h, sq, sk, d,
+                            causal, scale)
     return O
 
 

@@ -557,3 +557,179 @@ void vo_attention(const float *Q, const float *K, const float *V, const float *m
     }
     free(acc);
 }
+
+/* ----------------------------------------------------------------------- */
+/* The reference's AVX2 builds of the block's f32 ops, in their exact order  */
+/* of roundings (what the reference computes on an AVX2 host).  fmaf marks   */
+/* each fused multiply-add of the reference's intrinsics; everything else   */
+/* rounds separately (this file is built with -ffp-contract=off).           */
+/* ----------------------------------------------------------------------- */
+
+/* hsum256 (llm.cpp:20-28): (lo + hi), then two horizontal adds. */
+static float vo_hsum8(const float a[8])
+{
+    float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+    return (s0 + s1) + (s2 + s3);
+}
+
+/* rmsnorm_avx2_rows (llm.cpp:80-108): eight running sums of x*x (FMA) over
+ * each 8-wide step, hsum256, then the tail; y = (x*w)*inv over the 8-wide
+ * part and (x*inv)*w on the tail. */
+void vo_rmsnorm_avx2(const float *X, const float *W, float *Y, uint32_t rows, uint32_t cols, float eps)
+{
+    if (!(eps > 0.0f)) eps = 1e-5f;
+    for (uint32_t r = 0; r < rows; ++r) {
+        const float *x = X + (size_t)r * cols;
+        float *y = Y + (size_t)r * cols;
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        uint32_t j = 0;
+        for (; j + 8 <= cols; j += 8)
+            for (int l = 0; l < 8; ++l) acc[l] = fmaf(x[j + l], x[j + l], acc[l]);
+        float sum = vo_hsum8(acc);
+        for (; j < cols; ++j) sum = fmaf(x[j], x[j], sum);
+        float inv = 1.0f / sqrtf(sum / (float)cols + eps);
+        j = 0;
+        for (; j + 8 <= cols; j += 8)
+            for (int l = 0; l < 8; ++l) y[j + l] = (x[j + l] * (W ? W[j + l] : 1.0f)) * inv;
+        for (; j < cols; ++j) y[j] = x[j] * inv * (W ? W[j] : 1.0f);
+    }
+}
+
+/* exp256_ps (llm.cpp:31-56): x clamped to [-80, 80], z = x*log2e,
+ * f = z - floor(z), P5 by FMA Horner, times 2^floor(z). */
+float vo_exp_avx2(float x)
+{
+    x = x < -80.0f ? -80.0f : x;
+    x = x > 80.0f ? 80.0f : x;
+    float z = x * 1.4426950408889634f;
+    float zi = floorf(z);
+    float f = z - zi;
+    float p = fmaf(0.0013333558146428443f, f, 0.009618129107628477f);
+    p = fmaf(p, f, 0.05550410866482158f);
+    p = fmaf(p, f, 0.2402265069591007f);
+    p = fmaf(p, f, 0.6931471805599453f);
+    p = fmaf(p, f, 1.0f);
+    return ldexpf(p, (int)zi);
+}
+
+/* swiglu_avx2_range (llm.cpp:289-306): s = g / (1 + exp256(-g)),
+ * y = (s*u)*alpha; the scalar tail of a thread's range uses silu with the
+ * same FMA polynomial (its AVX2 function contracts it). */
+void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha)
+{
+    float a = alpha == 0.0f ? 1.0f : alpha;
+    for (uint64_t i = 0; i < count; ++i) {
+        float g = gate[i];
+        float s = g / (1.0f + vo_exp_avx2(-g));
+        Y[i] = (s * up[i]) * a;
+    }
+}
+
+/* gelu_avx2_range (llm.cpp:308-330): inner = k0 * fma(k1, x^3, x),
+ * t = 2 / (1 + exp256(-2 inner)) - 1, y = (0.5 x)(1 + t). */
+void vo_gelu_avx2(const float *X, float *Y, uint64_t count)
+{
+    for (uint64_t i = 0; i < count; ++i) {
+        float x = X[i];
+        float x3 = (x * x) * x;
+        float inner = 0.7978845608028654f * fmaf(0.035677408136300125f, x3, x);
+        float e = vo_exp_avx2(-2.0f * inner);
+        float t = 2.0f / (1.0f + e) - 1.0f;
+        Y[i] = (0.5f * x) * (1.0f + t);
+    }
+}
+
+/* mul_avx2_range (llm.cpp:273-287): y = fma(a*b, alpha, beta). */
+void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta)
+{
+    float a = alpha == 0.0f ? 1.0f : alpha;
+    for (uint64_t i = 0; i < count; ++i) Y[i] = fmaf(A[i] * B[i], a, beta);
+}
+
+/* dot_avx2 (llm.cpp:332-343): eight FMA chains over 8-wide steps, hsum256,
+ * then the tail (a separate multiply and add). */
+static float vo_dot_avx2(const float *a, const float *b, uint32_t n)
+{
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; ++l) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
+    float sum = vo_hsum8(acc);
+    for (; i < n; ++i) sum += a[i] * b[i];   /* the build leaves this tail unfused */
+    return sum;
+}
+
+/* attention_range (llm.cpp:442-546) with its AVX2 helpers: scores by
+ * dot_avx2, the online softmax in the function's own (non-AVX2, so unfused)
+ * scalar arithmetic with the scalar fast_expf, acc by axpy_avx2 (FMA). */
+void vo_attention_avx2(const float *Q, const float *K, const float *V, const float *mask, float *O,
+                       uint32_t batch, uint32_t heads, uint32_t seq_q, uint32_t seq_k,
+                       uint32_t head_dim, uint32_t causal, float scale)
+{
+    enum { BQ = 16, BK = 64 };
+    const uint32_t D = head_dim;
+    if (!(scale > 0.0f)) scale = 1.0f / sqrtf((float)D);
+    float scores[BQ * BK], probs[BQ * BK], m[BQ], l[BQ];
+    float *acc = (float *)malloc((size_t)BQ * D * sizeof(float));
+    const uint32_t off = seq_k > seq_q ? seq_k - seq_q : 0;
+    for (uint64_t bh = 0; bh < (uint64_t)batch * heads; ++bh) {
+        const float *Qh = Q + bh * seq_q * D;
+        const float *Kh = K + bh * seq_k * D;
+        const float *Vh = V + bh * seq_k * D;
+        const float *Mh = mask ? mask + bh * seq_q * seq_k : NULL;
+        float *Oh = O + bh * seq_q * D;
+        for (uint32_t q0 = 0; q0 < seq_q; q0 += BQ) {
+            uint32_t qc = umin(BQ, seq_q - q0);
+            for (uint32_t i = 0; i < qc; ++i) {
+                m[i] = -INFINITY;
+                l[i] = 0.0f;
+                for (uint32_t d = 0; d < D; ++d) acc[i * D + d] = 0.0f;
+            }
+            for (uint32_t k0 = 0; k0 < seq_k; k0 += BK) {
+                uint32_t kc = umin(BK, seq_k - k0);
+                for (uint32_t i = 0; i < qc; ++i) {
+                    uint32_t qi = q0 + i;
+                    for (uint32_t j = 0; j < kc; ++j) {
+                        uint32_t ki = k0 + j;
+                        float s;
+                        if (causal && ki > qi + off) {
+                            s = -INFINITY;
+                        } else {
+                            s = vo_dot_avx2(Qh + (size_t)qi * D, Kh + (size_t)ki * D, D) * scale;
+                            if (Mh) s += Mh[(size_t)qi * seq_k + ki];
+                        }
+                        scores[i * BK + j] = s;
+                    }
+                }
+                for (uint32_t i = 0; i < qc; ++i) {
+                    float bmax = -INFINITY;
+                    for (uint32_t j = 0; j < kc; ++j)
+                        bmax = (bmax < scores[i * BK + j]) ? scores[i * BK + j] : bmax;
+                    if (!isfinite(bmax)) continue;
+                    float new_m = (m[i] < bmax) ? bmax : m[i];
+                    float alpha = vo_fast_expf(m[i] - new_m);
+                    float sum_p = 0.0f;
+                    for (uint32_t j = 0; j < kc; ++j) {
+                        float p = vo_fast_expf(scores[i * BK + j] - new_m);
+                        probs[i * BK + j] = p;
+                        sum_p += p;
+                    }
+                    l[i] = l[i] * alpha + sum_p;
+                    for (uint32_t d = 0; d < D; ++d) acc[i * D + d] *= alpha;
+                    for (uint32_t j = 0; j < kc; ++j) {
+                        float p = probs[i * BK + j];
+                        if (p == 0.0f) continue;
+                        const float *v = Vh + (size_t)(k0 + j) * D;
+                        for (uint32_t d = 0; d < D; ++d) acc[i * D + d] = fmaf(v[d], p, acc[i * D + d]);
+                    }
+                    m[i] = new_m;
+                }
+            }
+            for (uint32_t i = 0; i < qc; ++i) {
+                float inv = l[i] > 0.0f ? 1.0f / l[i] : 0.0f;
+                for (uint32_t d = 0; d < D; ++d) Oh[(size_t)(q0 + i) * D + d] = acc[i * D + d] * inv;
+            }
+        }
+    }
+    free(acc);
+}

@@ -70,4 +70,14 @@ void vo_attention(const float *Q, const float *K, const float *V, const float *m
 }
 #endif
 
+/* The reference's AVX2 builds of the block's f32 ops, rounding for rounding. */
+void vo_rmsnorm_avx2(const float *X, const float *W, float *Y, uint32_t rows, uint32_t cols, float eps);
+float vo_exp_avx2(float x);
+void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha);
+void vo_gelu_avx2(const float *X, float *Y, uint64_t count);
+void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta);
+void vo_attention_avx2(const float *Q, const float *K, const float *V, const float *mask, float *O,
+                       uint32_t batch, uint32_t heads, uint32_t seq_q, uint32_t seq_k,
+                       uint32_t head_dim, uint32_t causal, float scale);
+
 #endif

@@ -18,20 +18,20 @@ def gemm(x, wq, ws):
     return oracle.matmul_i8(a8, wq, sa, ws)
 
 
-def attention_threaded(q, K, V, causal=1, workers=None, mask=None):
-    """oracle.attention over (batch, head) slices on a thread pool (the C call
-    releases the GIL); each slice is the same C restatement, so the result
-    equals one oracle.attention call."""
+def attention_threaded(q, K, V, causal=1, workers=None, mask=None, avx2=False):
+    """oracle.attention (or attention_avx2) over (batch, head) slices on a
+    thread pool (the C call releases the GIL); each slice is the same C
+    restatement, so the result equals one call over the whole tensor."""
     from concurrent.futures import ThreadPoolExecutor
 
     B, H = q.shape[:2]
     out = np.empty_like(q)
+    fn = oracle.attention_avx2 if avx2 else oracle.attention
 
     def one(i):
         b, h = divmod(i, H)
         m = None if mask is None else mask[b:b + 1, h:h + 1]
-        out[b, h] = oracle.attention(q[b:b + 1, h:h + 1], K[b:b + 1, h:h + 1],
-                                     V[b:b + 1, h:h + 1], m, causal)[0, 0]
+        out[b, h] = fn(q[b:b + 1, h:h + 1], K[b:b + 1, h:h + 1], V[b:b + 1, h:h + 1], m, causal)[0, 0]
 
     with ThreadPoolExecutor(max_workers=workers or min(16, os.cpu_count() or 1)) as ex:
         list(ex.map(one, range(B * H)))
@@ -39,16 +39,21 @@ def attention_threaded(q, K, V, causal=1, workers=None, mask=None):
 
 
 def block_stages(shape, wq, norm_attn, norm_ffn, x, batch, tokens, past=0, k_cache=None,
-                 v_cache=None, eps=1e-5, theta=10000.0):
+                 v_cache=None, eps=1e-5, theta=10000.0, avx2=False):
     """The block of block() at any size, keeping every stage: the int8 GEMMs
     through oracle.matmul_i8_blas (bit-identical to oracle.matmul_i8) and
-    attention per (batch, head) on threads.  Returns name -> array, with the
-    inputs of the four per-row quantize stages under xn1, att, xn2, ff."""
+    attention per (batch, head) on threads.  avx2=True composes the
+    oracle's restatements of the reference's AVX2 builds (RMSNORM, SWIGLU,
+    attention; each pinned bit for bit to the reference build), i.e. the
+    reference's own block output on an AVX2 host.  Returns name -> array, with
+    the inputs of the four per-row quantize stages under xn1, att, xn2, ff."""
     d, H, D = shape.d_model, shape.heads, shape.head_dim
     B, T = batch, tokens
+    rmsnorm = oracle.rmsnorm_avx2 if avx2 else oracle.rmsnorm
+    swiglu = oracle.swiglu_avx2 if avx2 else oracle.swiglu
     st = {}
     x = np.array(x, np.float32, copy=True)
-    st["xn1"] = oracle.rmsnorm(x, norm_attn, eps)
+    st["xn1"] = rmsnorm(x, norm_attn, eps)
 
     def g(name, a):
         a8, sa = oracle.quantize(a, 0)
@@ -69,14 +74,14 @@ def block_stages(shape, wq, norm_attn, norm_ffn, x, batch, tokens, past=0, k_cac
         Vc[:, :, past:past + T] = v
     else:
         Kc, Vc = k, v
-    st["o"] = o = attention_threaded(q, Kc, Vc, 1)
+    st["o"] = o = attention_threaded(q, Kc, Vc, 1, avx2=avx2)
     st["att"] = att = np.ascontiguousarray(o.transpose(0, 2, 1, 3).reshape(B * T, d))
     st["x1"] = x1 = oracle.add(x, g("o", att), 1.0, 1.0)
-    st["xn2"] = xn2 = oracle.rmsnorm(x1, norm_ffn, eps)
+    st["xn2"] = xn2 = rmsnorm(x1, norm_ffn, eps)
     a8, sa = oracle.quantize(xn2, 0)
     st["gate"] = gate = oracle.matmul_i8_blas(a8, wq["gate"][0], sa, wq["gate"][1])
     st["up"] = up = oracle.matmul_i8_blas(a8, wq["up"][0], sa, wq["up"][1])
-    st["ff"] = ff = oracle.swiglu(gate, up, 1.0)
+    st["ff"] = ff = swiglu(gate, up, 1.0)
     st["out"] = oracle.add(x1, g("down", ff), 1.0, 1.0)
     return st
 

@@ -215,3 +215,58 @@ def test_matmul_f32_config1_epilogue_and_packed_defect(ref):
     assert oracle.rel_error(got, want) <= 1e-4
     packed = g.matmul_f32(ref, A, B, M, K, N, bias=bias, epilogue=abi.EPI_SILU)
     assert oracle.rel_error(packed, want) > 1e-2
+
+
+# ---------------------------------------------------------------- AVX2 order
+# The reference on an AVX2 host runs its AVX2 builds of these ops; the
+# oracle's *_avx2 restatements follow their order of roundings and must
+# equal the reference build bit for bit (the GPU kernels are then held to
+# the same bits).
+
+def _bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 4096), (3, 4099), (5, 33), (2, 11008), (2, 7), (1, 20000)])
+def test_rmsnorm_avx2_order_bit_exact(ref, rows, cols):
+    X = RNG.standard_normal((rows, cols)).astype(np.float32) * 2
+    W = (1.0 + 0.1 * RNG.standard_normal(cols)).astype(np.float32)
+    assert _bits(g.unary_rows(ref, abi.OP_RMSNORM_F32, X, W=W, eps=1e-5), oracle.rmsnorm_avx2(X, W, 1e-5))
+    assert _bits(g.unary_rows(ref, abi.OP_RMSNORM_F32, X, eps=0.0), oracle.rmsnorm_avx2(X, None, 1e-5))
+
+
+@pytest.mark.parametrize("n", [8, 1001, 100000, 2048 * 11008 // 32])
+def test_swiglu_gelu_avx2_order_bit_exact(ref, n):
+    a = (RNG.standard_normal(n) * 4).astype(np.float32)
+    b = RNG.standard_normal(n).astype(np.float32)
+    assert _bits(g.elementwise(ref, abi.OP_SWIGLU_F32, a, b, alpha=0.0), oracle.swiglu_avx2(a, b, 1.0))
+    assert _bits(g.elementwise(ref, abi.OP_SWIGLU_F32, a, b, alpha=0.5), oracle.swiglu_avx2(a, b, 0.5))
+    assert _bits(g.elementwise(ref, abi.OP_GELU_F32, a), oracle.gelu_avx2(a))
+    assert _bits(g.elementwise(ref, abi.OP_ADD_F32, a, b, 0.0, 0.0), oracle.add(a, b, 1.0, 1.0))
+
+
+def test_rope_bit_exact(ref):
+    Q = RNG.standard_normal((2, 3, 50, 128)).astype(np.float32)
+    K = RNG.standard_normal((2, 3, 40, 128)).astype(np.float32)
+    for offset in (0, 4095):
+        gq, gk = g.rope(ref, Q, K, position_offset=offset)
+        oq, ok = oracle.rope(Q, K, position_offset=offset)
+        assert _bits(gq, oq) and _bits(gk, ok)
+
+
+@pytest.mark.parametrize("b,h,sq,sk,d,causal,mask", [
+    (2, 2, 100, 300, 128, 1, None), (1, 3, 1, 4096, 128, 1, None), (2, 2, 37, 70, 20, 0, "normal"),
+    (1, 2, 5, 130, 64, 1, "inf"), (1, 1, 16, 16, 64, 1, "row"), (1, 2, 3, 200, 96, 0, "inf")])
+def test_attention_avx2_order_bit_exact(ref, b, h, sq, sk, d, causal, mask):
+    Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
+    K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+    V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+    M = None
+    if mask:
+        M = RNG.standard_normal((b, h, sq, sk)).astype(np.float32)
+        if mask == "inf":
+            M[..., : sk // 3] = -np.inf
+        if mask == "row":
+            M[0, 0, 3, :] = -np.inf
+    got = g.attention(ref, Q, K, V, M, causal)
+    assert _bits(got, oracle.attention_avx2(Q, K, V, M, causal))
