@@ -273,6 +273,15 @@ def bench_attention(s: Session, steps: int, warmup: int):
     return out
 
 
+def reference_order_session() -> Session:
+    """A session whose device rounds in the reference's order
+    (VNPU_CONFIG_REFERENCE_ORDER: bit-exact attention, hence block)."""
+    cfg = abi.Config()
+    cfg.abi_version = 1
+    cfg.flags = abi.CONFIG_REFERENCE_ORDER
+    return Session(None, cfg)
+
+
 def bench_copy(s: Session, steps: int):
     """A device-to-device COPY of 256 MiB, `steps` times: a plain copy kernel of
     known size that calibrates the FETCH_SIZE / WRITE_SIZE counters behind
@@ -461,8 +470,14 @@ def main():
             log("copy", bench_copy(s, 5))
         elif args.only == "attention":
             log("attention", bench_attention(s, args.steps, args.warmup))
+            x = reference_order_session()
+            log("attention reference-order", bench_attention(x, args.steps, args.warmup))
+            x.close()
         elif args.only == "block":
             log("block", bench_block(s, args.steps))
+            x = reference_order_session()
+            log("block reference-order", bench_block(x, args.steps))
+            x.close()
         elif args.only == "config1":
             log("config1", bench_config1(s, args.steps))
         else:
@@ -507,6 +522,13 @@ def main():
         log("attention", extras["config4_attention"])
         extras["config4_block"] = {k: rounded(v, 3) for k, v in bench_block(s, 20).items()}
         log("block", extras["config4_block"])
+        x = reference_order_session()
+        extras["config4_attention_reference_order"] = {k: rounded(v, 3)
+                                                      for k, v in bench_attention(x, 20, 3).items()}
+        log("attention reference-order", extras["config4_attention_reference_order"])
+        extras["config4_block_reference_order"] = {k: rounded(v, 3) for k, v in bench_block(x, 20).items()}
+        log("block reference-order", extras["config4_block_reference_order"])
+        x.close()
         extras["config5"] = {k: rounded(v, 3) for k, v in bench_config5(s, 10).items()}
         log("config5", extras["config5"])
     if wq is not None:

@@ -52,6 +52,7 @@ CMD_FLAG_CELL_DMA = 1 << 3
 CMD_FLAG_VOODOO_FIFO = 1 << 4
 
 CONFIG_TRACE = 1 << 0
+CONFIG_REFERENCE_ORDER = 1 << 7   # kernels that round in the reference's order (include/vnpu.h)
 
 
 class Config(C.Structure):

@@ -23,6 +23,19 @@ def gpu():
 
 
 @pytest.fixture(scope="session")
+def exact_gpu():
+    """A second MI355X session whose device is created with
+    VNPU_CONFIG_REFERENCE_ORDER: every op rounds in the reference's order."""
+    from vnpu_mi355x import Session, abi
+    cfg = abi.Config()
+    cfg.abi_version = 1
+    cfg.flags = abi.CONFIG_REFERENCE_ORDER
+    s = Session(None, cfg)
+    yield s
+    s.close()
+
+
+@pytest.fixture(scope="session")
 def ref():
     """The reference runtime built from its own sources (CPU), if present."""
     import oracle

@@ -14,27 +14,17 @@ import ctypes as C
 import numpy as np
 import pytest
 
-import oracle
+import block_oracle
 import gpu_ops as g
-from vnpu_mi355x import Session, abi
+import oracle
+from vnpu_mi355x import abi
 
 pytestmark = pytest.mark.gpu
 RNG = np.random.default_rng(777)
-REFERENCE_ORDER = 1 << 7
 
 
 def bits(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
-
-
-@pytest.fixture(scope="module")
-def exact_gpu():
-    cfg = abi.Config()
-    cfg.abi_version = 1
-    cfg.flags = REFERENCE_ORDER
-    s = Session(None, cfg)
-    yield s
-    s.close()
 
 
 @pytest.mark.parametrize("rows,cols", [(2048, 4096), (8, 11008), (3, 12288), (3, 4099), (2, 20000), (5, 33),
@@ -133,29 +123,9 @@ def test_attention_reference_order_bit_exact(exact_gpu, b, h, sq, sk, d, causal,
         if mask == "row":
             M[0, 0, 3, :] = -np.inf
     got = g.attention(exact_gpu, Q, K, V, M, causal)
-    if b * h * sq * sk > 1_000_000:
-        import block_oracle
-        want = np.empty_like(Q)
-        for bi in range(b):   # per (batch, head) on threads: same C restatement
-            want[bi:bi + 1] = _threaded_avx2(Q[bi:bi + 1], K[bi:bi + 1], V[bi:bi + 1], causal)
-    else:
-        want = oracle.attention_avx2(Q, K, V, M, causal)
+    # per (batch, head) on threads: the same C restatement as one call
+    want = block_oracle.attention_threaded(Q, K, V, causal, mask=M, avx2=True)
     assert bits(got, want)
-
-
-def _threaded_avx2(Q, K, V, causal):
-    from concurrent.futures import ThreadPoolExecutor
-    B, H = Q.shape[:2]
-    out = np.empty_like(Q)
-
-    def one(i):
-        b, h = divmod(i, H)
-        out[b, h] = oracle.attention_avx2(Q[b:b + 1, h:h + 1], K[b:b + 1, h:h + 1], V[b:b + 1, h:h + 1],
-                                          None, causal)[0, 0]
-
-    with ThreadPoolExecutor(max_workers=16) as ex:
-        list(ex.map(one, range(B * H)))
-    return out
 
 
 def test_attention_reference_order_noalloc(exact_gpu):
