@@ -970,69 +970,69 @@ __global__ __launch_bounds__(kThreads) void attn_rowwise_kernel(Attn a, uint64_t
     for (uint32_t d = tid; d < D; d += kThreads) o[d] = o[d] * inv;
 }
 
-// The same arithmetic tiled for head_dim 64 or 128 and at most 65535
-// (batch, head) pairs: one workgroup of 256 threads per (batch, head) and QT
-// query rows.  Per 64-key block the K (row pitch D + 1 floats: lane j reads
-// key j's element i with no bank conflict) and V tiles are staged in LDS,
-// the next block's tiles already in flight in registers.
-//   scores: thread (key j = tid % 64, query group tid / 64) runs the eight
-//           dot chains for its QPT queries, each K element read once;
-//   softmax: wave w owns queries w, w + 4, ...: block max and the weights by
-//           lane j, the weight sum by lane 0 in key order;
-//   output: thread (d slot tid % (D / DPT), query group) keeps QPT x DPT
-//           accumulators and walks the block's keys in order.
-// QT = 1 (decode: one workgroup per query row) or 16 (prefill).
-template <int QT, int D>
-struct ExactCfg {
-    static constexpr int P = D + 1;                 // K row pitch in LDS (floats)
-    static constexpr int QG = QT == 1 ? 1 : 4;      // query groups (waves) in the score/output phases
-    static constexpr int QPT = QT / QG;             // queries per thread
-    static constexpr int DS = QT == 1 ? D : 64;     // output d slots
-    static constexpr int DPT = D / DS;              // d per thread
-    static constexpr int kFloats = RK * P + RK * D + QT * D + QT * RK + 4 * QT;
+// Reference-order prefill tiled for head_dim 64 or 128: one workgroup of
+// four waves per (batch, head) and 16 query rows, wave w owning rows
+// 4w .. 4w+3 through all three phases of a 64-key block, so the block's
+// weights never leave the wave's registers:
+//   scores:  lane j computes key j's eight dot chains for the wave's rows
+//            (K rows in LDS at pitch D + 4 floats: lane j's 16-byte reads are
+//            conflict-free; Q rows are broadcast reads);
+//   softmax: block max across the lanes, weights p_j in lane j; the weight
+//            sum of row i in key order by lane i from an LDS copy;
+//   output:  lane owns D / 64 output elements of each row and walks the keys
+//            in order, the weights read back from the LDS copy; the
+//            reference's "p_j != 0" skip tests a ballot mask of the nonzero
+//            weights (uniform), once per four keys when all are nonzero.
+// The workgroups of the longest (causal) rows are dispatched first.
+template <int D>
+struct ExactRows {
+    static constexpr int QT = 16;                // query rows per workgroup
+    static constexpr int RW = 4;                 // rows per wave
+    static constexpr int P = D + 4;              // K row pitch (floats)
+    static constexpr int WP = RK + 4;            // weight row pitch (floats)
+    static constexpr int DPT = D / 64;           // output elements per lane and row
+    static constexpr int kFloats = RK * P + RK * D + QT * D + QT * WP;
     static constexpr size_t kLds = static_cast<size_t>(kFloats) * sizeof(float);
     static constexpr int kPre = RK * D / 4 / kThreads;   // float4s of K (and of V) per thread per block
 };
 
-template <int QT, int D>
-__global__ __launch_bounds__(kThreads) void attn_exact_kernel(Attn a)
+__device__ __forceinline__ void wave_sync_lds()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_exact_rows_kernel(Attn a)
 {
 #pragma clang fp contract(off)
-    using G = ExactCfg<QT, D>;
-    extern __shared__ float sm[];
-    float *Ks = sm;                          // [64][P]
-    float *Vs = Ks + RK * G::P;              // [64][D]
-    float *Qs = Vs + RK * D;                 // [QT][D]
-    float *W = Qs + QT * D;                  // [QT][64] scores, then weights
-    float *Ml = W + QT * RK;                 // [QT] running max
-    float *Ll = Ml + QT;                     // [QT] running sum
-    float *Al = Ll + QT;                     // [QT] this block's alpha
-    float *Sk = Al + QT;                     // [QT] 1 = block skipped for the row
+    using G = ExactRows<D>;
+    constexpr int RW = G::RW, DPT = G::DPT;
+    extern __shared__ float4 sm4[];
+    float *Ks = reinterpret_cast<float *>(sm4);  // [64][P]
+    float *Vs = Ks + RK * G::P;                   // [64][D]
+    float *Qs = Vs + RK * D;                      // [QT][D]
+    float *Wl = Qs + G::QT * D;                   // [QT][WP] weights, for the row sums
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t bh = blockIdx.y;
     const uint32_t sq = a.seq_q, sk = a.seq_k;
     const uint32_t off = sk > sq ? sk - sq : 0;
-    const uint32_t q0 = blockIdx.x * QT;
-    const uint32_t nq = min(static_cast<uint32_t>(QT), sq - q0);
+    const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * G::QT;
+    const uint32_t nq = min(static_cast<uint32_t>(G::QT), sq - q0);
     const float *Kh = a.K + bh * sk * D;
     const float *Vh = a.V + bh * sk * D;
     const float *Mh = a.mask ? a.mask + bh * sq * sk : nullptr;
 
-    for (int i = tid; i < QT * D; i += kThreads) {
+    for (int i = tid; i < G::QT * D; i += kThreads) {
         const uint32_t r = i / D;
         Qs[i] = r < nq ? a.Q[(bh * sq + q0 + r) * D + (i % D)] : 0.0f;
-    }
-    if (tid < QT) {
-        Ml[tid] = -__builtin_inff();
-        Ll[tid] = 0.0f;
     }
     uint32_t kend = sk;
     if (a.causal) kend = min(sk, q0 + nq - 1 + off + 1);
     const uint32_t nblk = (kend + RK - 1) / RK;
 
-    // Staging of block b's K and V: float4 f = tid + kThreads * u of the
-    // block's 64 x D floats (rows past kend read as zero).
     float4 pk[G::kPre], pv[G::kPre];
     auto fetch = [&](uint32_t b) {
 #pragma unroll
@@ -1049,118 +1049,362 @@ __global__ __launch_bounds__(kThreads) void attn_exact_kernel(Attn a)
 #pragma unroll
         for (int u = 0; u < G::kPre; ++u) {
             const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);
-            float *kr = Ks + j * G::P + 4 * c4;
-            kr[0] = pk[u].x;
-            kr[1] = pk[u].y;
-            kr[2] = pk[u].z;
-            kr[3] = pk[u].w;
+            *reinterpret_cast<float4 *>(Ks + j * G::P + 4 * c4) = pk[u];
             reinterpret_cast<float4 *>(Vs)[f] = pv[u];
         }
     };
 
-    float acc[G::QPT][G::DPT];
+    // Row state: m (uniform per row), l of row `wave*RW + lane` in lane < RW.
+    float m[RW], acc[RW][DPT];
+    float l_mine = 0.0f;
 #pragma unroll
-    for (int i = 0; i < G::QPT; ++i)
+    for (int i = 0; i < RW; ++i) {
+        m[i] = -__builtin_inff();
 #pragma unroll
-        for (int e = 0; e < G::DPT; ++e) acc[i][e] = 0.0f;
+        for (int e = 0; e < DPT; ++e) acc[i][e] = 0.0f;
+    }
+    const int r0 = wave * RW;
+    float *wrow = Wl + r0 * G::WP;
 
     if (nblk) fetch(0);
     for (uint32_t b = 0; b < nblk; ++b) {
         const uint32_t k0 = b * RK, kc = min(static_cast<uint32_t>(RK), kend - k0);
-        __syncthreads();   // the previous block's tiles and weights are consumed
+        __syncthreads();   // the previous block's tiles are consumed
         stage();
         __syncthreads();
         if (b + 1 < nblk) fetch(b + 1);
 
-        // Scores.
-        if (QT > 1 || wave == 0) {
-            const int j = lane, g = QT > 1 ? wave : 0;
-            float ch[G::QPT][8];
+        // Scores of the wave's rows, key `lane`.
+        float ch[RW][8];
 #pragma unroll
-            for (int i = 0; i < G::QPT; ++i)
+        for (int i = 0; i < RW; ++i)
 #pragma unroll
-                for (int c = 0; c < 8; ++c) ch[i][c] = 0.0f;
-            const float *kr = Ks + j * G::P;
+            for (int c = 0; c < 8; ++c) ch[i][c] = 0.0f;
+        {
+            const float *kr = Ks + lane * G::P;
+            const float *qr = Qs + r0 * D;
+#pragma unroll 2
             for (int d = 0; d < D; d += 8) {
+                const float4 ka = *reinterpret_cast<const float4 *>(kr + d);
+                const float4 kb = *reinterpret_cast<const float4 *>(kr + d + 4);
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const float kv = kr[d + c];
-#pragma unroll
-                    for (int i = 0; i < G::QPT; ++i) ch[i][c] = fmaf(Qs[(g * G::QPT + i) * D + d + c], kv, ch[i][c]);
+                for (int i = 0; i < RW; ++i) {
+                    const float4 qa = *reinterpret_cast<const float4 *>(qr + i * D + d);
+                    const float4 qb = *reinterpret_cast<const float4 *>(qr + i * D + d + 4);
+                    ch[i][0] = fmaf(qa.x, ka.x, ch[i][0]);
+                    ch[i][1] = fmaf(qa.y, ka.y, ch[i][1]);
+                    ch[i][2] = fmaf(qa.z, ka.z, ch[i][2]);
+                    ch[i][3] = fmaf(qa.w, ka.w, ch[i][3]);
+                    ch[i][4] = fmaf(qb.x, kb.x, ch[i][4]);
+                    ch[i][5] = fmaf(qb.y, kb.y, ch[i][5]);
+                    ch[i][6] = fmaf(qb.z, kb.z, ch[i][6]);
+                    ch[i][7] = fmaf(qb.w, kb.w, ch[i][7]);
                 }
-            }
-#pragma unroll
-            for (int i = 0; i < G::QPT; ++i) {
-                const uint32_t r = g * G::QPT + i, qi = q0 + r;
-                float sc = -__builtin_inff();
-                const uint32_t key = k0 + j;
-                if (j < static_cast<int>(kc) && r < nq && !(a.causal && key > qi + off)) {
-                    const float dot = ((ch[i][0] + ch[i][4]) + (ch[i][1] + ch[i][5])) +
-                                      ((ch[i][2] + ch[i][6]) + (ch[i][3] + ch[i][7]));
-                    sc = dot * a.scale;
-                    if (Mh) sc = sc + Mh[static_cast<uint64_t>(qi) * sk + key];
-                }
-                W[r * RK + j] = sc;
             }
         }
-        __syncthreads();
 
-        // Softmax state per row: wave w takes rows w, w + 4, ...
-        for (int r = wave; r < static_cast<int>(nq); r += 4) {
-            const float sc = W[r * RK + lane];
+        // Softmax state and weights per row; p = 0 for a skipped row.
+        float p[RW], alpha[RW];
+        bool live[RW];
+        const uint32_t key = k0 + lane;
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            const uint32_t r = r0 + i, qi = q0 + r;
+            float sc = -__builtin_inff();
+            if (lane < static_cast<int>(kc) && r < nq && !(a.causal && key > qi + off)) {
+                const float dot = ((ch[i][0] + ch[i][4]) + (ch[i][1] + ch[i][5])) +
+                                  ((ch[i][2] + ch[i][6]) + (ch[i][3] + ch[i][7]));
+                sc = dot * a.scale;
+                if (Mh) sc = sc + Mh[static_cast<uint64_t>(qi) * sk + key];
+            }
             const float bmax = dev::wave_max(sc);
-            if (!isfinite(bmax)) {   // uniform over the wave
-                if (lane == 0) Sk[r] = 1.0f;
-                continue;
-            }
-            const float m = Ml[r];
-            const float nm = m < bmax ? bmax : m;
-            W[r * RK + lane] = dev::fast_expf_unfused(sc - nm);   // -inf scores give 0
-            if (lane == 0) {
-                const float alpha = dev::fast_expf_unfused(m - nm);
+            live[i] = isfinite(bmax);   // uniform over the wave
+            const float nm = m[i] < bmax ? bmax : m[i];
+            alpha[i] = live[i] ? dev::fast_expf_unfused(m[i] - nm) : 1.0f;
+            p[i] = live[i] ? dev::fast_expf_unfused(sc - nm) : 0.0f;   // -inf scores give 0
+            if (live[i]) m[i] = nm;
+            wrow[i * G::WP + lane] = p[i];
+        }
+        uint64_t nz[RW], all_nz = ~0ull;
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            nz[i] = __ballot(p[i] != 0.0f);
+            all_nz &= nz[i];
+        }
+        wave_sync_lds();
+        // Weight sums in key order, row r0 + lane by lane < RW.
+        if (lane < RW) {
+            float a_mine = alpha[0];
+            bool live_mine = live[0];
+#pragma unroll
+            for (int i = 1; i < RW; ++i)
+                if (lane == i) {
+                    a_mine = alpha[i];
+                    live_mine = live[i];
+                }
+            if (live_mine) {
+                const float *pr = wrow + lane * G::WP;
                 float psum = 0.0f;
-                for (uint32_t j = 0; j < kc; ++j) psum = psum + W[r * RK + j];
-                Ll[r] = Ll[r] * alpha + psum;
-                Ml[r] = nm;
-                Al[r] = alpha;
-                Sk[r] = 0.0f;
+                for (uint32_t j = 0; j < kc; j += 4) {
+                    const float4 w4 = *reinterpret_cast<const float4 *>(pr + j);
+                    psum = psum + w4.x;
+                    if (j + 1 < kc) psum = psum + w4.y;
+                    if (j + 2 < kc) psum = psum + w4.z;
+                    if (j + 3 < kc) psum = psum + w4.w;
+                }
+                l_mine = l_mine * a_mine + psum;
             }
         }
-        __syncthreads();
 
-        // Output accumulators.
-        if (QT > 1 || tid < D) {
-            const int ds = QT == 1 ? tid : lane, g = QT > 1 ? wave : 0;
+        // Output accumulators: acc = acc * alpha, then fma(v_j, p_j, acc) in key order.
 #pragma unroll
-            for (int i = 0; i < G::QPT; ++i) {
-                const int r = g * G::QPT + i;
-                if (r >= static_cast<int>(nq) || Sk[r] != 0.0f) continue;
-                const float alpha = Al[r];
+        for (int i = 0; i < RW; ++i)
+            if (live[i])
 #pragma unroll
-                for (int e = 0; e < G::DPT; ++e) acc[i][e] = acc[i][e] * alpha;
-                for (uint32_t j = 0; j < kc; ++j) {
-                    const float p = W[r * RK + j];
-                    if (p == 0.0f) continue;
+                for (int e = 0; e < DPT; ++e) acc[i][e] = acc[i][e] * alpha[i];
+        // Keys in groups of four (keys past kc have p = 0 and zero-filled V
+        // rows), the weights as broadcast reads of the LDS copy.  A group
+        // whose sixteen weights are all nonzero runs without a branch;
+        // otherwise each (row, key) tests its bit of the row's nonzero mask.
+        const float *vcol = Vs + lane * DPT;
+        for (uint32_t j = 0; j < kc; j += 4) {
+            float v[4][DPT];
 #pragma unroll
-                    for (int e = 0; e < G::DPT; ++e)
-                        acc[i][e] = fmaf(Vs[j * D + ds * G::DPT + e], p, acc[i][e]);
-                }
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int e = 0; e < DPT; ++e) v[t][e] = vcol[(j + t) * D + e];
+            float pw[RW][4];
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                const float4 w4 = *reinterpret_cast<const float4 *>(wrow + i * G::WP + j);
+                pw[i][0] = w4.x;
+                pw[i][1] = w4.y;
+                pw[i][2] = w4.z;
+                pw[i][3] = w4.w;
+            }
+            if (((all_nz >> j) & 15ull) == 15ull) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int i = 0; i < RW; ++i)
+#pragma unroll
+                        for (int e = 0; e < DPT; ++e) acc[i][e] = fmaf(v[t][e], pw[i][t], acc[i][e]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int i = 0; i < RW; ++i)
+                        if ((nz[i] >> (j + t)) & 1ull)
+#pragma unroll
+                            for (int e = 0; e < DPT; ++e) acc[i][e] = fmaf(v[t][e], pw[i][t], acc[i][e]);
             }
         }
     }
-    __syncthreads();
-    if (QT > 1 || tid < D) {
-        const int ds = QT == 1 ? tid : lane, g = QT > 1 ? wave : 0;
 #pragma unroll
-        for (int i = 0; i < G::QPT; ++i) {
-            const int r = g * G::QPT + i;
-            if (r >= static_cast<int>(nq)) continue;
-            const float l = Ll[r];
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            float *o = a.O + (bh * sq + q0 + r) * D + ds * G::DPT;
+    for (int i = 0; i < RW; ++i) {
+        const uint32_t r = r0 + i;
+        const float l = __uint_as_float(static_cast<uint32_t>(
+            __builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(l_mine)), i)));
+        if (r >= nq) continue;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        float *o = a.O + (bh * sq + q0 + r) * D + lane * DPT;
 #pragma unroll
-            for (int e = 0; e < G::DPT; ++e) o[e] = acc[i][e] * inv;
+        for (int e = 0; e < DPT; ++e) o[e] = acc[i][e] * inv;
+    }
+}
+
+// Reference-order decode (seq_q <= 4) for head_dim 64 or 128: one
+// workgroup of four waves per query row, the key blocks in a pipeline:
+//   waves 2-3 copy block t+1's K tile and block t's V tile from HBM straight
+//             into LDS (global_load_lds; the K tile at row pitch D + 4 floats,
+//             the pad slots take a dummy copy);
+//   wave 1    scores block t (lane j: key j's eight dot chains) and its
+//             softmax state: block max, m, alpha, the weights p_j (to LDS with
+//             alpha, a live flag and the nonzero mask) and, in lane 0, the
+//             weight sum in key order and l;
+//   wave 0    accumulates block t-1: acc = acc * alpha, then fma(v_j, p_j, acc)
+//             in key order for the nonzero p_j (lane owns D / 64 elements).
+// One barrier per step; two K and two V tiles alternate.  The scores and the
+// softmax state never wait for the output chain, so the chain of one row is
+// the only sequential work.
+template <int D>
+struct ExactDec {
+    static constexpr int P = D + 4;                     // K row pitch (floats)
+    static constexpr int KI = RK * (D / 4 + 1) / 64;    // 16-byte wave copies per K tile (with pads)
+    static constexpr int VI = RK * D / 4 / 64;          // per V tile
+    static constexpr int DPT = D / 64;
+    static constexpr int WS = RK + 8;                   // weights, alpha, live, nonzero mask
+    static constexpr int kFloats = 2 * RK * P + 2 * RK * D + D + 2 * WS + 4;
+    static constexpr size_t kLds = static_cast<size_t>(kFloats) * sizeof(float);
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_exact_decode_kernel(Attn a)
+{
+#pragma clang fp contract(off)
+    using G = ExactDec<D>;
+    constexpr int DPT = G::DPT;
+    extern __shared__ float4 sm4[];
+    float *Kt = reinterpret_cast<float *>(sm4);   // [2][64][P]
+    float *Vt = Kt + 2 * RK * G::P;                // [2][64][D]
+    float *Qs = Vt + 2 * RK * D;                   // [D]
+    float *Wr = Qs + D;                            // [2][WS]
+    float *Lf = Wr + 2 * G::WS;                    // the row's final l
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: the copies' LDS bases are scalar
+    const uint64_t bh = blockIdx.y;
+    const uint32_t sq = a.seq_q, sk = a.seq_k, qi = blockIdx.x;
+    const uint32_t off = sk > sq ? sk - sq : 0;
+    const uint64_t row = bh * sq + qi;
+    const float *Kh = a.K + bh * sk * D;
+    const float *Vh = a.V + bh * sk * D;
+    const float *Mr = a.mask ? a.mask + row * sk : nullptr;
+    uint32_t kend = sk;
+    if (a.causal) kend = min(sk, qi + off + 1);
+    const uint32_t nblk = (kend + RK - 1) / RK;
+
+    for (int i = tid; i < D; i += kThreads) Qs[i] = a.Q[row * D + i];
+    if (tid == 0) *Lf = 0.0f;
+
+    // Copies by waves 2 and 3: wave copy i covers 16-byte slots 64 i .. 64 i + 63.
+    auto copy_k = [&](uint32_t b) {
+        int8_t *dst = reinterpret_cast<int8_t *>(Kt + (b & 1) * RK * G::P);
+        for (int i = wave - 2; i < G::KI; i += 2) {
+            const uint32_t sl = static_cast<uint32_t>(i) * 64 + lane;
+            const uint32_t r = sl / (D / 4 + 1), c = sl % (D / 4 + 1);
+            const uint32_t key = min(b * RK + r, kend - 1);
+            lds::dma16(Kh + static_cast<uint64_t>(key) * D + (c < D / 4 ? 4 * c : 0), dst + i * 1024);
         }
+    };
+    auto copy_v = [&](uint32_t b) {
+        int8_t *dst = reinterpret_cast<int8_t *>(Vt + (b & 1) * RK * D);
+        for (int i = wave - 2; i < G::VI; i += 2) {
+            const uint32_t sl = static_cast<uint32_t>(i) * 64 + lane;
+            const uint32_t key = min(b * RK + sl / (D / 4), kend - 1);
+            lds::dma16(Vh + static_cast<uint64_t>(key) * D + 4 * (sl % (D / 4)), dst + i * 1024);
+        }
+    };
+    if (wave >= 2 && nblk) {
+        copy_k(0);
+        lds::wait_vmcnt<0>();
+    }
+    __syncthreads();
+
+    float m = -__builtin_inff(), l = 0.0f;   // wave 1 (l in lane 0)
+    float acc[DPT];                          // wave 0
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) acc[e] = 0.0f;
+
+    for (uint32_t t = 0; t <= nblk; ++t) {
+        if (wave >= 2) {
+            if (t + 1 < nblk) copy_k(t + 1);
+            if (t < nblk) copy_v(t);
+            lds::wait_vmcnt<0>();
+        } else if (wave == 1 && t < nblk) {
+            const uint32_t k0 = t * RK, kc = min(static_cast<uint32_t>(RK), kend - k0);
+            const float *kr = Kt + (t & 1) * RK * G::P + lane * G::P;
+            float ch[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+            for (int d = 0; d < D; d += 8) {
+                const float4 ka = *reinterpret_cast<const float4 *>(kr + d);
+                const float4 kb = *reinterpret_cast<const float4 *>(kr + d + 4);
+                const float4 qa = *reinterpret_cast<const float4 *>(Qs + d);
+                const float4 qb = *reinterpret_cast<const float4 *>(Qs + d + 4);
+                ch[0] = fmaf(qa.x, ka.x, ch[0]);
+                ch[1] = fmaf(qa.y, ka.y, ch[1]);
+                ch[2] = fmaf(qa.z, ka.z, ch[2]);
+                ch[3] = fmaf(qa.w, ka.w, ch[3]);
+                ch[4] = fmaf(qb.x, kb.x, ch[4]);
+                ch[5] = fmaf(qb.y, kb.y, ch[5]);
+                ch[6] = fmaf(qb.z, kb.z, ch[6]);
+                ch[7] = fmaf(qb.w, kb.w, ch[7]);
+            }
+            float sc = -__builtin_inff();
+            if (lane < static_cast<int>(kc)) {
+                const float dot = ((ch[0] + ch[4]) + (ch[1] + ch[5])) + ((ch[2] + ch[6]) + (ch[3] + ch[7]));
+                sc = dot * a.scale;
+                if (Mr) sc = sc + Mr[k0 + lane];
+            }
+            const float bmax = dev::wave_max(sc);
+            const bool live = isfinite(bmax);   // uniform over the wave
+            float p = 0.0f, alpha = 1.0f;
+            if (live) {
+                const float nm = m < bmax ? bmax : m;
+                alpha = dev::fast_expf_unfused(m - nm);
+                p = dev::fast_expf_unfused(sc - nm);   // -inf scores give 0
+                m = nm;
+            }
+            float *w = Wr + (t & 1) * G::WS;
+            w[lane] = p;
+            const uint64_t nz = __ballot(p != 0.0f);
+            if (lane == 0) {
+                w[RK] = alpha;
+                w[RK + 1] = live ? 1.0f : 0.0f;
+                w[RK + 2] = __uint_as_float(static_cast<uint32_t>(nz));
+                w[RK + 3] = __uint_as_float(static_cast<uint32_t>(nz >> 32));
+            }
+            wave_sync_lds();
+            if (lane == 0) {
+                if (live) {
+                    float psum = 0.0f;
+                    for (uint32_t j = 0; j < kc; j += 4) {
+                        const float4 w4 = *reinterpret_cast<const float4 *>(w + j);
+                        psum = psum + w4.x;
+                        if (j + 1 < kc) psum = psum + w4.y;
+                        if (j + 2 < kc) psum = psum + w4.z;
+                        if (j + 3 < kc) psum = psum + w4.w;
+                    }
+                    l = l * alpha + psum;
+                }
+                if (t + 1 == nblk) *Lf = l;
+            }
+        } else if (wave == 0 && t >= 1) {
+            const uint32_t b = t - 1, kc = min(static_cast<uint32_t>(RK), kend - b * RK);
+            const float *w = Wr + (b & 1) * G::WS;
+            const uint32_t live = __builtin_amdgcn_readfirstlane(static_cast<int>(__float_as_uint(w[RK + 1])));
+            if (live) {
+                const float alpha = __uint_as_float(static_cast<uint32_t>(
+                    __builtin_amdgcn_readfirstlane(static_cast<int>(__float_as_uint(w[RK])))));
+                const uint64_t nz =
+                    static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+                        static_cast<int>(__float_as_uint(w[RK + 2]))))) |
+                    (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+                         static_cast<int>(__float_as_uint(w[RK + 3]))))) << 32);
+#pragma unroll
+                for (int e = 0; e < DPT; ++e) acc[e] = acc[e] * alpha;
+                const float *vcol = Vt + (b & 1) * RK * D + lane * DPT;
+                for (uint32_t j = 0; j < kc; j += 4) {
+                    float v[4][DPT];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+#pragma unroll
+                        for (int e = 0; e < DPT; ++e) v[u][e] = vcol[(j + u) * D + e];
+                    const float4 w4 = *reinterpret_cast<const float4 *>(w + j);
+                    const float pj[4] = {w4.x, w4.y, w4.z, w4.w};
+                    if (((nz >> j) & 15ull) == 15ull) {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+#pragma unroll
+                            for (int e = 0; e < DPT; ++e) acc[e] = fmaf(v[u][e], pj[u], acc[e]);
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            if ((nz >> (j + u)) & 1ull)
+#pragma unroll
+                                for (int e = 0; e < DPT; ++e) acc[e] = fmaf(v[u][e], pj[u], acc[e]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (wave == 0) {
+        const float lf = *Lf;
+        const float inv = lf > 0.0f ? 1.0f / lf : 0.0f;
+        float *o = a.O + row * D + lane * DPT;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) o[e] = acc[e] * inv;
     }
 }
 
@@ -1264,25 +1508,38 @@ size_t attention_ws_bytes(const Attn &a)
     return static_cast<size_t>(splits) * rows * (a.head_dim + 2) * sizeof(float);
 }
 
-template <int QT, int D>
-void launch_exact(hipStream_t s, const Attn &a)
+template <int D>
+void launch_exact_rows(hipStream_t s, const Attn &a)
 {
-    using G = ExactCfg<QT, D>;
+    using G = ExactRows<D>;
     static std::atomic<bool> lds_optin{false};
     if (!lds_optin && G::kLds > 65536)
-        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_exact_kernel<QT, D>),
+        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_exact_rows_kernel<D>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                         static_cast<int>(G::kLds)) == hipSuccess;
-    const dim3 grid((a.seq_q + QT - 1) / QT, a.batch * a.heads);
-    attn_exact_kernel<QT, D><<<grid, kThreads, G::kLds, s>>>(a);
+    const dim3 grid((a.seq_q + G::QT - 1) / G::QT, a.batch * a.heads);
+    attn_exact_rows_kernel<D><<<grid, kThreads, G::kLds, s>>>(a);
+}
+
+template <int D>
+void launch_exact_decode(hipStream_t s, const Attn &a)
+{
+    using G = ExactDec<D>;
+    static std::atomic<bool> lds_optin{false};
+    if (!lds_optin && G::kLds > 65536)
+        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_exact_decode_kernel<D>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(G::kLds)) == hipSuccess;
+    const dim3 grid(a.seq_q, a.batch * a.heads);
+    attn_exact_decode_kernel<D><<<grid, kThreads, G::kLds, s>>>(a);
 }
 
 void attention(hipStream_t s, const Attn &a, float *ws)
 {
     if (use_exact_tiled(a)) {
         const bool decode = a.seq_q <= 4;
-        if (a.head_dim == 128) decode ? launch_exact<1, 128>(s, a) : launch_exact<16, 128>(s, a);
-        else decode ? launch_exact<1, 64>(s, a) : launch_exact<16, 64>(s, a);
+        if (a.head_dim == 128) decode ? launch_exact_decode<128>(s, a) : launch_exact_rows<128>(s, a);
+        else decode ? launch_exact_decode<64>(s, a) : launch_exact_rows<64>(s, a);
         return;
     }
     if (use_rowwise(a)) {
