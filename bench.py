@@ -327,15 +327,21 @@ def bench_config5(s: Session, steps: int):
     M = K = N = 4096
     w = synth.normal("c5/W", (K, N), 0.02)
     keep = synth.bernoulli_mask("c5/tiles", (K // 64, N // 64), 0.5)
+
+    def packed_of(wf):
+        bw = s.upload(wf)
+        wq, ws = s.alloc(K * N), s.alloc(4 * N)
+        s.run(abi.OP_QUANTIZE_I8, X=bw, Y=wq, scales=ws, rows=K, cols=N, axis=abi.QUANT_PER_COLUMN)
+        s.free(bw)
+        pk = s.pack(wq, K, N, scales=ws)
+        s.free(wq)
+        s.free(ws)
+        return pk
+
+    dense_w = packed_of(w)   # the same weights unculled: the dense baseline of the same kernel family
     w *= np.kron(keep, np.ones((64, 64), np.uint8)).astype(np.float32)
-    bw = s.upload(w)
+    packed = packed_of(w)
     del w
-    wq, ws = s.alloc(K * N), s.alloc(4 * N)
-    s.run(abi.OP_QUANTIZE_I8, X=bw, Y=wq, scales=ws, rows=K, cols=N, axis=abi.QUANT_PER_COLUMN)
-    s.free(bw)
-    packed = s.pack(wq, K, N, scales=ws)
-    s.free(wq)
-    s.free(ws)
     x = synth.normal("c5/A", (M, K))
     bx = s.upload(x)
     a8, sa, c = s.alloc(M * K), s.alloc(4 * M), s.alloc(4 * M * N)
@@ -343,13 +349,17 @@ def bench_config5(s: Session, steps: int):
     s.free(bx)
     mk = lambda i: s.command(abi.OP_MATMUL_I8, id=i, A=a8, B=packed, scale_a=sa, C=c, M=M, K=K, N=N)
     _, gpu_ns = timed(s, mk, steps, 3)
+    mkd = lambda i: s.command(abi.OP_MATMUL_I8, id=i, A=a8, B=dense_w, scale_a=sa, C=c, M=M, K=K, N=N)
+    _, dense_ns = timed(s, mkd, steps, 3)
     s.release_packed(packed)
+    s.release_packed(dense_w)
     for b in (a8, sa, c):
         s.free(b)
     dense = 2.0 * M * K * N
     out = {"cull_i8_4096": {"kernel_us": gpu_ns / 1e3, "zero_tiles": int(keep.size - keep.sum()),
                             "dense_equiv_tops": dense / gpu_ns / 1e3,
-                            "useful_tops": dense * keep.mean() / gpu_ns / 1e3}}
+                            "useful_tops": dense * keep.mean() / gpu_ns / 1e3,
+                            "dense_weights_kernel_us": dense_ns / 1e3, "vs_dense": gpu_ns / dense_ns}}
     G, H, V = 4, 4096, 32000
     hid = s.upload(synth.normal("c5/hidden", (G, H)))
     wm = synth.normal("c5/mtp_W", (H, V), 0.02)

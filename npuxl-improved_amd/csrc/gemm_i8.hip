@@ -681,10 +681,20 @@ struct FragsW {
     v4i a[2][4], b[2][NB];
 };
 
-template <int TN>
 // ps[0] and ps[1]: up to two independent problems with the same M in one
 // grid (tiles_n0 and tiles_n1 column tiles; tiles_n1 = 0 for one problem),
 // so the tiles of both fill whole rounds of CUs together.
+// kSkip (one problem with a zero-block map): a 32-column MFMA tile whose two
+// 1 KiB weight blocks of a 64-deep k block are both all zero is not copied
+// into LDS for that k block, and its fragment reads all point at 16 zero
+// bytes (one broadcast read); the MFMAs run unchanged on the zeros.  No
+// branch enters the scheduled loop: skipping the MFMAs themselves behind
+// uniform branches, per MFMA or per group of four, measured slower than the
+// dense kernel (the joins of the branches cost waits that outweigh the
+// skipped work), and MFMAs on zero operands take the same cycles.  The map
+// is reduced once per workgroup to one byte per k block, bit q = MFMA column
+// tile q of the workgroup's TN columns.
+template <int TN, bool kSkip = false>
 __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t tiles_m, uint32_t tiles_n0,
                                                          uint32_t tiles_n1)
 {
@@ -710,6 +720,31 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t
     const uint32_t KS = p.K / SK;
     const uint64_t KTp = p.Kp >> 6;
 
+    // Zero map of this tile's columns: zmap[kt] bit q = column blocks
+    // n0/16 + 2q and + 2q + 1 both all zero in k block kt (blocks past the
+    // packed width count as zero: their results are never stored).
+    constexpr uint32_t kZeroOff = G::kLds;                 // 16 zero bytes (kSkip)
+    uint8_t *zmap = reinterpret_cast<uint8_t *>(smem + G::kLds + 16);
+    if (kSkip) {
+        if (tid == 0) *reinterpret_cast<v4i *>(smem + kZeroOff) = (v4i){0, 0, 0, 0};
+        for (uint32_t kt = tid; kt < 2 * KS; kt += kThreads) {
+            uint32_t bits = 0;
+#pragma unroll
+            for (int q = 0; q < TN / 32; ++q) {
+                const uint32_t nb = (n0 >> 4) + 2 * q;
+                const bool z0 = nb >= NT || p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] != 0;
+                const bool z1 = nb + 1 >= NT || p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb + 1] != 0;
+                bits |= (z0 && z1) ? (1u << q) : 0u;
+            }
+            zmap[kt] = static_cast<uint8_t>(bits);
+        }
+        __syncthreads();
+    }
+    // Zero bits of k block kt (uniform).
+    auto zbits = [&](uint32_t kt) -> uint32_t {
+        return kSkip ? static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(zmap[kt])) : 0u;
+    };
+
     // DMA: A instruction 8*wave + j copies rows 64*wave + 8j + l/8 (M is a
     // multiple of 256 here, so no row clamp); lane l fetches k chunk
     // (l%8) ^ ((row >> 1) & 7) = (l%8) ^ (l/16) ^ 4(j%2).  B block
@@ -721,13 +756,15 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t
     const uint32_t a_lo = q * p.lda + 16 * ((lane & 7) ^ (q >> 1));
     const uint32_t a_lo_odd = q * p.lda + 16 * ((lane & 7) ^ (q >> 1) ^ 4);
     const uint32_t b_lo = lane * 16;
-    auto issue_one = [&](uint32_t s, int k) {
+    // z16: zero bits of the stage's k blocks 2s (low byte) and 2s + 1.
+    auto issue_one = [&](uint32_t s, int k, uint32_t z16) {
         int8_t *st = smem + (s & 1) * G::kStageBytes;
         if (k < kALoads) {
             dma16_s(a_base + static_cast<uint64_t>(8 * k) * p.lda + s * SK, (k & 1) ? a_lo_odd : a_lo,
                     st + (wave * kALoads + k) * 1024);
         } else {
             const int bi = wave * G::kBLoads + (k - kALoads);
+            if (kSkip && ((z16 >> (8 * (bi & 1) + (bi >> 2))) & 1u)) return;   // block of a skipped tile
             const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
             dma16_s(p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + static_cast<uint64_t>(s) * 2048,
                     b_lo, st + kBOff + bi * 1024);
@@ -748,17 +785,28 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t
         for (int h = 0; h < 2; ++h)
             a_rd[hh][h] = (wm * 128 + (lane & 31)) * 128 +
                           (((4 * hh + 2 * h + (lane >> 5)) ^ (((lane & 31) >> 1) & 7)) << 4);
-    const uint32_t b_rd = kBOff + ((wn * (TN / 16) + 2 * sub) << 10) + (((lane >> 5) * 16 + (lane & 15)) << 4);
-    auto read_one = [&](uint32_t st, int hh, FragsW<NB> &f, int k) {
+    const uint32_t b_lane = ((2 * sub) << 10) + (((lane >> 5) * 16 + (lane & 15)) << 4);
+    const uint32_t b_rd = kBOff + ((wn * (TN / 16)) << 10) + b_lane;
+    // zw: this wave's zero bits (bit j = its MFMA column tile j) of the k
+    // block being read; a zero tile's fragment comes from the zero block.
+    auto read_one = [&](uint32_t st, int hh, FragsW<NB> &f, int k, uint32_t zw) {
         const int h = k / (4 + NB), r = k % (4 + NB);
         if (r >= 1 && r <= 4) {
             const int i = r - 1;
             f.a[h][i] = *reinterpret_cast<const v4i *>(smem + st + a_rd[hh][h] + i * 4096);
         } else {
             const int j = r == 0 ? 0 : r - 4;
-            f.b[h][j] = *reinterpret_cast<const v4i *>(smem + st + b_rd + j * 4096 + hh * 1024 + h * 512);
+            if (kSkip) {
+                // every lane of a zero tile reads the same 16 zero bytes (a
+                // broadcast read costs a fraction of a full fragment read)
+                const uint32_t at = ((zw >> j) & 1u) ? kZeroOff : st + b_rd + j * 4096 + hh * 1024 + h * 512;
+                f.b[h][j] = *reinterpret_cast<const v4i *>(smem + at);
+            } else {
+                f.b[h][j] = *reinterpret_cast<const v4i *>(smem + st + b_rd + j * 4096 + hh * 1024 + h * 512);
+            }
         }
     };
+    auto wave_bits = [&](uint32_t z8) { return (z8 >> (wn * NB)) & ((1u << NB) - 1u); };
 
     v16i acc[4][NB];
 #pragma unroll
@@ -778,50 +826,62 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t
     // Second half's side work: the stage s+2 DMA, one per MFMA slot, then the
     // next stage's half-0 reads spread over the remaining slots.
     constexpr int kTail = G::kMfma - G::kLoads;
-    auto side2 = [&](int k, uint32_t s, uint32_t nxt, FragsW<NB> &f, bool dma) {
-        if (dma && k < G::kLoads) issue_one(s, k);
+    auto side2 = [&](int k, uint32_t s, uint32_t z16, uint32_t nxt, uint32_t zw_nxt, FragsW<NB> &f, bool dma) {
+        if (dma && k < G::kLoads) issue_one(s, k, z16);
 #pragma unroll
         for (int r = 0; r < G::kReads; ++r)
-            if (G::kLoads + (r * kTail) / G::kReads == k) read_one(nxt, 0, f, r);
+            if (G::kLoads + (r * kTail) / G::kReads == k) read_one(nxt, 0, f, r, zw_nxt);
     };
+    auto stage_bits = [&](uint32_t s) { return kSkip ? (zbits(2 * s) | (zbits(2 * s + 1) << 8)) : 0u; };
 
     // Prologue: stages 0 and 1 in flight, wait for 0, read its first half.
+    uint32_t z_cur = stage_bits(0);
 #pragma unroll
-    for (int k = 0; k < G::kLoads; ++k) issue_one(0, k);
+    for (int k = 0; k < G::kLoads; ++k) issue_one(0, k, z_cur);
     if (KS > 1) {
+        const uint32_t z1 = stage_bits(1);
 #pragma unroll
-        for (int k = 0; k < G::kLoads; ++k) issue_one(1, k);
-        wait_vmcnt<G::kLoads>();
+        for (int k = 0; k < G::kLoads; ++k) issue_one(1, k, z1);
+        // With skipped copies stage 1 may hold fewer than kLoads in flight.
+        if (kSkip) wait_vmcnt<0>();
+        else wait_vmcnt<G::kLoads>();
     } else {
         wait_vmcnt<0>();
     }
     block_barrier();
     FragsW<NB> f0, f1;
 #pragma unroll
-    for (int k = 0; k < G::kReads; ++k) read_one(0, 0, f0, k);
+    for (int k = 0; k < G::kReads; ++k) read_one(0, 0, f0, k, wave_bits(z_cur & 0xffu));
 
     uint32_t s = 0;
     for (; s + 2 < KS; ++s) {
         const uint32_t cur = (s & 1) * G::kStageBytes, nxt = G::kStageBytes - cur;
+        const uint32_t z_nxt = stage_bits(s + 1), z_far = stage_bits(s + 2);
+        const uint32_t zw1 = wave_bits(z_cur >> 8);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k, zw1); });
         wait_vmcnt<0>();
         block_barrier();
-        mma(f1, [&](int k) { side2(k, s + 2, nxt, f0, true); });
+        mma(f1, [&](int k) { side2(k, s + 2, z_far, nxt, wave_bits(z_nxt & 0xffu), f0, true); });
+        z_cur = z_nxt;
     }
     if (s + 1 < KS) {
         const uint32_t cur = (s & 1) * G::kStageBytes, nxt = ((s + 1) & 1) * G::kStageBytes;
+        const uint32_t z_nxt = stage_bits(s + 1);
+        const uint32_t zw1 = wave_bits(z_cur >> 8);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k, zw1); });
         wait_vmcnt<0>();
         block_barrier();
-        mma(f1, [&](int k) { side2(k, 0, nxt, f0, false); });
+        mma(f1, [&](int k) { side2(k, 0, 0u, nxt, wave_bits(z_nxt & 0xffu), f0, false); });
+        z_cur = z_nxt;
         ++s;
     }
     {
         const uint32_t cur = (s & 1) * G::kStageBytes;
+        const uint32_t zw1 = wave_bits(z_cur >> 8);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k, zw1); });
         mma(f1, [](int) {});
     }
 
@@ -907,7 +967,7 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
                          (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64 &&
                          p.K <= 16384;
     const bool k128 = aligned && p.K % pipe128::SK == 0;
-    const bool wide_ok = k128 && !p.zero_blocks && p.M % wide::TM == 0;
+    const bool wide_ok = k128 && p.M % wide::TM == 0;
     const uint32_t wm_ = p.M / wide::TM;
     const uint32_t wn256 = (p.N + 255) / 256, wn192 = (p.N + 191) / 192;
     const uint32_t tm = (p.M + pipe::TM - 1) / pipe::TM;
@@ -940,20 +1000,33 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
                                    reinterpret_cast<const void *>(gemm_i8_k128w8<false>),
                                    reinterpret_cast<const void *>(gemm_i8_k128w8<true>),
                                    reinterpret_cast<const void *>(gemm_i8_wide<256>),
-                                   reinterpret_cast<const void *>(gemm_i8_wide<192>)})
+                                   reinterpret_cast<const void *>(gemm_i8_wide<192>),
+                                   reinterpret_cast<const void *>(gemm_i8_wide<256, true>),
+                                   reinterpret_cast<const void *>(gemm_i8_wide<192, true>)})
                 ok = ok && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                160 * 1024) == hipSuccess;
             lds_optin = ok;
         }
     }
+    // Sixteen zero bytes and the zero map's per-workgroup reduction sit after
+    // the wide kernel's LDS plan (one byte per 64-deep k block).
+    const size_t zmap = p.zero_blocks ? 16 + (p.K / 64 + 15) / 16 * 16 : 0;
     switch (v) {
     case kI8Wide:
-        gemm_i8_wide<256><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
-                                                                                   wn256, 0);
+        if (p.zero_blocks)
+            gemm_i8_wide<256, true><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds + zmap, s>>>(
+                I8GemmPair{{p, p}}, wm_, wn256, 0);
+        else
+            gemm_i8_wide<256><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
+                                                                                       wn256, 0);
         return;
     case kI8Wide192:
-        gemm_i8_wide<192><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
-                                                                                   wn192, 0);
+        if (p.zero_blocks)
+            gemm_i8_wide<192, true><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds + zmap, s>>>(
+                I8GemmPair{{p, p}}, wm_, wn192, 0);
+        else
+            gemm_i8_wide<192><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
+                                                                                       wn192, 0);
         return;
     case kI8Wave8:
         if (p.zero_blocks) {

@@ -216,6 +216,45 @@ def test_matmul_i8_zero_weight_blocks_skipped_exactly(gpu):
         assert np.array_equal(got.astype(np.int64), A[:m].astype(np.int64) @ B.astype(np.int64))
 
 
+def _zero_pattern(kind, K, N, rng):
+    """A weight mask of zero 1 KiB blocks (64 deep x 16 columns) or larger."""
+    if kind == "tiles64":        # the config-5 pattern: 64 x 64 tiles
+        keep = rng.integers(0, 2, size=(K // 64, -(-N // 64))).astype(bool)
+        return np.kron(keep, np.ones((64, 64), bool))[:, :N]
+    if kind == "blocks16":       # single 16-column blocks: pairs half zero
+        keep = rng.random((K // 64, -(-N // 16))) < 0.4
+        return np.kron(keep, np.ones((64, 16), bool))[:, :N]
+    keep = np.ones((K // 64, 1), bool)   # whole k blocks zero, every column
+    keep[rng.random(K // 64) < 0.5] = False
+    keep[0] = False
+    return np.kron(keep, np.ones((64, N), bool))
+
+
+@pytest.mark.parametrize("tiles", [(256, 128, 256), (256, 128, 192), (256, 128, 128), (128, 128, 64)])
+@pytest.mark.parametrize("K", [128, 384, 1024])
+@pytest.mark.parametrize("kind", ["tiles64", "blocks16", "kblocks"])
+def test_matmul_i8_zero_maps_every_kernel(gpu, tiles, K, kind):
+    """Weights with all-zero blocks on every prefill kernel a tile triple can
+    select (the last the automatic choice): the wide kernels skip the copy,
+    the fragment reads and the MFMAs of a 32-column tile whose two blocks of
+    a k block are zero, so partly zero tiles, whole zero stages, one and
+    several stages, and a ragged last tile must all stay exact."""
+    rng = np.random.default_rng(K * 7 + len(kind))
+    M, N = 512, 520
+    A = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = rng.integers(-128, 128, size=(K, N)).astype(np.int8)
+    B *= _zero_pattern(kind, K, N, rng).astype(np.int8)
+    w = gpu.pack(B, K, N)
+    info0 = gpu.info()
+    assert gpu.lib.vnpu_device_set_tiles(gpu.dev, *tiles) == abi.OK
+    try:
+        got = g.matmul_i8(gpu, A, w, M, K, N)
+    finally:
+        gpu.lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n)
+        gpu.release_packed(w)
+    assert np.array_equal(got.astype(np.int64), A.astype(np.int64) @ B.astype(np.int64))
+
+
 # ---------------------------------------------------------------- matmul_f32
 F32_CASES = [(37, 53, 29, 0, 0), (17, 41, 23, 0, 1), (9, 33, 18, 1, 0), (1, 512, 137, 0, 0),
              (4, 4096, 1000, 0, 0), (8, 300, 33, 0, 1), (64, 128, 64, 1, 1), (200, 300, 130, 0, 0),
