@@ -95,6 +95,16 @@ __device__ __forceinline__ float swiglu_avx2(float g, float u, float alpha)
     return (s * u) * alpha;
 }
 
+// The scalar tail of swiglu_avx2_range: silu() with the scalar fast_expf
+// inlined into the AVX2 function (Horner steps contracted, so dev::fast_expf;
+// no clamp: a gate below -80 gives exp = inf and s = -0), then (s*u)*alpha.
+__device__ __forceinline__ float swiglu_tail(float g, float u, float alpha)
+{
+#pragma clang fp contract(off)
+    const float s = g / (1.0f + fast_expf(-g));
+    return (s * u) * alpha;
+}
+
 // gelu_avx2_range (llm.cpp:308-330): inner = k0 * fma(k1, x^3, x),
 // t = 2 / (1 + exp256(-2 inner)) - 1, y = (0.5 x)(1 + t).
 __device__ __forceinline__ float gelu_avx2(float x)

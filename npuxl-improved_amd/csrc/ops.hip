@@ -346,28 +346,39 @@ __global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ 
 
 enum EwOp { EW_SWIGLU = 0, EW_ADD = 1, EW_MUL = 2, EW_GELU = 3 };
 
+// The reference's AVX2 builds (llm.cpp:256-330), rounding for rounding.  They
+// run 8-wide steps from the start of a range and the last count % 8 elements
+// in a scalar tail loop whose expressions contract differently (MUL:
+// fma(alpha*a, b, beta)) or use the scalar exp without the clamp (SWIGLU);
+// `tail` marks those elements (the elements from count - count % 8 on, the
+// reference's single range per command whenever its chunk size is a multiple
+// of 8).  ADD's tail contracts to the same fma and GELU's gives the same
+// values.
 template <int OP>
-__device__ __forceinline__ float ew(float a, float b, float alpha, float beta)
+__device__ __forceinline__ float ew(float a, float b, float alpha, float beta, bool tail)
 {
-    // the reference's AVX2 builds (llm.cpp:256-330), rounding for rounding
-    if (OP == EW_SWIGLU) return dev::swiglu_avx2(a, b, alpha);
+    if (OP == EW_SWIGLU) return tail ? dev::swiglu_tail(a, b, alpha) : dev::swiglu_avx2(a, b, alpha);
     if (OP == EW_ADD) return fmaf(a, alpha, dev::mul_rn(b, beta));
-    if (OP == EW_MUL) return fmaf(dev::mul_rn(a, b), alpha, beta);
+    if (OP == EW_MUL) return tail ? fmaf(dev::mul_rn(alpha, a), b, beta) : fmaf(dev::mul_rn(a, b), alpha, beta);
     return dev::gelu_avx2(a);
 }
+
+// First element of the reference's scalar tail for `count` elements.
+__host__ __device__ __forceinline__ uint64_t tail_start(uint64_t count) { return count - count % 8; }
 
 template <int OP>
 __global__ __launch_bounds__(kThreads) void ew_vec_kernel(const float4 *__restrict__ A,
                                                           const float4 *__restrict__ B,
                                                           float4 *__restrict__ Y, uint64_t n4,
-                                                          float alpha, float beta)
+                                                          float alpha, float beta, uint64_t t0)
 {
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4;
          i += static_cast<uint64_t>(gridDim.x) * kThreads) {
         const float4 a = A[i];
         const float4 b = (OP == EW_GELU) ? a : B[i];
-        Y[i] = make_float4(ew<OP>(a.x, b.x, alpha, beta), ew<OP>(a.y, b.y, alpha, beta),
-                           ew<OP>(a.z, b.z, alpha, beta), ew<OP>(a.w, b.w, alpha, beta));
+        const bool tail = 4 * i >= t0;   // the tail is 0 or 4 elements: whole float4s
+        Y[i] = make_float4(ew<OP>(a.x, b.x, alpha, beta, tail), ew<OP>(a.y, b.y, alpha, beta, tail),
+                           ew<OP>(a.z, b.z, alpha, beta, tail), ew<OP>(a.w, b.w, alpha, beta, tail));
     }
 }
 
@@ -377,9 +388,10 @@ __global__ __launch_bounds__(kThreads) void ew_kernel(const float *__restrict__ 
                                                       float *__restrict__ Y, uint64_t n,
                                                       float alpha, float beta)
 {
+    const uint64_t t0 = tail_start(n);
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
          i += static_cast<uint64_t>(gridDim.x) * kThreads)
-        Y[i] = ew<OP>(A[i], (OP == EW_GELU) ? 0.0f : B[i], alpha, beta);
+        Y[i] = ew<OP>(A[i], (OP == EW_GELU) ? 0.0f : B[i], alpha, beta, i >= t0);
 }
 
 template <int OP>
@@ -395,7 +407,7 @@ void launch_ew(hipStream_t s, const float *A, const float *B, float *Y, uint64_t
     if (vec)
         ew_vec_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(
             reinterpret_cast<const float4 *>(A), reinterpret_cast<const float4 *>(B),
-            reinterpret_cast<float4 *>(Y), n / 4, alpha, beta);
+            reinterpret_cast<float4 *>(Y), n / 4, alpha, beta, tail_start(n));
     else
         ew_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(A, B, Y, n, alpha, beta);
 }
@@ -507,12 +519,18 @@ __global__ __launch_bounds__(NT) void row_chain_kernel(RowChain p)
             b[i] = j < n4 ? reinterpret_cast<const float4 *>(p.B)[off + j] : zero;
         }
         constexpr int OP = PRE == kChainAdd ? EW_ADD : EW_SWIGLU;
+        // the elementwise command spans all rows: its tail is the last
+        // (rows * cols) % 8 elements of the buffer
+        const uint64_t t0 = tail_start(static_cast<uint64_t>(p.rows) * p.cols);
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const uint32_t j = threadIdx.x + i * NT;
             if (j >= n4) continue;
-            v[i] = make_float4(ew<OP>(v[i].x, b[i].x, p.alpha, p.beta), ew<OP>(v[i].y, b[i].y, p.alpha, p.beta),
-                               ew<OP>(v[i].z, b[i].z, p.alpha, p.beta), ew<OP>(v[i].w, b[i].w, p.alpha, p.beta));
+            const uint64_t e = 4 * (off + j);
+            v[i] = make_float4(ew<OP>(v[i].x, b[i].x, p.alpha, p.beta, e >= t0),
+                               ew<OP>(v[i].y, b[i].y, p.alpha, p.beta, e + 1 >= t0),
+                               ew<OP>(v[i].z, b[i].z, p.alpha, p.beta, e + 2 >= t0),
+                               ew<OP>(v[i].w, b[i].w, p.alpha, p.beta, e + 3 >= t0));
             reinterpret_cast<float4 *>(p.Y)[off + j] = v[i];
         }
     }

@@ -57,6 +57,7 @@ def lib() -> C.CDLL:
             "vo_swiglu_avx2": (None, [vp, vp, vp, u64, f32]),
             "vo_gelu_avx2": (None, [vp, vp, u64]),
             "vo_mul_avx2": (None, [vp, vp, vp, u64, f32, f32]),
+            "vo_add_avx2": (None, [vp, vp, vp, u64, f32, f32]),
             "vo_attention_avx2": (None, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32]),
         }
         for name, (res, args) in sig.items():
@@ -275,6 +276,14 @@ def mul_avx2(a, b, alpha=1.0, beta=0.0):
     a, b = _c(a, np.float32), _c(b, np.float32)
     Y = np.empty_like(a)
     lib().vo_mul_avx2(_p(a), _p(b), _p(Y), a.size, alpha, beta)
+    return Y
+
+
+def add_avx2(a, b, alpha=1.0, beta=1.0):
+    """ADD in the order of the reference's AVX2 build (bit for bit)."""
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    Y = np.empty_like(a)
+    lib().vo_add_avx2(_p(a), _p(b), _p(Y), a.size, alpha, beta)
     return Y
 
 

@@ -615,12 +615,39 @@ float vo_exp_avx2(float x)
 /* swiglu_avx2_range (llm.cpp:289-306): s = g / (1 + exp256(-g)),
  * y = (s*u)*alpha; the scalar tail of a thread's range uses silu with the
  * same FMA polynomial (its AVX2 function contracts it). */
+/* The scalar fast_expf (internal.h:87-110) as inlined into the reference's
+ * AVX2-target functions: the Horner steps contract to FMAs; x beyond
+ * [-80, 80] gives 0 or +inf (no clamp to the bound). */
+static float vo_fast_expf_fma(float x)
+{
+    if (x < -80.0f) return 0.0f;
+    if (x > 80.0f) return INFINITY;
+    float z = x * 1.4426950408889634f;
+    float zi = floorf(z);
+    float f = z - zi;
+    float p = fmaf(0.0013333558146428443f, f, 0.009618129107628477f);
+    p = fmaf(p, f, 0.05550410866482158f);
+    p = fmaf(p, f, 0.2402265069591007f);
+    p = fmaf(p, f, 0.6931471805599453f);
+    p = fmaf(p, f, 1.0f);
+    return ldexpf(p, (int)zi);
+}
+
+/* The elementwise AVX2 ranges run 8-wide steps from the start of a range and
+ * the last count % 8 elements in their scalar tail loop (one range per
+ * command while the reference's chunk size, max(4096, count / (4 threads)),
+ * is a multiple of 8). */
+static uint64_t vo_tail_start(uint64_t count) { return count - count % 8; }
+
 void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha)
 {
     float a = alpha == 0.0f ? 1.0f : alpha;
+    const uint64_t t0 = vo_tail_start(count);
     for (uint64_t i = 0; i < count; ++i) {
         float g = gate[i];
-        float s = g / (1.0f + vo_exp_avx2(-g));
+        /* vector: exp256_ps clamps to [-80, 80]; tail: silu() with the
+         * scalar fast_expf (llm.cpp:240-246 inlined into swiglu_avx2_range) */
+        float s = g / (1.0f + (i < t0 ? vo_exp_avx2(-g) : vo_fast_expf_fma(-g)));
         Y[i] = (s * up[i]) * a;
     }
 }
@@ -639,11 +666,23 @@ void vo_gelu_avx2(const float *X, float *Y, uint64_t count)
     }
 }
 
-/* mul_avx2_range (llm.cpp:273-287): y = fma(a*b, alpha, beta). */
+/* mul_avx2_range (llm.cpp:273-287): y = fma(a*b, alpha, beta) in the 8-wide
+ * steps; the tail's alpha * a * b + beta contracts to fma(alpha*a, b, beta). */
 void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta)
 {
     float a = alpha == 0.0f ? 1.0f : alpha;
-    for (uint64_t i = 0; i < count; ++i) Y[i] = fmaf(A[i] * B[i], a, beta);
+    const uint64_t t0 = vo_tail_start(count);
+    for (uint64_t i = 0; i < count; ++i)
+        Y[i] = i < t0 ? fmaf(A[i] * B[i], a, beta) : fmaf(a * A[i], B[i], beta);
+}
+
+/* add_avx2_range (llm.cpp:256-271): y = fma(a, alpha, b*beta); the tail's
+ * alpha * a + beta * b contracts to the same fma. */
+void vo_add_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta)
+{
+    float al = (alpha == 0.0f && beta == 0.0f) ? 1.0f : alpha;
+    float be = (alpha == 0.0f && beta == 0.0f) ? 1.0f : beta;
+    for (uint64_t i = 0; i < count; ++i) Y[i] = fmaf(A[i], al, B[i] * be);
 }
 
 /* dot_avx2 (llm.cpp:332-343): eight FMA chains over 8-wide steps, hsum256,

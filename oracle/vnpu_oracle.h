@@ -75,6 +75,7 @@ void vo_rmsnorm_avx2(const float *X, const float *W, float *Y, uint32_t rows, ui
 float vo_exp_avx2(float x);
 void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha);
 void vo_gelu_avx2(const float *X, float *Y, uint64_t count);
+void vo_add_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta);
 void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta);
 void vo_attention_avx2(const float *Q, const float *K, const float *V, const float *mask, float *O,
                        uint32_t batch, uint32_t heads, uint32_t seq_q, uint32_t seq_k,

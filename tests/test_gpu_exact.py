@@ -36,16 +36,20 @@ def test_rmsnorm_bit_exact(gpu, rows, cols):
     assert bits(g.unary_rows(gpu, abi.OP_RMSNORM_F32, X, eps=0.0), oracle.rmsnorm_avx2(X, None, 1e-5))
 
 
-@pytest.mark.parametrize("n", [1, 1001, 4096 * 8 + 4, 2048 * 11008])
+@pytest.mark.parametrize("n", [1, 7, 1001, 4096 * 8 + 4, 4103, 2048 * 11008])
 def test_elementwise_bit_exact(gpu, n):
+    """Vector kernel (n % 4 == 0) and scalar kernel, with the reference's
+    scalar tail (last n % 8 elements) and exp's clamp edges in both parts."""
     a = (RNG.standard_normal(n) * 4).astype(np.float32)
     b = RNG.standard_normal(n).astype(np.float32)
-    a[: min(n, 3)] = [90.0, -95.0, 0.0][: min(n, 3)]   # outside exp's clamp, and zero
-    assert bits(g.elementwise(gpu, abi.OP_SWIGLU_F32, a, b, alpha=0.0), oracle.swiglu_avx2(a, b, 1.0))
-    assert bits(g.elementwise(gpu, abi.OP_SWIGLU_F32, a, b, alpha=0.75), oracle.swiglu_avx2(a, b, 0.75))
+    edges = np.array([90.0, -95.0, 0.0, -0.0, -80.5, -88.0], np.float32)   # outside exp's clamp, zeros
+    a[: min(n, 3)] = edges[: min(n, 3)]
+    a[-min(n, 3):] = edges[-min(n, 3):]
+    for al, be in ((0.0, 0.0), (0.75, 0.25), (-1.5, 2.0)):
+        assert bits(g.elementwise(gpu, abi.OP_SWIGLU_F32, a, b, alpha=al), oracle.swiglu_avx2(a, b, al or 1.0))
+        assert bits(g.elementwise(gpu, abi.OP_ADD_F32, a, b, al, be), oracle.add_avx2(a, b, al, be))
+        assert bits(g.elementwise(gpu, abi.OP_MUL_F32, a, b, al, be), oracle.mul_avx2(a, b, al or 1.0, be))
     assert bits(g.elementwise(gpu, abi.OP_GELU_F32, a), oracle.gelu_avx2(a))
-    assert bits(g.elementwise(gpu, abi.OP_ADD_F32, a, b, 0.0, 0.0), oracle.add(a, b, 1.0, 1.0))
-    assert bits(g.elementwise(gpu, abi.OP_MUL_F32, a, b, 0.0, 0.25), oracle.mul_avx2(a, b, 1.0, 0.25))
 
 
 @pytest.mark.parametrize("interleaved", [0, 1])

@@ -235,14 +235,22 @@ def test_rmsnorm_avx2_order_bit_exact(ref, rows, cols):
     assert _bits(g.unary_rows(ref, abi.OP_RMSNORM_F32, X, eps=0.0), oracle.rmsnorm_avx2(X, None, 1e-5))
 
 
-@pytest.mark.parametrize("n", [8, 1001, 100000, 2048 * 11008 // 32])
-def test_swiglu_gelu_avx2_order_bit_exact(ref, n):
+@pytest.mark.parametrize("n", [3, 8, 1001, 4103, 16384, 2048 * 11008 // 32])
+def test_elementwise_avx2_order_bit_exact(ref, n):
+    """SWIGLU, GELU, ADD and MUL: 8-wide steps, then the last n % 8 elements in
+    the scalar tail (MUL contracts differently there, SWIGLU's exp is not
+    clamped there).  Sizes keep the reference's range partition to one range
+    (chunks of max(4096, n / 16) at 4 threads are multiples of 8)."""
     a = (RNG.standard_normal(n) * 4).astype(np.float32)
     b = RNG.standard_normal(n).astype(np.float32)
-    assert _bits(g.elementwise(ref, abi.OP_SWIGLU_F32, a, b, alpha=0.0), oracle.swiglu_avx2(a, b, 1.0))
-    assert _bits(g.elementwise(ref, abi.OP_SWIGLU_F32, a, b, alpha=0.5), oracle.swiglu_avx2(a, b, 0.5))
+    edges = np.array([90.0, -90.0, 80.0, -80.0, 80.5, -80.5, 0.0, -0.0, -88.0, -87.5], np.float32)   # exp's clamp
+    a[: min(n, 8)] = edges[: min(n, 8)]
+    a[-min(n, 3):] = edges[-min(n, 3):]   # the scalar tail too
+    for al, be in ((0.0, 0.0), (0.5, 0.25), (-1.75, 3.0)):
+        assert _bits(g.elementwise(ref, abi.OP_SWIGLU_F32, a, b, alpha=al), oracle.swiglu_avx2(a, b, al or 1.0))
+        assert _bits(g.elementwise(ref, abi.OP_ADD_F32, a, b, al, be), oracle.add_avx2(a, b, al, be))
+        assert _bits(g.elementwise(ref, abi.OP_MUL_F32, a, b, al, be), oracle.mul_avx2(a, b, al or 1.0, be))
     assert _bits(g.elementwise(ref, abi.OP_GELU_F32, a), oracle.gelu_avx2(a))
-    assert _bits(g.elementwise(ref, abi.OP_ADD_F32, a, b, 0.0, 0.0), oracle.add(a, b, 1.0, 1.0))
 
 
 def test_rope_bit_exact(ref):
