@@ -141,6 +141,28 @@ hipEvent_t vnpu_stream::acquire_event()
     return e;
 }
 
+void vnpu_stream::open_period()
+{
+    if (period_start) return;
+    period_start = acquire_event();
+    if (period_start) (void)hipEventRecord(period_start, hip);
+    period_batches = 0;
+}
+
+void vnpu_stream::close_period()
+{
+    if (!period_start) return;
+    hipEvent_t stop = acquire_event();
+    if (stop) {
+        (void)hipEventRecord(stop, hip);
+        batch_timing.emplace_back(period_start, stop);
+    } else {
+        event_pool.push_back(period_start);
+    }
+    period_start = nullptr;
+    period_batches = 0;
+}
+
 void vnpu_stream::resolve_timing(bool wait_all)
 {
     size_t keep = 0;
@@ -456,6 +478,7 @@ static void destroy_stream_obj(vnpu_stream_t *s)
 {
     if (!s) return;
     if (s->hip) {
+        s->close_period();
         (void)hipStreamSynchronize(s->hip);
         s->resolve_timing(true);
         (void)hipStreamDestroy(s->hip);
@@ -741,6 +764,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_sync(vnpu_stream_t *stream)
     {
         std::lock_guard<std::mutex> lock(stream->mutex);
         (void)hipSetDevice(stream->device->hip_device);
+        stream->close_period();
         e = hipStreamSynchronize(stream->hip);
         if (e == hipSuccess) stream->resolve_timing(true);
     }
@@ -786,8 +810,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
         d->busy.fetch_add(1);
         d->active_workers.fetch_add(1);
         if (stream->batch_timing.size() >= 256) stream->resolve_timing(false);
-        hipEvent_t batch_start = stream->acquire_event();
-        if (batch_start) (void)hipEventRecord(batch_start, stream->hip);
+        stream->open_period();
         auto account = [&](const ExecStats &st, uint64_t host) {
             d->dispatch_ns.fetch_add(host);
             d->bytes_read.fetch_add(st.bytes_read);
@@ -909,15 +932,7 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
             }
             if (rc != VNPU_OK) fail(rc);
         }
-        if (batch_start) {
-            hipEvent_t batch_stop = stream->acquire_event();
-            if (batch_stop) {
-                (void)hipEventRecord(batch_stop, stream->hip);
-                stream->batch_timing.emplace_back(batch_start, batch_stop);
-            } else {
-                stream->event_pool.push_back(batch_start);
-            }
-        }
+        if (++stream->period_batches >= 256) stream->close_period();
         if (event) {
             std::lock_guard<std::mutex> el(event->mutex);
             if (event->hip && event->hip_device != d->hip_device) {

@@ -130,12 +130,19 @@ struct vnpu_stream {
     void *workspace = nullptr;
     size_t workspace_bytes = 0;
     void *ensure_workspace(size_t bytes);
-    // GPU time of submitted batches: one hipEvent pair per batch, recorded on
-    // the stream and folded into the device's kernel time once complete.
-    // Guarded by mutex.
+    // GPU time of submitted work by busy periods: a timing event is recorded
+    // before the first batch after a synchronization and another when the
+    // period closes (stream sync, stream destruction, every 256 batches);
+    // closed pairs are folded into the device's kernel time once complete.
+    // Every event record on a stream costs the next kernel ~3 us of start
+    // latency, so a pair per batch would tax every batch.  Guarded by mutex.
     std::vector<std::pair<hipEvent_t, hipEvent_t>> batch_timing;
     std::vector<hipEvent_t> event_pool;
+    hipEvent_t period_start = nullptr;
+    uint32_t period_batches = 0;
     hipEvent_t acquire_event();
+    void open_period();
+    void close_period();
     void resolve_timing(bool wait_all);   // adds finished pairs to kernel_ns
 };
 
