@@ -252,18 +252,26 @@ extern "C" vnpu_status_t vnpu_block_run(const vnpu_backend_v1_t *api, vnpu_strea
     att.args.attention.head_dim = D;
     att.args.attention.causal = 1;
     cmds.push_back(att);
-    if (!submit(cmds)) return rc;
-    if (hs) {
-        const uint64_t n4 = rd / 4;
-        merge_heads_kernel<<<dim3(blocks_for(n4)), 256, 0, hs>>>(
-            reinterpret_cast<const float4 *>(b->o), reinterpret_cast<float4 *>(b->att), T, H, D, n4);
-        if (!launched()) return rc;
+    // One token per sequence: [B][H][1][D] is already the token-major
+    // [B][H*D] layout, so the O projection reads the attention output as is.
+    const float *att_rows = b->att;
+    if (T == 1) {
+        att_rows = b->o;
     } else {
-        merge_heads_host(b->o, b->att, rows, T, H, D);
+        if (!submit(cmds)) return rc;
+        if (hs) {
+            const uint64_t n4 = rd / 4;
+            merge_heads_kernel<<<dim3(blocks_for(n4)), 256, 0, hs>>>(
+                reinterpret_cast<const float4 *>(b->o), reinterpret_cast<float4 *>(b->att), T, H, D, n4);
+            if (!launched()) return rc;
+        } else {
+            merge_heads_host(b->o, b->att, rows, T, H, D);
+        }
     }
 
-    // Batch 4: O projection + residual, FFN RMSNorm, gate/up, SwiGLU, down + residual.
-    gemm_i8(cmds, b->att, b->a8, b->scale_a, w->o, b->proj, rows, d, d, true);
+    // Batch 4 (with the attention when T = 1): O projection + residual, FFN
+    // RMSNorm, gate/up, SwiGLU, down + residual.
+    gemm_i8(cmds, att_rows, b->a8, b->scale_a, w->o, b->proj, rows, d, d, true);
     cmds.push_back(add(b->x, b->proj, b->x, rd));
     cmds.push_back(rmsnorm(b->x, w->norm_ffn, b->xn, rows, d, cfg->eps));
     gemm_i8(cmds, b->xn, b->a8, b->scale_a, w->gate, b->gate, rows, d, F, true);

@@ -55,24 +55,53 @@ __device__ __forceinline__ float block_max(float v, float *red)
 // across workgroups.  kChainFloats bounds the LDS staging of one pass.
 constexpr uint32_t kChainFloats = 12288;
 
-// Eight chain lanes accumulate row[0 .. n) (n a multiple of 8, staged in LDS)
-// into acc; call with every thread, between barriers.
-__device__ __forceinline__ void chain_sumsq(const float *row, uint32_t n, float &acc)
+// The row's 8-wide part is staged in LDS chain-major: element e at
+// (e % 8) * P + e / 8, so chain c is one contiguous run its lane reads with
+// 16-byte loads.  P = chain_pitch(elements per chain) is a multiple of 4,
+// and P = 4 (mod 64) puts the eight lanes' reads of one step in distinct
+// 16-byte bank slots.
+__host__ __device__ constexpr uint32_t chain_pitch(uint32_t len) { return (len + 63) / 64 * 64 + 4; }
+// Floats of LDS for a row of `cols`: the chain-major part plus the tail.
+__host__ __device__ constexpr uint32_t chain_floats(uint32_t cols)
+{
+    return 8 * chain_pitch((cols & ~7u) / 8) + 8;
+}
+
+// Elements e0 .. e0+3 (e0 a multiple of 4) of the 8-wide part.
+__device__ __forceinline__ void chain_put4(float *rowt, uint32_t P, uint32_t e0, float4 v)
+{
+    const uint32_t c = e0 & 4u, s = e0 >> 3;
+    rowt[c * P + s] = v.x;
+    rowt[(c + 1) * P + s] = v.y;
+    rowt[(c + 2) * P + s] = v.z;
+    rowt[(c + 3) * P + s] = v.w;
+}
+
+// Eight chain lanes accumulate len elements each (chain c at rowt + c * P)
+// into acc in element order; the next four are in flight while four are
+// summed.  Call with every thread, between barriers.
+__device__ __forceinline__ void chain_sumsq(const float *rowt, uint32_t P, uint32_t len, float &acc)
 {
     const uint32_t c = threadIdx.x;
     if (c >= 8) return;
-    uint32_t s = 0;
-    for (; s + 8 <= n / 8; s += 8) {
-        float x[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = row[(s + u) * 8 + c];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc = fmaf(x[u], x[u], acc);
+    const float *r = rowt + c * P;
+    const uint32_t n4 = len / 4;
+    if (n4) {
+        float4 cur = *reinterpret_cast<const float4 *>(r);
+        for (uint32_t i = 1; i < n4; ++i) {
+            const float4 nxt = *reinterpret_cast<const float4 *>(r + 4 * i);
+            acc = fmaf(cur.x, cur.x, acc);
+            acc = fmaf(cur.y, cur.y, acc);
+            acc = fmaf(cur.z, cur.z, acc);
+            acc = fmaf(cur.w, cur.w, acc);
+            cur = nxt;
+        }
+        acc = fmaf(cur.x, cur.x, acc);
+        acc = fmaf(cur.y, cur.y, acc);
+        acc = fmaf(cur.z, cur.z, acc);
+        acc = fmaf(cur.w, cur.w, acc);
     }
-    for (; s < n / 8; ++s) {
-        const float x = row[s * 8 + c];
-        acc = fmaf(x, x, acc);
-    }
+    for (uint32_t i = 4 * n4; i < len; ++i) acc = fmaf(r[i], r[i], acc);
 }
 
 // Combines the chain sums (red8, written by lanes 0..7) and the tail
@@ -104,7 +133,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
                                                            float *__restrict__ Y, uint32_t cols,
                                                            float eps)
 {
-    extern __shared__ float row_lds[];   // min(cols, kChainFloats) floats
+    extern __shared__ float row_lds[];   // chain_floats(min(cols, kChainFloats)) floats
     __shared__ float red8[8];
     const uint64_t r = blockIdx.x;
     const float *x = X + r * cols;
@@ -112,11 +141,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
     const uint32_t cols8 = cols & ~7u;
     float acc = 0.0f;
     for (uint32_t c0 = 0; c0 < cols8; c0 += kChainFloats) {
-        const uint32_t n = min(kChainFloats, cols8 - c0);
+        const uint32_t n = min(kChainFloats, cols8 - c0), P = chain_pitch(n / 8);
         __syncthreads();
-        for (uint32_t j = threadIdx.x; j < n; j += kThreads) row_lds[j] = x[c0 + j];
+        for (uint32_t j = threadIdx.x; j < n; j += kThreads) row_lds[(j & 7u) * P + (j >> 3)] = x[c0 + j];
         __syncthreads();
-        chain_sumsq(row_lds, n, acc);
+        chain_sumsq(row_lds, P, n / 8, acc);
     }
     __syncthreads();
     if (threadIdx.x < 8) red8[threadIdx.x] = acc;
@@ -134,27 +163,30 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_reg_kernel(const float *__re
                                                                float *__restrict__ Y, uint32_t cols,
                                                                float eps)
 {
-    extern __shared__ float4 row4[];   // cols floats
+    extern __shared__ float4 row4[];   // chain_floats(cols) floats
     __shared__ float red8[8];
     const uint64_t r = blockIdx.x;
     const float4 *x = reinterpret_cast<const float4 *>(X + r * cols);
     float4 *y = reinterpret_cast<float4 *>(Y + r * cols);
     const float4 *w = reinterpret_cast<const float4 *>(W);
-    const uint32_t n4 = cols >> 2, cols8 = cols & ~7u;
+    const uint32_t n4 = cols >> 2, cols8 = cols & ~7u, P = chain_pitch(cols8 / 8);
+    float *rowt = reinterpret_cast<float *>(row4), *tail = rowt + 8 * P;
     float4 v[VPT];
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * kThreads;
         v[i] = j < n4 ? x[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (j < n4) row4[j] = v[i];
+        if (j < n4) {
+            if (4 * j < cols8) chain_put4(rowt, P, 4 * j, v[i]);
+            else *reinterpret_cast<float4 *>(tail) = v[i];   // the one float4 past cols8
+        }
     }
     __syncthreads();
-    const float *row = reinterpret_cast<const float *>(row4);
     float acc = 0.0f;
-    chain_sumsq(row, cols8, acc);
+    chain_sumsq(rowt, P, cols8 / 8, acc);
     if (threadIdx.x < 8) red8[threadIdx.x] = acc;
     __syncthreads();
-    const float inv = rms_inv(chain_total(red8, row + cols8, cols - cols8), cols, eps);
+    const float inv = rms_inv(chain_total(red8, tail, cols - cols8), cols, eps);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * kThreads;
@@ -536,21 +568,23 @@ __global__ __launch_bounds__(NT) void row_chain_kernel(RowChain p)
     }
     if (NORM) {
         // rmsnorm_reg_kernel's arithmetic (the reference's AVX2 order)
-        extern __shared__ float4 row4[];   // cols floats
+        extern __shared__ float4 row4[];   // chain_floats(cols) floats
         __shared__ float red8[8];
+        const uint32_t cols8 = p.cols & ~7u, P = chain_pitch(cols8 / 8);
+        float *rowt = reinterpret_cast<float *>(row4), *tail = rowt + 8 * P;
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const uint32_t j = threadIdx.x + i * NT;
-            if (j < n4) row4[j] = v[i];
+            if (j >= n4) continue;
+            if (4 * j < cols8) chain_put4(rowt, P, 4 * j, v[i]);
+            else *reinterpret_cast<float4 *>(tail) = v[i];
         }
         __syncthreads();
-        const float *row = reinterpret_cast<const float *>(row4);
-        const uint32_t cols8 = p.cols & ~7u;
         float acc = 0.0f;
-        chain_sumsq(row, cols8, acc);
+        chain_sumsq(rowt, P, cols8 / 8, acc);
         if (threadIdx.x < 8) red8[threadIdx.x] = acc;
         __syncthreads();
-        const float inv = rms_inv(chain_total(red8, row + cols8, p.cols - cols8), p.cols, p.eps);
+        const float inv = rms_inv(chain_total(red8, tail, p.cols - cols8), p.cols, p.eps);
         const float4 *w = reinterpret_cast<const float4 *>(p.W);
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
@@ -587,7 +621,7 @@ bool launch_row_chain(hipStream_t s, const RowChain &p)
 {
     const dim3 grid(p.rows), block(kThreads);
     const bool norm = p.Nrm != nullptr, quant = p.Q != nullptr;
-    const size_t lds = norm ? static_cast<size_t>(p.cols) * sizeof(float) : 0;
+    const size_t lds = norm ? static_cast<size_t>(chain_floats(p.cols)) * sizeof(float) : 0;
     if (p.pre == kChainAdd && norm && quant)
         row_chain_kernel<VPT, kChainAdd, true, true><<<grid, block, lds, s>>>(p);
     else if (p.pre == kChainAdd && norm)
@@ -625,13 +659,13 @@ void rmsnorm(hipStream_t s, const float *X, const float *W, float *Y, uint32_t r
                      ((reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y) |
                        (W ? reinterpret_cast<uintptr_t>(W) : 0)) % 16 == 0);
     const uint32_t n4 = cols / 4;
-    const size_t row_bytes = static_cast<size_t>(cols) * sizeof(float);
+    const size_t row_bytes = static_cast<size_t>(chain_floats(cols)) * sizeof(float);
     if (vec && n4 <= kThreads * 4)
         rmsnorm_reg_kernel<4><<<dim3(rows), kThreads, row_bytes, s>>>(X, W, Y, cols, eps);
     else if (vec && n4 <= kThreads * 12)
         rmsnorm_reg_kernel<12><<<dim3(rows), kThreads, row_bytes, s>>>(X, W, Y, cols, eps);
     else
-        rmsnorm_kernel<<<dim3(rows), kThreads, std::min<size_t>(row_bytes, kChainFloats * sizeof(float)), s>>>(
+        rmsnorm_kernel<<<dim3(rows), kThreads, chain_floats(std::min(cols, kChainFloats)) * sizeof(float), s>>>(
             X, W, Y, cols, eps);
 }
 

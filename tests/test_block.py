@@ -147,7 +147,10 @@ def _full_block(gpu, B, T, past, ctx, tag):
         get = lambda n, shp: gpu.download(blk.bufs[n], np.float32, shp)
         wq = {n: blk.quantized_weights(n) for n in PROJECTIONS}
         out = {"qkv": get("qkv", (rows, 3 * d)), "q": get("q", (B, H, T, D)), "k": get("k", (B, H, T, D)),
-               "v": get("v", (B, H, T, D)), "o": get("o", (B, H, T, D)), "att": get("att", (rows, d)),
+               "v": get("v", (B, H, T, D)), "o": get("o", (B, H, T, D)),
+               # one token per sequence: the harness feeds the O projection the
+               # attention output itself ([B][H][1][D] is the [B][H*D] layout)
+               "att": get("o" if T == 1 else "att", (rows, d)),
                "gate": get("gate", (rows, F)), "up": get("up", (rows, F)), "ff": get("ff", (rows, F)),
                "down": get("proj", (rows, d)), "x": get("x", (rows, d)), "xn2": get("xn", (rows, d))}
         if ctx:
