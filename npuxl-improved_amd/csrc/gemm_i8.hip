@@ -577,24 +577,89 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = (v16i){0};
 
-    issue(0);
-    if (KS > 1) issue(1);
-    for (uint32_t s = 0; s < KS; ++s) {
-        if (s + 1 < KS) wait_vmcnt<kLoads>();
-        else wait_vmcnt<0>();
-        block_barrier();
-        if (s + 2 < KS) issue(s + 2);
-        const bool skip = kSkip && *reinterpret_cast<const uint32_t *>(zflags + (2 * s + gk) * pipe::kBBlocks + wn * 4) ==
-                                       0x01010101u;
-        if (!skip) {
-            Frags f;
-            read_frags(s, f);
+    if constexpr (kSkip) {
+        issue(0);
+        if (KS > 1) issue(1);
+        for (uint32_t s = 0; s < KS; ++s) {
+            if (s + 1 < KS) wait_vmcnt<kLoads>();
+            else wait_vmcnt<0>();
+            block_barrier();
+            if (s + 2 < KS) issue(s + 2);
+            const bool skip = *reinterpret_cast<const uint32_t *>(zflags + (2 * s + gk) * pipe::kBBlocks + wn * 4) ==
+                              0x01010101u;
+            if (!skip) {
+                Frags f;
+                read_frags(s, f);
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    } else {
+        // Software-pipelined: stage s's 16 MFMAs run from fragments read
+        // during stage s-1; after the first four, one wait + barrier makes
+        // stage s+1 visible (its copy was issued a stage earlier), and the
+        // remaining twelve MFMA slots each carry one fragment read of stage
+        // s+1 and, in the first six, one copy instruction of stage s+2.  The
+        // ring buffer the copy refills held stage s-1, whose fragments every
+        // wave read before this barrier.
+        auto issue_one = [&](uint32_t st_i, int j) {
+            int8_t *st = smem + (st_i % kStages) * kStageBytes;
+            if (j < kAPer)
+                dma16(src[j] + st_i * SK, st + (wave * kAPer + j) * 1024);
+            else
+                dma16(src[j] + static_cast<uint64_t>(st_i) * 2048, st + kBOff + (wave * kBPer + j - kAPer) * 1024);
+        };
+        auto read_one = [&](uint32_t st_i, Frags &f, int k) {
+            const int8_t *st = smem + (st_i % kStages) * kStageBytes;
+            const int h = k / 6, r = k % 6;
+            if (r == 0 || r == 5) {
+                const int nb = r == 5;
+                const int boff = kBOff + (((wn * 4 + sub) * 2 + gk) << 10) +
+                                 (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
+                f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
+            } else {
+                const int mb = r - 1;
+                const uint32_t row = wm * 128 + mb * 32 + (lane & 31);
+                const uint32_t c = 4 * gk + 2 * h + (lane >> 5);
+                f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_off[mb] + ((c ^ ((row >> 1) & 7)) << 4));
+            }
+        };
+        auto step = [&](const Frags &cur, Frags &nxt, uint32_t s) {
+            const bool more = s + 1 < KS, dma = s + 2 < KS;
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
                 const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[h][i], cur.b[h][j], acc[i][j], 0, 0, 0);
+                if (k == 3 && more) {
+                    wait_vmcnt<0>();
+                    block_barrier();
+                }
+                if (k >= 4 && more) {
+                    if (dma && k - 4 < kLoads) issue_one(s + 2, k - 4);
+                    read_one(s + 1, nxt, k - 4);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
+        };
+        Frags f0, f1;
+        issue(0);
+        if (KS > 1) {
+            issue(1);
+            wait_vmcnt<kLoads>();
+        } else {
+            wait_vmcnt<0>();
         }
+        block_barrier();
+        read_frags(0, f0);
+        uint32_t s = 0;
+        for (; s + 1 < KS; s += 2) {
+            step(f0, f1, s);
+            step(f1, f0, s + 1);
+        }
+        if (s < KS) step(f0, f1, s);
     }
 
     // Sum the two k halves in the staged tile, then the shared epilogue.
