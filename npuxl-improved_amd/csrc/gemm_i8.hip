@@ -759,9 +759,8 @@ struct FragsW {
 // skipped work), and MFMAs on zero operands take the same cycles.  The map
 // is reduced once per workgroup to one byte per k block, bit q = MFMA column
 // tile q of the workgroup's TN columns.
-template <int TN, bool kSkip = false>
-__global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t tiles_m, uint32_t tiles_n0,
-                                                         uint32_t tiles_n1)
+template <int TN, bool kSkip>
+__device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_t tni)
 {
     using namespace wide;
     using G = Cfg<TN>;
@@ -772,14 +771,6 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-
-    const uint32_t first = tiles_m * tiles_n0, total = first + tiles_m * tiles_n1;
-    uint32_t g = blockIdx.x;
-    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
-    const bool second = g >= first;
-    const I8Gemm &p = second ? ps.p[1] : ps.p[0];
-    if (second) g -= first;
-    const uint32_t tmi = g % tiles_m, tni = g / tiles_m;
     const uint32_t m0 = tmi * TM, n0 = tni * TN;
     const uint32_t NT = p.Np >> 4;
     const uint32_t KS = p.K / SK;
@@ -985,6 +976,52 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t
     }
 }
 
+// Workgroup g (XCD-aware order) -> problem and tile: the first
+// tiles_m * tiles_n0 tiles belong to ps.p[0], the rest to ps.p[1].
+__device__ __forceinline__ bool wide_tile_of(uint32_t tiles_m, uint32_t tiles_n0, uint32_t tiles_n1, uint32_t &tmi,
+                                             uint32_t &tni)
+{
+    const uint32_t first = tiles_m * tiles_n0, total = first + tiles_m * tiles_n1;
+    uint32_t g = blockIdx.x;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const bool second = g >= first;
+    if (second) g -= first;
+    tmi = g % tiles_m;
+    tni = g / tiles_m;
+    return second;
+}
+
+template <int TN, bool kSkip = false>
+__global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t tiles_m, uint32_t tiles_n0,
+                                                         uint32_t tiles_n1)
+{
+    uint32_t tmi, tni;
+    const bool second = wide_tile_of(tiles_m, tiles_n0, tiles_n1, tmi, tni);
+    wide_tile<TN, kSkip>(ps.p[second ? 1 : 0], tmi, tni);
+}
+
+// One problem in two column ranges: ps.p[0] (the first columns) on 256-wide
+// tiles, ps.p[1] (the rest) on 192-wide tiles, sized so the grid fills whole
+// rounds of one tile per CU (N = 14336 at M = 2048: 32 + 32 tile columns, 512
+// tiles = two rounds, where 256-wide tiles alone are 448 = 1.75 rounds).
+// Each range fills whole rounds, and workgroups are dispatched in index
+// order, so the first rounds run the 256-wide tiles and the last ones the
+// 192-wide tiles (every CU one of each); the XCD-aware order applies within
+// each range.
+__global__ __launch_bounds__(kThreads) void gemm_i8_wide_mix(I8GemmPair ps, uint32_t tiles_m, uint32_t tiles_n0,
+                                                             uint32_t tiles_n1)
+{
+    const uint32_t first = tiles_m * tiles_n0;
+    const bool second = blockIdx.x >= first;
+    const uint32_t n = second ? tiles_m * tiles_n1 : first;
+    uint32_t g = second ? blockIdx.x - first : blockIdx.x;
+    if ((n & 7u) == 0) g = (g & 7u) * (n >> 3) + (g >> 3);
+    if (second)
+        wide_tile<192, false>(ps.p[1], g % tiles_m, g / tiles_m);
+    else
+        wide_tile<256, false>(ps.p[0], g % tiles_m, g / tiles_m);
+}
+
 }  // namespace
 
 uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t tile_n)
@@ -1042,6 +1079,7 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
     uint32_t v = p.variant;
     if (((v == kI8Wide || v == kI8Wide192) && !wide_ok) || (v == kI8Wave8 && !k128) || (v == kI8Pipe && !aligned))
         v = kI8Auto;
+    uint32_t mix_a = 0, mix_b = 0;   // tile columns of 256 and 192 (mixed grid)
     if (v == kI8Auto) {
         // The tile that finishes first: whole rounds of one tile per CU times
         // the tile's cost (a 256-wide grid of 344 or 384 tiles runs two
@@ -1052,8 +1090,26 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
             const double c8 = tile_cost(static_cast<uint64_t>(tm) * tn, cus, 256, 128, 1.4);
             const double c256 = tile_cost(static_cast<uint64_t>(wm_) * wn256, cus, 256, 256, 1.0);
             const double c192 = tile_cost(static_cast<uint64_t>(wm_) * wn192, cus, 256, 192, 1.2);
-            if (c256 <= c192 && c256 < c8) v = kI8Wide;
-            else if (c192 < c8) v = kI8Wide192;
+            double best = c8;
+            if (c256 <= c192 && c256 < c8) v = kI8Wide, best = c256;
+            else if (c192 < c8) v = kI8Wide192, best = c192;
+            // Mixed widths (dense weights): r1 whole rounds of 256-wide tiles
+            // on the first columns, r2 of 192-wide tiles on the rest.
+            if (!p.zero_blocks && cus % wm_ == 0) {
+                const uint32_t per = cus / wm_;   // tile columns per round
+                for (uint32_t r1 = 1; r1 <= 3; ++r1)
+                    for (uint32_t r2 = 1; r2 <= 3; ++r2) {
+                        const uint64_t n256 = 256ull * per * r1, ncols = n256 + 192ull * per * r2;
+                        if (n256 >= p.N || ncols < p.N || ncols - 192ull * per >= p.N) continue;
+                        const double c = r1 * 65536.0 * 1.0 + r2 * 49152.0 * 1.2;
+                        if (c < best) {
+                            best = c;
+                            v = kI8Wide;
+                            mix_a = per * r1;
+                            mix_b = per * r2;
+                        }
+                    }
+            }
         }
     }
     if (v != kI8Generic) {
@@ -1067,7 +1123,8 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
                                    reinterpret_cast<const void *>(gemm_i8_wide<256>),
                                    reinterpret_cast<const void *>(gemm_i8_wide<192>),
                                    reinterpret_cast<const void *>(gemm_i8_wide<256, true>),
-                                   reinterpret_cast<const void *>(gemm_i8_wide<192, true>)})
+                                   reinterpret_cast<const void *>(gemm_i8_wide<192, true>),
+                                   reinterpret_cast<const void *>(gemm_i8_wide_mix)})
                 ok = ok && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                160 * 1024) == hipSuccess;
             lds_optin = ok;
@@ -1076,6 +1133,22 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
     // Sixteen zero bytes and the zero map's per-workgroup reduction sit after
     // the wide kernel's LDS plan (one byte per 64-deep k block).
     const size_t zmap = p.zero_blocks ? 16 + (p.K / 64 + 15) / 16 * 16 : 0;
+    if (mix_a) {
+        // Column split of one problem: the packed weights are strip-major, so
+        // columns from nsplit on start nsplit / 16 strips into the fragments.
+        const uint32_t nsplit = 256 * mix_a;
+        I8Gemm p0 = p, p1 = p;
+        p0.N = p0.Np = nsplit;
+        p1.N = p.N - nsplit;
+        p1.Np = p.Np - nsplit;
+        p1.frag = p.frag + static_cast<uint64_t>(nsplit / 16) * (p.Kp / 64) * 1024;
+        p1.scale_b = p.scale_b + nsplit;
+        p1.bias = p.bias ? p.bias + nsplit : nullptr;
+        p1.C = p.C + nsplit;
+        gemm_i8_wide_mix<<<dim3(wm_ * (mix_a + mix_b)), kThreads, wide::Cfg<256>::kLds, s>>>(I8GemmPair{{p0, p1}},
+                                                                                             wm_, mix_a, mix_b);
+        return;
+    }
     switch (v) {
     case kI8Wide:
         if (p.zero_blocks)

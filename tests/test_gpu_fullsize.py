@@ -76,6 +76,33 @@ def test_config3_int8_prefill_full(gpu, N):
     assert _bits_equal(got, oracle.matmul_i8_blas(ha, hq, has, hs))
 
 
+@pytest.mark.parametrize("N,epi", [(13000, 1), (14336, 0), (14336, 3)])
+def test_int8_mixed_width_grid(gpu, N, epi):
+    """2048-row problems whose columns split into whole rounds of 256-wide and
+    192-wide tiles on 256 CUs (N in (12288, 14336]): the second range starts
+    32 strips into the packed weights, with its own scales, bias and C
+    columns; a ragged last tile; bias and activation epilogues (bit-exact up
+    to ReLU; GELU within the int8 epilogue bar of 1e-6)."""
+    M, K = 2048, 256
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = ((RNG.random(M) + 0.5) / 127).astype(np.float32)
+    sb = ((RNG.random(N) + 0.5) / 127).astype(np.float32)
+    bias = RNG.standard_normal(N).astype(np.float32)
+    w = gpu.pack(B, K, N, scales=sb)
+    ba, bsa, bb, bc = gpu.upload(A), gpu.upload(sa), gpu.upload(bias), gpu.alloc(4 * M * N)
+    gpu.run(abi.OP_MATMUL_I8, A=ba, B=w, scale_a=bsa.ptr, bias=bb.ptr, C=bc, M=M, K=K, N=N, epilogue=epi)
+    got = gpu.download(bc, np.float32, (M, N))
+    for b in (ba, bsa, bb, bc):
+        gpu.free(b)
+    gpu.release_packed(w)
+    want = oracle.matmul_i8_blas(A, B, sa, sb, bias, epi)
+    if epi <= 1:
+        assert _bits_equal(got, want)
+    else:
+        assert oracle.rel_error(got, want) <= 1e-6
+
+
 def test_int8_pair_k4096_full(gpu):
     """The block's gate/up pair at prefill size (2048 x 4096 x 11008, twice,
     one batch): the paired wide-tile grid over 32 k stages, bit-exact."""
