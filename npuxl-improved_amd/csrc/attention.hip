@@ -1003,17 +1003,21 @@ __device__ __forceinline__ void wave_sync_lds()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Two workgroups per CU at most (LDS), so two waves per SIMD: the register
+// budget is 256, and the K/V prefetch registers must not go to scratch.
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_exact_rows_kernel(Attn a)
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_exact_rows_kernel(Attn a)
 {
 #pragma clang fp contract(off)
     using G = ExactRows<D>;
     constexpr int RW = G::RW, DPT = G::DPT;
+    // Q rows and weights first: their reads then take immediate offsets
+    // (the 16-bit offset field of ds_read covers the first 64 KiB).
     extern __shared__ float4 sm4[];
-    float *Ks = reinterpret_cast<float *>(sm4);  // [64][P]
-    float *Vs = Ks + RK * G::P;                   // [64][D]
-    float *Qs = Vs + RK * D;                      // [QT][D]
+    float *Qs = reinterpret_cast<float *>(sm4);  // [QT][D]
     float *Wl = Qs + G::QT * D;                   // [QT][WP] weights, for the row sums
+    float *Ks = Wl + G::QT * G::WP;               // [64][P]
+    float *Vs = Ks + RK * G::P;                   // [64][D]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t bh = blockIdx.y;
@@ -1033,26 +1037,11 @@ __global__ __launch_bounds__(kThreads) void attn_exact_rows_kernel(Attn a)
     if (a.causal) kend = min(sk, q0 + nq - 1 + off + 1);
     const uint32_t nblk = (kend + RK - 1) / RK;
 
+    // Keys past kend load key kend - 1 and keep zeros (a select on the loaded
+    // values: a branch around the loads would make the compiler wait for
+    // them at once).
     float4 pk[G::kPre], pv[G::kPre];
-    auto fetch = [&](uint32_t b) {
-#pragma unroll
-        for (int u = 0; u < G::kPre; ++u) {
-            const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);
-            const uint32_t key = b * RK + j;
-            const bool in = key < kend;
-            const uint64_t at = static_cast<uint64_t>(in ? key : 0) * (D / 4) + c4;
-            pk[u] = in ? reinterpret_cast<const float4 *>(Kh)[at] : make_float4(0.f, 0.f, 0.f, 0.f);
-            pv[u] = in ? reinterpret_cast<const float4 *>(Vh)[at] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    auto stage = [&]() {
-#pragma unroll
-        for (int u = 0; u < G::kPre; ++u) {
-            const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);
-            *reinterpret_cast<float4 *>(Ks + j * G::P + 4 * c4) = pk[u];
-            reinterpret_cast<float4 *>(Vs)[f] = pv[u];
-        }
-    };
+    const float4 *K4 = reinterpret_cast<const float4 *>(Kh), *V4 = reinterpret_cast<const float4 *>(Vh);
 
     // Row state: m (uniform per row), l of row `wave*RW + lane` in lane < RW.
     float m[RW], acc[RW][DPT];
@@ -1066,13 +1055,34 @@ __global__ __launch_bounds__(kThreads) void attn_exact_rows_kernel(Attn a)
     const int r0 = wave * RW;
     float *wrow = Wl + r0 * G::WP;
 
-    if (nblk) fetch(0);
+#define VNPU_EXACT_FETCH(blk)                                                                      \
+    _Pragma("unroll") for (int u = 0; u < G::kPre; ++u) {                                          \
+        const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);                  \
+        const uint32_t key_ = (blk) * RK + j;                                                      \
+        const uint64_t at = static_cast<uint64_t>(min(key_, kend - 1)) * (D / 4) + c4;             \
+        const float4 kx = K4[at], vx = V4[at];                                                     \
+        const bool in_ = key_ < kend;                                                              \
+        pk[u] = make_float4(in_ ? kx.x : 0.f, in_ ? kx.y : 0.f, in_ ? kx.z : 0.f, in_ ? kx.w : 0.f); \
+        pv[u] = make_float4(in_ ? vx.x : 0.f, in_ ? vx.y : 0.f, in_ ? vx.z : 0.f, in_ ? vx.w : 0.f); \
+    }
+    if (nblk) {
+        VNPU_EXACT_FETCH(0u)
+    }
     for (uint32_t b = 0; b < nblk; ++b) {
         const uint32_t k0 = b * RK, kc = min(static_cast<uint32_t>(RK), kend - k0);
         __syncthreads();   // the previous block's tiles are consumed
-        stage();
+#pragma unroll
+        for (int u = 0; u < G::kPre; ++u) {
+            const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);
+            *reinterpret_cast<float4 *>(Ks + j * G::P + 4 * c4) = pk[u];
+            reinterpret_cast<float4 *>(Vs)[f] = pv[u];
+        }
         __syncthreads();
-        if (b + 1 < nblk) fetch(b + 1);
+        // the next block's tiles (past the last block: the last one again,
+        // never used, so the loads need no branch)
+        const uint32_t bn = b + 1 < nblk ? b + 1 : b;
+        VNPU_EXACT_FETCH(bn)
+#undef VNPU_EXACT_FETCH
 
         // Scores of the wave's rows, key `lane`.
         float ch[RW][8];
@@ -1162,8 +1172,8 @@ __global__ __launch_bounds__(kThreads) void attn_exact_rows_kernel(Attn a)
             if (live[i])
 #pragma unroll
                 for (int e = 0; e < DPT; ++e) acc[i][e] = acc[i][e] * alpha[i];
-        // Keys in groups of four (keys past kc have p = 0 and zero-filled V
-        // rows), the weights as broadcast reads of the LDS copy.  A group
+        // Keys in groups of four (keys past kc have p = 0 and zero V rows),
+        // the weights as broadcast reads of the LDS copy.  A group
         // whose sixteen weights are all nonzero runs without a branch;
         // otherwise each (row, key) tests its bit of the row's nonzero mask.
         const float *vcol = Vs + lane * DPT;
