@@ -52,7 +52,7 @@ ROTATE_BYTES = 800 << 20
 # copy kernel of known size (FETCH x2.000, WRITE x1.000):
 # 64,169.1 KiB x 2 + 125 KiB.  Measured offline with the commands in
 # profiles/gemv_i8_m1_k4096_n32000_traffic.md; re-measure when the kernel changes.
-GEMV_TRAFFIC_BYTES = 131_546_317
+GEMV_TRAFFIC_BYTES = 131_545_502
 
 
 def log(*a):
