@@ -78,10 +78,12 @@ namespace {
 // Host-pointer staging for one command.  Device-accessible pointers are used
 // as is; a pageable host pointer gets an HBM copy (in), a result copy-back
 // (out) or both.  Any staging makes the command synchronous: pageable
-// host copies are synchronous in HIP anyway.
+// host copies are synchronous in HIP anyway.  The copies live in the
+// stream's staging arena; a command needing more than it holds allocates the
+// rest, and the arena grows to that size once the command has finished.
 class Stager {
 public:
-    explicit Stager(hipStream_t s) : s_(s) {}
+    explicit Stager(hipStream_t s, vnpu_stream_t *owner = nullptr) : s_(s), owner_(owner) {}
     ~Stager() { release(); }
 
     template <typename T>
@@ -109,7 +111,6 @@ public:
         outs_.emplace_back(static_cast<void *>(p), d, bytes);
         return static_cast<T *>(d);
     }
-    bool staged() const { return !temps_.empty(); }
     void finish()
     {
         for (auto &o : outs_)
@@ -122,6 +123,13 @@ public:
 private:
     void *alloc(size_t bytes)
     {
+        const size_t need = (bytes + 255) & ~static_cast<size_t>(255);
+        total_ += need;
+        if (owner_ && owner_->staging && used_ + need <= owner_->staging_bytes) {
+            void *d = static_cast<char *>(owner_->staging) + used_;
+            used_ += need;
+            return d;
+        }
         void *d = nullptr;
         VNPU_HIP(hipMalloc(&d, bytes));
         temps_.push_back(d);
@@ -129,12 +137,28 @@ private:
     }
     void release()
     {
-        if (temps_.empty()) return;
+        if (!total_) return;
         (void)hipStreamSynchronize(s_);
         for (void *d : temps_) (void)hipFree(d);
         temps_.clear();
+        if (owner_ && total_ > owner_->staging_bytes) {
+            // the stream is idle (synchronized above): replace the arena
+            if (owner_->staging) (void)hipFree(owner_->staging);
+            owner_->staging = nullptr;
+            owner_->staging_bytes = 0;
+            void *d = nullptr;
+            if (hipMalloc(&d, total_) == hipSuccess) {
+                owner_->staging = d;
+                owner_->staging_bytes = total_;
+            } else {
+                (void)hipGetLastError();
+            }
+        }
+        total_ = used_ = 0;
     }
     hipStream_t s_;
+    vnpu_stream_t *owner_;
+    size_t used_ = 0, total_ = 0;
     std::vector<void *> temps_;
     std::vector<std::tuple<void *, void *, size_t>> outs_;
 };
@@ -349,7 +373,7 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
     // fix the K depth per workgroup; other tiles leave the choice automatic.
     p.k_split_depth = dev->f32_depth.load();
 
-    Stager sg(s->hip);
+    Stager sg(s->hip, s);
     p.A = sg.in(in.A, in.trans_a ? span(in.K, in.M, p.lda, 4) : span(in.M, in.K, p.lda, 4));
     p.B = sg.in(in.B, in.trans_b ? span(in.N, in.K, p.ldb, 4) : span(in.K, in.N, p.ldb, 4));
     p.bias = sg.in(in.bias, in.bias ? static_cast<size_t>(in.N) * 4 : 0);
@@ -363,12 +387,39 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
         cull_geometry(dev, unit, in.M, in.N, tm, tn);
         const uint32_t mt = cdiv(in.M, tm), nt = cdiv(in.N, tn);
         const uint8_t *mask = in.tile_mask;
-        std::vector<uint8_t> host_mask;
+        uint32_t bm, bn;
+        k::gemm_f32_tile_dims(bm, bn);
+        const uint32_t gm = cdiv(in.M, bm), gn = cdiv(in.N, bn);
+        total_tiles = static_cast<uint64_t>(mt) * nt;
+        p.cull_tm = tm;
+        p.cull_tn = tn;
+        p.cull_nt = nt;
         if (is_device_pointer(mask)) {
-            host_mask.resize(static_cast<size_t>(in.mask_tile_m) * in.mask_tile_n);
-            VNPU_HIP(hipMemcpy(host_mask.data(), mask, host_mask.size(), hipMemcpyDeviceToHost));
-            mask = host_mask.data();
+            // The mask may be written by earlier work on this stream: build
+            // the cull map and tile states on the GPU, in stream order, and
+            // count the culled tiles there (the status adds that count).
+            {
+                std::lock_guard<std::mutex> lock(dev->culled_mutex);
+                if (!dev->culled_dev) {
+                    void *c = nullptr;
+                    VNPU_HIP(hipMalloc(&c, sizeof(unsigned long long)));
+                    VNPU_HIP(hipMemset(c, 0, sizeof(unsigned long long)));
+                    dev->culled_dev = static_cast<unsigned long long *>(c);
+                }
+            }
+            const size_t cull_bytes = (total_tiles + 255) / 256 * 256;
+            uint8_t *scratch = static_cast<uint8_t *>(
+                s->ensure_cull_scratch(cull_bytes + static_cast<size_t>(gm) * gn));
+            k::cull_classify(s->hip, mask, in.mask_tile_m, in.mask_tile_n, in.M, in.N, tm, tn, scratch,
+                             scratch + cull_bytes, dev->culled_dev);
+            p.cull = scratch;
+            p.ktile_state = scratch + cull_bytes;
         }
+    }
+    if (has_mask && p.cull == nullptr) {   // a host mask: classified here
+        const uint32_t mt = cdiv(in.M, p.cull_tm), nt = p.cull_nt;
+        const uint32_t tm = p.cull_tm, tn = p.cull_tn;
+        const uint8_t *mask = in.tile_mask;
         cull.assign(static_cast<size_t>(mt) * nt, 0);
         for (uint32_t mi = 0; mi < mt; ++mi)
             for (uint32_t ni = 0; ni < nt; ++ni) {
@@ -381,7 +432,6 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
                     ++culled_tiles;
                 }
             }
-        total_tiles = static_cast<uint64_t>(mt) * nt;
         uint32_t bm, bn;
         k::gemm_f32_tile_dims(bm, bn);
         const uint32_t gm = cdiv(in.M, bm), gn = cdiv(in.N, bn);
@@ -398,9 +448,6 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
             }
         p.cull = sg.in(cull.data(), cull.size());
         p.ktile_state = sg.in(state.data(), state.size());
-        p.cull_tm = tm;
-        p.cull_tn = tn;
-        p.cull_nt = nt;
         // A host vector always stages; keep them alive until finish().
     }
     const bool c_in = in.beta != 0.0f || p.ldc != in.N;
@@ -454,7 +501,7 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     p.variant = dev->i8_variant.load();
     require(in.epilogue <= VNPU_EPILOGUE_GELU_ERF, "invalid matmul_i8 epilogue");
 
-    Stager sg(s->hip);
+    Stager sg(s->hip, s);
     p.A = sg.in(in.A, span(in.M, in.K, p.lda, 1));
     p.scale_a = sg.in(in.scale_a, in.scale_a ? static_cast<size_t>(in.M) * 4 : 0);
     p.bias = sg.in(in.bias, in.bias ? static_cast<size_t>(in.N) * 4 : 0);
@@ -694,7 +741,7 @@ void exec_quantize(vnpu_device_t *, vnpu_stream_t *s, const vnpu_quantize_i8_arg
     const uint64_t total = a.rows * a.cols;
     const size_t n_scales = a.axis == VNPU_QUANT_PER_ROW ? a.rows
                             : a.axis == VNPU_QUANT_PER_COLUMN ? a.cols : 1;
-    Stager sg(s->hip);
+    Stager sg(s->hip, s);
     const float *X = sg.in(a.X, total * 4);
     int8_t *Y = sg.out(a.Y, total);
     float *sc = sg.out(a.scales, n_scales * 4);
@@ -721,7 +768,7 @@ void exec_rmsnorm(vnpu_stream_t *s, const vnpu_rmsnorm_f32_args_t &a, ExecStats 
     require(a.X && a.Y && a.rows && a.cols, "invalid rmsnorm arguments");
     const float eps = a.eps > 0.0f ? a.eps : 1e-5f;
     const uint64_t n = static_cast<uint64_t>(a.rows) * a.cols;
-    Stager sg(s->hip);
+    Stager sg(s->hip, s);
     const float *X = sg.in(a.X, n * 4);
     const float *W = sg.in(a.W, a.W ? static_cast<size_t>(a.cols) * 4 : 0);
     float *Y = (a.Y == a.X) ? sg.inout(a.Y, n * 4) : sg.out(a.Y, n * 4);
@@ -740,7 +787,7 @@ void exec_softmax(vnpu_stream_t *s, const vnpu_softmax_f32_args_t &a, ExecStats 
     require(a.X && a.Y && a.rows && a.cols, "invalid softmax arguments");
     const float inv_t = a.temperature > 0.0f ? 1.0f / a.temperature : 1.0f;
     const uint64_t n = static_cast<uint64_t>(a.rows) * a.cols;
-    Stager sg(s->hip);
+    Stager sg(s->hip, s);
     const float *X = sg.in(a.X, n * 4);
     float *Y = (a.Y == a.X) ? sg.inout(a.Y, n * 4) : sg.out(a.Y, n * 4);
     if (a.Y == a.X && !is_device_pointer(a.X)) X = Y;
@@ -779,7 +826,7 @@ void exec_rope(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_rope_f32_args_t 
     uint32_t cs_rows = 0;
     const float2 *cs = rope_cos_sin_table(dev, theta, a.head_dim, scaling,
                                           static_cast<uint32_t>(std::min<uint64_t>(need, kRopeMaxRows)), cs_rows);
-    Stager sg(s->hip);
+    Stager sg(s->hip, s);
     float *Q = a.Q && a.q_seq ? sg.inout(a.Q, qn * 4) : nullptr;
     float *K = a.K && a.k_seq ? sg.inout(a.K, kn * 4) : nullptr;
     const int32_t *pos = sg.in(a.positions, a.positions ? static_cast<size_t>(seq) * 4 : 0);
@@ -794,7 +841,7 @@ void exec_rope(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_rope_f32_args_t 
 
 void exec_elementwise(vnpu_stream_t *s, const vnpu_command_t &cmd, ExecStats &st)
 {
-    Stager sg(s->hip);
+    Stager sg(s->hip, s);
     if (cmd.opcode == VNPU_OP_SWIGLU_F32) {
         const auto &a = cmd.args.swiglu;  // scheduler.cpp:536-548
         require(a.gate && a.up && a.Y && a.count, "invalid swiglu arguments");
@@ -865,7 +912,7 @@ void exec_attention(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecSt
     const uint64_t bh = static_cast<uint64_t>(a.batch) * a.heads;
     const uint64_t qn = bh * a.seq_q * a.head_dim, kn = bh * a.seq_k * a.head_dim;
     const uint64_t mn = a.mask ? bh * a.seq_q * a.seq_k : 0;
-    Stager sg(s->hip);
+    Stager sg(s->hip, s);
     p.Q = sg.in(a.Q, qn * 4);
     p.K = sg.in(a.K, kn * 4);
     p.V = sg.in(a.V, kn * 4);

@@ -635,6 +635,63 @@ void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn)
     bn = BN;
 }
 
+namespace {
+
+// Cull grid tile (mi, ni) samples the mask at (mi * mask_m / mt,
+// ni * mask_n / nt), as the host path and the reference's geometry do; one
+// count per wave goes to *culled.
+__global__ __launch_bounds__(kThreads) void cull_map_kernel(const uint8_t *__restrict__ mask, uint32_t mask_m,
+                                                            uint32_t mask_n, uint32_t mt, uint32_t nt,
+                                                            uint8_t *__restrict__ cull,
+                                                            unsigned long long *__restrict__ culled)
+{
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    bool c = false;
+    if (i < static_cast<uint64_t>(mt) * nt) {
+        const uint32_t mi = static_cast<uint32_t>(i / nt), ni = static_cast<uint32_t>(i % nt);
+        const uint32_t mm = min(mask_m - 1, static_cast<uint32_t>((static_cast<uint64_t>(mi) * mask_m) / mt));
+        const uint32_t nn = min(mask_n - 1, static_cast<uint32_t>((static_cast<uint64_t>(ni) * mask_n) / nt));
+        c = mask[static_cast<uint64_t>(mm) * mask_n + nn] == 0;
+        cull[i] = c ? 1 : 0;
+    }
+    const uint64_t n = __popcll(__ballot(c));
+    if ((threadIdx.x & 63) == 0 && n) atomicAdd(culled, static_cast<unsigned long long>(n));
+}
+
+// Kernel tile (gi, gj) of BM x BN outputs: compute (0), all culled (1) or
+// mixed (2) over the cull tiles it overlaps.
+__global__ __launch_bounds__(kThreads) void cull_state_kernel(const uint8_t *__restrict__ cull, uint32_t nt,
+                                                              uint32_t M, uint32_t N, uint32_t tm, uint32_t tn,
+                                                              uint32_t gm, uint32_t gn, uint8_t *__restrict__ state)
+{
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= static_cast<uint64_t>(gm) * gn) return;
+    const uint32_t gi = static_cast<uint32_t>(i / gn), gj = static_cast<uint32_t>(i % gn);
+    const uint32_t r0 = gi * BM / tm, r1 = (min(M, (gi + 1) * BM) - 1) / tm;
+    const uint32_t c0 = gj * BN / tn, c1 = (min(N, (gj + 1) * BN) - 1) / tn;
+    bool any_c = false, any_k = false;
+    for (uint32_t r = r0; r <= r1; ++r)
+        for (uint32_t c = c0; c <= c1; ++c) {
+            if (cull[static_cast<uint64_t>(r) * nt + c]) any_c = true;
+            else any_k = true;
+        }
+    state[i] = any_c ? (any_k ? 2 : 1) : 0;
+}
+
+}  // namespace
+
+void cull_classify(hipStream_t s, const uint8_t *mask, uint32_t mask_m, uint32_t mask_n, uint32_t M, uint32_t N,
+                   uint32_t tm, uint32_t tn, uint8_t *cull, uint8_t *state, unsigned long long *culled)
+{
+    const uint32_t mt = (M + tm - 1) / tm, nt = (N + tn - 1) / tn;
+    const uint32_t gm = (M + BM - 1) / BM, gn = (N + BN - 1) / BN;
+    const uint64_t n1 = static_cast<uint64_t>(mt) * nt, n2 = static_cast<uint64_t>(gm) * gn;
+    cull_map_kernel<<<dim3(static_cast<uint32_t>((n1 + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
+        mask, mask_m, mask_n, mt, nt, cull, culled);
+    cull_state_kernel<<<dim3(static_cast<uint32_t>((n2 + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
+        cull, nt, M, N, tm, tn, gm, gn, state);
+}
+
 // Grids of fewer than 128 tiles leave most CUs idle: split K over up to
 // 256 workgroups, at least 64 deep each (not with a cull map, whose per-tile
 // state is read by the single-pass kernel).

@@ -87,6 +87,12 @@ struct F32Gemm {
     uint32_t k_split_depth = 0;
 };
 void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn);
+// The Wildcat cull of MATMUL_F32 built on the GPU from a device-resident
+// mask (the same sampling and kernel-tile classification as the host path):
+// cull[mt][nt] (1 = culled), state[gm][gn] (0 compute, 1 all culled, 2
+// mixed); the number of culled tiles is added to *culled.
+void cull_classify(hipStream_t s, const uint8_t *mask, uint32_t mask_m, uint32_t mask_n, uint32_t M, uint32_t N,
+                   uint32_t tm, uint32_t tn, uint8_t *cull, uint8_t *state, unsigned long long *culled);
 // Grids of few tiles split K over workgroups: ws holds gemm_f32_ws_bytes(p)
 // bytes (0 when the single-pass kernel is used).
 size_t gemm_f32_ws_bytes(const F32Gemm &p);

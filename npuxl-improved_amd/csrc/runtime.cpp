@@ -118,6 +118,21 @@ void *vnpu_stream::ensure_workspace(size_t bytes)
     return workspace;
 }
 
+void *vnpu_stream::ensure_cull_scratch(size_t bytes)
+{
+    if (bytes <= cull_scratch_bytes) return cull_scratch;
+    if (cull_scratch) {
+        VNPU_HIP(hipStreamSynchronize(hip));
+        VNPU_HIP(hipFree(cull_scratch));
+        cull_scratch = nullptr;
+        cull_scratch_bytes = 0;
+    }
+    const size_t want = std::max<size_t>(bytes, 64u << 10);
+    VNPU_HIP(hipMalloc(&cull_scratch, want));
+    cull_scratch_bytes = want;
+    return cull_scratch;
+}
+
 // Events that only time GPU work: no system-scope fence when they complete
 // (the default event writes back and invalidates the caches, which costs
 // several microseconds per record and slows the kernels that follow).
@@ -485,6 +500,8 @@ static void destroy_stream_obj(vnpu_stream_t *s)
     }
     for (hipEvent_t e : s->event_pool) (void)hipEventDestroy(e);
     if (s->workspace) (void)hipFree(s->workspace);
+    if (s->staging) (void)hipFree(s->staging);
+    if (s->cull_scratch) (void)hipFree(s->cull_scratch);
     delete s;
 }
 
@@ -505,6 +522,7 @@ VNPU_API void VNPU_CALL vnpu_device_destroy(vnpu_device_t *device)
         vnpu_trace_write_chrome(device, device->trace.trace_file.c_str());
     device->trace.reset();
     release_device_tables(device);
+    if (device->culled_dev) (void)hipFree(device->culled_dev);
     delete device;
 }
 
@@ -535,6 +553,19 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_device_get_status(const vnpu_device_t *dev
     status->flops = device->flops.load();
     status->tiles_dispatched = device->tiles_dispatched.load();
     status->tiles_culled = device->tiles_culled.load();
+    {
+        // GPU-counted culls (device-resident masks): a copy only when any exist.
+        auto *d = const_cast<vnpu_device_t *>(device);
+        std::lock_guard<std::mutex> lock(d->culled_mutex);
+        if (d->culled_dev) {
+            unsigned long long v = 0;
+            if (hipSetDevice(d->hip_device) == hipSuccess &&
+                hipMemcpy(&v, d->culled_dev, sizeof(v), hipMemcpyDeviceToHost) == hipSuccess)
+                status->tiles_culled += v;
+            else
+                (void)hipGetLastError();
+        }
+    }
     status->dma_bytes = device->dma_bytes.load();
     status->interrupts = device->interrupts.load();
     status->busy = device->busy.load();
@@ -554,6 +585,12 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_device_reset(vnpu_device_t *device)
                     &device->tiles_dispatched, &device->tiles_culled, &device->dma_bytes,
                     &device->interrupts})
         a->store(0);
+    {
+        std::lock_guard<std::mutex> lock(device->culled_mutex);
+        if (device->culled_dev && (hipSetDevice(device->hip_device) != hipSuccess ||
+                                   hipMemset(device->culled_dev, 0, sizeof(unsigned long long)) != hipSuccess))
+            (void)hipGetLastError();
+    }
     device->error.store(0);
     device->last_opcode.store(0);
     device->regs[VNPU_REG_ERROR / 4].store(0);

@@ -129,6 +129,16 @@ struct vnpu_stream {
     std::atomic<uint64_t> pending{0};
     void *workspace = nullptr;
     size_t workspace_bytes = 0;
+    // Device copies of host-pointer operands: one grow-only arena reused by
+    // every staged command (each staged command synchronizes before it
+    // returns, so the next one may overwrite it).  Guarded by mutex.
+    void *staging = nullptr;
+    size_t staging_bytes = 0;
+    // The cull map and kernel-tile states of a MATMUL_F32 whose tile mask is
+    // in device memory, built on the GPU in stream order (grow-only).
+    void *cull_scratch = nullptr;
+    size_t cull_scratch_bytes = 0;
+    void *ensure_cull_scratch(size_t bytes);
     void *ensure_workspace(size_t bytes);
     // GPU time of submitted work by busy periods: a timing event is recorded
     // before the first batch after a synchronization and another when the
@@ -177,6 +187,10 @@ struct vnpu_device {
     std::atomic<uint32_t> i8_variant{0};   // int8 GEMM kernel (gemm_i8_variant_for_tiles)
     std::atomic<uint32_t> f32_depth{0};    // f32 K depth per workgroup (split-K)
     bool reference_order = false;          // VNPU_CONFIG_REFERENCE_ORDER: attention bit-exact
+    // Culled tiles counted on the GPU (MATMUL_F32 with a device-resident tile
+    // mask); folded into the status when read.  Allocated on first use.
+    unsigned long long *culled_dev = nullptr;
+    std::mutex culled_mutex;
     std::vector<vnpu_stream_t *> streams;
     std::mutex stream_mutex;
     vnpu_interrupt_cb_t irq_cb = nullptr;

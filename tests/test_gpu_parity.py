@@ -311,6 +311,32 @@ def test_matmul_f32_wildcat_cull(gpu, M, N, unit):
     assert rel(got, want) <= 1e-4
 
 
+@pytest.mark.parametrize("M,N,unit", [(256, 512, 2), (300, 200, 3), (1000, 1100, 2)])
+def test_matmul_f32_cull_device_mask_matches_host_mask(gpu, M, N, unit):
+    """A tile mask in device memory is sampled and classified on the GPU (no
+    copy back in submit): the same outputs as the same mask in host memory,
+    and the same culled-tile count in the device status."""
+    K = 40
+    mask = RNG.integers(0, 2, size=(5, 7)).astype(np.uint8)
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    B = RNG.standard_normal((K, N)).astype(np.float32)
+    ba, bb, bm = gpu.upload(A), gpu.upload(B), gpu.upload(mask)
+    outs, culled = [], []
+    for mptr in (mask.ctypes.data, bm.ptr):
+        bc = gpu.alloc(4 * M * N)
+        before = gpu.status().tiles_culled
+        gpu.run(abi.OP_MATMUL_F32, A=ba, B=bb, C=bc, M=M, K=K, N=N, unit=unit, tile_mask=mptr,
+                mask_tile_m=mask.shape[0], mask_tile_n=mask.shape[1])
+        assert gpu.sync() == abi.OK
+        culled.append(gpu.status().tiles_culled - before)
+        outs.append(gpu.download(bc, np.float32, (M, N)))
+        gpu.free(bc)
+    for b in (ba, bb, bm):
+        gpu.free(b)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert culled[0] == culled[1] > 0
+
+
 # ---------------------------------------------------------------- row / elementwise ops
 @pytest.mark.parametrize("rows,cols", [(1, 7), (7, 300), (64, 4096), (3, 32000), (5, 11008), (2, 12288),
                                        (3, 12292)])
