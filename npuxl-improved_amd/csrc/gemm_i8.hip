@@ -480,6 +480,105 @@ constexpr int kLoads = kAPer + kBPer;
 constexpr int kStages = pipe128::kStages;
 }  // namespace w8
 
+// ---------------------------------------------------------------------------
+// Epilogue from registers (8-wave and wide tiles).  A 32 x 32 MFMA
+// accumulator leaves column l % 32 and rows 8q + 4(l / 32) + rr in register
+// 4q + rr of lane l, so one dword store covers 32 columns of two rows (two
+// full 128-byte lines).  The stores go through a buffer over the wave's 128
+// rows of C: rows past M fall outside it and columns past N get an offset
+// past its end, so the buffer's range check drops out-of-range results
+// without branches (the whole offset is in the per-lane operand, which the
+// range check covers).  Needs
+// ldc <= kRegStoreMaxLdc (128 rows of C within a 31-bit byte range).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kRegStoreMaxLdc = (1u << 22) - 1;
+constexpr int kCBufferWord3 = 0x00020000;   // raw buffer, 32-bit data format
+constexpr int kCStorePolicy = 2;            // nontemporal: C is written once
+constexpr uint32_t kDropOffset = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t c_rows(const I8Gemm &p, uint32_t mrow)
+{
+    const uint32_t rows = mrow < p.M ? min(128u, p.M - mrow) : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc(p.C + static_cast<uint64_t>(mrow) * p.ldc, 0,
+                                             static_cast<int>(rows * p.ldc * 4u), kCBufferWord3);
+}
+
+// Column scales and bias of the NB 32-column tiles of lane l (column ncol +
+// 32j), and the lane's store offsets (row half l / 32 included).
+template <int NB>
+struct ColEpi {
+    float sb[NB], bias[NB];
+    uint32_t off[NB];
+    __device__ __forceinline__ ColEpi(const I8Gemm &p, uint32_t ncol, int lane)
+    {
+        const uint32_t h4 = static_cast<uint32_t>(lane >> 5) * 4u;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint32_t n = ncol + 32 * j;
+            const bool ok = n < p.N;
+            sb[j] = ok ? p.scale_b[n] : 0.0f;
+            bias[j] = (ok && p.bias) ? p.bias[n] : 0.0f;
+            off[j] = ok ? (h4 * p.ldc + n) * 4u : kDropOffset;
+        }
+    }
+};
+
+// Row tiles I0 .. I0+NI-1 of a wave's accumulators (plus, with kXch, the
+// partner wave's partial sums of the same tiles from LDS), stored in the
+// reference's order ((float)acc * sa) * sb + bias -> epi.  sa: the row scales
+// of the wave's 128 rows (LDS).
+template <int EPI, int NB, int I0, int NI, bool kXch>
+__device__ __forceinline__ void reg_store(const I8Gemm &p, const v16i (&acc)[4][NB], const v4i *theirs,
+                                          const float *sa, uint32_t mrow, const ColEpi<NB> &ce, int lane)
+{
+#pragma clang fp contract(off)
+    const __amdgpu_buffer_rsrc_t rs = c_rows(p, mrow);
+    const uint32_t ld4 = p.ldc * 4u;
+    const int h = lane >> 5;
+#pragma unroll
+    for (int ii = 0; ii < NI; ++ii)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r0 = (I0 + ii) * 32 + 8 * q;
+            const v4f s4 = *reinterpret_cast<const v4f *>(sa + r0 + 4 * h);
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                v4i o = (v4i){0, 0, 0, 0};
+                if (kXch) o = theirs[((ii * NB + j) * 4 + q) * 64 + lane];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const int32_t v = acc[I0 + ii][j][4 * q + rr] + o[rr];
+                    float f = (static_cast<float>(v) * s4[rr]) * ce.sb[j];
+                    if (p.bias) f = f + ce.bias[j];
+                    f = dev::epilogue(f, EPI);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, f), rs,
+                                                          static_cast<int>(ce.off[j] + (r0 + rr) * ld4), 0,
+                                                          kCStorePolicy);
+                }
+            }
+        }
+}
+
+// Epilogue exchange of the 8-wave tile: a wave's two MFMA row tiles x two
+// column tiles x 16 accumulators, as [tile][column tile][4 registers][lane]
+// 16-byte slots (lane-contiguous, so conflict-free), 16 KiB per wave.
+constexpr int kXchBytes = 2 * 2 * 4 * 64 * 16;
+static_assert(8 * kXchBytes + pipe128::TM * 4 <= static_cast<int>(pipe128::kLds), "exchange + row scales fit");
+
+template <int I0>
+__device__ __forceinline__ void xchg_put(const v16i (&acc)[4][2], v4i *dst, int lane)
+{
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const v16i &a = acc[I0 + ii][j];
+                dst[((ii * 2 + j) * 4 + q) * 64 + lane] = (v4i){a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+            }
+}
+
 template <bool kSkip>
 __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
 {
@@ -662,43 +761,36 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
         if (s < KS) step(f0, f1, s);
     }
 
-    // Sum the two k halves in the staged tile, then the shared epilogue.
+    // Waves w and w+4 hold the two k halves of the same 128 x 64 block.
+    // Wave group gk finishes MFMA row tiles 2gk and 2gk+1: it hands the other
+    // two tiles' partial sums to its partner through LDS and takes the
+    // partner's partials of its own two, then converts and stores them from
+    // registers.  One exchange barrier, half the tile through LDS each way.
+    const ColEpi<2> ce(p, n0 + wn * 64 + (lane & 31), lane);
+    const float sa_g = (tid < TM && p.scale_a && m0 + tid < p.M) ? p.scale_a[m0 + tid] : 1.0f;
+    __syncthreads();   // every wave's last fragment reads are done: the ring is free
+    v4i *xch = reinterpret_cast<v4i *>(smem);                      // [wave][2 x 2 x 4][64 lanes]
+    float *sa_lds = reinterpret_cast<float *>(smem + 8 * kXchBytes);
+    if (gk == 0)
+        xchg_put<2>(acc, xch + wave * (kXchBytes / 16), lane);
+    else
+        xchg_put<0>(acc, xch + wave * (kXchBytes / 16), lane);
+    if (tid < TM) sa_lds[tid] = sa_g;
     __syncthreads();
-    int32_t *tile = reinterpret_cast<int32_t *>(smem);
-    auto tile_at = [&](int i, int j, int r) -> int32_t & {
-        return tile[(wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * pipe::kOutPitch + wn * 64 +
-                    j * 32 + (lane & 31)];
-    };
-    if (gk == 1) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) tile_at(i, j, r) = acc[i][j][r];
-    }
-    float *sa_lds = reinterpret_cast<float *>(smem + pipe::kScaleOff);
-    if (tid < TM) {
-        const uint32_t m = m0 + tid;
-        sa_lds[tid] = (p.scale_a && m < p.M) ? p.scale_a[m] : 1.0f;
-    }
-    __syncthreads();
-    if (gk == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) tile_at(i, j, r) += acc[i][j][r];
-    }
-    __syncthreads();
+    const v4i *theirs = xch + (wave ^ 4) * (kXchBytes / 16);
+    const float *sa = sa_lds + wm * 128;
+    const uint32_t mrow = m0 + wm * 128;
+#define VNPU_W8_STORE(E)                                                   \
+    (gk ? reg_store<E, 2, 2, 2, true>(p, acc, theirs, sa, mrow, ce, lane) \
+        : reg_store<E, 2, 0, 2, true>(p, acc, theirs, sa, mrow, ce, lane))
     switch (p.epilogue) {
-    case 1: store_tile<1, w8::kThreads8>(p, tile, sa_lds, m0, n0, tid); break;
-    case 2: store_tile<2, w8::kThreads8>(p, tile, sa_lds, m0, n0, tid); break;
+    case 1: VNPU_W8_STORE(1); break;
+    case 2: VNPU_W8_STORE(2); break;
     case 3:
-    case 4: store_tile<3, w8::kThreads8>(p, tile, sa_lds, m0, n0, tid); break;
-    default: store_tile<0, w8::kThreads8>(p, tile, sa_lds, m0, n0, tid); break;
+    case 4: VNPU_W8_STORE(3); break;
+    default: VNPU_W8_STORE(0); break;
     }
+#undef VNPU_W8_STORE
 }
 
 // ---------------------------------------------------------------------------
@@ -715,13 +807,13 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
 //     between them; vmcnt(0) (stage s+1 landed) and one barrier (stage s
 //     fully read); the MFMAs of half 1 with stage s+2's DMA instructions and
 //     stage s+1's half-0 reads threaded between them;
-//   * the epilogue stages 128 rows at a time through LDS.
+//   * the epilogue stores each wave's block from registers; its row and
+//     column scales load during the last stage's MFMAs.
 // ---------------------------------------------------------------------------
 namespace wide {
 constexpr int TM = 256, SK = 128;
 constexpr int kALoads = 8;                            // A DMA per wave per stage
 constexpr int kBOff = 32 * 1024;                      // B's offset in a stage
-constexpr int kOutRows = 128;                         // rows staged at a time
 template <int TN>
 struct Cfg {
     static constexpr int NB = TN / 64;                // 32-column MFMA tiles per wave
@@ -730,10 +822,8 @@ struct Cfg {
     static constexpr int kLoads = kALoads + kBLoads;
     static constexpr int kStageBytes = kBOff + kBBlocks * 1024;
     static constexpr int kRing = 2 * kStageBytes;
-    static constexpr int kOutPitch = TN + 4;          // int32 per staged row
-    static constexpr int kOut = kOutRows * kOutPitch * 4;
-    static constexpr int kScaleOff = kOut;
-    static constexpr size_t kLds = static_cast<size_t>(kOut + TM * 4 > kRing ? kOut + TM * 4 : kRing);
+    static constexpr int kScaleOff = kRing;           // 256 row scales after the ring
+    static constexpr size_t kLds = static_cast<size_t>(kRing + TM * 4);
     static constexpr int kReads = 2 * (4 + NB);       // fragment reads per 64-deep half
     static constexpr int kMfma = 2 * 4 * NB;          // MFMAs per 64-deep half
     static_assert(kLds <= 160 * 1024, "LDS plan");
@@ -933,6 +1023,9 @@ __device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_
         z_cur = z_nxt;
         ++s;
     }
+    // The epilogue's row and column scales load during the last stage.
+    const float sa_g = p.scale_a ? p.scale_a[m0 + tid] : 1.0f;   // M % 256 == 0: row m0 + tid exists
+    const ColEpi<NB> ce(p, n0 + wn * (TN / 2) + (lane & 31), lane);
     {
         const uint32_t cur = (s & 1) * G::kStageBytes;
         const uint32_t zw1 = wave_bits(z_cur >> 8);
@@ -941,38 +1034,18 @@ __device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_
         mma(f1, [](int) {});
     }
 
-    // Epilogue, 128 rows (the rows of waves with wm == half) at a time.
-    __syncthreads();
-    int32_t *tile = reinterpret_cast<int32_t *>(smem);
+    // Epilogue: each wave stores its own 128 x TN/2 block from registers.
     float *sa_lds = reinterpret_cast<float *>(smem + G::kScaleOff);
-    {
-        const uint32_t m = m0 + tid;
-        sa_lds[tid] = (p.scale_a && m < p.M) ? p.scale_a[m] : 1.0f;
-    }
-    for (int half = 0; half < 2; ++half) {
-        const uint32_t mh = m0 + half * kOutRows;
-        if (wm == half) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < NB; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        tile[(i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * G::kOutPitch + wn * (TN / 2) +
-                             j * 32 + (lane & 31)] = acc[i][j][r];
-        }
-        __syncthreads();
-        if (mh < p.M) {
-            const float *sa = sa_lds + half * kOutRows;
-            switch (p.epilogue) {
-            case 1: store_tile<1, kThreads, TN, G::kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
-            case 2: store_tile<2, kThreads, TN, G::kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
-            case 3:
-            case 4: store_tile<3, kThreads, TN, G::kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
-            default: store_tile<0, kThreads, TN, G::kOutPitch, kOutRows>(p, tile, sa, mh, n0, tid); break;
-            }
-        }
-        __syncthreads();
+    sa_lds[tid] = sa_g;
+    __syncthreads();
+    const float *sa = sa_lds + wm * 128;
+    const uint32_t mrow = m0 + wm * 128;
+    switch (p.epilogue) {
+    case 1: reg_store<1, NB, 0, 4, false>(p, acc, nullptr, sa, mrow, ce, lane); break;
+    case 2: reg_store<2, NB, 0, 4, false>(p, acc, nullptr, sa, mrow, ce, lane); break;
+    case 3:
+    case 4: reg_store<3, NB, 0, 4, false>(p, acc, nullptr, sa, mrow, ce, lane); break;
+    default: reg_store<0, NB, 0, 4, false>(p, acc, nullptr, sa, mrow, ce, lane); break;
     }
 }
 
@@ -1068,7 +1141,7 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
     const bool aligned = (p.K % 64 == 0) && (p.lda % 16 == 0) &&
                          (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64 &&
                          p.K <= 16384;
-    const bool k128 = aligned && p.K % pipe128::SK == 0;
+    const bool k128 = aligned && p.K % pipe128::SK == 0 && p.ldc <= kRegStoreMaxLdc;
     const bool wide_ok = k128 && p.M % wide::TM == 0;
     const uint32_t wm_ = p.M / wide::TM;
     const uint32_t wn256 = (p.N + 255) / 256, wn192 = (p.N + 191) / 192;
@@ -1197,6 +1270,7 @@ bool gemm_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1)
     auto wide_ok = [](const I8Gemm &p) {
         return p.K % 64 == 0 && p.lda % 16 == 0 && reinterpret_cast<uintptr_t>(p.A) % 16 == 0 && p.M >= 64 &&
                p.K <= 16384 && p.K % pipe128::SK == 0 && !p.zero_blocks && p.M % wide::TM == 0 &&
+               p.ldc <= kRegStoreMaxLdc &&
                p.variant == kI8Auto;
     };
     if (p0.M != p1.M || !wide_ok(p0) || !wide_ok(p1)) return false;
