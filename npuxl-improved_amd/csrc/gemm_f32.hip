@@ -387,8 +387,12 @@ __device__ __forceinline__ void x3_stash(const X3Slice &s, int tid, int8_t *hi_p
 // WM wave rows: the tile is 64*WM x 128 (WM = 2: four waves, two workgroups
 // per CU; WM = 4: eight waves, one workgroup per CU, each A slice converted
 // once for twice the columns... the B slice once for twice the rows).
+// blockIdx.y selects the k range [y * k_per_split, + k_per_split) (a
+// multiple of the 32-deep stage) when K is split over workgroups; then the
+// raw sums go to ws[y][m][n] and gemm_f32_splitk_reduce applies alpha, bias,
+// beta and the epilogue once.
 template <bool TA, bool TB, int WM>
-__global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p)
+__global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p, uint32_t k_per_split, float *ws)
 {
     constexpr uint32_t TM = 64 * WM, TN = x3::TN, XBK = x3::BK;
     constexpr int NT = 128 * WM;
@@ -405,15 +409,16 @@ __global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p)
     uint32_t g = blockIdx.x;
     if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
     const uint32_t m0 = (g % tiles_m) * TM, n0 = (g / tiles_m) * TN;
-    const uint32_t KT = (p.K + XBK - 1) / XBK;
+    const uint32_t kb = blockIdx.y * k_per_split;
+    const uint32_t KT = (min(p.K, kb + k_per_split) - kb + XBK - 1) / XBK;
     const int h = lane >> 5, col = lane & 31;
 
     // The next stage's f32 slices load into registers while this stage is
     // multiplied, then are split into the other LDS buffer.
     X3Slice sa, sb;
     auto fetch = [&](uint32_t kt) {
-        x3_fetch<!TA, TM, NT>(p.A, p.lda, p.M, p.K, m0, kt * XBK, tid, sa);
-        x3_fetch<TB, TN, NT>(p.B, p.ldb, p.N, p.K, n0, kt * XBK, tid, sb);
+        x3_fetch<!TA, TM, NT>(p.A, p.lda, p.M, p.K, m0, kb + kt * XBK, tid, sa);
+        x3_fetch<TB, TN, NT>(p.B, p.ldb, p.N, p.K, n0, kb + kt * XBK, tid, sb);
     };
     auto stash = [&](uint32_t kt) {
         int8_t *st = smem + (kt & 1) * kStage;
@@ -482,7 +487,11 @@ __global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const uint32_t m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m < p.M) store_out(p, m, n, acc[i][j][r], false);
+                if (m >= p.M) continue;
+                if (ws)
+                    ws[(static_cast<uint64_t>(blockIdx.y) * p.M + m) * p.N + n] = acc[i][j][r];
+                else
+                    store_out(p, m, n, acc[i][j][r], false);
             }
     }
 }
@@ -715,18 +724,45 @@ static uint32_t gemm_f32_splits(const F32Gemm &p)
     return tiles >= 128 ? 1 : splits;
 }
 
-// The split-bf16 kernel takes grids of at least 128 tiles of 128 x 128
-// without a cull map or a requested K depth, on 16-byte aligned operands.
-static bool use_x3(const F32Gemm &p)
+// The split-bf16 kernel takes every MATMUL_F32 without a cull map or a
+// requested K depth on 16-byte aligned operands.  Grids of fewer than 128
+// tiles of 128 x 128 split K over workgroups (32-deep stages, at least two
+// per slice) until the grid has 128 or more, with the partial sums reduced
+// in slice order by a second pass.
+struct X3Plan {
+    bool x3 = false;
+    int wm = 2;
+    uint32_t splits = 1, kps = 0;
+};
+
+static X3Plan x3_plan(const F32Gemm &p)
 {
-    const uint64_t tiles = static_cast<uint64_t>((p.M + 127) / 128) * ((p.N + x3::TN - 1) / x3::TN);
+    X3Plan x;
     const bool al = (p.lda % 4 == 0) && (p.ldb % 4 == 0) && (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) &&
                     (reinterpret_cast<uintptr_t>(p.B) % 16 == 0);
-    return !p.cull && !p.ktile_state && p.k_split_depth == 0 && tiles >= 128 && al;
+    if (p.cull || p.ktile_state || p.k_split_depth != 0 || !al) return x;
+    x.x3 = true;
+    x.kps = p.K;
+    const uint64_t tiles = static_cast<uint64_t>((p.M + 127) / 128) * ((p.N + x3::TN - 1) / x3::TN);
+    // 256 x 128 tiles (eight waves) when they still give every CU one: each
+    // workgroup splits an A slice once for 128 columns and a B slice once
+    // for 256 rows (a quarter less conversion per MFMA).
+    const uint64_t tiles256 = static_cast<uint64_t>((p.M + 255) / 256) * ((p.N + x3::TN - 1) / x3::TN);
+    if (tiles256 >= 256) x.wm = 4;
+    if (tiles >= 128) return x;
+    uint32_t want = 1;
+    while (tiles * want < 128 && p.K / (want * 2) >= 2 * x3::BK) want *= 2;
+    const uint64_t per_split = static_cast<uint64_t>(p.M) * p.N * sizeof(float);
+    want = static_cast<uint32_t>(std::min<uint64_t>(want, std::max<uint64_t>(1, kMaxSplitWs / per_split)));
+    if (want > 1) {
+        x.kps = ((p.K + want - 1) / want + x3::BK - 1) / x3::BK * x3::BK;
+        x.splits = (p.K + x.kps - 1) / x.kps;   // every slice starts below K
+    }
+    return x;
 }
 
 template <int WM>
-static void launch_x3(hipStream_t s, const F32Gemm &p)
+static void launch_x3(hipStream_t s, const F32Gemm &p, const X3Plan &x, float *ws)
 {
     static std::atomic<bool> lds_optin{false};  // launches may come from several host threads
     constexpr int lds = x3::lds_bytes(WM);
@@ -739,30 +775,36 @@ static void launch_x3(hipStream_t s, const F32Gemm &p)
                                         hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess &&
                     hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_x3<true, true, WM>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, lds) == hipSuccess;
-    const dim3 grid(((p.N + x3::TN - 1) / x3::TN) * ((p.M + 64 * WM - 1) / (64 * WM)));
+    const dim3 grid(((p.N + x3::TN - 1) / x3::TN) * ((p.M + 64 * WM - 1) / (64 * WM)), x.splits);
     const dim3 block(128 * WM);
-    if (!p.trans_a && !p.trans_b) gemm_f32_x3<false, false, WM><<<grid, block, lds, s>>>(p);
-    else if (!p.trans_a) gemm_f32_x3<false, true, WM><<<grid, block, lds, s>>>(p);
-    else if (!p.trans_b) gemm_f32_x3<true, false, WM><<<grid, block, lds, s>>>(p);
-    else gemm_f32_x3<true, true, WM><<<grid, block, lds, s>>>(p);
+    float *out = x.splits > 1 ? ws : nullptr;
+    if (!p.trans_a && !p.trans_b) gemm_f32_x3<false, false, WM><<<grid, block, lds, s>>>(p, x.kps, out);
+    else if (!p.trans_a) gemm_f32_x3<false, true, WM><<<grid, block, lds, s>>>(p, x.kps, out);
+    else if (!p.trans_b) gemm_f32_x3<true, false, WM><<<grid, block, lds, s>>>(p, x.kps, out);
+    else gemm_f32_x3<true, true, WM><<<grid, block, lds, s>>>(p, x.kps, out);
 }
 
 size_t gemm_f32_ws_bytes(const F32Gemm &p)
 {
-    if (use_x3(p)) return 0;
-    const uint32_t splits = gemm_f32_splits(p);
+    const X3Plan x = x3_plan(p);
+    const uint32_t splits = x.x3 ? x.splits : gemm_f32_splits(p);
     return splits > 1 ? static_cast<size_t>(splits) * p.M * p.N * sizeof(float) : 0;
+}
+
+static void splitk_reduce(hipStream_t s, const F32Gemm &p, const float *ws, uint32_t splits)
+{
+    const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
+    gemm_f32_splitk_reduce<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
+        p, ws, splits);
 }
 
 void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
 {
-    if (use_x3(p)) {
-        // 256 x 128 tiles (eight waves) when they still give every CU one:
-        // each workgroup splits an A slice once for 128 columns and a B slice
-        // once for 256 rows (a quarter less conversion per MFMA).
-        const uint64_t tiles256 = static_cast<uint64_t>((p.M + 255) / 256) * ((p.N + x3::TN - 1) / x3::TN);
-        if (tiles256 >= 256) launch_x3<4>(s, p);
-        else launch_x3<2>(s, p);
+    const X3Plan x = x3_plan(p);
+    if (x.x3) {
+        if (x.wm == 4) launch_x3<4>(s, p, x, ws);
+        else launch_x3<2>(s, p, x, ws);
+        if (x.splits > 1) splitk_reduce(s, p, ws, x.splits);
         return;
     }
     const uint32_t want = gemm_f32_splits(p);
@@ -771,11 +813,7 @@ void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
     const uint32_t splits = want > 1 ? (p.K + kps - 1) / kps : 1;
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, splits);
     gemm_f32_kernel<<<grid, kThreads, 0, s>>>(p, kps, splits > 1 ? ws : nullptr);
-    if (splits > 1) {
-        const uint64_t total = static_cast<uint64_t>(p.M) * p.N;
-        gemm_f32_splitk_reduce<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
-            p, ws, splits);
-    }
+    if (splits > 1) splitk_reduce(s, p, ws, splits);
 }
 
 size_t gemv_f32_ws_bytes(const F32Gemm &p)
