@@ -387,6 +387,61 @@ __device__ __forceinline__ void x3_stash(const X3Slice &s, int tid, int8_t *hi_p
 // WM wave rows: the tile is 64*WM x 128 (WM = 2: four waves, two workgroups
 // per CU; WM = 4: eight waves, one workgroup per CU, each A slice converted
 // once for twice the columns... the B slice once for twice the rows).
+// The epilogue of a wave's 64 x 64 block straight from its accumulators
+// (store_out's arithmetic: alpha * acc + bias + beta * C_in -> epi).  The
+// wave's 64 rows of C are one buffer whose range check drops rows past M,
+// and columns past N get an offset past its end, so loads and stores need
+// no branches; the column's bias is loaded once and every C_in value of the
+// block is in flight before the first is used.  Needs ldc <= kX3MaxLdc (64
+// rows of C within a 31-bit byte range).
+constexpr uint32_t kX3MaxLdc = (1u << 23) - 1;
+constexpr int kCBufferWord3 = 0x00020000;   // raw buffer, 32-bit data format
+constexpr int kCStorePolicy = 2;            // nontemporal: C is written once
+
+__device__ __forceinline__ void x3_store_rows(const F32Gemm &p, const v16f (&acc)[2][2], uint32_t mrow,
+                                              uint32_t ncol, int h)
+{
+    const uint32_t rows = mrow < p.M ? min(64u, p.M - mrow) : 0u;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        p.C + static_cast<uint64_t>(mrow) * p.ldc, 0, static_cast<int>(rows * p.ldc * 4u), kCBufferWord3);
+    const uint32_t ld4 = p.ldc * 4u;
+    float bv[2];
+    uint32_t off[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t n = ncol + 32 * j;
+        const bool ok = n < p.N;
+        bv[j] = (ok && p.bias) ? p.bias[n] : 0.0f;
+        off[j] = ok ? (static_cast<uint32_t>(4 * h) * p.ldc + n) * 4u : 0x80000000u;
+    }
+    auto at = [&](int i, int j, int r) {
+        return static_cast<int>(off[j] + static_cast<uint32_t>(32 * i + 8 * (r >> 2) + (r & 3)) * ld4);
+    };
+    float cin[2][2][16];
+    if (p.beta != 0.0f) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    cin[i][j][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, at(i, j, r), 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float out = p.alpha * acc[i][j][r];
+                if (p.bias) out += bv[j];
+                if (p.beta != 0.0f) out += p.beta * cin[i][j][r];
+                out = dev::epilogue(out, p.epilogue);
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), rs, at(i, j, r), 0,
+                                                      kCStorePolicy);
+            }
+}
+
 // blockIdx.y selects the k range [y * k_per_split, + k_per_split) (a
 // multiple of the 32-deep stage) when K is split over workgroups; then the
 // raw sums go to ws[y][m][n] and gemm_f32_splitk_reduce applies alpha, bias,
@@ -478,6 +533,14 @@ __global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p, uint32_t k_pe
 
     // 32 x 32 accumulator: lane l holds column l%32, rows 8j' + 4(l/32) + i'
     // in register 4j' + i'; a store instruction writes two 128-byte row runs.
+    // (The four-wave tile keeps the per-element stores: the direct epilogue's
+    // registers slowed its main loop, which small and split grids run.)
+    if constexpr (WM == 4) {
+        if (!ws && p.ldc <= kX3MaxLdc) {
+            x3_store_rows(p, acc, m0 + wm * 64, n0 + wn * 64 + col, h);
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const uint32_t n = n0 + wn * 64 + 32 * j + col;

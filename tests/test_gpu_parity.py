@@ -337,6 +337,34 @@ def test_matmul_f32_split_bf16(gpu, M, K, N, ta, tb, epi, beta):
     assert rel(got, want) <= 1e-4
 
 
+@pytest.mark.parametrize("beta", [0.0, 0.5])
+def test_matmul_f32_split_bf16_padded_c(gpu, beta):
+    """The eight-wave split-bf16 tile stores C (and reads C_in for beta)
+    straight from its accumulators through a buffer whose range check drops
+    rows past M and columns past N: with ldc > N and sentinel rows after row
+    M, the padding and the sentinel rows keep their contents and the rest is
+    alpha * A B + bias + beta * C_in -> GELU to the f32 bar."""
+    rng = np.random.default_rng(77 + int(beta * 10))
+    M, K, N, ldc, extra = 1100, 96, 6600, 6616, 8       # 5 x 52 tiles of 256 x 128, ragged M and N
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    sentinel = np.float32(-3.5)
+    C0 = np.full((M + extra, ldc), sentinel, np.float32)
+    C0[:M, :N] = rng.standard_normal((M, N)).astype(np.float32)
+    ba, bb, bbias, bc = gpu.upload(A), gpu.upload(B), gpu.upload(bias), gpu.upload(C0)
+    try:
+        gpu.run(abi.OP_MATMUL_F32, A=ba, B=bb, bias=bbias.ptr, C=bc, M=M, K=K, N=N, ldc=ldc, alpha=1.0,
+                beta=beta, epilogue=abi.EPI_GELU_TANH)
+        out = gpu.download(bc, np.float32, (M + extra, ldc))
+    finally:
+        for b in (ba, bb, bbias, bc):
+            gpu.free(b)
+    assert np.all(out[:, N:] == sentinel) and np.all(out[M:] == sentinel)
+    want = oracle.matmul_f32(A, B, C0[:M, :N], bias, M, K, N, 0, 0, 1.0, beta, abi.EPI_GELU_TANH, acc64=True)
+    assert rel(out[:M, :N], want) <= 1e-4
+
+
 @pytest.mark.parametrize("M,N,unit", [(256, 512, 2), (40, 96, 2), (128, 128, 1), (300, 200, 3),
                                       (4, 300, 0)])
 def test_matmul_f32_wildcat_cull(gpu, M, N, unit):
