@@ -635,11 +635,13 @@ bool launch_row_chain(hipStream_t s, const RowChain &p)
 
 bool launch_swiglu_chain(hipStream_t s, const RowChain &p)
 {
-    const dim3 grid(p.rows), block(1024);
-    if (p.cols / 4 <= 1024)
-        row_chain_kernel<1, kChainSwiglu, false, true, 1024><<<grid, block, 0, s>>>(p);
+    const dim3 grid(p.rows);
+    if (p.rows >= 256)
+        row_chain_kernel<12, kChainSwiglu, false, true, 256><<<grid, dim3(256), 0, s>>>(p);
+    else if (p.cols / 4 <= 1024)
+        row_chain_kernel<1, kChainSwiglu, false, true, 1024><<<grid, dim3(1024), 0, s>>>(p);
     else
-        row_chain_kernel<3, kChainSwiglu, false, true, 1024><<<grid, block, 0, s>>>(p);
+        row_chain_kernel<3, kChainSwiglu, false, true, 1024><<<grid, dim3(1024), 0, s>>>(p);
     return true;
 }
 
