@@ -1109,6 +1109,19 @@ uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t ti
 
 namespace {
 
+
+// Estimated time of a grid of `tiles` tiles of area tm x tn on `cus` CUs:
+// whole rounds of one tile per CU, each tile costing its area times the
+// kernel's measured time per unit area (relative: 256 x 256 tile 1.0,
+// 256 x 192 1.2, 256 x 128 8-wave 1.4; from 2048 x 4096 x N runs).
+double tile_cost(uint64_t tiles, uint32_t cus, uint32_t tm, uint32_t tn, double per_area)
+{
+    const uint64_t rounds = (tiles + cus - 1) / cus;
+    return static_cast<double>(rounds) * tm * tn * per_area;
+}
+
+}  // namespace
+
 uint32_t cu_count()
 {
     static const uint32_t n = [] {
@@ -1122,18 +1135,6 @@ uint32_t cu_count()
     }();
     return n;
 }
-
-// Estimated time of a grid of `tiles` tiles of area tm x tn on `cus` CUs:
-// whole rounds of one tile per CU, each tile costing its area times the
-// kernel's measured time per unit area (relative: 256 x 256 tile 1.0,
-// 256 x 192 1.2, 256 x 128 8-wave 1.4; from 2048 x 4096 x N runs).
-double tile_cost(uint64_t tiles, uint32_t cus, uint32_t tm, uint32_t tn, double per_area)
-{
-    const uint64_t rounds = (tiles + cus - 1) / cus;
-    return static_cast<double>(rounds) * tm * tn * per_area;
-}
-
-}  // namespace
 
 void gemm_i8(hipStream_t s, const I8Gemm &p)
 {

@@ -34,11 +34,17 @@
 #include "kernels.hpp"
 #include "device_math.hpp"
 
+#include <atomic>
+
 namespace vnpu {
 namespace k {
 namespace {
 
 constexpr uint32_t kLdsA = 32768;   // max bytes of staged activations per chunk
+// The same for grids of 16-wave workgroups with at most one workgroup per CU:
+// a whole 8 x 11008 activation block (the decode down projection) fits in
+// one chunk, so the weight stream is not drained at chunk boundaries.
+constexpr uint32_t kLdsAOwnCu = 128 * 1024;
 constexpr int kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
 constexpr int kNontemporal = 2;           // cache policy bits of the weight loads
 
@@ -336,6 +342,25 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
 //     <8,4,1> (M=8 N=11008 11.9 -> 11.1 us); below, <16,2,1> (M=8 N=4096
 //     6.9 -> 6.2 us).
 int mfma_variant(uint32_t NT) { return NT >= 1024 ? 0 : NT >= 512 ? 1 : 2; }
+
+// k extent (a multiple of 64) of one staged chunk of M activation rows: below
+// 512 strips both kernels run one 16-wave workgroup per strip, and when those
+// fit one per CU the chunk may take up to kLdsAOwnCu bytes.
+uint32_t chunk_k_for(uint32_t Kp, int M, uint32_t NT)
+{
+    const uint32_t budget = (NT < 512 && NT <= cu_count()) ? kLdsAOwnCu : kLdsA;
+    return std::min<uint32_t>(Kp, (budget / M) & ~63u);
+}
+
+// Dynamic LDS above 64 KiB needs the kernel's opt-in (once per kernel).
+template <auto Kernel>
+void lds_optin()
+{
+    static std::atomic<bool> done{false};
+    if (!done)
+        done = hipFuncSetAttribute(reinterpret_cast<const void *>(Kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   static_cast<int>(kLdsAOwnCu)) == hipSuccess;
+}
 uint32_t mfma_grid(uint32_t NT) { return mfma_variant(NT) == 0 ? (NT + 3) / 4 : NT; }
 
 template <int M>
@@ -348,32 +373,39 @@ void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t
         gemv_i8_mfma<M, 4, 4, 4><<<grid, 256, lds, s>>>(ps, grid0, chunk_k);
     else if (variant == 1)
         gemv_i8_mfma<M, 8, 4, 1><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
-    else
+    else {
+        lds_optin<gemv_i8_mfma<M, 16, 2, 1>>();
         gemv_i8_mfma<M, 16, 2, 1><<<grid, 1024, lds, s>>>(ps, grid0, chunk_k);
+    }
 }
 
 template <int M>
 void launch_m(hipStream_t s, const I8Gemm &p)
 {
     const uint32_t NT = p.Np >> 4;
-    const uint32_t chunk_k = std::min<uint32_t>(p.Kp, (kLdsA / M) & ~63u);
+    const uint32_t chunk_k = chunk_k_for(p.Kp, M, NT);
     const size_t lds = static_cast<size_t>(chunk_k) * M;
     if constexpr (M >= 5) {
         I8GemmPair ps;
         ps.p[0] = ps.p[1] = p;
         launch_mfma_pair<M>(s, ps, mfma_variant(NT), mfma_grid(NT), 0, chunk_k);
     } else if constexpr (M == 2) {
-        if (NT >= 512)
+        if (NT >= 512) {
             gemv_i8_kernel<M, 4, 2, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
-        else
+        } else {
+            lds_optin<gemv_i8_kernel<M, 16, 2, 1>>();
             gemv_i8_kernel<M, 16, 2, 1><<<dim3(NT), 1024, lds, s>>>(p, chunk_k);
+        }
     } else {
-        if (NT >= 512)
+        if (NT >= 512) {
             gemv_i8_kernel<M, 8, 2, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
-        else if constexpr (M == 1)
+        } else if constexpr (M == 1) {
+            lds_optin<gemv_i8_kernel<M, 16, 4, 1>>();
             gemv_i8_kernel<M, 16, 4, 1><<<dim3(NT), 1024, lds, s>>>(p, chunk_k);
-        else
+        } else {
+            lds_optin<gemv_i8_kernel<M, 16, 2, 1>>();
             gemv_i8_kernel<M, 16, 2, 1><<<dim3(NT), 1024, lds, s>>>(p, chunk_k);
+        }
     }
 }
 
@@ -399,7 +431,7 @@ bool gemv_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1)
     if (p0.M != p1.M || p0.M < 5 || p0.M > 8 || p0.Kp != p1.Kp) return false;
     const uint32_t nt0 = p0.Np >> 4, nt1 = p1.Np >> 4;
     if (mfma_variant(nt0) != mfma_variant(nt1)) return false;
-    const uint32_t chunk_k = std::min<uint32_t>(p0.Kp, (kLdsA / p0.M) & ~63u);
+    const uint32_t chunk_k = chunk_k_for(p0.Kp, p0.M, mfma_variant(nt0) == 2 ? nt0 + nt1 : 512);
     const I8GemmPair ps{{p0, p1}};
     switch (p0.M) {
     case 5: launch_mfma_pair<5>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;

@@ -30,6 +30,10 @@ void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint
                     uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,
                     int32_t *column_sums, uint8_t *zero_blocks);
 
+// Compute units of the current device (read once per process; 256 if the
+// query fails).  Launch shapes are chosen in whole rounds of these.
+uint32_t cu_count();
+
 // ---- MATMUL_I8 (gemv_i8.hip, gemm_i8.hip) ----
 struct I8Gemm {
     const int8_t *A = nullptr;   // [M][lda]
