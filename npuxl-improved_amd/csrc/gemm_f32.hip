@@ -280,8 +280,9 @@ __device__ __forceinline__ void split8(const float (&x)[8], v8bf &hi, v8bf &lo)
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const float c0 = fminf(fmaxf(x[2 * e], -kBf16Max), kBf16Max);
-        const float c1 = fminf(fmaxf(x[2 * e + 1], -kBf16Max), kBf16Max);
+        // one v_med3 each (fminf(fmaxf()) adds a NaN-quieting max per input)
+        const float c0 = __builtin_amdgcn_fmed3f(x[2 * e], -kBf16Max, kBf16Max);
+        const float c1 = __builtin_amdgcn_fmed3f(x[2 * e + 1], -kBf16Max, kBf16Max);
         hw[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f){c0, c1}, v2bf));
         const float h0 = __builtin_bit_cast(float, hw[e] << 16);
         const float h1 = __builtin_bit_cast(float, hw[e] & 0xFFFF0000u);
@@ -398,6 +399,9 @@ constexpr uint32_t kX3MaxLdc = (1u << 23) - 1;
 constexpr int kCBufferWord3 = 0x00020000;   // raw buffer, 32-bit data format
 constexpr int kCStorePolicy = 2;            // nontemporal: C is written once
 
+// EPI: the epilogue (0 none, 1 ReLU, 2 SiLU, 3 GELU); NB: C_in batches (the
+// loads of one batch of row tiles are all in flight before the first is used).
+template <int EPI, int NB>
 __device__ __forceinline__ void x3_store_rows(const F32Gemm &p, const v16f (&acc)[2][2], uint32_t mrow,
                                               uint32_t ncol, int h)
 {
@@ -417,29 +421,49 @@ __device__ __forceinline__ void x3_store_rows(const F32Gemm &p, const v16f (&acc
     auto at = [&](int i, int j, int r) {
         return static_cast<int>(off[j] + static_cast<uint32_t>(32 * i + 8 * (r >> 2) + (r & 3)) * ld4);
     };
-    float cin[2][2][16];
-    if (p.beta != 0.0f) {
+    constexpr int PER = 2 / NB;   // row tiles per batch
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+    for (int bt = 0; bt < NB; ++bt) {
+        float cin[PER][2][16];
+        if (p.beta != 0.0f) {
+#pragma unroll
+            for (int ii = 0; ii < PER; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        cin[ii][j][r] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rs, at(bt * PER + ii, j, r), 0, 0));
+        }
+#pragma unroll
+        for (int ii = 0; ii < PER; ++ii)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    cin[i][j][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, at(i, j, r), 0, 0));
+                for (int r = 0; r < 16; ++r) {
+                    const int i = bt * PER + ii;
+                    float out = p.alpha * acc[i][j][r];
+                    if (p.bias) out += bv[j];
+                    if (p.beta != 0.0f) out += p.beta * cin[ii][j][r];
+                    out = dev::epilogue(out, EPI);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), rs, at(i, j, r), 0,
+                                                          kCStorePolicy);
+                }
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float out = p.alpha * acc[i][j][r];
-                if (p.bias) out += bv[j];
-                if (p.beta != 0.0f) out += p.beta * cin[i][j][r];
-                out = dev::epilogue(out, p.epilogue);
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), rs, at(i, j, r), 0,
-                                                      kCStorePolicy);
-            }
+}
+
+// x3_store_rows with the epilogue chosen once per call.
+template <int NB>
+__device__ __forceinline__ void x3_store_rows_epi(const F32Gemm &p, const v16f (&acc)[2][2], uint32_t mrow,
+                                                  uint32_t ncol, int h)
+{
+    switch (p.epilogue) {
+    case 1: x3_store_rows<1, NB>(p, acc, mrow, ncol, h); break;
+    case 2: x3_store_rows<2, NB>(p, acc, mrow, ncol, h); break;
+    case 3:
+    case 4: x3_store_rows<3, NB>(p, acc, mrow, ncol, h); break;
+    default: x3_store_rows<0, NB>(p, acc, mrow, ncol, h); break;
+    }
 }
 
 // blockIdx.y selects the k range [y * k_per_split, + k_per_split) (a
@@ -537,7 +561,7 @@ __global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p, uint32_t k_pe
     // registers slowed its main loop, which small and split grids run.)
     if constexpr (WM == 4) {
         if (!ws && p.ldc <= kX3MaxLdc) {
-            x3_store_rows(p, acc, m0 + wm * 64, n0 + wn * 64 + col, h);
+            x3_store_rows_epi<1>(p, acc, m0 + wm * 64, n0 + wn * 64 + col, h);
             return;
         }
     }
@@ -556,6 +580,304 @@ __global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p, uint32_t k_pe
                 else
                     store_out(p, m, n, acc[i][j][r], false);
             }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Warp-specialised split-bf16 kernel (op(A) = A, 256 x 128 tiles).
+//
+// The lock-step kernel above has every wave load, split and store a stage
+// and then multiply between two barriers, so the matrix cores idle while the
+// splits run.  Here four producer waves (one per SIMD) load the f32 slices of
+// stage s + 2 and s + 1 into registers while they split stage s into a ring
+// of three LDS stages (the layout above), and four consumer waves (one per
+// SIMD) run only fragment reads and MFMAs, each owning a 128 x 64 block.
+// The two sides meet through per-wave LDS flags instead of barriers:
+// producer p sets prod[slot][p] = s + 1 once stage s is in the slot,
+// consumer c sets cons[slot][c] = s + 1 once it has read stage s, and a
+// producer refills a slot only when every consumer has released the stage
+// three before.  Every wait is bounded (after kWsMaxSpin polls it goes on,
+// so a protocol error shows as wrong results, never as a hung wave).
+// Operand loads are raw buffer loads over the whole matrix (out of range
+// reads return zero), rows past M / N are clamped and k past K is zeroed
+// with selects: no branch around a load, so the three stages of loads stay
+// in flight.
+// ---------------------------------------------------------------------------
+namespace ws {
+constexpr int TM = 256, TN = 128, BK = 32, kSlots = 3;
+constexpr int kPlaneA = TM * BK * 2, kPlaneB = TN * BK * 2;   // bytes of one bf16 plane
+constexpr int kSlotBytes = 2 * kPlaneA + 2 * kPlaneB;        // 48 KiB
+constexpr int kFlagOff = kSlots * kSlotBytes;                 // 144 KiB
+constexpr int kLds = kFlagOff + 2 * 4 * kSlots * 4;
+constexpr uint32_t kMaxSpin = 1u << 22;
+constexpr int kBufWord3 = 0x00020000;
+static_assert(kLds <= 160 * 1024, "ring + flags fit in LDS");
+}  // namespace ws
+
+// Flag words are read and written with asm: a volatile C++ access makes the
+// compiler drain every outstanding global load first (vmcnt(0)), which would
+// empty the producers' load pipeline at each poll.  The "memory" clobber keeps
+// the compiler from moving LDS accesses across them; one wave's LDS operations
+// execute in order, so data written before a flag is in place when the flag
+// is seen, and a consumer's reads of a stage precede its release.
+__device__ __forceinline__ uint32_t lds_addr(const uint32_t *p)
+{
+    return static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint32_t *)(p)));
+}
+
+// Waits until the four flags f[0..3] (one per wave of the other side) are at
+// least `target`.
+__device__ __forceinline__ void ws_wait(const uint32_t *f, uint32_t target)
+{
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const uint32_t a = lds_addr(f);
+    for (uint32_t spin = 0; spin < ws::kMaxSpin; ++spin) {
+        v4u v;
+        asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+        const uint32_t lo = min(min(v.x, v.y), min(v.z, v.w));
+        if (__builtin_amdgcn_readfirstlane(lo) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Publishes `v` after this wave's earlier LDS reads and writes completed.
+__device__ __forceinline__ void ws_release(uint32_t *f, uint32_t v)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\tds_write_b32 %0, %1" : : "v"(lds_addr(f)), "v"(v) : "memory");
+}
+
+// One producer thread's share of a stage: A (k-contiguous) 4 chunks of 8 k,
+// B 2 chunks (k-contiguous, TB) or 8 k x 2 adjacent columns (!TB).
+struct WsSlice {
+    float a[4][8];
+    float b[2][8];
+};
+
+__device__ __forceinline__ void put4(float *d, const float4 v)
+{
+    d[0] = v.x;
+    d[1] = v.y;
+    d[2] = v.z;
+    d[3] = v.w;
+}
+
+template <bool TB>
+__global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p)
+{
+    using ws::kSlots;
+    using ws::kSlotBytes;
+    using ws::kPlaneA;
+    using ws::kPlaneB;
+    using ws::kFlagOff;
+    using ws::TM;
+    using ws::TN;
+    constexpr uint32_t WBK = ws::BK;
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+    uint32_t *flags = reinterpret_cast<uint32_t *>(smem + kFlagOff);   // prod[slot][4], cons[slot][4]
+    uint32_t *prod = flags, *cons = flags + 4 * kSlots;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t tiles_m = (p.M + TM - 1) / TM, total = tiles_m * ((p.N + TN - 1) / TN);
+    uint32_t g = blockIdx.x;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const uint32_t m0 = (g % tiles_m) * TM, n0 = (g / tiles_m) * TN;
+    const uint32_t KT = (p.K + WBK - 1) / WBK;
+    if (tid < 2 * 4 * kSlots) flags[tid] = 0;
+    __syncthreads();
+
+    if (wave >= 4) {
+        // ---------------- producers ----------------
+        const int pw = wave - 4, pt = tid - 256;
+        const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(p.A), 0, static_cast<int>(static_cast<uint64_t>(p.M) * p.lda * 4), ws::kBufWord3);
+        const uint32_t brows = TB ? p.N : p.K;
+        const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(p.B), 0, static_cast<int>(static_cast<uint64_t>(brows) * p.ldb * 4), ws::kBufWord3);
+        // A item u: row pt/4 + 64u, chunk pt%4 (a wave reads 16 whole 128-byte row runs)
+        uint32_t a_off[4];
+        bool a_ok[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t r = (pt >> 2) + 64 * u, m = m0 + r;
+            a_ok[u] = m < p.M;
+            a_off[u] = (min(m, p.M - 1) * p.lda + 8 * (pt & 3)) * 4;
+        }
+        // B items: TB as A (rows pt/4 + 64u, u < 2); !TB rows 2(pt%64), +1 at chunk pt/64
+        uint32_t b_off[2];
+        bool b_ok[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (TB) {
+                const uint32_t n = n0 + (pt >> 2) + 64 * u;
+                b_ok[u] = n < p.N;
+                b_off[u] = (min(n, p.N - 1) * p.ldb + 8 * (pt & 3)) * 4;
+            } else {
+                // the float2 load starts at an even column (8-byte aligned rows: ldb % 4 == 0)
+                const uint32_t n = n0 + 2 * (pt & 63) + u;
+                b_ok[u] = n < p.N;
+                b_off[u] = min(n0 + 2 * (pt & 63), (p.N - 1) & ~1u) * 4;
+            }
+        }
+        auto load = [&](WsSlice &x, uint32_t s) {
+            const uint32_t k0 = min(s, KT - 1) * WBK;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int v = 0; v < 2; ++v)
+                    put4(&x.a[u][4 * v], __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                       ra, a_off[u] + (k0 + 4 * v) * 4, 0, 0)));
+            if (TB) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int v = 0; v < 2; ++v)
+                        put4(&x.b[u][4 * v], __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                           rb, b_off[u] + (k0 + 4 * v) * 4, 0, 0)));
+            } else {
+                // rows k0 + 8c + e (c = pt/64), columns 2(pt%64) and +1: a float2 per k
+                const uint32_t kc = k0 + 8 * (pt >> 6);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t kk = min(kc + e, p.K - 1);
+                    const float2 v2 = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                                     rb, kk * p.ldb * 4 + b_off[0], 0, 0));
+                    x.b[0][e] = v2.x;
+                    x.b[1][e] = v2.y;
+                }
+            }
+        };
+        // LDS byte offsets within a slot.  A rows pt/4 + 64u all have the
+        // swizzle (pt/16) & 3, so one base plus immediates (4096 u, the lo
+        // plane) places every chunk; B likewise (TB: rows pt/4 + 64u; !TB:
+        // rows 2(pt%64) + u, swizzle (pt%64)/2 & 3, 64 bytes apart).
+        const uint32_t a_lds = (pt >> 2) * (WBK * 2) + (((pt & 3) ^ ((pt >> 4) & 3)) << 4);
+        const uint32_t b_lds = TB ? a_lds
+                                  : 2 * (pt & 63) * (WBK * 2) + (((pt >> 6) ^ (((pt & 63) >> 1) & 3)) << 4);
+        constexpr uint32_t kBStep = TB ? 4096 : 64;
+        auto write = [&](const WsSlice &x, uint32_t slot) {
+            int8_t *sa = smem + slot * kSlotBytes + a_lds;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                v8bf h, l;
+                split8(x.a[u], h, l);
+                *reinterpret_cast<v8bf *>(sa + 4096 * u) = h;
+                *reinterpret_cast<v8bf *>(sa + kPlaneA + 4096 * u) = l;
+            }
+            int8_t *sb = smem + slot * kSlotBytes + 2 * kPlaneA + b_lds;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                v8bf h, l;
+                split8(x.b[u], h, l);
+                *reinterpret_cast<v8bf *>(sb + kBStep * u) = h;
+                *reinterpret_cast<v8bf *>(sb + kPlaneB + kBStep * u) = l;
+            }
+        };
+        // Rows past M / N and k past K read as zero: selects only on edge
+        // tiles and the last stage (uniform branch, no load inside it).
+        const bool edge = m0 + TM > p.M || n0 + TN > p.N;
+        auto put = [&](const WsSlice &x, uint32_t s) {
+            const uint32_t slot = s % kSlots;
+            const uint32_t k0 = s * WBK;
+            if (s >= kSlots) ws_wait(cons + 4 * slot, s - kSlots + 1);
+            if (edge || k0 + WBK > p.K) {
+                WsSlice y;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t kb = k0 + 8 * (pt & 3);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) y.a[u][e] = (a_ok[u] && kb + e < p.K) ? x.a[u][e] : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const uint32_t kb = k0 + 8 * (TB ? (pt & 3) : (pt >> 6));
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) y.b[u][e] = (b_ok[u] && kb + e < p.K) ? x.b[u][e] : 0.0f;
+                }
+                write(y, slot);
+            } else {
+                write(x, slot);
+            }
+            ws_release(prod + 4 * slot + pw, s + 1);
+        };
+        WsSlice x0, x1, x2;
+        load(x0, 0);
+        load(x1, 1);
+        for (uint32_t s = 0; s < KT; s += 3) {
+            load(x2, s + 2);
+            put(x0, s);
+            load(x0, s + 3);
+            if (s + 1 < KT) put(x1, s + 1);
+            load(x1, s + 4);
+            if (s + 2 < KT) put(x2, s + 2);
+        }
+        return;
+    }
+
+    // ---------------- consumers ----------------
+    const int cw = wave, wm = cw >> 1, wn = cw & 1;
+    const int h = lane >> 5, col = lane & 31;
+    struct Frag {
+        v8bf ah[4], al[4], bh[2], bl[2];
+    };
+    // Rows wm*128 + 32i + col of A and wn*64 + 32j + col of B all have the
+    // swizzle (col/4) & 3: per k16 step one lane base each, row tiles and
+    // planes are immediates.
+    uint32_t a_lane[2], b_lane[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+        const uint32_t sw = (((2 * s2 + h) ^ ((col >> 2) & 3)) << 4);
+        a_lane[s2] = (wm * 128 + col) * (WBK * 2) + sw;
+        b_lane[s2] = 2 * kPlaneA + (wn * 64 + col) * (WBK * 2) + sw;
+    }
+    auto read = [&](Frag &f, uint32_t s, int s2) {
+        const int8_t *pa = smem + (s % kSlots) * kSlotBytes + a_lane[s2];
+        const int8_t *pb = smem + (s % kSlots) * kSlotBytes + b_lane[s2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f.ah[i] = *reinterpret_cast<const v8bf *>(pa + 2048 * i);
+            f.al[i] = *reinterpret_cast<const v8bf *>(pa + kPlaneA + 2048 * i);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f.bh[j] = *reinterpret_cast<const v8bf *>(pb + 2048 * j);
+            f.bl[j] = *reinterpret_cast<const v8bf *>(pb + kPlaneB + 2048 * j);
+        }
+    };
+    v16f acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16f){0.f};
+    auto mma = [&](const Frag &f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.al[i], f.bh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.ah[i], f.bl[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.ah[i], f.bh[j], acc[i][j], 0, 0, 0);
+            }
+    };
+    Frag f0, f1;
+    ws_wait(prod, 1);
+    read(f0, 0, 0);
+    for (uint32_t s = 0; s < KT; ++s) {
+        read(f1, s, 1);
+        mma(f0);
+        ws_release(cons + 4 * (s % kSlots) + cw, s + 1);
+        if (s + 1 < KT) {
+            ws_wait(prod + 4 * ((s + 1) % kSlots), s + 2);
+            read(f0, s + 1, 0);
+        }
+        mma(f1);
+    }
+    // Rows wm*128 + 64q .. +63 of the block: the split-bf16 kernel's register
+    // epilogue, twice.
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const v16f part[2][2] = {{acc[2 * q][0], acc[2 * q][1]}, {acc[2 * q + 1][0], acc[2 * q + 1][1]}};
+        x3_store_rows_epi<2>(p, part, m0 + wm * 128 + 64 * q, n0 + wn * 64 + col, h);
     }
 }
 
@@ -794,6 +1116,7 @@ static uint32_t gemm_f32_splits(const F32Gemm &p)
 // in slice order by a second pass.
 struct X3Plan {
     bool x3 = false;
+    bool ws = false;   // the warp-specialised 256 x 128 kernel (op(A) = A)
     int wm = 2;
     uint32_t splits = 1, kps = 0;
 };
@@ -811,7 +1134,13 @@ static X3Plan x3_plan(const F32Gemm &p)
     // workgroup splits an A slice once for 128 columns and a B slice once
     // for 256 rows (a quarter less conversion per MFMA).
     const uint64_t tiles256 = static_cast<uint64_t>((p.M + 255) / 256) * ((p.N + x3::TN - 1) / x3::TN);
-    if (tiles256 >= 256) x.wm = 4;
+    if (tiles256 >= 256) {
+        x.wm = 4;
+        // The warp-specialised kernel reads A and B through 31-bit buffer ranges.
+        const uint64_t a_bytes = static_cast<uint64_t>(p.M) * p.lda * 4;
+        const uint64_t b_bytes = static_cast<uint64_t>(p.trans_b ? p.N : p.K) * p.ldb * 4;
+        x.ws = !p.trans_a && a_bytes < (1ull << 31) && b_bytes < (1ull << 31);
+    }
     if (tiles >= 128) return x;
     uint32_t want = 1;
     while (tiles * want < 128 && p.K / (want * 2) >= 2 * x3::BK) want *= 2;
@@ -864,6 +1193,18 @@ static void splitk_reduce(hipStream_t s, const F32Gemm &p, const float *ws, uint
 void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
 {
     const X3Plan x = x3_plan(p);
+    if (x.ws) {
+        static std::atomic<bool> lds_optin{false};  // launches may come from several host threads
+        if (!lds_optin)
+            lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_ws<false>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, ws::kLds) == hipSuccess &&
+                        hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_ws<true>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, ws::kLds) == hipSuccess;
+        const dim3 grid(((p.N + ws::TN - 1) / ws::TN) * ((p.M + ws::TM - 1) / ws::TM));
+        if (p.trans_b) gemm_f32_ws<true><<<grid, 512, ws::kLds, s>>>(p);
+        else gemm_f32_ws<false><<<grid, 512, ws::kLds, s>>>(p);
+        return;
+    }
     if (x.x3) {
         if (x.wm == 4) launch_x3<4>(s, p, x, ws);
         else launch_x3<2>(s, p, x, ws);
