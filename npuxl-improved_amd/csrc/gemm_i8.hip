@@ -704,15 +704,42 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
         // s+1 and, in the first six, one copy instruction of stage s+2.  The
         // ring buffer the copy refills held stage s-1, whose fragments every
         // wave read before this barrier.
-        auto issue_one = [&](uint32_t st_i, int j) {
-            int8_t *st = smem + (st_i % kStages) * kStageBytes;
+        //
+        // Copy addresses: wave-uniform bases (SGPRs, advanced per stage by
+        // scalar adds) plus one 32-bit per-lane offset each.  A instruction j
+        // copies rows rb .. rb+7 (rb = 8(4 wave + j) in the tile); lane rows
+        // past M are clamped to M - 1 and so is the base row, so a lane's
+        // offset stays below 8 lda.
+        const int8_t *a_base[kAPer];
+        uint32_t a_lo[kAPer];
+#pragma unroll
+        for (int j = 0; j < kAPer; ++j) {
+            const uint32_t rb = (wave * kAPer + j) * 8;
+            const uint32_t r = rb + (lane >> 3);
+            const uint32_t brow = min(m0 + rb, p.M - 1);
+            const uint32_t row = min(m0 + r, p.M - 1);
+            a_base[j] = p.A + static_cast<uint64_t>(brow) * p.lda;
+            a_lo[j] = (row - brow) * p.lda + 16 * ((lane & 7) ^ ((r >> 1) & 7));
+        }
+        const int8_t *b_base[kBPer];
+#pragma unroll
+        for (int j = 0; j < kBPer; ++j) {
+            const int bi = wave * kBPer + j;
+            const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
+            b_base[j] = p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10);
+        }
+        const uint32_t b_lo = lane * 16;
+        // Copy instruction j of stage st_i into ring slot `slot`.
+        auto issue_one = [&](uint32_t st_i, uint32_t slot, int j) {
+            int8_t *st = smem + slot * kStageBytes;
             if (j < kAPer)
-                dma16(src[j] + st_i * SK, st + (wave * kAPer + j) * 1024);
+                dma16_s(a_base[j] + st_i * SK, a_lo[j], st + (wave * kAPer + j) * 1024);
             else
-                dma16(src[j] + static_cast<uint64_t>(st_i) * 2048, st + kBOff + (wave * kBPer + j - kAPer) * 1024);
+                dma16_s(b_base[j - kAPer] + static_cast<uint64_t>(st_i) * 2048, b_lo,
+                        st + kBOff + (wave * kBPer + j - kAPer) * 1024);
         };
-        auto read_one = [&](uint32_t st_i, Frags &f, int k) {
-            const int8_t *st = smem + (st_i % kStages) * kStageBytes;
+        auto read_one = [&](uint32_t slot, Frags &f, int k) {
+            const int8_t *st = smem + slot * kStageBytes;
             const int h = k / 6, r = k % 6;
             if (r == 0 || r == 5) {
                 const int nb = r == 5;
@@ -726,8 +753,11 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
                 f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_off[mb] + ((c ^ ((row >> 1) & 7)) << 4));
             }
         };
-        auto step = [&](const Frags &cur, Frags &nxt, uint32_t s) {
-            const bool more = s + 1 < KS, dma = s + 2 < KS;
+        // Stage s: multiply `cur`, read stage s+1 (ring slot rd) into `nxt`
+        // and copy stage s+2 into ring slot cp.  `more` (s+1 < KS) and `dma`
+        // (s+2 < KS) are compile-time true in the steady-state loop, which
+        // then has no branch.
+        auto step = [&](const Frags &cur, Frags &nxt, uint32_t s, uint32_t rd, uint32_t cp, bool more, bool dma) {
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
                 const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
@@ -737,28 +767,41 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
                     block_barrier();
                 }
                 if (k >= 4 && more) {
-                    if (dma && k - 4 < kLoads) issue_one(s + 2, k - 4);
-                    read_one(s + 1, nxt, k - 4);
+                    if (dma && k - 4 < kLoads) issue_one(s + 2, cp, k - 4);
+                    read_one(rd, nxt, k - 4);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
         Frags f0, f1;
-        issue(0);
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) issue_one(0, 0, j);
         if (KS > 1) {
-            issue(1);
+#pragma unroll
+            for (int j = 0; j < kLoads; ++j) issue_one(1, 1, j);
             wait_vmcnt<kLoads>();
         } else {
             wait_vmcnt<0>();
         }
         block_barrier();
-        read_frags(0, f0);
+#pragma unroll
+        for (int k = 0; k < 12; ++k) read_one(0, f0, k);
+        // Six stages per trip (a multiple of both the ring depth and the two
+        // fragment sets), so every ring slot is a constant.
         uint32_t s = 0;
-        for (; s + 1 < KS; s += 2) {
-            step(f0, f1, s);
-            step(f1, f0, s + 1);
+        for (; s + 7 < KS; s += 6) {
+            step(f0, f1, s, 1, 2, true, true);
+            step(f1, f0, s + 1, 2, 0, true, true);
+            step(f0, f1, s + 2, 0, 1, true, true);
+            step(f1, f0, s + 3, 1, 2, true, true);
+            step(f0, f1, s + 4, 2, 0, true, true);
+            step(f1, f0, s + 5, 0, 1, true, true);
         }
-        if (s < KS) step(f0, f1, s);
+        for (; s + 1 < KS; s += 2) {
+            step(f0, f1, s, (s + 1) % kStages, (s + 2) % kStages, true, s + 2 < KS);
+            step(f1, f0, s + 1, (s + 2) % kStages, (s + 3) % kStages, s + 2 < KS, s + 3 < KS);
+        }
+        if (s < KS) step(f0, f1, s, (s + 1) % kStages, (s + 2) % kStages, false, false);
     }
 
     // Waves w and w+4 hold the two k halves of the same 128 x 64 block.
@@ -1142,7 +1185,9 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
     const bool aligned = (p.K % 64 == 0) && (p.lda % 16 == 0) &&
                          (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64 &&
                          p.K <= 16384;
-    const bool k128 = aligned && p.K % pipe128::SK == 0 && p.ldc <= kRegStoreMaxLdc;
+    // The 128-deep kernels address 8 rows of A per copy as a 32-bit lane
+    // offset from a uniform base (below 8 lda).
+    const bool k128 = aligned && p.K % pipe128::SK == 0 && p.ldc <= kRegStoreMaxLdc && p.lda < (1u << 29);
     const bool wide_ok = k128 && p.M % wide::TM == 0;
     const uint32_t wm_ = p.M / wide::TM;
     const uint32_t wn256 = (p.N + 255) / 256, wn192 = (p.N + 191) / 192;

@@ -121,6 +121,28 @@ def test_matmul_i8_wide_tile(gpu, M, K, N):
     assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("M,KS", [(321, 1), (300, 2), (321, 3), (300, 5), (321, 7), (300, 8), (321, 9),
+                                  (300, 13), (321, 14), (300, 15)])
+def test_matmul_i8_eight_wave_k_depths(gpu, M, KS):
+    """Row tiles that are not whole 256-row tiles take the 8-wave kernel of
+    128-deep stages; its loop runs six stages per trip and finishes the
+    remaining one to seven stages separately, so each stage count from 1 to
+    15 that ends in a different remainder is covered, with row clamping in
+    the last row tile (M - 256 rows, not a multiple of 8).  Bit-exact
+    against the exact float64 accumulator."""
+    K, N = 128 * KS, 200
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    w = gpu.pack(B, K, N, scales=sb)
+    got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa)
+    gpu.release_packed(w)
+    acc = A.astype(np.float64) @ B.astype(np.float64)
+    want = (acc.astype(np.float32) * sa[:, None]) * sb[None, :]
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
 @pytest.mark.parametrize("M,N0,N1,alias", [(512, 3000, 2000, False), (512, 11008, 11008, False),
                                            (512, 1000, 700, True), (8, 11008, 11008, False),
                                            (6, 3000, 2000, False), (8, 1000, 700, True),
