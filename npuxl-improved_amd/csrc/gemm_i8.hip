@@ -466,11 +466,12 @@ static_assert(pipe::kOut + TM * 4 <= static_cast<int>(kLds), "staged tile + row 
 // has a second wave to issue MFMAs whenever the other waits on its fragment
 // reads or the barrier.  The two partial accumulators are summed through LDS
 // (exact int32) before the shared epilogue.
-//   * 3 LDS stages; stage s+2 is copied while stage s is multiplied; each
-//     wave issues 6 of the 48 DMA instructions of a stage;
-//   * per stage and wave: vmcnt wait for its own copy of stage s, one
-//     barrier (stage s visible; stage s-1's buffer free), 12 fragment reads,
-//     16 MFMAs that each wait only for their own operands.
+//   * 3 LDS stages; stage s+3 is copied while stage s is multiplied (the
+//     dense kernel: two stages in flight; the zero-map kernel copies stage
+//     s+2); each wave issues 6 of the 48 DMA instructions of a stage;
+//   * per stage and wave: vmcnt wait for its own copy of the stage to be
+//     read, one barrier, 12 fragment reads, 16 MFMAs that each wait only
+//     for their own operands.
 // ---------------------------------------------------------------------------
 namespace w8 {
 constexpr int kThreads8 = 512;
@@ -699,11 +700,12 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
     } else {
         // Software-pipelined: stage s's 16 MFMAs run from fragments read
         // during stage s-1; after the first four, one wait + barrier makes
-        // stage s+1 visible (its copy was issued a stage earlier), and the
-        // remaining twelve MFMA slots each carry one fragment read of stage
-        // s+1 and, in the first six, one copy instruction of stage s+2.  The
-        // ring buffer the copy refills held stage s-1, whose fragments every
-        // wave read before this barrier.
+        // stage s+1 visible (its copy was issued two stages earlier; stage
+        // s+2's copy stays in flight), and the remaining twelve MFMA slots
+        // each carry one fragment read of stage s+1 and, in the first six,
+        // one copy instruction of stage s+3.  That copy refills the ring slot
+        // of stage s itself: every wave read stage s's fragments during stage
+        // s-1 and waited for them before this barrier.
         //
         // Copy addresses: wave-uniform bases (SGPRs, advanced per stage by
         // scalar adds) plus one 32-bit per-lane offset each.  A instruction j
@@ -754,54 +756,67 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
             }
         };
         // Stage s: multiply `cur`, read stage s+1 (ring slot rd) into `nxt`
-        // and copy stage s+2 into ring slot cp.  `more` (s+1 < KS) and `dma`
-        // (s+2 < KS) are compile-time true in the steady-state loop, which
-        // then has no branch.
-        auto step = [&](const Frags &cur, Frags &nxt, uint32_t s, uint32_t rd, uint32_t cp, bool more, bool dma) {
+        // and copy stage s+3 into ring slot s % 3 (cp).  more: s+1 < KS;
+        // ahead: stage s+2 was copied (s+2 < KS), so its copy may stay in
+        // flight while stage s+1's is waited for; dma: s+3 < KS.  All three
+        // are compile-time true in the steady-state loops, which then have no
+        // branch.
+        auto step = [&](const Frags &cur, Frags &nxt, uint32_t s, uint32_t rd, uint32_t cp, bool more, bool ahead,
+                        bool dma) {
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
                 const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[h][i], cur.b[h][j], acc[i][j], 0, 0, 0);
                 if (k == 3 && more) {
-                    wait_vmcnt<0>();
+                    if (ahead)
+                        wait_vmcnt<kLoads>();
+                    else
+                        wait_vmcnt<0>();
                     block_barrier();
                 }
                 if (k >= 4 && more) {
-                    if (dma && k - 4 < kLoads) issue_one(s + 2, cp, k - 4);
+                    if (dma && k - 4 < kLoads) issue_one(s + 3, cp, k - 4);
                     read_one(rd, nxt, k - 4);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
         Frags f0, f1;
+        const uint32_t pre = min(KS, static_cast<uint32_t>(kStages));
+        for (uint32_t st_i = 0; st_i < pre; ++st_i) {
 #pragma unroll
-        for (int j = 0; j < kLoads; ++j) issue_one(0, 0, j);
-        if (KS > 1) {
-#pragma unroll
-            for (int j = 0; j < kLoads; ++j) issue_one(1, 1, j);
-            wait_vmcnt<kLoads>();
-        } else {
-            wait_vmcnt<0>();
+            for (int j = 0; j < kLoads; ++j) issue_one(st_i, st_i, j);
         }
+        if (pre == 3)
+            wait_vmcnt<2 * kLoads>();
+        else if (pre == 2)
+            wait_vmcnt<kLoads>();
+        else
+            wait_vmcnt<0>();
         block_barrier();
 #pragma unroll
         for (int k = 0; k < 12; ++k) read_one(0, f0, k);
         // Six stages per trip (a multiple of both the ring depth and the two
-        // fragment sets), so every ring slot is a constant.
+        // fragment sets), so every ring slot is a constant; then pairs of
+        // stages with every flag still true; then the last stages.
         uint32_t s = 0;
-        for (; s + 7 < KS; s += 6) {
-            step(f0, f1, s, 1, 2, true, true);
-            step(f1, f0, s + 1, 2, 0, true, true);
-            step(f0, f1, s + 2, 0, 1, true, true);
-            step(f1, f0, s + 3, 1, 2, true, true);
-            step(f0, f1, s + 4, 2, 0, true, true);
-            step(f1, f0, s + 5, 0, 1, true, true);
+        for (; s + 8 < KS; s += 6) {
+            step(f0, f1, s, 1, 0, true, true, true);
+            step(f1, f0, s + 1, 2, 1, true, true, true);
+            step(f0, f1, s + 2, 0, 2, true, true, true);
+            step(f1, f0, s + 3, 1, 0, true, true, true);
+            step(f0, f1, s + 4, 2, 1, true, true, true);
+            step(f1, f0, s + 5, 0, 2, true, true, true);
+        }
+        for (; s + 4 < KS; s += 2) {
+            step(f0, f1, s, (s + 1) % kStages, s % kStages, true, true, true);
+            step(f1, f0, s + 1, (s + 2) % kStages, (s + 1) % kStages, true, true, true);
         }
         for (; s + 1 < KS; s += 2) {
-            step(f0, f1, s, (s + 1) % kStages, (s + 2) % kStages, true, s + 2 < KS);
-            step(f1, f0, s + 1, (s + 2) % kStages, (s + 3) % kStages, s + 2 < KS, s + 3 < KS);
+            step(f0, f1, s, (s + 1) % kStages, s % kStages, true, s + 2 < KS, s + 3 < KS);
+            step(f1, f0, s + 1, (s + 2) % kStages, (s + 1) % kStages, s + 2 < KS, s + 3 < KS, s + 4 < KS);
         }
-        if (s < KS) step(f0, f1, s, (s + 1) % kStages, (s + 2) % kStages, false, false);
+        if (s < KS) step(f0, f1, s, 0, 0, false, false, false);
     }
 
     // Waves w and w+4 hold the two k halves of the same 128 x 64 block.
