@@ -354,9 +354,14 @@ def bench_config5(s: Session, steps: int):
     s.run(abi.OP_QUANTIZE_I8, X=bx, Y=a8, scales=sa, rows=M, cols=K, axis=abi.QUANT_PER_ROW)
     s.free(bx)
     mk = lambda i: s.command(abi.OP_MATMUL_I8, id=i, A=a8, B=packed, scale_a=sa, C=c, M=M, K=K, N=N)
-    _, gpu_ns = timed(s, mk, steps, 3)
     mkd = lambda i: s.command(abi.OP_MATMUL_I8, id=i, A=a8, B=dense_w, scale_a=sa, C=c, M=M, K=K, N=N)
-    _, dense_ns = timed(s, mkd, steps, 3)
+    # Culled and dense runs alternate (the chip's clock drifts with its
+    # temperature over a run); each figure is the median of its rounds.
+    cul, den = [], []
+    for _ in range(3):
+        cul.append(timed(s, mk, max(1, steps // 3), 3)[1])
+        den.append(timed(s, mkd, max(1, steps // 3), 3)[1])
+    gpu_ns, dense_ns = float(np.median(cul)), float(np.median(den))
     s.release_packed(packed)
     s.release_packed(dense_w)
     for b in (a8, sa, c):

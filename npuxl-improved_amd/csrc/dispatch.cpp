@@ -493,7 +493,6 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     require(p.lda >= in.K && p.ldc >= in.N, "invalid int8 leading dimensions");
     p.frag = w->frag;
     // The zero-block map only costs lookups when there are zero blocks.
-    p.zero_blocks = w->zero_block_count ? w->zero_blocks : nullptr;
     p.Kp = w->Kp;
     p.Np = w->Np;
     p.scale_b = w->scales_dev;
@@ -558,7 +557,6 @@ bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t
             return false;
         k::I8Gemm &q = p[i];
         q.A = a.A; q.lda = lda; q.frag = w->frag;
-        q.zero_blocks = w->zero_block_count ? w->zero_blocks : nullptr;
         q.Kp = w->Kp; q.Np = w->Np; q.scale_a = a.scale_a; q.scale_b = w->scales_dev; q.bias = a.bias;
         q.C = a.C; q.ldc = ldc; q.M = a.M; q.N = a.N; q.K = a.K; q.epilogue = a.epilogue; q.variant = variant;
         auto range = [](const void *ptr, size_t bytes) {
@@ -1083,7 +1081,6 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
     VNPU_HIP(hipMalloc(&w->frag, w->frag_bytes));
     register_device_range(w->frag, w->frag_bytes);
     VNPU_HIP(hipMalloc(&w->scales_dev, static_cast<size_t>(w->Np) * 4));
-    VNPU_HIP(hipMalloc(&w->zero_blocks, blocks));
     int32_t *sums_dev = nullptr;
     VNPU_HIP(hipMalloc(&sums_dev, static_cast<size_t>(N) * 4));
     std::unique_ptr<int32_t, hipError_t (*)(void *)> sums_guard(sums_dev, hipFree);
@@ -1095,7 +1092,7 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
     const size_t b_bytes = trans_b ? span(N, K, ld, 1) : span(K, N, ld, 1);
     Stager sg(st);
     const int8_t *Bd = sg.in(B, b_bytes);
-    k::pack_fragments(st, Bd, K, N, ld, trans_b, w->frag, w->Kp, w->Np, sums_dev, w->zero_blocks);
+    k::pack_fragments(st, Bd, K, N, ld, trans_b, w->frag, w->Kp, w->Np, sums_dev);
     VNPU_HIP(hipGetLastError());
 
     // Scales: NULL keeps 1.0 (the reference does not derive them, F5 of its
@@ -1114,10 +1111,6 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
     w->column_sums.assign(w->Np, 0);
     VNPU_HIP(hipMemcpy(w->column_sums.data(), sums_dev, static_cast<size_t>(N) * 4,
                        hipMemcpyDeviceToHost));
-    std::vector<uint8_t> zb(blocks);
-    VNPU_HIP(hipMemcpy(zb.data(), w->zero_blocks, blocks, hipMemcpyDeviceToHost));
-    w->zero_block_count = 0;
-    for (uint8_t z : zb) w->zero_block_count += z;
     sg.finish();
     VNPU_HIP(hipStreamSynchronize(st));
     dev->dma_bytes.fetch_add(static_cast<uint64_t>(K) * N * 2);
@@ -1132,7 +1125,6 @@ void destroy_packed(vnpu_packed_weights_t *w)
         (void)hipFree(w->frag);
     }
     if (w->scales_dev) (void)hipFree(w->scales_dev);
-    if (w->zero_blocks) (void)hipFree(w->zero_blocks);
     delete w;
 }
 

@@ -6,14 +6,13 @@
 // then C = epi(((float)acc * scale_a[m]) * scale_b[n] + bias[n]).
 //
 // Kernels, chosen by gemm_i8() at the end of the file:
-//   * gemm_i8_wide   - 256 x 256 tiles, dense weights, M % 256 == 0,
-//                      K % 128 == 0, >= 256 tiles;
+//   * gemm_i8_wide   - 256 x 256 (or 192) tiles, M % 256 == 0,
+//                      K % 128 == 0, when whole rounds of tiles favour them;
 //   * gemm_i8_k128w8 - 256 x 128 tiles, 8 waves, K % 128 == 0;
 //   * gemm_i8_pipe   - 256 x 128 tiles, 64-deep stages, K % 64 == 0;
 //   * gemm_i8_generic - any shape and alignment (below).
 // All of them multiply int8 fragments read from the packed weight layout and
-// accumulate exactly in int32; a 64-deep weight block known to be all zero
-// (PACK_WEIGHTS_I8's zero map) may be skipped: exact, it only adds zeros.
+// accumulate exactly in int32.
 //
 // Generic kernel: workgroup tile BM x BN = 128 x 128, 4 waves in a 2 x 2
 // grid, wave tile 64 x 64 = 4 x 4 v_mfma_i32_16x16x64_i8 blocks; A staged
@@ -86,7 +85,6 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_generic(I8Gemm p)
         for (int j = 0; j < 4; ++j) {
             const uint32_t nb = nbase + j;
             z[j] = nb >= NT;
-            if (!z[j] && p.zero_blocks) z[j] = p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] != 0;
             b[j] = (v4i){0, 0, 0, 0};
             if (!z[j])
                 b[j] = *reinterpret_cast<const v4i *>(p.frag + ((static_cast<uint64_t>(nb) * KT + kt) << 10) + lane * 16);
@@ -259,7 +257,6 @@ __device__ void store_tile(const I8Gemm &p, const int32_t *tile, const float *sa
     }
 }
 
-template <bool kSkip>
 __global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
 {
     using pipe::kABlocks;
@@ -323,17 +320,6 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tile
         }
     };
 
-    // All-zero weight-block flags of this tile's 8 column blocks, staged once
-    // in LDS (after the ring) so the k loop never waits on a global load.
-    uint8_t *zflags = reinterpret_cast<uint8_t *>(smem + pipe::kLds);
-    if (kSkip) {
-        for (uint32_t i = tid; i < KT * kBBlocks; i += kThreads) {
-            const uint32_t kt = i / kBBlocks, nb = (n0 >> 4) + (i % kBBlocks);
-            zflags[i] = nb < NT ? p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] : 1;
-        }
-        __syncthreads();
-    }
-
     v16i acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -342,14 +328,7 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tile
 
     // 32x32x32 rather than 16x16x64: at one wave per SIMD it keeps the int8
     // matrix pipe ~85% busy where the 16x16 shape issues at ~55%.
-    // A wave's 64 columns x 64 k of all-zero weights add nothing: the MFMAs
-    // of such a step are skipped (wave-uniform).  The flag is read before the
-    // next stage's fragments so waiting for it never waits for those.
-    auto zero_step = [&](uint32_t kt) -> bool {
-        return kSkip && *reinterpret_cast<const uint32_t *>(zflags + kt * kBBlocks + wn * 4) == 0x01010101u;
-    };
-    auto mma = [&](const Frags &f, bool skip) {
-        if (skip) return;
+    auto mma = [&](const Frags &f) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -377,36 +356,37 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tile
     // sched_barrier(0) keeps the three phases of a step in order: the
     // compiler would otherwise pull the next stage's reads into the MFMA
     // sequence and stall it on lgkmcnt.
-    // A step's zero flag is read right after the previous step's MFMAs, so
-    // the next barrier's LDS drain covers it.
     uint32_t kt = 0;
-    bool sk0 = zero_step(0), sk1 = false;
     for (; kt + kStages + 1 < KT; kt += 2) {
         wait_vmcnt<(kStages - 2) * kLoads>();
         block_barrier();
         issue(kt + kStages);
         read_frags(kt + 1, f1);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, sk0);
-        sk1 = zero_step(kt + 1);
+        mma(f0);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<(kStages - 2) * kLoads>();
         block_barrier();
         issue(kt + 1 + kStages);
         read_frags(kt + 2, f0);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f1, sk1);
-        sk0 = zero_step(kt + 2);
+        mma(f1);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // Drain: every remaining stage is already issued; wait for all of it once.
+    // Drain.  The loop has issued stages up to kt + 5; with an odd KT (every
+    // K % 128 == 64 this kernel takes) stage kt + 6 = KT - 1 is still to be
+    // copied, into the slot of stage kt once every wave has read stage kt's
+    // fragments.  Then wait for all of it once.
+    if (kt + kStages < KT) {
+        block_barrier();
+        issue(kt + kStages);
+    }
     wait_vmcnt<0>();
     block_barrier();
-    mma(f0, sk0);
+    mma(f0);
     for (++kt; kt < KT; ++kt) {
-        const bool sk = zero_step(kt);
         read_frags(kt, f1);
-        mma(f1, sk);
+        mma(f1);
     }
 
     // Stage the accumulators row-major (32x32 block: lane l holds column
@@ -466,9 +446,9 @@ static_assert(pipe::kOut + TM * 4 <= static_cast<int>(kLds), "staged tile + row 
 // has a second wave to issue MFMAs whenever the other waits on its fragment
 // reads or the barrier.  The two partial accumulators are summed through LDS
 // (exact int32) before the shared epilogue.
-//   * 3 LDS stages; stage s+3 is copied while stage s is multiplied (the
-//     dense kernel: two stages in flight; the zero-map kernel copies stage
-//     s+2); each wave issues 6 of the 48 DMA instructions of a stage;
+//   * 3 LDS stages; stage s+3 is copied while stage s is multiplied (two
+//     stages in flight); each wave issues 6 of the 48 DMA instructions of a
+//     stage;
 //   * per stage and wave: vmcnt wait for its own copy of the stage to be
 //     read, one barrier, 12 fragment reads, 16 MFMAs that each wait only
 //     for their own operands.
@@ -580,7 +560,6 @@ __device__ __forceinline__ void xchg_put(const v16i (&acc)[4][2], v4i *dst, int 
             }
 }
 
-template <bool kSkip>
 __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32_t tiles_m, uint32_t tiles_n)
 {
     using pipe128::kBOff;
@@ -607,33 +586,7 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
     const uint32_t m0 = tmi * TM, n0 = tni * TN;
     const uint32_t NT = p.Np >> 4;
     const uint32_t KS = p.K / SK;
-    const uint32_t KT = p.K >> 6;
     const uint64_t KTp = p.Kp >> 6;
-
-    // DMA sources: A instructions 4*wave + j (8 rows each), B instructions
-    // 2*wave + j (column block bi/2, k block bi%2).
-    const int8_t *src[kLoads];
-#pragma unroll
-    for (int j = 0; j < kAPer; ++j) {
-        const uint32_t r = (wave * kAPer + j) * 8 + (lane >> 3);
-        const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);
-        const uint32_t row = min(m0 + r, p.M - 1);
-        src[j] = p.A + static_cast<uint64_t>(row) * p.lda + c * 16;
-    }
-#pragma unroll
-    for (int j = 0; j < kBPer; ++j) {
-        const int bi = wave * kBPer + j;
-        const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
-        src[kAPer + j] = p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + lane * 16;
-    }
-    auto issue = [&](uint32_t s) {
-        int8_t *st = smem + (s % kStages) * kStageBytes;
-#pragma unroll
-        for (int j = 0; j < kAPer; ++j) dma16(src[j] + s * SK, st + (wave * kAPer + j) * 1024);
-#pragma unroll
-        for (int j = 0; j < kBPer; ++j)
-            dma16(src[kAPer + j] + static_cast<uint64_t>(s) * 2048, st + kBOff + (wave * kBPer + j) * 1024);
-    };
 
     // Fragment reads of half gk of a stage, in MFMA consumption order.
     const int sub = (lane >> 4) & 1;
@@ -643,33 +596,6 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
         const uint32_t r = wm * 128 + mb * 32 + (lane & 31);
         a_off[mb] = r * 128;
     }
-    auto read_frags = [&](uint32_t s, Frags &f) {
-        const int8_t *st = smem + (s % kStages) * kStageBytes;
-#pragma unroll
-        for (int k = 0; k < 12; ++k) {
-            const int h = k / 6, r = k % 6;
-            if (r == 0 || r == 5) {
-                const int nb = r == 5;
-                const int boff = kBOff + (((wn * 4 + sub) * 2 + gk) << 10) +
-                                 (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
-                f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
-            } else {
-                const int mb = r - 1;
-                const uint32_t row = wm * 128 + mb * 32 + (lane & 31);
-                const uint32_t c = 4 * gk + 2 * h + (lane >> 5);
-                f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_off[mb] + ((c ^ ((row >> 1) & 7)) << 4));
-            }
-        }
-    };
-
-    uint8_t *zflags = reinterpret_cast<uint8_t *>(smem + pipe128::kLds);
-    if (kSkip) {
-        for (uint32_t i = tid; i < KT * pipe::kBBlocks; i += w8::kThreads8) {
-            const uint32_t kt = i / pipe::kBBlocks, nb = (n0 >> 4) + (i % pipe::kBBlocks);
-            zflags[i] = nb < NT ? p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] : 1;
-        }
-        __syncthreads();
-    }
 
     v16i acc[4][2];
 #pragma unroll
@@ -677,147 +603,125 @@ __global__ __launch_bounds__(w8::kThreads8) void gemm_i8_k128w8(I8Gemm p, uint32
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = (v16i){0};
 
-    if constexpr (kSkip) {
-        issue(0);
-        if (KS > 1) issue(1);
-        for (uint32_t s = 0; s < KS; ++s) {
-            if (s + 1 < KS) wait_vmcnt<kLoads>();
-            else wait_vmcnt<0>();
-            block_barrier();
-            if (s + 2 < KS) issue(s + 2);
-            const bool skip = *reinterpret_cast<const uint32_t *>(zflags + (2 * s + gk) * pipe::kBBlocks + wn * 4) ==
-                              0x01010101u;
-            if (!skip) {
-                Frags f;
-                read_frags(s, f);
+    // Software-pipelined: stage s's 16 MFMAs run from fragments read
+    // during stage s-1; after the first four, one wait + barrier makes
+    // stage s+1 visible (its copy was issued two stages earlier; stage
+    // s+2's copy stays in flight), and the remaining twelve MFMA slots
+    // each carry one fragment read of stage s+1 and, in the first six,
+    // one copy instruction of stage s+3.  That copy refills the ring slot
+    // of stage s itself: every wave read stage s's fragments during stage
+    // s-1 and waited for them before this barrier.
+    //
+    // Copy addresses: wave-uniform bases (SGPRs, advanced per stage by
+    // scalar adds) plus one 32-bit per-lane offset each.  A instruction j
+    // copies rows rb .. rb+7 (rb = 8(4 wave + j) in the tile); lane rows
+    // past M are clamped to M - 1 and so is the base row, so a lane's
+    // offset stays below 8 lda.
+    const int8_t *a_base[kAPer];
+    uint32_t a_lo[kAPer];
 #pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
-                }
-            }
-        }
-    } else {
-        // Software-pipelined: stage s's 16 MFMAs run from fragments read
-        // during stage s-1; after the first four, one wait + barrier makes
-        // stage s+1 visible (its copy was issued two stages earlier; stage
-        // s+2's copy stays in flight), and the remaining twelve MFMA slots
-        // each carry one fragment read of stage s+1 and, in the first six,
-        // one copy instruction of stage s+3.  That copy refills the ring slot
-        // of stage s itself: every wave read stage s's fragments during stage
-        // s-1 and waited for them before this barrier.
-        //
-        // Copy addresses: wave-uniform bases (SGPRs, advanced per stage by
-        // scalar adds) plus one 32-bit per-lane offset each.  A instruction j
-        // copies rows rb .. rb+7 (rb = 8(4 wave + j) in the tile); lane rows
-        // past M are clamped to M - 1 and so is the base row, so a lane's
-        // offset stays below 8 lda.
-        const int8_t *a_base[kAPer];
-        uint32_t a_lo[kAPer];
-#pragma unroll
-        for (int j = 0; j < kAPer; ++j) {
-            const uint32_t rb = (wave * kAPer + j) * 8;
-            const uint32_t r = rb + (lane >> 3);
-            const uint32_t brow = min(m0 + rb, p.M - 1);
-            const uint32_t row = min(m0 + r, p.M - 1);
-            a_base[j] = p.A + static_cast<uint64_t>(brow) * p.lda;
-            a_lo[j] = (row - brow) * p.lda + 16 * ((lane & 7) ^ ((r >> 1) & 7));
-        }
-        const int8_t *b_base[kBPer];
-#pragma unroll
-        for (int j = 0; j < kBPer; ++j) {
-            const int bi = wave * kBPer + j;
-            const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
-            b_base[j] = p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10);
-        }
-        const uint32_t b_lo = lane * 16;
-        // Copy instruction j of stage st_i into ring slot `slot`.
-        auto issue_one = [&](uint32_t st_i, uint32_t slot, int j) {
-            int8_t *st = smem + slot * kStageBytes;
-            if (j < kAPer)
-                dma16_s(a_base[j] + st_i * SK, a_lo[j], st + (wave * kAPer + j) * 1024);
-            else
-                dma16_s(b_base[j - kAPer] + static_cast<uint64_t>(st_i) * 2048, b_lo,
-                        st + kBOff + (wave * kBPer + j - kAPer) * 1024);
-        };
-        auto read_one = [&](uint32_t slot, Frags &f, int k) {
-            const int8_t *st = smem + slot * kStageBytes;
-            const int h = k / 6, r = k % 6;
-            if (r == 0 || r == 5) {
-                const int nb = r == 5;
-                const int boff = kBOff + (((wn * 4 + sub) * 2 + gk) << 10) +
-                                 (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
-                f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
-            } else {
-                const int mb = r - 1;
-                const uint32_t row = wm * 128 + mb * 32 + (lane & 31);
-                const uint32_t c = 4 * gk + 2 * h + (lane >> 5);
-                f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_off[mb] + ((c ^ ((row >> 1) & 7)) << 4));
-            }
-        };
-        // Stage s: multiply `cur`, read stage s+1 (ring slot rd) into `nxt`
-        // and copy stage s+3 into ring slot s % 3 (cp).  more: s+1 < KS;
-        // ahead: stage s+2 was copied (s+2 < KS), so its copy may stay in
-        // flight while stage s+1's is waited for; dma: s+3 < KS.  All three
-        // are compile-time true in the steady-state loops, which then have no
-        // branch.
-        auto step = [&](const Frags &cur, Frags &nxt, uint32_t s, uint32_t rd, uint32_t cp, bool more, bool ahead,
-                        bool dma) {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[h][i], cur.b[h][j], acc[i][j], 0, 0, 0);
-                if (k == 3 && more) {
-                    if (ahead)
-                        wait_vmcnt<kLoads>();
-                    else
-                        wait_vmcnt<0>();
-                    block_barrier();
-                }
-                if (k >= 4 && more) {
-                    if (dma && k - 4 < kLoads) issue_one(s + 3, cp, k - 4);
-                    read_one(rd, nxt, k - 4);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        };
-        Frags f0, f1;
-        const uint32_t pre = min(KS, static_cast<uint32_t>(kStages));
-        for (uint32_t st_i = 0; st_i < pre; ++st_i) {
-#pragma unroll
-            for (int j = 0; j < kLoads; ++j) issue_one(st_i, st_i, j);
-        }
-        if (pre == 3)
-            wait_vmcnt<2 * kLoads>();
-        else if (pre == 2)
-            wait_vmcnt<kLoads>();
-        else
-            wait_vmcnt<0>();
-        block_barrier();
-#pragma unroll
-        for (int k = 0; k < 12; ++k) read_one(0, f0, k);
-        // Six stages per trip (a multiple of both the ring depth and the two
-        // fragment sets), so every ring slot is a constant; then pairs of
-        // stages with every flag still true; then the last stages.
-        uint32_t s = 0;
-        for (; s + 8 < KS; s += 6) {
-            step(f0, f1, s, 1, 0, true, true, true);
-            step(f1, f0, s + 1, 2, 1, true, true, true);
-            step(f0, f1, s + 2, 0, 2, true, true, true);
-            step(f1, f0, s + 3, 1, 0, true, true, true);
-            step(f0, f1, s + 4, 2, 1, true, true, true);
-            step(f1, f0, s + 5, 0, 2, true, true, true);
-        }
-        for (; s + 4 < KS; s += 2) {
-            step(f0, f1, s, (s + 1) % kStages, s % kStages, true, true, true);
-            step(f1, f0, s + 1, (s + 2) % kStages, (s + 1) % kStages, true, true, true);
-        }
-        for (; s + 1 < KS; s += 2) {
-            step(f0, f1, s, (s + 1) % kStages, s % kStages, true, s + 2 < KS, s + 3 < KS);
-            step(f1, f0, s + 1, (s + 2) % kStages, (s + 1) % kStages, s + 2 < KS, s + 3 < KS, s + 4 < KS);
-        }
-        if (s < KS) step(f0, f1, s, 0, 0, false, false, false);
+    for (int j = 0; j < kAPer; ++j) {
+        const uint32_t rb = (wave * kAPer + j) * 8;
+        const uint32_t r = rb + (lane >> 3);
+        const uint32_t brow = min(m0 + rb, p.M - 1);
+        const uint32_t row = min(m0 + r, p.M - 1);
+        a_base[j] = p.A + static_cast<uint64_t>(brow) * p.lda;
+        a_lo[j] = (row - brow) * p.lda + 16 * ((lane & 7) ^ ((r >> 1) & 7));
     }
+    const int8_t *b_base[kBPer];
+#pragma unroll
+    for (int j = 0; j < kBPer; ++j) {
+        const int bi = wave * kBPer + j;
+        const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
+        b_base[j] = p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10);
+    }
+    const uint32_t b_lo = lane * 16;
+    // Copy instruction j of stage st_i into ring slot `slot`.
+    auto issue_one = [&](uint32_t st_i, uint32_t slot, int j) {
+        int8_t *st = smem + slot * kStageBytes;
+        if (j < kAPer)
+            dma16_s(a_base[j] + st_i * SK, a_lo[j], st + (wave * kAPer + j) * 1024);
+        else
+            dma16_s(b_base[j - kAPer] + static_cast<uint64_t>(st_i) * 2048, b_lo,
+                    st + kBOff + (wave * kBPer + j - kAPer) * 1024);
+    };
+    auto read_one = [&](uint32_t slot, Frags &f, int k) {
+        const int8_t *st = smem + slot * kStageBytes;
+        const int h = k / 6, r = k % 6;
+        if (r == 0 || r == 5) {
+            const int nb = r == 5;
+            const int boff = kBOff + (((wn * 4 + sub) * 2 + gk) << 10) +
+                             (((2 * h + (lane >> 5)) * 16 + (lane & 15)) << 4);
+            f.b[h][nb] = *reinterpret_cast<const v4i *>(st + boff + nb * 2 * 2 * 1024);
+        } else {
+            const int mb = r - 1;
+            const uint32_t row = wm * 128 + mb * 32 + (lane & 31);
+            const uint32_t c = 4 * gk + 2 * h + (lane >> 5);
+            f.a[h][mb] = *reinterpret_cast<const v4i *>(st + a_off[mb] + ((c ^ ((row >> 1) & 7)) << 4));
+        }
+    };
+    // Stage s: multiply `cur`, read stage s+1 (ring slot rd) into `nxt`
+    // and copy stage s+3 into ring slot s % 3 (cp).  more: s+1 < KS;
+    // ahead: stage s+2 was copied (s+2 < KS), so its copy may stay in
+    // flight while stage s+1's is waited for; dma: s+3 < KS.  All three
+    // are compile-time true in the steady-state loops, which then have no
+    // branch.
+    auto step = [&](const Frags &cur, Frags &nxt, uint32_t s, uint32_t rd, uint32_t cp, bool more, bool ahead,
+                    bool dma) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int h = k >> 3, j = (k >> 2) & 1, i = k & 3;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[h][i], cur.b[h][j], acc[i][j], 0, 0, 0);
+            if (k == 3 && more) {
+                if (ahead)
+                    wait_vmcnt<kLoads>();
+                else
+                    wait_vmcnt<0>();
+                block_barrier();
+            }
+            if (k >= 4 && more) {
+                if (dma && k - 4 < kLoads) issue_one(s + 3, cp, k - 4);
+                read_one(rd, nxt, k - 4);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    Frags f0, f1;
+    const uint32_t pre = min(KS, static_cast<uint32_t>(kStages));
+    for (uint32_t st_i = 0; st_i < pre; ++st_i) {
+#pragma unroll
+        for (int j = 0; j < kLoads; ++j) issue_one(st_i, st_i, j);
+    }
+    if (pre == 3)
+        wait_vmcnt<2 * kLoads>();
+    else if (pre == 2)
+        wait_vmcnt<kLoads>();
+    else
+        wait_vmcnt<0>();
+    block_barrier();
+#pragma unroll
+    for (int k = 0; k < 12; ++k) read_one(0, f0, k);
+    // Six stages per trip (a multiple of both the ring depth and the two
+    // fragment sets), so every ring slot is a constant; then pairs of
+    // stages with every flag still true; then the last stages.
+    uint32_t s = 0;
+    for (; s + 8 < KS; s += 6) {
+        step(f0, f1, s, 1, 0, true, true, true);
+        step(f1, f0, s + 1, 2, 1, true, true, true);
+        step(f0, f1, s + 2, 0, 2, true, true, true);
+        step(f1, f0, s + 3, 1, 0, true, true, true);
+        step(f0, f1, s + 4, 2, 1, true, true, true);
+        step(f1, f0, s + 5, 0, 2, true, true, true);
+    }
+    for (; s + 4 < KS; s += 2) {
+        step(f0, f1, s, (s + 1) % kStages, s % kStages, true, true, true);
+        step(f1, f0, s + 1, (s + 2) % kStages, (s + 1) % kStages, true, true, true);
+    }
+    for (; s + 1 < KS; s += 2) {
+        step(f0, f1, s, (s + 1) % kStages, s % kStages, true, s + 2 < KS, s + 3 < KS);
+        step(f1, f0, s + 1, (s + 2) % kStages, (s + 1) % kStages, s + 2 < KS, s + 3 < KS, s + 4 < KS);
+    }
+    if (s < KS) step(f0, f1, s, 0, 0, false, false, false);
 
     // Waves w and w+4 hold the two k halves of the same 128 x 64 block.
     // Wave group gk finishes MFMA row tiles 2gk and 2gk+1: it hands the other
@@ -897,17 +801,7 @@ struct FragsW {
 // ps[0] and ps[1]: up to two independent problems with the same M in one
 // grid (tiles_n0 and tiles_n1 column tiles; tiles_n1 = 0 for one problem),
 // so the tiles of both fill whole rounds of CUs together.
-// kSkip (one problem with a zero-block map): a 32-column MFMA tile whose two
-// 1 KiB weight blocks of a 64-deep k block are both all zero is not copied
-// into LDS for that k block, and its fragment reads all point at 16 zero
-// bytes (one broadcast read); the MFMAs run unchanged on the zeros.  No
-// branch enters the scheduled loop: skipping the MFMAs themselves behind
-// uniform branches, per MFMA or per group of four, measured slower than the
-// dense kernel (the joins of the branches cost waits that outweigh the
-// skipped work), and MFMAs on zero operands take the same cycles.  The map
-// is reduced once per workgroup to one byte per k block, bit q = MFMA column
-// tile q of the workgroup's TN columns.
-template <int TN, bool kSkip>
+template <int TN>
 __device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_t tni)
 {
     using namespace wide;
@@ -924,31 +818,6 @@ __device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_
     const uint32_t KS = p.K / SK;
     const uint64_t KTp = p.Kp >> 6;
 
-    // Zero map of this tile's columns: zmap[kt] bit q = column blocks
-    // n0/16 + 2q and + 2q + 1 both all zero in k block kt (blocks past the
-    // packed width count as zero: their results are never stored).
-    constexpr uint32_t kZeroOff = G::kLds;                 // 16 zero bytes (kSkip)
-    uint8_t *zmap = reinterpret_cast<uint8_t *>(smem + G::kLds + 16);
-    if (kSkip) {
-        if (tid == 0) *reinterpret_cast<v4i *>(smem + kZeroOff) = (v4i){0, 0, 0, 0};
-        for (uint32_t kt = tid; kt < 2 * KS; kt += kThreads) {
-            uint32_t bits = 0;
-#pragma unroll
-            for (int q = 0; q < TN / 32; ++q) {
-                const uint32_t nb = (n0 >> 4) + 2 * q;
-                const bool z0 = nb >= NT || p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb] != 0;
-                const bool z1 = nb + 1 >= NT || p.zero_blocks[static_cast<uint64_t>(kt) * NT + nb + 1] != 0;
-                bits |= (z0 && z1) ? (1u << q) : 0u;
-            }
-            zmap[kt] = static_cast<uint8_t>(bits);
-        }
-        __syncthreads();
-    }
-    // Zero bits of k block kt (uniform).
-    auto zbits = [&](uint32_t kt) -> uint32_t {
-        return kSkip ? static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(zmap[kt])) : 0u;
-    };
-
     // DMA: A instruction 8*wave + j copies rows 64*wave + 8j + l/8 (M is a
     // multiple of 256 here, so no row clamp); lane l fetches k chunk
     // (l%8) ^ ((row >> 1) & 7) = (l%8) ^ (l/16) ^ 4(j%2).  B block
@@ -960,15 +829,13 @@ __device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_
     const uint32_t a_lo = q * p.lda + 16 * ((lane & 7) ^ (q >> 1));
     const uint32_t a_lo_odd = q * p.lda + 16 * ((lane & 7) ^ (q >> 1) ^ 4);
     const uint32_t b_lo = lane * 16;
-    // z16: zero bits of the stage's k blocks 2s (low byte) and 2s + 1.
-    auto issue_one = [&](uint32_t s, int k, uint32_t z16) {
+    auto issue_one = [&](uint32_t s, int k) {
         int8_t *st = smem + (s & 1) * G::kStageBytes;
         if (k < kALoads) {
             dma16_s(a_base + static_cast<uint64_t>(8 * k) * p.lda + s * SK, (k & 1) ? a_lo_odd : a_lo,
                     st + (wave * kALoads + k) * 1024);
         } else {
             const int bi = wave * G::kBLoads + (k - kALoads);
-            if (kSkip && ((z16 >> (8 * (bi & 1) + (bi >> 2))) & 1u)) return;   // block of a skipped tile
             const uint32_t nb = min((n0 >> 4) + (bi >> 1), NT - 1);
             dma16_s(p.frag + ((static_cast<uint64_t>(nb) * KTp + (bi & 1)) << 10) + static_cast<uint64_t>(s) * 2048,
                     b_lo, st + kBOff + bi * 1024);
@@ -991,26 +858,16 @@ __device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_
                           (((4 * hh + 2 * h + (lane >> 5)) ^ (((lane & 31) >> 1) & 7)) << 4);
     const uint32_t b_lane = ((2 * sub) << 10) + (((lane >> 5) * 16 + (lane & 15)) << 4);
     const uint32_t b_rd = kBOff + ((wn * (TN / 16)) << 10) + b_lane;
-    // zw: this wave's zero bits (bit j = its MFMA column tile j) of the k
-    // block being read; a zero tile's fragment comes from the zero block.
-    auto read_one = [&](uint32_t st, int hh, FragsW<NB> &f, int k, uint32_t zw) {
+    auto read_one = [&](uint32_t st, int hh, FragsW<NB> &f, int k) {
         const int h = k / (4 + NB), r = k % (4 + NB);
         if (r >= 1 && r <= 4) {
             const int i = r - 1;
             f.a[h][i] = *reinterpret_cast<const v4i *>(smem + st + a_rd[hh][h] + i * 4096);
         } else {
             const int j = r == 0 ? 0 : r - 4;
-            if (kSkip) {
-                // every lane of a zero tile reads the same 16 zero bytes (a
-                // broadcast read costs a fraction of a full fragment read)
-                const uint32_t at = ((zw >> j) & 1u) ? kZeroOff : st + b_rd + j * 4096 + hh * 1024 + h * 512;
-                f.b[h][j] = *reinterpret_cast<const v4i *>(smem + at);
-            } else {
-                f.b[h][j] = *reinterpret_cast<const v4i *>(smem + st + b_rd + j * 4096 + hh * 1024 + h * 512);
-            }
+            f.b[h][j] = *reinterpret_cast<const v4i *>(smem + st + b_rd + j * 4096 + hh * 1024 + h * 512);
         }
     };
-    auto wave_bits = [&](uint32_t z8) { return (z8 >> (wn * NB)) & ((1u << NB) - 1u); };
 
     v16i acc[4][NB];
 #pragma unroll
@@ -1030,55 +887,44 @@ __device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_
     // Second half's side work: the stage s+2 DMA, one per MFMA slot, then the
     // next stage's half-0 reads spread over the remaining slots.
     constexpr int kTail = G::kMfma - G::kLoads;
-    auto side2 = [&](int k, uint32_t s, uint32_t z16, uint32_t nxt, uint32_t zw_nxt, FragsW<NB> &f, bool dma) {
-        if (dma && k < G::kLoads) issue_one(s, k, z16);
+    auto side2 = [&](int k, uint32_t s, uint32_t nxt, FragsW<NB> &f, bool dma) {
+        if (dma && k < G::kLoads) issue_one(s, k);
 #pragma unroll
         for (int r = 0; r < G::kReads; ++r)
-            if (G::kLoads + (r * kTail) / G::kReads == k) read_one(nxt, 0, f, r, zw_nxt);
+            if (G::kLoads + (r * kTail) / G::kReads == k) read_one(nxt, 0, f, r);
     };
-    auto stage_bits = [&](uint32_t s) { return kSkip ? (zbits(2 * s) | (zbits(2 * s + 1) << 8)) : 0u; };
 
     // Prologue: stages 0 and 1 in flight, wait for 0, read its first half.
-    uint32_t z_cur = stage_bits(0);
 #pragma unroll
-    for (int k = 0; k < G::kLoads; ++k) issue_one(0, k, z_cur);
+    for (int k = 0; k < G::kLoads; ++k) issue_one(0, k);
     if (KS > 1) {
-        const uint32_t z1 = stage_bits(1);
 #pragma unroll
-        for (int k = 0; k < G::kLoads; ++k) issue_one(1, k, z1);
-        // With skipped copies stage 1 may hold fewer than kLoads in flight.
-        if (kSkip) wait_vmcnt<0>();
-        else wait_vmcnt<G::kLoads>();
+        for (int k = 0; k < G::kLoads; ++k) issue_one(1, k);
+        wait_vmcnt<G::kLoads>();
     } else {
         wait_vmcnt<0>();
     }
     block_barrier();
     FragsW<NB> f0, f1;
 #pragma unroll
-    for (int k = 0; k < G::kReads; ++k) read_one(0, 0, f0, k, wave_bits(z_cur & 0xffu));
+    for (int k = 0; k < G::kReads; ++k) read_one(0, 0, f0, k);
 
     uint32_t s = 0;
     for (; s + 2 < KS; ++s) {
         const uint32_t cur = (s & 1) * G::kStageBytes, nxt = G::kStageBytes - cur;
-        const uint32_t z_nxt = stage_bits(s + 1), z_far = stage_bits(s + 2);
-        const uint32_t zw1 = wave_bits(z_cur >> 8);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k, zw1); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
         wait_vmcnt<0>();
         block_barrier();
-        mma(f1, [&](int k) { side2(k, s + 2, z_far, nxt, wave_bits(z_nxt & 0xffu), f0, true); });
-        z_cur = z_nxt;
+        mma(f1, [&](int k) { side2(k, s + 2, nxt, f0, true); });
     }
     if (s + 1 < KS) {
         const uint32_t cur = (s & 1) * G::kStageBytes, nxt = ((s + 1) & 1) * G::kStageBytes;
-        const uint32_t z_nxt = stage_bits(s + 1);
-        const uint32_t zw1 = wave_bits(z_cur >> 8);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k, zw1); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
         wait_vmcnt<0>();
         block_barrier();
-        mma(f1, [&](int k) { side2(k, 0, 0u, nxt, wave_bits(z_nxt & 0xffu), f0, false); });
-        z_cur = z_nxt;
+        mma(f1, [&](int k) { side2(k, 0, nxt, f0, false); });
         ++s;
     }
     // The epilogue's row and column scales load during the last stage.
@@ -1086,9 +932,8 @@ __device__ __forceinline__ void wide_tile(const I8Gemm &p, uint32_t tmi, uint32_
     const ColEpi<NB> ce(p, n0 + wn * (TN / 2) + (lane & 31), lane);
     {
         const uint32_t cur = (s & 1) * G::kStageBytes;
-        const uint32_t zw1 = wave_bits(z_cur >> 8);
         __builtin_amdgcn_sched_barrier(0);
-        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k, zw1); });
+        mma(f0, [&](int k) { if (k < G::kReads) read_one(cur, 1, f1, k); });
         mma(f1, [](int) {});
     }
 
@@ -1122,13 +967,13 @@ __device__ __forceinline__ bool wide_tile_of(uint32_t tiles_m, uint32_t tiles_n0
     return second;
 }
 
-template <int TN, bool kSkip = false>
+template <int TN>
 __global__ __launch_bounds__(kThreads) void gemm_i8_wide(I8GemmPair ps, uint32_t tiles_m, uint32_t tiles_n0,
                                                          uint32_t tiles_n1)
 {
     uint32_t tmi, tni;
     const bool second = wide_tile_of(tiles_m, tiles_n0, tiles_n1, tmi, tni);
-    wide_tile<TN, kSkip>(ps.p[second ? 1 : 0], tmi, tni);
+    wide_tile<TN>(ps.p[second ? 1 : 0], tmi, tni);
 }
 
 // One problem in two column ranges: ps.p[0] (the first columns) on 256-wide
@@ -1148,9 +993,9 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_wide_mix(I8GemmPair ps, uint
     uint32_t g = second ? blockIdx.x - first : blockIdx.x;
     if ((n & 7u) == 0) g = (g & 7u) * (n >> 3) + (g >> 3);
     if (second)
-        wide_tile<192, false>(ps.p[1], g % tiles_m, g / tiles_m);
+        wide_tile<192>(ps.p[1], g % tiles_m, g / tiles_m);
     else
-        wide_tile<256, false>(ps.p[0], g % tiles_m, g / tiles_m);
+        wide_tile<256>(ps.p[0], g % tiles_m, g / tiles_m);
 }
 
 }  // namespace
@@ -1196,10 +1041,8 @@ uint32_t cu_count()
 
 void gemm_i8(hipStream_t s, const I8Gemm &p)
 {
-    // The zero-flag table must fit next to the staged tile (K <= 16384).
     const bool aligned = (p.K % 64 == 0) && (p.lda % 16 == 0) &&
-                         (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64 &&
-                         p.K <= 16384;
+                         (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64;
     // The 128-deep kernels address 8 rows of A per copy as a 32-bit lane
     // offset from a uniform base (below 8 lda).
     const bool k128 = aligned && p.K % pipe128::SK == 0 && p.ldc <= kRegStoreMaxLdc && p.lda < (1u << 29);
@@ -1229,7 +1072,7 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
             else if (c192 < c8) v = kI8Wide192, best = c192;
             // Mixed widths (dense weights): r1 whole rounds of 256-wide tiles
             // on the first columns, r2 of 192-wide tiles on the rest.
-            if (!p.zero_blocks && cus % wm_ == 0) {
+            if (cus % wm_ == 0) {
                 const uint32_t per = cus / wm_;   // tile columns per round
                 for (uint32_t r1 = 1; r1 <= 3; ++r1)
                     for (uint32_t r2 = 1; r2 <= 3; ++r2) {
@@ -1250,23 +1093,16 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
         static std::atomic<bool> lds_optin{false};  // launches may come from several host threads
         if (!lds_optin) {
             bool ok = true;
-            for (const void *fn : {reinterpret_cast<const void *>(gemm_i8_pipe<false>),
-                                   reinterpret_cast<const void *>(gemm_i8_pipe<true>),
-                                   reinterpret_cast<const void *>(gemm_i8_k128w8<false>),
-                                   reinterpret_cast<const void *>(gemm_i8_k128w8<true>),
+            for (const void *fn : {reinterpret_cast<const void *>(gemm_i8_pipe),
+                                   reinterpret_cast<const void *>(gemm_i8_k128w8),
                                    reinterpret_cast<const void *>(gemm_i8_wide<256>),
                                    reinterpret_cast<const void *>(gemm_i8_wide<192>),
-                                   reinterpret_cast<const void *>(gemm_i8_wide<256, true>),
-                                   reinterpret_cast<const void *>(gemm_i8_wide<192, true>),
                                    reinterpret_cast<const void *>(gemm_i8_wide_mix)})
                 ok = ok && hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                160 * 1024) == hipSuccess;
             lds_optin = ok;
         }
     }
-    // Sixteen zero bytes and the zero map's per-workgroup reduction sit after
-    // the wide kernel's LDS plan (one byte per 64-deep k block).
-    const size_t zmap = p.zero_blocks ? 16 + (p.K / 64 + 15) / 16 * 16 : 0;
     if (mix_a) {
         // Column split of one problem: the packed weights are strip-major, so
         // columns from nsplit on start nsplit / 16 strips into the fragments.
@@ -1285,38 +1121,18 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
     }
     switch (v) {
     case kI8Wide:
-        if (p.zero_blocks)
-            gemm_i8_wide<256, true><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds + zmap, s>>>(
-                I8GemmPair{{p, p}}, wm_, wn256, 0);
-        else
-            gemm_i8_wide<256><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
-                                                                                       wn256, 0);
+        gemm_i8_wide<256><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
+                                                                                   wn256, 0);
         return;
     case kI8Wide192:
-        if (p.zero_blocks)
-            gemm_i8_wide<192, true><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds + zmap, s>>>(
-                I8GemmPair{{p, p}}, wm_, wn192, 0);
-        else
-            gemm_i8_wide<192><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
-                                                                                       wn192, 0);
+        gemm_i8_wide<192><<<dim3(wm_ * wn192), kThreads, wide::Cfg<192>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
+                                                                                   wn192, 0);
         return;
     case kI8Wave8:
-        if (p.zero_blocks) {
-            const size_t lds = pipe128::kLds + ((p.K / 64) * pipe::kBBlocks + 15) / 16 * 16;
-            gemm_i8_k128w8<true><<<dim3(tm * tn), w8::kThreads8, lds, s>>>(p, tm, tn);
-        } else {
-            gemm_i8_k128w8<false><<<dim3(tm * tn), w8::kThreads8, pipe128::kLds, s>>>(p, tm, tn);
-        }
+        gemm_i8_k128w8<<<dim3(tm * tn), w8::kThreads8, pipe128::kLds, s>>>(p, tm, tn);
         return;
     case kI8Pipe:
-        // Weights with all-zero 1 KiB blocks take the variant that skips
-        // their MFMAs; dense weights the one without the flag reads.
-        if (p.zero_blocks) {
-            const size_t lds = pipe::kLds + ((p.K / 64) * pipe::kBBlocks + 15) / 16 * 16;  // <= 160 KiB for K <= 16384
-            gemm_i8_pipe<true><<<dim3(tm * tn), kThreads, lds, s>>>(p, tm, tn);
-        } else {
-            gemm_i8_pipe<false><<<dim3(tm * tn), kThreads, pipe::kLds, s>>>(p, tm, tn);
-        }
+        gemm_i8_pipe<<<dim3(tm * tn), kThreads, pipe::kLds, s>>>(p, tm, tn);
         return;
     default: {
         dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
@@ -1330,7 +1146,7 @@ bool gemm_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1)
 {
     auto wide_ok = [](const I8Gemm &p) {
         return p.K % 64 == 0 && p.lda % 16 == 0 && reinterpret_cast<uintptr_t>(p.A) % 16 == 0 && p.M >= 64 &&
-               p.K <= 16384 && p.K % pipe128::SK == 0 && !p.zero_blocks && p.M % wide::TM == 0 &&
+               p.K % pipe128::SK == 0 && p.M % wide::TM == 0 &&
                p.ldc <= kRegStoreMaxLdc &&
                p.variant == kI8Auto;
     };

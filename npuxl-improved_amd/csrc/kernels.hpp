@@ -24,11 +24,11 @@ void quantize_tensor(hipStream_t s, const float *X, int8_t *Y, float *scales, ui
                      float *ws);
 
 // ---- PACK_WEIGHTS_I8 (pack.hip) ----
-// Writes the fragment layout [Np/16][Kp/64][4][16][16] (zero padded), the
-// per-column sums [N] and the all-zero 1 KiB block map [Kp/64][Np/16].
+// Writes the fragment layout [Np/16][Kp/64][4][16][16] (zero padded) and the
+// per-column sums [N].
 void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint32_t ldb,
                     uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,
-                    int32_t *column_sums, uint8_t *zero_blocks);
+                    int32_t *column_sums);
 
 // Compute units of the current device (read once per process; 256 if the
 // query fails).  Launch shapes are chosen in whole rounds of these.
@@ -39,7 +39,6 @@ struct I8Gemm {
     const int8_t *A = nullptr;   // [M][lda]
     uint32_t lda = 0;
     const int8_t *frag = nullptr;
-    const uint8_t *zero_blocks = nullptr;  // optional K-block skip map
     uint32_t Kp = 0, Np = 0;
     const float *scale_a = nullptr;  // [M] or null
     const float *scale_b = nullptr;  // [Np]

@@ -13,9 +13,7 @@
 // column-strip-major: the Kp/64 blocks of one 16-column strip are one
 // contiguous run, so the decode GEMV streams each strip sequentially.
 //
-// Also produced: per-column sums (reference scheduler.cpp:798-800) and a
-// [Kp/64][Np/16] all-zero block map that lets MATMUL_I8 skip zero weight
-// blocks exactly.
+// Also produced: per-column sums (reference scheduler.cpp:798-800).
 #include "kernels.hpp"
 
 namespace vnpu {
@@ -83,25 +81,11 @@ __global__ __launch_bounds__(256) void column_sums_kernel(const int8_t *__restri
     }
 }
 
-// One wave per 1 KiB block (frag order): 1 if every byte is zero, written
-// to the [kt][nt] map.
-__global__ __launch_bounds__(64) void zero_block_kernel(const int8_t *__restrict__ frag,
-                                                        uint32_t KT, uint32_t NT,
-                                                        uint8_t *__restrict__ zero_blocks)
-{
-    const uint64_t blk = blockIdx.x;
-    const int4 v = reinterpret_cast<const int4 *>(frag + blk * 1024)[threadIdx.x];
-    const int any = (v.x | v.y | v.z | v.w) != 0;
-    const unsigned long long nz = __ballot(any);
-    const uint32_t kt = static_cast<uint32_t>(blk % KT), nt = static_cast<uint32_t>(blk / KT);
-    if (threadIdx.x == 0) zero_blocks[static_cast<uint64_t>(kt) * NT + nt] = nz == 0ull ? 1 : 0;
-}
-
 }  // namespace
 
 void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint32_t ldb,
                     uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,
-                    int32_t *column_sums, uint8_t *zero_blocks)
+                    int32_t *column_sums)
 {
     const uint32_t NT = Np / 16, KT = Kp / 64;
     const uint64_t blocks = static_cast<uint64_t>(KT) * NT;
@@ -109,7 +93,6 @@ void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint
     pack_frag_kernel<<<dim3(static_cast<uint32_t>((chunks + 255) / 256)), 256, 0, s>>>(
         B, K, N, ldb, trans_b, frag, KT, chunks);
     column_sums_kernel<<<dim3(NT), 256, 0, s>>>(frag, KT, N, column_sums);
-    zero_block_kernel<<<dim3(static_cast<uint32_t>(blocks)), 64, 0, s>>>(frag, KT, NT, zero_blocks);
 }
 
 }  // namespace k

@@ -113,8 +113,6 @@ struct vnpu_packed_weights {
     uint32_t Np = 0;               // N rounded up to 16
     int8_t *frag = nullptr;        // HBM, [Np/16][Kp/64][4][16][16] fragment layout
     float *scales_dev = nullptr;   // HBM [Np], padding = 1
-    uint8_t *zero_blocks = nullptr;// HBM [Kp/64][Np/16]: 1 = all 1 KiB of the block zero
-    uint64_t zero_block_count = 0;
     uint64_t frag_bytes = 0;
     std::vector<float> scales;     // host copies for vnpu_packed_weights_info
     std::vector<int32_t> column_sums;

@@ -143,6 +143,46 @@ def test_matmul_i8_eight_wave_k_depths(gpu, M, KS):
     assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
 
 
+@pytest.mark.parametrize("K", [192, 320, 448, 576, 704, 832, 960, 4160])
+def test_matmul_i8_pipe_odd_stage_counts(gpu, K):
+    """K % 128 == 64 (an odd number of 64-deep stages) takes the 64-deep
+    pipelined kernel; its loop issues two stages per trip and the drain copies
+    the last one: 3 to 65 stages, bit-exact against the float64 accumulator
+    (from 7 stages up the last stage used to be left uncopied)."""
+    M, N = 300, 200
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    w = gpu.pack(B, K, N, scales=sb)
+    got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa)
+    gpu.release_packed(w)
+    acc = A.astype(np.float64) @ B.astype(np.float64)
+    want = (acc.astype(np.float32) * sa[:, None]) * sb[None, :]
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("tiles,K", [((256, 128, 256), 20480), ((256, 128, 192), 20480),
+                                     ((256, 128, 128), 20480), ((256, 64, 128), 20544)])
+def test_matmul_i8_long_k_every_kernel(gpu, tiles, K):
+    """K above 16384 on the wide, 8-wave and 64-deep pipelined kernels
+    (160 or 321 stages): the exact integer product, C = (float)acc."""
+    rng = np.random.default_rng(K + tiles[2])
+    M, N = 512, 520
+    A = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = rng.integers(-128, 128, size=(K, N)).astype(np.int8)
+    w = gpu.pack(B, K, N)
+    info0 = gpu.info()
+    assert gpu.lib.vnpu_device_set_tiles(gpu.dev, *tiles) == abi.OK
+    try:
+        got = g.matmul_i8(gpu, A, w, M, K, N)
+    finally:
+        gpu.lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n)
+        gpu.release_packed(w)
+    acc = A.astype(np.float64) @ B.astype(np.float64)   # exact: |acc| < 2^53
+    assert np.array_equal(got, acc.astype(np.float32))
+
+
 @pytest.mark.parametrize("M,N0,N1,alias", [(512, 3000, 2000, False), (512, 11008, 11008, False),
                                            (512, 1000, 700, True), (8, 11008, 11008, False),
                                            (6, 3000, 2000, False), (8, 1000, 700, True),
@@ -225,7 +265,9 @@ def test_matmul_i8_strided_and_trans_b(gpu, M):
     assert np.array_equal(got.astype(np.int64), acc)
 
 
-def test_matmul_i8_zero_weight_blocks_skipped_exactly(gpu):
+def test_matmul_i8_zero_weight_blocks_exact(gpu):
+    """Weights with zero 64 x 64 tiles (the config-5 pattern), on the GEMM
+    (M = 64) and the GEMV (M = 4): the exact integer product."""
     M, K, N = 64, 512, 256
     A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
     B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
@@ -296,12 +338,11 @@ def test_matmul_i8_register_epilogue_padded_c(gpu, tiles, epi):
 @pytest.mark.parametrize("tiles", [(256, 128, 256), (256, 128, 192), (256, 128, 128), (128, 128, 64)])
 @pytest.mark.parametrize("K", [128, 384, 1024])
 @pytest.mark.parametrize("kind", ["tiles64", "blocks16", "kblocks"])
-def test_matmul_i8_zero_maps_every_kernel(gpu, tiles, K, kind):
-    """Weights with all-zero blocks on every prefill kernel a tile triple can
-    select (the last the automatic choice): the wide kernels skip the copy,
-    the fragment reads and the MFMAs of a 32-column tile whose two blocks of
-    a k block are zero, so partly zero tiles, whole zero stages, one and
-    several stages, and a ragged last tile must all stay exact."""
+def test_matmul_i8_zero_weight_blocks_every_kernel(gpu, tiles, K, kind):
+    """Weights with all-zero blocks (64 x 64 tiles, single 16-column
+    blocks, whole k blocks) on every prefill kernel a tile triple can select
+    (the last the automatic choice): one and several stages and a ragged last
+    tile, exact."""
     rng = np.random.default_rng(K * 7 + len(kind))
     M, N = 512, 520
     A = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
