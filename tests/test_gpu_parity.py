@@ -265,6 +265,27 @@ def test_matmul_i8_strided_and_trans_b(gpu, M):
     assert np.array_equal(got.astype(np.int64), acc)
 
 
+@pytest.mark.parametrize("tiles,M,K", [((256, 128, 256), 512, 640), ((256, 128, 192), 512, 640),
+                                        ((256, 128, 128), 320, 640), ((256, 64, 128), 320, 576)])
+def test_matmul_i8_strided_a_every_kernel(gpu, tiles, M, K):
+    """A with a row stride above K (lda = K + 48) and a padded C on each
+    pipelined kernel: their copies address rows as a base plus lda steps."""
+    rng = np.random.default_rng(K + M + tiles[2])
+    N, lda, ldc = 300, K + 48, 312
+    A = rng.integers(-128, 128, size=(M, lda)).astype(np.int8)
+    B = rng.integers(-128, 128, size=(K, N)).astype(np.int8)
+    w = gpu.pack(B, K, N)
+    info0 = gpu.info()
+    assert gpu.lib.vnpu_device_set_tiles(gpu.dev, *tiles) == abi.OK
+    try:
+        got = g.matmul_i8(gpu, A, w, M, K, N, lda=lda, ldc=ldc)
+    finally:
+        gpu.lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n)
+        gpu.release_packed(w)
+    acc = A[:, :K].astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(got, acc.astype(np.float32))
+
+
 def test_matmul_i8_zero_weight_blocks_exact(gpu):
     """Weights with zero 64 x 64 tiles (the config-5 pattern), on the GEMM
     (M = 64) and the GEMV (M = 4): the exact integer product."""
