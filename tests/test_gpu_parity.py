@@ -421,6 +421,33 @@ def test_matmul_f32_split_bf16(gpu, M, K, N, ta, tb, epi, beta):
     assert rel(got, want) <= 1e-4
 
 
+
+@pytest.mark.parametrize("M,K,N,ta,tb", [(1100, 520, 6600, 0, 0), (1300, 520, 6200, 0, 1),
+                                         (1100, 520, 1920, 1, 0), (512, 512, 512, 0, 1)])
+def test_matmul_f32_strided_operands(gpu, M, K, N, ta, tb):
+    """A and B with row strides above their widths on the split-bf16 paths:
+    the warp-specialised kernel (B as K x N and as N x K), the four-wave tile
+    with op(A) = A^T, and a K-split small grid; to the f32 bar."""
+    rng = np.random.default_rng(M + K + N + 10 * ta + tb)
+    a_rows, a_cols = (K, M) if ta else (M, K)
+    b_rows, b_cols = (N, K) if tb else (K, N)
+    lda, ldb = a_cols + 12, b_cols + 20
+    A = rng.standard_normal((a_rows, lda)).astype(np.float32)
+    B = rng.standard_normal((b_rows, ldb)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    ba, bb, bbias, bc = gpu.upload(A), gpu.upload(B), gpu.upload(bias), gpu.upload(C0)
+    try:
+        gpu.run(abi.OP_MATMUL_F32, A=ba, B=bb, bias=bbias.ptr, C=bc, M=M, K=K, N=N, lda=lda, ldb=ldb,
+                trans_a=ta, trans_b=tb, alpha=1.0, beta=0.5, epilogue=abi.EPI_SILU)
+        got = gpu.download(bc, np.float32, (M, N))
+    finally:
+        for b in (ba, bb, bbias, bc):
+            gpu.free(b)
+    want = oracle.matmul_f32(np.ascontiguousarray(A[:, :a_cols]), np.ascontiguousarray(B[:, :b_cols]), C0, bias,
+                             M, K, N, ta, tb, 1.0, 0.5, abi.EPI_SILU, acc64=True)
+    assert rel(got, want) <= 1e-4
+
 @pytest.mark.parametrize("beta", [0.0, 0.5])
 def test_matmul_f32_split_bf16_padded_c(gpu, beta):
     """The eight-wave split-bf16 tile stores C (and reads C_in for beta)
