@@ -356,6 +356,45 @@ def test_matmul_i8_register_epilogue_padded_c(gpu, tiles, epi):
         assert rel(out[:M, :N], want) <= 1e-6
 
 
+@pytest.mark.parametrize("tiles,K,M", [((256, 64, 128), 448, 320), ((128, 128, 64), 448, 320),
+                                        ((256, 64, 128), 576, 64), ((128, 128, 64), 1000, 257)])
+@pytest.mark.parametrize("epi", [abi.EPI_NONE, abi.EPI_RELU, abi.EPI_SILU, abi.EPI_GELU_TANH])
+def test_matmul_i8_staged_epilogue_padded_c(gpu, tiles, K, M, epi):
+    """The 64-deep pipelined kernel and the generic one store C from an LDS-
+    staged tile (row scales, column scales, bias, epilogue): with a padded C
+    and sentinel rows after row M the padding and those rows keep their
+    contents, and the values follow store_i8_c's order
+    (src/kernels/kernels.cpp:526-535)."""
+    rng = np.random.default_rng(2000 + 10 * epi + K + M)
+    N, ldc, extra = 520, 536, 8
+    A = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = rng.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = ((rng.random(M) + 0.5) / 127).astype(np.float32)
+    sb = ((rng.random(N) + 0.5) / 127).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    w = gpu.pack(B, K, N, scales=sb)
+    sentinel = np.float32(-1.75)
+    ba, bsa, bb = gpu.upload(A), gpu.upload(sa), gpu.upload(bias)
+    bc = gpu.upload(np.full((M + extra, ldc), sentinel, np.float32))
+    info0 = gpu.info()
+    assert gpu.lib.vnpu_device_set_tiles(gpu.dev, *tiles) == abi.OK
+    try:
+        gpu.run(abi.OP_MATMUL_I8, A=ba, B=w, scale_a=bsa.ptr, bias=bb.ptr, C=bc, M=M, K=K, N=N, ldc=ldc,
+                epilogue=epi)
+        out = gpu.download(bc, np.float32, (M + extra, ldc))
+    finally:
+        gpu.lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n)
+        gpu.release_packed(w)
+        for b in (ba, bsa, bb, bc):
+            gpu.free(b)
+    assert np.all(out[:, N:] == sentinel) and np.all(out[M:] == sentinel)
+    want = oracle.matmul_i8(A, B, sa, sb, bias, epi)
+    if epi == abi.EPI_NONE:
+        assert np.array_equal(out[:M, :N].view(np.uint32), want.view(np.uint32))
+    else:
+        assert rel(out[:M, :N], want) <= 1e-6
+
+
 @pytest.mark.parametrize("tiles", [(256, 128, 256), (256, 128, 192), (256, 128, 128), (128, 128, 64)])
 @pytest.mark.parametrize("K", [128, 384, 1024])
 @pytest.mark.parametrize("kind", ["tiles64", "blocks16", "kblocks"])
