@@ -79,8 +79,7 @@ I8_SHAPES = [(1, 64, 16), (1, 4096, 4096), (1, 300, 1100), (2, 257, 33), (3, 100
              (4, 4096, 11008), (5, 77, 19), (7, 129, 4000), (8, 4096, 1024),
              (9, 64, 16), (16, 300, 200), (64, 128, 96), (130, 257, 129), (257, 1000, 300),
              (512, 512, 512), (320, 4096, 700), (100, 1024, 2000), (513, 192, 130),
-             # decode shapes of the config-4 block: the activations of K = 11008
-             # (M=8) and K = 40000 (M=1) are staged in several LDS chunks
+             # decode shapes of the config-4 block and long-K rows
              (8, 11008, 4096), (8, 4096, 12288), (1, 11008, 4096), (1, 40000, 48), (5, 9000, 33),
              # six or more rows over >= 1024 column strips: four strips per
              # workgroup (a ragged last group; K not a multiple of 64)
@@ -98,6 +97,29 @@ def test_matmul_i8_bit_exact(gpu, M, K, N):
     want = oracle.matmul_i8(A, B, sa, sb)
     gpu.release_packed(w)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K,N", [(8, 11008, 8200), (8, 20000, 4096), (6, 9000, 16400), (4, 11008, 8200),
+                                   (2, 20000, 8200), (3, 50000, 300), (1, 140000, 48)])
+def test_matmul_i8_gemv_multi_chunk(gpu, M, K, N):
+    """Decode GEMVs whose activations are staged in two or three LDS chunks
+    (up to 32 KiB per chunk from 512 column strips, 128 KiB below when the
+    grid fits one workgroup per CU; a ragged last chunk): every GEMV kernel
+    shape (matrix core <8,4,1>, <16,2,1>, <4,4,4>; v_dot4 for 1 to 4 rows),
+    bit-exact against the float64 accumulator."""
+    rng = np.random.default_rng(M * 100003 + K + N)
+    A = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = rng.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = ((rng.random(M) + 0.5) / 127).astype(np.float32)
+    sb = ((rng.random(N) + 0.5) / 127).astype(np.float32)
+    w = gpu.pack(B, K, N, scales=sb)
+    got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa)
+    gpu.release_packed(w)
+    acc = np.zeros((M, N))
+    for k0 in range(0, K, 4096):   # float64 BLAS in slices: exact, bounded memory
+        acc += A[:, k0:k0 + 4096].astype(np.float64) @ B[k0:k0 + 4096].astype(np.float64)
+    want = (acc.astype(np.float32) * sa[:, None]) * sb[None, :]
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
 
 
 @pytest.mark.parametrize("M,K,N", [(2048, 256, 12288), (2304, 384, 11000), (2048, 128, 12288),
