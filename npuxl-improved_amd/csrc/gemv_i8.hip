@@ -333,7 +333,9 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
 // more resident waves, which matters more than deeper per-wave prefetch:
 //   * v_dot4 kernel (M <= 4), from 512 strips: M = 1, 3, 4 eight waves with two
 //     blocks (M=1 N=32000 21.7 -> 20.4 us, N=11008 9.7 -> 8.5 us; M=4 N=32000
-//     25.5 -> 22.2 us), M = 2 four waves with two; below 512 strips (one
+//     25.5 -> 22.2 us), M = 1 with two strips per workgroup (N=32000 a further
+//     1.6%: 21.8-22.1 -> 21.4-21.7 us on one box; 4 waves with 8 blocks, or 4
+//     strips, were slower), M = 2 four waves with two; below 512 strips (one
 //     workgroup per strip, at most 256 workgroups) sixteen waves with four
 //     (M = 1) or two blocks (M=1 N=4096 5.2 -> 4.8 us).
 //   * matrix-core kernel (M >= 5; at three and four rows v_dot4 is as fast):
@@ -398,7 +400,12 @@ void launch_m(hipStream_t s, const I8Gemm &p)
         }
     } else {
         if (NT >= 512) {
-            gemv_i8_kernel<M, 8, 2, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+            // One row: two strips per workgroup (half the workgroups, each
+            // wave's loads alternating between them).
+            if constexpr (M == 1)
+                gemv_i8_kernel<M, 8, 2, 2><<<dim3((NT + 1) / 2), 512, lds, s>>>(p, chunk_k);
+            else
+                gemv_i8_kernel<M, 8, 2, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
         } else if constexpr (M == 1) {
             lds_optin<gemv_i8_kernel<M, 16, 4, 1>>();
             gemv_i8_kernel<M, 16, 4, 1><<<dim3(NT), 1024, lds, s>>>(p, chunk_k);

@@ -83,7 +83,10 @@ I8_SHAPES = [(1, 64, 16), (1, 4096, 4096), (1, 300, 1100), (2, 257, 33), (3, 100
              (8, 11008, 4096), (8, 4096, 12288), (1, 11008, 4096), (1, 40000, 48), (5, 9000, 33),
              # six or more rows over >= 1024 column strips: four strips per
              # workgroup (a ragged last group; K not a multiple of 64)
-             (8, 1000, 16400), (6, 4096, 32000), (7, 130, 20000)]
+             (8, 1000, 16400), (6, 4096, 32000), (7, 130, 20000),
+             # one row over >= 512 strips: two strips per workgroup (513 and 1025
+             # strips leave a last workgroup with one), and the headline shape
+             (1, 4096, 8200), (1, 1000, 16400), (1, 4096, 32000)]
 
 
 @pytest.mark.parametrize("M,K,N", I8_SHAPES)
