@@ -50,9 +50,9 @@ ROTATE_BYTES = 800 << 20
 # HBM bytes per headline GEMV launch from two rocprofv3 PMC passes (FETCH_SIZE,
 # WRITE_SIZE; KiB per dispatch), each scaled by what the counter reads for a
 # copy kernel of known size (FETCH x2.000, WRITE x1.000):
-# 64,169.1 KiB x 2 + 125 KiB.  Measured offline with the commands in
+# 64,112.2 KiB x 2 + 125 KiB.  Measured offline with the commands in
 # profiles/gemv_i8_m1_k4096_n32000_traffic.md; re-measure when the kernel changes.
-GEMV_TRAFFIC_BYTES = 131_545_502
+GEMV_TRAFFIC_BYTES = 131_417_766
 
 
 def log(*a):
