@@ -341,8 +341,9 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
 //   * matrix-core kernel (M >= 5; at three and four rows v_dot4 is as fast):
 //     from 1024 strips four strips per workgroup so one staged activation
 //     chunk serves four weight streams, <W,U,T> = <4,4,4>; 512-1023 strips
-//     <8,4,1> (M=8 N=11008 11.9 -> 11.1 us); below, <16,2,1> (M=8 N=4096
-//     6.9 -> 6.2 us).
+//     two strips per workgroup, <8,2,2> (M=8 N=11008 11.9 -> 11.1 us with
+//     <8,4,1>, then N=12288 11.8 -> 11.5 us and N=8200 10.6 -> 9.9 us with two
+//     strips); below, <16,2,1> (M=8 N=4096 6.9 -> 6.2 us).
 int mfma_variant(uint32_t NT) { return NT >= 1024 ? 0 : NT >= 512 ? 1 : 2; }
 
 // k extent (a multiple of 64) of one staged chunk of M activation rows: below
@@ -363,7 +364,11 @@ void lds_optin()
         done = hipFuncSetAttribute(reinterpret_cast<const void *>(Kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    static_cast<int>(kLdsAOwnCu)) == hipSuccess;
 }
-uint32_t mfma_grid(uint32_t NT) { return mfma_variant(NT) == 0 ? (NT + 3) / 4 : NT; }
+uint32_t mfma_grid(uint32_t NT)
+{
+    const int v = mfma_variant(NT);
+    return v == 0 ? (NT + 3) / 4 : v == 1 ? (NT + 1) / 2 : NT;
+}
 
 template <int M>
 void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t grid0, uint32_t grid1,
@@ -374,7 +379,7 @@ void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t
     if (variant == 0)
         gemv_i8_mfma<M, 4, 4, 4><<<grid, 256, lds, s>>>(ps, grid0, chunk_k);
     else if (variant == 1)
-        gemv_i8_mfma<M, 8, 4, 1><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
+        gemv_i8_mfma<M, 8, 2, 2><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
     else {
         lds_optin<gemv_i8_mfma<M, 16, 2, 1>>();
         gemv_i8_mfma<M, 16, 2, 1><<<grid, 1024, lds, s>>>(ps, grid0, chunk_k);

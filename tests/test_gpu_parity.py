@@ -84,6 +84,8 @@ I8_SHAPES = [(1, 64, 16), (1, 4096, 4096), (1, 300, 1100), (2, 257, 33), (3, 100
              # six or more rows over >= 1024 column strips: four strips per
              # workgroup (a ragged last group; K not a multiple of 64)
              (8, 1000, 16400), (6, 4096, 32000), (7, 130, 20000),
+             # 512-1023 strips on the matrix core: two strips per workgroup, odd counts
+             (8, 4096, 8200), (5, 2000, 9000),
              # one row over >= 512 strips: two strips per workgroup (513 and 1025
              # strips leave a last workgroup with one), and the headline shape
              (1, 4096, 8200), (1, 1000, 16400), (1, 4096, 32000)]
@@ -209,6 +211,7 @@ def test_matmul_i8_long_k_every_kernel(gpu, tiles, K):
 
 
 @pytest.mark.parametrize("M,N0,N1,alias", [(512, 3000, 2000, False), (512, 11008, 11008, False),
+                                           (6, 9000, 9000, False), (8, 8200, 9000, False),
                                            (512, 1000, 700, True), (8, 11008, 11008, False),
                                            (6, 3000, 2000, False), (8, 1000, 700, True),
                                            (8, 20000, 700, False), (5, 4096, 4096, False),
