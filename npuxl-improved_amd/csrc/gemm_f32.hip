@@ -20,6 +20,9 @@
 //     weights streamed with branch-free bounds-checked buffer loads,
 //     activations read as wave-uniform scalars; partial sums reduced in a
 //     second deterministic pass when K is split across workgroups.
+//   * gemv_f32_wide: the same for N of 200 x 128 columns and more (the MTP
+//     head's vocabulary): 128 columns x all of K per 16-wave workgroup, one
+//     pass, no partials.
 #include "kernels.hpp"
 
 #include <atomic>
@@ -993,6 +996,145 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_reduce(F32Gemm p, const flo
     store_out(p, m, n, s, false);
 }
 
+// Wide-N variant (N >= 200 x 128): one workgroup of 16 waves per 128 columns
+// and the whole of K, so no split partials and no second pass.  For M > 1 the
+// activations are staged once in LDS as at[k][MP] (MP = M rounded up to 4,
+// zero padded), so each row's M values are one or two broadcast ds_read_b128
+// instead of M scalar loads from a 32-128 KiB region the scalar cache cannot
+// hold; one row (16 KiB at K = 4096) stays on scalar loads.  Lane l of wave w reads float2 columns n0 + 2l .. +1 of rows w + 16i
+// (kWideUnroll of them in flight per wave); rows past K and columns past N in
+// the last row read as zero through the buffer's bounds check.  The 16 wave
+// sums are added in wave order in LDS, over the staged activations.
+constexpr int kWideCols = 128;  // 64 lanes x float2
+constexpr int kWideWaves = 16;
+constexpr int kWideUnroll = 16;
+constexpr uint32_t kWideMinBlocks = 200;
+constexpr uint32_t kWideMaxLds = 128 * 1024;
+
+__host__ __device__ constexpr uint32_t wide_mp(int M) { return (M + 3) & ~3; }
+
+template <int M>
+__host__ __device__ constexpr uint32_t wide_red_bytes() { return kWideWaves * M * 64 * 8; }
+
+template <int M>
+__global__ __launch_bounds__(64 * kWideWaves) void gemv_f32_wide(F32Gemm p)
+{
+    constexpr uint32_t MP = wide_mp(M);
+    extern __shared__ float4 wide_lds[];
+    float *at = reinterpret_cast<float *>(wide_lds);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t n0 = blockIdx.x * kWideCols;
+    const uint64_t row_bytes = static_cast<uint64_t>(p.ldb) * 4;
+    const uint64_t span = (p.K - 1) * row_bytes + static_cast<uint64_t>(p.N - n0) * 4;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(p.B) + n0, 0, static_cast<int>(span), kBufferWord3);
+
+    if constexpr (M > 1) {
+#pragma unroll
+        for (uint32_t m = 0; m < MP; ++m)
+            for (uint32_t k = tid; k < p.K; k += 64 * kWideWaves)
+                at[k * MP + m] = m < M ? p.A[static_cast<uint64_t>(m) * p.lda + k] : 0.0f;
+        __syncthreads();
+    }
+
+    float2 acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = make_float2(0.f, 0.f);
+    for (uint32_t k = wave; k < p.K; k += kWideWaves * kWideUnroll) {
+        float2 b[kWideUnroll];
+#pragma unroll
+        for (int u = 0; u < kWideUnroll; ++u) {
+            const uint32_t off = static_cast<uint32_t>((k + u * kWideWaves) * row_bytes) + lane * 8;
+            b[u] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kNontemporal));
+        }
+#pragma unroll
+        for (int u = 0; u < kWideUnroll; ++u) {
+            const uint32_t kk = k + u * kWideWaves;
+            const bool in = kk < p.K;
+            if constexpr (M == 1) {
+                const float a = in ? p.A[kk] : 0.0f;
+                acc[0].x = fmaf(a, b[u].x, acc[0].x);
+                acc[0].y = fmaf(a, b[u].y, acc[0].y);
+                continue;
+            }
+            const float4 *ar = reinterpret_cast<const float4 *>(at + (in ? kk : p.K - 1) * MP);
+            float av[MP];
+#pragma unroll
+            for (uint32_t q = 0; q < MP / 4; ++q) {
+                const float4 t = ar[q];
+                av[4 * q] = t.x; av[4 * q + 1] = t.y; av[4 * q + 2] = t.z; av[4 * q + 3] = t.w;
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float a = in ? av[m] : 0.0f;
+                acc[m].x = fmaf(a, b[u].x, acc[m].x);
+                acc[m].y = fmaf(a, b[u].y, acc[m].y);
+            }
+        }
+    }
+    __syncthreads();  // every wave is done with at[] before red[] reuses it
+    float2 *red = reinterpret_cast<float2 *>(wide_lds);  // [wave][m][lane]
+#pragma unroll
+    for (int m = 0; m < M; ++m) red[(wave * M + m) * 64 + lane] = acc[m];
+    __syncthreads();
+    if (tid < M * kWideCols) {
+        const uint32_t m = tid / kWideCols, c = tid % kWideCols;
+        const float *r = reinterpret_cast<const float *>(red) + m * kWideCols + c;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWideWaves; ++w) v += r[static_cast<size_t>(w) * M * kWideCols];
+        if (n0 + c < p.N) store_out(p, m, n0 + c, v, false);
+    }
+}
+
+template <int M>
+uint32_t wide_lds_bytes(const F32Gemm &p)
+{
+    const uint32_t a = M > 1 ? p.K * wide_mp(M) * 4 : 0;
+    return a > wide_red_bytes<M>() ? a : wide_red_bytes<M>();
+}
+
+template <int M>
+bool wide_lds_optin()
+{
+    static std::atomic<bool> done{false};  // launches may come from several host threads
+    if (!done)
+        done = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_f32_wide<M>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    return done;
+}
+
+bool wide_lds_optin(uint32_t M)
+{
+    switch (M) {
+    case 1: return wide_lds_optin<1>();
+    case 2: return wide_lds_optin<2>();
+    case 3: return wide_lds_optin<3>();
+    case 4: return wide_lds_optin<4>();
+    case 5: return wide_lds_optin<5>();
+    case 6: return wide_lds_optin<6>();
+    case 7: return wide_lds_optin<7>();
+    case 8: return wide_lds_optin<8>();
+    default: return false;
+    }
+}
+
+// The wide variant needs float2-aligned rows (even N and ldb, 8-byte B),
+// enough column blocks to fill the chip, the staged activations within
+// kWideMaxLds (K <= 8192 for M of 2 to 4, 4096 above), and its last batch of rows
+// (up to kWideWaves * kWideUnroll past K) addressable with 32-bit offsets;
+// LDS above 64 KiB is opted into once per kernel.
+bool use_wide(const F32Gemm &p)
+{
+    const uint64_t row_bytes = static_cast<uint64_t>(p.ldb) * 4;
+    return p.N % 2 == 0 && p.ldb % 2 == 0 && reinterpret_cast<uintptr_t>(p.B) % 8 == 0 &&
+           (p.N + kWideCols - 1) / kWideCols >= kWideMinBlocks &&
+           (p.M == 1 || static_cast<uint64_t>(p.K) * wide_mp(p.M) * 4 <= kWideMaxLds) &&
+           (static_cast<uint64_t>(p.K) + kWideWaves * kWideUnroll) * row_bytes < 0x7fffffffull &&
+           wide_lds_optin(p.M);
+}
+
 // K split: enough workgroups to keep the weight stream in flight, and each
 // workgroup's buffer (its rows of B, plus the rows a final partial batch
 // reads past them) addressable with 32-bit offsets.
@@ -1018,6 +1160,10 @@ SkinnyPlan skinny_plan(const F32Gemm &p)
 template <int M>
 void launch_skinny(hipStream_t s, const F32Gemm &p, float *ws)
 {
+    if (use_wide(p)) {
+        gemv_f32_wide<M><<<dim3((p.N + kWideCols - 1) / kWideCols), 64 * kWideWaves, wide_lds_bytes<M>(p), s>>>(p);
+        return;
+    }
     const SkinnyPlan plan = skinny_plan(p);
     dim3 grid((p.N + kSkinnyCols - 1) / kSkinnyCols, plan.splits);
     gemv_f32_kernel<M><<<grid, kThreads, 0, s>>>(p, plan.kps, ws, plan.splits);
@@ -1229,6 +1375,7 @@ void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
 
 size_t gemv_f32_ws_bytes(const F32Gemm &p)
 {
+    if (use_wide(p)) return 0;
     const SkinnyPlan plan = skinny_plan(p);
     return plan.splits > 1 ? static_cast<size_t>(plan.splits) * p.M * p.N * sizeof(float) : 0;
 }

@@ -515,6 +515,38 @@ def test_matmul_f32_strided_operands(gpu, M, K, N, ta, tb):
                              M, K, N, ta, tb, 1.0, 0.5, abi.EPI_SILU, acc64=True)
     assert rel(got, want) <= 1e-4
 
+
+@pytest.mark.parametrize("M,K,N,pad", [(1, 4096, 32000, 0), (4, 1000, 25600, 0), (8, 300, 25602, 0),
+                                       (3, 17, 26000, 6), (5, 1, 25600, 0), (2, 2000, 25601, 0),
+                                       (7, 513, 25800, 3), (6, 4100, 25472, 0), (1, 12000, 25600, 0),
+                                       (4, 8192, 25600, 0), (5, 4096, 25602, 2)])
+def test_matmul_f32_gemv_wide_n(gpu, M, K, N, pad):
+    """M <= 8 with at least 200 column blocks of 128 (the MTP head's width)
+    runs the one-pass 16-wave GEMV when N and ldb are even: a partial last
+    block, K below the wave count, a padded ldb, the largest K whose staged
+    activations fit LDS (8192 at 4 rows, 4096 at 5-8), one row at a K past
+    that (scalar activations), and the cases that fall back to the split-K
+    GEMV (odd N, odd ldb, 199 blocks); bias, beta and GELU epilogue, to the
+    f32 bar."""
+    rng = np.random.default_rng(M * 7 + K + N + pad)
+    ldb = N + pad
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, ldb)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    ba, bb, bbias, bc = gpu.upload(A), gpu.upload(B), gpu.upload(bias), gpu.upload(C0)
+    try:
+        gpu.run(abi.OP_MATMUL_F32, A=ba, B=bb, bias=bbias.ptr, C=bc, M=M, K=K, N=N, ldb=ldb,
+                alpha=1.0, beta=0.5, epilogue=abi.EPI_GELU_TANH)
+        got = gpu.download(bc, np.float32, (M, N))
+    finally:
+        for b in (ba, bb, bbias, bc):
+            gpu.free(b)
+    want = oracle.matmul_f32(A, np.ascontiguousarray(B[:, :N]), C0, bias, M, K, N, 0, 0, 1.0, 0.5,
+                             abi.EPI_GELU_TANH, acc64=True)
+    assert rel(got, want) <= 1e-4
+
+
 @pytest.mark.parametrize("beta", [0.0, 0.5])
 def test_matmul_f32_split_bf16_padded_c(gpu, beta):
     """The eight-wave split-bf16 tile stores C (and reads C_in for beta)
