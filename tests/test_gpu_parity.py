@@ -526,23 +526,24 @@ def test_matmul_f32_gemv_wide_n(gpu, M, K, N, pad):
     block, K below the wave count, a padded ldb, the largest K whose staged
     activations fit LDS (8192 at 4 rows, 4096 at 5-8), one row at a K past
     that (scalar activations), and the cases that fall back to the split-K
-    GEMV (odd N, odd ldb, 199 blocks); bias, beta and GELU epilogue, to the
-    f32 bar."""
+    GEMV (odd N, odd ldb, 199 blocks); bias, alpha (-2 at odd M), beta and
+    GELU epilogue, to the f32 bar."""
     rng = np.random.default_rng(M * 7 + K + N + pad)
     ldb = N + pad
     A = rng.standard_normal((M, K)).astype(np.float32)
     B = rng.standard_normal((K, ldb)).astype(np.float32)
     bias = rng.standard_normal(N).astype(np.float32)
     C0 = rng.standard_normal((M, N)).astype(np.float32)
+    alpha = -2.0 if M % 2 else 1.0
     ba, bb, bbias, bc = gpu.upload(A), gpu.upload(B), gpu.upload(bias), gpu.upload(C0)
     try:
         gpu.run(abi.OP_MATMUL_F32, A=ba, B=bb, bias=bbias.ptr, C=bc, M=M, K=K, N=N, ldb=ldb,
-                alpha=1.0, beta=0.5, epilogue=abi.EPI_GELU_TANH)
+                alpha=alpha, beta=0.5, epilogue=abi.EPI_GELU_TANH)
         got = gpu.download(bc, np.float32, (M, N))
     finally:
         for b in (ba, bb, bbias, bc):
             gpu.free(b)
-    want = oracle.matmul_f32(A, np.ascontiguousarray(B[:, :N]), C0, bias, M, K, N, 0, 0, 1.0, 0.5,
+    want = oracle.matmul_f32(A, np.ascontiguousarray(B[:, :N]), C0, bias, M, K, N, 0, 0, alpha, 0.5,
                              abi.EPI_GELU_TANH, acc64=True)
     assert rel(got, want) <= 1e-4
 
