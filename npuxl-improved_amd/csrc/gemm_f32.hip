@@ -1001,10 +1001,11 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_reduce(F32Gemm p, const flo
 // activations are staged once in LDS as at[k][MP] (MP = M rounded up to 4,
 // zero padded), so each row's M values are one or two broadcast ds_read_b128
 // instead of M scalar loads from a 32-128 KiB region the scalar cache cannot
-// hold; one row (16 KiB at K = 4096) stays on scalar loads.  Lane l of wave w reads float2 columns n0 + 2l .. +1 of rows w + 16i
-// (kWideUnroll of them in flight per wave); rows past K and columns past N in
-// the last row read as zero through the buffer's bounds check.  The 16 wave
-// sums are added in wave order in LDS, over the staged activations.
+// hold; one row (16 KiB at K = 4096) stays on scalar loads.  Lane l of wave
+// w reads float2 columns n0 + 2l .. +1 of rows w + 16i (kWideUnroll of them
+// in flight per wave); rows past K and columns past N in the last row read as
+// zero through the buffer's bounds check.  The 16 wave sums are added in wave
+// order in LDS, over the staged activations.
 constexpr int kWideCols = 128;  // 64 lanes x float2
 constexpr int kWideWaves = 16;
 constexpr int kWideUnroll = 16;
@@ -1122,9 +1123,9 @@ bool wide_lds_optin(uint32_t M)
 
 // The wide variant needs float2-aligned rows (even N and ldb, 8-byte B),
 // enough column blocks to fill the chip, the staged activations within
-// kWideMaxLds (K <= 8192 for M of 2 to 4, 4096 above), and its last batch of rows
-// (up to kWideWaves * kWideUnroll past K) addressable with 32-bit offsets;
-// LDS above 64 KiB is opted into once per kernel.
+// kWideMaxLds (K <= 8192 for M of 2 to 4, 4096 above), and its last batch of
+// rows (up to kWideWaves * kWideUnroll past K) addressable with 32-bit
+// offsets; LDS above 64 KiB is opted into once per kernel.
 bool use_wide(const F32Gemm &p)
 {
     const uint64_t row_bytes = static_cast<uint64_t>(p.ldb) * 4;
