@@ -1042,13 +1042,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void gemv_f32_wide(F32Gemm p)
     float2 acc[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = make_float2(0.f, 0.f);
-    for (uint32_t k = wave; k < p.K; k += kWideWaves * kWideUnroll) {
-        float2 b[kWideUnroll];
+    auto load_rows = [&](float2 (&b)[kWideUnroll], uint32_t k) {
 #pragma unroll
         for (int u = 0; u < kWideUnroll; ++u) {
             const uint32_t off = static_cast<uint32_t>((k + u * kWideWaves) * row_bytes) + lane * 8;
             b[u] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kNontemporal));
         }
+    };
+    auto fma_rows = [&](const float2 (&b)[kWideUnroll], uint32_t k) {
 #pragma unroll
         for (int u = 0; u < kWideUnroll; ++u) {
             const uint32_t kk = k + u * kWideWaves;
@@ -1073,6 +1074,19 @@ __global__ __launch_bounds__(64 * kWideWaves) void gemv_f32_wide(F32Gemm p)
                 acc[m].y = fmaf(a, b[u].y, acc[m].y);
             }
         }
+    };
+    // Two register sets of kWideUnroll rows: the next set's loads are issued
+    // before the current set's FMAs.
+    constexpr uint32_t kStep = kWideWaves * kWideUnroll;
+    float2 b0[kWideUnroll], b1[kWideUnroll];
+    uint32_t k = wave;
+    if (k < p.K) load_rows(b0, k);
+    for (; k < p.K; k += 2 * kStep) {
+        load_rows(b1, k + kStep);
+        fma_rows(b0, k);
+        if (k + kStep >= p.K) break;
+        load_rows(b0, k + 2 * kStep);
+        fma_rows(b1, k + kStep);
     }
     __syncthreads();  // every wave is done with at[] before red[] reuses it
     float2 *red = reinterpret_cast<float2 *>(wide_lds);  // [wave][m][lane]
@@ -1123,16 +1137,16 @@ bool wide_lds_optin(uint32_t M)
 
 // The wide variant needs float2-aligned rows (even N and ldb, 8-byte B),
 // enough column blocks to fill the chip, the staged activations within
-// kWideMaxLds (K <= 8192 for M of 2 to 4, 4096 above), and its last batch of
-// rows (up to kWideWaves * kWideUnroll past K) addressable with 32-bit
-// offsets; LDS above 64 KiB is opted into once per kernel.
+// kWideMaxLds (K <= 8192 for M of 2 to 4, 4096 above), and its last two
+// batches of rows (up to 2 * kWideWaves * kWideUnroll past K) addressable with
+// 32-bit offsets; LDS above 64 KiB is opted into once per kernel.
 bool use_wide(const F32Gemm &p)
 {
     const uint64_t row_bytes = static_cast<uint64_t>(p.ldb) * 4;
     return p.N % 2 == 0 && p.ldb % 2 == 0 && reinterpret_cast<uintptr_t>(p.B) % 8 == 0 &&
            (p.N + kWideCols - 1) / kWideCols >= kWideMinBlocks &&
            (p.M == 1 || static_cast<uint64_t>(p.K) * wide_mp(p.M) * 4 <= kWideMaxLds) &&
-           (static_cast<uint64_t>(p.K) + kWideWaves * kWideUnroll) * row_bytes < 0x7fffffffull &&
+           (static_cast<uint64_t>(p.K) + 2 * kWideWaves * kWideUnroll) * row_bytes < 0x7fffffffull &&
            wide_lds_optin(p.M);
 }
 
