@@ -29,6 +29,7 @@
 #include "device_math.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace vnpu {
 namespace k {
@@ -1049,11 +1050,12 @@ __global__ __launch_bounds__(64 * kWideWaves) void gemv_f32_wide(F32Gemm p)
             b[u] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kNontemporal));
         }
     };
-    auto fma_rows = [&](const float2 (&b)[kWideUnroll], uint32_t k) {
+    // all_in: every row of the set is below K (no per-row selects).
+    auto fma_rows = [&](const float2 (&b)[kWideUnroll], uint32_t k, auto all_in) {
 #pragma unroll
         for (int u = 0; u < kWideUnroll; ++u) {
             const uint32_t kk = k + u * kWideWaves;
-            const bool in = kk < p.K;
+            const bool in = decltype(all_in)::value || kk < p.K;
             if constexpr (M == 1) {
                 const float a = in ? p.A[kk] : 0.0f;
                 acc[0].x = fmaf(a, b[u].x, acc[0].x);
@@ -1081,12 +1083,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void gemv_f32_wide(F32Gemm p)
     float2 b0[kWideUnroll], b1[kWideUnroll];
     uint32_t k = wave;
     if (k < p.K) load_rows(b0, k);
+    using yes = std::true_type;
+    using no = std::false_type;
     for (; k < p.K; k += 2 * kStep) {
         load_rows(b1, k + kStep);
-        fma_rows(b0, k);
+        if (k + kStep <= p.K) fma_rows(b0, k, yes{}); else fma_rows(b0, k, no{});
         if (k + kStep >= p.K) break;
         load_rows(b0, k + 2 * kStep);
-        fma_rows(b1, k + kStep);
+        if (k + 2 * kStep <= p.K) fma_rows(b1, k + kStep, yes{}); else fma_rows(b1, k + kStep, no{});
     }
     __syncthreads();  // every wave is done with at[] before red[] reuses it
     float2 *red = reinterpret_cast<float2 *>(wide_lds);  // [wave][m][lane]
