@@ -899,21 +899,6 @@ void decode_launch(int qn, int v4, dim3 grid, hipStream_t s, const Attn &a, uint
 // ---------------------------------------------------------------------------
 constexpr int RK = 64;   // keys per block (the reference's BK)
 
-// dot_avx2 over d in [0, D): chains c = 0..7 over d = 8i + c, hsum256, tail.
-__device__ __forceinline__ float dot_ref(const float *q, const float *k, uint32_t D)
-{
-#pragma clang fp contract(off)
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    const uint32_t D8 = D & ~7u;
-    for (uint32_t i = 0; i < D8; i += 8) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc[c] = fmaf(q[i + c], k[i + c], acc[c]);
-    }
-    float sum = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
-    for (uint32_t i = D8; i < D; ++i) sum = sum + q[i] * k[i];
-    return sum;
-}
-
 // Any head_dim and any number of (batch, head) pairs: one workgroup per
 // query row (a 1-D grid), the scores of a block by the lanes of wave 0 (one
 // key each), the running output in the output row itself (no bound on
@@ -940,7 +925,7 @@ __global__ __launch_bounds__(kThreads) void attn_rowwise_kernel(Attn a, uint64_t
         const uint32_t kc = min(static_cast<uint32_t>(RK), kend - k0);
         __syncthreads();   // the previous block's weights are consumed
         if (tid < static_cast<int>(kc)) {
-            float sc = dot_ref(q, Kh + static_cast<uint64_t>(k0 + tid) * D, D) * a.scale;
+            float sc = dev::dot_ref(q, Kh + static_cast<uint64_t>(k0 + tid) * D, D) * a.scale;
             if (a.mask) sc = sc + a.mask[row * sk + k0 + tid];
             pw[tid] = sc;
         }
@@ -970,257 +955,11 @@ __global__ __launch_bounds__(kThreads) void attn_rowwise_kernel(Attn a, uint64_t
     for (uint32_t d = tid; d < D; d += kThreads) o[d] = o[d] * inv;
 }
 
-// Reference-order prefill tiled for head_dim 64 or 128: one workgroup of
-// four waves per (batch, head) and 16 query rows, wave w owning rows
-// 4w .. 4w+3 through all three phases of a 64-key block, so the block's
-// weights never leave the wave's registers:
-//   scores:  lane j computes key j's eight dot chains for the wave's rows
-//            (K rows in LDS at pitch D + 4 floats: lane j's 16-byte reads are
-//            conflict-free; Q rows are broadcast reads);
-//   softmax: block max across the lanes, weights p_j in lane j; the weight
-//            sum of row i in key order by lane i from an LDS copy;
-//   output:  lane owns D / 64 output elements of each row and walks the keys
-//            in order, the weights read back from the LDS copy; the
-//            reference's "p_j != 0" skip tests a ballot mask of the nonzero
-//            weights (uniform), once per four keys when all are nonzero.
-// The workgroups of the longest (causal) rows are dispatched first.
-template <int D>
-struct ExactRows {
-    static constexpr int QT = 16;                // query rows per workgroup
-    static constexpr int RW = 4;                 // rows per wave
-    static constexpr int P = D + 4;              // K row pitch (floats)
-    static constexpr int WP = RK + 4;            // weight row pitch (floats)
-    static constexpr int DPT = D / 64;           // output elements per lane and row
-    static constexpr int kFloats = RK * P + RK * D + QT * D + QT * WP;
-    static constexpr size_t kLds = static_cast<size_t>(kFloats) * sizeof(float);
-    static constexpr int kPre = RK * D / 4 / kThreads;   // float4s of K (and of V) per thread per block
-};
-
 __device__ __forceinline__ void wave_sync_lds()
 {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Two workgroups per CU at most (LDS), so two waves per SIMD: the register
-// budget is 256, and the K/V prefetch registers must not go to scratch.
-template <int D>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_exact_rows_kernel(Attn a)
-{
-#pragma clang fp contract(off)
-    using G = ExactRows<D>;
-    constexpr int RW = G::RW, DPT = G::DPT;
-    // Q rows and weights first: their reads then take immediate offsets
-    // (the 16-bit offset field of ds_read covers the first 64 KiB).
-    extern __shared__ float4 sm4[];
-    float *Qs = reinterpret_cast<float *>(sm4);  // [QT][D]
-    float *Wl = Qs + G::QT * D;                   // [QT][WP] weights, for the row sums
-    float *Ks = Wl + G::QT * G::WP;               // [64][P]
-    float *Vs = Ks + RK * G::P;                   // [64][D]
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint64_t bh = blockIdx.y;
-    const uint32_t sq = a.seq_q, sk = a.seq_k;
-    const uint32_t off = sk > sq ? sk - sq : 0;
-    const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * G::QT;
-    const uint32_t nq = min(static_cast<uint32_t>(G::QT), sq - q0);
-    const float *Kh = a.K + bh * sk * D;
-    const float *Vh = a.V + bh * sk * D;
-    const float *Mh = a.mask ? a.mask + bh * sq * sk : nullptr;
-
-    for (int i = tid; i < G::QT * D; i += kThreads) {
-        const uint32_t r = i / D;
-        Qs[i] = r < nq ? a.Q[(bh * sq + q0 + r) * D + (i % D)] : 0.0f;
-    }
-    uint32_t kend = sk;
-    if (a.causal) kend = min(sk, q0 + nq - 1 + off + 1);
-    const uint32_t nblk = (kend + RK - 1) / RK;
-
-    // Keys past kend load key kend - 1 and keep zeros (a select on the loaded
-    // values: a branch around the loads would make the compiler wait for
-    // them at once).
-    float4 pk[G::kPre], pv[G::kPre];
-    const float4 *K4 = reinterpret_cast<const float4 *>(Kh), *V4 = reinterpret_cast<const float4 *>(Vh);
-
-    // Row state: m (uniform per row), l of row `wave*RW + lane` in lane < RW.
-    float m[RW], acc[RW][DPT];
-    float l_mine = 0.0f;
-#pragma unroll
-    for (int i = 0; i < RW; ++i) {
-        m[i] = -__builtin_inff();
-#pragma unroll
-        for (int e = 0; e < DPT; ++e) acc[i][e] = 0.0f;
-    }
-    const int r0 = wave * RW;
-    float *wrow = Wl + r0 * G::WP;
-
-#define VNPU_EXACT_FETCH(blk)                                                                      \
-    _Pragma("unroll") for (int u = 0; u < G::kPre; ++u) {                                          \
-        const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);                  \
-        const uint32_t key_ = (blk) * RK + j;                                                      \
-        const uint64_t at = static_cast<uint64_t>(min(key_, kend - 1)) * (D / 4) + c4;             \
-        const float4 kx = K4[at], vx = V4[at];                                                     \
-        const bool in_ = key_ < kend;                                                              \
-        pk[u] = make_float4(in_ ? kx.x : 0.f, in_ ? kx.y : 0.f, in_ ? kx.z : 0.f, in_ ? kx.w : 0.f); \
-        pv[u] = make_float4(in_ ? vx.x : 0.f, in_ ? vx.y : 0.f, in_ ? vx.z : 0.f, in_ ? vx.w : 0.f); \
-    }
-    if (nblk) {
-        VNPU_EXACT_FETCH(0u)
-    }
-    for (uint32_t b = 0; b < nblk; ++b) {
-        const uint32_t k0 = b * RK, kc = min(static_cast<uint32_t>(RK), kend - k0);
-        __syncthreads();   // the previous block's tiles are consumed
-#pragma unroll
-        for (int u = 0; u < G::kPre; ++u) {
-            const uint32_t f = tid + kThreads * u, j = f / (D / 4), c4 = f % (D / 4);
-            *reinterpret_cast<float4 *>(Ks + j * G::P + 4 * c4) = pk[u];
-            reinterpret_cast<float4 *>(Vs)[f] = pv[u];
-        }
-        __syncthreads();
-        // the next block's tiles (past the last block: the last one again,
-        // never used, so the loads need no branch)
-        const uint32_t bn = b + 1 < nblk ? b + 1 : b;
-        VNPU_EXACT_FETCH(bn)
-#undef VNPU_EXACT_FETCH
-
-        // Scores of the wave's rows, key `lane`.
-        float ch[RW][8];
-#pragma unroll
-        for (int i = 0; i < RW; ++i)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) ch[i][c] = 0.0f;
-        {
-            const float *kr = Ks + lane * G::P;
-            const float *qr = Qs + r0 * D;
-#pragma unroll 2
-            for (int d = 0; d < D; d += 8) {
-                const float4 ka = *reinterpret_cast<const float4 *>(kr + d);
-                const float4 kb = *reinterpret_cast<const float4 *>(kr + d + 4);
-#pragma unroll
-                for (int i = 0; i < RW; ++i) {
-                    const float4 qa = *reinterpret_cast<const float4 *>(qr + i * D + d);
-                    const float4 qb = *reinterpret_cast<const float4 *>(qr + i * D + d + 4);
-                    ch[i][0] = fmaf(qa.x, ka.x, ch[i][0]);
-                    ch[i][1] = fmaf(qa.y, ka.y, ch[i][1]);
-                    ch[i][2] = fmaf(qa.z, ka.z, ch[i][2]);
-                    ch[i][3] = fmaf(qa.w, ka.w, ch[i][3]);
-                    ch[i][4] = fmaf(qb.x, kb.x, ch[i][4]);
-                    ch[i][5] = fmaf(qb.y, kb.y, ch[i][5]);
-                    ch[i][6] = fmaf(qb.z, kb.z, ch[i][6]);
-                    ch[i][7] = fmaf(qb.w, kb.w, ch[i][7]);
-                }
-            }
-        }
-
-        // Softmax state and weights per row; p = 0 for a skipped row.
-        float p[RW], alpha[RW];
-        bool live[RW];
-        const uint32_t key = k0 + lane;
-#pragma unroll
-        for (int i = 0; i < RW; ++i) {
-            const uint32_t r = r0 + i, qi = q0 + r;
-            float sc = -__builtin_inff();
-            if (lane < static_cast<int>(kc) && r < nq && !(a.causal && key > qi + off)) {
-                const float dot = ((ch[i][0] + ch[i][4]) + (ch[i][1] + ch[i][5])) +
-                                  ((ch[i][2] + ch[i][6]) + (ch[i][3] + ch[i][7]));
-                sc = dot * a.scale;
-                if (Mh) sc = sc + Mh[static_cast<uint64_t>(qi) * sk + key];
-            }
-            const float bmax = dev::wave_max(sc);
-            live[i] = isfinite(bmax);   // uniform over the wave
-            const float nm = m[i] < bmax ? bmax : m[i];
-            alpha[i] = live[i] ? dev::fast_expf_unfused(m[i] - nm) : 1.0f;
-            p[i] = live[i] ? dev::fast_expf_unfused(sc - nm) : 0.0f;   // -inf scores give 0
-            if (live[i]) m[i] = nm;
-            wrow[i * G::WP + lane] = p[i];
-        }
-        uint64_t nz[RW], all_nz = ~0ull;
-#pragma unroll
-        for (int i = 0; i < RW; ++i) {
-            nz[i] = __ballot(p[i] != 0.0f);
-            all_nz &= nz[i];
-        }
-        wave_sync_lds();
-        // Weight sums in key order, row r0 + lane by lane < RW.
-        if (lane < RW) {
-            float a_mine = alpha[0];
-            bool live_mine = live[0];
-#pragma unroll
-            for (int i = 1; i < RW; ++i)
-                if (lane == i) {
-                    a_mine = alpha[i];
-                    live_mine = live[i];
-                }
-            if (live_mine) {
-                const float *pr = wrow + lane * G::WP;
-                float psum = 0.0f;
-                for (uint32_t j = 0; j < kc; j += 4) {
-                    const float4 w4 = *reinterpret_cast<const float4 *>(pr + j);
-                    psum = psum + w4.x;
-                    if (j + 1 < kc) psum = psum + w4.y;
-                    if (j + 2 < kc) psum = psum + w4.z;
-                    if (j + 3 < kc) psum = psum + w4.w;
-                }
-                l_mine = l_mine * a_mine + psum;
-            }
-        }
-
-        // Output accumulators: acc = acc * alpha, then fma(v_j, p_j, acc) in key order.
-#pragma unroll
-        for (int i = 0; i < RW; ++i)
-            if (live[i])
-#pragma unroll
-                for (int e = 0; e < DPT; ++e) acc[i][e] = acc[i][e] * alpha[i];
-        // Keys in groups of four (keys past kc have p = 0 and zero V rows),
-        // the weights as broadcast reads of the LDS copy.  A group
-        // whose sixteen weights are all nonzero runs without a branch;
-        // otherwise each (row, key) tests its bit of the row's nonzero mask.
-        const float *vcol = Vs + lane * DPT;
-        for (uint32_t j = 0; j < kc; j += 4) {
-            float v[4][DPT];
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int e = 0; e < DPT; ++e) v[t][e] = vcol[(j + t) * D + e];
-            float pw[RW][4];
-#pragma unroll
-            for (int i = 0; i < RW; ++i) {
-                const float4 w4 = *reinterpret_cast<const float4 *>(wrow + i * G::WP + j);
-                pw[i][0] = w4.x;
-                pw[i][1] = w4.y;
-                pw[i][2] = w4.z;
-                pw[i][3] = w4.w;
-            }
-            if (((all_nz >> j) & 15ull) == 15ull) {
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-#pragma unroll
-                    for (int i = 0; i < RW; ++i)
-#pragma unroll
-                        for (int e = 0; e < DPT; ++e) acc[i][e] = fmaf(v[t][e], pw[i][t], acc[i][e]);
-            } else {
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-#pragma unroll
-                    for (int i = 0; i < RW; ++i)
-                        if ((nz[i] >> (j + t)) & 1ull)
-#pragma unroll
-                            for (int e = 0; e < DPT; ++e) acc[i][e] = fmaf(v[t][e], pw[i][t], acc[i][e]);
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < RW; ++i) {
-        const uint32_t r = r0 + i;
-        const float l = __uint_as_float(static_cast<uint32_t>(
-            __builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(l_mine)), i)));
-        if (r >= nq) continue;
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        float *o = a.O + (bh * sq + q0 + r) * D + lane * DPT;
-#pragma unroll
-        for (int e = 0; e < DPT; ++e) o[e] = acc[i][e] * inv;
-    }
 }
 
 // Reference-order decode (seq_q <= 4) for head_dim 64 or 128: one
@@ -1521,19 +1260,6 @@ size_t attention_ws_bytes(const Attn &a)
 }
 
 template <int D>
-void launch_exact_rows(hipStream_t s, const Attn &a)
-{
-    using G = ExactRows<D>;
-    static std::atomic<bool> lds_optin{false};
-    if (!lds_optin && G::kLds > 65536)
-        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_exact_rows_kernel<D>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(G::kLds)) == hipSuccess;
-    const dim3 grid((a.seq_q + G::QT - 1) / G::QT, a.batch * a.heads);
-    attn_exact_rows_kernel<D><<<grid, kThreads, G::kLds, s>>>(a);
-}
-
-template <int D>
 void launch_exact_decode(hipStream_t s, const Attn &a)
 {
     using G = ExactDec<D>;
@@ -1550,8 +1276,8 @@ void attention(hipStream_t s, const Attn &a, float *ws)
 {
     if (use_exact_tiled(a)) {
         const bool decode = a.seq_q <= 4;
-        if (a.head_dim == 128) decode ? launch_exact_decode<128>(s, a) : launch_exact_rows<128>(s, a);
-        else decode ? launch_exact_decode<64>(s, a) : launch_exact_rows<64>(s, a);
+        if (a.head_dim == 128) decode ? launch_exact_decode<128>(s, a) : attention_exact_prefill(s, a);
+        else decode ? launch_exact_decode<64>(s, a) : attention_exact_prefill(s, a);
         return;
     }
     if (use_rowwise(a)) {

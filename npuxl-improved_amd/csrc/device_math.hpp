@@ -162,6 +162,24 @@ __device__ __forceinline__ float scale_from_max(float maxabs)
     return scale;
 }
 
+// dot_avx2 (reference src/kernels/llm.cpp:332-343) over d in [0, D): eight
+// FMA chains c = 0..7 over d = 8i + c, hsum256's pairing
+// ((c0+c4) + (c1+c5)) + ((c2+c6) + (c3+c7)), then the tail d >= D & ~7 as
+// unfused multiply-adds.
+__device__ __forceinline__ float dot_ref(const float *q, const float *k, uint32_t D)
+{
+#pragma clang fp contract(off)
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint32_t D8 = D & ~7u;
+    for (uint32_t i = 0; i < D8; i += 8) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = fmaf(q[i + c], k[i + c], acc[c]);
+    }
+    float sum = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+    for (uint32_t i = D8; i < D; ++i) sum = sum + q[i] * k[i];
+    return sum;
+}
+
 // Wave-wide reductions (wave64).
 __device__ __forceinline__ float wave_max(float v)
 {

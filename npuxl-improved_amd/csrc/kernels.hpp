@@ -163,6 +163,9 @@ struct Attn {
 };
 size_t attention_ws_bytes(const Attn &a);
 void attention(hipStream_t s, const Attn &a, float *ws);
+// Reference-order prefill (exact, seq_q > 4, head_dim 64 or 128) on the fp32
+// matrix cores (attn_exact.hip).
+void attention_exact_prefill(hipStream_t s, const Attn &a);
 // The allocation-free attention entry point's device scratch: a file-scope
 // array of kAttnScratchBytes in attention.hip, one copy per GPU.  Setup looks
 // its address up once per device (that device current) and keeps it;
