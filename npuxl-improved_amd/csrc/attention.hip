@@ -955,208 +955,6 @@ __global__ __launch_bounds__(kThreads) void attn_rowwise_kernel(Attn a, uint64_t
     for (uint32_t d = tid; d < D; d += kThreads) o[d] = o[d] * inv;
 }
 
-__device__ __forceinline__ void wave_sync_lds()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Reference-order decode (seq_q <= 4) for head_dim 64 or 128: one
-// workgroup of four waves per query row, the key blocks in a pipeline:
-//   waves 2-3 copy block t+1's K tile and block t's V tile from HBM straight
-//             into LDS (global_load_lds; the K tile at row pitch D + 4 floats,
-//             the pad slots take a dummy copy);
-//   wave 1    scores block t (lane j: key j's eight dot chains) and its
-//             softmax state: block max, m, alpha, the weights p_j (to LDS with
-//             alpha, a live flag and the nonzero mask) and, in lane 0, the
-//             weight sum in key order and l;
-//   wave 0    accumulates block t-1: acc = acc * alpha, then fma(v_j, p_j, acc)
-//             in key order for the nonzero p_j (lane owns D / 64 elements).
-// One barrier per step; two K and two V tiles alternate.  The scores and the
-// softmax state never wait for the output chain, so the chain of one row is
-// the only sequential work.
-template <int D>
-struct ExactDec {
-    static constexpr int P = D + 4;                     // K row pitch (floats)
-    static constexpr int KI = RK * (D / 4 + 1) / 64;    // 16-byte wave copies per K tile (with pads)
-    static constexpr int VI = RK * D / 4 / 64;          // per V tile
-    static constexpr int DPT = D / 64;
-    static constexpr int WS = RK + 8;                   // weights, alpha, live, nonzero mask
-    static constexpr int kFloats = 2 * RK * P + 2 * RK * D + D + 2 * WS + 4;
-    static constexpr size_t kLds = static_cast<size_t>(kFloats) * sizeof(float);
-};
-
-template <int D>
-__global__ __launch_bounds__(kThreads) void attn_exact_decode_kernel(Attn a)
-{
-#pragma clang fp contract(off)
-    using G = ExactDec<D>;
-    constexpr int DPT = G::DPT;
-    extern __shared__ float4 sm4[];
-    float *Kt = reinterpret_cast<float *>(sm4);   // [2][64][P]
-    float *Vt = Kt + 2 * RK * G::P;                // [2][64][D]
-    float *Qs = Vt + 2 * RK * D;                   // [D]
-    float *Wr = Qs + D;                            // [2][WS]
-    float *Lf = Wr + 2 * G::WS;                    // the row's final l
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: the copies' LDS bases are scalar
-    const uint64_t bh = blockIdx.y;
-    const uint32_t sq = a.seq_q, sk = a.seq_k, qi = blockIdx.x;
-    const uint32_t off = sk > sq ? sk - sq : 0;
-    const uint64_t row = bh * sq + qi;
-    const float *Kh = a.K + bh * sk * D;
-    const float *Vh = a.V + bh * sk * D;
-    const float *Mr = a.mask ? a.mask + row * sk : nullptr;
-    uint32_t kend = sk;
-    if (a.causal) kend = min(sk, qi + off + 1);
-    const uint32_t nblk = (kend + RK - 1) / RK;
-
-    for (int i = tid; i < D; i += kThreads) Qs[i] = a.Q[row * D + i];
-    if (tid == 0) *Lf = 0.0f;
-
-    // Copies by waves 2 and 3: wave copy i covers 16-byte slots 64 i .. 64 i + 63.
-    auto copy_k = [&](uint32_t b) {
-        int8_t *dst = reinterpret_cast<int8_t *>(Kt + (b & 1) * RK * G::P);
-        for (int i = wave - 2; i < G::KI; i += 2) {
-            const uint32_t sl = static_cast<uint32_t>(i) * 64 + lane;
-            const uint32_t r = sl / (D / 4 + 1), c = sl % (D / 4 + 1);
-            const uint32_t key = min(b * RK + r, kend - 1);
-            lds::dma16(Kh + static_cast<uint64_t>(key) * D + (c < D / 4 ? 4 * c : 0), dst + i * 1024);
-        }
-    };
-    auto copy_v = [&](uint32_t b) {
-        int8_t *dst = reinterpret_cast<int8_t *>(Vt + (b & 1) * RK * D);
-        for (int i = wave - 2; i < G::VI; i += 2) {
-            const uint32_t sl = static_cast<uint32_t>(i) * 64 + lane;
-            const uint32_t key = min(b * RK + sl / (D / 4), kend - 1);
-            lds::dma16(Vh + static_cast<uint64_t>(key) * D + 4 * (sl % (D / 4)), dst + i * 1024);
-        }
-    };
-    if (wave >= 2 && nblk) {
-        copy_k(0);
-        lds::wait_vmcnt<0>();
-    }
-    __syncthreads();
-
-    float m = -__builtin_inff(), l = 0.0f;   // wave 1 (l in lane 0)
-    float acc[DPT];                          // wave 0
-#pragma unroll
-    for (int e = 0; e < DPT; ++e) acc[e] = 0.0f;
-
-    for (uint32_t t = 0; t <= nblk; ++t) {
-        if (wave >= 2) {
-            if (t + 1 < nblk) copy_k(t + 1);
-            if (t < nblk) copy_v(t);
-            lds::wait_vmcnt<0>();
-        } else if (wave == 1 && t < nblk) {
-            const uint32_t k0 = t * RK, kc = min(static_cast<uint32_t>(RK), kend - k0);
-            const float *kr = Kt + (t & 1) * RK * G::P + lane * G::P;
-            float ch[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-            for (int d = 0; d < D; d += 8) {
-                const float4 ka = *reinterpret_cast<const float4 *>(kr + d);
-                const float4 kb = *reinterpret_cast<const float4 *>(kr + d + 4);
-                const float4 qa = *reinterpret_cast<const float4 *>(Qs + d);
-                const float4 qb = *reinterpret_cast<const float4 *>(Qs + d + 4);
-                ch[0] = fmaf(qa.x, ka.x, ch[0]);
-                ch[1] = fmaf(qa.y, ka.y, ch[1]);
-                ch[2] = fmaf(qa.z, ka.z, ch[2]);
-                ch[3] = fmaf(qa.w, ka.w, ch[3]);
-                ch[4] = fmaf(qb.x, kb.x, ch[4]);
-                ch[5] = fmaf(qb.y, kb.y, ch[5]);
-                ch[6] = fmaf(qb.z, kb.z, ch[6]);
-                ch[7] = fmaf(qb.w, kb.w, ch[7]);
-            }
-            float sc = -__builtin_inff();
-            if (lane < static_cast<int>(kc)) {
-                const float dot = ((ch[0] + ch[4]) + (ch[1] + ch[5])) + ((ch[2] + ch[6]) + (ch[3] + ch[7]));
-                sc = dot * a.scale;
-                if (Mr) sc = sc + Mr[k0 + lane];
-            }
-            const float bmax = dev::wave_max(sc);
-            const bool live = isfinite(bmax);   // uniform over the wave
-            float p = 0.0f, alpha = 1.0f;
-            if (live) {
-                const float nm = m < bmax ? bmax : m;
-                alpha = dev::fast_expf_unfused(m - nm);
-                p = dev::fast_expf_unfused(sc - nm);   // -inf scores give 0
-                m = nm;
-            }
-            float *w = Wr + (t & 1) * G::WS;
-            w[lane] = p;
-            const uint64_t nz = __ballot(p != 0.0f);
-            if (lane == 0) {
-                w[RK] = alpha;
-                w[RK + 1] = live ? 1.0f : 0.0f;
-                w[RK + 2] = __uint_as_float(static_cast<uint32_t>(nz));
-                w[RK + 3] = __uint_as_float(static_cast<uint32_t>(nz >> 32));
-            }
-            wave_sync_lds();
-            if (lane == 0) {
-                if (live) {
-                    float psum = 0.0f;
-                    for (uint32_t j = 0; j < kc; j += 4) {
-                        const float4 w4 = *reinterpret_cast<const float4 *>(w + j);
-                        psum = psum + w4.x;
-                        if (j + 1 < kc) psum = psum + w4.y;
-                        if (j + 2 < kc) psum = psum + w4.z;
-                        if (j + 3 < kc) psum = psum + w4.w;
-                    }
-                    l = l * alpha + psum;
-                }
-                if (t + 1 == nblk) *Lf = l;
-            }
-        } else if (wave == 0 && t >= 1) {
-            const uint32_t b = t - 1, kc = min(static_cast<uint32_t>(RK), kend - b * RK);
-            const float *w = Wr + (b & 1) * G::WS;
-            const uint32_t live = __builtin_amdgcn_readfirstlane(static_cast<int>(__float_as_uint(w[RK + 1])));
-            if (live) {
-                const float alpha = __uint_as_float(static_cast<uint32_t>(
-                    __builtin_amdgcn_readfirstlane(static_cast<int>(__float_as_uint(w[RK])))));
-                const uint64_t nz =
-                    static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
-                        static_cast<int>(__float_as_uint(w[RK + 2]))))) |
-                    (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
-                         static_cast<int>(__float_as_uint(w[RK + 3]))))) << 32);
-#pragma unroll
-                for (int e = 0; e < DPT; ++e) acc[e] = acc[e] * alpha;
-                const float *vcol = Vt + (b & 1) * RK * D + lane * DPT;
-                for (uint32_t j = 0; j < kc; j += 4) {
-                    float v[4][DPT];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u)
-#pragma unroll
-                        for (int e = 0; e < DPT; ++e) v[u][e] = vcol[(j + u) * D + e];
-                    const float4 w4 = *reinterpret_cast<const float4 *>(w + j);
-                    const float pj[4] = {w4.x, w4.y, w4.z, w4.w};
-                    if (((nz >> j) & 15ull) == 15ull) {
-#pragma unroll
-                        for (int u = 0; u < 4; ++u)
-#pragma unroll
-                            for (int e = 0; e < DPT; ++e) acc[e] = fmaf(v[u][e], pj[u], acc[e]);
-                    } else {
-#pragma unroll
-                        for (int u = 0; u < 4; ++u)
-                            if ((nz >> (j + u)) & 1ull)
-#pragma unroll
-                                for (int e = 0; e < DPT; ++e) acc[e] = fmaf(v[u][e], pj[u], acc[e]);
-                    }
-                }
-            }
-        }
-        __syncthreads();
-    }
-    if (wave == 0) {
-        const float lf = *Lf;
-        const float inv = lf > 0.0f ? 1.0f / lf : 0.0f;
-        float *o = a.O + row * D + lane * DPT;
-#pragma unroll
-        for (int e = 0; e < DPT; ++e) o[e] = acc[e] * inv;
-    }
-}
-
 bool use_rowwise(const Attn &a)
 {
     return a.head_dim > 256 || static_cast<uint64_t>(a.batch) * a.heads > 65535u ||
@@ -1245,7 +1043,8 @@ float *attention_scratch(int hip_device)
 
 size_t attention_ws_bytes(const Attn &a)
 {
-    if (use_rowwise(a) || use_exact_tiled(a)) return 0;
+    if (use_exact_tiled(a)) return a.seq_q <= 4 ? attention_exact_decode_ws_bytes(a) : 0;
+    if (use_rowwise(a)) return 0;
     uint32_t qb, splits, kps;
     plan(a, qb, splits, kps);
     if (use_prefill(a)) {
@@ -1259,25 +1058,12 @@ size_t attention_ws_bytes(const Attn &a)
     return static_cast<size_t>(splits) * rows * (a.head_dim + 2) * sizeof(float);
 }
 
-template <int D>
-void launch_exact_decode(hipStream_t s, const Attn &a)
-{
-    using G = ExactDec<D>;
-    static std::atomic<bool> lds_optin{false};
-    if (!lds_optin && G::kLds > 65536)
-        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_exact_decode_kernel<D>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(G::kLds)) == hipSuccess;
-    const dim3 grid(a.seq_q, a.batch * a.heads);
-    attn_exact_decode_kernel<D><<<grid, kThreads, G::kLds, s>>>(a);
-}
-
 void attention(hipStream_t s, const Attn &a, float *ws)
 {
     if (use_exact_tiled(a)) {
         const bool decode = a.seq_q <= 4;
-        if (a.head_dim == 128) decode ? launch_exact_decode<128>(s, a) : attention_exact_prefill(s, a);
-        else decode ? launch_exact_decode<64>(s, a) : attention_exact_prefill(s, a);
+        if (decode) attention_exact_decode(s, a, ws);
+        else attention_exact_prefill(s, a);
         return;
     }
     if (use_rowwise(a)) {

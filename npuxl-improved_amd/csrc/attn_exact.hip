@@ -47,6 +47,7 @@
 // rows are dispatched first.
 #include "kernels.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include "device_math.hpp"
 #include "lds_dma.hpp"
@@ -212,22 +213,32 @@ __global__ __launch_bounds__(XT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             if (t == 1 && kc_w <= 32) continue;   // uniform: no key of the second tile is seen
-            f32x32 acc0, acc1, acc2, acc3;
-#pragma unroll
-            for (int r = 0; r < 32; ++r) acc0[r] = acc1[r] = acc2[r] = acc3[r] = 0.0f;
+            // Two passes of two chain pairs each: (0,4) and (1,5), then (2,6)
+            // and (3,7); hsum256's ((c0+c4) + (c1+c5)) + ((c2+c6) + (c3+c7)).
             const float *kr = Kb + (32 * t + c32) * L::KP + 4 * h;
+            float s01[16];
+            f32x32 acc0, acc1;
+#pragma unroll
+            for (int r = 0; r < 32; ++r) acc0[r] = acc1[r] = 0.0f;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const float4 kv = *reinterpret_cast<const float4 *>(kr + 8 * i);
+                const float2 kv = *reinterpret_cast<const float2 *>(kr + 8 * i);
                 acc0 = mfma1(kv.x, qop[i].x, acc0);
                 acc1 = mfma1(kv.y, qop[i].y, acc1);
-                acc2 = mfma1(kv.z, qop[i].z, acc2);
-                acc3 = mfma1(kv.w, qop[i].w, acc3);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s01[r] = (acc0[r] + acc0[r + 16]) + (acc1[r] + acc1[r + 16]);
+#pragma unroll
+            for (int r = 0; r < 32; ++r) acc0[r] = acc1[r] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const float2 kv = *reinterpret_cast<const float2 *>(kr + 8 * i + 2);
+                acc0 = mfma1(kv.x, qop[i].z, acc0);
+                acc1 = mfma1(kv.y, qop[i].w, acc1);
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float dot = ((acc0[r] + acc0[r + 16]) + (acc1[r] + acc1[r + 16])) +
-                                  ((acc2[r] + acc2[r + 16]) + (acc3[r] + acc3[r + 16]));
+                const float dot = s01[r] + ((acc0[r] + acc0[r + 16]) + (acc1[r] + acc1[r + 16]));
                 const uint32_t key = k0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
                 const float sc = dot * a.scale;
                 const bool valid = qvalid && key < kend && !(a.causal && key > qi + off);
@@ -255,46 +266,48 @@ __global__ __launch_bounds__(XT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         const bool live = isfinite(bmax);
         const float nm = m < bmax ? bmax : m;
         const float alpha = live ? dev::fast_expf_unfused(m - nm) : 1.0f;
-        // Weights in key order: Plo[t][r] is key 32t + 8(r/4) + r%4, Phi[t][r]
-        // key 32t + 8(r/4) + 4 + r%4 (the other half's keys by exchange).
-        float Plo[2][16], Phi[2][16];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = live ? dev::fast_expf_unfused(S[t][r] - nm) : 0.0f;
-                const float x = __shfl_xor(p, 32, 64);
-                Plo[t][r] = h ? x : p;
-                Phi[t][r] = h ? p : x;
-            }
-        if (live) {
-            float psum = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int a4 = 0; a4 < 4; ++a4) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) psum = psum + Plo[t][4 * a4 + j];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) psum = psum + Phi[t][4 * a4 + j];
-                }
-            l = l * alpha + psum;
-            m = nm;
-        }
 #pragma unroll
         for (int mm = 0; mm < NM; ++mm)
 #pragma unroll
             for (int r = 0; r < 32; ++r) oacc[mm][r] = oacc[mm][r] * alpha;
 
-        // Output chain, keys ascending; keys no row of the wave sees are skipped.
+        // Keys in groups of eight (32t + 8g .. +7): the weights of this
+        // half's four keys, the other half's four by exchange, the weight
+        // sum in key order, then the output chain, keys ascending (keys no
+        // row of the wave sees are skipped).
+        float psum = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < XB; ++kk) {
-            const int t = kk >> 5, r = 4 * ((kk & 31) >> 3) + (kk & 3);
-            const float p = (kk & 4) ? Phi[t][r] : Plo[t][r];
-            if (kk < static_cast<int>(kc_w)) {   // uniform
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int mm = 0; mm < NM; ++mm) oacc[mm] = mfma1(Vb[kk * D + 64 * mm + lane], p, oacc[mm]);
+            for (int g = 0; g < 4; ++g) {
+                // One group's operands in registers at a time: without the
+                // fence the scheduler hoists every V read of the block.
+                __builtin_amdgcn_sched_barrier(0);
+                float lo[4], hi[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float p = live ? dev::fast_expf_unfused(S[t][4 * g + j] - nm) : 0.0f;
+                    const float x = __shfl_xor(p, 32, 64);
+                    lo[j] = h ? x : p;
+                    hi[j] = h ? p : x;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) psum = psum + lo[j];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) psum = psum + hi[j];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int kk = 32 * t + 8 * g + j;
+                    if (kk < static_cast<int>(kc_w)) {   // uniform
+#pragma unroll
+                        for (int mm = 0; mm < NM; ++mm)
+                            oacc[mm] = mfma1(Vb[kk * D + 64 * mm + lane], j < 4 ? lo[j] : hi[j - 4], oacc[mm]);
+                    }
+                }
             }
+        if (live) {
+            l = l * alpha + psum;
+            m = nm;
         }
     }
 
@@ -338,12 +351,266 @@ void launch(hipStream_t s, const Attn &a)
     attn_exact_mfma_kernel<D><<<grid, XT, L::kLds, s>>>(a);
 }
 
+// ---------------------------------------------------------------------------
+// Reference-order decode (seq_q <= 4).  In attention_range only the output
+// chain is sequential over keys; the scores are independent per key and the
+// chain is independent per head element.  So decode runs as two kernels:
+//   attn_dec_scores  s[row][key] = dot_avx2(q_row, k_key) * scale, then -inf
+//                    for a causally masked key or + mask, every key in
+//                    parallel (two lanes per key, chains 0-3 and 4-7; the
+//                    pair exchange gives hsum256's pairing);
+//   attn_dec_chain   one wave per (row, 64 head elements): per 64-key block
+//                    the block max, m, alpha and the weights from the saved
+//                    scores (every wave of a row derives the same ones), the
+//                    weight sum and acc = fma(v_j, p_j, acc) in key order for
+//                    p_j != 0, with the V slices and the scores of the next
+//                    three blocks copied from HBM into LDS meanwhile.
+// The scores live in a workspace of rows x pitch floats (pitch = seq_k
+// rounded up to 64); calls whose scores exceed kDecScoreCap run over
+// consecutive (batch, head) ranges.
+// ---------------------------------------------------------------------------
+constexpr int DTPW = 4;                     // 64-key K tiles per scores wave
+constexpr int DNB = 4;                      // blocks in flight per chain wave
+constexpr int DTV = XB * 64;                // floats per V tile (64 keys x 64 head elements)
+constexpr int DOPS = 17;                    // copies per block: 16 of V, one of scores
+constexpr size_t kDecLds = static_cast<size_t>(DNB) * (DTV + XB) * sizeof(float) + XB * sizeof(float);
+constexpr uint64_t kDecScoreCap = 32ull << 20;
+
+uint32_t dec_pitch(const Attn &a) { return (a.seq_k + XB - 1) / XB * XB; }
+
+template <int D>
+constexpr size_t dec_scores_lds() { return (static_cast<size_t>(XB) * XL<D>::KP + 4 * D) * sizeof(float); }
+
+// Maximum over the wave's 64 lanes, in every lane (order-free: NaN operands
+// are ignored as by fmaxf, and the sign of a zero maximum never matters).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, ROWS, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v)
+{
+    v = fmaxf(v, dpp_f<0xB1, 0xf>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E, 0xf>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141, 0xf>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140, 0xf>(v));   // row_mirror: every lane holds its row's max
+    v = fmaxf(v, dpp_f<0x142, 0xa>(v));   // row_bcast15 into rows 1 and 3
+    v = fmaxf(v, dpp_f<0x143, 0xc>(v));   // row_bcast31 into rows 2 and 3: lane 63 holds the max
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Scores: one wave per (batch, head) and DTPW tiles of 64 keys (four such
+// workgroups per CU by LDS); the wave copies a tile's K rows into LDS (row
+// pitch D + 4 floats: lane j's 16-byte reads of key j are conflict-free) and
+// lane j runs key j's eight chains for every query row (the rows' elements
+// as broadcast reads).
+template <int D>
+__global__ __launch_bounds__(64) void attn_dec_scores(Attn a, float *S, uint32_t pitch)
+{
+#pragma clang fp contract(off)
+    using L = XL<D>;
+    constexpr int NI = D / 8;
+    extern __shared__ float4 sm4[];
+    const int lane = threadIdx.x;
+    float *Kt = reinterpret_cast<float *>(sm4);          // [64][KP]
+    float *Qs = Kt + XB * L::KP;                         // [sq][D]
+    const uint64_t bh = blockIdx.y;
+    const uint32_t sq = a.seq_q, sk = a.seq_k;
+    const uint32_t off = sk > sq ? sk - sq : 0;
+    const float *Kh = a.K + bh * sk * D;
+    for (uint32_t i = lane; i < sq * D; i += 64) Qs[i] = a.Q[bh * sq * D + i];
+    __syncthreads();
+    const uint32_t t0 = blockIdx.x * DTPW;
+    for (uint32_t tt = 0; tt < DTPW; ++tt) {
+        const uint32_t k0 = (t0 + tt) * XB;
+        if (k0 >= sk) break;   // uniform over the wave; no barrier follows
+        for (int i = 0; i < L::KCH; ++i) {
+            const uint32_t sl = static_cast<uint32_t>(i) * 64 + lane;
+            const uint32_t r = sl / L::KCH, c = sl % L::KCH;
+            const uint32_t key = min(k0 + r, sk - 1);
+            lds::dma16_nt(Kh + static_cast<uint64_t>(key) * D + (c < D / 4 ? 4 * c : 0),
+                          reinterpret_cast<int8_t *>(Kt) + i * 1024);
+        }
+        lds::wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+        const uint32_t key = k0 + lane;
+        const float *kr = Kt + lane * L::KP;
+        for (uint32_t r = 0; r < sq; ++r) {
+            const float *qr = Qs + r * D;
+            float c8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const float4 ka = *reinterpret_cast<const float4 *>(kr + 8 * i);
+                const float4 kb = *reinterpret_cast<const float4 *>(kr + 8 * i + 4);
+                const float4 qa = *reinterpret_cast<const float4 *>(qr + 8 * i);
+                const float4 qb = *reinterpret_cast<const float4 *>(qr + 8 * i + 4);
+                c8[0] = fmaf(qa.x, ka.x, c8[0]);
+                c8[1] = fmaf(qa.y, ka.y, c8[1]);
+                c8[2] = fmaf(qa.z, ka.z, c8[2]);
+                c8[3] = fmaf(qa.w, ka.w, c8[3]);
+                c8[4] = fmaf(qb.x, kb.x, c8[4]);
+                c8[5] = fmaf(qb.y, kb.y, c8[5]);
+                c8[6] = fmaf(qb.z, kb.z, c8[6]);
+                c8[7] = fmaf(qb.w, kb.w, c8[7]);
+            }
+            const float dot = ((c8[0] + c8[4]) + (c8[1] + c8[5])) + ((c8[2] + c8[6]) + (c8[3] + c8[7]));
+            const uint64_t row = bh * sq + r;
+            if (key < sk) {
+                float sc = dot * a.scale;
+                if (a.causal && key > r + off) sc = -__builtin_inff();
+                else if (a.mask) sc = sc + a.mask[row * sk + key];
+                S[row * pitch + key] = sc;
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the tile is read before the next copy
+    }
+}
+
+// Output chain: one wave per (row, 64 head elements).
+template <int D>
+__global__ __launch_bounds__(64) void attn_dec_chain(Attn a, const float *S, uint32_t pitch)
+{
+#pragma clang fp contract(off)
+    extern __shared__ float4 sm4[];
+    float *Vt = reinterpret_cast<float *>(sm4);   // [DNB][64 keys][64]
+    float *St = Vt + DNB * DTV;                   // [DNB][64] scores
+    float *Pw = St + DNB * XB;                    // [64] weights of the current block
+    const int lane = threadIdx.x;
+    const uint64_t row = blockIdx.x;
+    const uint32_t sq = a.seq_q, sk = a.seq_k;
+    const uint32_t off = sk > sq ? sk - sq : 0;
+    const uint64_t bh = row / sq;
+    const uint32_t qi = static_cast<uint32_t>(row % sq);
+    const uint32_t kend = a.causal ? min(sk, qi + off + 1) : sk;
+    const uint32_t nblk = (kend + XB - 1) / XB;
+    const float *Vh = a.V + bh * sk * D + blockIdx.y * 64;
+    const float *Sr = S + row * pitch;
+
+    // Block t's copies: 16 of four keys x 64 head elements each, then the
+    // block's 64 scores by lanes 0-15 (the row pitch keeps them in the row).
+    auto copy = [&](uint32_t t) {
+        int8_t *vd = reinterpret_cast<int8_t *>(Vt + (t % DNB) * DTV);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const uint32_t key = min(t * XB + 4 * u + (lane >> 4), kend - 1);
+            lds::dma16_nt(Vh + static_cast<uint64_t>(key) * D + 4 * (lane & 15), vd + u * 1024);
+        }
+        if (lane < 16) lds::dma16(Sr + t * XB + 4 * lane, reinterpret_cast<int8_t *>(St + (t % DNB) * XB));
+    };
+    for (uint32_t t = 0; t < DNB - 1 && t < nblk; ++t) copy(t);
+
+    float m = -__builtin_inff(), l = 0.0f, acc = 0.0f;
+    for (uint32_t t = 0; t < nblk; ++t) {
+        if (t + DNB - 1 < nblk) {
+            copy(t + DNB - 1);
+            lds::wait_vmcnt<DOPS * (DNB - 1)>();
+        } else {
+            lds::wait_vmcnt<0>();
+        }
+        asm volatile("" ::: "memory");
+        const uint32_t k0 = t * XB, kc = min(static_cast<uint32_t>(XB), kend - k0);
+        const float *vt = Vt + (t % DNB) * DTV + lane;
+        const float sc = lane < static_cast<int>(kc) ? St[(t % DNB) * XB + lane] : -__builtin_inff();
+        const float bmax = wave_max_dpp(sc);
+        if (isfinite(bmax)) {   // uniform
+            const float nm = m < bmax ? bmax : m;
+            const float alpha = dev::fast_expf_unfused(m - nm);
+            const float p = dev::fast_expf_unfused(sc - nm);   // 0 past kc
+            Pw[lane] = p;
+            const uint64_t nz = __ballot(p != 0.0f);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            float psum = 0.0f;
+            acc = acc * alpha;
+            if (kc == XB && nz == ~0ull) {
+                // Every weight of a whole block is nonzero: the chains without
+                // a test, every read of the block issued up front.
+                float v[XB], pj[XB];
+#pragma unroll
+                for (int j = 0; j < XB; j += 4) {
+                    const float4 w4 = *reinterpret_cast<const float4 *>(Pw + j);
+                    pj[j] = w4.x; pj[j + 1] = w4.y; pj[j + 2] = w4.z; pj[j + 3] = w4.w;
+                }
+#pragma unroll
+                for (int j = 0; j < XB; ++j) v[j] = vt[j * 64];
+#pragma unroll
+                for (int j = 0; j < XB; ++j) {
+                    psum = psum + pj[j];
+                    acc = fmaf(v[j], pj[j], acc);
+                }
+            } else {
+                for (uint32_t j = 0; j < kc; j += 4) {
+                    const float4 w4 = *reinterpret_cast<const float4 *>(Pw + j);
+                    const float pq[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        if (j + u < kc) psum = psum + pq[u];
+                        if ((nz >> (j + u)) & 1ull) acc = fmaf(vt[(j + u) * 64], pq[u], acc);
+                    }
+                }
+            }
+            l = l * alpha + psum;
+            m = nm;
+        }
+        // This wave's reads of slot t % DNB are done before block t + DNB's
+        // copies land in it.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    a.O[row * D + blockIdx.y * 64 + lane] = acc * inv;
+}
+
+template <int D>
+void launch_decode(hipStream_t s, const Attn &a, float *ws)
+{
+    static std::atomic<bool> lds_optin{false};
+    if (!lds_optin)
+        lds_optin = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_dec_chain<D>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kDecLds)) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void *>(attn_dec_scores<D>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(dec_scores_lds<D>())) == hipSuccess;
+    const uint32_t pitch = dec_pitch(a);
+    const uint64_t per_bh = static_cast<uint64_t>(a.seq_q) * pitch * sizeof(float);
+    const uint64_t nbh = static_cast<uint64_t>(a.batch) * a.heads;
+    const uint64_t step = std::max<uint64_t>(1, kDecScoreCap / per_bh);
+    for (uint64_t b0 = 0; b0 < nbh; b0 += step) {
+        const uint32_t n = static_cast<uint32_t>(std::min(step, nbh - b0));
+        Attn c = a;   // the (batch, head) range [b0, b0 + n) as a batch of n single heads
+        const uint64_t qo = b0 * a.seq_q * D, ko = b0 * a.seq_k * D;
+        c.Q = a.Q + qo; c.K = a.K + ko; c.V = a.V + ko; c.O = a.O + qo;
+        c.mask = a.mask ? a.mask + b0 * a.seq_q * a.seq_k : nullptr;
+        c.batch = n;
+        c.heads = 1;
+        const uint32_t tiles = (a.seq_k + XB - 1) / XB;
+        attn_dec_scores<D><<<dim3((tiles + DTPW - 1) / DTPW, n), 64, dec_scores_lds<D>(), s>>>(c, ws, pitch);
+        attn_dec_chain<D><<<dim3(n * a.seq_q, D / 64), 64, kDecLds, s>>>(c, ws, pitch);
+    }
+}
+
 }  // namespace
 
 void attention_exact_prefill(hipStream_t s, const Attn &a)
 {
     if (a.head_dim == 128) launch<128>(s, a);
     else launch<64>(s, a);
+}
+
+size_t attention_exact_decode_ws_bytes(const Attn &a)
+{
+    const uint64_t per_bh = static_cast<uint64_t>(a.seq_q) * dec_pitch(a) * sizeof(float);
+    const uint64_t nbh = static_cast<uint64_t>(a.batch) * a.heads;
+    const uint64_t step = std::max<uint64_t>(1, kDecScoreCap / per_bh);
+    return static_cast<size_t>(std::min(step, nbh) * per_bh);
+}
+
+void attention_exact_decode(hipStream_t s, const Attn &a, float *ws)
+{
+    if (a.head_dim == 128) launch_decode<128>(s, a, ws);
+    else launch_decode<64>(s, a, ws);
 }
 
 }  // namespace k

@@ -166,6 +166,11 @@ void attention(hipStream_t s, const Attn &a, float *ws);
 // Reference-order prefill (exact, seq_q > 4, head_dim 64 or 128) on the fp32
 // matrix cores (attn_exact.hip).
 void attention_exact_prefill(hipStream_t s, const Attn &a);
+// Reference-order decode (exact, seq_q <= 4, head_dim 64 or 128): scores,
+// then the output chain (attn_exact.hip); ws holds
+// attention_exact_decode_ws_bytes(a).
+size_t attention_exact_decode_ws_bytes(const Attn &a);
+void attention_exact_decode(hipStream_t s, const Attn &a, float *ws);
 // The allocation-free attention entry point's device scratch: a file-scope
 // array of kAttnScratchBytes in attention.hip, one copy per GPU.  Setup looks
 // its address up once per device (that device current) and keeps it;

@@ -51,6 +51,18 @@ __device__ __forceinline__ void dma16(const void *src, int8_t *lds_dst)
                  : "memory", "m0");
 }
 
+// The same copy of data read once (nontemporal: no cache line is kept for
+// reuse), for streams such as attention's K and V.
+__device__ __forceinline__ void dma16_nt(const void *src, int8_t *lds_dst)
+{
+    const uint32_t lds = static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t *)(lds_dst)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory", "m0");
+}
+
 // The same copy with a wave-uniform 64-bit base (SGPRs) and a 32-bit
 // per-lane byte offset: lane l reads base + voff and writes lds_dst + 16 l.
 __device__ __forceinline__ void dma16_s(const int8_t *base, uint32_t voff, int8_t *lds_dst)

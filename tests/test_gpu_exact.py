@@ -150,3 +150,74 @@ def test_attention_reference_order_noalloc(exact_gpu):
     for x in (bq, bk, bv, bo):
         s.free(x)
     assert bits(got, oracle.attention_avx2(Q, K, V, None, 1))
+
+
+def bits_or_nan(a, b):
+    """Bit for bit, except that a NaN matches a NaN of any payload (x86's
+    default NaN is 0xffc00000, the GPU's 0x7fc00000)."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+@pytest.mark.parametrize("b,h,sq,sk,d,causal,mask", [
+    (2, 3, 200, 130, 128, 1, None),        # seq_k < seq_q, causal
+    (1, 2, 129, 1000, 128, 0, "normal"),   # ragged row tiles, additive mask
+    (1, 2, 100, 300, 64, 1, None)])        # seq_k > seq_q, causal offset
+def test_attention_reference_order_prefill_shapes(exact_gpu, b, h, sq, sk, d, causal, mask):
+    """The matrix-core prefill tiles (32 rows per wave, 128 per workgroup,
+    64-key blocks) at ragged sizes and both causal offsets."""
+    Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
+    K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+    V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+    M = RNG.standard_normal((b, h, sq, sk)).astype(np.float32) if mask else None
+    got = g.attention(exact_gpu, Q, K, V, M, causal)
+    assert bits(got, block_oracle.attention_threaded(Q, K, V, causal, mask=M, avx2=True))
+
+
+def test_attention_reference_order_nonfinite_v_masked(exact_gpu):
+    """Infinite and NaN values of V at keys some rows never weigh: the matrix
+    core would turn v * 0 into NaN where the reference skips the key, so
+    those waves take the exact vector-ALU recompute; rows that see the key
+    are inf/NaN in both."""
+    b, h, s, d = 1, 2, 70, 128
+    Q = RNG.standard_normal((b, h, s, d)).astype(np.float32)
+    K = RNG.standard_normal((b, h, s, d)).astype(np.float32)
+    V = RNG.standard_normal((b, h, s, d)).astype(np.float32)
+    V[0, 0, 50, :] = np.inf
+    V[0, 1, 60, 3] = -np.inf
+    V[0, 1, 20, 7] = np.nan
+    got = g.attention(exact_gpu, Q, K, V, None, 1)
+    want = block_oracle.attention_threaded(Q, K, V, 1, avx2=True)
+    assert np.isfinite(want[0, 0, :50]).all() and not np.isfinite(want[0, 0, 50:]).all()
+    assert bits_or_nan(got, want)
+
+
+def test_attention_reference_order_denormal_v(exact_gpu):
+    """V of denormal magnitude: products underflow to signed zeros, so the
+    sign of a zero accumulator decides the output's bits; the waves with
+    zero outputs take the exact recompute."""
+    b, h, s, d = 1, 2, 40, 64
+    Q = RNG.standard_normal((b, h, s, d)).astype(np.float32)
+    K = RNG.standard_normal((b, h, s, d)).astype(np.float32)
+    tiny = np.float32(1.4e-45)
+    V = (RNG.choice([-1.0, 1.0], (b, h, s, d)) * RNG.integers(1, 4, (b, h, s, d))).astype(np.float32) * tiny
+    got = g.attention(exact_gpu, Q, K, V, None, 1)
+    want = block_oracle.attention_threaded(Q, K, V, 1, avx2=True)
+    assert (want == 0).any() and np.signbit(want[want == 0]).any()
+    assert bits(got, want)
+
+
+def test_attention_reference_order_nan_scores(exact_gpu):
+    """A NaN query row (every score NaN: the block max ignores them, the row
+    is never live, output 0) and a NaN key (its weight is NaN in every row)."""
+    b, h, s, d = 1, 2, 64, 128
+    Q = RNG.standard_normal((b, h, s, d)).astype(np.float32)
+    K = RNG.standard_normal((b, h, s, d)).astype(np.float32)
+    V = RNG.standard_normal((b, h, s, d)).astype(np.float32)
+    Q[0, 0, 5, 3] = np.nan
+    K[0, 1, 9, :] = np.nan
+    got = g.attention(exact_gpu, Q, K, V, None, 0)
+    want = block_oracle.attention_threaded(Q, K, V, 0, avx2=True)
+    assert (want[0, 0, 5] == 0).all() and np.isnan(want[0, 1]).all()
+    assert bits_or_nan(got, want)
