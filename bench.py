@@ -279,13 +279,20 @@ def bench_attention(s: Session, steps: int, warmup: int):
     return out
 
 
-def reference_order_session() -> Session:
-    """A session whose device rounds in the reference's order
-    (VNPU_CONFIG_REFERENCE_ORDER: bit-exact attention, hence block)."""
+def high_throughput_session() -> Session:
+    """A session whose device is created with VNPU_CONFIG_HIGH_THROUGHPUT:
+    split-bf16 matrix-core attention, within 2e-3 of the reference's
+    attention but not of its block (int8 roundings flip downstream)."""
     cfg = abi.Config()
     cfg.abi_version = 1
-    cfg.flags = abi.CONFIG_REFERENCE_ORDER
+    cfg.flags = abi.CONFIG_HIGH_THROUGHPUT
     return Session(None, cfg)
+
+
+# The block on a high-throughput device, end to end against the reference's
+# block output (tests/test_block.py, measured on MI355X).
+HIGH_THROUGHPUT_BLOCK_NOTE = ("not tolerance-matched: end to end 9.9e-3 (decode) and 1.55e-2 (prefill) "
+                              "max-rel > 2e-3; the default device's block is bit-exact")
 
 
 def bench_copy(s: Session, steps: int):
@@ -491,13 +498,13 @@ def main():
             log("copy", bench_copy(s, 5))
         elif args.only == "attention":
             log("attention", bench_attention(s, args.steps, args.warmup))
-            x = reference_order_session()
-            log("attention reference-order", bench_attention(x, args.steps, args.warmup))
+            x = high_throughput_session()
+            log("attention high-throughput", bench_attention(x, args.steps, args.warmup))
             x.close()
         elif args.only == "block":
             log("block", bench_block(s, args.steps))
-            x = reference_order_session()
-            log("block reference-order", bench_block(x, args.steps))
+            x = high_throughput_session()
+            log("block high-throughput", bench_block(x, args.steps))
             x.close()
         elif args.only == "config1":
             log("config1", bench_config1(s, args.steps))
@@ -539,16 +546,20 @@ def main():
         for n in (4096, 14336):
             extras["config3_gemm_f32"].append(rounded(bench_gemm_f32(s, 2048, 4096, n, 5, 2)))
             log("gemm_f32", extras["config3_gemm_f32"][-1])
+        # The default device: attention in the reference's order, so the
+        # block is bit-exact with the reference's (the north-star parity bar).
         extras["config4_attention"] = {k: rounded(v, 3) for k, v in bench_attention(s, 20, 3).items()}
         log("attention", extras["config4_attention"])
         extras["config4_block"] = {k: rounded(v, 3) for k, v in bench_block(s, 20).items()}
+        extras["config4_block"]["parity"] = "bit-exact with the reference's block output"
         log("block", extras["config4_block"])
-        x = reference_order_session()
-        extras["config4_attention_reference_order"] = {k: rounded(v, 3)
-                                                      for k, v in bench_attention(x, 20, 3).items()}
-        log("attention reference-order", extras["config4_attention_reference_order"])
-        extras["config4_block_reference_order"] = {k: rounded(v, 3) for k, v in bench_block(x, 20).items()}
-        log("block reference-order", extras["config4_block_reference_order"])
+        x = high_throughput_session()
+        extras["config4_attention_high_throughput"] = {k: rounded(v, 3)
+                                                       for k, v in bench_attention(x, 20, 3).items()}
+        log("attention high-throughput", extras["config4_attention_high_throughput"])
+        extras["config4_block_high_throughput"] = {k: rounded(v, 3) for k, v in bench_block(x, 20).items()}
+        extras["config4_block_high_throughput"]["parity"] = HIGH_THROUGHPUT_BLOCK_NOTE
+        log("block high-throughput", extras["config4_block_high_throughput"])
         x.close()
         extras["config5"] = {k: rounded(v, 3) for k, v in bench_config5(s, 10).items()}
         log("config5", extras["config5"])

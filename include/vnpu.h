@@ -88,8 +88,11 @@ extern "C" {
 #define VNPU_CONFIG_LOW_LATENCY     (1u << 5)
 #define VNPU_CONFIG_HIGH_THROUGHPUT (1u << 6)
 /* MI355X extension (additive; no reference counterpart): ATTENTION_F32 in the
- * reference CPU build's order of roundings, bit for bit (slower for prefill).
- * The environment variable VNPU_REFERENCE_ORDER=1 sets it for every device. */
+ * reference CPU build's order of roundings, bit for bit.  This is the default;
+ * the flag keeps it when VNPU_CONFIG_HIGH_THROUGHPUT (or the environment
+ * variable VNPU_REFERENCE_ORDER=0) would select the faster split-bf16
+ * matrix-core attention (about 1.5e-5 from float64 softmax attention, not the
+ * reference's bits).  VNPU_REFERENCE_ORDER=1 sets it for every device. */
 #define VNPU_CONFIG_REFERENCE_ORDER (1u << 7)
 
 /* Command flags: reference include/vnpu.h:95-100.  They are OR-ed over a

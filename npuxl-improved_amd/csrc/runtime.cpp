@@ -442,8 +442,13 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_device_create(const vnpu_config_t *config,
             tn = 64;
         }
         apply_tiles(d, tm, tk, tn, kTilesI8 | kTilesF32);
+        // ATTENTION_F32 rounds in the reference's order unless the caller
+        // asks for throughput (VNPU_CONFIG_HIGH_THROUGHPUT, or
+        // VNPU_REFERENCE_ORDER=0 for every device); VNPU_CONFIG_REFERENCE_ORDER
+        // or VNPU_REFERENCE_ORDER=1 keep the reference's order regardless.
         const char *ro = std::getenv("VNPU_REFERENCE_ORDER");
-        d->reference_order = (cfg.flags & VNPU_CONFIG_REFERENCE_ORDER) != 0 || (ro && ro[0] == '1');
+        const bool fast = (cfg.flags & VNPU_CONFIG_HIGH_THROUGHPUT) != 0 || (ro && ro[0] == '0');
+        d->reference_order = (cfg.flags & VNPU_CONFIG_REFERENCE_ORDER) != 0 || (ro && ro[0] == '1') || !fast;
         // "threads" = parallel units: the CU count unless the caller pins it.
         const uint32_t units = cfg.num_threads ? cfg.num_threads : d->cu_count;
 

@@ -184,7 +184,7 @@ struct vnpu_device {
     // of the dtype it tuned.  0 = automatic.
     std::atomic<uint32_t> i8_variant{0};   // int8 GEMM kernel (gemm_i8_variant_for_tiles)
     std::atomic<uint32_t> f32_depth{0};    // f32 K depth per workgroup (split-K)
-    bool reference_order = false;          // VNPU_CONFIG_REFERENCE_ORDER: attention bit-exact
+    bool reference_order = true;           // attention bit-exact (off: VNPU_CONFIG_HIGH_THROUGHPUT)
     // Culled tiles counted on the GPU (MATMUL_F32 with a device-resident tile
     // mask); folded into the status when read.  Allocated on first use.
     unsigned long long *culled_dev = nullptr;

@@ -52,7 +52,8 @@ CMD_FLAG_CELL_DMA = 1 << 3
 CMD_FLAG_VOODOO_FIFO = 1 << 4
 
 CONFIG_TRACE = 1 << 0
-CONFIG_REFERENCE_ORDER = 1 << 7   # kernels that round in the reference's order (include/vnpu.h)
+CONFIG_HIGH_THROUGHPUT = 1 << 6   # the faster split-bf16 attention (not the reference's bits)
+CONFIG_REFERENCE_ORDER = 1 << 7   # attention in the reference's order (the default; include/vnpu.h)
 
 
 class Config(C.Structure):

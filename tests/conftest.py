@@ -15,7 +15,8 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def gpu():
-    """One MI355X session for all GPU tests (device + stream on libvnpu.so)."""
+    """One MI355X session for all GPU tests (device + stream on libvnpu.so;
+    the default device: ATTENTION_F32 in the reference's order)."""
     from vnpu_mi355x import Session
     s = Session()
     yield s
@@ -23,9 +24,23 @@ def gpu():
 
 
 @pytest.fixture(scope="session")
+def fast_gpu():
+    """An MI355X session whose device is created with
+    VNPU_CONFIG_HIGH_THROUGHPUT: ATTENTION_F32 on the split-bf16 matrix-core
+    kernels (within tolerance of the reference, not its bits)."""
+    from vnpu_mi355x import Session, abi
+    cfg = abi.Config()
+    cfg.abi_version = 1
+    cfg.flags = abi.CONFIG_HIGH_THROUGHPUT
+    s = Session(None, cfg)
+    yield s
+    s.close()
+
+
+@pytest.fixture(scope="session")
 def exact_gpu():
-    """A second MI355X session whose device is created with
-    VNPU_CONFIG_REFERENCE_ORDER: every op rounds in the reference's order."""
+    """An MI355X session whose device is created with
+    VNPU_CONFIG_REFERENCE_ORDER (the default order, asked for explicitly)."""
     from vnpu_mi355x import Session, abi
     cfg = abi.Config()
     cfg.abi_version = 1

@@ -122,15 +122,16 @@ def test_block_stages_equals_block():
         assert np.array_equal(a.view(np.uint32), st["out"].view(np.uint32))
 
 
-# End-to-end bound of the full-size block in the default (fast attention)
-# mode, against the reference's own block output (the oracle's AVX2-order
-# chain): every stage but attention is bit-exact, and attention's f32
-# summation-order differences of ~1e-7 flip a few int8 roundings at the
-# three quantize stages after it; each flip moves later stages by a whole
-# int8 step, so the end-to-end error is the flips', not the ops'.  Measured
-# on MI355X: decode 9.9e-3, prefill 1.55e-2; the bounds are twice that.  On
-# a device created with VNPU_CONFIG_REFERENCE_ORDER the block is bit-exact.
-FULL_E2E_BOUND = {"decode": 0.02, "prefill": 0.03}
+# The north-star bar for the block: within 2e-3 max-rel of the reference's
+# block output (the oracle's AVX2-order chain).  The default device computes
+# ATTENTION_F32 in the reference's order, so its block is bit-exact.  A device
+# created with VNPU_CONFIG_HIGH_THROUGHPUT runs the split-bf16 attention:
+# every other stage is still bit-exact on its input, but attention's ~1e-7
+# summation-order differences flip a few int8 roundings at the three quantize
+# stages after it, and each flip moves later stages by a whole int8 step
+# (measured on MI355X: decode 9.9e-3, prefill 1.55e-2 end to end), so that
+# mode misses the bar and is reported as an expected failure.
+NORTH_STAR_TOL = 2e-3
 
 
 def _full_block(gpu, B, T, past, ctx, tag):
@@ -169,7 +170,8 @@ def _full_block(gpu, B, T, past, ctx, tag):
 def _check_stages(shape, w32, wq, inputs, gpu_out, B, T, past, ctx, exact):
     """Each op's GPU output against the oracle's restatement of the
     reference's AVX2 build applied to the GPU's own input of that stage:
-    every stage bit-exact except attention in the default mode (within 2e-3).
+    every stage bit-exact except attention on a high-throughput device
+    (within 2e-3).
     Then the whole block against the oracle's chain from the same x, which is
     the reference's block output bit for bit
     (test_reference_block_bit_exact_avx2_chain).  Returns (end-to-end error,
@@ -220,7 +222,15 @@ def _check_stages(shape, w32, wq, inputs, gpu_out, B, T, past, ctx, exact):
     return e2e, fl, att_err
 
 
-MODES = [pytest.param(False, id="fast-attention"), pytest.param(True, id="reference-order")]
+MODES = [pytest.param(False, id="high-throughput"), pytest.param(True, id="reference-order")]
+
+
+def _e2e_bar(e2e, exact, what):
+    if exact:
+        assert e2e <= NORTH_STAR_TOL
+    elif e2e > NORTH_STAR_TOL:
+        pytest.xfail(f"{what} on a VNPU_CONFIG_HIGH_THROUGHPUT device: end to end {e2e:.3g} > 2e-3 "
+                     "(split-bf16 attention flips int8 roundings downstream; the default device is bit-exact)")
 
 
 @pytest.mark.gpu
@@ -229,20 +239,20 @@ def test_gpu_block_full_decode_stagewise(request, exact):
     """Config 4 decode at full size (batch 8, context 4096, new token at 4095).
 
     Stage by stage, each op's GPU output against the oracle applied to the
-    GPU's own input of that stage: bit-exact, attention aside in the default
-    mode (within 2e-3).  End to end the block is compared with the
+    GPU's own input of that stage: bit-exact (attention within 2e-3 on a
+    high-throughput device).  End to end the block is compared with the
     reference's block output (the oracle's AVX2-order chain) from the same
     input, and the number of int8 elements that differ at each of the four
-    per-row quantize stages is printed.  With VNPU_CONFIG_REFERENCE_ORDER the
-    whole block is bit-exact.
+    per-row quantize stages is printed.  On the default device the whole
+    block is bit-exact.
     """
-    gpu = request.getfixturevalue("exact_gpu" if exact else "gpu")
+    gpu = request.getfixturevalue("gpu" if exact else "fast_gpu")
     B, T, ctx = 8, 1, 4096
     shape, w32, wq, inputs, G = _full_block(gpu, B, T, ctx - 1, ctx, "config4/decode")
     e2e, fl, att_err = _check_stages(shape, w32, wq, inputs, G, B, T, ctx - 1, ctx, exact)
-    print(f"\n[block decode B8 ctx4096 {'reference-order' if exact else 'fast'}] attention {att_err:.3g}, "
+    print(f"\n[block decode B8 ctx4096 {'reference-order' if exact else 'high-throughput'}] attention {att_err:.3g}, "
           f"end to end {e2e:.3g}, int8 flips per stage (elements, scales): {fl}", flush=True)
-    assert e2e <= FULL_E2E_BOUND["decode"]
+    _e2e_bar(e2e, exact, "block decode")
 
 
 @pytest.mark.gpu
@@ -250,10 +260,10 @@ def test_gpu_block_full_decode_stagewise(request, exact):
 def test_gpu_block_full_prefill_stagewise(request, exact):
     """Config 4 prefill at full size (batch 1, 2048 tokens, causal), with the
     same stage-by-stage bars and end-to-end report as the decode test."""
-    gpu = request.getfixturevalue("exact_gpu" if exact else "gpu")
+    gpu = request.getfixturevalue("gpu" if exact else "fast_gpu")
     B, T = 1, 2048
     shape, w32, wq, inputs, G = _full_block(gpu, B, T, 0, 0, "config4/prefill")
     e2e, fl, att_err = _check_stages(shape, w32, wq, inputs, G, B, T, 0, 0, exact)
-    print(f"\n[block prefill B1 S2048 {'reference-order' if exact else 'fast'}] attention {att_err:.3g}, "
+    print(f"\n[block prefill B1 S2048 {'reference-order' if exact else 'high-throughput'}] attention {att_err:.3g}, "
           f"end to end {e2e:.3g}, int8 flips per stage (elements, scales): {fl}", flush=True)
-    assert e2e <= FULL_E2E_BOUND["prefill"]
+    _e2e_bar(e2e, exact, "block prefill")

@@ -221,3 +221,23 @@ def test_attention_reference_order_nan_scores(exact_gpu):
     want = block_oracle.attention_threaded(Q, K, V, 0, avx2=True)
     assert (want[0, 0, 5] == 0).all() and np.isnan(want[0, 1]).all()
     assert bits_or_nan(got, want)
+
+
+@pytest.mark.parametrize("flags", [0, abi.CONFIG_HIGH_THROUGHPUT | abi.CONFIG_REFERENCE_ORDER])
+def test_attention_default_device_is_reference_order(flags):
+    """ATTENTION_F32 is bit-exact on a device created without flags, and
+    VNPU_CONFIG_REFERENCE_ORDER wins over VNPU_CONFIG_HIGH_THROUGHPUT."""
+    from vnpu_mi355x import Session
+    cfg = abi.Config()
+    cfg.abi_version = 1
+    cfg.flags = flags
+    s = Session(None, cfg)
+    try:
+        for b, h, sq, sk, d in ((1, 2, 200, 200, 128), (2, 3, 1, 700, 64)):
+            Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
+            K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+            V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
+            got = g.attention(s, Q, K, V, None, 1)
+            assert bits(got, block_oracle.attention_threaded(Q, K, V, 1, avx2=True))
+    finally:
+        s.close()

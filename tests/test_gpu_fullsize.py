@@ -205,12 +205,14 @@ def test_config5_mtp_head_softmax_full(gpu):
 @pytest.mark.parametrize("b,h,sq,sk,d,causal", [
     (1, 2, 1, 100, 128, 0), (2, 3, 1, 5000, 128, 1), (1, 2, 4, 3000, 64, 0), (2, 2, 2, 40, 32, 1),
     (1, 2, 64, 200, 128, 1), (1, 2, 150, 700, 64, 0), (1, 2, 20, 50, 80, 0), (1, 1, 1, 1, 128, 0)])
-def test_attention_neg_inf_mask(gpu, b, h, sq, sk, d, causal):
+@pytest.mark.parametrize("dev", ["gpu", "fast_gpu"])
+def test_attention_neg_inf_mask(request, dev, b, h, sq, sk, d, causal):
     """Additive masks holding -inf (padding): leading keys masked, scattered
     -inf entries and one fully masked query row, on the decode kernel (one
     split and several), the prefill kernel and the generic kernel.  A fully
-    masked row is 0, as in the reference (l = 0 -> inv 0)."""
+    masked row is 0, as in the reference (l = 0 -> inv 0).  Both device modes."""
     import gpu_ops as g
+    gpu = request.getfixturevalue(dev)
     Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
     K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
     V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
@@ -278,10 +280,12 @@ def test_forced_f32_depth_large_grid(gpu):
 @pytest.mark.parametrize("b,h,sq,sk,d,causal,use_mask", [
     (1, 2, 5, 40, 320, 1, False), (2, 1, 3, 150, 1024, 0, True), (1, 2, 70, 70, 264, 1, True),
     (1, 70000, 1, 5, 8, 1, False), (2, 40000, 2, 3, 32, 0, True)])
-def test_attention_wide_heads_and_many_heads(gpu, b, h, sq, sk, d, causal, use_mask):
+@pytest.mark.parametrize("dev", ["gpu", "fast_gpu"])
+def test_attention_wide_heads_and_many_heads(request, dev, b, h, sq, sk, d, causal, use_mask):
     """head_dim above 256 and more than 65535 (batch, head) pairs: the
     row-wise kernel (the reference takes any head_dim and any count)."""
     import gpu_ops as g
+    gpu = request.getfixturevalue(dev)
     Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
     K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
     V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)

@@ -706,7 +706,11 @@ def test_rope_positions_and_identity(gpu):
     (2, 3, 129, 200, 64, 0, True), (1, 2, 256, 256, 128, 1, True), (1, 2, 100, 1000, 128, 1, False),
     (1, 1, 5, 5, 128, 1, False), (1, 2, 300, 120, 64, 1, False), (1, 1, 640, 640, 128, 1, False),
     (1, 1, 17, 9, 64, 1, False), (1, 2, 40, 40, 80, 0, False)])
-def test_attention(gpu, b, h, sq, sk, d, causal, use_mask):
+@pytest.mark.parametrize("dev", ["gpu", "fast_gpu"])
+def test_attention(request, dev, b, h, sq, sk, d, causal, use_mask):
+    """Both device modes: the default (reference order) and high throughput
+    (split-bf16 prefill, split decode, generic and row-wise kernels)."""
+    gpu = request.getfixturevalue(dev)
     Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
     K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
     V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
@@ -718,7 +722,7 @@ def test_attention(gpu, b, h, sq, sk, d, causal, use_mask):
 
 @pytest.mark.parametrize("b,h,sq,sk,d,causal", [
     (1, 4, 512, 512, 128, 1), (1, 2, 300, 700, 64, 1), (2, 2, 256, 384, 128, 0)])
-def test_attention_prefill_split_precision(gpu, b, h, sq, sk, d, causal):
+def test_attention_prefill_split_precision(fast_gpu, b, h, sq, sk, d, causal):
     """The prefill kernel's three-term bf16 products (hi*hi + hi*lo + lo*hi)
     against float64 softmax attention: about 2^-16 relative per product, so
     the result sits far below the 2e-3 bar (checked at 1e-4 here; the
@@ -726,7 +730,7 @@ def test_attention_prefill_split_precision(gpu, b, h, sq, sk, d, causal):
     Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)
     K = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
     V = RNG.standard_normal((b, h, sk, d)).astype(np.float32)
-    got = g.attention(gpu, Q, K, V, None, causal)
+    got = g.attention(fast_gpu, Q, K, V, None, causal)
     s = np.einsum("bhqd,bhkd->bhqk", Q.astype(np.float64), K.astype(np.float64)) / np.sqrt(d)
     if causal:
         qi = np.arange(sq)[:, None] + (sk - sq if sk > sq else 0)
@@ -736,9 +740,11 @@ def test_attention_prefill_split_precision(gpu, b, h, sq, sk, d, causal):
     assert rel(got, want) <= 1e-4
 
 
-def test_attention_prefill_invariants(gpu):
-    # Prefill kernel (head_dim 128): V constant -> O constant (0.75 is exact
-    # in bf16, so only the weights' split error remains); causal row 0 = V[0].
+def test_attention_prefill_invariants(fast_gpu):
+    # Split-bf16 prefill kernel (head_dim 128): V constant -> O constant (0.75
+    # is exact in bf16, so only the weights' split error remains); causal
+    # row 0 = V[0].
+    gpu = fast_gpu
     Q = RNG.standard_normal((1, 2, 200, 128)).astype(np.float32)
     K = RNG.standard_normal((1, 2, 200, 128)).astype(np.float32)
     V = np.full((1, 2, 200, 128), 0.75, np.float32)
@@ -748,8 +754,10 @@ def test_attention_prefill_invariants(gpu):
     assert np.allclose(O[:, :, 0], V[:, :, 0], atol=3e-5 * np.abs(V).max())
 
 
-def test_attention_invariants(gpu):
+@pytest.mark.parametrize("dev", ["gpu", "fast_gpu"])
+def test_attention_invariants(request, dev):
     # V constant -> O constant; causal row 0 attends only key 0 -> O[0] = V[0].
+    gpu = request.getfixturevalue(dev)
     Q = RNG.standard_normal((1, 2, 20, 32)).astype(np.float32)
     K = RNG.standard_normal((1, 2, 20, 32)).astype(np.float32)
     V = np.full((1, 2, 20, 32), 0.75, np.float32)

@@ -52,21 +52,28 @@ def _case(gpu, b, h, sq, sk, d, causal, use_mask):
     assert oracle.rel_error(got, want) <= 2e-3
 
 
-@pytest.mark.parametrize("first,second", [
-    # split decode (partial triples in the scratch): config-4 decode, then smaller
-    ((8, 32, 1, 4096, 128, 1, False), (2, 4, 1, 1000, 128, 1, True)),
-    # prefill (split K / V^T blocks in the scratch): 32 heads x 2048 keys at
-    # head_dim 128 fills the 64 MiB exactly, then a smaller masked call
-    ((1, 32, 2048, 2048, 128, 1, False), (1, 2, 300, 300, 64, 0, True)),
+@pytest.mark.parametrize("dev,first,second", [
+    # high-throughput device, split decode (partial triples in the scratch):
+    # config-4 decode, then smaller
+    ("fast_gpu", (8, 32, 1, 4096, 128, 1, False), (2, 4, 1, 1000, 128, 1, True)),
+    # split-bf16 prefill (split K / V^T blocks in the scratch): 32 heads x
+    # 2048 keys at head_dim 128 fills the 64 MiB exactly, then a smaller
+    # masked call
+    ("fast_gpu", (1, 32, 2048, 2048, 128, 1, False), (1, 2, 300, 300, 64, 0, True)),
     # the generic kernel (head_dim 80) with a split key range, then smaller
-    ((1, 2, 20, 3000, 80, 1, False), (1, 1, 5, 700, 80, 0, True)),
+    ("fast_gpu", (1, 2, 20, 3000, 80, 1, False), (1, 1, 5, 700, 80, 0, True)),
+    # default device, reference-order decode (the scores in the scratch):
+    # config-4 decode, then three query rows at head_dim 64 with a mask
+    ("gpu", (8, 32, 1, 4096, 128, 1, False), (2, 4, 3, 1000, 64, 1, True)),
 ])
-def test_noalloc_matches_attention_two_calls(gpu, first, second):
+def test_noalloc_matches_attention_two_calls(request, dev, first, second):
+    gpu = request.getfixturevalue(dev)
     _case(gpu, *first)
     _case(gpu, *second)
 
 
-def test_noalloc_refuses_oversize_and_host_pointers(gpu):
+def test_noalloc_refuses_oversize_and_host_pointers(fast_gpu):
+    gpu = fast_gpu
     b, h, s, d = 1, 32, 2100, 128   # 66 split blocks per head: 66 MiB of scratch
     Q = gpu.alloc(b * h * s * d * 4)
     K = gpu.alloc(b * h * s * d * 4)
