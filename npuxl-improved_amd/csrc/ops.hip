@@ -198,7 +198,20 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_reg_kernel(const float *__re
     }
 }
 
-// reference llm.cpp:116-180 (exp is the reference's polynomial)
+// The weight of element j as the reference's AVX2 build computes it
+// (softmax_avx2_rows, llm.cpp:137-180): exp256 (clamped to [-80, 80]) of
+// the separately rounded (x - max) * inv_t over the 8-wide steps, j below
+// cols & ~7; the scalar fast_expf (Horner steps contracted, 0 below -80) in
+// the tail.  Each weight is the reference's bit for bit; the sums below add
+// them in tree order, not in the reference's eight lanes.
+__device__ __forceinline__ float softmax_exp(float x, float mx, float inv_t, uint32_t j, uint32_t cols8)
+{
+#pragma clang fp contract(off)
+    const float t = (x - mx) * inv_t;
+    return j < cols8 ? dev::exp_avx2(t) : dev::fast_expf(t);
+}
+
+// reference llm.cpp:137-180
 __global__ __launch_bounds__(kThreads) void softmax_kernel(const float *__restrict__ X,
                                                            float *__restrict__ Y, uint32_t cols,
                                                            float inv_t)
@@ -210,18 +223,19 @@ __global__ __launch_bounds__(kThreads) void softmax_kernel(const float *__restri
     float mx = -__builtin_inff();
     for (uint32_t j = threadIdx.x; j < cols; j += kThreads) mx = fmaxf(mx, x[j]);
     mx = block_max(mx, red);
+    const uint32_t cols8 = cols & ~7u;
     float sum = 0.0f;
-    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) sum += dev::fast_expf((x[j] - mx) * inv_t);
+    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) sum += softmax_exp(x[j], mx, inv_t, j, cols8);
     sum = block_sum(sum, red);
     const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) y[j] = dev::fast_expf((x[j] - mx) * inv_t) * inv;
+    for (uint32_t j = threadIdx.x; j < cols; j += kThreads) y[j] = softmax_exp(x[j], mx, inv_t, j, cols8) * inv;
 }
 
 // Few long rows (e.g. the MTP head's [4, 32000] logits): each row is split
 // into chunks over many workgroups, in three passes that keep the
 // reference's terms exactly: chunk maxima -> the row max M; chunk sums of
-// fast_expf((x - M) * inv_t) -> the row sum L; y = fast_expf((x - M) * inv_t)
-// * (1 / L).  ws holds rows x chunks x 2 floats.
+// the weights (softmax_exp) -> the row sum L; y = weight * (1 / L).  ws
+// holds rows x chunks x 2 floats.
 __device__ __forceinline__ float row_max_of(const float *part, uint32_t chunks, float *red)
 {
     float m = -__builtin_inff();
@@ -259,8 +273,9 @@ __global__ __launch_bounds__(kThreads) void softmax_chunk_sum(const float *__res
     const uint32_t c0 = blockIdx.x * chunk, c1 = min(cols, c0 + chunk);
     const float *x = X + r * cols;
     const float mx = row_max_of(ws + r * gridDim.x * 2, gridDim.x, red);
+    const uint32_t cols8 = cols & ~7u;
     float sum = 0.0f;
-    for (uint32_t j = c0 + threadIdx.x; j < c1; j += kThreads) sum += dev::fast_expf((x[j] - mx) * inv_t);
+    for (uint32_t j = c0 + threadIdx.x; j < c1; j += kThreads) sum += softmax_exp(x[j], mx, inv_t, j, cols8);
     sum = block_sum(sum, red);
     if (threadIdx.x == 0) ws[(r * gridDim.x + blockIdx.x) * 2 + 1] = sum;
 }
@@ -279,7 +294,8 @@ __global__ __launch_bounds__(kThreads) void softmax_chunk_norm(const float *__re
     const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
     const float *x = X + r * cols;
     float *y = Y + r * cols;
-    for (uint32_t j = c0 + threadIdx.x; j < c1; j += kThreads) y[j] = dev::fast_expf((x[j] - mx) * inv_t) * inv;
+    const uint32_t cols8 = cols & ~7u;
+    for (uint32_t j = c0 + threadIdx.x; j < c1; j += kThreads) y[j] = softmax_exp(x[j], mx, inv_t, j, cols8) * inv;
 }
 
 // reference llm.cpp:188-217, 576-602: one thread per rotated pair.
@@ -474,9 +490,8 @@ __device__ __forceinline__ float block_sum_n(float v, float *red)
 
 // Softmax of few long rows (the MTP head's [gamma, vocab] logits) in one
 // launch: a 1024-thread workgroup per row keeps the row in registers, takes
-// the max, then each e = fast_expf((x - max) * inv_t) once (kept for the
-// output) and their sum; y = e * (1 / sum), the reference's terms
-// (llm.cpp:116-134) with a tree sum.
+// the max, then each weight once (softmax_exp, kept for the output) and
+// their sum; y = e * (1 / sum), the reference's terms with a tree sum.
 template <int VPT>
 __global__ __launch_bounds__(1024) void softmax_reg_kernel(const float *__restrict__ X, float *__restrict__ Y,
                                                           uint32_t cols, float inv_t)
@@ -496,13 +511,15 @@ __global__ __launch_bounds__(1024) void softmax_reg_kernel(const float *__restri
         mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
     }
     mx = block_max_n<1024>(mx, red);
+    const uint32_t cols8 = cols & ~7u;
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * 1024;
         if (j >= n4) continue;
-        v[i] = make_float4(dev::fast_expf((v[i].x - mx) * inv_t), dev::fast_expf((v[i].y - mx) * inv_t),
-                           dev::fast_expf((v[i].z - mx) * inv_t), dev::fast_expf((v[i].w - mx) * inv_t));
+        // four consecutive elements lie on one side of cols & ~7
+        v[i] = make_float4(softmax_exp(v[i].x, mx, inv_t, 4 * j, cols8), softmax_exp(v[i].y, mx, inv_t, 4 * j, cols8),
+                           softmax_exp(v[i].z, mx, inv_t, 4 * j, cols8), softmax_exp(v[i].w, mx, inv_t, 4 * j, cols8));
         sum += v[i].x;
         sum += v[i].y;
         sum += v[i].z;

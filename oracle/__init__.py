@@ -55,6 +55,7 @@ def lib() -> C.CDLL:
             "vo_rmsnorm_avx2": (None, [vp, vp, vp, u32, u32, f32]),
             "vo_exp_avx2": (f32, [f32]),
             "vo_swiglu_avx2": (None, [vp, vp, vp, u64, f32]),
+            "vo_softmax_avx2": (None, [vp, vp, u32, u32, f32]),
             "vo_gelu_avx2": (None, [vp, vp, u64]),
             "vo_mul_avx2": (None, [vp, vp, vp, u64, f32, f32]),
             "vo_add_avx2": (None, [vp, vp, vp, u64, f32, f32]),
@@ -193,6 +194,14 @@ def softmax(X, temperature=1.0):
     X = _c(X, np.float32)
     Y = np.empty_like(X)
     lib().vo_softmax(_p(X), _p(Y), X.shape[0], X.shape[1], temperature)
+    return Y
+
+
+def softmax_avx2(X, temperature=1.0):
+    """The reference's AVX2 build of SOFTMAX_F32 (llm.cpp:137-180), bit for bit."""
+    X = _c(X, np.float32)
+    Y = np.empty_like(X)
+    lib().vo_softmax_avx2(_p(X), _p(Y), X.shape[0], X.shape[1], temperature)
     return Y
 
 

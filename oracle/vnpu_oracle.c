@@ -599,8 +599,10 @@ void vo_rmsnorm_avx2(const float *X, const float *W, float *Y, uint32_t rows, ui
  * f = z - floor(z), P5 by FMA Horner, times 2^floor(z). */
 float vo_exp_avx2(float x)
 {
-    x = x < -80.0f ? -80.0f : x;
-    x = x > 80.0f ? 80.0f : x;
+    /* _mm256_max_ps(-80, _mm256_min_ps(x, 80)): each returns its second
+     * operand unless the comparison holds, so a NaN becomes 80. */
+    x = x < 80.0f ? x : 80.0f;
+    x = -80.0f > x ? -80.0f : x;
     float z = x * 1.4426950408889634f;
     float zi = floorf(z);
     float f = z - zi;
@@ -631,6 +633,46 @@ static float vo_fast_expf_fma(float x)
     p = fmaf(p, f, 0.6931471805599453f);
     p = fmaf(p, f, 1.0f);
     return ldexpf(p, (int)zi);
+}
+
+/* softmax_avx2_rows (llm.cpp:137-180), one row at a time as each of the
+ * reference's threads takes whole rows: lane maxima over the 8-wide steps by
+ * _mm256_max_ps(m, x) = m > x ? m : x (a NaN element becomes the lane's
+ * running max, and the next element replaces it), the eight lanes then the
+ * tail by std::max (a < b ? b : a); over the 8-wide steps e = exp256 of the
+ * separately rounded (x - max) * inv_t, summed per lane and combined as
+ * hsum256 does, ((s0+s4) + (s1+s5)) + ((s2+s6) + (s3+s7)); the tail with the
+ * scalar fast_expf as inlined into the AVX2 function, added in order;
+ * y = e * (1 / sum), 0 when sum is 0. */
+void vo_softmax_avx2(const float *X, float *Y, uint32_t rows, uint32_t cols, float temperature)
+{
+    const float inv_t = temperature > 0.0f ? 1.0f / temperature : 1.0f;
+    const uint32_t c8 = cols & ~7u;
+    for (uint32_t r = 0; r < rows; ++r) {
+        const float *x = X + (size_t)r * cols;
+        float *y = Y + (size_t)r * cols;
+        float vm[8], s[8];
+        for (int c = 0; c < 8; ++c) { vm[c] = -INFINITY; s[c] = 0.0f; }
+        for (uint32_t j = 0; j < c8; j += 8)
+            for (int c = 0; c < 8; ++c) vm[c] = vm[c] > x[j + c] ? vm[c] : x[j + c];
+        float maxv = -INFINITY;
+        for (int c = 0; c < 8; ++c) maxv = maxv < vm[c] ? vm[c] : maxv;
+        for (uint32_t j = c8; j < cols; ++j) maxv = maxv < x[j] ? x[j] : maxv;
+        for (uint32_t j = 0; j < c8; j += 8)
+            for (int c = 0; c < 8; ++c) {
+                const float e = vo_exp_avx2((x[j + c] - maxv) * inv_t);
+                y[j + c] = e;
+                s[c] = s[c] + e;
+            }
+        float sum = ((s[0] + s[4]) + (s[1] + s[5])) + ((s[2] + s[6]) + (s[3] + s[7]));
+        for (uint32_t j = c8; j < cols; ++j) {
+            const float e = vo_fast_expf_fma((x[j] - maxv) * inv_t);
+            y[j] = e;
+            sum = sum + e;
+        }
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        for (uint32_t j = 0; j < cols; ++j) y[j] = y[j] * inv;
+    }
 }
 
 /* The elementwise AVX2 ranges run 8-wide steps from the start of a range and

@@ -74,6 +74,7 @@ void vo_attention(const float *Q, const float *K, const float *V, const float *m
 void vo_rmsnorm_avx2(const float *X, const float *W, float *Y, uint32_t rows, uint32_t cols, float eps);
 float vo_exp_avx2(float x);
 void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha);
+void vo_softmax_avx2(const float *X, float *Y, uint32_t rows, uint32_t cols, float temperature);
 void vo_gelu_avx2(const float *X, float *Y, uint64_t count);
 void vo_add_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta);
 void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta);

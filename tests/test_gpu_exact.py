@@ -241,3 +241,27 @@ def test_attention_default_device_is_reference_order(flags):
             assert bits(got, block_oracle.attention_threaded(Q, K, V, 1, avx2=True))
     finally:
         s.close()
+
+
+@pytest.mark.parametrize("rows,cols,temp", [(4, 32000, 1.0), (3, 50000, 0.7), (600, 300, 1.0), (5, 33, 2.0),
+                                            (2, 4099, 0.0), (1, 7, 1.0)])
+def test_softmax_avx2_elementwise(gpu, rows, cols, temp):
+    """Every SOFTMAX_F32 kernel (one row per workgroup, the register kernel for
+    few long rows, the three-pass chunked kernels) against the reference's
+    AVX2 softmax, element by element with no element left out: each weight is
+    the reference's bit for bit (exp256 with its clamp over the 8-wide part,
+    the scalar exp in the tail, including weights exp(-80) * ... of logits
+    more than 80 below the max and -inf logits); only the row sum's order
+    differs."""
+    X = (RNG.standard_normal((rows, cols)) * 4).astype(np.float32)
+    X[0, 0] = 40.0
+    X[0, 1] = -60.0
+    X[0, cols - 1] = -60.0
+    if rows > 1:
+        X[1, 2] = -np.inf
+    got = g.unary_rows(gpu, abi.OP_SOFTMAX_F32, X, temperature=temp)
+    want = oracle.softmax_avx2(X, temp)
+    zero = want == 0
+    assert np.array_equal(got[zero], want[zero])
+    rel = np.abs(got[~zero].astype(np.float64) - want[~zero]) / want[~zero]
+    assert rel.max() <= 1e-5, f"max elementwise relative error {rel.max():.3g}"

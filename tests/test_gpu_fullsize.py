@@ -188,18 +188,19 @@ def test_config5_mtp_head_softmax_full(gpu):
         gpu.free(b)
     want_l = oracle.matmul_f32_blas(hid, wm)
     assert oracle.rel_error(gl, want_l) <= 1e-4
-    want_p = oracle.softmax(want_l, 1.0)
-    big = want_p > 1e-6
-    assert big.sum() > G * V // 2
-    relp = np.abs(gp[big].astype(np.float64) - want_p[big]) / want_p[big]
+    # the probabilities against the reference's AVX2 softmax of the float64
+    # logits rounded to f32, every element (relative to each one)
+    want_p = oracle.softmax_avx2(want_l, 1.0)
+    assert (want_p > 0).all()
+    relp = np.abs(gp.astype(np.float64) - want_p) / want_p
     assert relp.max() <= 1e-4, f"max relative probability error {relp.max():.3g}"
-    if (~big).any():
-        assert np.abs(gp[~big] - want_p[~big]).max() <= 1e-10
     assert np.allclose(gp.sum(axis=1), 1.0, atol=1e-5)
-    # the softmax step alone, on the GPU's own logits: the same bar
-    own = oracle.softmax(gl, 1.0)
-    big = own > 1e-6
-    assert (np.abs(gp[big].astype(np.float64) - own[big]) / own[big]).max() <= 1e-4
+    # the softmax step alone, on the GPU's own logits: each weight is the
+    # reference's bit for bit, only the order of the row sum differs
+    own = oracle.softmax_avx2(gl, 1.0)
+    relo = np.abs(gp.astype(np.float64) - own) / own
+    print(f"\n[config5 softmax] elementwise vs the AVX2 softmax of the GPU's logits: {relo.max():.3g}", flush=True)
+    assert relo.max() <= 1e-5
 
 
 @pytest.mark.parametrize("b,h,sq,sk,d,causal", [
@@ -296,3 +297,37 @@ def test_attention_wide_heads_and_many_heads(request, dev, b, h, sq, sk, d, caus
     want = oracle.attention(Q, K, V, mask, causal)
     assert np.isfinite(got).all()
     assert oracle.rel_error(got, want) <= 2e-3
+
+
+def test_config1_exact_calls(gpu):
+    """Config 1 as the bench times it (the same seeded tensors): MATMUL_F32
+    512^3 with B not transposed, bias ~ N(0, 0.1), alpha 1, beta 0 and SiLU
+    against the documented semantics silu(A.B + bias) with float64 sums (the
+    reference's VNPU_PACK=0 result; its default packed path applies the
+    epilogue after the first K block, kernels.cpp:313-323), every element
+    within 1e-4 of the output's scale, twice with identical bits; and the
+    int8 half (per-row QUANTIZE_I8 of A, per-column of B, PACK, MATMUL_I8)
+    bit for bit."""
+    import gpu_ops as g
+    M = K = N = 512
+    a = synth.normal("c1/A", (M, K))
+    b = synth.normal("c1/B", (K, N), 0.02)
+    bias = synth.normal("c1/bias", (N,), 0.1)
+    got = g.matmul_f32(gpu, a, b, M, K, N, bias=bias, alpha=1.0, beta=0.0, epilogue=abi.EPI_SILU)
+    again = g.matmul_f32(gpu, a, b, M, K, N, bias=bias, alpha=1.0, beta=0.0, epilogue=abi.EPI_SILU)
+    want = oracle.matmul_f32(a, b, None, bias, M, K, N, 0, 0, 1.0, 0.0, abi.EPI_SILU, acc64=True)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
+    assert oracle.rel_error(got, want) <= 1e-4
+    a8, sa = g.quantize(gpu, a, abi.QUANT_PER_ROW)
+    b8, sb = g.quantize(gpu, b, abi.QUANT_PER_COLUMN)
+    oa8, osa = oracle.quantize(a, abi.QUANT_PER_ROW)
+    ob8, osb = oracle.quantize(b, abi.QUANT_PER_COLUMN)
+    assert np.array_equal(a8, oa8) and np.array_equal(b8, ob8)
+    assert _bits_equal(sa, osa) and _bits_equal(sb, osb)
+    w = gpu.pack(b8, K, N, scales=sb)
+    try:
+        c = g.matmul_i8(gpu, a8, w, M, K, N, scale_a=sa)
+    finally:
+        gpu.release_packed(w)
+    assert _bits_equal(c, oracle.matmul_i8(oa8, ob8, osa, osb))

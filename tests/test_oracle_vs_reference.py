@@ -278,3 +278,28 @@ def test_attention_avx2_order_bit_exact(ref, b, h, sq, sk, d, causal, mask):
             M[0, 0, 3, :] = -np.inf
     got = g.attention(ref, Q, K, V, M, causal)
     assert _bits(got, oracle.attention_avx2(Q, K, V, M, causal))
+
+
+@pytest.mark.parametrize("rows,cols,temp", [(4, 32000, 1.0), (3, 4099, 0.7), (5, 33, 1.0), (2, 7, 2.0),
+                                            (1, 20000, 0.0), (6, 64, 1.5)])
+def test_softmax_avx2_order_bit_exact(ref, rows, cols, temp):
+    """SOFTMAX_F32 as the reference's AVX2 build computes it: per-lane maxima
+    and sums over 8-wide steps, hsum256, the scalar tail, exp256's clamp to
+    [-80, 80] (a logit 90 below the max keeps exp(-80), not 0, in the 8-wide
+    part; the tail's scalar exp gives 0), -inf logits and a NaN row (a NaN
+    element resets its lane's running max)."""
+    X = (RNG.standard_normal((rows, cols)) * 4).astype(np.float32)
+    X[0, 0] = 40.0
+    X[0, 1] = -60.0             # 100 below the max: clamped in the 8-wide part
+    X[0, cols - 1] = -60.0      # and in the tail (when cols % 8 != 0)
+    if rows > 1:
+        X[1, 3] = -np.inf
+        X[1, cols - 1] = -np.inf
+    if rows > 2 and cols > 16:
+        X[2, 5] = np.nan        # lane 5's max restarts after it
+        X[2, 13] = -3.0
+    got = g.unary_rows(ref, abi.OP_SOFTMAX_F32, X, temperature=temp)
+    want = oracle.softmax_avx2(X, temp)
+    assert _bits(got, want)
+    if rows > 1 and cols % 8 == 0:
+        assert want[1, 3] > 0.0   # exp(-80) of the clamp, as the reference
