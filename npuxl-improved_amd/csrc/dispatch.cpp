@@ -372,6 +372,8 @@ void exec_matmul_f32(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_f32
     // Device tiles 128 x depth x 128 (vnpu_device_set_tiles, an f32 autotune)
     // fix the K depth per workgroup; other tiles leave the choice automatic.
     p.k_split_depth = dev->f32_depth.load();
+    p.err = s->err_dev;
+    p.max_spin = dev->ws_max_spin;
 
     Stager sg(s->hip, s);
     p.A = sg.in(in.A, in.trans_a ? span(in.K, in.M, p.lda, 4) : span(in.M, in.K, p.lda, 4));

@@ -600,8 +600,11 @@ __global__ __launch_bounds__(128 * WM) void gemm_f32_x3(F32Gemm p, uint32_t k_pe
 // producer p sets prod[slot][p] = s + 1 once stage s is in the slot,
 // consumer c sets cons[slot][c] = s + 1 once it has read stage s, and a
 // producer refills a slot only when every consumer has released the stage
-// three before.  Every wait is bounded (after kWsMaxSpin polls it goes on,
-// so a protocol error shows as wrong results, never as a hung wave).
+// three before.  Every wait is bounded: after p.max_spin polls (kMaxSpin when
+// 0) the wave goes on, so a protocol error never hangs a wave; it stores 1
+// into p.err (the stream's error word in host-coherent memory), which the
+// stream's sync turns into a sticky device error, so the wrong C it leaves
+// is never reported as success.
 // Operand loads are raw buffer loads over the whole matrix (out of range
 // reads return zero), rows past M / N are clamped and k past K is zeroed
 // with selects: no branch around a load, so the three stages of loads stay
@@ -631,19 +634,22 @@ __device__ __forceinline__ uint32_t lds_addr(const uint32_t *p)
 }
 
 // Waits until the four flags f[0..3] (one per wave of the other side) are at
-// least `target`.
-__device__ __forceinline__ void ws_wait(const uint32_t *f, uint32_t target)
+// least `target`, at most p.max_spin polls (kMaxSpin when 0); a wait that
+// gives up marks the launch failed in p.err.
+__device__ __forceinline__ void ws_wait(const F32Gemm &p, const uint32_t *f, uint32_t target)
 {
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));
     const uint32_t a = lds_addr(f);
-    for (uint32_t spin = 0; spin < ws::kMaxSpin; ++spin) {
+    const uint32_t limit = p.max_spin ? p.max_spin : ws::kMaxSpin;
+    for (uint32_t spin = 0; spin < limit; ++spin) {
         v4u v;
         asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
         const uint32_t lo = min(min(v.x, v.y), min(v.z, v.w));
         // No s_sleep: each poll already waits for its LDS read, and a sleep
         // measured 3-5% slower (the waiter reacts later).
-        if (__builtin_amdgcn_readfirstlane(lo) >= target) break;
+        if (__builtin_amdgcn_readfirstlane(lo) >= target) return;
     }
+    if (p.err) __hip_atomic_store(p.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Publishes `v` after this wave's earlier LDS reads and writes completed.
@@ -784,7 +790,7 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p)
         auto put = [&](const WsSlice &x, uint32_t s) {
             const uint32_t slot = s % kSlots;
             const uint32_t k0 = s * WBK;
-            if (s >= kSlots) ws_wait(cons + 4 * slot, s - kSlots + 1);
+            if (s >= kSlots) ws_wait(p, cons + 4 * slot, s - kSlots + 1);
             if (edge || k0 + WBK > p.K) {
                 WsSlice y;
 #pragma unroll
@@ -871,14 +877,14 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p)
             for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.ah[i], f.bh[j], acc[i][j], 0, 0, 0);
     };
     Frag f0, f1;
-    ws_wait(prod, 1);
+    ws_wait(p, prod, 1);
     read(f0, 0, 0);
     for (uint32_t s = 0; s < KT; ++s) {
         read(f1, s, 1);
         mma(f0);
         ws_release(cons + 4 * (s % kSlots) + cw, s + 1);
         if (s + 1 < KT) {
-            ws_wait(prod + 4 * ((s + 1) % kSlots), s + 2);
+            ws_wait(p, prod + 4 * ((s + 1) % kSlots), s + 2);
             read(f0, s + 1, 0);
         }
         mma(f1);

@@ -88,6 +88,11 @@ struct F32Gemm {
     // K depth per workgroup when a 128 x 128 x depth tile was requested
     // (vnpu_device_set_tiles / autotune); 0 = choose the split automatically.
     uint32_t k_split_depth = 0;
+    // The warp-specialised kernel's bounded waits: at most max_spin polls
+    // (0 = the kernel's default); a wait that gives up stores 1 into *err
+    // (host-coherent, read at the stream's sync).  err may be null.
+    uint32_t *err = nullptr;
+    uint32_t max_spin = 0;
 };
 void gemm_f32_tile_dims(uint32_t &bm, uint32_t &bn);
 // The Wildcat cull of MATMUL_F32 built on the GPU from a device-resident

@@ -446,6 +446,10 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_device_create(const vnpu_config_t *config,
         // asks for throughput (VNPU_CONFIG_HIGH_THROUGHPUT, or
         // VNPU_REFERENCE_ORDER=0 for every device); VNPU_CONFIG_REFERENCE_ORDER
         // or VNPU_REFERENCE_ORDER=1 keep the reference's order regardless.
+        // VNPU_WS_MAX_SPIN bounds the f32 GEMM's producer/consumer waits
+        // (polls per wait): a test hook that forces the bounded-wait failure.
+        if (const char *ms = std::getenv("VNPU_WS_MAX_SPIN"))
+            d->ws_max_spin = static_cast<uint32_t>(std::strtoul(ms, nullptr, 10));
         const char *ro = std::getenv("VNPU_REFERENCE_ORDER");
         const bool fast = (cfg.flags & VNPU_CONFIG_HIGH_THROUGHPUT) != 0 || (ro && ro[0] == '0');
         d->reference_order = (cfg.flags & VNPU_CONFIG_REFERENCE_ORDER) != 0 || (ro && ro[0] == '1') || !fast;
@@ -507,6 +511,7 @@ static void destroy_stream_obj(vnpu_stream_t *s)
     if (s->workspace) (void)hipFree(s->workspace);
     if (s->staging) (void)hipFree(s->staging);
     if (s->cull_scratch) (void)hipFree(s->cull_scratch);
+    if (s->err_host) (void)hipHostFree(s->err_host);
     delete s;
 }
 
@@ -729,8 +734,16 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_create(vnpu_device_t *device, int p
         s->device = device;
         s->priority = priority;  // recorded only: every stream runs at default priority
         hipError_t e = hipStreamCreate(&s->hip);
+        if (e == hipSuccess)
+            e = hipHostMalloc(reinterpret_cast<void **>(&s->err_host), sizeof(uint32_t),
+                              hipHostMallocMapped | hipHostMallocCoherent);
+        if (e == hipSuccess) {
+            *s->err_host = 0;
+            e = hipHostGetDevicePointer(reinterpret_cast<void **>(&s->err_dev), s->err_host, 0);
+        }
         if (e != hipSuccess) {
-            delete s;
+            (void)hipGetLastError();
+            destroy_stream_obj(s);
             return VNPU_ERR_DEVICE_ERROR;
         }
         {
@@ -815,6 +828,15 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_sync(vnpu_stream_t *stream)
     if (e != hipSuccess) {
         (void)hipGetLastError();
         const uint32_t code = static_cast<uint32_t>(-VNPU_ERR_DEVICE_ERROR);
+        stream->last_error.store(code);
+        d->error.store(code);
+        d->regs[VNPU_REG_ERROR / 4].store(code);
+    } else if (stream->err_host && __atomic_exchange_n(stream->err_host, 0u, __ATOMIC_ACQ_REL) != 0) {
+        // A kernel's bounded wait gave up (its output is not valid): a
+        // failed command, sticky on this stream as in the reference
+        // (runtime.cpp:1248-1254, 1281-1289).
+        debug_log("vnpu_stream_sync: a kernel's bounded wait gave up; its output is invalid");
+        const uint32_t code = static_cast<uint32_t>(-VNPU_ERR_INTERNAL);
         stream->last_error.store(code);
         d->error.store(code);
         d->regs[VNPU_REG_ERROR / 4].store(code);

@@ -127,6 +127,11 @@ struct vnpu_stream {
     std::atomic<uint64_t> pending{0};
     void *workspace = nullptr;
     size_t workspace_bytes = 0;
+    // Error word of the kernels on this stream whose bounded waits may give
+    // up (pinned, host-coherent: err_host on the host, err_dev in kernels);
+    // nonzero at a sync = a launch since the last sync computed garbage.
+    uint32_t *err_host = nullptr;
+    uint32_t *err_dev = nullptr;
     // Device copies of host-pointer operands: one grow-only arena reused by
     // every staged command (each staged command synchronizes before it
     // returns, so the next one may overwrite it).  Guarded by mutex.
@@ -185,6 +190,7 @@ struct vnpu_device {
     std::atomic<uint32_t> i8_variant{0};   // int8 GEMM kernel (gemm_i8_variant_for_tiles)
     std::atomic<uint32_t> f32_depth{0};    // f32 K depth per workgroup (split-K)
     bool reference_order = true;           // attention bit-exact (off: VNPU_CONFIG_HIGH_THROUGHPUT)
+    uint32_t ws_max_spin = 0;              // bound of the f32 GEMM's flag waits (0: kernel default)
     // Culled tiles counted on the GPU (MATMUL_F32 with a device-resident tile
     // mask); folded into the status when read.  Allocated on first use.
     unsigned long long *culled_dev = nullptr;

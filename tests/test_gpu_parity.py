@@ -844,3 +844,38 @@ def test_backend_table_and_info(gpu):
     assert info.num_compute_units >= 1 and info.total_memory_bytes > 0
     assert b"gfx950" in info.cpu_arch
     assert gpu.lib.vnpu_mmio_read32(gpu.dev, 0) == 0x56504E55
+
+
+def test_f32_bounded_wait_timeout_is_reported(monkeypatch):
+    """The warp-specialised MATMUL_F32 kernel's producer/consumer waits are
+    bounded.  With the bound forced down to one poll from the host
+    (VNPU_WS_MAX_SPIN=1 at device creation) the first waits give up while
+    the operands are still in flight: every wave still finishes (the waits
+    end, all accesses stay in the ring and the matrices), the result is
+    wrong, and the stream's sync reports it as a device error, sticky on
+    that stream, with the device error register set.  A device created
+    without the bound computes the same call correctly."""
+    from vnpu_mi355x import Session
+    M, K, N = 2048, 256, 4096     # 8 x 32 = 256 tiles of 256 x 128: the warp-specialised kernel
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    B = RNG.standard_normal((K, N)).astype(np.float32)
+    monkeypatch.setenv("VNPU_WS_MAX_SPIN", "1")
+    s = Session()
+    monkeypatch.delenv("VNPU_WS_MAX_SPIN")
+    try:
+        ba, bb, bc = s.upload(A), s.upload(B), s.alloc(4 * M * N)
+        assert s.sync() == abi.OK
+        cmd = s.command(abi.OP_MATMUL_F32, A=ba, B=bb, C=bc, M=M, K=K, N=N, alpha=1.0)
+        assert s.submit([cmd]) == abi.OK
+        assert s.sync() == abi.ERR_DEVICE_ERROR
+        assert s.sync() == abi.ERR_DEVICE_ERROR          # sticky
+        assert s.status().error == (-abi.ERR_INTERNAL) & 0xffffffff
+    finally:
+        s.close()
+    ok = Session()
+    try:
+        got = g.matmul_f32(ok, A, B, M, K, N)
+        assert ok.sync() == abi.OK
+    finally:
+        ok.close()
+    assert rel(got, oracle.matmul_f32_blas(A, B)) <= 1e-4
