@@ -264,3 +264,51 @@ def test_forced_f32_split_depths(gpu, depth):
         gpu.lib.vnpu_device_set_tiles(gpu.dev, info0.tile_m, info0.tile_k, info0.tile_n)
     want = oracle.matmul_f32(A, B, Cin, bias, M, K, N, 0, 0, 1.0, 0.5, 3, acc64=True)
     assert oracle.rel_error(got, want) <= 1e-4
+
+
+def test_autotune_leaves_the_other_dtype():
+    """vnpu_autotune_gemm writes back only the tuned dtype's kernel choice.
+    After an int8 tune (whatever tile triple it leaves on the device, e.g.
+    128 x 64 x 128 for the generic int8 kernel) MATMUL_F32 still runs its
+    automatic split-bf16 kernel: the same bits as on an untuned device (the
+    fp32 split-K kernel a 128 x 64 x 128 f32 choice would force gives other
+    bits) in about the same time; after an f32 tune the int8 GEMM keeps its
+    time.  (vnpu_device_set_tiles, as in the reference, sets both.)"""
+    import time
+    from vnpu_mi355x import Session
+    import gpu_ops as g
+    s = Session()
+    try:
+        Mf, Kf, Nf = 2048, 512, 4096
+        A = RNG.standard_normal((Mf, Kf)).astype(np.float32)
+        B = RNG.standard_normal((Kf, Nf)).astype(np.float32)
+        ba, bb, bc = s.upload(A), s.upload(B), s.alloc(4 * Mf * Nf)
+        Mi, Ki, Ni = 2048, 4096, 4096
+        A8 = RNG.integers(-128, 128, (Mi, Ki)).astype(np.int8)
+        w = s.pack(RNG.integers(-128, 128, (Ki, Ni)).astype(np.int8), Ki, Ni)
+        b8, bi = s.upload(A8), s.alloc(4 * Mi * Ni)
+        f32_cmd = s.command(abi.OP_MATMUL_F32, A=ba, B=bb, C=bc, M=Mf, K=Kf, N=Nf, alpha=1.0)
+        i8_cmd = s.command(abi.OP_MATMUL_I8, A=b8, B=w, C=bi, M=Mi, K=Ki, N=Ni)
+
+        def timed(cmd, n=20):
+            s.check("submit", s.submit([cmd] * 3))
+            s.check("sync", s.sync())
+            t0 = time.perf_counter()
+            s.check("submit", s.submit([cmd] * n))
+            s.check("sync", s.sync())
+            return (time.perf_counter() - t0) / n
+
+        t_f32, t_i8 = timed(f32_cmd), timed(i8_cmd)
+        r0 = s.download(bc, np.float32, (Mf, Nf))
+        res = abi.TuneResult()
+        assert s.lib.vnpu_autotune_gemm(s.dev, 512, 1024, 768, 3, 3, C.byref(res)) == abi.OK   # int8
+        s.check("submit", s.submit([f32_cmd]))
+        s.check("sync", s.sync())
+        r1 = s.download(bc, np.float32, (Mf, Nf))
+        assert np.array_equal(r0.view(np.uint32), r1.view(np.uint32)), (res.tile_m, res.tile_k, res.tile_n)
+        assert timed(f32_cmd) < 1.5 * t_f32
+        assert s.lib.vnpu_autotune_gemm(s.dev, 256, 2048, 256, 3, 0, C.byref(res)) == abi.OK    # f32
+        assert timed(i8_cmd) < 1.5 * t_i8
+        s.release_packed(w)
+    finally:
+        s.close()
