@@ -352,6 +352,10 @@ def bench_config5(s: Session, steps: int):
         return pk
 
     dense_w = packed_of(w)   # the same weights unculled: the dense baseline of the same kernel family
+    # Beside config 5's half-zero tiles, a quarter-nonzero mask of the same
+    # weights: below 40% nonzero tiles the strip kernel skips the zero ones.
+    keep25 = synth.bernoulli_mask("c5/tiles25", (K // 64, N // 64), 0.25)
+    sparse_w = packed_of(w * np.kron(keep25, np.ones((64, 64), np.uint8)).astype(np.float32))
     w *= np.kron(keep, np.ones((64, 64), np.uint8)).astype(np.float32)
     packed = packed_of(w)
     del w
@@ -364,20 +368,26 @@ def bench_config5(s: Session, steps: int):
     mkd = lambda i: s.command(abi.OP_MATMUL_I8, id=i, A=a8, B=dense_w, scale_a=sa, C=c, M=M, K=K, N=N)
     # Culled and dense runs alternate (the chip's clock drifts with its
     # temperature over a run); each figure is the median of its rounds.
-    cul, den = [], []
+    mks = lambda i: s.command(abi.OP_MATMUL_I8, id=i, A=a8, B=sparse_w, scale_a=sa, C=c, M=M, K=K, N=N)
+    cul, den, spa = [], [], []
     for _ in range(3):
         cul.append(timed(s, mk, max(1, steps // 3), 3)[1])
         den.append(timed(s, mkd, max(1, steps // 3), 3)[1])
-    gpu_ns, dense_ns = float(np.median(cul)), float(np.median(den))
+        spa.append(timed(s, mks, max(1, steps // 3), 3)[1])
+    gpu_ns, dense_ns, sparse_ns = float(np.median(cul)), float(np.median(den)), float(np.median(spa))
     s.release_packed(packed)
     s.release_packed(dense_w)
+    s.release_packed(sparse_w)
     for b in (a8, sa, c):
         s.free(b)
     dense = 2.0 * M * K * N
     out = {"cull_i8_4096": {"kernel_us": gpu_ns / 1e3, "zero_tiles": int(keep.size - keep.sum()),
                             "dense_equiv_tops": dense / gpu_ns / 1e3,
                             "useful_tops": dense * keep.mean() / gpu_ns / 1e3,
-                            "dense_weights_kernel_us": dense_ns / 1e3, "vs_dense": gpu_ns / dense_ns}}
+                            "dense_weights_kernel_us": dense_ns / 1e3, "vs_dense": gpu_ns / dense_ns},
+           "cull_i8_4096_quarter_nonzero": {"us": sparse_ns / 1e3, "nonzero_tiles": int(keep25.sum()),
+                                            "useful_tops": dense * keep25.mean() / sparse_ns / 1e3,
+                                            "vs_dense": sparse_ns / dense_ns}}
     G, H, V = 4, 4096, 32000
     hid = s.upload(synth.normal("c5/hidden", (G, H)))
     wm = synth.normal("c5/mtp_W", (H, V), 0.02)

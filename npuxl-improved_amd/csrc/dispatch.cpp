@@ -494,9 +494,11 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     p.ldc = in.ldc ? in.ldc : in.N;
     require(p.lda >= in.K && p.ldc >= in.N, "invalid int8 leading dimensions");
     p.frag = w->frag;
-    // The zero-block map only costs lookups when there are zero blocks.
     p.Kp = w->Kp;
     p.Np = w->Np;
+    p.nz_list = w->nz_list;
+    p.nz_count = w->nz_count;
+    p.nz_tiles = w->nz_tiles;
     p.scale_b = w->scales_dev;
     p.epilogue = in.epilogue;
     p.variant = dev->i8_variant.load();
@@ -512,7 +514,7 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     if (in.M <= 8)
         k::gemv_i8(s->hip, p);
     else
-        k::gemm_i8(s->hip, p);
+        k::gemm_i8(s->hip, p, static_cast<int8_t *>(s->ensure_workspace(k::gemm_i8_ws_bytes(p))));
     VNPU_HIP(hipGetLastError());
     sg.finish();
 
@@ -1096,6 +1098,17 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
     const int8_t *Bd = sg.in(B, b_bytes);
     k::pack_fragments(st, Bd, K, N, ld, trans_b, w->frag, w->Kp, w->Np, sums_dev);
     VNPU_HIP(hipGetLastError());
+    // Nonzero 64 x 64 tiles: per 64-column group, the k blocks to walk.
+    const uint32_t groups = (w->Np / 16 + 3) / 4, kblocks = w->Kp / 64;
+    VNPU_HIP(hipMalloc(&w->nz_list, static_cast<size_t>(groups) * kblocks * 4));
+    VNPU_HIP(hipMalloc(&w->nz_count, static_cast<size_t>(groups) * 4));
+    uint8_t *flag_dev = nullptr;
+    VNPU_HIP(hipMalloc(&flag_dev, static_cast<size_t>(groups) * kblocks));
+    std::unique_ptr<uint8_t, hipError_t (*)(void *)> flag_guard(flag_dev, hipFree);
+    k::tile_lists(st, w->frag, w->Kp, w->Np, flag_dev, w->nz_list, w->nz_count);
+    VNPU_HIP(hipGetLastError());
+    std::vector<uint32_t> counts(groups);
+    VNPU_HIP(hipMemcpyAsync(counts.data(), w->nz_count, static_cast<size_t>(groups) * 4, hipMemcpyDeviceToHost, st));
 
     // Scales: NULL keeps 1.0 (the reference does not derive them, F5 of its
     // scheduler.cpp:806-808).
@@ -1115,6 +1128,7 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
                        hipMemcpyDeviceToHost));
     sg.finish();
     VNPU_HIP(hipStreamSynchronize(st));
+    for (uint32_t c : counts) w->nz_tiles += c;
     dev->dma_bytes.fetch_add(static_cast<uint64_t>(K) * N * 2);
     return w.release();
 }
@@ -1127,6 +1141,8 @@ void destroy_packed(vnpu_packed_weights_t *w)
         (void)hipFree(w->frag);
     }
     if (w->scales_dev) (void)hipFree(w->scales_dev);
+    if (w->nz_list) (void)hipFree(w->nz_list);
+    if (w->nz_count) (void)hipFree(w->nz_count);
     delete w;
 }
 

@@ -25,6 +25,7 @@
 #include "kernels.hpp"
 
 #include <atomic>
+#include <type_traits>
 #include "device_math.hpp"
 #include "lds_dma.hpp"
 
@@ -413,6 +414,237 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_pipe(I8Gemm p, uint32_t tile
     case 3:
     case 4: store_tile<3>(p, tile, sa_lds, m0, n0, tid); break;
     default: store_tile<0>(p, tile, sa_lds, m0, n0, tid); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Strip kernel for weights with all-zero 64 x 64 tiles (the Wildcat cull
+// geometry of config 5; the reference's int8 culled tile, kernels.cpp:927-931,
+// is never reached).  A workgroup owns TM = 512 rows x one group of four
+// 16-column strips (64 columns) and walks only that group's nonzero 64-deep
+// k blocks, from the list built at pack time (tile_lists): stage s holds
+// k block list[s] of both operands, A gathered from its 64 columns, so a
+// zero tile costs neither copies nor MFMAs, and every wave of the workgroup
+// takes the same stages (no per-MFMA test).  Otherwise the pipelined
+// kernel's scheme: 8 waves of 64 x 64 (2 x 2 v_mfma_i32_32x32x32_i8 blocks;
+// two waves per SIMD, so one wave's stage overhead overlaps the other's
+// MFMAs), stages copied into an LDS ring by global_load_lds_dwordx4 (A from
+// its fragment-block copy, B as packed), three stages in flight, fragments
+// double-buffered in registers, the accumulators leaving through LDS for the
+// dequant epilogue.
+// The list sits in registers: lane l holds entry 64q + l of register q, and a
+// stage's k block is a readlane, so no load waits on it.
+// ---------------------------------------------------------------------------
+// A in fragment blocks for the strip kernel: block (rb, kb) is 1 KiB, lane
+// l's 16 bytes = A[16 rb + l % 16][64 kb + 16 (l / 16) .. +16] (rows past M
+// zero), so a stage's copy of a 16-row block is one contiguous 1 KiB read
+// (whole cache lines) instead of 16 half lines of row-major A.
+__global__ __launch_bounds__(256) void a_blocks_kernel(const int8_t *__restrict__ A, uint32_t lda, uint32_t M,
+                                                       uint32_t KTp, uint64_t chunks, int8_t *__restrict__ out)
+{
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= chunks) return;
+    const uint32_t l = idx & 63;
+    const uint64_t blk = idx >> 6;
+    const uint32_t kb = static_cast<uint32_t>(blk % KTp), rb = static_cast<uint32_t>(blk / KTp);
+    const uint32_t row = rb * 16 + (l & 15);
+    v4i v = {0, 0, 0, 0};
+    if (row < M) v = *reinterpret_cast<const v4i *>(A + static_cast<uint64_t>(row) * lda + kb * 64 + (l >> 4) * 16);
+    reinterpret_cast<v4i *>(out)[idx] = v;
+}
+
+namespace strip {
+constexpr int TM = 512, TN = 64;
+constexpr int kStages = 4;
+constexpr int kABlocks = TM / 16;                    // 32
+constexpr int kBBlocks = TN / 16;                    // 4
+constexpr int kBlocks = kABlocks + kBBlocks;         // 36 x 1 KiB per stage
+constexpr int kThreads = 512;                        // 8 waves
+constexpr int kLoadsLo = 5, kLoadsHi = 4;            // copies per stage: waves 0-3, waves 4-7
+constexpr int kStageBytes = kBlocks * 1024;
+constexpr int kRing = kStages * kStageBytes;         // 144 KiB
+constexpr int kOutPitch = TN + 4;
+constexpr int kOut = TM * kOutPitch * 4;             // 136 KiB
+constexpr int kScaleOff = kOut;
+constexpr uint32_t kMaxKBlocks = 256;                // list registers: 4 x 64
+constexpr size_t kLds = kRing;
+static_assert(kOut + TM * 4 <= kRing, "staged tile + row scales fit in the ring");
+static_assert(4 * kLoadsLo + 4 * kLoadsHi == kBlocks, "every block of a stage has one copy");
+}  // namespace strip
+
+__global__ __launch_bounds__(strip::kThreads) void gemm_i8_strip(I8Gemm p, uint32_t tiles_m, uint32_t groups,
+                                                                 const int8_t *__restrict__ ablk)
+{
+    using strip::kABlocks;
+    using strip::kLoadsHi;
+    using strip::kLoadsLo;
+    using strip::kStageBytes;
+    using strip::kStages;
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int fr = lane & 15, fg = lane >> 4;
+
+    // XCD-aware order: each XCD takes a contiguous run of tiles, column
+    // groups fastest, so its L2 keeps the run's row tiles of A (512 rows x K)
+    // while the groups' weights stream past.
+    const uint32_t total = tiles_m * groups;
+    uint32_t g = blockIdx.x;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const uint32_t tmi = g / groups, grp = g % groups;
+    const uint32_t m0 = tmi * strip::TM, n0 = grp * strip::TN;
+    const uint32_t NT = p.Np >> 4;
+    const uint32_t KTp = p.Kp >> 6;
+    const uint32_t NS = p.nz_count[grp];   // stages: the group's nonzero k blocks
+    const uint32_t *lst = p.nz_list + static_cast<uint64_t>(grp) * KTp;
+    uint32_t lv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t i = 64u * q + lane;
+        lv[q] = i < NS ? lst[i] : 0u;
+    }
+    auto kblock = [&](uint32_t s) -> uint32_t {
+        const uint32_t q = s >> 6;
+        const uint32_t v = q == 0 ? lv[0] : q == 1 ? lv[1] : q == 2 ? lv[2] : lv[3];
+        return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(s & 63)));
+    };
+
+    // This wave's blocks of every stage (5 for waves 0-3, 4 for waves 4-7):
+    // a block's run of k blocks (A blocks and packed B strips are both
+    // k-block-major, 1 KiB apart).  The fifth slot of waves 4-7 is unused.
+    const bool lo = wave < 4;
+    const int b0 = lo ? wave * kLoadsLo : 4 * kLoadsLo + (wave - 4) * kLoadsHi;
+    const int8_t *src[kLoadsLo];
+#pragma unroll
+    for (int j = 0; j < kLoadsLo; ++j) {
+        const int b = min(b0 + j, strip::kBlocks - 1);
+        if (b < kABlocks) {
+            const uint32_t rb = min((m0 >> 4) + b, (p.M + 15) / 16 - 1);
+            src[j] = ablk + ((static_cast<uint64_t>(rb) * KTp) << 10) + lane * 16;
+        } else {
+            const uint32_t nb = min((n0 >> 4) + (b - kABlocks), NT - 1);
+            src[j] = p.frag + ((static_cast<uint64_t>(nb) * KTp) << 10) + lane * 16;
+        }
+    }
+    auto issue = [&](uint32_t s) {
+        int8_t *st = smem + (s % kStages) * kStageBytes;
+        const uint64_t kb = kblock(s);
+#pragma unroll
+        for (int j = 0; j < kLoadsHi; ++j) dma16(src[j] + (kb << 10), st + (b0 + j) * 1024);
+        if (lo) dma16(src[kLoadsHi] + (kb << 10), st + (b0 + kLoadsHi) * 1024);
+    };
+    // Waits for all but this wave's last n stages of copies.
+    auto wait_stages = [&](auto n) {
+        constexpr int N = decltype(n)::value;
+        if (lo) wait_vmcnt<N * kLoadsLo>();
+        else wait_vmcnt<N * kLoadsHi>();
+    };
+    // A 32-row (32-column) operand is two 16-row fragment blocks of the
+    // stage: lane l takes block (l/16)%2, row l%16, k group 2h + l/32.
+    const int sub = (lane >> 4) & 1;
+    struct SFrags {
+        v4i a[2][2], b[2][2];
+    };
+    auto read_frags = [&](uint32_t s, SFrags &f) {
+        const int8_t *st = smem + (s % kStages) * kStageBytes;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int off = ((2 * h + (lane >> 5)) * 16 + (lane & 15)) * 16;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+                f.b[h][nb] = *reinterpret_cast<const v4i *>(st + (kABlocks + 2 * nb + sub) * 1024 + off);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+                f.a[h][mb] = *reinterpret_cast<const v4i *>(st + (wave * 4 + 2 * mb + sub) * 1024 + off);
+        }
+    };
+
+    v16i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16i){0};
+    auto mma = [&](const SFrags &f) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[h][i], f.b[h][j], acc[i][j], 0, 0, 0);
+    };
+
+    if (NS) {
+        // The pipelined kernel's schedule over the NS listed stages.
+        const uint32_t pre = min(NS, static_cast<uint32_t>(kStages));
+        for (uint32_t s = 0; s < pre; ++s) issue(s);
+        if (NS > static_cast<uint32_t>(kStages)) wait_stages(std::integral_constant<int, kStages - 1>{});
+        else wait_vmcnt<0>();
+        block_barrier();
+        SFrags f0, f1;
+        read_frags(0, f0);
+        uint32_t s = 0;
+        for (; s + kStages + 1 < NS; s += 2) {
+            wait_stages(std::integral_constant<int, kStages - 2>{});
+            block_barrier();
+            issue(s + kStages);
+            read_frags(s + 1, f1);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(f0);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_stages(std::integral_constant<int, kStages - 2>{});
+            block_barrier();
+            issue(s + 1 + kStages);
+            read_frags(s + 2, f0);
+            __builtin_amdgcn_sched_barrier(0);
+            mma(f1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // Drain: at most stage s + kStages is still to be copied, into the
+        // slot of stage s once every wave holds stage s's fragments.
+        if (s + kStages < NS) {
+            block_barrier();
+            issue(s + kStages);
+        }
+        wait_vmcnt<0>();
+        block_barrier();
+        mma(f0);
+        for (++s; s < NS; ++s) {
+            read_frags(s, f1);
+            mma(f1);
+        }
+    }
+
+    // Stage the accumulators row-major (32x32 block: lane l holds column
+    // l%32, rows 8j + 4(l/32) + q in register 4j + q) and the row scales.
+    __syncthreads();
+    int32_t *tile = reinterpret_cast<int32_t *>(smem);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                tile[(wave * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * strip::kOutPitch + j * 32 +
+                     (lane & 31)] = acc[i][j][r];
+    float *sa_lds = reinterpret_cast<float *>(smem + strip::kScaleOff);
+    for (int r = tid; r < strip::TM; r += strip::kThreads) {
+        const uint32_t m = m0 + r;
+        sa_lds[r] = (p.scale_a && m < p.M) ? p.scale_a[m] : 1.0f;
+    }
+    __syncthreads();
+    using strip::kOutPitch;
+    using strip::TM;
+    using strip::TN;
+    constexpr int kT = strip::kThreads;
+    switch (p.epilogue) {
+    case 1: store_tile<1, kT, TN, kOutPitch, TM>(p, tile, sa_lds, m0, n0, tid); break;
+    case 2: store_tile<2, kT, TN, kOutPitch, TM>(p, tile, sa_lds, m0, n0, tid); break;
+    case 3:
+    case 4: store_tile<3, kT, TN, kOutPitch, TM>(p, tile, sa_lds, m0, n0, tid); break;
+    default: store_tile<0, kT, TN, kOutPitch, TM>(p, tile, sa_lds, m0, n0, tid); break;
     }
 }
 
@@ -1039,7 +1271,34 @@ uint32_t cu_count()
     return n;
 }
 
-void gemm_i8(hipStream_t s, const I8Gemm &p)
+// Largest share of nonzero 64 x 64 weight tiles at which the strip kernel
+// (with its copy of A in fragment blocks) beats the dense ones.  Measured at
+// 4096^3 against the 256 x 256 dense kernel on the same weights: 1.06x the
+// dense time at 50% nonzero tiles, 0.88x at 37.5%, 0.77x at 25%, 0.63x at
+// 12.5%.  The int8 GEMM is bound by operand traffic into LDS, not by the
+// matrix cores: skipping a zero tile halves its MFMAs, but A is read once
+// per 64-column group instead of once per 256-column tile.
+constexpr double kStripDensity = 0.4;
+
+// The strip kernel takes the call: packed weights with nonzero-tile lists,
+// the pipelined kernels' alignment, at most 256 k blocks, and at most
+// kStripDensity of the tiles nonzero (unless another kernel was requested).
+static bool use_strip(const I8Gemm &p)
+{
+    const uint32_t KTp = p.Kp / 64, groups = (p.Np / 16 + 3) / 4;
+    const bool aligned = (p.K % 64 == 0) && (p.lda % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64;
+    if (!aligned || !p.nz_list || !p.nz_count || KTp > strip::kMaxKBlocks) return false;
+    if (p.variant != kI8Auto && p.variant != kI8Strip) return false;
+    return p.variant == kI8Strip || static_cast<double>(p.nz_tiles) <= kStripDensity * groups * KTp;
+}
+
+size_t gemm_i8_ws_bytes(const I8Gemm &p)
+{
+    return use_strip(p) ? static_cast<size_t>((p.M + 15) / 16) * 16 * p.Kp : 0;
+}
+
+void gemm_i8(hipStream_t s, const I8Gemm &p, int8_t *ws)
 {
     const bool aligned = (p.K % 64 == 0) && (p.lda % 16 == 0) &&
                          (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) && p.M >= 64;
@@ -1053,8 +1312,13 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
     const uint32_t tn = (p.N + pipe::TN - 1) / pipe::TN;
     // A requested kernel that cannot take this shape falls back to the
     // automatic choice.
+    // The strip kernel walks only the nonzero 64 x 64 weight tiles (ws holds
+    // gemm_i8_ws_bytes(p): A in fragment blocks).
+    const uint32_t KTp = p.Kp / 64, groups = (p.Np / 16 + 3) / 4;
     uint32_t v = p.variant;
-    if (((v == kI8Wide || v == kI8Wide192) && !wide_ok) || (v == kI8Wave8 && !k128) || (v == kI8Pipe && !aligned))
+    if (ws && use_strip(p)) v = kI8Strip;
+    if (((v == kI8Wide || v == kI8Wide192) && !wide_ok) || (v == kI8Wave8 && !k128) || (v == kI8Pipe && !aligned) ||
+        v == kI8Strip && !(ws && use_strip(p)))
         v = kI8Auto;
     uint32_t mix_a = 0, mix_b = 0;   // tile columns of 256 and 192 (mixed grid)
     if (v == kI8Auto) {
@@ -1094,6 +1358,7 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
         if (!lds_optin) {
             bool ok = true;
             for (const void *fn : {reinterpret_cast<const void *>(gemm_i8_pipe),
+                                   reinterpret_cast<const void *>(gemm_i8_strip),
                                    reinterpret_cast<const void *>(gemm_i8_k128w8),
                                    reinterpret_cast<const void *>(gemm_i8_wide<256>),
                                    reinterpret_cast<const void *>(gemm_i8_wide<192>),
@@ -1120,6 +1385,14 @@ void gemm_i8(hipStream_t s, const I8Gemm &p)
         return;
     }
     switch (v) {
+    case kI8Strip: {
+        const uint32_t tiles_m = (p.M + strip::TM - 1) / strip::TM;
+        const uint64_t chunks = static_cast<uint64_t>((p.M + 15) / 16) * KTp * 64;
+        a_blocks_kernel<<<dim3(static_cast<uint32_t>((chunks + 255) / 256)), 256, 0, s>>>(p.A, p.lda, p.M, KTp,
+                                                                                          chunks, ws);
+        gemm_i8_strip<<<dim3(tiles_m * groups), strip::kThreads, strip::kLds, s>>>(p, tiles_m, groups, ws);
+        return;
+    }
     case kI8Wide:
         gemm_i8_wide<256><<<dim3(wm_ * wn256), kThreads, wide::Cfg<256>::kLds, s>>>(I8GemmPair{{p, p}}, wm_,
                                                                                    wn256, 0);

@@ -29,6 +29,12 @@ void quantize_tensor(hipStream_t s, const float *X, int8_t *Y, float *scales, ui
 void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint32_t ldb,
                     uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,
                     int32_t *column_sums);
+// The nonzero 64 x 64 weight tiles of packed fragments: for each group g of
+// four 16-column strips, list[g][0 .. count[g]) = its k blocks (64 deep)
+// holding a nonzero, ascending (flag: [groups][Kp/64] bytes of scratch;
+// list: [groups][Kp/64], count: [groups], groups = ceil(Np / 64)).
+void tile_lists(hipStream_t s, const int8_t *frag, uint32_t Kp, uint32_t Np, uint8_t *flag, uint32_t *list,
+                uint32_t *count);
 
 // Compute units of the current device (read once per process; 256 if the
 // query fails).  Launch shapes are chosen in whole rounds of these.
@@ -48,19 +54,27 @@ struct I8Gemm {
     uint32_t M = 0, N = 0, K = 0;
     uint32_t epilogue = 0;
     uint32_t variant = 0;            // kI8*: which prefill kernel (0 = choose)
+    // Nonzero 64 x 64 weight tiles (tile_lists): per group of four strips,
+    // the k blocks the strip kernel walks; nz_tiles of (groups x Kp/64) are
+    // nonzero.  Null lists: every block is walked (dense kernels).
+    const uint32_t *nz_list = nullptr, *nz_count = nullptr;
+    uint64_t nz_tiles = 0;
 };
 struct I8GemmPair {
     I8Gemm p[2];
 };
 // Prefill kernels (gemm_i8.hip): a requested one that cannot take the shape
 // falls back to the automatic choice.
-enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generic = 4, kI8Wide192 = 5 };
+enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generic = 4, kI8Wide192 = 5, kI8Strip = 6 };
 // vnpu_device_set_tiles / autotune: tile triples (M, K, N) that name a kernel
 // select it: 256x128x256 wide, 256x128x128 8-wave, 256x64x128 64-deep,
 // 128x64x128 generic; anything else chooses automatically.
 uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t tile_n);
 void gemv_i8(hipStream_t s, const I8Gemm &p);  // M <= 8 (matrix core from 5 rows)
-void gemm_i8(hipStream_t s, const I8Gemm &p);  // any M, int8 MFMA
+// Any M, int8 MFMA; ws holds gemm_i8_ws_bytes(p) (the strip kernel's A in
+// fragment blocks; nothing for the dense kernels, where ws may be null).
+size_t gemm_i8_ws_bytes(const I8Gemm &p);
+void gemm_i8(hipStream_t s, const I8Gemm &p, int8_t *ws);
 // Two independent MATMUL_I8 problems with the same M in one wide-tile grid
 // when that runs fewer whole rounds of tiles; false (nothing launched) when
 // either cannot take the wide kernel or one grid would not be faster.

@@ -13,7 +13,10 @@
 // column-strip-major: the Kp/64 blocks of one 16-column strip are one
 // contiguous run, so the decode GEMV streams each strip sequentially.
 //
-// Also produced: per-column sums (reference scheduler.cpp:798-800).
+// Also produced: per-column sums (reference scheduler.cpp:798-800), and for
+// each group of four strips (64 columns, the reference's 64 x 64 cull tile
+// width) the list of its 64-deep k blocks that hold a nonzero weight, which
+// the strip GEMM walks instead of every k block.
 #include "kernels.hpp"
 
 namespace vnpu {
@@ -81,7 +84,47 @@ __global__ __launch_bounds__(256) void column_sums_kernel(const int8_t *__restri
     }
 }
 
+// Which 64 x 64 weight tiles hold a nonzero: one wave per (k block, group
+// of four 16-column strips); flag[g][kt] = 1 when any of the group's four
+// 1 KiB blocks at k block kt is nonzero.
+__global__ __launch_bounds__(64) void tile_nz_kernel(const int8_t *__restrict__ frag, uint32_t KT, uint32_t NT,
+                                                     uint8_t *__restrict__ flag)
+{
+    const uint32_t kt = blockIdx.x, g = blockIdx.y;
+    const int lane = threadIdx.x;
+    int any = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t nt = 4 * g + j;
+        if (nt >= NT) break;   // uniform
+        const int4 v = reinterpret_cast<const int4 *>(frag + (static_cast<uint64_t>(nt) * KT + kt) * 1024)[lane];
+        any |= v.x | v.y | v.z | v.w;
+    }
+    const uint64_t nz = __ballot(any != 0);
+    if (lane == 0) flag[static_cast<uint64_t>(g) * KT + kt] = nz != 0 ? 1 : 0;
+}
+
+// Each group's nonzero k blocks in ascending order: list[g][0 .. count[g]).
+__global__ __launch_bounds__(64) void tile_list_kernel(const uint8_t *__restrict__ flag, uint32_t KT, uint32_t NG,
+                                                       uint32_t *__restrict__ list, uint32_t *__restrict__ count)
+{
+    const uint32_t g = blockIdx.x * 64 + threadIdx.x;
+    if (g >= NG) return;
+    uint32_t n = 0;
+    for (uint32_t kt = 0; kt < KT; ++kt)
+        if (flag[static_cast<uint64_t>(g) * KT + kt]) list[static_cast<uint64_t>(g) * KT + n++] = kt;
+    count[g] = n;
+}
+
 }  // namespace
+
+void tile_lists(hipStream_t s, const int8_t *frag, uint32_t Kp, uint32_t Np, uint8_t *flag, uint32_t *list,
+                uint32_t *count)
+{
+    const uint32_t KT = Kp / 64, NT = Np / 16, NG = (NT + 3) / 4;
+    tile_nz_kernel<<<dim3(KT, NG), 64, 0, s>>>(frag, KT, NT, flag);
+    tile_list_kernel<<<dim3((NG + 63) / 64), 64, 0, s>>>(flag, KT, NG, list, count);
+}
 
 void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint32_t ldb,
                     uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,

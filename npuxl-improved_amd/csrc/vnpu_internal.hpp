@@ -114,6 +114,11 @@ struct vnpu_packed_weights {
     int8_t *frag = nullptr;        // HBM, [Np/16][Kp/64][4][16][16] fragment layout
     float *scales_dev = nullptr;   // HBM [Np], padding = 1
     uint64_t frag_bytes = 0;
+    // Nonzero 64 x 64 tiles (k::tile_lists): HBM [groups][Kp/64] k-block
+    // lists and [groups] counts, groups = ceil(Np / 64); nz_tiles in total.
+    uint32_t *nz_list = nullptr;
+    uint32_t *nz_count = nullptr;
+    uint64_t nz_tiles = 0;
     std::vector<float> scales;     // host copies for vnpu_packed_weights_info
     std::vector<int32_t> column_sums;
 };

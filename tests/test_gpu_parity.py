@@ -879,3 +879,42 @@ def test_f32_bounded_wait_timeout_is_reported(monkeypatch):
     finally:
         ok.close()
     assert rel(got, oracle.matmul_f32_blas(A, B)) <= 1e-4
+
+
+@pytest.mark.parametrize("M,K,N,density,epi,use_bias", [
+    (512, 1024, 512, 0.3, 0, False),      # whole 512 x 64 tiles
+    (700, 1024, 520, 0.25, 2, True),      # rows past M clamped, a partial last column group, bias, SiLU
+    (1100, 2048, 200, 0.35, 3, True),     # GELU, 200 columns: the last group has 8 of 64 columns
+    (512, 640, 256, 0.0, 1, True),        # every tile zero: the epilogue of the bias alone
+    (600, 16384, 192, 0.2, 0, False),     # 256 k blocks: all four list registers
+    (300, 512, 384, 0.9, 0, False),       # above the strip kernel's density: the dense kernels
+    (512, 1024, 512, 0.5, 1, True),       # config 5's density: the dense kernels
+])
+def test_int8_zero_tile_strip_kernel(gpu, M, K, N, density, epi, use_bias):
+    """Weights whose 64 x 64 tiles are zero with probability 1 - density (the
+    config-5 geometry; one column group and one k block are zeroed entirely):
+    packing lists each 64-column group's nonzero k blocks and, at most 40%
+    of the tiles nonzero, the strip kernel walks only those.  The int32 accumulators, hence C without an exp-based
+    activation, bit-exact with the oracle; SiLU and GELU within 1e-6 (their
+    exp, as in the dense kernels' epilogue tests)."""
+    A = RNG.integers(-128, 128, (M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, (K, N)).astype(np.int8)
+    groups = (N + 63) // 64
+    keep = (RNG.random((K // 64, groups)) < density).astype(np.int8)
+    if density > 0:
+        keep[:, 0] = 0          # a column group without any nonzero tile
+        keep[K // 128, :] = 0   # a k block zero in every group
+    B *= np.kron(keep, np.ones((64, 64), np.int8))[:, :N]
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    bias = RNG.standard_normal(N).astype(np.float32) if use_bias else None
+    w = gpu.pack(B, K, N, scales=sb)
+    try:
+        got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa, bias=bias, epilogue=epi)
+    finally:
+        gpu.release_packed(w)
+    want = oracle.matmul_i8_blas(A, B, sa, sb, bias, epi)
+    if epi in (abi.EPI_NONE, abi.EPI_RELU):
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:
+        assert rel(got, want) <= 1e-6
