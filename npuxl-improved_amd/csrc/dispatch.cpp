@@ -185,6 +185,15 @@ inline size_t span(uint64_t rows, uint64_t cols, uint64_t ld, size_t elem)
 
 inline uint32_t cdiv(uint32_t a, uint32_t b) { return b ? (a + b - 1) / b : 0; }
 
+// Range length of the reference's elementwise commands on a device of
+// info.num_threads units (scheduler.cpp:541-543, 556-557, 569-570); each
+// range has its own scalar tail, which SWIGLU and MUL round differently.
+uint64_t ew_grain(const vnpu_device_t *dev, uint64_t count)
+{
+    const uint64_t units = std::max<uint32_t>(1, dev->info.num_threads);
+    return std::max<uint64_t>(4096, count / (units * 4));
+}
+
 // choose_unit (reference scheduler.cpp:43-59).  UNIT_GPU is this backend's
 // native unit and behaves like AUTO.
 uint32_t choose_unit(uint32_t unit, bool has_mask, uint32_t flags)
@@ -667,6 +676,7 @@ uint32_t try_execute_chain(vnpu_stream_t *s, const vnpu_command_t *c, uint64_t n
     }
     const uint64_t elems = static_cast<uint64_t>(p.rows) * p.cols;
     if (pre_count && pre_count != elems) return 0;
+    p.grain = ew_grain(s->device, elems);
 
     // Aliasing: every output must be disjoint from every other buffer of the
     // chain, except that float rows (A, B, Y, Nrm) may be the same buffer;
@@ -851,7 +861,7 @@ void exec_elementwise(vnpu_stream_t *s, const vnpu_command_t &cmd, ExecStats &st
         const float *g = sg.in(a.gate, a.count * 4);
         const float *u = sg.in(a.up, a.count * 4);
         float *Y = sg.out(a.Y, a.count * 4);
-        k::swiglu(s->hip, g, u, Y, a.count, alpha);
+        k::swiglu(s->hip, g, u, Y, a.count, alpha, ew_grain(s->device, a.count));
         st.bytes_read += a.count * 8;
         st.bytes_written += a.count * 4;
         st.flops += a.count * 8;
@@ -874,7 +884,8 @@ void exec_elementwise(vnpu_stream_t *s, const vnpu_command_t &cmd, ExecStats &st
             const bool both0 = a.alpha == 0.0f && a.beta == 0.0f;  // llm.cpp:226-227
             k::add(s->hip, A, B, Y, a.count, both0 ? 1.0f : a.alpha, both0 ? 1.0f : a.beta);
         } else {
-            k::mul(s->hip, A, B, Y, a.count, a.alpha == 0.0f ? 1.0f : a.alpha, a.beta);
+            k::mul(s->hip, A, B, Y, a.count, a.alpha == 0.0f ? 1.0f : a.alpha, a.beta,
+                   ew_grain(s->device, a.count));
         }
         st.bytes_read += a.count * 8;
         st.bytes_written += a.count * 4;

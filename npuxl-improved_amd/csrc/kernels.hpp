@@ -140,11 +140,15 @@ void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t 
           uint32_t heads, uint32_t q_seq, uint32_t k_seq, uint32_t head_dim,
           uint32_t position_offset, uint32_t interleaved, float scaling, const float *inv_freq,
           const float2 *cs, uint32_t cs_rows);
-void swiglu(hipStream_t s, const float *g, const float *u, float *Y, uint64_t n, float alpha);
+// SWIGLU and MUL round their scalar tails differently: `grain` is the length
+// of the reference's ranges (each with its own tail; 0 = one range).  ADD and
+// GELU give the same bits in a tail.
+void swiglu(hipStream_t s, const float *g, const float *u, float *Y, uint64_t n, float alpha,
+            uint64_t grain);
 void add(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha,
          float beta);
 void mul(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha,
-         float beta);
+         float beta, uint64_t grain);
 void gelu(hipStream_t s, const float *X, float *Y, uint64_t n);
 
 // A run of row-wise commands over the same rows x cols float rows, executed
@@ -163,6 +167,7 @@ struct RowChain {
     const float *A = nullptr, *B = nullptr;
     float *Y = nullptr;
     float alpha = 1.0f, beta = 1.0f;
+    uint64_t grain = 0;    // SWIGLU: range length of the rows * cols command (as k::swiglu)
     const float *W = nullptr;
     float *Nrm = nullptr;  // null: no RMSNORM
     float eps = 1e-5f;

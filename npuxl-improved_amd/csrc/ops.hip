@@ -411,22 +411,64 @@ __device__ __forceinline__ float ew(float a, float b, float alpha, float beta, b
     return dev::gelu_avx2(a);
 }
 
-// First element of the reference's scalar tail for `count` elements.
-__host__ __device__ __forceinline__ uint64_t tail_start(uint64_t count) { return count - count % 8; }
+// Which elements of an elementwise command fall in a scalar tail.  The
+// reference runs a command over n elements as ranges [c*grain, (c+1)*grain)
+// (scheduler.cpp:536-581: grain = max(4096, n / (4 * num_threads));
+// ThreadPool::parallel_for, internal.h:273-340), each as 8-wide steps from
+// its own start and a scalar tail of (length % 8) elements.  When only the
+// last range can have a tail (grain % 8 == 0, or one range) the tail is the
+// last n % 8 elements: grain is then 0 and t0 = n - n % 8.
+struct EwTail {
+    uint64_t n = 0, grain = 0, t0 = 0;
+    __device__ __forceinline__ bool operator()(uint64_t x) const
+    {
+        if (grain == 0) return x >= t0;
+        const uint64_t b = x / grain * grain;
+        const uint64_t len = n - b < grain ? n - b : grain;
+        return x - b >= (len & ~7ull);
+    }
+    // bit k: element e + k (all four < n); one division per call
+    __device__ __forceinline__ uint32_t mask4(uint64_t e) const
+    {
+        uint32_t m = 0;
+        if (grain == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) m |= uint32_t(e + k >= t0) << k;
+            return m;
+        }
+        uint64_t b = e / grain * grain;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (e + k >= b + grain) b += grain;   // grain >= 4096: one step at most
+            const uint64_t len = n - b < grain ? n - b : grain;
+            m |= uint32_t(e + k - b >= (len & ~7ull)) << k;
+        }
+        return m;
+    }
+};
+
+__host__ __device__ inline EwTail ew_tail(uint64_t n, uint64_t grain)
+{
+    EwTail t;
+    t.n = n;
+    if (grain == 0 || grain >= n || grain % 8 == 0) t.t0 = n - n % 8;
+    else t.grain = grain;
+    return t;
+}
 
 template <int OP>
 __global__ __launch_bounds__(kThreads) void ew_vec_kernel(const float4 *__restrict__ A,
                                                           const float4 *__restrict__ B,
                                                           float4 *__restrict__ Y, uint64_t n4,
-                                                          float alpha, float beta, uint64_t t0)
+                                                          float alpha, float beta, EwTail tl)
 {
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n4;
          i += static_cast<uint64_t>(gridDim.x) * kThreads) {
         const float4 a = A[i];
         const float4 b = (OP == EW_GELU) ? a : B[i];
-        const bool tail = 4 * i >= t0;   // the tail is 0 or 4 elements: whole float4s
-        Y[i] = make_float4(ew<OP>(a.x, b.x, alpha, beta, tail), ew<OP>(a.y, b.y, alpha, beta, tail),
-                           ew<OP>(a.z, b.z, alpha, beta, tail), ew<OP>(a.w, b.w, alpha, beta, tail));
+        const uint32_t t = tl.mask4(4 * i);
+        Y[i] = make_float4(ew<OP>(a.x, b.x, alpha, beta, t & 1), ew<OP>(a.y, b.y, alpha, beta, t & 2),
+                           ew<OP>(a.z, b.z, alpha, beta, t & 4), ew<OP>(a.w, b.w, alpha, beta, t & 8));
     }
 }
 
@@ -434,17 +476,16 @@ template <int OP>
 __global__ __launch_bounds__(kThreads) void ew_kernel(const float *__restrict__ A,
                                                       const float *__restrict__ B,
                                                       float *__restrict__ Y, uint64_t n,
-                                                      float alpha, float beta)
+                                                      float alpha, float beta, EwTail tl)
 {
-    const uint64_t t0 = tail_start(n);
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
          i += static_cast<uint64_t>(gridDim.x) * kThreads)
-        Y[i] = ew<OP>(A[i], (OP == EW_GELU) ? 0.0f : B[i], alpha, beta, i >= t0);
+        Y[i] = ew<OP>(A[i], (OP == EW_GELU) ? 0.0f : B[i], alpha, beta, tl(i));
 }
 
 template <int OP>
 void launch_ew(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha,
-               float beta)
+               float beta, uint64_t grain)
 {
     const bool vec = (n % 4 == 0) && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(Y) |
                                        (B ? reinterpret_cast<uintptr_t>(B) : 0)) % 16 == 0);
@@ -455,9 +496,10 @@ void launch_ew(hipStream_t s, const float *A, const float *B, float *Y, uint64_t
     if (vec)
         ew_vec_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(
             reinterpret_cast<const float4 *>(A), reinterpret_cast<const float4 *>(B),
-            reinterpret_cast<float4 *>(Y), n / 4, alpha, beta, tail_start(n));
+            reinterpret_cast<float4 *>(Y), n / 4, alpha, beta, ew_tail(n, grain));
     else
-        ew_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(A, B, Y, n, alpha, beta);
+        ew_kernel<OP><<<dim3(static_cast<uint32_t>(blocks)), kThreads, 0, s>>>(A, B, Y, n, alpha, beta,
+                                                                              ew_tail(n, grain));
 }
 
 template <int NT>
@@ -568,18 +610,18 @@ __global__ __launch_bounds__(NT) void row_chain_kernel(RowChain p)
             b[i] = j < n4 ? reinterpret_cast<const float4 *>(p.B)[off + j] : zero;
         }
         constexpr int OP = PRE == kChainAdd ? EW_ADD : EW_SWIGLU;
-        // the elementwise command spans all rows: its tail is the last
-        // (rows * cols) % 8 elements of the buffer
-        const uint64_t t0 = tail_start(static_cast<uint64_t>(p.rows) * p.cols);
+        // the elementwise command spans all rows: its ranges and tails are
+        // those of rows * cols elements
+        const EwTail tl = ew_tail(static_cast<uint64_t>(p.rows) * p.cols, p.grain);
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const uint32_t j = threadIdx.x + i * NT;
             if (j >= n4) continue;
-            const uint64_t e = 4 * (off + j);
-            v[i] = make_float4(ew<OP>(v[i].x, b[i].x, p.alpha, p.beta, e >= t0),
-                               ew<OP>(v[i].y, b[i].y, p.alpha, p.beta, e + 1 >= t0),
-                               ew<OP>(v[i].z, b[i].z, p.alpha, p.beta, e + 2 >= t0),
-                               ew<OP>(v[i].w, b[i].w, p.alpha, p.beta, e + 3 >= t0));
+            const uint32_t t = OP == EW_ADD ? 0u : tl.mask4(4 * (off + j));   // ADD: tail = body
+            v[i] = make_float4(ew<OP>(v[i].x, b[i].x, p.alpha, p.beta, t & 1),
+                               ew<OP>(v[i].y, b[i].y, p.alpha, p.beta, t & 2),
+                               ew<OP>(v[i].z, b[i].z, p.alpha, p.beta, t & 4),
+                               ew<OP>(v[i].w, b[i].w, p.alpha, p.beta, t & 8));
             reinterpret_cast<float4 *>(p.Y)[off + j] = v[i];
         }
     }
@@ -745,24 +787,26 @@ void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t 
         inv_freq, cs, cs_rows);
 }
 
-void swiglu(hipStream_t s, const float *g, const float *u, float *Y, uint64_t n, float alpha)
+void swiglu(hipStream_t s, const float *g, const float *u, float *Y, uint64_t n, float alpha,
+            uint64_t grain)
 {
-    launch_ew<EW_SWIGLU>(s, g, u, Y, n, alpha, 0.0f);
+    launch_ew<EW_SWIGLU>(s, g, u, Y, n, alpha, 0.0f, grain);
 }
 
 void add(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha, float beta)
 {
-    launch_ew<EW_ADD>(s, A, B, Y, n, alpha, beta);
+    launch_ew<EW_ADD>(s, A, B, Y, n, alpha, beta, 0);   // tail = body (fma(a, alpha, b * beta))
 }
 
-void mul(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha, float beta)
+void mul(hipStream_t s, const float *A, const float *B, float *Y, uint64_t n, float alpha, float beta,
+         uint64_t grain)
 {
-    launch_ew<EW_MUL>(s, A, B, Y, n, alpha, beta);
+    launch_ew<EW_MUL>(s, A, B, Y, n, alpha, beta, grain);
 }
 
 void gelu(hipStream_t s, const float *X, float *Y, uint64_t n)
 {
-    launch_ew<EW_GELU>(s, X, nullptr, Y, n, 0.0f, 0.0f);
+    launch_ew<EW_GELU>(s, X, nullptr, Y, n, 0.0f, 0.0f, 0);   // tail = body
 }
 
 bool row_chain(hipStream_t s, const RowChain &p)

@@ -54,10 +54,10 @@ def lib() -> C.CDLL:
             "vo_attention": (None, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32]),
             "vo_rmsnorm_avx2": (None, [vp, vp, vp, u32, u32, f32]),
             "vo_exp_avx2": (f32, [f32]),
-            "vo_swiglu_avx2": (None, [vp, vp, vp, u64, f32]),
+            "vo_swiglu_avx2": (None, [vp, vp, vp, u64, f32, u64]),
             "vo_softmax_avx2": (None, [vp, vp, u32, u32, f32]),
             "vo_gelu_avx2": (None, [vp, vp, u64]),
-            "vo_mul_avx2": (None, [vp, vp, vp, u64, f32, f32]),
+            "vo_mul_avx2": (None, [vp, vp, vp, u64, f32, f32, u64]),
             "vo_add_avx2": (None, [vp, vp, vp, u64, f32, f32]),
             "vo_attention_avx2": (None, [vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, f32]),
         }
@@ -264,11 +264,20 @@ def rmsnorm_avx2(X, W=None, eps=1e-5):
     return Y
 
 
-def swiglu_avx2(g, u, alpha=1.0):
-    """SWIGLU in the order of the reference's AVX2 build (bit for bit)."""
+def ew_grain(count, num_threads):
+    """Range length of the reference's elementwise commands on a device of
+    num_threads units (src/core/scheduler.cpp:541-543): max(4096, count /
+    (4 num_threads)); None -> 0, one range."""
+    return 0 if num_threads is None else max(4096, count // (4 * num_threads))
+
+
+def swiglu_avx2(g, u, alpha=1.0, num_threads=None):
+    """SWIGLU in the order of the reference's AVX2 build (bit for bit), split
+    into the ranges the reference runs on a device of num_threads units (each
+    range has its own scalar tail; None: one range)."""
     g, u = _c(g, np.float32), _c(u, np.float32)
     Y = np.empty_like(g)
-    lib().vo_swiglu_avx2(_p(g), _p(u), _p(Y), g.size, alpha)
+    lib().vo_swiglu_avx2(_p(g), _p(u), _p(Y), g.size, alpha, ew_grain(g.size, num_threads))
     return Y
 
 
@@ -280,11 +289,12 @@ def gelu_avx2(x):
     return Y
 
 
-def mul_avx2(a, b, alpha=1.0, beta=0.0):
-    """MUL in the order of the reference's AVX2 build (bit for bit)."""
+def mul_avx2(a, b, alpha=1.0, beta=0.0, num_threads=None):
+    """MUL in the order of the reference's AVX2 build (bit for bit), ranges as
+    in swiglu_avx2."""
     a, b = _c(a, np.float32), _c(b, np.float32)
     Y = np.empty_like(a)
-    lib().vo_mul_avx2(_p(a), _p(b), _p(Y), a.size, alpha, beta)
+    lib().vo_mul_avx2(_p(a), _p(b), _p(Y), a.size, alpha, beta, ew_grain(a.size, num_threads))
     return Y
 
 

@@ -675,21 +675,31 @@ void vo_softmax_avx2(const float *X, float *Y, uint32_t rows, uint32_t cols, flo
     }
 }
 
-/* The elementwise AVX2 ranges run 8-wide steps from the start of a range and
- * the last count % 8 elements in their scalar tail loop (one range per
- * command while the reference's chunk size, max(4096, count / (4 threads)),
- * is a multiple of 8). */
-static uint64_t vo_tail_start(uint64_t count) { return count - count % 8; }
+/* The elementwise commands run as ranges [c * grain, min(count, (c + 1) *
+ * grain)) (scheduler.cpp:536-581 with grain = max(4096, count / (4 *
+ * num_threads)); ThreadPool::parallel_for, internal.h:273-340, hands each
+ * range to a *_avx2_range call), and each range runs 8-wide steps from its
+ * own start and the last (length % 8) elements in its scalar tail.  grain 0
+ * (or >= count) is one range.  The hybrid-core weighted split of
+ * parallel_for (internal.h:301-340: a device whose units run at different
+ * speeds and few chunks) is host-specific and not restated. */
+static int vo_in_tail(uint64_t i, uint64_t count, uint64_t grain)
+{
+    if (grain == 0 || grain > count) grain = count;
+    const uint64_t b = i / grain * grain;
+    const uint64_t len = count - b < grain ? count - b : grain;
+    return i - b >= (len & ~(uint64_t)7);
+}
 
-void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha)
+void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha,
+                    uint64_t grain)
 {
     float a = alpha == 0.0f ? 1.0f : alpha;
-    const uint64_t t0 = vo_tail_start(count);
     for (uint64_t i = 0; i < count; ++i) {
         float g = gate[i];
         /* vector: exp256_ps clamps to [-80, 80]; tail: silu() with the
          * scalar fast_expf (llm.cpp:240-246 inlined into swiglu_avx2_range) */
-        float s = g / (1.0f + (i < t0 ? vo_exp_avx2(-g) : vo_fast_expf_fma(-g)));
+        float s = g / (1.0f + (vo_in_tail(i, count, grain) ? vo_fast_expf_fma(-g) : vo_exp_avx2(-g)));
         Y[i] = (s * up[i]) * a;
     }
 }
@@ -710,12 +720,12 @@ void vo_gelu_avx2(const float *X, float *Y, uint64_t count)
 
 /* mul_avx2_range (llm.cpp:273-287): y = fma(a*b, alpha, beta) in the 8-wide
  * steps; the tail's alpha * a * b + beta contracts to fma(alpha*a, b, beta). */
-void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta)
+void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta,
+                 uint64_t grain)
 {
     float a = alpha == 0.0f ? 1.0f : alpha;
-    const uint64_t t0 = vo_tail_start(count);
     for (uint64_t i = 0; i < count; ++i)
-        Y[i] = i < t0 ? fmaf(A[i] * B[i], a, beta) : fmaf(a * A[i], B[i], beta);
+        Y[i] = vo_in_tail(i, count, grain) ? fmaf(a * A[i], B[i], beta) : fmaf(A[i] * B[i], a, beta);
 }
 
 /* add_avx2_range (llm.cpp:256-271): y = fma(a, alpha, b*beta); the tail's

@@ -73,11 +73,15 @@ void vo_attention(const float *Q, const float *K, const float *V, const float *m
 /* The reference's AVX2 builds of the block's f32 ops, rounding for rounding. */
 void vo_rmsnorm_avx2(const float *X, const float *W, float *Y, uint32_t rows, uint32_t cols, float eps);
 float vo_exp_avx2(float x);
-void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha);
+/* SWIGLU and MUL round differently in each range's scalar tail: ranges of
+ * `grain` elements (0: one range), as the reference's command splits them. */
+void vo_swiglu_avx2(const float *gate, const float *up, float *Y, uint64_t count, float alpha,
+                    uint64_t grain);
 void vo_softmax_avx2(const float *X, float *Y, uint32_t rows, uint32_t cols, float temperature);
 void vo_gelu_avx2(const float *X, float *Y, uint64_t count);
 void vo_add_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta);
-void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta);
+void vo_mul_avx2(const float *A, const float *B, float *Y, uint64_t count, float alpha, float beta,
+                 uint64_t grain);
 void vo_attention_avx2(const float *Q, const float *K, const float *V, const float *mask, float *O,
                        uint32_t batch, uint32_t heads, uint32_t seq_q, uint32_t seq_k,
                        uint32_t head_dim, uint32_t causal, float scale);

@@ -52,6 +52,44 @@ def test_elementwise_bit_exact(gpu, n):
     assert bits(g.elementwise(gpu, abi.OP_GELU_F32, a), oracle.gelu_avx2(a))
 
 
+@pytest.fixture(scope="module")
+def gpu4():
+    """A device created with num_threads = 4: the reference's elementwise
+    ranges (max(4096, n / (4 * num_threads)) elements) follow the unit count."""
+    from vnpu_mi355x import Session
+    cfg = abi.Config()
+    cfg.abi_version = 1
+    cfg.num_threads = 4
+    s = Session(None, cfg)
+    yield s
+    s.close()
+
+
+@pytest.mark.parametrize("dev_name,n", [("gpu4", 70001), ("gpu4", 100004), ("gpu", 5_000_004),
+                                        ("gpu", 5_000_003)])
+def test_elementwise_reference_ranges(request, dev_name, n):
+    """Above 16384 * num_threads elements the reference runs ranges whose
+    length is not a multiple of 8, each ending in its own scalar tail: the
+    GPU gives the same bits as the oracle split the same way (vector and
+    scalar kernels), and not those of one range."""
+    dev = request.getfixturevalue(dev_name)
+    threads = dev.info().num_threads
+    grain = oracle.ew_grain(n, threads)
+    assert grain % 8 != 0 and n > grain, (threads, grain)
+    a = (RNG.standard_normal(n) * 4).astype(np.float32)
+    b = RNG.standard_normal(n).astype(np.float32)
+    for end in list(range(grain, n, grain)) + [n]:
+        a[end - 3:end] = (-90.0, -85.0, -81.0)     # exp's clamp edges in each range's tail
+    for al, be in ((0.0, 0.0), (-1.5, 2.0)):
+        sw = g.elementwise(dev, abi.OP_SWIGLU_F32, a, b, alpha=al)
+        mu = g.elementwise(dev, abi.OP_MUL_F32, a, b, al, be)
+        assert bits(sw, oracle.swiglu_avx2(a, b, al or 1.0, num_threads=threads))
+        assert bits(mu, oracle.mul_avx2(a, b, al or 1.0, be, num_threads=threads))
+        assert not bits(sw, oracle.swiglu_avx2(a, b, al or 1.0))
+        assert bits(g.elementwise(dev, abi.OP_ADD_F32, a, b, al, be), oracle.add_avx2(a, b, al, be))
+    assert bits(g.elementwise(dev, abi.OP_GELU_F32, a), oracle.gelu_avx2(a))
+
+
 @pytest.mark.parametrize("interleaved", [0, 1])
 @pytest.mark.parametrize("shape_q,shape_k,offset", [((1, 32, 2048, 128), (1, 32, 2048, 128), 0),
                                                     ((8, 32, 1, 128), (8, 32, 1, 128), 4095),

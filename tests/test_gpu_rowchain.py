@@ -124,6 +124,29 @@ def test_chain_equals_commands_one_by_one(gpu, kind, rows, cols, alias):
         assert np.array_equal(fused["scales"].view(np.uint32), np.asarray(s, np.float32).view(np.uint32))
 
 
+def test_swiglu_chain_reference_ranges(gpu):
+    """SWIGLU -> QUANTIZE_I8 over 512 x 11004 elements: above 16384 *
+    num_threads the reference's SWIGLU ranges (max(4096, n / (4 *
+    num_threads))) are not multiples of 8 and each ends in a scalar tail; the
+    chain and the commands one by one give the oracle's bits split that way."""
+    rows, cols = 512, 11004
+    threads = gpu.info().num_threads
+    grain = oracle.ew_grain(rows * cols, threads)
+    if grain % 8 == 0 or grain >= rows * cols:
+        pytest.skip(f"num_threads {threads}: ranges of {grain} elements end on 8-element steps")
+    p = _params("swiglu_quant", rows, cols)
+    flat = p["x"].reshape(-1)
+    for end in list(range(grain, rows * cols, grain)) + [rows * cols]:
+        flat[end - 2:end] = (-90.0, -85.0)
+    fused = _run(gpu, "swiglu_quant", rows, cols, False, True, p)
+    single = _run(gpu, "swiglu_quant", rows, cols, False, False, p)
+    _same_bits(fused, single)
+    want = oracle.swiglu_avx2(p["x"], p["y"], 1.0, num_threads=threads).reshape(rows, cols)
+    assert np.array_equal(fused["ff"].view(np.uint32), want.view(np.uint32))
+    q, s = oracle.quantize(want, abi.QUANT_PER_ROW)
+    assert np.array_equal(fused["q"], q)
+
+
 @pytest.mark.parametrize("kind", ["add_norm_quant", "swiglu_quant"])
 def test_chain_scalars(gpu, kind):
     """Non-default ADD alpha/beta and SWIGLU alpha, and ADD with alpha = beta

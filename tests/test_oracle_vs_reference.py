@@ -239,8 +239,9 @@ def test_rmsnorm_avx2_order_bit_exact(ref, rows, cols):
 def test_elementwise_avx2_order_bit_exact(ref, n):
     """SWIGLU, GELU, ADD and MUL: 8-wide steps, then the last n % 8 elements in
     the scalar tail (MUL contracts differently there, SWIGLU's exp is not
-    clamped there).  Sizes keep the reference's range partition to one range
-    (chunks of max(4096, n / 16) at 4 threads are multiples of 8)."""
+    clamped there).  At these sizes the reference's ranges (max(4096, n / 16)
+    elements at 4 threads) are multiples of 8, so only the last range has a
+    tail."""
     a = (RNG.standard_normal(n) * 4).astype(np.float32)
     b = RNG.standard_normal(n).astype(np.float32)
     edges = np.array([90.0, -90.0, 80.0, -80.0, 80.5, -80.5, 0.0, -0.0, -88.0, -87.5], np.float32)   # exp's clamp
@@ -250,6 +251,31 @@ def test_elementwise_avx2_order_bit_exact(ref, n):
         assert _bits(g.elementwise(ref, abi.OP_SWIGLU_F32, a, b, alpha=al), oracle.swiglu_avx2(a, b, al or 1.0))
         assert _bits(g.elementwise(ref, abi.OP_ADD_F32, a, b, al, be), oracle.add_avx2(a, b, al, be))
         assert _bits(g.elementwise(ref, abi.OP_MUL_F32, a, b, al, be), oracle.mul_avx2(a, b, al or 1.0, be))
+    assert _bits(g.elementwise(ref, abi.OP_GELU_F32, a), oracle.gelu_avx2(a))
+
+
+@pytest.mark.parametrize("n", [70001, 100004])
+def test_elementwise_avx2_ranges_bit_exact(ref, n):
+    """Above 16384 * num_threads elements the reference splits a command into
+    ranges of max(4096, n / (4 * num_threads)) elements; at 4 threads these
+    sizes give ranges that are not multiples of 8, so every range ends in a
+    scalar tail of its own (SWIGLU's unclamped exp, MUL's other contraction)."""
+    grain = oracle.ew_grain(n, 4)
+    assert grain % 8 != 0 and n > grain
+    a = (RNG.standard_normal(n) * 4).astype(np.float32)
+    b = RNG.standard_normal(n).astype(np.float32)
+    for end in list(range(grain, n, grain)) + [n]:
+        a[end - 3:end] = (-90.0, -85.0, -81.0)     # exp's clamp edges in each range's tail
+    for al, be in ((0.0, 0.0), (-1.75, 3.0)):
+        sw = g.elementwise(ref, abi.OP_SWIGLU_F32, a, b, alpha=al)
+        mu = g.elementwise(ref, abi.OP_MUL_F32, a, b, al, be)
+        assert _bits(sw, oracle.swiglu_avx2(a, b, al or 1.0, num_threads=4))
+        assert _bits(mu, oracle.mul_avx2(a, b, al or 1.0, be, num_threads=4))
+        # one range (only the last n % 8 in a tail) is not the reference's result
+        assert not _bits(sw, oracle.swiglu_avx2(a, b, al or 1.0))
+        if al:   # alpha 1, beta 0: both of MUL's contractions are the exact product
+            assert not _bits(mu, oracle.mul_avx2(a, b, al or 1.0, be))
+        assert _bits(g.elementwise(ref, abi.OP_ADD_F32, a, b, al, be), oracle.add_avx2(a, b, al, be))
     assert _bits(g.elementwise(ref, abi.OP_GELU_F32, a), oracle.gelu_avx2(a))
 
 
