@@ -318,9 +318,23 @@ struct DevBuf {
 // -------------------------------------------------------------------------
 // Node server
 // -------------------------------------------------------------------------
+// Freed by whoever drops the last reference: the weight map when a SET_WEIGHTS
+// replaces it, or a MATMUL_F32 that still held it (it releases it only after
+// its stream synchronized, so no kernel reads freed memory).
 struct NodeWeights {
     void *dev = nullptr;       // HBM, as received: K x N, or N x K when trans_b
+    int hip_device = 0;
     uint32_t K = 0, N = 0, trans_b = 0;
+    NodeWeights() = default;
+    NodeWeights(const NodeWeights &) = delete;
+    NodeWeights &operator=(const NodeWeights &) = delete;
+    ~NodeWeights()
+    {
+        if (dev) {
+            (void)hipSetDevice(hip_device);
+            (void)hipFree(dev);
+        }
+    }
 };
 
 struct NodeState {
@@ -329,14 +343,6 @@ struct NodeState {
     std::unordered_map<uint64_t, std::shared_ptr<NodeWeights>> weights;
     std::atomic<uint64_t> requests{0}, errors{0};
     std::string node_name;
-    ~NodeState()
-    {
-        for (auto &kv : weights)
-            if (kv.second->dev) {
-                (void)hipSetDevice(device->hip_device);
-                (void)hipFree(kv.second->dev);
-            }
-    }
 };
 
 std::atomic<bool> g_node_stop{false};
@@ -442,21 +448,19 @@ void serve_client(int fd, std::shared_ptr<NodeState> st, std::string token)
                 w->K = req.K;
                 w->N = req.N;
                 w->trans_b = req.trans_b ? 1 : 0;
+                w->hip_device = dev;
                 VNPU_HIP(hipSetDevice(dev));
                 VNPU_HIP(hipMalloc(&w->dev, bytes));
                 VNPU_HIP(hipMemcpyAsync(w->dev, pin, bytes, hipMemcpyHostToDevice, stream->hip));
                 VNPU_HIP(hipStreamSynchronize(stream->hip));
-                std::shared_ptr<NodeWeights> old;
+                std::shared_ptr<NodeWeights> old;   // freed below unless a MATMUL_F32 still holds it
                 {
                     std::lock_guard<std::mutex> lock(st->weights_mutex);
                     auto &slot = st->weights[req.weight_id];
                     old.swap(slot);
                     slot = w;
                 }
-                if (old && old.use_count() == 1 && old->dev) {
-                    (void)hipFree(old->dev);
-                    old->dev = nullptr;
-                }
+                old.reset();
                 reply_status(fd, h.op, h.request_id, VNPU_OK);
                 break;
             }

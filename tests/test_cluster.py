@@ -313,3 +313,55 @@ def test_node_shutdown_op(gpu):
     c.close()
     node.thread.join(timeout=60)
     assert not node.thread.is_alive() and node.rc == abi.OK
+
+
+@pytest.mark.gpu
+def test_node_frees_replaced_weights(gpu):
+    """STORE over a weight id that a MATMUL on another connection may be
+    using at that moment: the replaced weights are freed by whichever drops
+    them last, so HBM does not grow over many replacements."""
+    hip = C.CDLL("libamdhip64.so")
+
+    def free_bytes():
+        f, t = C.c_size_t(), C.c_size_t()
+        assert hip.hipMemGetInfo(C.byref(f), C.byref(t)) == 0
+        return f.value
+
+    K, N, M = 2048, 4096, 256                       # 32 MiB of weights
+    B = RNG.standard_normal((K, N)).astype(np.float32)
+    A = RNG.standard_normal((M, K)).astype(np.float32)
+    wid = fnv1a64("replaced")
+    store = STORE.pack(wid, K, N, 0, 0, b"r") + B.tobytes()
+    mm = MATMUL.pack(wid, M, K, N, 0, 0, 0) + A.tobytes()
+    node = Node(gpu.lib)
+    try:
+        c1, c2 = Raw(node.port), Raw(node.port)
+        assert c1.request(OP_HELLO, hello(b""))[0] == 0 and c2.request(OP_HELLO, hello(b""))[0] == 0
+        for _ in range(2):                           # both connections' buffers at their size
+            assert c1.request(OP_STORE, store)[0] == 0
+            assert c2.request(OP_MATMUL, mm)[0] == 0
+        base = free_bytes()
+        stop, statuses = threading.Event(), []
+
+        def matmuls():
+            while not stop.is_set():
+                st, out = c2.request(OP_MATMUL, mm)
+                statuses.append(st)
+                if st != 0 or len(out) != 4 * M * N:
+                    break
+
+        t = threading.Thread(target=matmuls)
+        t.start()
+        try:
+            for _ in range(24):
+                assert c1.request(OP_STORE, store)[0] == 0
+        finally:
+            stop.set()
+            t.join(timeout=120)
+        assert not t.is_alive() and statuses and all(s == 0 for s in statuses)
+        lost = base - free_bytes()
+        assert lost <= 2 * K * N * 4, f"{lost >> 20} MiB of HBM not returned after 24 replacements"
+        c1.close()
+        c2.close()
+    finally:
+        node.stop()
