@@ -357,8 +357,7 @@ void launch(hipStream_t s, const Attn &a)
 // chain is independent per head element.  So decode runs as two kernels:
 //   attn_dec_scores  s[row][key] = dot_avx2(q_row, k_key) * scale, then -inf
 //                    for a causally masked key or + mask, every key in
-//                    parallel (two lanes per key, chains 0-3 and 4-7; the
-//                    pair exchange gives hsum256's pairing);
+//                    parallel (one lane per key running its eight chains);
 //   attn_dec_chain   one wave per (row, 64 head elements): per 64-key block
 //                    the block max, m, alpha and the weights from the saved
 //                    scores (every wave of a row derives the same ones), the

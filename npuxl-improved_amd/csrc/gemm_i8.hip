@@ -1276,8 +1276,8 @@ uint32_t cu_count()
 // 4096^3 against the 256 x 256 dense kernel on the same weights: 1.06x the
 // dense time at 50% nonzero tiles, 0.88x at 37.5%, 0.77x at 25%, 0.63x at
 // 12.5%.  The int8 GEMM is bound by operand traffic into LDS, not by the
-// matrix cores: skipping a zero tile halves its MFMAs, but A is read once
-// per 64-column group instead of once per 256-column tile.
+// matrix cores: at 50% zero tiles the skip removes half the MFMAs, but A is
+// read once per 64-column group instead of once per 256-column tile.
 constexpr double kStripDensity = 0.4;
 
 // The strip kernel takes the call: packed weights with nonzero-tile lists,
