@@ -81,6 +81,57 @@ __device__ __forceinline__ f32x32 mfma1(float a, float b, f32x32 c)
     return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
 }
 
+// Both halves' values of a lane's column: lo[l] = v of lane l % 32, hi[l] =
+// v of lane 32 + l % 32 (one v_permlane32_swap_b32).
+__device__ __forceinline__ void halves(float v, float &lo, float &hi)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+}
+
+// The weights and the output chain of one 64-key block for the lane's row
+// (keys 32t + 8g + 4h + j of S[t][4g + j] in half h): per group of eight keys,
+// the weights of both halves, the weight sum in key order, then one
+// instruction per key and 64 head elements, keys ascending.  FULL: every key
+// of the block is seen by some row of the wave (no per-key test).  Returns
+// the block's weight sum.
+template <int D, bool FULL>
+__device__ __forceinline__ float weights_output(f32x32 (&oacc)[D / 64], const float (&S)[2][16], float nm,
+                                                bool live, uint32_t kc_w, int lane, const float *Vb)
+{
+#pragma clang fp contract(off)
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            // One group's operands in registers at a time: without the fence
+            // the scheduler hoists every V read of the block.
+            __builtin_amdgcn_sched_barrier(0);
+            float lo[4], hi[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float e = dev::fast_expf_unfused(S[t][4 * g + j] - nm);
+                halves(live ? e : 0.0f, lo[j], hi[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) psum = psum + lo[j];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) psum = psum + hi[j];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int kk = 32 * t + 8 * g + j;
+                if (FULL || kk < static_cast<int>(kc_w)) {   // uniform
+#pragma unroll
+                    for (int mm = 0; mm < D / 64; ++mm)
+                        oacc[mm] = mfma1(Vb[kk * D + 64 * mm + lane], j < 4 ? lo[j] : hi[j - 4], oacc[mm]);
+                }
+            }
+        }
+    return psum;
+}
+
 // One query row in the reference's order on the vector ALUs, by one wave:
 // lane j scores key k0 + j of each block, lane e owns head elements e,
 // e + 64, ... of the output row.
@@ -262,49 +313,25 @@ __global__ __launch_bounds__(XT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) bmax = fmaxf(bmax, S[t][r]);
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        {
+            float b0, b1;
+            halves(bmax, b0, b1);
+            bmax = fmaxf(b0, b1);
+        }
         const bool live = isfinite(bmax);
         const float nm = m < bmax ? bmax : m;
         const float alpha = live ? dev::fast_expf_unfused(m - nm) : 1.0f;
+        if (__ballot(alpha != 1.0f)) {   // acc * 1 is acc: skipped when no row's max moved
 #pragma unroll
-        for (int mm = 0; mm < NM; ++mm)
+            for (int mm = 0; mm < NM; ++mm)
 #pragma unroll
-            for (int r = 0; r < 32; ++r) oacc[mm][r] = oacc[mm][r] * alpha;
+                for (int r = 0; r < 32; ++r) oacc[mm][r] = oacc[mm][r] * alpha;
+        }
 
-        // Keys in groups of eight (32t + 8g .. +7): the weights of this
-        // half's four keys, the other half's four by exchange, the weight
-        // sum in key order, then the output chain, keys ascending (keys no
-        // row of the wave sees are skipped).
-        float psum = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                // One group's operands in registers at a time: without the
-                // fence the scheduler hoists every V read of the block.
-                __builtin_amdgcn_sched_barrier(0);
-                float lo[4], hi[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float p = live ? dev::fast_expf_unfused(S[t][4 * g + j] - nm) : 0.0f;
-                    const float x = __shfl_xor(p, 32, 64);
-                    lo[j] = h ? x : p;
-                    hi[j] = h ? p : x;
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) psum = psum + lo[j];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) psum = psum + hi[j];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int kk = 32 * t + 8 * g + j;
-                    if (kk < static_cast<int>(kc_w)) {   // uniform
-#pragma unroll
-                        for (int mm = 0; mm < NM; ++mm)
-                            oacc[mm] = mfma1(Vb[kk * D + 64 * mm + lane], j < 4 ? lo[j] : hi[j - 4], oacc[mm]);
-                    }
-                }
-            }
+        // Keys in groups of eight (32t + 8g .. +7); keys no row of the wave
+        // sees are skipped.
+        const float psum = kc_w == XB ? weights_output<D, true>(oacc, S, nm, live, kc_w, lane, Vb)
+                                      : weights_output<D, false>(oacc, S, nm, live, kc_w, lane, Vb);
         if (live) {
             l = l * alpha + psum;
             m = nm;

@@ -53,11 +53,12 @@ __device__ __forceinline__ float add_rn(float a, float b)
 // fast_expf as the reference's baseline x86-64 build evaluates it in code
 // without an AVX2 target (its attention_range, llm.cpp:442-546): the same
 // steps with every multiply and add of the polynomial rounded separately.
+// The range tests are selects, not branches: the polynomial is evaluated for
+// every x and discarded outside [-80, 80] (a NaN takes the polynomial, as in
+// the reference), so lanes of a wave never diverge here.
 __device__ __forceinline__ float fast_expf_unfused(float x)
 {
 #pragma clang fp contract(off)
-    if (x < -80.0f) return 0.0f;
-    if (x > 80.0f) return __builtin_inff();
     const float z = x * 1.4426950408889634f;
     const float zi = floorf(z);
     const float f = z - zi;
@@ -66,7 +67,8 @@ __device__ __forceinline__ float fast_expf_unfused(float x)
                     f * (0.05550410866482158f +
                     f * (0.009618129107628477f +
                     f * 0.0013333558146428443f))));
-    return ldexpf(p, static_cast<int>(zi));
+    const float r = ldexpf(p, static_cast<int>(fminf(fmaxf(zi, -256.0f), 256.0f)));
+    return x < -80.0f ? 0.0f : (x > 80.0f ? __builtin_inff() : r);
 }
 
 // exp256_ps (reference src/kernels/llm.cpp:31-56), the vector exp of the
