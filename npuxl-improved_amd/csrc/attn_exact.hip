@@ -95,40 +95,48 @@ __device__ __forceinline__ void halves(float v, float &lo, float &hi)
 // the weights of both halves, the weight sum in key order, then one
 // instruction per key and 64 head elements, keys ascending.  FULL: every key
 // of the block is seen by some row of the wave (no per-key test).  Returns
-// the block's weight sum.
+// the block's weight sum.  Every S - nm is <= 0 or NaN (nm is the max).
 template <int D, bool FULL>
 __device__ __forceinline__ float weights_output(f32x32 (&oacc)[D / 64], const float (&S)[2][16], float nm,
                                                 bool live, uint32_t kc_w, int lane, const float *Vb)
 {
 #pragma clang fp contract(off)
     float psum = 0.0f;
+    float lo[4], hi[4], nlo[4], nhi[4];
+    auto weights = [&](int t, int g, float (&wl)[4], float (&wh)[4]) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+        for (int j = 0; j < 4; ++j) {
+            const float e = dev::fast_expf_nonpos(S[t][4 * g + j] - nm);
+            halves(live ? e : 0.0f, wl[j], wh[j]);
+        }
+    };
+    weights(0, 0, nlo, nhi);
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            // One group's operands in registers at a time: without the fence
-            // the scheduler hoists every V read of the block.
-            __builtin_amdgcn_sched_barrier(0);
-            float lo[4], hi[4];
+    for (int q = 0; q < 8; ++q) {   // group q: keys 8q .. 8q + 7
+        // One group's V operands in registers at a time (without the fence
+        // the scheduler hoists every V read of the block); the next group's
+        // weights are computed while this group's instructions run.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float e = dev::fast_expf_unfused(S[t][4 * g + j] - nm);
-                halves(live ? e : 0.0f, lo[j], hi[j]);
-            }
+        for (int j = 0; j < 4; ++j) {
+            lo[j] = nlo[j];
+            hi[j] = nhi[j];
+        }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) psum = psum + lo[j];
+        for (int j = 0; j < 4; ++j) psum = psum + lo[j];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) psum = psum + hi[j];
+        for (int j = 0; j < 4; ++j) psum = psum + hi[j];
+        if (q < 7) weights((q + 1) / 4, (q + 1) % 4, nlo, nhi);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int kk = 32 * t + 8 * g + j;
-                if (FULL || kk < static_cast<int>(kc_w)) {   // uniform
+        for (int j = 0; j < 8; ++j) {
+            const int kk = 8 * q + j;
+            if (FULL || kk < static_cast<int>(kc_w)) {   // uniform
 #pragma unroll
-                    for (int mm = 0; mm < D / 64; ++mm)
-                        oacc[mm] = mfma1(Vb[kk * D + 64 * mm + lane], j < 4 ? lo[j] : hi[j - 4], oacc[mm]);
-                }
+                for (int mm = 0; mm < D / 64; ++mm)
+                    oacc[mm] = mfma1(Vb[kk * D + 64 * mm + lane], j < 4 ? lo[j] : hi[j - 4], oacc[mm]);
             }
         }
+    }
     return psum;
 }
 
@@ -257,13 +265,12 @@ __global__ __launch_bounds__(XT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         const float *Kb = Kt + (b & 1) * L::KTILE;
         const float *Vb = Vt + (b & 1) * L::VTILE;
 
-        // Scores: S[t][r] is (key k0 + 32t + 8(r/4) + 4h + r%4, row qi).
+        // Scores: S[t][r] is (key k0 + 32t + 8(r/4) + 4h + r%4, row qi).  Both
+        // 32-key tiles are computed (a tile no row sees is masked below), so
+        // the two tiles' products and sums share one scheduling region.
         float S[2][16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) S[1][r] = -__builtin_inff();
-#pragma unroll
         for (int t = 0; t < 2; ++t) {
-            if (t == 1 && kc_w <= 32) continue;   // uniform: no key of the second tile is seen
             // Two passes of two chain pairs each: (0,4) and (1,5), then (2,6)
             // and (3,7); hsum256's ((c0+c4) + (c1+c5)) + ((c2+c6) + (c3+c7)).
             const float *kr = Kb + (32 * t + c32) * L::KP + 4 * h;
@@ -288,13 +295,20 @@ __global__ __launch_bounds__(XT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 acc1 = mfma1(kv.y, qop[i].w, acc1);
             }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float dot = s01[r] + ((acc0[r] + acc0[r + 16]) + (acc1[r] + acc1[r + 16]));
-                const uint32_t key = k0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-                const float sc = dot * a.scale;
-                const bool valid = qvalid && key < kend && !(a.causal && key > qi + off);
-                S[t][r] = valid ? sc : -__builtin_inff();
-            }
+            for (int r = 0; r < 16; ++r)
+                S[t][r] = (s01[r] + ((acc0[r] + acc0[r + 16]) + (acc1[r] + acc1[r + 16]))) * a.scale;
+        }
+        // Every row of the wave sees every key of the block: no masking.
+        const bool dense = qw0 + XQW <= sq && k0 + XB <= kend && (!a.causal || k0 + XB - 1 <= qw0 + off);
+        if (!dense) {   // uniform
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t key = k0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const bool valid = qvalid && key < kend && !(a.causal && key > qi + off);
+                    S[t][r] = valid ? S[t][r] : -__builtin_inff();
+                }
         }
         if (Mh) {   // the additive mask on the scores the row sees (uniform)
 #pragma unroll

@@ -71,6 +71,24 @@ __device__ __forceinline__ float fast_expf_unfused(float x)
     return x < -80.0f ? 0.0f : (x > 80.0f ? __builtin_inff() : r);
 }
 
+// fast_expf_unfused for x <= 0 or NaN (a softmax weight or rescale factor:
+// x = s - max): the same result with the x > 80 test and the upper clamp of
+// the exponent dropped, since neither can apply.
+__device__ __forceinline__ float fast_expf_nonpos(float x)
+{
+#pragma clang fp contract(off)
+    const float z = x * 1.4426950408889634f;
+    const float zi = floorf(z);
+    const float f = z - zi;
+    const float p = 1.0f + f * (0.6931471805599453f +
+                    f * (0.2402265069591007f +
+                    f * (0.05550410866482158f +
+                    f * (0.009618129107628477f +
+                    f * 0.0013333558146428443f))));
+    const float r = ldexpf(p, static_cast<int>(fmaxf(zi, -256.0f)));
+    return x < -80.0f ? 0.0f : r;
+}
+
 // exp256_ps (reference src/kernels/llm.cpp:31-56), the vector exp of the
 // reference's AVX2 SWIGLU / GELU / SOFTMAX: x clamped to [-80, 80] (a NaN
 // becomes 80, as min_ps/max_ps give), then fast_expf's steps.
