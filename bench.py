@@ -598,7 +598,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": GEMV_TRAFFIC_BYTES, "kernel": "gemv_i8_kernel", "kernel_us": round(head["kernel_us"], 3),
-                     "algorithmic_bytes": b},
+                     "algorithmic_bytes": b,
+                     "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE passes of this command, scaled by a copy "
+                                       "kernel of known size: profiles/gemv_i8_m1_k4096_n32000_traffic.md"},
         "cpu_baseline": cpu,
         "extras": extras,
     }
