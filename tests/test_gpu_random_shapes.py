@@ -7,6 +7,7 @@ src/kernels/kernels.cpp:922-978 accumulation and store_i8_c order)."""
 import numpy as np
 import pytest
 
+import gpu_ops as g
 import oracle
 import test_gpu_rowchain as rc
 from vnpu_mi355x import abi
@@ -52,3 +53,37 @@ def test_random_matmul_i8_pairs_small_m(gpu):
         for g_, B, s in zip(got, Bs, ss):
             want = oracle.matmul_i8(A, B, sa, s)
             assert np.array_equal(g_.view(np.uint32), want.view(np.uint32)), (M, K, N0, N1)
+
+
+def test_random_attention_both_devices(gpu, fast_gpu):
+    """Seeded random ATTENTION_F32 calls (reference src/kernels/llm.cpp:442-546):
+    batch, heads, query and key lengths (decode and prefill paths, ragged
+    64-key blocks and 128-row tiles), head sizes 64 and 128 (the tiled
+    kernels) and others (the row-wise kernel), causal offsets, additive masks
+    with -inf runs, explicit and default scales.  The default device must give
+    the reference's bits (the oracle's AVX2-order restatement); the
+    high-throughput device must be within the attention bar."""
+    rng = np.random.default_rng(20261210)
+    for case in range(24):
+        b, h = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+        d = int(rng.choice([64, 128, 128, 64, 32, 80]))
+        sq = int(rng.choice([1, 2, 4])) if rng.integers(3) == 0 else int(rng.integers(5, 300))
+        sk = sq + int(rng.integers(0, 400))
+        causal = int(rng.integers(2))
+        scale = 0.0 if rng.integers(2) else float(rng.uniform(0.02, 0.3))
+        Q = (rng.standard_normal((b, h, sq, d)) * rng.uniform(0.5, 3)).astype(np.float32)
+        K = rng.standard_normal((b, h, sk, d)).astype(np.float32)
+        V = rng.standard_normal((b, h, sk, d)).astype(np.float32)
+        M = None
+        if rng.integers(3) == 0:
+            M = rng.standard_normal((b, h, sq, sk)).astype(np.float32)
+            lo = int(rng.integers(0, sk))
+            M[..., lo:lo + int(rng.integers(1, 80))] = -np.inf
+        what = (case, b, h, sq, sk, d, causal, scale, M is not None)
+        want = oracle.attention_avx2(Q, K, V, M, causal, scale)
+        got = g.attention(gpu, Q, K, V, M, causal, scale)
+        same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+        assert same.all(), what
+        fast = g.attention(fast_gpu, Q, K, V, M, causal, scale)
+        assert oracle.rel_error(fast, want) <= 2e-3, what
+
