@@ -182,10 +182,26 @@ __device__ __forceinline__ float scale_from_max(float maxabs)
     return scale;
 }
 
+// The scalar tail loop `sum += a[i] * b[i]` of the reference's AVX2
+// reductions (rmsnorm_avx2_rows llm.cpp:91, dot_avx2 :342) as its build
+// compiles it: g++ -O3 gives the loop a 4-wide vector epilogue, so with four
+// or more elements left the first four products are rounded (one vector
+// multiply) and added to the sum in order, and the remaining one to three
+// (or all of a shorter tail) are contracted into FMAs.
+__device__ __forceinline__ float tail_dot(const float *a, const float *b, uint32_t n, float sum)
+{
+#pragma clang fp contract(off)
+    uint32_t i = 0;
+    if (n >= 4)
+        for (; i < 4; ++i) sum = sum + a[i] * b[i];
+    for (; i < n; ++i) sum = fmaf(a[i], b[i], sum);
+    return sum;
+}
+
 // dot_avx2 (reference src/kernels/llm.cpp:332-343) over d in [0, D): eight
 // FMA chains c = 0..7 over d = 8i + c, hsum256's pairing
-// ((c0+c4) + (c1+c5)) + ((c2+c6) + (c3+c7)), then the tail d >= D & ~7 as
-// unfused multiply-adds.
+// ((c0+c4) + (c1+c5)) + ((c2+c6) + (c3+c7)), then the tail d >= D & ~7
+// (tail_dot).
 __device__ __forceinline__ float dot_ref(const float *q, const float *k, uint32_t D)
 {
 #pragma clang fp contract(off)
@@ -195,9 +211,8 @@ __device__ __forceinline__ float dot_ref(const float *q, const float *k, uint32_
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc[c] = fmaf(q[i + c], k[i + c], acc[c]);
     }
-    float sum = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
-    for (uint32_t i = D8; i < D; ++i) sum = sum + q[i] * k[i];
-    return sum;
+    const float sum = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+    return tail_dot(q + D8, k + D8, D - D8, sum);
 }
 
 // Wave-wide reductions (wave64).

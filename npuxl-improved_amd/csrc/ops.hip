@@ -47,7 +47,9 @@ __device__ __forceinline__ float block_max(float v, float *red)
 //   * the sum of squares runs as eight FMA chains, chain c over elements c,
 //     c + 8, c + 16, ... in order; the eight sums combine as
 //     ((s0 + s4) + (s1 + s5)) + ((s2 + s6) + (s3 + s7)) (hsum256), and the
-//     cols % 8 tail elements follow one FMA each;
+//     cols % 8 tail elements follow as the reference's build adds them
+//     (dev::tail_dot: four rounded products first when four or more remain,
+//     then FMAs);
 //   * inv = 1 / sqrt(sum / cols + eps), correctly rounded;
 //   * y = (x * w) * inv on the 8-wide part, (x * inv) * w on the tail.
 // A chain is one sequential dependency (cols / 8 FMAs), so eight lanes walk
@@ -109,9 +111,8 @@ __device__ __forceinline__ void chain_sumsq(const float *rowt, uint32_t P, uint3
 // gets the result.  Call after a barrier that follows the chains' writes.
 __device__ __forceinline__ float chain_total(const float *red8, const float *row_tail, uint32_t tail)
 {
-    float sum = ((red8[0] + red8[4]) + (red8[1] + red8[5])) + ((red8[2] + red8[6]) + (red8[3] + red8[7]));
-    for (uint32_t j = 0; j < tail; ++j) sum = fmaf(row_tail[j], row_tail[j], sum);
-    return sum;
+    const float sum = ((red8[0] + red8[4]) + (red8[1] + red8[5])) + ((red8[2] + red8[6]) + (red8[3] + red8[7]));
+    return dev::tail_dot(row_tail, row_tail, tail, sum);
 }
 
 __device__ __forceinline__ float rms_inv(float sum, uint32_t cols, float eps)

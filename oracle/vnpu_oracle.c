@@ -572,6 +572,24 @@ static float vo_hsum8(const float a[8])
     return (s0 + s1) + (s2 + s3);
 }
 
+/* The scalar tail loop `sum += a[i] * b[i]` of the reference's AVX2 reductions
+ * (rmsnorm_avx2_rows llm.cpp:91, dot_avx2 :342) as its build compiles it: g++
+ * -O3 gives the loop a 4-wide vector epilogue, so with four or more elements
+ * left the first four products are rounded as one vector multiply and added to
+ * the sum in order, and the remaining one to three (or all of a shorter tail)
+ * are contracted into FMAs. */
+static float vo_tail_dot(const float *a, const float *b, uint32_t n, float sum)
+{
+    uint32_t i = 0;
+    if (n >= 4)
+        for (; i < 4; ++i) {
+            const float p = a[i] * b[i];
+            sum = sum + p;
+        }
+    for (; i < n; ++i) sum = fmaf(a[i], b[i], sum);
+    return sum;
+}
+
 /* rmsnorm_avx2_rows (llm.cpp:80-108): eight running sums of x*x (FMA) over
  * each 8-wide step, hsum256, then the tail; y = (x*w)*inv over the 8-wide
  * part and (x*inv)*w on the tail. */
@@ -585,8 +603,7 @@ void vo_rmsnorm_avx2(const float *X, const float *W, float *Y, uint32_t rows, ui
         uint32_t j = 0;
         for (; j + 8 <= cols; j += 8)
             for (int l = 0; l < 8; ++l) acc[l] = fmaf(x[j + l], x[j + l], acc[l]);
-        float sum = vo_hsum8(acc);
-        for (; j < cols; ++j) sum = fmaf(x[j], x[j], sum);
+        float sum = vo_tail_dot(x + j, x + j, cols - j, vo_hsum8(acc));
         float inv = 1.0f / sqrtf(sum / (float)cols + eps);
         j = 0;
         for (; j + 8 <= cols; j += 8)
@@ -738,16 +755,14 @@ void vo_add_avx2(const float *A, const float *B, float *Y, uint64_t count, float
 }
 
 /* dot_avx2 (llm.cpp:332-343): eight FMA chains over 8-wide steps, hsum256,
- * then the tail (a separate multiply and add). */
+ * then the tail (vo_tail_dot). */
 static float vo_dot_avx2(const float *a, const float *b, uint32_t n)
 {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t i = 0;
     for (; i + 8 <= n; i += 8)
         for (int l = 0; l < 8; ++l) acc[l] = fmaf(a[i + l], b[i + l], acc[l]);
-    float sum = vo_hsum8(acc);
-    for (; i < n; ++i) sum += a[i] * b[i];   /* the build leaves this tail unfused */
-    return sum;
+    return vo_tail_dot(a + i, b + i, n - i, vo_hsum8(acc));
 }
 
 /* attention_range (llm.cpp:442-546) with its AVX2 helpers: scores by

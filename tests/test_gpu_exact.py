@@ -28,7 +28,7 @@ def bits(a, b):
 
 
 @pytest.mark.parametrize("rows,cols", [(2048, 4096), (8, 11008), (3, 12288), (3, 4099), (2, 20000), (5, 33),
-                                       (4, 4100), (1, 7)])
+                                       (4, 4100), (1, 7), (256, 7), (256, 13), (128, 12), (64, 4103)])
 def test_rmsnorm_bit_exact(gpu, rows, cols):
     X = (RNG.standard_normal((rows, cols)) * 2).astype(np.float32)
     W = (1.0 + 0.1 * RNG.standard_normal(cols)).astype(np.float32)
@@ -152,6 +152,7 @@ def test_row_chain_add_norm_quant_bit_exact(gpu):
     (1, 4, 256, 256, 128, 1, None),        # prefill tiles
     (1, 2, 300, 700, 64, 1, "inf"), (2, 2, 3, 500, 128, 0, "normal"), (1, 2, 17, 40, 64, 1, "row"),
     (1, 2, 37, 70, 20, 0, "normal"),       # other head sizes: the row-wise kernel
+    (1, 2, 9, 40, 13, 1, None), (2, 2, 3, 50, 23, 0, None), (1, 2, 6, 30, 6, 1, None),
     (1, 1, 5, 64, 96, 1, None), (2, 3, 1, 1, 128, 0, None)])
 def test_attention_reference_order_bit_exact(exact_gpu, b, h, sq, sk, d, causal, mask):
     Q = RNG.standard_normal((b, h, sq, d)).astype(np.float32)

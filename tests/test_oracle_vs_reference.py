@@ -235,6 +235,30 @@ def test_rmsnorm_avx2_order_bit_exact(ref, rows, cols):
     assert _bits(g.unary_rows(ref, abi.OP_RMSNORM_F32, X, eps=0.0), oracle.rmsnorm_avx2(X, None, 1e-5))
 
 
+@pytest.mark.parametrize("cols", [1, 2, 3, 4, 5, 6, 7, 9, 11, 12, 13, 15, 20, 31, 4100, 4103])
+def test_rmsnorm_avx2_tail_forms(ref, cols):
+    """The sum of squares' scalar tail as the reference's build compiles it:
+    with four or more tail elements the first four products are rounded (a
+    4-wide vector epilogue) and added in order, the rest fused; a shorter
+    tail is all fused.  Short rows make every rounding visible (many rows of
+    7 differ between the all-fused form and the reference)."""
+    X = (RNG.standard_normal((256 if cols < 100 else 16, cols)) * 2).astype(np.float32)
+    W = (1.0 + 0.1 * RNG.standard_normal(cols)).astype(np.float32)
+    assert _bits(g.unary_rows(ref, abi.OP_RMSNORM_F32, X, W=W, eps=1e-5), oracle.rmsnorm_avx2(X, W, 1e-5))
+    assert _bits(g.unary_rows(ref, abi.OP_RMSNORM_F32, X, eps=0.0), oracle.rmsnorm_avx2(X, None, 1e-5))
+
+
+@pytest.mark.parametrize("d", [3, 5, 6, 7, 12, 13, 15, 21, 23])
+def test_attention_avx2_dot_tail_forms(ref, d):
+    """dot_avx2's scalar tail, compiled like the sum of squares above (head
+    sizes that leave 1..7 elements after the 8-wide steps)."""
+    Q = (RNG.standard_normal((2, 2, 9, d)) * 2).astype(np.float32)
+    K = RNG.standard_normal((2, 2, 40, d)).astype(np.float32)
+    V = RNG.standard_normal((2, 2, 40, d)).astype(np.float32)
+    got = g.attention(ref, Q, K, V, None, 1)
+    assert _bits(got, oracle.attention_avx2(Q, K, V, None, 1))
+
+
 @pytest.mark.parametrize("n", [3, 8, 1001, 4103, 16384, 2048 * 11008 // 32])
 def test_elementwise_avx2_order_bit_exact(ref, n):
     """SWIGLU, GELU, ADD and MUL: 8-wide steps, then the last n % 8 elements in
