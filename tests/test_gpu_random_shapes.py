@@ -87,3 +87,40 @@ def test_random_attention_both_devices(gpu, fast_gpu):
         fast = g.attention(fast_gpu, Q, K, V, M, causal, scale)
         assert oracle.rel_error(fast, want) <= 2e-3, what
 
+
+
+def test_random_reference_order_small_shapes(gpu):
+    """Seeded random short rows and odd head sizes, where every rounding of
+    the reference's AVX2 build shows: RMSNORM (reduction tails of any length),
+    SWIGLU/MUL/ADD/GELU (scalar tails) and ATTENTION with head sizes 1..39
+    (the row-wise kernel's dot tails), each bit-exact with the oracle's
+    AVX2-order restatement."""
+    rng = np.random.default_rng(20261211)
+
+    def same(a, b):
+        return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+    for _ in range(40):
+        rows, cols = int(rng.integers(1, 300)), int(rng.integers(1, 80))
+        X = (rng.standard_normal((rows, cols)) * rng.uniform(0.1, 10)).astype(np.float32)
+        W = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+        assert same(g.unary_rows(gpu, abi.OP_RMSNORM_F32, X, W=W, eps=1e-5), oracle.rmsnorm_avx2(X, W, 1e-5)), \
+            (rows, cols)
+        n = int(rng.integers(1, 200))
+        a = (rng.standard_normal(n) * rng.uniform(0.1, 30)).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        al, be = float(rng.choice([0.0, 1.0, -1.5])), float(rng.choice([0.0, 2.5]))
+        assert same(g.elementwise(gpu, abi.OP_SWIGLU_F32, a, b, alpha=al), oracle.swiglu_avx2(a, b, al or 1.0)), n
+        assert same(g.elementwise(gpu, abi.OP_MUL_F32, a, b, al, be), oracle.mul_avx2(a, b, al or 1.0, be)), n
+        assert same(g.elementwise(gpu, abi.OP_ADD_F32, a, b, al, be), oracle.add_avx2(a, b, al, be)), n
+        assert same(g.elementwise(gpu, abi.OP_GELU_F32, a), oracle.gelu_avx2(a)), n
+    for _ in range(24):
+        h, d = int(rng.integers(1, 3)), int(rng.integers(1, 40))
+        sq = int(rng.integers(1, 40))
+        sk = sq + int(rng.integers(0, 140))
+        causal = int(rng.integers(2))
+        Q = (rng.standard_normal((1, h, sq, d)) * rng.uniform(0.5, 3)).astype(np.float32)
+        K = rng.standard_normal((1, h, sk, d)).astype(np.float32)
+        V = rng.standard_normal((1, h, sk, d)).astype(np.float32)
+        assert same(g.attention(gpu, Q, K, V, None, causal), oracle.attention_avx2(Q, K, V, None, causal)), \
+            (h, sq, sk, d, causal)

@@ -353,3 +353,42 @@ def test_softmax_avx2_order_bit_exact(ref, rows, cols, temp):
     assert _bits(got, want)
     if rows > 1 and cols % 8 == 0:
         assert want[1, 3] > 0.0   # exp(-80) of the clamp, as the reference
+
+
+def test_avx2_orders_random_sweep(ref):
+    """Seeded random small shapes through every AVX2-order restatement at
+    once (short rows, where every rounding of the reference's build shows):
+    RMSNORM (eps defaults), SOFTMAX (temperatures), SWIGLU/MUL/ADD/GELU
+    (alpha/beta defaults) and ATTENTION (head sizes 1..39 with any tail,
+    causal offsets, masks, explicit scales)."""
+    rng = np.random.default_rng(777)
+    for _ in range(120):
+        rows, cols = int(rng.integers(1, 6)), int(rng.integers(1, 80))
+        X = (rng.standard_normal((rows, cols)) * rng.uniform(0.1, 10)).astype(np.float32)
+        W = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+        eps = float(rng.choice([0.0, 1e-5, 1e-6, 0.1]))
+        assert _bits(g.unary_rows(ref, abi.OP_RMSNORM_F32, X, W=W, eps=eps),
+                     oracle.rmsnorm_avx2(X, W, eps if eps > 0 else 1e-5)), (rows, cols, eps)
+        t = float(rng.choice([0.0, 0.5, 1.0, 2.0, 0.7]))
+        assert _bits(g.unary_rows(ref, abi.OP_SOFTMAX_F32, X, temperature=t),
+                     oracle.softmax_avx2(X, t if t > 0 else 1.0)), (rows, cols, t)
+    for _ in range(120):
+        n = int(rng.integers(1, 200))
+        a = (rng.standard_normal(n) * rng.uniform(0.1, 30)).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        al, be = float(rng.choice([0.0, 1.0, -1.5, 0.3])), float(rng.choice([0.0, 1.0, 2.5, -0.7]))
+        assert _bits(g.elementwise(ref, abi.OP_SWIGLU_F32, a, b, alpha=al), oracle.swiglu_avx2(a, b, al or 1.0)), n
+        assert _bits(g.elementwise(ref, abi.OP_MUL_F32, a, b, al, be), oracle.mul_avx2(a, b, al or 1.0, be)), n
+        assert _bits(g.elementwise(ref, abi.OP_ADD_F32, a, b, al, be), oracle.add_avx2(a, b, al, be)), n
+        assert _bits(g.elementwise(ref, abi.OP_GELU_F32, a), oracle.gelu_avx2(a)), n
+    for _ in range(60):
+        h, d = int(rng.integers(1, 3)), int(rng.integers(1, 40))
+        sq = int(rng.integers(1, 40))
+        sk = sq + int(rng.integers(0, 140))
+        causal, scale = int(rng.integers(2)), (0.0 if rng.integers(2) else float(rng.uniform(0.05, 0.5)))
+        Q = (rng.standard_normal((1, h, sq, d)) * rng.uniform(0.5, 3)).astype(np.float32)
+        K = rng.standard_normal((1, h, sk, d)).astype(np.float32)
+        V = rng.standard_normal((1, h, sk, d)).astype(np.float32)
+        M = rng.standard_normal((1, h, sq, sk)).astype(np.float32) if rng.integers(3) == 0 else None
+        assert _bits(g.attention(ref, Q, K, V, M, causal, scale),
+                     oracle.attention_avx2(Q, K, V, M, causal, scale)), (h, sq, sk, d, causal, scale)
