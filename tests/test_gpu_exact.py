@@ -28,7 +28,8 @@ def bits(a, b):
 
 
 @pytest.mark.parametrize("rows,cols", [(2048, 4096), (8, 11008), (3, 12288), (3, 4099), (2, 20000), (5, 33),
-                                       (4, 4100), (1, 7), (256, 7), (256, 13), (128, 12), (64, 4103)])
+                                       (4, 4100), (1, 7), (256, 7), (256, 13), (128, 12), (64, 4103),
+                                       (3, 20005), (2, 12295)])
 def test_rmsnorm_bit_exact(gpu, rows, cols):
     X = (RNG.standard_normal((rows, cols)) * 2).astype(np.float32)
     W = (1.0 + 0.1 * RNG.standard_normal(cols)).astype(np.float32)
