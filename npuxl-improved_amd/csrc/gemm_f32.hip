@@ -673,8 +673,13 @@ __device__ __forceinline__ void put4(float *d, const float4 v)
     d[3] = v.w;
 }
 
+// Workgroups from `full` on split the remaining tiles over K: two per tile,
+// the first taking k stages [0, ks_half), the second [ks_half, KT); each
+// writes its raw sums as a 256 x 128 row-major tile into part (tile pair i
+// at part + 2i * 256 * 128) and gemm_f32_tail_reduce finishes them.  Used
+// when the last round of tiles would leave at least half the CUs idle.
 template <bool TB>
-__global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p)
+__global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p, uint32_t full, uint32_t ks_half, float *part)
 {
     using ws::kSlots;
     using ws::kSlotBytes;
@@ -690,10 +695,15 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t tiles_m = (p.M + TM - 1) / TM, total = tiles_m * ((p.N + TN - 1) / TN);
-    uint32_t g = blockIdx.x;
+    const bool split = blockIdx.x >= full;
+    const uint32_t half = split ? (blockIdx.x - full) & 1u : 0u;
+    uint32_t g = split ? full + ((blockIdx.x - full) >> 1) : blockIdx.x;
     if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
     const uint32_t m0 = (g % tiles_m) * TM, n0 = (g / tiles_m) * TN;
-    const uint32_t KT = (p.K + WBK - 1) / WBK;
+    const uint32_t KTall = (p.K + WBK - 1) / WBK;
+    // This workgroup's k stages: [ks0, ks0 + KT)
+    const uint32_t ks0 = split && half ? ks_half : 0u;
+    const uint32_t KT = split ? (half ? KTall - ks_half : ks_half) : KTall;
     if (tid < 2 * 4 * kSlots) flags[tid] = 0;
     __syncthreads();
 
@@ -731,7 +741,7 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p)
             }
         }
         auto load = [&](WsSlice &x, uint32_t s) {
-            const uint32_t k0 = min(s, KT - 1) * WBK;
+            const uint32_t k0 = (ks0 + min(s, KT - 1)) * WBK;
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -789,7 +799,7 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p)
         const bool edge = m0 + TM > p.M || n0 + TN > p.N;
         auto put = [&](const WsSlice &x, uint32_t s) {
             const uint32_t slot = s % kSlots;
-            const uint32_t k0 = s * WBK;
+            const uint32_t k0 = (ks0 + s) * WBK;
             if (s >= kSlots) ws_wait(p, cons + 4 * slot, s - kSlots + 1);
             if (edge || k0 + WBK > p.K) {
                 WsSlice y;
@@ -890,12 +900,52 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p)
         mma(f1);
     }
     // Rows wm*128 + 64q .. +63 of the block: the split-bf16 kernel's register
-    // epilogue, twice.
+    // epilogue, twice; a K-split workgroup stores its raw sums (alpha 1, no
+    // bias, beta 0, no activation) into its 256 x 128 partial tile instead.
+    if (split) {
+        F32Gemm t = p;
+        t.C = part + static_cast<uint64_t>((blockIdx.x - full) >> 1) * 2 * TM * TN + half * TM * TN;
+        t.M = TM;
+        t.N = TN;
+        t.ldc = TN;
+        t.alpha = 1.0f;
+        t.beta = 0.0f;
+        t.bias = nullptr;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const v16f pq[2][2] = {{acc[2 * q][0], acc[2 * q][1]}, {acc[2 * q + 1][0], acc[2 * q + 1][1]}};
+            x3_store_rows<0, 2>(t, pq, wm * 128 + 64 * q, wn * 64 + col, h);
+        }
+        return;
+    }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-        const v16f part[2][2] = {{acc[2 * q][0], acc[2 * q][1]}, {acc[2 * q + 1][0], acc[2 * q + 1][1]}};
-        x3_store_rows_epi<2>(p, part, m0 + wm * 128 + 64 * q, n0 + wn * 64 + col, h);
+        const v16f pq[2][2] = {{acc[2 * q][0], acc[2 * q][1]}, {acc[2 * q + 1][0], acc[2 * q + 1][1]}};
+        x3_store_rows_epi<2>(p, pq, m0 + wm * 128 + 64 * q, n0 + wn * 64 + col, h);
     }
+}
+
+// The tiles gemm_f32_ws split over K: C = epi(alpha (s0 + s1) + bias +
+// beta C) for tile pair blockIdx.y, 1024 elements (four per thread) per
+// workgroup.
+__global__ __launch_bounds__(kThreads) void gemm_f32_tail_reduce(F32Gemm p, const float *part, uint32_t full)
+{
+    using ws::TM;
+    using ws::TN;
+    const uint32_t tiles_m = (p.M + TM - 1) / TM, total = tiles_m * ((p.N + TN - 1) / TN);
+    uint32_t g = full + blockIdx.y;
+    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    const uint32_t m0 = (g % tiles_m) * TM, n0 = (g / tiles_m) * TN;
+    const uint32_t e = (blockIdx.x * kThreads + threadIdx.x) * 4;   // element of the 256 x 128 tile
+    const float *p0 = part + static_cast<uint64_t>(blockIdx.y) * 2 * TM * TN;
+    const float4 a = *reinterpret_cast<const float4 *>(p0 + e);
+    const float4 b = *reinterpret_cast<const float4 *>(p0 + TM * TN + e);
+    const uint32_t m = m0 + e / TN, n = n0 + e % TN;
+    if (m >= p.M) return;
+    const float s[4] = {a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (n + i < p.N) store_out(p, m, n + i, s[i], false);
 }
 
 // ---------------------------------------------------------------------------
@@ -1354,9 +1404,29 @@ static void launch_x3(hipStream_t s, const F32Gemm &p, const X3Plan &x, float *w
     else gemm_f32_x3<true, true, WM><<<grid, block, lds, s>>>(p, x.kps, out);
 }
 
+// Tiles of the warp-specialised kernel that run split over K: when the last
+// round of 256 x 128 tiles would fill at most half the CUs, each of its tiles
+// runs as two workgroups over half of K each (the round then takes half as
+// long), provided K has at least 16 stages.  Returns the number of such
+// tiles (0: none); *full receives the number of whole tiles before them.
+static uint32_t ws_tail_tiles(const F32Gemm &p, uint32_t *full)
+{
+    const uint32_t total = ((p.M + ws::TM - 1) / ws::TM) * ((p.N + ws::TN - 1) / ws::TN);
+    const uint32_t cus = std::max<uint32_t>(1, cu_count());
+    const uint32_t rest = total % cus;
+    *full = total;
+    if (total < cus || rest == 0 || rest > cus / 2 || (p.K + ws::BK - 1) / ws::BK < 16) return 0;
+    *full = total - rest;
+    return rest;
+}
+
 size_t gemm_f32_ws_bytes(const F32Gemm &p)
 {
     const X3Plan x = x3_plan(p);
+    if (x.ws) {
+        uint32_t full;
+        return static_cast<size_t>(ws_tail_tiles(p, &full)) * 2 * ws::TM * ws::TN * sizeof(float);
+    }
     const uint32_t splits = x.x3 ? x.splits : gemm_f32_splits(p);
     return splits > 1 ? static_cast<size_t>(splits) * p.M * p.N * sizeof(float) : 0;
 }
@@ -1378,9 +1448,15 @@ void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
                                             hipFuncAttributeMaxDynamicSharedMemorySize, ws::kLds) == hipSuccess &&
                         hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_ws<true>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, ws::kLds) == hipSuccess;
-        const dim3 grid(((p.N + ws::TN - 1) / ws::TN) * ((p.M + ws::TM - 1) / ws::TM));
-        if (p.trans_b) gemm_f32_ws<true><<<grid, 512, ws::kLds, s>>>(p);
-        else gemm_f32_ws<false><<<grid, 512, ws::kLds, s>>>(p);
+        uint32_t full;
+        const uint32_t tail = ws ? ws_tail_tiles(p, &full) : 0;
+        if (!tail) full = ((p.N + ws::TN - 1) / ws::TN) * ((p.M + ws::TM - 1) / ws::TM);
+        const uint32_t ks_half = (p.K + ws::BK - 1) / ws::BK / 2;
+        const dim3 grid(full + 2 * tail);
+        if (p.trans_b) gemm_f32_ws<true><<<grid, 512, ws::kLds, s>>>(p, full, ks_half, ws);
+        else gemm_f32_ws<false><<<grid, 512, ws::kLds, s>>>(p, full, ks_half, ws);
+        if (tail)
+            gemm_f32_tail_reduce<<<dim3(ws::TM * ws::TN / (4 * kThreads), tail), kThreads, 0, s>>>(p, ws, full);
         return;
     }
     if (x.x3) {

@@ -147,6 +147,29 @@ def test_config3_f32_prefill_full(gpu, N):
     assert oracle.rel_error(got, want) <= 1e-4
 
 
+@pytest.mark.parametrize("M,K,N", [(2000, 1000, 4100), (1700, 1000, 4700), (2048, 520, 14336)])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_f32_last_round_k_split(gpu, M, K, N, tb):
+    """Grids of 256 x 128 tiles whose last round fills at most half of the
+    256 CUs (264, 259 and 896 tiles): those tiles run as two workgroups over
+    half of K each, then a second pass adds the halves and applies alpha,
+    bias, beta and the epilogue.  Ragged M / N / K edges land in the split
+    tiles; 259 tiles also skip the XCD remap (not a multiple of 8)."""
+    a = RNG.standard_normal((M, K), dtype=np.float32)
+    b = (RNG.standard_normal((N, K) if tb else (K, N), dtype=np.float32) * 0.05).astype(np.float32)
+    bias = RNG.standard_normal(N, dtype=np.float32) * 0.1
+    c0 = RNG.standard_normal((M, N), dtype=np.float32)
+    ba, bb, bbias, bc = gpu.upload(a), gpu.upload(b), gpu.upload(bias), gpu.upload(c0)
+    gpu.run(abi.OP_MATMUL_F32, A=ba, B=bb, bias=bbias, C=bc, M=M, K=K, N=N, trans_b=tb, alpha=0.75,
+            beta=0.5, epilogue=abi.EPI_GELU_TANH)
+    got = gpu.download(bc, np.float32, (M, N))
+    for x in (ba, bb, bbias, bc):
+        gpu.free(x)
+    want = oracle.matmul_f32_blas(a, b, c0, bias, 0, tb, 0.75, 0.5, abi.EPI_GELU_TANH)
+    assert np.isfinite(got).all()
+    assert oracle.rel_error(got, want) <= 1e-4
+
+
 def test_config5_cull_int8_4096_full(gpu):
     """Config 5: 4096^3 int8 with half of the 64 x 64 weight tiles zeroed by
     the seeded Bernoulli mask (the bench's tensors), bit-exact."""
