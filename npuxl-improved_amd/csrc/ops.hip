@@ -14,6 +14,8 @@ namespace k {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kRawBuf = 0x00020000;   // raw buffer resource word 3: 32-bit data, no swizzle
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float block_sum(float v, float *red)
 {
@@ -80,29 +82,55 @@ __device__ __forceinline__ void chain_put4(float *rowt, uint32_t P, uint32_t e0,
 }
 
 // Eight chain lanes accumulate len elements each (chain c at rowt + c * P)
-// into acc in element order; the next four are in flight while four are
-// summed.  Call with every thread, between barriers.
+// into acc in element order.  A chain is one dependent FMA after another, so
+// the LDS reads must run ahead of it: the next kChainGroup float4s are
+// issued before the current ones are summed, and a scheduling barrier keeps
+// the compiler from sinking those reads below the FMAs (it did, and each
+// float4 then waited out a whole LDS round trip: about 16 cycles per
+// element).  Call with every thread, between barriers.
+constexpr uint32_t kChainGroup = 4;
 __device__ __forceinline__ void chain_sumsq(const float *rowt, uint32_t P, uint32_t len, float &acc)
 {
     const uint32_t c = threadIdx.x;
     if (c >= 8) return;
     const float *r = rowt + c * P;
-    const uint32_t n4 = len / 4;
-    if (n4) {
-        float4 cur = *reinterpret_cast<const float4 *>(r);
-        for (uint32_t i = 1; i < n4; ++i) {
-            const float4 nxt = *reinterpret_cast<const float4 *>(r + 4 * i);
-            acc = fmaf(cur.x, cur.x, acc);
-            acc = fmaf(cur.y, cur.y, acc);
-            acc = fmaf(cur.z, cur.z, acc);
-            acc = fmaf(cur.w, cur.w, acc);
-            cur = nxt;
+    const float4 *r4 = reinterpret_cast<const float4 *>(r);
+    const uint32_t n4 = len / 4, groups = n4 / kChainGroup;
+    auto sum4 = [&](const float4 &v) {
+        acc = fmaf(v.x, v.x, acc);
+        acc = fmaf(v.y, v.y, acc);
+        acc = fmaf(v.z, v.z, acc);
+        acc = fmaf(v.w, v.w, acc);
+    };
+    auto load = [&](float4 (&x)[kChainGroup], uint32_t g) {
+#pragma unroll
+        for (uint32_t u = 0; u < kChainGroup; ++u) x[u] = r4[g * kChainGroup + u];
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto sum = [&](const float4 (&x)[kChainGroup]) {
+#pragma unroll
+        for (uint32_t u = 0; u < kChainGroup; ++u) sum4(x[u]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    if (groups) {
+        float4 x0[kChainGroup], x1[kChainGroup];   // ping-pong: group g + 1 loads while g is summed
+        load(x0, 0);
+        uint32_t g = 1;
+        for (; g + 1 < groups; g += 2) {
+            load(x1, g);
+            sum(x0);
+            load(x0, g + 1);
+            sum(x1);
         }
-        acc = fmaf(cur.x, cur.x, acc);
-        acc = fmaf(cur.y, cur.y, acc);
-        acc = fmaf(cur.z, cur.z, acc);
-        acc = fmaf(cur.w, cur.w, acc);
+        if (g < groups) {
+            load(x1, g);
+            sum(x0);
+            sum(x1);
+        } else {
+            sum(x0);
+        }
     }
+    for (uint32_t i = groups * kChainGroup; i < n4; ++i) sum4(r4[i]);
     for (uint32_t i = 4 * n4; i < len; ++i) acc = fmaf(r[i], r[i], acc);
 }
 
@@ -172,10 +200,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_reg_kernel(const float *__re
     const float4 *w = reinterpret_cast<const float4 *>(W);
     const uint32_t n4 = cols >> 2, cols8 = cols & ~7u, P = chain_pitch(cols8 / 8);
     float *rowt = reinterpret_cast<float *>(row4), *tail = rowt + 8 * P;
-    float4 v[VPT];
+    float4 v[VPT], g[VPT];   // the weights load while the sum runs
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * kThreads;
+        g[i] = (W && j < n4) ? w[j] : make_float4(1.f, 1.f, 1.f, 1.f);
         v[i] = j < n4 ? x[j] : make_float4(0.f, 0.f, 0.f, 0.f);
         if (j < n4) {
             if (4 * j < cols8) chain_put4(rowt, P, 4 * j, v[i]);
@@ -192,10 +221,9 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_reg_kernel(const float *__re
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * kThreads;
         if (j >= n4) continue;
-        const float4 g = W ? w[j] : make_float4(1.f, 1.f, 1.f, 1.f);
         const uint32_t e = 4 * j;
-        y[j] = make_float4(rms_scale(v[i].x, g.x, inv, e, cols8), rms_scale(v[i].y, g.y, inv, e + 1, cols8),
-                           rms_scale(v[i].z, g.z, inv, e + 2, cols8), rms_scale(v[i].w, g.w, inv, e + 3, cols8));
+        y[j] = make_float4(rms_scale(v[i].x, g[i].x, inv, e, cols8), rms_scale(v[i].y, g[i].y, inv, e + 1, cols8),
+                           rms_scale(v[i].z, g[i].z, inv, e + 2, cols8), rms_scale(v[i].w, g[i].w, inv, e + 3, cols8));
     }
 }
 
@@ -592,40 +620,72 @@ __global__ __launch_bounds__(NT) void row_chain_kernel(RowChain p)
 {
     static_assert(!NORM || NT == kThreads, "RMSNORM as rmsnorm_reg_kernel computes it");
     __shared__ float red[NT / 64];
-    const uint32_t n4 = p.cols >> 2;
+    const uint32_t n4 = p.cols >> 2, row_bytes = p.cols * 4u;
     const uint64_t off = static_cast<uint64_t>(blockIdx.x) * n4;
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 v[VPT];
-    if (PRE == kChainNone) {
+    // Every global access goes through a raw buffer over this row, so float4
+    // slots past the row need no branch (reads return zero, writes are
+    // dropped).  With a branch around each load the compiler could not tell
+    // which loads were still in flight and waited for all memory operations,
+    // stores included, before later uses of those registers: a memory round
+    // trip on the row's critical path after each store.
+    const uint32_t lane_off = threadIdx.x * 16u;
+    auto rsrc = [&](const void *base, uint32_t bytes) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), kRawBuf);
+    };
+    auto ld4 = [&](__amdgpu_buffer_rsrc_t r, int i) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off + i * NT * 16u, 0, 0));
+    };
+    auto st4 = [&](__amdgpu_buffer_rsrc_t r, int i, float4 x) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32, x), r, lane_off + i * NT * 16u, 0, 0);
+    };
+    // The RMSNORM weights are read up front: loaded after the sum, each load
+    // would wait behind the previous element's Nrm store (the buffers may
+    // alias, so the compiler keeps them in order).
+    float4 g[NORM ? VPT : 1];
+    if (NORM) {
+        const bool has_w = p.W != nullptr;
+        const auto rw = rsrc(p.W, has_w ? row_bytes : 0u);
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
-            const uint32_t j = threadIdx.x + i * NT;
-            v[i] = j < n4 ? reinterpret_cast<const float4 *>(p.A)[off + j] : zero;
+            const float4 x = ld4(rw, i);
+            g[i] = has_w ? x : make_float4(1.f, 1.f, 1.f, 1.f);
         }
-    } else {
+    }
+    const auto ra = rsrc(p.A + off * 4, row_bytes);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) v[i] = ld4(ra, i);
+    if (PRE != kChainNone) {
         float4 b[VPT];
+        const auto rb = rsrc(p.B + off * 4, row_bytes);
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const uint32_t j = threadIdx.x + i * NT;
-            v[i] = j < n4 ? reinterpret_cast<const float4 *>(p.A)[off + j] : zero;
-            b[i] = j < n4 ? reinterpret_cast<const float4 *>(p.B)[off + j] : zero;
-        }
+        for (int i = 0; i < VPT; ++i) b[i] = ld4(rb, i);
         constexpr int OP = PRE == kChainAdd ? EW_ADD : EW_SWIGLU;
         // the elementwise command spans all rows: its ranges and tails are
         // those of rows * cols elements
         const EwTail tl = ew_tail(static_cast<uint64_t>(p.rows) * p.cols, p.grain);
+        const auto ry = rsrc(p.Y + off * 4, row_bytes);
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const uint32_t j = threadIdx.x + i * NT;
-            if (j >= n4) continue;
             const uint32_t t = OP == EW_ADD ? 0u : tl.mask4(4 * (off + j));   // ADD: tail = body
             v[i] = make_float4(ew<OP>(v[i].x, b[i].x, p.alpha, p.beta, t & 1),
                                ew<OP>(v[i].y, b[i].y, p.alpha, p.beta, t & 2),
                                ew<OP>(v[i].z, b[i].z, p.alpha, p.beta, t & 4),
                                ew<OP>(v[i].w, b[i].w, p.alpha, p.beta, t & 8));
-            reinterpret_cast<float4 *>(p.Y)[off + j] = v[i];
+            // slots past the row: zero in, so the max below is unchanged
+            if (j >= n4) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            st4(ry, i, v[i]);
         }
     }
+    auto local_absmax = [](const float4 (&x)[VPT]) {
+        float r = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+            r = fmaxf(r, fmaxf(fmaxf(fabsf(x[i].x), fabsf(x[i].y)), fmaxf(fabsf(x[i].z), fabsf(x[i].w))));
+        return r;
+    };
+    float m = 0.0f;   // this thread's max |v| for the quantize stage
     if (NORM) {
         // rmsnorm_reg_kernel's arithmetic (the reference's AVX2 order)
         extern __shared__ float4 row4[];   // chain_floats(cols) floats
@@ -645,33 +705,35 @@ __global__ __launch_bounds__(NT) void row_chain_kernel(RowChain p)
         if (threadIdx.x < 8) red8[threadIdx.x] = acc;
         __syncthreads();
         const float inv = rms_inv(chain_total(red8, tail, p.cols - cols8), p.cols, p.eps);
-        const float4 *w = reinterpret_cast<const float4 *>(p.W);
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const uint32_t j = threadIdx.x + i * NT;
             if (j >= n4) continue;
-            const float4 g = w ? w[j] : make_float4(1.f, 1.f, 1.f, 1.f);
             const uint32_t e = 4 * j;
-            v[i] = make_float4(rms_scale(v[i].x, g.x, inv, e, cols8), rms_scale(v[i].y, g.y, inv, e + 1, cols8),
-                               rms_scale(v[i].z, g.z, inv, e + 2, cols8), rms_scale(v[i].w, g.w, inv, e + 3, cols8));
-            reinterpret_cast<float4 *>(p.Nrm)[off + j] = v[i];
+            v[i] = make_float4(rms_scale(v[i].x, g[i].x, inv, e, cols8), rms_scale(v[i].y, g[i].y, inv, e + 1, cols8),
+                               rms_scale(v[i].z, g[i].z, inv, e + 2, cols8),
+                               rms_scale(v[i].w, g[i].w, inv, e + 3, cols8));
         }
+        // The quantize stage's max is taken before the Nrm stores: the
+        // compiler waits for every outstanding memory operation (stores
+        // included) before the first use of these registers after them.
+        if (QUANT) m = local_absmax(v);
+        const auto rn = rsrc(p.Nrm + off * 4, row_bytes);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) st4(rn, i, v[i]);
     }
     if (QUANT) {
-        float m = 0.0f;
-#pragma unroll
-        for (int i = 0; i < VPT; ++i)
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        if (!NORM) m = local_absmax(v);
         const float scale = dev::scale_from_max(block_max_n<NT>(m, red));
         const float inv = __fdiv_rn(1.0f, scale);
         if (threadIdx.x == 0) p.scales[blockIdx.x] = scale;
-        char4 *out = reinterpret_cast<char4 *>(p.Q) + off;
+        const auto rq = rsrc(p.Q + off * 4, p.cols);
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
-            const uint32_t j = threadIdx.x + i * NT;
-            if (j < n4)
-                out[j] = make_char4(dev::q8(v[i].x, inv), dev::q8(v[i].y, inv), dev::q8(v[i].z, inv),
-                                    dev::q8(v[i].w, inv));
+            const char4 q = make_char4(dev::q8(v[i].x, inv), dev::q8(v[i].y, inv), dev::q8(v[i].z, inv),
+                                       dev::q8(v[i].w, inv));
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, q), rq,
+                                                  threadIdx.x * 4u + i * NT * 4u, 0, 0);
         }
     }
 }
