@@ -385,16 +385,14 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ Q, f
 
 // Half-rotation layout with head_dim % 8 == 0 and 16-byte aligned rows: one
 // thread rotates pairs j..j+3 with one float4 from each half of the row.
-__device__ __forceinline__ void rotate4(float *row, uint32_t j4, uint32_t half4, const float (&c)[4],
-                                        const float (&s)[4])
+__device__ __forceinline__ void rotate4(const float4 a, const float4 b, const float (&c)[4], const float (&s)[4],
+                                        float4 &lo, float4 &hi)
 {
 #pragma clang fp contract(off)
-    float4 *x = reinterpret_cast<float4 *>(row);
-    const float4 a = x[j4], b = x[half4 + j4];
-    x[j4] = make_float4(a.x * c[0] - b.x * s[0], a.y * c[1] - b.y * s[1], a.z * c[2] - b.z * s[2],
-                        a.w * c[3] - b.w * s[3]);
-    x[half4 + j4] = make_float4(a.x * s[0] + b.x * c[0], a.y * s[1] + b.y * c[1], a.z * s[2] + b.z * c[2],
-                                a.w * s[3] + b.w * c[3]);
+    lo = make_float4(a.x * c[0] - b.x * s[0], a.y * c[1] - b.y * s[1], a.z * c[2] - b.z * s[2],
+                     a.w * c[3] - b.w * s[3]);
+    hi = make_float4(a.x * s[0] + b.x * c[0], a.y * s[1] + b.y * c[1], a.z * s[2] + b.z * c[2],
+                     a.w * s[3] + b.w * c[3]);
 }
 
 __global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ Q, float *__restrict__ K,
@@ -414,11 +412,37 @@ __global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ 
     const uint32_t t = static_cast<uint32_t>(tok % seq);
     const uint64_t bh = tok / seq;
     const int32_t p = positions ? positions[t] : static_cast<int32_t>(t + offset);
+    // Q's and K's pairs load before anything is stored, through raw buffers
+    // over the row (an empty range when the row is absent: zero in, writes
+    // dropped), so no branch sits between the loads and the stores and the
+    // K loads do not wait behind the Q stores.
+    const bool has_q = Q && t < q_seq, has_k = K && t < k_seq;
+    const uint32_t row_bytes = head_dim * 4u;
+    float *qrow = has_q ? Q + (bh * q_seq + t) * head_dim : Q, *krow = has_k ? K + (bh * k_seq + t) * head_dim : K;
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc(qrow, 0, static_cast<int>(has_q ? row_bytes : 0u), kRawBuf);
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc(krow, 0, static_cast<int>(has_k ? row_bytes : 0u), kRawBuf);
+    const uint32_t o0 = j4 * 16u, o1 = (half4 + j4) * 16u;
+    auto ld = [](__amdgpu_buffer_rsrc_t r, uint32_t o) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
+    };
+    const float4 qa = ld(rq, o0), qb = ld(rq, o1), ka = ld(rk, o0), kb = ld(rk, o1);
     float c[4], s[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) rope_cos_sin(p, 4 * j4 + e, head_dim / 2, scaling, inv_freq, cs, cs_rows, c[e], s[e]);
-    if (Q && t < q_seq) rotate4(Q + (bh * q_seq + t) * head_dim, j4, half4, c, s);
-    if (K && t < k_seq) rotate4(K + (bh * k_seq + t) * head_dim, j4, half4, c, s);
+    auto st = [](__amdgpu_buffer_rsrc_t r, uint32_t o, float4 x) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32, x), r, o, 0, 0);
+    };
+    float4 lo, hi;
+    rotate4(qa, qb, c, s, lo, hi);
+    st(rq, o0, lo);
+    st(rq, o1, hi);
+    // Q and K the same row: K is rotated again, from Q's result, as in
+    // command order
+    const bool same = has_q && qrow == krow;
+    const float4 ka2 = same ? lo : ka, kb2 = same ? hi : kb;
+    rotate4(ka2, kb2, c, s, lo, hi);
+    st(rk, o0, lo);
+    st(rk, o1, hi);
 }
 
 enum EwOp { EW_SWIGLU = 0, EW_ADD = 1, EW_MUL = 2, EW_GELU = 3 };

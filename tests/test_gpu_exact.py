@@ -109,6 +109,23 @@ def test_rope_bit_exact(gpu, interleaved, shape_q, shape_k, offset):
         assert oracle.rel_error(gq, oq) <= 1e-4 and oracle.rel_error(gk, ok) <= 1e-4
 
 
+@pytest.mark.parametrize("interleaved", [0, 1])
+def test_rope_q_and_k_same_buffer(gpu, interleaved):
+    """Q and K pointing at one buffer: the rows are rotated twice, K's pass
+    starting from Q's result, as the reference's two passes over the same
+    memory do."""
+    X = RNG.standard_normal((2, 3, 5, 128)).astype(np.float32)
+    bx = gpu.upload(X)
+    b, h, t, d = X.shape
+    gpu.run(abi.OP_ROPE_F32, Q=bx, K=bx, batch=b, heads=h, q_seq=t, k_seq=t, head_dim=d, position_offset=11,
+            interleaved=interleaved)
+    got = gpu.download(bx, np.float32, X.shape)
+    gpu.free(bx)
+    once, _ = oracle.rope(X, None, position_offset=11, interleaved=interleaved)
+    twice, _ = oracle.rope(once, None, position_offset=11, interleaved=interleaved)
+    assert np.array_equal(got.view(np.uint32), twice.view(np.uint32))
+
+
 def test_rope_host_positions_bit_exact(gpu):
     """A host position array is scanned for the table rows it needs."""
     Q = RNG.standard_normal((1, 2, 6, 32)).astype(np.float32)
