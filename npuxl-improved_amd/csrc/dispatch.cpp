@@ -604,6 +604,77 @@ bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t
     return true;
 }
 
+// MATMUL_I8 at M <= 8 followed by an ADD_F32 of its output (the block's
+// down projection + residual at decode): the GEMV's store also writes the
+// ADD's result, one launch instead of two.  Device-resident buffers, C
+// contiguous, the ADD over exactly C's M x N elements with C as one operand;
+// its output may be the other operand (in place) or C itself, and must not
+// overlap anything else the GEMV reads.  Returns false, having launched
+// nothing, when the pair does not qualify.
+bool try_execute_matmul_add(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &c0,
+                            const vnpu_command_t &c1, uint32_t flags, ExecStats &st0, ExecStats &st1)
+{
+    if (c0.opcode != VNPU_OP_MATMUL_I8 || c1.opcode != VNPU_OP_ADD_F32) return false;
+    const vnpu_matmul_i8_args_t &in = c0.args.matmul_i8;
+    const vnpu_binary_f32_args_t &ad = c1.args.binary;
+    const vnpu_packed_weights_t *w = in.B;
+    if (!in.A || !w || !in.C || !in.M || !in.K || !in.N || in.M > 8) return false;
+    if (w->K != in.K || w->N != in.N || in.epilogue > VNPU_EPILOGUE_GELU_ERF) return false;
+    if (w->device && w->device->hip_device != dev->hip_device) return false;
+    const uint32_t lda = in.lda ? in.lda : in.K;
+    if (lda < in.K || (in.ldc && in.ldc != in.N)) return false;
+    const uint64_t count = static_cast<uint64_t>(in.M) * in.N;
+    if (ad.count != count || !ad.Y || (ad.A == in.C) == (ad.B == in.C)) return false;
+    const bool c_first = ad.A == in.C;
+    const float *res = c_first ? ad.B : ad.A;
+    if (!res) return false;
+    for (const void *q : {static_cast<const void *>(in.A), static_cast<const void *>(in.C),
+                          static_cast<const void *>(in.scale_a), static_cast<const void *>(in.bias),
+                          static_cast<const void *>(res), static_cast<const void *>(ad.Y)})
+        if (q && !is_device_pointer(q)) return false;
+    auto lo = [](const void *q) { return reinterpret_cast<uintptr_t>(q); };
+    auto overlaps = [&](const void *a, size_t an, const void *b, size_t bn) {
+        return a && b && lo(a) < lo(b) + bn && lo(b) < lo(a) + an;
+    };
+    const size_t fb = count * 4;
+    // C and the other operand: disjoint (each is read or written once per element)
+    if (overlaps(in.C, fb, res, fb)) return false;
+    // Y: exactly the other operand or C, or disjoint from both; never over the GEMV's inputs
+    if (ad.Y != res && overlaps(ad.Y, fb, res, fb)) return false;
+    if (ad.Y != in.C && overlaps(ad.Y, fb, in.C, fb)) return false;
+    if (overlaps(ad.Y, fb, in.A, span(in.M, in.K, lda, 1)) ||
+        overlaps(ad.Y, fb, in.scale_a, in.scale_a ? static_cast<size_t>(in.M) * 4 : 0) ||
+        overlaps(ad.Y, fb, in.bias, in.bias ? static_cast<size_t>(in.N) * 4 : 0) ||
+        overlaps(in.C, fb, in.A, span(in.M, in.K, lda, 1)))
+        return false;
+
+    k::I8Gemm p;
+    p.A = in.A; p.lda = lda; p.frag = w->frag;
+    p.Kp = w->Kp; p.Np = w->Np; p.scale_a = in.scale_a; p.scale_b = w->scales_dev; p.bias = in.bias;
+    p.nz_list = w->nz_list; p.nz_count = w->nz_count; p.nz_tiles = w->nz_tiles;
+    p.C = in.C; p.ldc = in.N; p.M = in.M; p.N = in.N; p.K = in.K; p.epilogue = in.epilogue;
+    p.variant = dev->i8_variant.load();
+    const bool both0 = ad.alpha == 0.0f && ad.beta == 0.0f;  // llm.cpp:226-227
+    p.res = res;
+    p.res_out = ad.Y;
+    p.res_alpha = both0 ? 1.0f : ad.alpha;
+    p.res_beta = both0 ? 1.0f : ad.beta;
+    p.res_c_first = c_first ? 1u : 0u;
+    k::gemv_i8(s->hip, p);
+    VNPU_HIP(hipGetLastError());
+
+    st0.unit = choose_unit(in.unit, false, flags);
+    st0.tiles_dispatched += 1;
+    st0.bytes_read += static_cast<uint64_t>(in.M) * in.K + static_cast<uint64_t>(in.K) * in.N +
+                      static_cast<uint64_t>(in.N + (in.scale_a ? in.M : 0)) * 4;
+    st0.bytes_written += count * 4;
+    st0.flops += 2ull * in.M * in.K * in.N;
+    st1.bytes_read += count * 8;
+    st1.bytes_written += count * 4;
+    st1.flops += count * 3;
+    return true;
+}
+
 uint32_t try_execute_chain(vnpu_stream_t *s, const vnpu_command_t *c, uint64_t n,
                            uint32_t *matched, ExecStats *st)
 {

@@ -64,7 +64,7 @@ __device__ __forceinline__ int dot16(const int4 a, const int4 b, int acc)
 template <int NO, int NTH>
 struct EpiOperands {
     static constexpr int S = (NO + NTH - 1) / NTH;
-    float sa[S], sb[S], bias[S];
+    float sa[S], sb[S], bias[S], res[S];
     __device__ __forceinline__ EpiOperands(const I8Gemm &p, uint32_t nt0, int M, int tid)
     {
         const uint32_t NT = p.Np >> 4;
@@ -77,6 +77,9 @@ struct EpiOperands {
             sa[j] = live && p.scale_a ? p.scale_a[m] : 1.0f;
             sb[j] = live ? p.scale_b[n] : 1.0f;
             bias[j] = live && p.bias ? p.bias[n] : 0.0f;
+            // the fused ADD's other operand, read before any output is written
+            // (it may be the ADD's own output buffer)
+            res[j] = live && p.res ? p.res[static_cast<uint64_t>(m) * p.N + n] : 0.0f;
         }
     }
     template <int W, int T, int M>
@@ -94,7 +97,13 @@ struct EpiOperands {
             for (int w = 0; w < W; ++w) s += red[w][t][m][c];
             float out = dev::mul_rn(dev::mul_rn(static_cast<float>(s), sa[j]), sb[j]);
             if (p.bias) out = dev::add_rn(out, bias[j]);
-            p.C[static_cast<uint64_t>(m) * p.ldc + n] = dev::epilogue(out, p.epilogue);
+            out = dev::epilogue(out, p.epilogue);
+            p.C[static_cast<uint64_t>(m) * p.ldc + n] = out;
+            if (p.res) {
+                // ADD_F32's fma(a, alpha, b * beta), a and b in command order
+                const float x = p.res_c_first ? out : res[j], y = p.res_c_first ? res[j] : out;
+                p.res_out[static_cast<uint64_t>(m) * p.N + n] = fmaf(x, p.res_alpha, dev::mul_rn(y, p.res_beta));
+            }
         }
     }
 };

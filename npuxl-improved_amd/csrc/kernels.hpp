@@ -59,6 +59,14 @@ struct I8Gemm {
     // nonzero.  Null lists: every block is walked (dense kernels).
     const uint32_t *nz_list = nullptr, *nz_count = nullptr;
     uint64_t nz_tiles = 0;
+    // An ADD_F32 of the output fused into the store (GEMV path, M <= 8, C
+    // contiguous): res_out[m*N + n] = fma(x, res_alpha, y * res_beta) with
+    // (x, y) = (res[m*N + n], c), or (c, res[...]) when res_c_first; C is
+    // stored as well.  Null res: no fused add.
+    const float *res = nullptr;
+    float *res_out = nullptr;
+    float res_alpha = 1.0f, res_beta = 1.0f;
+    uint32_t res_c_first = 0;
 };
 struct I8GemmPair {
     I8Gemm p[2];

@@ -920,6 +920,30 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_stream_submit(vnpu_stream_t *stream,
                     continue;
                 }
             }
+            // A decode-sized MATMUL_I8 and an ADD of its output may share the
+            // GEMV's launch (not while tracing).
+            if (!tracing && i + 1 < count && cmd.opcode == VNPU_OP_MATMUL_I8 &&
+                commands[i + 1].opcode == VNPU_OP_ADD_F32) {
+                ExecStats s0, s1;
+                bool fused = false;
+                try {
+                    fused = try_execute_matmul_add(d, stream, cmd, commands[i + 1], flags, s0, s1);
+                } catch (const std::exception &ex) {
+                    debug_log("matmul_i8 + add failed: %s", ex.what());
+                    (void)hipGetLastError();
+                    fail(VNPU_ERR_INTERNAL);
+                    ++i;
+                    continue;
+                }
+                if (fused) {
+                    d->last_opcode.store(VNPU_OP_ADD_F32);
+                    const uint64_t host = now_ns() - t0;
+                    account(s0, host / 2);
+                    account(s1, host - host / 2);
+                    ++i;
+                    continue;
+                }
+            }
             // ADD / SWIGLU / RMSNORM followed by the row commands that consume
             // their output may run as one row-chain kernel (not while tracing).
             if (!tracing && i + 1 < count &&

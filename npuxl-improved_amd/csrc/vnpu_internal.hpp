@@ -226,6 +226,10 @@ struct ExecStats {
 // Two independent MATMUL_I8 commands in one grid; false: run them one by one.
 bool try_execute_pair(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &c0,
                       const vnpu_command_t &c1, uint32_t flags, ExecStats &st0, ExecStats &st1);
+// MATMUL_I8 (M <= 8) then an ADD_F32 of its output in one GEMV launch;
+// false: run them one by one.
+bool try_execute_matmul_add(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t &c0,
+                            const vnpu_command_t &c1, uint32_t flags, ExecStats &st0, ExecStats &st1);
 // A row chain at the head of c[0..n): ADD -> RMSNORM [-> QUANTIZE_I8 per row],
 // RMSNORM -> QUANTIZE_I8 or SWIGLU -> QUANTIZE_I8 over the same rows, device
 // buffers only, run as one kernel.  Returns the number of commands executed

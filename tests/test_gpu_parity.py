@@ -253,6 +253,55 @@ def test_matmul_i8_pair_in_one_batch(gpu, M, N0, N1, alias):
     assert rel(c1, want1) <= 1e-4
 
 
+@pytest.mark.parametrize("M,N,mode", [(8, 4096, "in_place"), (1, 4096, "in_place"), (8, 1000, "c_first"),
+                                        (5, 700, "y_is_c"), (8, 2000, "both0"), (3, 3000, "scaled"),
+                                        (8, 1000, "count_mismatch"), (12, 1000, "in_place")])
+def test_matmul_i8_then_add_in_one_batch(gpu, M, N, mode):
+    """MATMUL_I8 at M <= 8 followed by an ADD_F32 of its output in the same
+    batch (the block's down projection + residual at decode) may run as one
+    GEMV launch whose store also writes the ADD's result.  Both outputs must
+    be the bits of the same two commands submitted in separate batches (and C
+    the oracle's within 1e-4 under its SiLU epilogue): the residual in place, C as the ADD's first operand, the
+    ADD writing over C, alpha = beta = 0 (the defaults 1, 1), other scales;
+    a count that is not M x N and M > 8 run unfused."""
+    K = 512
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    bias = RNG.standard_normal(N).astype(np.float32)
+    x = RNG.standard_normal(M * N).astype(np.float32) * 100
+    w = gpu.pack(B, K, N, scales=sb)
+    ba, bsa, bb = gpu.upload(A), gpu.upload(sa), gpu.upload(bias)
+    alpha, beta = {"both0": (0.0, 0.0), "scaled": (0.5, -2.0)}.get(mode, (1.0, 1.0))
+    count = M * N - 4 if mode == "count_mismatch" else M * N
+
+    def run(fused):
+        bc, bx, by = gpu.alloc(4 * M * N), gpu.upload(x), gpu.alloc(4 * M * N)
+        mm = gpu.command(abi.OP_MATMUL_I8, A=ba, B=w, scale_a=bsa.ptr, bias=bb.ptr, C=bc, M=M, K=K, N=N,
+                         epilogue=2)
+        a_, b_, y_ = (bc, bx, by) if mode == "c_first" else (bx, bc, bc if mode == "y_is_c" else
+                                                             (bx if mode in ("in_place", "count_mismatch") else by))
+        add = gpu.command(abi.OP_ADD_F32, A=a_, B=b_, Y=y_, count=count, alpha=alpha, beta=beta)
+        batches = [[mm, add]] if fused else [[mm], [add]]
+        for cmds in batches:
+            assert gpu.submit(cmds) == abi.OK and gpu.sync() == abi.OK
+        out = {n: gpu.download(b, np.float32, (M * N,)) for n, b in (("c", bc), ("x", bx), ("y", by))}
+        for b in (bc, bx, by):
+            gpu.free(b)
+        return out
+
+    got, want = run(True), run(False)
+    for b in (ba, bsa, bb):
+        gpu.free(b)
+    gpu.release_packed(w)
+    for n in ("c", "x", "y"):
+        assert np.array_equal(got[n].view(np.uint32), want[n].view(np.uint32)), n
+    if mode != "y_is_c":   # there the ADD overwrote C in both runs
+        # SiLU epilogue: the same bar as the paired test's
+        assert rel(got["c"], oracle.matmul_i8(A, B, sa, sb, bias, 2).reshape(-1)) <= 1e-4
+
+
 @pytest.mark.parametrize("M", [1, 6, 40])
 def test_matmul_i8_accumulator_exact(gpu, M):
     # scale 1 everywhere: C == (float)acc exactly while |acc| < 2^24
