@@ -782,7 +782,13 @@ bool launch_row_chain(hipStream_t s, const RowChain &p)
 bool launch_swiglu_chain(hipStream_t s, const RowChain &p)
 {
     const dim3 grid(p.rows);
-    if (p.rows >= 256)
+    // many rows: 256 threads, as few float4 slots per thread as the row needs
+    // (unused slots still hold registers and cut the waves per SIMD)
+    if (p.rows >= 256 && p.cols / 4 <= 4 * 256)
+        row_chain_kernel<4, kChainSwiglu, false, true, 256><<<grid, dim3(256), 0, s>>>(p);
+    else if (p.rows >= 256 && p.cols / 4 <= 8 * 256)
+        row_chain_kernel<8, kChainSwiglu, false, true, 256><<<grid, dim3(256), 0, s>>>(p);
+    else if (p.rows >= 256)
         row_chain_kernel<12, kChainSwiglu, false, true, 256><<<grid, dim3(256), 0, s>>>(p);
     else if (p.cols / 4 <= 1024)
         row_chain_kernel<1, kChainSwiglu, false, true, 1024><<<grid, dim3(1024), 0, s>>>(p);

@@ -21,8 +21,11 @@ pytestmark = pytest.mark.gpu
 RNG = np.random.default_rng(20261207)
 KINDS = ["add_norm_quant", "add_norm", "norm_quant", "swiglu_quant"]
 # (rows, cols): the block's d_model and FFN rows, odd row counts, a short row,
-# and 12300 columns (beyond the register-resident row length: single kernels).
-SHAPES = [(8, 4096), (64, 4096), (5, 11008), (3, 12288), (6, 100), (2, 12300), (1, 4)]
+# and 12300 columns (beyond the register-resident row length: single kernels);
+# 256 rows or more take SWIGLU -> QUANTIZE's 256-thread kernels (4, 8 and 12
+# float4 slots per thread by row length).
+SHAPES = [(8, 4096), (64, 4096), (5, 11008), (3, 12288), (6, 100), (2, 12300), (1, 4), (300, 4096), (260, 6000),
+          (256, 11008)]
 
 
 def _inputs(kind, rows, cols):
