@@ -502,55 +502,71 @@ __device__ __forceinline__ void split_bf16(const float (&x)[8], v8bf &hi, v8bf &
     lo = __builtin_bit_cast(v8bf, (v4u){lw[0], lw[1], lw[2], lw[3]});
 }
 
-// One (32-key block, batch*head) per workgroup of 256 threads.
+// One (32-key block, batch*head) per workgroup of 256 threads.  Every load
+// is issued before the first split, through raw buffers over the block's
+// keys (keys past seq_k read as zero, which is what the layout holds for
+// them), so no branch separates loads from stores: with loads under
+// branches the compiler waited for all memory operations, the previous
+// item's stores included, before each item.
+//   * K: item (key, 16-byte chunk c), C = D / 8 chunks per key, 4D items;
+//   * V^T: item (position chunk ch, column pair d2): 8 keys' float2 at
+//     columns 2 d2, 2 d2 + 1 give rows 2 d2 and 2 d2 + 1 of chunk ch; 2D
+//     items, so every thread has one at D = 128.
 template <int D>
 __global__ __launch_bounds__(256) void attn_split_kv(Attn a, uint32_t nkb, int8_t *split)
 {
     using S = SplitBlk<D>;
     constexpr int C = S::kChunks;
-    const uint32_t kb = blockIdx.x;
+    constexpr int KItems = XK * C, VItems = (XK / 8) * (D / 2);
+    constexpr int NK = (KItems + 255) / 256, NV = (VItems + 255) / 256;
+    const uint32_t kb = blockIdx.x, tid = threadIdx.x;
     const uint64_t bh = blockIdx.y;
-    const uint32_t sk = a.seq_k;
+    const uint32_t sk = a.seq_k, key0 = kb * XK, nk = min(static_cast<uint32_t>(XK), sk - key0);
     int8_t *blk = split + (bh * nkb + kb) * S::kBytes;
-    const float *Kh = a.K + bh * sk * D;
-    const float *Vh = a.V + bh * sk * D;
-    for (uint32_t it = threadIdx.x; it < XK * C; it += 256) {
-        const uint32_t key = it / C, c = it % C;
-        const uint32_t gk = kb * XK + key;
-        float x[8];
-        if (gk < sk) {
-            const float4 *src = reinterpret_cast<const float4 *>(Kh + static_cast<uint64_t>(gk) * D + 8 * c);
-            const float4 u = src[0], v = src[1];
-            x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
-            x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
-        } else {
+    const uint64_t base = (bh * sk + key0) * D;
+    const int bytes = static_cast<int>(nk * D * 4u);
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.K + base), 0, bytes, 0x00020000);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.V + base), 0, bytes, 0x00020000);
+    float kx[NK][8];
+    float2 vx[NV][8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+    for (int i = 0; i < NK; ++i) {
+        const uint32_t it = tid + 256 * i, key = it / C, c = it % C;
+        const int off = static_cast<int>((key * D + 8 * c) * 4);
+        const float4 u = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+        const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+        kx[i][0] = u.x; kx[i][1] = u.y; kx[i][2] = u.z; kx[i][3] = u.w;
+        kx[i][4] = v.x; kx[i][5] = v.y; kx[i][6] = v.z; kx[i][7] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t it = tid + 256 * i, d2 = it % (D / 2), ch = it / (D / 2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int off = static_cast<int>((vt_key(8 * ch + e) * D + 2 * d2) * 4);
+            vx[i][e] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0));
         }
+    }
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+        const uint32_t it = tid + 256 * i, key = it / C, c = it % C;
+        if (it >= KItems) continue;
         v8bf hi, lo;
-        split_bf16(x, hi, lo);
+        split_bf16(kx[i], hi, lo);
         const uint32_t off = key * (D * 2) + ((c ^ k_swizzle<D>(key)) << 4);
         *reinterpret_cast<v8bf *>(blk + off) = hi;
         *reinterpret_cast<v8bf *>(blk + S::kHalfK + off) = lo;
     }
-    // V^T: a thread takes 4 columns (one float4) of the 8 keys of position
-    // chunk ch and writes those 4 rows' chunk; lanes take consecutive float4
-    // of a key row, so the reads are coalesced.
-    for (uint32_t it = threadIdx.x; it < D; it += 256) {
-        const uint32_t d4 = it % (D / 4), ch = it / (D / 4);
-        float4 v[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t gk = kb * XK + vt_key(8 * ch + e);
-            v[e] = gk < sk ? *reinterpret_cast<const float4 *>(Vh + static_cast<uint64_t>(gk) * D + 4 * d4)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+    for (int i = 0; i < NV; ++i) {
+        const uint32_t it = tid + 256 * i, d2 = it % (D / 2), ch = it / (D / 2);
+        if (it >= VItems) continue;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t d = 4 * d4 + q;
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t d = 2 * d2 + q;
             float x[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = q == 0 ? v[e].x : q == 1 ? v[e].y : q == 2 ? v[e].z : v[e].w;
+            for (int e = 0; e < 8; ++e) x[e] = q ? vx[i][e].y : vx[i][e].x;
             v8bf hi, lo;
             split_bf16(x, hi, lo);
             const uint32_t off = d * (XK * 2) + ((ch ^ ((d >> 2) & 3)) << 4);
