@@ -673,13 +673,32 @@ __device__ __forceinline__ void put4(float *d, const float4 v)
     d[3] = v.w;
 }
 
-// Workgroups from `full` on split the remaining tiles over K: two per tile,
-// the first taking k stages [0, ks_half), the second [ks_half, KT); each
-// writes its raw sums as a 256 x 128 row-major tile into part (tile pair i
-// at part + 2i * 256 * 128) and gemm_f32_tail_reduce finishes them.  Used
-// when the last round of tiles would leave at least half the CUs idle.
+// Tile of workgroup b: the first `full` workgroups take tiles [0, full) one
+// each; the rest split the remaining T2 = total - full tiles over K,
+// workgroup full + sp * T2 + t taking k-slice sp of split tile t.  Within each
+// part the tiles are remapped so that the workgroups of one XCD (b % 8, as
+// they are dispatched round-robin) get a contiguous run of tiles, whose A
+// rows and B columns then meet in that XCD's L2.
+__host__ __device__ inline uint32_t ws_tile_of(uint32_t b, uint32_t full, uint32_t total, uint32_t *slice)
+{
+    if (b < full) {
+        *slice = 0;
+        return (full & 7u) == 0 ? (b & 7u) * (full >> 3) + (b >> 3) : b;
+    }
+    const uint32_t t2 = total - full, r = b - full, t = r % t2;
+    *slice = r / t2;
+    return full + ((t2 & 7u) == 0 ? (t & 7u) * (t2 >> 3) + (t >> 3) : t);
+}
+
+// Workgroups from `full` on split the remaining tiles over K, `splits` per
+// tile, slice sp taking k stages [sp * ks_per, + ks_per) (the last one the
+// rest); each writes its raw sums as a 256 x 128 row-major tile into part
+// (workgroup full + r at part + r * 256 * 128) and gemm_f32_tail_reduce adds
+// the slices in order and finishes them.  Used when the last round of tiles
+// would leave at least half the CUs idle (two slices) and for grids of fewer
+// tiles than CUs (as many slices as fill the CUs).
 template <bool TB>
-__global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p, uint32_t full, uint32_t ks_half, float *part)
+__global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p, uint32_t full, uint32_t ks_per, float *part)
 {
     using ws::kSlots;
     using ws::kSlotBytes;
@@ -696,14 +715,14 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p, uint32_t full, uin
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t tiles_m = (p.M + TM - 1) / TM, total = tiles_m * ((p.N + TN - 1) / TN);
     const bool split = blockIdx.x >= full;
-    const uint32_t half = split ? (blockIdx.x - full) & 1u : 0u;
-    uint32_t g = split ? full + ((blockIdx.x - full) >> 1) : blockIdx.x;
-    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    uint32_t sp;
+    const uint32_t g = ws_tile_of(blockIdx.x, full, total, &sp);
     const uint32_t m0 = (g % tiles_m) * TM, n0 = (g / tiles_m) * TN;
     const uint32_t KTall = (p.K + WBK - 1) / WBK;
-    // This workgroup's k stages: [ks0, ks0 + KT)
-    const uint32_t ks0 = split && half ? ks_half : 0u;
-    const uint32_t KT = split ? (half ? KTall - ks_half : ks_half) : KTall;
+    // This workgroup's k stages: [ks0, ks0 + KT); the host gives every slice
+    // at least one stage
+    const uint32_t ks0 = split ? sp * ks_per : 0u;
+    const uint32_t KT = split ? min(ks_per, KTall - ks0) : KTall;
     if (tid < 2 * 4 * kSlots) flags[tid] = 0;
     __syncthreads();
 
@@ -904,7 +923,7 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p, uint32_t full, uin
     // bias, beta 0, no activation) into its 256 x 128 partial tile instead.
     if (split) {
         F32Gemm t = p;
-        t.C = part + static_cast<uint64_t>((blockIdx.x - full) >> 1) * 2 * TM * TN + half * TM * TN;
+        t.C = part + static_cast<uint64_t>(blockIdx.x - full) * TM * TN;
         t.M = TM;
         t.N = TN;
         t.ldc = TN;
@@ -925,27 +944,32 @@ __global__ __launch_bounds__(512) void gemm_f32_ws(F32Gemm p, uint32_t full, uin
     }
 }
 
-// The tiles gemm_f32_ws split over K: C = epi(alpha (s0 + s1) + bias +
-// beta C) for tile pair blockIdx.y, 1024 elements (four per thread) per
-// workgroup.
-__global__ __launch_bounds__(kThreads) void gemm_f32_tail_reduce(F32Gemm p, const float *part, uint32_t full)
+// The tiles gemm_f32_ws split over K: C = epi(alpha (s_0 + s_1 + ...) +
+// bias + beta C), the slices added in order, for split tile blockIdx.y,
+// 1024 elements (four per thread) per workgroup.
+__global__ __launch_bounds__(kThreads) void gemm_f32_tail_reduce(F32Gemm p, const float *part, uint32_t full,
+                                                                 uint32_t splits)
 {
     using ws::TM;
     using ws::TN;
     const uint32_t tiles_m = (p.M + TM - 1) / TM, total = tiles_m * ((p.N + TN - 1) / TN);
-    uint32_t g = full + blockIdx.y;
-    if ((total & 7u) == 0) g = (g & 7u) * (total >> 3) + (g >> 3);
+    uint32_t sp;
+    const uint32_t g = ws_tile_of(full + blockIdx.y, full, total, &sp);   // slice 0 of tile blockIdx.y
     const uint32_t m0 = (g % tiles_m) * TM, n0 = (g / tiles_m) * TN;
     const uint32_t e = (blockIdx.x * kThreads + threadIdx.x) * 4;   // element of the 256 x 128 tile
-    const float *p0 = part + static_cast<uint64_t>(blockIdx.y) * 2 * TM * TN;
-    const float4 a = *reinterpret_cast<const float4 *>(p0 + e);
-    const float4 b = *reinterpret_cast<const float4 *>(p0 + TM * TN + e);
+    const uint64_t t2 = total - full, stride = t2 * TM * TN;
+    const float *p0 = part + static_cast<uint64_t>(blockIdx.y) * TM * TN + e;
     const uint32_t m = m0 + e / TN, n = n0 + e % TN;
     if (m >= p.M) return;
-    const float s[4] = {a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
+    float4 a = *reinterpret_cast<const float4 *>(p0);
+    for (uint32_t i = 1; i < splits; ++i) {
+        const float4 b = *reinterpret_cast<const float4 *>(p0 + i * stride);
+        a = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    }
+    const float s4[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        if (n + i < p.N) store_out(p, m, n + i, s[i], false);
+        if (n + i < p.N) store_out(p, m, n + i, s4[i], false);
 }
 
 // ---------------------------------------------------------------------------
@@ -1342,6 +1366,54 @@ static uint32_t gemm_f32_splits(const F32Gemm &p)
 // tiles of 128 x 128 split K over workgroups (32-deep stages, at least two
 // per slice) until the grid has 128 or more, with the partial sums reduced
 // in slice order by a second pass.
+// Grid targets (swept on MI355X, 256 CUs).  The lock-step four-wave kernel
+// splits K until it has kX3Grid workgroups (two per CU): against 128, at
+// 1024x4096x2048 206 -> 97 us, 2048^3 109 -> 100 us, 1024x1024x2048 78 -> 40
+// us (256 and 1024 were slower).  The warp-specialised kernel takes grids of
+// fewer 256 x 128 tiles than CUs when slices of K of at least kWsMinStages
+// stages bring them to kWsMinGrid workgroups.
+constexpr uint64_t kX3Grid = 512;
+constexpr uint32_t kWsMinStages = 16;
+constexpr uint64_t kWsMinGrid = 192;
+
+// K slices per tile for a grid of `tiles` 256 x 128 tiles below the CU count:
+// as many as fill the CUs, each of at least kWsMinStages stages (1: none).
+static uint32_t ws_slices(uint64_t tiles, uint32_t K)
+{
+    const uint32_t cus = std::max<uint32_t>(1, cu_count());
+    const uint32_t kt = (K + ws::BK - 1) / ws::BK;
+    if (!tiles || tiles >= cus) return 1;
+    return std::max<uint32_t>(1, std::min<uint32_t>(static_cast<uint32_t>(cus / tiles), kt / kWsMinStages));
+}
+
+// How the warp-specialised kernel covers its tiles: the first `full` whole,
+// the rest as `splits` K slices of ks_per stages each.  A last round that
+// would fill at most half the CUs is split in two (its round then takes half
+// as long); a grid of fewer tiles than CUs is split by ws_slices.
+struct WsSplit {
+    uint32_t total, full, splits, ks_per, kt;
+};
+static WsSplit ws_split(const F32Gemm &p)
+{
+    WsSplit w;
+    w.total = ((p.M + ws::TM - 1) / ws::TM) * ((p.N + ws::TN - 1) / ws::TN);
+    w.kt = (p.K + ws::BK - 1) / ws::BK;
+    w.full = w.total;
+    w.splits = 1;
+    const uint32_t cus = std::max<uint32_t>(1, cu_count()), rest = w.total % cus;
+    if (w.total < cus) {
+        w.splits = ws_slices(w.total, p.K);
+        if (w.splits > 1) w.full = 0;
+    } else if (rest && rest <= cus / 2 && w.kt >= 16) {
+        w.full = w.total - rest;
+        w.splits = 2;
+    }
+    w.ks_per = (w.kt + w.splits - 1) / w.splits;
+    w.splits = (w.kt + w.ks_per - 1) / w.ks_per;   // every slice has at least one stage
+    if (w.splits == 1) w.full = w.total;
+    return w;
+}
+
 struct X3Plan {
     bool x3 = false;
     bool ws = false;   // the warp-specialised 256 x 128 kernel (op(A) = A)
@@ -1362,16 +1434,24 @@ static X3Plan x3_plan(const F32Gemm &p)
     // workgroup splits an A slice once for 128 columns and a B slice once
     // for 256 rows (a quarter less conversion per MFMA).
     const uint64_t tiles256 = static_cast<uint64_t>((p.M + 255) / 256) * ((p.N + x3::TN - 1) / x3::TN);
+    const uint64_t a_bytes = static_cast<uint64_t>(p.M) * p.lda * 4;
+    const uint64_t b_bytes = static_cast<uint64_t>(p.trans_b ? p.N : p.K) * p.ldb * 4;
+    // The warp-specialised kernel reads A and B through 31-bit buffer ranges.
+    const bool ws_ok = !p.trans_a && a_bytes < (1ull << 31) && b_bytes < (1ull << 31);
     if (tiles256 >= 256) {
         x.wm = 4;
-        // The warp-specialised kernel reads A and B through 31-bit buffer ranges.
-        const uint64_t a_bytes = static_cast<uint64_t>(p.M) * p.lda * 4;
-        const uint64_t b_bytes = static_cast<uint64_t>(p.trans_b ? p.N : p.K) * p.ldb * 4;
-        x.ws = !p.trans_a && a_bytes < (1ull << 31) && b_bytes < (1ull << 31);
+        x.ws = ws_ok;
+    } else if (ws_ok && tiles256 * ws_slices(tiles256, p.K) >= kWsMinGrid) {
+        // fewer tiles than CUs, but K slices of at least kWsMinStages fill
+        // three quarters of the CUs or more
+        x.wm = 4;
+        x.ws = true;
+        return x;
     }
-    if (tiles >= 128) return x;
+    // The lock-step kernel splits K until the grid has two workgroups per CU.
+    if (x.ws || tiles >= kX3Grid) return x;
     uint32_t want = 1;
-    while (tiles * want < 128 && p.K / (want * 2) >= 2 * x3::BK) want *= 2;
+    while (tiles * want < kX3Grid && p.K / (want * 2) >= 2 * x3::BK) want *= 2;
     const uint64_t per_split = static_cast<uint64_t>(p.M) * p.N * sizeof(float);
     want = static_cast<uint32_t>(std::min<uint64_t>(want, std::max<uint64_t>(1, kMaxSplitWs / per_split)));
     if (want > 1) {
@@ -1404,28 +1484,12 @@ static void launch_x3(hipStream_t s, const F32Gemm &p, const X3Plan &x, float *w
     else gemm_f32_x3<true, true, WM><<<grid, block, lds, s>>>(p, x.kps, out);
 }
 
-// Tiles of the warp-specialised kernel that run split over K: when the last
-// round of 256 x 128 tiles would fill at most half the CUs, each of its tiles
-// runs as two workgroups over half of K each (the round then takes half as
-// long), provided K has at least 16 stages.  Returns the number of such
-// tiles (0: none); *full receives the number of whole tiles before them.
-static uint32_t ws_tail_tiles(const F32Gemm &p, uint32_t *full)
-{
-    const uint32_t total = ((p.M + ws::TM - 1) / ws::TM) * ((p.N + ws::TN - 1) / ws::TN);
-    const uint32_t cus = std::max<uint32_t>(1, cu_count());
-    const uint32_t rest = total % cus;
-    *full = total;
-    if (total < cus || rest == 0 || rest > cus / 2 || (p.K + ws::BK - 1) / ws::BK < 16) return 0;
-    *full = total - rest;
-    return rest;
-}
-
 size_t gemm_f32_ws_bytes(const F32Gemm &p)
 {
     const X3Plan x = x3_plan(p);
     if (x.ws) {
-        uint32_t full;
-        return static_cast<size_t>(ws_tail_tiles(p, &full)) * 2 * ws::TM * ws::TN * sizeof(float);
+        const WsSplit w = ws_split(p);
+        return static_cast<size_t>(w.total - w.full) * w.splits * ws::TM * ws::TN * sizeof(float);
     }
     const uint32_t splits = x.x3 ? x.splits : gemm_f32_splits(p);
     return splits > 1 ? static_cast<size_t>(splits) * p.M * p.N * sizeof(float) : 0;
@@ -1448,15 +1512,15 @@ void gemm_f32(hipStream_t s, const F32Gemm &p, float *ws)
                                             hipFuncAttributeMaxDynamicSharedMemorySize, ws::kLds) == hipSuccess &&
                         hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_f32_ws<true>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize, ws::kLds) == hipSuccess;
-        uint32_t full;
-        const uint32_t tail = ws ? ws_tail_tiles(p, &full) : 0;
-        if (!tail) full = ((p.N + ws::TN - 1) / ws::TN) * ((p.M + ws::TM - 1) / ws::TM);
-        const uint32_t ks_half = (p.K + ws::BK - 1) / ws::BK / 2;
-        const dim3 grid(full + 2 * tail);
-        if (p.trans_b) gemm_f32_ws<true><<<grid, 512, ws::kLds, s>>>(p, full, ks_half, ws);
-        else gemm_f32_ws<false><<<grid, 512, ws::kLds, s>>>(p, full, ks_half, ws);
+        WsSplit w = ws_split(p);
+        if (!ws) w = WsSplit{w.total, w.total, 1, w.kt};   // no workspace: every tile whole
+        const uint32_t tail = w.total - w.full;
+        const dim3 grid(w.full + tail * w.splits);
+        if (p.trans_b) gemm_f32_ws<true><<<grid, 512, ws::kLds, s>>>(p, w.full, w.ks_per, ws);
+        else gemm_f32_ws<false><<<grid, 512, ws::kLds, s>>>(p, w.full, w.ks_per, ws);
         if (tail)
-            gemm_f32_tail_reduce<<<dim3(ws::TM * ws::TN / (4 * kThreads), tail), kThreads, 0, s>>>(p, ws, full);
+            gemm_f32_tail_reduce<<<dim3(ws::TM * ws::TN / (4 * kThreads), tail), kThreads, 0, s>>>(p, ws, w.full,
+                                                                                                    w.splits);
         return;
     }
     if (x.x3) {

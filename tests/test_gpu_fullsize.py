@@ -147,14 +147,17 @@ def test_config3_f32_prefill_full(gpu, N):
     assert oracle.rel_error(got, want) <= 1e-4
 
 
-@pytest.mark.parametrize("M,K,N", [(2000, 1000, 4100), (1700, 1000, 4700), (2048, 520, 14336)])
+@pytest.mark.parametrize("M,K,N", [(2000, 1000, 4100), (1700, 1000, 4700), (2048, 520, 14336), (1024, 4096, 2048),
+                                   (1536, 4096, 1536), (1000, 3000, 1900), (2048, 2048, 2048)])
 @pytest.mark.parametrize("tb", [0, 1])
 def test_f32_last_round_k_split(gpu, M, K, N, tb):
     """Grids of 256 x 128 tiles whose last round fills at most half of the
     256 CUs (264, 259 and 896 tiles): those tiles run as two workgroups over
     half of K each, then a second pass adds the halves and applies alpha,
-    bias, beta and the epilogue.  Ragged M / N / K edges land in the split
-    tiles; 259 tiles also skip the XCD remap (not a multiple of 8)."""
+    bias, beta and the epilogue.  Grids of fewer tiles than CUs (64, 72, 60
+    and 128 tiles) run every tile as 4, 3, 4 or 2 K slices the same way.
+    Ragged M / N / K edges land in the split tiles; 259 and 60 tiles also
+    skip the XCD remap (not a multiple of 8)."""
     a = RNG.standard_normal((M, K), dtype=np.float32)
     b = (RNG.standard_normal((N, K) if tb else (K, N), dtype=np.float32) * 0.05).astype(np.float32)
     bias = RNG.standard_normal(N, dtype=np.float32) * 0.1
