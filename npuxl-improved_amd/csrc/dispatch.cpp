@@ -6,8 +6,9 @@
 //      same rejections) - a rejected command throws ArgError, which the
 //      stream turns into the reference's sticky-error behaviour;
 //   2. stages host pointers through HBM (device pointers pass through);
-//   3. picks the kernel from the shape (the "grid scheduler": decode GEMV for
-//      M <= 8, MFMA GEMM otherwise) and enqueues it on the stream;
+//   3. picks the kernel from the shape (the "grid scheduler": int8 weight-
+//      streaming GEMV below 64 rows, MFMA GEMM otherwise) and enqueues it on
+//      the stream;
 //   4. accounts algorithmic bytes / flops exactly as the reference does.
 #include "vnpu_internal.hpp"
 #include "kernels.hpp"
@@ -520,7 +521,7 @@ void exec_matmul_i8(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_matmul_i8_a
     const size_t c_bytes = span(in.M, in.N, p.ldc, 4);
     p.C = p.ldc != in.N ? sg.inout(in.C, c_bytes) : sg.out(in.C, c_bytes);
 
-    if (in.M <= 8)
+    if (k::gemv_i8_takes(in.M, in.N))
         k::gemv_i8(s->hip, p);
     else
         k::gemm_i8(s->hip, p, static_cast<int8_t *>(s->ensure_workspace(k::gemm_i8_ws_bytes(p))));

@@ -73,7 +73,7 @@ struct EpiOperands {
             const int o = tid + j * NTH;
             const int c = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
             const uint32_t n = (nt0 + t) * 16 + c;
-            const bool live = o < NO && nt0 + t < NT && n < p.N;
+            const bool live = o < NO && nt0 + t < NT && n < p.N && static_cast<uint32_t>(m) < p.M;
             sa[j] = live && p.scale_a ? p.scale_a[m] : 1.0f;
             sb[j] = live ? p.scale_b[n] : 1.0f;
             bias[j] = live && p.bias ? p.bias[n] : 0.0f;
@@ -91,7 +91,7 @@ struct EpiOperands {
             const int o = tid + j * NTH;
             const int c = o & 15, m = (o >> 4) % M, t = (o >> 4) / M;
             const uint32_t n = (nt0 + t) * 16 + c;
-            if (o >= NO || nt0 + t >= NT || n >= p.N) continue;
+            if (o >= NO || nt0 + t >= NT || n >= p.N || static_cast<uint32_t>(m) >= p.M) continue;
             int s = 0;
 #pragma unroll
             for (int w = 0; w < W; ++w) s += red[w][t][m][c];
@@ -227,13 +227,17 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_kernel(I8Gemm p, uint32_t chun
     epi.template store<W, T, M>(p, red, nt0, NT, tid);
 }
 
-// The same stream for 3..8 rows with the int8 matrix core doing the math: a
+// The same stream for 3..64 rows with the int8 matrix core doing the math: a
 // packed 1 KiB weight block is exactly the B operand of one
 // v_mfma_i32_16x16x64_i8 (lane 16kg + c holds k 16kg..16kg+15 of column c),
-// and the A operand is the staged activations (lane l: row l%16, the same 16
-// k; rows past M are zero).  One MFMA per block replaces 4M v_dot4 and M
-// ds_read_b128 per lane, which at M = 8 made the VALU the bottleneck.  The
-// 16 x 16 result leaves row 4(l/16) + i, column l%16 in lane l, register i.
+// and the A operand is the staged activations (lane l: row l%16 of a group of
+// 16 rows, the same 16 k; rows past M are zero).  One MFMA per block and row
+// group replaces 4M v_dot4 and M ds_read_b128 per lane, which at M = 8 made
+// the VALU the bottleneck.  The 16 x 16 result leaves row 4(l/16) + i, column
+// l%16 in lane l, register i.  M is the row capacity: the kernels for up to
+// 8 rows are built per row count, those for 16, 32 and 64 take any p.M up to
+// it (the staged layout uses p.M; rows past it are zero and not stored), and
+// above 16 rows the wave sums go through the activation LDS once it is free.
 template <int M, int W, int U, int T>
 __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t grid0, uint32_t chunk_k)
 {
@@ -242,10 +246,13 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
     const bool second = blockIdx.x >= grid0;
     const I8Gemm &p = ps.p[second ? 1 : 0];
     const uint32_t bx = second ? blockIdx.x - grid0 : blockIdx.x;
-    static_assert(M <= 16, "rows of one 16 x 16 tile");
+    static_assert(M <= 64, "at most four 16-row groups");
+    constexpr int MG = (M + 15) / 16;
     typedef int v4i __attribute__((ext_vector_type(4)));
-    extern __shared__ __attribute__((aligned(16))) int8_t a_lds[];  // [chunk_k/16][M][16]
-    __shared__ int red[W][T][M][16];
+    extern __shared__ __attribute__((aligned(16))) int8_t a_lds[];  // [chunk_k/16][Mr][16]
+    __shared__ int red_s[M <= 16 ? W * T * M * 16 : 1];
+    // rows present: the template's count up to 8 rows, else the call's
+    const uint32_t Mr = M <= 8 ? static_cast<uint32_t>(M) : ps.p[0].M;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -255,9 +262,11 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
     const uint32_t KT = p.Kp >> 6;
     const bool vec_a = ((p.lda & 15u) == 0) && ((reinterpret_cast<uintptr_t>(p.A) & 15u) == 0);
 
-    v4i acc[T];
+    v4i acc[MG][T];
 #pragma unroll
-    for (int t = 0; t < T; ++t) acc[t] = (v4i){0, 0, 0, 0};
+    for (int g = 0; g < MG; ++g)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[g][t] = (v4i){0, 0, 0, 0};
     const EpiOperands<T * M * 16, 64 * W> epi(p, nt0, M, tid);
 
     for (uint32_t kc = 0; kc < p.Kp; kc += chunk_k) {
@@ -284,9 +293,9 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
             for (int t = 0; t < T; ++t) bc[u][t] = ld(t, u);
 
         if (kc) __syncthreads();  // previous chunk fully consumed
-        const uint32_t chunks = (kt1 - kt0) * 4 * M;
+        const uint32_t chunks = (kt1 - kt0) * 4 * Mr;
         for (uint32_t i = tid; i < chunks; i += 64 * W) {
-            const uint32_t m = i % M, k16 = i / M;
+            const uint32_t m = i % Mr, k16 = i / Mr;
             const uint32_t k = kc + k16 * 16;
             const int8_t *src = p.A + static_cast<uint64_t>(m) * p.lda + k;
             int4 v;
@@ -301,7 +310,7 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
                 for (int j = 0; j < 16; ++j) u.b[j] = (k + j < p.K) ? src[j] : 0;
                 v = u.v;
             }
-            *reinterpret_cast<int4 *>(a_lds + (k16 * M + m) * 16) = v;
+            *reinterpret_cast<int4 *>(a_lds + (k16 * Mr + m) * 16) = v;
         }
         __syncthreads();
 
@@ -313,10 +322,15 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const uint32_t ktl = first + W * min(i + u, cnt - 1) - kt0;
-                v4i a = (v4i){0, 0, 0, 0};
-                if (row < M) a = *reinterpret_cast<const v4i *>(a_lds + ((ktl * 4 + kg) * M + row) * 16);
 #pragma unroll
-                for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bc[u][t], acc[t], 0, 0, 0);
+                for (int g = 0; g < MG; ++g) {
+                    const uint32_t r = 16 * g + row;
+                    v4i a = (v4i){0, 0, 0, 0};
+                    if (r < Mr) a = *reinterpret_cast<const v4i *>(a_lds + ((ktl * 4 + kg) * Mr + r) * 16);
+#pragma unroll
+                    for (int t = 0; t < T; ++t)
+                        acc[g][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bc[u][t], acc[g][t], 0, 0, 0);
+                }
             }
 #pragma unroll
             for (int u = 0; u < U; ++u)
@@ -325,14 +339,20 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
         }
     }
 
-    // Lane l holds rows 4(l/16) + i of column l%16; sum the waves in LDS.
+    // Lane l holds rows 16g + 4(l/16) + i of column l%16; sum the waves in LDS
+    // (above 16 rows in the activation area, once every wave is done with it).
+    if constexpr (M > 16) __syncthreads();
+    auto &red = *reinterpret_cast<int (*)[W][T][M][16]>(M <= 16 ? static_cast<void *>(red_s)
+                                                                 : static_cast<void *>(a_lds));
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+    for (int g = 0; g < MG; ++g)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * kg + i;
-            if (m < M) red[wave][t][m][row] = acc[t][i];
-        }
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * g + 4 * kg + i;
+                if (m < M) red[wave][t][m][row] = acc[g][t][i];
+            }
     __syncthreads();
     epi.template store<W, T, M>(p, red, nt0, NT, tid);
 }
@@ -383,13 +403,17 @@ template <int M>
 void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t grid0, uint32_t grid1,
                       uint32_t chunk_k)
 {
-    const size_t lds = static_cast<size_t>(chunk_k) * M;
+    // above 16 rows the wave sums ([W][T][M][16] int32, 64 W T M bytes; W T =
+    // 16 in every variant) reuse the activation LDS
+    const size_t lds = std::max<size_t>(static_cast<size_t>(chunk_k) * M, M > 16 ? 64u * 16u * M : 0u);
     const dim3 grid(grid0 + grid1);
-    if (variant == 0)
+    if (variant == 0) {
+        if (M > 16) lds_optin<gemv_i8_mfma<M, 4, 4, 4>>();
         gemv_i8_mfma<M, 4, 4, 4><<<grid, 256, lds, s>>>(ps, grid0, chunk_k);
-    else if (variant == 1)
+    } else if (variant == 1) {
+        if (M > 16) lds_optin<gemv_i8_mfma<M, 8, 2, 2>>();
         gemv_i8_mfma<M, 8, 2, 2><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
-    else {
+    } else {
         lds_optin<gemv_i8_mfma<M, 16, 2, 1>>();
         gemv_i8_mfma<M, 16, 2, 1><<<grid, 1024, lds, s>>>(ps, grid0, chunk_k);
     }
@@ -443,7 +467,12 @@ void gemv_i8(hipStream_t s, const I8Gemm &p)
     case 6: launch_m<6>(s, p); break;
     case 7: launch_m<7>(s, p); break;
     case 8: launch_m<8>(s, p); break;
-    default: break;
+    default:
+        // 9..64 rows: the matrix-core kernel with a row capacity of 16, 32 or 64
+        if (p.M <= 16) launch_m<16>(s, p);
+        else if (p.M <= 32) launch_m<32>(s, p);
+        else if (p.M <= kGemvMaxRows) launch_m<64>(s, p);
+        break;
     }
 }
 

@@ -78,7 +78,18 @@ enum : uint32_t { kI8Auto = 0, kI8Wide = 1, kI8Wave8 = 2, kI8Pipe = 3, kI8Generi
 // select it: 256x128x256 wide, 256x128x128 8-wave, 256x64x128 64-deep,
 // 128x64x128 generic; anything else chooses automatically.
 uint32_t gemm_i8_variant_for_tiles(uint32_t tile_m, uint32_t tile_k, uint32_t tile_n);
-void gemv_i8(hipStream_t s, const I8Gemm &p);  // M <= 8 (matrix core from 5 rows)
+// Weight-streaming path for few rows: v_dot4 up to 4 rows, the int8 matrix
+// core from 5 to kGemvMaxRows rows.  It takes every MATMUL_I8 below 64 rows
+// (the GEMM kernels' 64-row tiles need M >= 64; below that they fell back to
+// the generic kernel, 9..48 rows 71-77 us where this runs 6-12 us at
+// 4096 x 4096) and 64 rows below 512 column strips (at 11008 and 32000
+// columns the 256 x 128 GEMM tiles are faster: 24 / 33 against 33 / 79 us).
+constexpr uint32_t kGemvMaxRows = 64;
+inline bool gemv_i8_takes(uint32_t M, uint32_t N)
+{
+    return M < kGemvMaxRows || (M == kGemvMaxRows && N < 512 * 16);
+}
+void gemv_i8(hipStream_t s, const I8Gemm &p);
 // Any M, int8 MFMA; ws holds gemm_i8_ws_bytes(p) (the strip kernel's A in
 // fragment blocks; nothing for the dense kernels, where ws may be null).
 size_t gemm_i8_ws_bytes(const I8Gemm &p);

@@ -302,6 +302,30 @@ def test_matmul_i8_then_add_in_one_batch(gpu, M, N, mode):
         assert rel(got["c"], oracle.matmul_i8(A, B, sa, sb, bias, 2).reshape(-1)) <= 1e-4
 
 
+@pytest.mark.parametrize("M", [9, 13, 16, 17, 31, 32, 33, 48, 64, 65])
+@pytest.mark.parametrize("K,N", [(320, 4096), (4160, 9000), (192, 17600), (1000, 100)])
+def test_matmul_i8_few_rows(gpu, M, K, N):
+    """9..64 rows run the weight-streaming matrix-core kernel with a row
+    capacity of 16, 32 or 64 (rows past M zero, not stored), in each of its
+    three launch shapes (4096, 9000 and 17600 columns: 256, 563 and 1100
+    strips); 65 rows take the GEMM kernels.  Bit-exact with scales, bias and
+    a ReLU epilogue, and a ragged K (1000)."""
+    A = RNG.integers(-128, 128, size=(M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, size=(K, N)).astype(np.int8)
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    bias = RNG.standard_normal(N).astype(np.float32)
+    w = gpu.pack(B, K, N, scales=sb)
+    ba, bsa, bb, bc = gpu.upload(A), gpu.upload(sa), gpu.upload(bias), gpu.alloc(4 * M * N)
+    gpu.run(abi.OP_MATMUL_I8, A=ba, B=w, scale_a=bsa.ptr, bias=bb.ptr, C=bc, M=M, K=K, N=N, epilogue=1)
+    got = gpu.download(bc, np.float32, (M, N))
+    for b in (ba, bsa, bb, bc):
+        gpu.free(b)
+    gpu.release_packed(w)
+    want = oracle.matmul_i8(A, B, sa, sb, bias, 1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("M", [1, 6, 40])
 def test_matmul_i8_accumulator_exact(gpu, M):
     # scale 1 everywhere: C == (float)acc exactly while |acc| < 2^24
