@@ -341,24 +341,23 @@ def bench_config5(s: Session, steps: int):
     w = synth.normal("c5/W", (K, N), 0.02)
     keep = synth.bernoulli_mask("c5/tiles", (K // 64, N // 64), 0.5)
 
-    def packed_of(wf):
-        bw = s.upload(wf)
-        wq, ws = s.alloc(K * N), s.alloc(4 * N)
-        s.run(abi.OP_QUANTIZE_I8, X=bw, Y=wq, scales=ws, rows=K, cols=N, axis=abi.QUANT_PER_COLUMN)
-        s.free(bw)
-        pk = s.pack(wq, K, N, scales=ws)
-        s.free(wq)
-        s.free(ws)
-        return pk
-
-    dense_w = packed_of(w)   # the same weights unculled: the dense baseline of the same kernel family
-    # Beside config 5's half-zero tiles, a quarter-nonzero mask of the same
-    # weights: below 40% nonzero tiles the strip kernel skips the zero ones.
+    # The dense weights quantized per column once; config 5's mask is passed
+    # in at packing (vnpu_pack_weights_i8_masked), which packs the culled
+    # tiles as zeros.  The unmasked packing is the dense baseline of the same
+    # kernel family; beside config 5's half-zero tiles, a quarter-nonzero mask
+    # of the same weights (below 40% nonzero tiles the strip kernel skips the
+    # zero ones).
     keep25 = synth.bernoulli_mask("c5/tiles25", (K // 64, N // 64), 0.25)
-    sparse_w = packed_of(w * np.kron(keep25, np.ones((64, 64), np.uint8)).astype(np.float32))
-    w *= np.kron(keep, np.ones((64, 64), np.uint8)).astype(np.float32)
-    packed = packed_of(w)
+    bw = s.upload(w)
     del w
+    wq, ws = s.alloc(K * N), s.alloc(4 * N)
+    s.run(abi.OP_QUANTIZE_I8, X=bw, Y=wq, scales=ws, rows=K, cols=N, axis=abi.QUANT_PER_COLUMN)
+    s.free(bw)
+    dense_w = s.pack(wq, K, N, scales=ws)
+    packed = s.pack(wq, K, N, scales=ws, tile_mask=keep)
+    sparse_w = s.pack(wq, K, N, scales=ws, tile_mask=keep25)
+    s.free(wq)
+    s.free(ws)
     x = synth.normal("c5/A", (M, K))
     bx = s.upload(x)
     a8, sa, c = s.alloc(M * K), s.alloc(4 * M), s.alloc(4 * M * N)

@@ -753,6 +753,29 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_speculative_step(vnpu_cluster_t *cluster,
  * a NULL stream. */
 VNPU_API void *VNPU_CALL vnpu_stream_hip_handle(vnpu_stream_t *stream);
 
+/* MI355X extension (additive; no counterpart in the reference, whose int8
+ * ABI carries no cull mask: MATMUL_I8 is scheduled with a NULL mask at
+ * src/core/scheduler.cpp:385-386, and the culled int8 tile of
+ * src/kernels/kernels.cpp:927-931 is unreachable).  vnpu_pack_weights_i8
+ * with a Wildcat weight-tile mask passed in: tile_mask is
+ * [ceil(K/64)][mask_ld] bytes (host or device memory; mask_ld 0 means
+ * ceil(N/64)), and a zero byte at (kb, g) culls the 64 x 64 weight tile
+ * k in [64 kb, 64 kb + 64), n in [64 g, 64 g + 64) of the K x N weights
+ * (after trans_b): it is packed as zeros, whatever B holds there, so every
+ * MATMUL_I8 with these weights equals one with those tiles of B zeroed (the
+ * column sums are those of the culled weights), and the int8 kernels that
+ * walk only nonzero tiles skip it.  NULL tile_mask is vnpu_pack_weights_i8. */
+VNPU_API vnpu_status_t VNPU_CALL vnpu_pack_weights_i8_masked(vnpu_device_t *device,
+                                                             const int8_t *B,
+                                                             const float *scales,
+                                                             uint32_t K,
+                                                             uint32_t N,
+                                                             uint32_t ldb,
+                                                             uint32_t trans_b,
+                                                             const uint8_t *tile_mask,
+                                                             uint32_t mask_ld,
+                                                             vnpu_packed_weights_t **out_weights);
+
 /* MI355X extension (additive; no counterpart in the reference): ATTENTION_F32
  * that allocates nothing, for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops).  Same arguments and kernels

@@ -1151,10 +1151,14 @@ void execute_command(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t 
 // ---------------------------------------------------------------------------
 
 vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const float *scales,
-                                    uint32_t K, uint32_t N, uint32_t ldb, uint32_t trans_b)
+                                    uint32_t K, uint32_t N, uint32_t ldb, uint32_t trans_b,
+                                    const uint8_t *tile_mask, uint32_t mask_ld)
 {
     const uint32_t ld = ldb ? ldb : (trans_b ? K : N);
     require(ld >= (trans_b ? K : N), "invalid pack ldb");
+    const uint32_t mask_cols = (N + 63) / 64, mask_rows = (K + 63) / 64;
+    const uint32_t mld = mask_ld ? mask_ld : mask_cols;
+    require(!tile_mask || mld >= mask_cols, "invalid pack mask_ld");
     VNPU_HIP(hipSetDevice(dev->hip_device));
     std::unique_ptr<vnpu_packed_weights_t, void (*)(vnpu_packed_weights_t *)> w(
         new vnpu_packed_weights_t(), destroy_packed);
@@ -1179,7 +1183,9 @@ vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const f
     const size_t b_bytes = trans_b ? span(N, K, ld, 1) : span(K, N, ld, 1);
     Stager sg(st);
     const int8_t *Bd = sg.in(B, b_bytes);
-    k::pack_fragments(st, Bd, K, N, ld, trans_b, w->frag, w->Kp, w->Np, sums_dev);
+    const uint8_t *maskd =
+        tile_mask ? sg.in(tile_mask, static_cast<size_t>(mask_rows - 1) * mld + mask_cols) : nullptr;
+    k::pack_fragments(st, Bd, K, N, ld, trans_b, maskd, mld, w->frag, w->Kp, w->Np, sums_dev);
     VNPU_HIP(hipGetLastError());
     // Nonzero 64 x 64 tiles: per 64-column group, the k blocks to walk.
     const uint32_t groups = (w->Np / 16 + 3) / 4, kblocks = w->Kp / 64;

@@ -25,10 +25,11 @@ void quantize_tensor(hipStream_t s, const float *X, int8_t *Y, float *scales, ui
 
 // ---- PACK_WEIGHTS_I8 (pack.hip) ----
 // Writes the fragment layout [Np/16][Kp/64][4][16][16] (zero padded) and the
-// per-column sums [N].
+// per-column sums [N].  A non-null tile_mask ([Kp/64][mask_ld] bytes, device
+// memory) packs the 64 x 64 tiles whose byte is zero as zeros.
 void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint32_t ldb,
-                    uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,
-                    int32_t *column_sums);
+                    uint32_t trans_b, const uint8_t *tile_mask, uint32_t mask_ld, int8_t *frag,
+                    uint32_t Kp, uint32_t Np, int32_t *column_sums);
 // The nonzero 64 x 64 weight tiles of packed fragments: for each group g of
 // four 16-column strips, list[g][0 .. count[g]) = its k blocks (64 deep)
 // holding a nonzero, ascending (flag: [groups][Kp/64] bytes of scratch;

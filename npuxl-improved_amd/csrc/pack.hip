@@ -13,6 +13,10 @@
 // column-strip-major: the Kp/64 blocks of one 16-column strip are one
 // contiguous run, so the decode GEMV streams each strip sequentially.
 //
+// With a Wildcat weight-tile mask (tile_mask[kb * mask_ld + g], one byte per
+// 64 x 64 tile: k block kb, columns 64 g .. 64 g + 63), a zero byte packs its
+// tile as zeros whatever B holds there.
+//
 // Also produced: per-column sums (reference scheduler.cpp:798-800), and for
 // each group of four strips (64 columns, the reference's 64 x 64 cull tile
 // width) the list of its 64-deep k blocks that hold a nonzero weight, which
@@ -25,6 +29,7 @@ namespace {
 
 __global__ __launch_bounds__(256) void pack_frag_kernel(const int8_t *__restrict__ B, uint32_t K,
                                                         uint32_t N, uint32_t ldb, uint32_t trans_b,
+                                                        const uint8_t *__restrict__ tile_mask, uint32_t mask_ld,
                                                         int8_t *__restrict__ frag, uint32_t KT,
                                                         uint64_t chunks)
 {
@@ -38,6 +43,8 @@ __global__ __launch_bounds__(256) void pack_frag_kernel(const int8_t *__restrict
     const uint32_t nt = static_cast<uint32_t>(blk / KT);
     const uint32_t n = nt * 16 + c;
     const uint32_t k0 = kt * 64 + kg * 16;
+    // The 16 k of this chunk lie in k block kt, its column in group n / 64.
+    const bool culled = tile_mask && n < N && tile_mask[static_cast<uint64_t>(kt) * mask_ld + n / 64] == 0;
     union {
         int8_t b[16];
         int4 v;
@@ -46,7 +53,7 @@ __global__ __launch_bounds__(256) void pack_frag_kernel(const int8_t *__restrict
     for (int j = 0; j < 16; ++j) {
         const uint32_t k = k0 + j;
         int8_t v = 0;
-        if (n < N && k < K)
+        if (n < N && k < K && !culled)
             v = trans_b ? B[static_cast<uint64_t>(n) * ldb + k] : B[static_cast<uint64_t>(k) * ldb + n];
         u.b[j] = v;
     }
@@ -127,14 +134,14 @@ void tile_lists(hipStream_t s, const int8_t *frag, uint32_t Kp, uint32_t Np, uin
 }
 
 void pack_fragments(hipStream_t s, const int8_t *B, uint32_t K, uint32_t N, uint32_t ldb,
-                    uint32_t trans_b, int8_t *frag, uint32_t Kp, uint32_t Np,
-                    int32_t *column_sums)
+                    uint32_t trans_b, const uint8_t *tile_mask, uint32_t mask_ld, int8_t *frag,
+                    uint32_t Kp, uint32_t Np, int32_t *column_sums)
 {
     const uint32_t NT = Np / 16, KT = Kp / 64;
     const uint64_t blocks = static_cast<uint64_t>(KT) * NT;
     const uint64_t chunks = blocks * 64;
     pack_frag_kernel<<<dim3(static_cast<uint32_t>((chunks + 255) / 256)), 256, 0, s>>>(
-        B, K, N, ldb, trans_b, frag, KT, chunks);
+        B, K, N, ldb, trans_b, tile_mask, mask_ld, frag, KT, chunks);
     column_sums_kernel<<<dim3(NT), 256, 0, s>>>(frag, KT, N, column_sums);
 }
 

@@ -1145,6 +1145,23 @@ VNPU_API vnpu_status_t VNPU_CALL vnpu_pack_weights_i8(vnpu_device_t *device, con
     });
 }
 
+VNPU_API vnpu_status_t VNPU_CALL vnpu_pack_weights_i8_masked(vnpu_device_t *device, const int8_t *B,
+                                                             const float *scales, uint32_t K, uint32_t N,
+                                                             uint32_t ldb, uint32_t trans_b,
+                                                             const uint8_t *tile_mask, uint32_t mask_ld,
+                                                             vnpu_packed_weights_t **out_weights)
+{
+    if (!device || !B || !out_weights || !K || !N || trans_b > 1) return VNPU_ERR_INVALID_ARGUMENT;
+    *out_weights = nullptr;
+    const uint32_t ld = ldb ? ldb : (trans_b ? K : N);
+    if (ld < (trans_b ? K : N)) return VNPU_ERR_INVALID_ARGUMENT;
+    if (tile_mask && mask_ld && mask_ld < (N + 63) / 64) return VNPU_ERR_INVALID_ARGUMENT;
+    return guard([&]() -> vnpu_status_t {
+        *out_weights = pack_weights(device, B, scales, K, N, ldb, trans_b, tile_mask, mask_ld);
+        return VNPU_OK;
+    });
+}
+
 VNPU_API void VNPU_CALL vnpu_packed_weights_destroy(vnpu_packed_weights_t *weights)
 {
     destroy_packed(weights);

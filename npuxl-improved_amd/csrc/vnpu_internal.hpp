@@ -248,9 +248,12 @@ void execute_command(vnpu_device_t *dev, vnpu_stream_t *s, const vnpu_command_t 
 // nothing.  Throws ArgError for invalid arguments, host pointers or a
 // scratch need above k::kAttnScratchBytes.
 void enqueue_attention_noalloc(vnpu_stream_t *s, const vnpu_attention_f32_args_t &a, ExecStats &st);
-// Pack int8 weights (synchronous); B may be a host or a device pointer.
+// Pack int8 weights (synchronous); B and tile_mask may be host or device
+// pointers.  A non-null tile_mask ([ceil(K/64)][mask_ld] bytes; mask_ld 0 =
+// ceil(N/64)) packs the 64 x 64 tiles whose byte is zero as zeros.
 vnpu_packed_weights_t *pack_weights(vnpu_device_t *dev, const int8_t *B, const float *scales,
-                                    uint32_t K, uint32_t N, uint32_t ldb, uint32_t trans_b);
+                                    uint32_t K, uint32_t N, uint32_t ldb, uint32_t trans_b,
+                                    const uint8_t *tile_mask = nullptr, uint32_t mask_ld = 0);
 void destroy_packed(vnpu_packed_weights_t *w);
 
 bool is_device_pointer(const void *p);

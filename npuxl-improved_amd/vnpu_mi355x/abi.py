@@ -296,6 +296,7 @@ SIGNATURES = {
     "vnpu_buffer_copy": (st, [vp, vp, vp, u64, u32]),
     "vnpu_buffer_memset": (st, [vp, vp, u32, u64]),
     "vnpu_pack_weights_i8": (st, [vp, vp, vp, u32, u32, u32, u32, vp]),
+    "vnpu_pack_weights_i8_masked": (st, [vp, vp, vp, u32, u32, u32, u32, vp, u32, vp]),
     "vnpu_packed_weights_destroy": (None, [vp]),
     "vnpu_packed_weights_info": (st, [vp, vp, vp, vp, vp, vp]),
     "vnpu_matmul_f32": (st, [vp, vp]),

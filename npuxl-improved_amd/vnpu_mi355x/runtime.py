@@ -172,7 +172,10 @@ class Session:
         self.check("vnpu_stream_sync", self.sync())
 
     def pack(self, B: Buffer | np.ndarray, K: int, N: int, scales=None, ldb: int = 0,
-             trans_b: int = 0) -> C.c_void_p:
+             trans_b: int = 0, tile_mask=None, mask_ld: int = 0) -> C.c_void_p:
+        """PACK_WEIGHTS_I8; with tile_mask (uint8 [ceil(K/64), >= ceil(N/64)],
+        or a device Buffer with mask_ld), vnpu_pack_weights_i8_masked: the
+        64 x 64 weight tiles whose byte is zero are packed as zeros."""
         if isinstance(B, np.ndarray):
             B = np.ascontiguousarray(B, dtype=np.int8)
             bptr = B.ctypes.data_as(C.c_void_p)
@@ -186,8 +189,18 @@ class Session:
             scales = np.ascontiguousarray(scales, dtype=np.float32)
             sptr = scales.ctypes.data_as(C.c_void_p)
         w = C.c_void_p()
-        self.check("vnpu_pack_weights_i8", self.lib.vnpu_pack_weights_i8(
-            self.dev, bptr, sptr, K, N, ldb, trans_b, C.byref(w)))
+        if tile_mask is None:
+            self.check("vnpu_pack_weights_i8", self.lib.vnpu_pack_weights_i8(
+                self.dev, bptr, sptr, K, N, ldb, trans_b, C.byref(w)))
+        else:
+            if isinstance(tile_mask, Buffer):
+                mptr = C.c_void_p(tile_mask.ptr)
+            else:
+                tile_mask = np.ascontiguousarray(tile_mask, dtype=np.uint8)
+                mask_ld = mask_ld or tile_mask.shape[1]
+                mptr = tile_mask.ctypes.data_as(C.c_void_p)
+            self.check("vnpu_pack_weights_i8_masked", self.lib.vnpu_pack_weights_i8_masked(
+                self.dev, bptr, sptr, K, N, ldb, trans_b, mptr, mask_ld, C.byref(w)))
         self._packed.append(w)
         return w
 

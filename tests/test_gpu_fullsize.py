@@ -196,6 +196,30 @@ def test_config5_cull_int8_4096_full(gpu):
     assert _bits_equal(got, oracle.matmul_i8_blas(ha, hq, has, hs))
 
 
+def test_config5_cull_int8_4096_mask_passed_in(gpu):
+    """Config 5 with the mask passed in: the dense weights quantized per
+    column, the seeded Bernoulli 64 x 64 tile mask handed to
+    vnpu_pack_weights_i8_masked, bit-exact with the oracle on the quantized
+    weights with the culled tiles zeroed."""
+    M = K = N = 4096
+    w = synth.normal("c5/W", (K, N), 0.02)
+    keep = synth.bernoulli_mask("c5/tiles", (K // 64, N // 64), 0.5)
+    wq, ws, hq, hs = _quantized_weights(gpu, K, N, w)
+    del w
+    packed = gpu.pack(wq, K, N, scales=ws, tile_mask=keep)
+    gpu.free(wq)
+    gpu.free(ws)
+    a8, sa, ha, has = _quantized_rows(gpu, synth.normal("c5/A", (M, K)))
+    c = gpu.alloc(4 * M * N)
+    gpu.run(abi.OP_MATMUL_I8, A=a8, B=packed, scale_a=sa, C=c, M=M, K=K, N=N)
+    got = gpu.download(c, np.float32, (M, N))
+    gpu.release_packed(packed)
+    for b in (a8, sa, c):
+        gpu.free(b)
+    hq *= np.kron(keep, np.ones((64, 64), np.uint8)).astype(np.int8)
+    assert _bits_equal(got, oracle.matmul_i8_blas(ha, hq, has, hs))
+
+
 def test_config5_mtp_head_softmax_full(gpu):
     """Config 5: MTP head [4,4096] x [4096,32000] f32 then SOFTMAX over the
     vocabulary, one batch (the bench's tensors)."""

@@ -997,3 +997,65 @@ def test_int8_zero_tile_strip_kernel(gpu, M, K, N, density, epi, use_bias):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     else:
         assert rel(got, want) <= 1e-6
+
+
+@pytest.mark.parametrize("M,K,N,density,trans_b,ldb,mask_ld,on_device", [
+    (512, 1024, 512, 0.25, 0, 0, 0, False),      # strip kernel density, host mask
+    (512, 1024, 512, 0.5, 0, 0, 0, True),        # config 5's density (dense kernels), device mask
+    (300, 1000, 520, 0.3, 1, 1003, 11, False),   # ragged K and N (partial tiles), trans_b, ldb > K, mask_ld > groups
+    (8, 4096, 4096, 0.5, 0, 0, 0, False),        # decode GEMV over culled weights
+    (64, 640, 200, 0.0, 0, 0, 5, True),          # every tile culled
+])
+def test_pack_weights_i8_masked(gpu, M, K, N, density, trans_b, ldb, mask_ld, on_device):
+    """vnpu_pack_weights_i8_masked: the weights are dense random int8, the
+    Wildcat 64 x 64 weight-tile mask is passed in, and every MATMUL_I8 with
+    the packed weights equals the oracle's on B with the culled tiles zeroed
+    (bit-exact), with the culled weights' column sums, on whichever kernel
+    the shape and density select."""
+    Bl = RNG.integers(-128, 128, (K, N)).astype(np.int8)          # logical K x N
+    A = RNG.integers(-128, 128, (M, K)).astype(np.int8)
+    rows, groups = (K + 63) // 64, (N + 63) // 64
+    ld_m = mask_ld or groups
+    mask = np.full((rows, ld_m), 7, np.uint8)                     # bytes past the groups are ignored
+    mask[:, :groups] = (RNG.random((rows, groups)) < density).astype(np.uint8) * 3
+    culled = np.kron((mask[:, :groups] != 0).astype(np.int8), np.ones((64, 64), np.int8))[:K, :N]
+    if trans_b:
+        ld = ldb or K
+        Bs = np.zeros((N, ld), np.int8)
+        Bs[:, :K] = Bl.T
+    else:
+        ld = ldb or N
+        Bs = np.zeros((K, ld), np.int8)
+        Bs[:, :N] = Bl
+    sa = (RNG.random(M).astype(np.float32) + 0.5) / 127
+    sb = (RNG.random(N).astype(np.float32) + 0.5) / 127
+    mbuf = gpu.upload(mask) if on_device else None
+    w = gpu.pack(Bs, K, N, scales=sb, ldb=ldb, trans_b=trans_b,
+                 tile_mask=mbuf if on_device else mask, mask_ld=ld_m)
+    try:
+        got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa)
+        _, _, _, _, sums = gpu.unpack_info(w)
+    finally:
+        gpu.release_packed(w)
+        if mbuf is not None:
+            gpu.free(mbuf)
+    Bm = Bl * culled
+    assert np.array_equal(sums, Bm.astype(np.int64).sum(axis=0).astype(np.int32))
+    want = oracle.matmul_i8_blas(A, Bm, sa, sb, None, 0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if 0 < density < 1:
+        assert not np.array_equal(want, oracle.matmul_i8_blas(A, Bl, sa, sb, None, 0))
+
+
+def test_pack_weights_i8_masked_rejects_short_mask_ld(gpu):
+    B = np.ones((128, 200), np.int8)
+    mask = np.ones((2, 4), np.uint8)
+    w = C.c_void_p()
+    st = gpu.lib.vnpu_pack_weights_i8_masked(gpu.dev, B.ctypes.data_as(C.c_void_p), None, 128, 200, 0, 0,
+                                             mask.ctypes.data_as(C.c_void_p), 3, C.byref(w))
+    assert st == abi.ERR_INVALID_ARGUMENT and not w.value
+    # NULL mask: vnpu_pack_weights_i8
+    st = gpu.lib.vnpu_pack_weights_i8_masked(gpu.dev, B.ctypes.data_as(C.c_void_p), None, 128, 200, 0, 0,
+                                             None, 0, C.byref(w))
+    assert st == abi.OK and w.value
+    gpu.lib.vnpu_packed_weights_destroy(w)
