@@ -17,38 +17,41 @@
 
 namespace {
 
-// qkv [rows][3d] (row r = b*T + t) -> q, k, v [B][H][T][D]; one float4 per thread.
+// qkv [rows][3d] (row r = b*T + t) -> q, k, v [B][H][T][D]; one float4 per
+// thread, grid (chunks of 256 float4 of a row, row groups): a row's index is
+// the grid's y (rows past gridDim.y take further trips), so the index math
+// is 32-bit with no 64-bit division.
 __global__ __launch_bounds__(256) void split_qkv_kernel(const float4 *__restrict__ qkv,
                                                         float4 *__restrict__ q, float4 *__restrict__ k,
-                                                        float4 *__restrict__ v, uint32_t T, uint32_t H,
-                                                        uint32_t D, uint64_t total4)
+                                                        float4 *__restrict__ v, uint32_t rows, uint32_t T,
+                                                        uint32_t H, uint32_t D)
 {
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= total4) return;
-    const uint32_t d4 = (H * D) >> 2;              // float4s per q/k/v row part
-    const uint64_t r = i / (3 * d4);
-    const uint32_t c4 = static_cast<uint32_t>(i % (3 * d4));
-    const uint32_t which = c4 / d4, w4 = c4 % d4;
-    const uint32_t h = (w4 * 4) / D, dd4 = ((w4 * 4) % D) >> 2;
-    const uint64_t b = r / T, t = r % T;
-    const uint64_t dst = (((b * H + h) * T + t) * D >> 2) + dd4;
+    const uint32_t d4 = (H * D) >> 2, D4 = D >> 2;   // float4s per q/k/v row part, per head
+    const uint32_t c4 = blockIdx.x * 256 + threadIdx.x;
+    if (c4 >= 3 * d4) return;
+    const uint32_t which = c4 / d4, w4 = c4 - which * d4;
+    const uint32_t h = w4 / D4, dd4 = w4 - h * D4;
     float4 *out = which == 0 ? q : which == 1 ? k : v;
-    out[dst] = qkv[i];
+    for (uint32_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const uint32_t b = r / T, t = r - b * T;
+        out[(static_cast<uint64_t>(b * H + h) * T + t) * D4 + dd4] = qkv[static_cast<uint64_t>(r) * 3 * d4 + c4];
+    }
 }
 
-// o [B][H][T][D] -> y [rows][H*D]; one float4 per thread (coalesced writes).
+// o [B][H][T][D] -> y [rows][H*D]; one float4 per thread (coalesced writes),
+// the same grid as split_qkv_kernel.
 __global__ __launch_bounds__(256) void merge_heads_kernel(const float4 *__restrict__ o,
-                                                          float4 *__restrict__ y, uint32_t T,
-                                                          uint32_t H, uint32_t D, uint64_t total4)
+                                                          float4 *__restrict__ y, uint32_t rows, uint32_t T,
+                                                          uint32_t H, uint32_t D)
 {
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= total4) return;
-    const uint32_t d4 = (H * D) >> 2;
-    const uint64_t r = i / d4;
-    const uint32_t w4 = static_cast<uint32_t>(i % d4);
-    const uint32_t h = (w4 * 4) / D, dd4 = ((w4 * 4) % D) >> 2;
-    const uint64_t b = r / T, t = r % T;
-    y[i] = o[(((b * H + h) * T + t) * D >> 2) + dd4];
+    const uint32_t d4 = (H * D) >> 2, D4 = D >> 2;
+    const uint32_t w4 = blockIdx.x * 256 + threadIdx.x;
+    if (w4 >= d4) return;
+    const uint32_t h = w4 / D4, dd4 = w4 - h * D4;
+    for (uint32_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const uint32_t b = r / T, t = r - b * T;
+        y[static_cast<uint64_t>(r) * d4 + w4] = o[(static_cast<uint64_t>(b * H + h) * T + t) * D4 + dd4];
+    }
 }
 
 // k, v [B][H][T][D] -> caches [B][H][S][D] at rows past .. past+T-1.
@@ -70,6 +73,11 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float4 *__restrict
 }
 
 inline uint32_t blocks_for(uint64_t n) { return static_cast<uint32_t>((n + 255) / 256); }
+// Grid of the row-layout kernels: chunks of 256 float4 per row, up to 65535 row groups.
+inline dim3 row_grid(uint64_t f4_per_row, uint64_t rows)
+{
+    return dim3(blocks_for(f4_per_row), static_cast<uint32_t>(rows < 65535 ? rows : 65535));
+}
 
 // Host twins of the three layout kernels (reference CPU build).
 void split_qkv_host(const float *qkv, float *q, float *k, float *v, uint64_t rows, uint32_t T,
@@ -200,10 +208,10 @@ extern "C" vnpu_status_t vnpu_block_run(const vnpu_backend_v1_t *api, vnpu_strea
     gemm_i8(cmds, b->xn, b->a8, b->scale_a, w->qkv, b->qkv, rows, d, 3 * d, true);
     if (!submit(cmds)) return rc;
     if (hs) {
-        const uint64_t n4 = rd * 3 / 4;
-        split_qkv_kernel<<<dim3(blocks_for(n4)), 256, 0, hs>>>(
+        split_qkv_kernel<<<row_grid(3 * d / 4, rows), 256, 0, hs>>>(
             reinterpret_cast<const float4 *>(b->qkv), reinterpret_cast<float4 *>(b->q),
-            reinterpret_cast<float4 *>(b->k), reinterpret_cast<float4 *>(b->v), T, H, D, n4);
+            reinterpret_cast<float4 *>(b->k), reinterpret_cast<float4 *>(b->v), static_cast<uint32_t>(rows), T, H,
+            D);
         if (!launched()) return rc;
     } else {
         split_qkv_host(b->qkv, b->q, b->k, b->v, rows, T, H, D);
@@ -260,9 +268,9 @@ extern "C" vnpu_status_t vnpu_block_run(const vnpu_backend_v1_t *api, vnpu_strea
     } else {
         if (!submit(cmds)) return rc;
         if (hs) {
-            const uint64_t n4 = rd / 4;
-            merge_heads_kernel<<<dim3(blocks_for(n4)), 256, 0, hs>>>(
-                reinterpret_cast<const float4 *>(b->o), reinterpret_cast<float4 *>(b->att), T, H, D, n4);
+            merge_heads_kernel<<<row_grid(d / 4, rows), 256, 0, hs>>>(
+                reinterpret_cast<const float4 *>(b->o), reinterpret_cast<float4 *>(b->att),
+                static_cast<uint32_t>(rows), T, H, D);
             if (!launched()) return rc;
         } else {
             merge_heads_host(b->o, b->att, rows, T, H, D);
