@@ -395,6 +395,9 @@ __device__ __forceinline__ void rotate4(const float4 a, const float4 b, const fl
                      a.w * s[3] + b.w * c[3]);
 }
 
+// Grid: x = chunks of kThreads (token, pair group) items of one (batch, head),
+// y = (batch, head) pairs (those past gridDim.y take further trips), so the
+// index math is 32-bit (seq * head_dim / 8 < 2^32 is required).
 __global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ Q, float *__restrict__ K,
                                                             const int32_t *__restrict__ positions,
                                                             uint64_t bh_count, uint32_t q_seq,
@@ -405,44 +408,43 @@ __global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ 
                                                             const float2 *__restrict__ cs, uint32_t cs_rows)
 {
     const uint32_t half4 = head_dim / 8;
-    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (idx >= bh_count * seq * half4) return;
-    const uint32_t j4 = static_cast<uint32_t>(idx % half4);
-    const uint64_t tok = idx / half4;
-    const uint32_t t = static_cast<uint32_t>(tok % seq);
-    const uint64_t bh = tok / seq;
+    const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= seq * half4) return;
+    const uint32_t t = idx / half4, j4 = idx - t * half4;
     const int32_t p = positions ? positions[t] : static_cast<int32_t>(t + offset);
-    // Q's and K's pairs load before anything is stored, through raw buffers
-    // over the row (an empty range when the row is absent: zero in, writes
-    // dropped), so no branch sits between the loads and the stores and the
-    // K loads do not wait behind the Q stores.
-    const bool has_q = Q && t < q_seq, has_k = K && t < k_seq;
-    const uint32_t row_bytes = head_dim * 4u;
-    float *qrow = has_q ? Q + (bh * q_seq + t) * head_dim : Q, *krow = has_k ? K + (bh * k_seq + t) * head_dim : K;
-    const auto rq = __builtin_amdgcn_make_buffer_rsrc(qrow, 0, static_cast<int>(has_q ? row_bytes : 0u), kRawBuf);
-    const auto rk = __builtin_amdgcn_make_buffer_rsrc(krow, 0, static_cast<int>(has_k ? row_bytes : 0u), kRawBuf);
-    const uint32_t o0 = j4 * 16u, o1 = (half4 + j4) * 16u;
-    auto ld = [](__amdgpu_buffer_rsrc_t r, uint32_t o) {
-        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
-    };
-    const float4 qa = ld(rq, o0), qb = ld(rq, o1), ka = ld(rk, o0), kb = ld(rk, o1);
     float c[4], s[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) rope_cos_sin(p, 4 * j4 + e, head_dim / 2, scaling, inv_freq, cs, cs_rows, c[e], s[e]);
-    auto st = [](__amdgpu_buffer_rsrc_t r, uint32_t o, float4 x) {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32, x), r, o, 0, 0);
-    };
-    float4 lo, hi;
-    rotate4(qa, qb, c, s, lo, hi);
-    st(rq, o0, lo);
-    st(rq, o1, hi);
-    // Q and K the same row: K is rotated again, from Q's result, as in
-    // command order
-    const bool same = has_q && qrow == krow;
-    const float4 ka2 = same ? lo : ka, kb2 = same ? hi : kb;
-    rotate4(ka2, kb2, c, s, lo, hi);
-    st(rk, o0, lo);
-    st(rk, o1, hi);
+    for (uint64_t bh = blockIdx.y; bh < bh_count; bh += gridDim.y) {
+        // Q's and K's pairs load before anything is stored, through raw buffers
+        // over the row (an empty range when the row is absent: zero in, writes
+        // dropped), so no branch sits between the loads and the stores and the
+        // K loads do not wait behind the Q stores.
+        const bool has_q = Q && t < q_seq, has_k = K && t < k_seq;
+        const uint32_t row_bytes = head_dim * 4u;
+        float *qrow = has_q ? Q + (bh * q_seq + t) * head_dim : Q, *krow = has_k ? K + (bh * k_seq + t) * head_dim : K;
+        const auto rq = __builtin_amdgcn_make_buffer_rsrc(qrow, 0, static_cast<int>(has_q ? row_bytes : 0u), kRawBuf);
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(krow, 0, static_cast<int>(has_k ? row_bytes : 0u), kRawBuf);
+        const uint32_t o0 = j4 * 16u, o1 = (half4 + j4) * 16u;
+        auto ld = [](__amdgpu_buffer_rsrc_t r, uint32_t o) {
+            return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
+        };
+        const float4 qa = ld(rq, o0), qb = ld(rq, o1), ka = ld(rk, o0), kb = ld(rk, o1);
+        auto st = [](__amdgpu_buffer_rsrc_t r, uint32_t o, float4 x) {
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32, x), r, o, 0, 0);
+        };
+        float4 lo, hi;
+        rotate4(qa, qb, c, s, lo, hi);
+        st(rq, o0, lo);
+        st(rq, o1, hi);
+        // Q and K the same row: K is rotated again, from Q's result, as in
+        // command order
+        const bool same = has_q && qrow == krow;
+        const float4 ka2 = same ? lo : ka, kb2 = same ? hi : kb;
+        rotate4(ka2, kb2, c, s, lo, hi);
+        st(rk, o0, lo);
+        st(rk, o1, hi);
+    }
 }
 
 enum EwOp { EW_SWIGLU = 0, EW_ADD = 1, EW_MUL = 2, EW_GELU = 3 };
@@ -869,10 +871,12 @@ void rope(hipStream_t s, float *Q, float *K, const int32_t *positions, uint32_t 
     if (!total) return;
     const bool vec = !interleaved && head_dim % 8 == 0 &&
                      ((reinterpret_cast<uintptr_t>(Q) | reinterpret_cast<uintptr_t>(K)) % 16 == 0);
-    if (vec) {
-        const uint64_t t4 = total / 4;
-        rope_vec_kernel<<<dim3(static_cast<uint32_t>((t4 + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
-            Q, K, positions, bh, q_seq, k_seq, seq, head_dim, position_offset, scaling, inv_freq, cs, cs_rows);
+    const uint64_t per_bh4 = static_cast<uint64_t>(seq) * (head_dim / 8);
+    if (vec && per_bh4 + kThreads < (1ull << 32)) {
+        const dim3 grid(static_cast<uint32_t>((per_bh4 + kThreads - 1) / kThreads),
+                        static_cast<uint32_t>(bh < 65535 ? bh : 65535));
+        rope_vec_kernel<<<grid, kThreads, 0, s>>>(Q, K, positions, bh, q_seq, k_seq, seq, head_dim, position_offset,
+                                                  scaling, inv_freq, cs, cs_rows);
         return;
     }
     rope_kernel<<<dim3(static_cast<uint32_t>((total + kThreads - 1) / kThreads)), kThreads, 0, s>>>(
