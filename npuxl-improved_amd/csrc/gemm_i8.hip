@@ -485,7 +485,6 @@ __global__ __launch_bounds__(strip::kThreads) void gemm_i8_strip(I8Gemm p, uint3
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int fr = lane & 15, fg = lane >> 4;
 
     // XCD-aware order: each XCD takes a contiguous run of tiles, column
     // groups fastest, so its L2 keeps the run's row tiles of A (512 rows x K)
