@@ -1317,7 +1317,7 @@ void gemm_i8(hipStream_t s, const I8Gemm &p, int8_t *ws)
     uint32_t v = p.variant;
     if (ws && use_strip(p)) v = kI8Strip;
     if (((v == kI8Wide || v == kI8Wide192) && !wide_ok) || (v == kI8Wave8 && !k128) || (v == kI8Pipe && !aligned) ||
-        v == kI8Strip && !(ws && use_strip(p)))
+        (v == kI8Strip && !(ws && use_strip(p))))
         v = kI8Auto;
     uint32_t mix_a = 0, mix_b = 0;   // tile columns of 256 and 192 (mixed grid)
     if (v == kI8Auto) {
