@@ -124,3 +124,39 @@ def test_random_reference_order_small_shapes(gpu):
         V = rng.standard_normal((1, h, sk, d)).astype(np.float32)
         assert same(g.attention(gpu, Q, K, V, None, causal), oracle.attention_avx2(Q, K, V, None, causal)), \
             (h, sq, sk, d, causal)
+
+
+def test_random_masked_pack_matmul_i8(gpu):
+    """Seeded random vnpu_pack_weights_i8_masked calls: random K, N, kept-tile
+    density (from all tiles culled to none), trans_b and padded mask rows,
+    then MATMUL_I8 at decode and prefill row counts (the GEMV, the dense
+    GEMM kernels and, at low density, the kernel that walks only nonzero
+    tiles): bit-exact with the oracle on the weights with the culled 64 x 64
+    tiles zeroed, column sums included."""
+    rng = np.random.default_rng(20261210)
+    for it in range(16):
+        M = int(rng.choice([1, 5, 8, 64, 300, 512]))
+        K = int(64 * rng.integers(1, 48)) if rng.integers(2) else int(rng.integers(1, 3000))
+        N = int(rng.integers(1, 3000))
+        density = float(rng.choice([0.0, 0.1, 0.3, 0.5, 0.9, 1.0]))
+        trans_b = int(rng.integers(2))
+        rows, groups = (K + 63) // 64, (N + 63) // 64
+        mask_ld = groups + int(rng.integers(0, 3))
+        mask = np.zeros((rows, mask_ld), np.uint8)
+        mask[:, :groups] = rng.random((rows, groups)) < density
+        Bl = rng.integers(-128, 128, size=(K, N)).astype(np.int8)
+        A = rng.integers(-128, 128, size=(M, K)).astype(np.int8)
+        sa = (rng.random(M).astype(np.float32) + 0.5) / 127
+        sb = (rng.random(N).astype(np.float32) + 0.5) / 127
+        w = gpu.pack(np.ascontiguousarray(Bl.T) if trans_b else Bl, K, N, scales=sb, trans_b=trans_b,
+                     tile_mask=mask, mask_ld=mask_ld)
+        try:
+            got = g.matmul_i8(gpu, A, w, M, K, N, scale_a=sa)
+            sums = gpu.unpack_info(w)[4]
+        finally:
+            gpu.release_packed(w)
+        Bm = Bl * np.kron(mask[:, :groups], np.ones((64, 64), np.uint8))[:K, :N].astype(np.int8)
+        case = (it, M, K, N, density, trans_b, mask_ld)
+        assert np.array_equal(sums, Bm.astype(np.int64).sum(axis=0).astype(np.int32)), case
+        want = oracle.matmul_i8_blas(A, Bm, sa, sb, None, 0)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), case
