@@ -781,98 +781,9 @@ bool launch_row_chain(hipStream_t s, const RowChain &p)
     return true;
 }
 
-// SWIGLU -> QUANTIZE_I8 over many rows, pipelined: one 1024-thread
-// workgroup per CU walks rows blockIdx.x, + gridDim.x, ..., and loads the
-// next row's gate and up before it computes and stores the current one, so
-// one row's loads overlap the previous row's SiLU math and stores (with one
-// row per workgroup every workgroup loads, computes and stores at the same
-// time).  Each element's arithmetic, its range tail and the row's max are
-// row_chain_kernel's, so the outputs are the same bits.  Rows are disjoint,
-// and Y is either disjoint from the inputs or the very same rows (checked by
-// the caller), so reading row r + gridDim.x before writing row r is the
-// commands' order.
-template <int VPT>
-__global__ __launch_bounds__(1024) void swiglu_quant_rows_kernel(RowChain p)
-{
-    constexpr int NT = 1024;
-    __shared__ float red[NT / 64];
-    const uint32_t n4 = p.cols >> 2, row_bytes = p.cols * 4u;
-    const uint32_t lane_off = threadIdx.x * 16u;
-    const EwTail tl = ew_tail(static_cast<uint64_t>(p.rows) * p.cols, p.grain);
-    auto rsrc = [&](const void *base, uint32_t bytes) {
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), kRawBuf);
-    };
-    auto ld4 = [&](__amdgpu_buffer_rsrc_t r, int i) {
-        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off + i * NT * 16u, 0, 0));
-    };
-    // a row past the last reads zeros (empty buffers) and is never processed
-    auto load = [&](uint32_t row, float4 (&g)[VPT], float4 (&u)[VPT]) {
-        const bool live = row < p.rows;
-        const uint64_t off = static_cast<uint64_t>(live ? row : 0u) * n4 * 4u;
-        const auto rg = rsrc(p.A + off, live ? row_bytes : 0u), ru = rsrc(p.B + off, live ? row_bytes : 0u);
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            g[i] = ld4(rg, i);
-            u[i] = ld4(ru, i);
-        }
-    };
-    auto process = [&](uint32_t row, float4 (&g)[VPT], const float4 (&u)[VPT]) {
-        const uint64_t off = static_cast<uint64_t>(row) * n4;
-        const auto ry = rsrc(p.Y + off * 4, row_bytes);
-        float m = 0.0f;
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const uint32_t j = threadIdx.x + i * NT;
-            const uint32_t t = tl.mask4(4 * (off + j));
-            float4 v = make_float4(ew<EW_SWIGLU>(g[i].x, u[i].x, p.alpha, p.beta, t & 1),
-                                   ew<EW_SWIGLU>(g[i].y, u[i].y, p.alpha, p.beta, t & 2),
-                                   ew<EW_SWIGLU>(g[i].z, u[i].z, p.alpha, p.beta, t & 4),
-                                   ew<EW_SWIGLU>(g[i].w, u[i].w, p.alpha, p.beta, t & 8));
-            if (j >= n4) v = make_float4(0.f, 0.f, 0.f, 0.f);   // slots past the row
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32, v), ry, lane_off + i * NT * 16u, 0, 0);
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-            g[i] = v;
-        }
-        const float scale = dev::scale_from_max(block_max_n<NT>(m, red));
-        const float inv = __fdiv_rn(1.0f, scale);
-        if (threadIdx.x == 0) p.scales[row] = scale;
-        const auto rq = rsrc(p.Q + off * 4, p.cols);
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const char4 q = make_char4(dev::q8(g[i].x, inv), dev::q8(g[i].y, inv), dev::q8(g[i].z, inv),
-                                       dev::q8(g[i].w, inv));
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, q), rq,
-                                                  threadIdx.x * 4u + i * NT * 4u, 0, 0);
-        }
-    };
-    float4 ga[VPT], ua[VPT], gb[VPT], ub[VPT];
-    const uint32_t step = gridDim.x;
-    uint32_t r = blockIdx.x;
-    load(r, ga, ua);
-    for (; r < p.rows; r += 2 * step) {
-        load(r + step, gb, ub);
-        process(r, ga, ua);
-        if (r + step >= p.rows) break;
-        load(r + 2 * step, ga, ua);
-        process(r + step, gb, ub);
-    }
-}
-
 bool launch_swiglu_chain(hipStream_t s, const RowChain &p)
 {
     const dim3 grid(p.rows);
-    // many rows: one pipelined 1024-thread workgroup per CU
-    const uint32_t n4 = p.cols / 4;
-    if (p.rows >= 2 * cu_count()) {
-        const dim3 pgrid(cu_count());
-        if (n4 <= 1024)
-            swiglu_quant_rows_kernel<1><<<pgrid, dim3(1024), 0, s>>>(p);
-        else if (n4 <= 2048)
-            swiglu_quant_rows_kernel<2><<<pgrid, dim3(1024), 0, s>>>(p);
-        else
-            swiglu_quant_rows_kernel<3><<<pgrid, dim3(1024), 0, s>>>(p);
-        return true;
-    }
     // many rows: 256 threads, as few float4 slots per thread as the row needs
     // (unused slots still hold registers and cut the waves per SIMD)
     if (p.rows >= 256 && p.cols / 4 <= 4 * 256)
