@@ -58,18 +58,21 @@ __global__ __launch_bounds__(256) void merge_heads_kernel(const float4 *__restri
 __global__ __launch_bounds__(256) void kv_append_kernel(const float4 *__restrict__ k,
                                                         const float4 *__restrict__ v,
                                                         float4 *__restrict__ kc, float4 *__restrict__ vc,
-                                                        uint32_t T, uint32_t S, uint32_t D,
-                                                        uint32_t past, uint64_t total4)
+                                                        uint32_t bh_count, uint32_t T, uint32_t S, uint32_t D,
+                                                        uint32_t past)
 {
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= total4) return;
+    // grid: x = chunks of one (batch, head)'s T x D/4 float4, y = (batch,
+    // head) pairs (those past gridDim.y take further trips)
     const uint32_t D4 = D >> 2;
-    const uint64_t bh = i / (static_cast<uint64_t>(T) * D4);
-    const uint32_t rem = static_cast<uint32_t>(i % (static_cast<uint64_t>(T) * D4));
-    const uint32_t t = rem / D4, dd4 = rem % D4;
-    const uint64_t dst = (bh * S + past + t) * D4 + dd4;
-    kc[dst] = k[i];
-    vc[dst] = v[i];
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= T * D4) return;
+    const uint32_t t = i / D4, dd4 = i - t * D4;
+    for (uint32_t bh = blockIdx.y; bh < bh_count; bh += gridDim.y) {
+        const uint64_t src = static_cast<uint64_t>(bh) * T * D4 + i;
+        const uint64_t dst = (static_cast<uint64_t>(bh) * S + past + t) * D4 + dd4;
+        kc[dst] = k[src];
+        vc[dst] = v[src];
+    }
 }
 
 inline uint32_t blocks_for(uint64_t n) { return static_cast<uint32_t>((n + 255) / 256); }
@@ -234,11 +237,11 @@ extern "C" vnpu_status_t vnpu_block_run(const vnpu_backend_v1_t *api, vnpu_strea
     if (!submit(cmds)) return rc;
     if (decode) {
         if (hs) {
-            const uint64_t n4 = rd / 4;
-            kv_append_kernel<<<dim3(blocks_for(n4)), 256, 0, hs>>>(
+            const dim3 grid = row_grid(static_cast<uint64_t>(T) * D / 4, static_cast<uint64_t>(B) * H);
+            kv_append_kernel<<<grid, 256, 0, hs>>>(
                 reinterpret_cast<const float4 *>(b->k), reinterpret_cast<const float4 *>(b->v),
-                reinterpret_cast<float4 *>(b->k_cache), reinterpret_cast<float4 *>(b->v_cache), T,
-                cfg->cache_len, D, cfg->past, n4);
+                reinterpret_cast<float4 *>(b->k_cache), reinterpret_cast<float4 *>(b->v_cache), B * H, T,
+                cfg->cache_len, D, cfg->past);
             if (!launched()) return rc;
         } else {
             kv_append_host(b->k, b->v, b->k_cache, b->v_cache, static_cast<uint64_t>(B) * H, T,
