@@ -373,7 +373,19 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
 //     two strips per workgroup, <8,2,2> (M=8 N=11008 11.9 -> 11.1 us with
 //     <8,4,1>, then N=12288 11.8 -> 11.5 us and N=8200 10.6 -> 9.9 us with two
 //     strips); below, <16,2,1> (M=8 N=4096 6.9 -> 6.2 us).
+//   * one problem whose two-strip grid has more workgroups than CUs but
+//     whose three-strip grid has no more (513-768 strips on 256 CUs): three
+//     strips per workgroup, <8,2,3>, so no CU streams twice the bytes of
+//     another (768 strips at N = 12288: 384 workgroups of two strips leave
+//     half the CUs with two of them).  M=8 N=12288 11.8 -> 11.3 us, N=11008
+//     11.4 -> 10.7 us, M=16 N=12288 14.1 -> 12.6 us; the pair grids keep two
+//     strips (two problems of 688 strips balance no better with three).
 int mfma_variant(uint32_t NT) { return NT >= 1024 ? 0 : NT >= 512 ? 1 : 2; }
+int mfma_variant_one(uint32_t NT)
+{
+    const int v = mfma_variant(NT);
+    return v == 1 && (NT + 1) / 2 > cu_count() && (NT + 2) / 3 <= cu_count() ? 3 : v;
+}
 
 // k extent (a multiple of 64) of one staged chunk of M activation rows: below
 // 512 strips both kernels run one 16-wave workgroup per strip, and when those
@@ -393,10 +405,9 @@ void lds_optin()
         done = hipFuncSetAttribute(reinterpret_cast<const void *>(Kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    static_cast<int>(kLdsAOwnCu)) == hipSuccess;
 }
-uint32_t mfma_grid(uint32_t NT)
+uint32_t mfma_grid(uint32_t NT, int v)
 {
-    const int v = mfma_variant(NT);
-    return v == 0 ? (NT + 3) / 4 : v == 1 ? (NT + 1) / 2 : NT;
+    return v == 0 ? (NT + 3) / 4 : v == 1 ? (NT + 1) / 2 : v == 3 ? (NT + 2) / 3 : NT;
 }
 
 template <int M>
@@ -404,8 +415,9 @@ void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t
                       uint32_t chunk_k)
 {
     // above 16 rows the wave sums ([W][T][M][16] int32, 64 W T M bytes; W T =
-    // 16 in every variant) reuse the activation LDS
-    const size_t lds = std::max<size_t>(static_cast<size_t>(chunk_k) * M, M > 16 ? 64u * 16u * M : 0u);
+    // 24 for <8,2,3>, 16 in the other variants) reuse the activation LDS
+    const size_t wt = variant == 3 ? 24u : 16u;
+    const size_t lds = std::max<size_t>(static_cast<size_t>(chunk_k) * M, M > 16 ? 64u * wt * M : 0u);
     const dim3 grid(grid0 + grid1);
     if (variant == 0) {
         if (M > 16) lds_optin<gemv_i8_mfma<M, 4, 4, 4>>();
@@ -413,6 +425,9 @@ void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t
     } else if (variant == 1) {
         if (M > 16) lds_optin<gemv_i8_mfma<M, 8, 2, 2>>();
         gemv_i8_mfma<M, 8, 2, 2><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
+    } else if (variant == 3) {
+        if (M > 16) lds_optin<gemv_i8_mfma<M, 8, 2, 3>>();
+        gemv_i8_mfma<M, 8, 2, 3><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
     } else {
         lds_optin<gemv_i8_mfma<M, 16, 2, 1>>();
         gemv_i8_mfma<M, 16, 2, 1><<<grid, 1024, lds, s>>>(ps, grid0, chunk_k);
@@ -428,7 +443,8 @@ void launch_m(hipStream_t s, const I8Gemm &p)
     if constexpr (M >= 5) {
         I8GemmPair ps;
         ps.p[0] = ps.p[1] = p;
-        launch_mfma_pair<M>(s, ps, mfma_variant(NT), mfma_grid(NT), 0, chunk_k);
+        const int v = mfma_variant_one(NT);
+        launch_mfma_pair<M>(s, ps, v, mfma_grid(NT, v), 0, chunk_k);
     } else if constexpr (M == 2) {
         if (NT >= 512) {
             gemv_i8_kernel<M, 4, 2, 1><<<dim3(NT), 256, lds, s>>>(p, chunk_k);
@@ -483,11 +499,13 @@ bool gemv_i8_pair(hipStream_t s, const I8Gemm &p0, const I8Gemm &p1)
     if (mfma_variant(nt0) != mfma_variant(nt1)) return false;
     const uint32_t chunk_k = chunk_k_for(p0.Kp, p0.M, mfma_variant(nt0) == 2 ? nt0 + nt1 : 512);
     const I8GemmPair ps{{p0, p1}};
+    const int v = mfma_variant(nt0);
+    const uint32_t g0 = mfma_grid(nt0, v), g1 = mfma_grid(nt1, v);
     switch (p0.M) {
-    case 5: launch_mfma_pair<5>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;
-    case 6: launch_mfma_pair<6>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;
-    case 7: launch_mfma_pair<7>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;
-    default: launch_mfma_pair<8>(s, ps, mfma_variant(nt0), mfma_grid(nt0), mfma_grid(nt1), chunk_k); break;
+    case 5: launch_mfma_pair<5>(s, ps, v, g0, g1, chunk_k); break;
+    case 6: launch_mfma_pair<6>(s, ps, v, g0, g1, chunk_k); break;
+    case 7: launch_mfma_pair<7>(s, ps, v, g0, g1, chunk_k); break;
+    default: launch_mfma_pair<8>(s, ps, v, g0, g1, chunk_k); break;
     }
     return true;
 }
