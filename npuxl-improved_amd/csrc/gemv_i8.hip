@@ -456,10 +456,17 @@ void launch_m(hipStream_t s, const I8Gemm &p)
         if (NT >= 512) {
             // One row: two strips per workgroup (half the workgroups, each
             // wave's loads alternating between them).
-            if constexpr (M == 1)
-                gemv_i8_kernel<M, 8, 2, 2><<<dim3((NT + 1) / 2), 512, lds, s>>>(p, chunk_k);
-            else
+            // (three strips where two would put two workgroups on some CUs
+            // and one on others: M=1 N=11008 9.7 -> 9.0 us; three and four
+            // rows were slower with three strips)
+            if constexpr (M == 1) {
+                if ((NT + 1) / 2 > cu_count() && (NT + 2) / 3 <= cu_count())
+                    gemv_i8_kernel<M, 8, 2, 3><<<dim3((NT + 2) / 3), 512, lds, s>>>(p, chunk_k);
+                else
+                    gemv_i8_kernel<M, 8, 2, 2><<<dim3((NT + 1) / 2), 512, lds, s>>>(p, chunk_k);
+            } else {
                 gemv_i8_kernel<M, 8, 2, 1><<<dim3(NT), 512, lds, s>>>(p, chunk_k);
+            }
         } else if constexpr (M == 1) {
             lds_optin<gemv_i8_kernel<M, 16, 4, 1>>();
             gemv_i8_kernel<M, 16, 4, 1><<<dim3(NT), 1024, lds, s>>>(p, chunk_k);
