@@ -357,21 +357,22 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma(I8GemmPair ps, uint32_t g
     epi.template store<W, T, M>(p, red, nt0, NT, tid);
 }
 
-// The matrix-core GEMV of one strip per workgroup with the activations read
-// straight from global memory instead of staged in LDS: lane (kg, row) loads
-// its 16 bytes of row `row` for each weight block alongside that block, so
-// no staging pass and barrier sit between the first weight loads and the
-// first MFMA.  Needs 16-byte aligned rows (lda % 16 == 0, K % 16 == 0); rows
-// past p.M and k past K read as zeros through the buffer's range check.
-template <int M, int W, int U>
+// The matrix-core GEMV with the activations read straight from global memory
+// instead of staged in LDS: lane (kg, row) loads its 16 bytes of row `row`
+// for each k block alongside that block's weights (one A load serves the T
+// strips), so no staging pass and barrier sit between the first weight loads
+// and the first MFMA.  Needs 16-byte aligned rows (lda % 16 == 0,
+// K % 16 == 0); rows past p.M and k past K read as zeros through the
+// buffer's range check.
+template <int M, int W, int U, int T>
 __global__ __launch_bounds__(64 * W) void gemv_i8_mfma_direct(I8GemmPair ps, uint32_t grid0)
 {
     static_assert(M <= 16, "one 16-row group");
     const bool second = blockIdx.x >= grid0;
     const I8Gemm &p = ps.p[second ? 1 : 0];
-    const uint32_t nt0 = second ? blockIdx.x - grid0 : blockIdx.x;
+    const uint32_t nt0 = (second ? blockIdx.x - grid0 : blockIdx.x) * T;
     typedef int v4i __attribute__((ext_vector_type(4)));
-    __shared__ int red[W][1][M][16];
+    __shared__ int red[W][T][M][16];
     const uint32_t Mr = M <= 8 ? static_cast<uint32_t>(M) : p.M;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -379,22 +380,26 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma_direct(I8GemmPair ps, uin
     const int kg = lane >> 4, row = lane & 15;
     const uint32_t NT = p.Np >> 4;
     const uint32_t KT = p.Kp >> 6;
-    const EpiOperands<M * 16, 64 * W> epi(p, nt0, M, tid);
+    const EpiOperands<T * M * 16, 64 * W> epi(p, nt0, M, tid);
 
     const uint32_t first = wave;
     const uint32_t cnt = first < KT ? (KT - first + W - 1) / W : 0;
-    const int8_t *strip = p.frag + static_cast<uint64_t>(min(nt0, NT - 1)) * KT * 1024;
-    const int wbytes = (cnt && nt0 < NT) ? static_cast<int>(((cnt - 1) * W + 1) * 1024) : 0;
-    const auto rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(strip) + static_cast<uint64_t>(first) * 1024,
-                                                      0, wbytes, kBufferWord3);
+    __amdgpu_buffer_rsrc_t rw[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int8_t *strip = p.frag + static_cast<uint64_t>(min(nt0 + t, NT - 1)) * KT * 1024;
+        const int bytes = (cnt && nt0 + t < NT) ? static_cast<int>(((cnt - 1) * W + 1) * 1024) : 0;
+        rw[t] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(strip) + static_cast<uint64_t>(first) * 1024,
+                                                  0, bytes, kBufferWord3);
+    }
     // A: one buffer over the Mr rows; the lane's offset is past the end for a
-    // row past Mr or 16 bytes past K
+    // row past Mr, a block past the wave's last or k past K
     const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p.A), 0,
                                                       static_cast<int>((Mr - 1) * p.lda + p.K), kBufferWord3);
     const bool row_live = static_cast<uint32_t>(row) < Mr;
     const uint32_t a_row = row_live ? row * p.lda : 0u;
-    auto ldb = [&](uint32_t i) {
-        return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, i * W * 1024 + lane * 16, 0,
+    auto ldb = [&](int t, uint32_t i) {
+        return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw[t], i * W * 1024 + lane * 16, 0,
                                                                              kNontemporal));
     };
     auto lda_ = [&](uint32_t i) {
@@ -403,35 +408,44 @@ __global__ __launch_bounds__(64 * W) void gemv_i8_mfma_direct(I8GemmPair ps, uin
         return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, live ? a_row + k : 0x80000000u, 0,
                                                                              0));
     };
-    v4i acc = (v4i){0, 0, 0, 0};
-    v4i bc[U], bn[U], ac[U], an[U];
+    v4i acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = (v4i){0, 0, 0, 0};
+    v4i bc[U][T], bn[U][T], ac[U], an[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        bc[u] = ldb(u);
+#pragma unroll
+        for (int t = 0; t < T; ++t) bc[u][t] = ldb(t, u);
         ac[u] = lda_(u);
     }
     for (uint32_t i = 0; i < cnt; i += U) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            bn[u] = ldb(i + U + u);
+#pragma unroll
+            for (int t = 0; t < T; ++t) bn[u][t] = ldb(t, i + U + u);
             an[u] = lda_(i + U + u);
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(ac[u], bc[u], acc, 0, 0, 0);
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ac[u], bc[u][t], acc[t], 0, 0, 0);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            bc[u] = bn[u];
+#pragma unroll
+            for (int t = 0; t < T; ++t) bc[u][t] = bn[u][t];
             ac[u] = an[u];
         }
     }
     // lane l holds rows 4(l/16) + i of column l%16
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 4 * kg + i;
-        if (m < M) red[wave][0][m][row] = acc[i];
-    }
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * kg + i;
+            if (m < M) red[wave][t][m][row] = acc[t][i];
+        }
     __syncthreads();
-    epi.template store<W, 1, M>(p, red, nt0, NT, tid);
+    epi.template store<W, T, M>(p, red, nt0, NT, tid);
 }
 
 // Launch shapes (swept on MI355X at K = 4096 with the weights streamed from
@@ -504,7 +518,19 @@ void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t
     const size_t wt = variant == 3 ? 24u : 16u;
     const size_t lds = std::max<size_t>(static_cast<size_t>(chunk_k) * M, M > 16 ? 64u * wt * M : 0u);
     const dim3 grid(grid0 + grid1);
-    if (variant == 0) {
+    const bool direct = M <= 16 && direct_a(ps.p[0]) && (grid1 == 0 || direct_a(ps.p[1]));
+    if (direct) {
+        if constexpr (M <= 16) {
+            if (variant == 0)
+                gemv_i8_mfma_direct<M, 4, 4, 4><<<grid, 256, 0, s>>>(ps, grid0);
+            else if (variant == 1)
+                gemv_i8_mfma_direct<M, 8, 2, 2><<<grid, 512, 0, s>>>(ps, grid0);
+            else if (variant == 3)
+                gemv_i8_mfma_direct<M, 8, 2, 3><<<grid, 512, 0, s>>>(ps, grid0);
+            else
+                gemv_i8_mfma_direct<M, 16, 2, 1><<<grid, 1024, 0, s>>>(ps, grid0);
+        }
+    } else if (variant == 0) {
         if (M > 16) lds_optin<gemv_i8_mfma<M, 4, 4, 4>>();
         gemv_i8_mfma<M, 4, 4, 4><<<grid, 256, lds, s>>>(ps, grid0, chunk_k);
     } else if (variant == 1) {
@@ -513,8 +539,6 @@ void launch_mfma_pair(hipStream_t s, const I8GemmPair &ps, int variant, uint32_t
     } else if (variant == 3) {
         if (M > 16) lds_optin<gemv_i8_mfma<M, 8, 2, 3>>();
         gemv_i8_mfma<M, 8, 2, 3><<<grid, 512, lds, s>>>(ps, grid0, chunk_k);
-    } else if (M <= 16 && direct_a(ps.p[0]) && (grid1 == 0 || direct_a(ps.p[1]))) {
-        if constexpr (M <= 16) gemv_i8_mfma_direct<M, 16, 2><<<grid, 1024, 0, s>>>(ps, grid0);
     } else {
         lds_optin<gemv_i8_mfma<M, 16, 2, 1>>();
         gemv_i8_mfma<M, 16, 2, 1><<<grid, 1024, lds, s>>>(ps, grid0, chunk_k);
