@@ -23,7 +23,10 @@
 //     once and are not worth an L2 allocation;
 //   * the activations (M x K int8, tiny) are staged in LDS as [k/16][m][16]
 //     (dynamic LDS sized to the chunk actually used), so lane kg reads its
-//     16 bytes of every row with one ds_read_b128 per row;
+//     16 bytes of every row with one ds_read_b128 per row; the matrix-core
+//     kernel for up to 16 rows instead reads them from global memory with
+//     each weight block when the rows are 16-byte aligned
+//     (gemv_i8_mfma_direct);
 //   * v_dot4_i32_i8 (4 per 16 bytes per row) accumulates in int32 for up
 //     to four rows; from five rows one v_mfma_i32_16x16x64_i8 per block
 //     does it (gemv_i8_mfma below);
