@@ -383,6 +383,24 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *__restrict__ Q, f
     if (K && t < k_seq) rotate_pair(K + (bh * k_seq + t) * head_dim, i0, i1, c, s);
 }
 
+// cos and sin of pairs 4 j4 .. 4 j4 + 3 at position p: two 16-byte table
+// reads where the table covers p (half is a multiple of 4 on the vector
+// path, so they are aligned), rope_cos_sin per pair otherwise.
+__device__ __forceinline__ void rope_cos_sin4(int32_t p, uint32_t j4, uint32_t half, float scaling,
+                                              const float *inv_freq, const float2 *cs, uint32_t cs_rows,
+                                              float (&c)[4], float (&s)[4])
+{
+    if (cs && p >= 0 && static_cast<uint32_t>(p) < cs_rows) {
+        const float4 *t = reinterpret_cast<const float4 *>(cs + static_cast<uint64_t>(p) * half + 4 * j4);
+        const float4 a = t[0], b = t[1];
+        c[0] = a.x; s[0] = a.y; c[1] = a.z; s[1] = a.w;
+        c[2] = b.x; s[2] = b.y; c[3] = b.z; s[3] = b.w;
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rope_cos_sin(p, 4 * j4 + e, half, scaling, inv_freq, cs, cs_rows, c[e], s[e]);
+}
+
 // Half-rotation layout with head_dim % 8 == 0 and 16-byte aligned rows: one
 // thread rotates pairs j..j+3 with one float4 from each half of the row.
 __device__ __forceinline__ void rotate4(const float4 a, const float4 b, const float (&c)[4], const float (&s)[4],
@@ -413,8 +431,7 @@ __global__ __launch_bounds__(kThreads) void rope_vec_kernel(float *__restrict__ 
     const uint32_t t = idx / half4, j4 = idx - t * half4;
     const int32_t p = positions ? positions[t] : static_cast<int32_t>(t + offset);
     float c[4], s[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) rope_cos_sin(p, 4 * j4 + e, head_dim / 2, scaling, inv_freq, cs, cs_rows, c[e], s[e]);
+    rope_cos_sin4(p, j4, head_dim / 2, scaling, inv_freq, cs, cs_rows, c, s);
     for (uint64_t bh = blockIdx.y; bh < bh_count; bh += gridDim.y) {
         // Q's and K's pairs load before anything is stored, through raw buffers
         // over the row (an empty range when the row is absent: zero in, writes
