@@ -45,24 +45,27 @@ __global__ __launch_bounds__(kThreads) void quant_rows_reg(const float *__restri
 {
     __shared__ float red[kThreads / 64];
     const uint64_t r = blockIdx.x;
-    const float4 *row = reinterpret_cast<const float4 *>(X + r * cols);
-    const uint32_t n4 = cols >> 2;
+    // The row through raw buffers: slots past it read zeros and their stores
+    // are dropped, so no branch sits around a load or a store.
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(X + r * cols), 0,
+                                                      static_cast<int>(cols * 4u), 0x00020000);
+    const auto ry = __builtin_amdgcn_make_buffer_rsrc(Y + r * cols, 0, static_cast<int>(cols), 0x00020000);
     float4 v[VPT];
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * kThreads;
-        v[i] = j < n4 ? row[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, j * 16u, 0, 0));
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
     }
     const float scale = scale_from_max(block_max(m, red));
     const float inv = __fdiv_rn(1.0f, scale);
     if (threadIdx.x == 0) scales[r] = scale;
-    char4 *out = reinterpret_cast<char4 *>(Y + r * cols);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const uint32_t j = threadIdx.x + i * kThreads;
-        if (j < n4) out[j] = make_char4(q8(v[i].x, inv), q8(v[i].y, inv), q8(v[i].z, inv), q8(v[i].w, inv));
+        const char4 q = make_char4(q8(v[i].x, inv), q8(v[i].y, inv), q8(v[i].z, inv), q8(v[i].w, inv));
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, q), ry, j * 4u, 0, 0);
     }
 }
 
